@@ -1,0 +1,159 @@
+"""Pins the CPU oracle before anything is checked against it (no GPU needed).
+
+- drafter restatement vs golden vectors written by the reference's own C++
+  Drafter (tests/golden/make_golden.py), five configurations;
+- restricted head == gathered full head (tests/test_vocab.py:37-47 invariant);
+- KV compaction vs the reference KVCache::compact goldens and its known answer;
+- tree verification / tree mask / causal mask vs reference goldens;
+- Philox4x64-10 vs numpy.random.Philox (library routine);
+- RoPE table recipe vs the reference's ops::rope on unit vectors.
+"""
+import numpy as np
+import pytest
+
+from conftest import load_golden
+from drafter_replay import compare, fixture_config, fixture_weights, replay
+from oracle import core, refcpp
+from oracle import sampling as osamp
+
+DRAFTER_FIXTURES = ["tiny", "tiny_prenorm", "tiny_window", "tiny_2layer", "mid"]
+
+
+class OracleAdapter:
+    def __init__(self, cfg, w, kv_bf16=False):
+        self.d = core.Drafter(cfg, w)
+        self.kv_bf16 = kv_bf16
+
+    def fuse(self, taps):
+        return self.d.fuse(taps)
+
+    def make_cache(self, cap):
+        return self.d.make_cache(cap, self.kv_bf16)
+
+    def forward(self, tokens, feat, cache, positions=None, mask=None):
+        return self.d.forward(tokens, feat, cache, positions, mask)
+
+    def feedback(self, hidden, out):
+        return self.d.feedback(hidden, out)
+
+    def logits(self, out):
+        return self.d.logits(out)
+
+    def cache_rows(self, cache, layer):
+        n = cache.offset
+        k = cache.keys_f32(layer)[:, :n].transpose(1, 0, 2).reshape(n, -1)
+        v = cache.values_f32(layer)[:, :n].transpose(1, 0, 2).reshape(n, -1)
+        return k, v
+
+
+@pytest.mark.parametrize("name", DRAFTER_FIXTURES)
+def test_oracle_drafter_matches_reference_cpp(name):
+    z = load_golden(f"drafter_{name}.npz")
+    res = replay(OracleAdapter(fixture_config(z), fixture_weights(z)), z)
+    compare(res, z, rtol=2e-6, what=f"oracle/{name}")
+
+
+def test_oracle_drafter_bf16_cache_is_close():
+    """bf16 KV storage moves outputs by bf16 rounding only (sanity of the bf16 mode)."""
+    z = load_golden("drafter_mid.npz")
+    res = replay(OracleAdapter(fixture_config(z), fixture_weights(z), kv_bf16=True), z)
+    compare(res, z, rtol=2e-2, what="oracle-bf16kv/mid")
+
+
+def test_restricted_head_equals_gathered_full_head():
+    z = load_golden("drafter_mid.npz")
+    cfg, w = fixture_config(z), fixture_weights(z)
+    full = core.Drafter(cfg, w)
+    ids = np.array([0, 3, 7, 8, 21, 49, 150, 299], dtype=np.int32)
+    restricted = core.Drafter(cfg, w, d2t=ids)
+    out = np.random.default_rng(0).standard_normal((2, cfg["hidden_size"])).astype(np.float32)
+    np.testing.assert_array_equal(restricted.logits(out), full.logits(out)[:, ids])
+    rows = np.argmax(restricted.logits(out), axis=-1)
+    assert restricted.token_ids(rows).tolist() == [int(ids[r]) for r in rows]
+
+
+def test_kv_compact_known_answer():
+    """tests/cpp/test_main.cpp:42-50: rows 0..4, compact(1, {0,2,3}) keeps rows 1,3,4."""
+    k = np.repeat(np.arange(5, dtype=np.float32), 2).reshape(1, 5, 2)
+    v = k.copy()
+    core.kv_compact([k], [v], 1, [0, 2, 3])
+    assert k[0, 1, 0] == 1 and k[0, 2, 0] == 3 and k[0, 3, 0] == 4
+
+
+def test_kv_compact_matches_reference_goldens():
+    z = load_golden("kv_compact.npz")
+    for c in range(12):
+        start, keep = int(z[f"c{c}.start"]), z[f"c{c}.keep"]
+        kin, vin = z[f"c{c}.k_in"], z[f"c{c}.v_in"]  # [layers][T][heads*dim]
+        layers, T, row = kin.shape
+        heads = 2
+        ks = [np.ascontiguousarray(kin[l].reshape(T, heads, -1).transpose(1, 0, 2)) for l in range(layers)]
+        vs = [np.ascontiguousarray(vin[l].reshape(T, heads, -1).transpose(1, 0, 2)) for l in range(layers)]
+        core.kv_compact(ks, vs, start, keep)
+        n = int(z[f"c{c}.size"])
+        for l in range(layers):
+            np.testing.assert_array_equal(ks[l][:, :n].transpose(1, 0, 2).reshape(n, row), z[f"c{c}.k_out"][l][:n])
+            np.testing.assert_array_equal(vs[l][:, :n].transpose(1, 0, 2).reshape(n, row), z[f"c{c}.v_out"][l][:n])
+
+
+def test_tree_greedy_and_masks_match_reference_goldens():
+    z = load_golden("verify.npz")
+    for c in range(40):
+        tree = osamp.DraftTree(z[f"t{c}.tokens"].tolist(), z[f"t{c}.parents"].tolist(), z[f"t{c}.depth"].tolist())
+        path, nxt = osamp.verify_tree_greedy(z[f"t{c}.am"], tree)
+        assert path == z[f"t{c}.path"].tolist() and nxt == int(z[f"t{c}.next"])
+        np.testing.assert_array_equal(osamp.tree_attention_mask(tree, int(z[f"t{c}.prefix"])), z[f"t{c}.mask"])
+
+
+def test_probs_from_logits_matches_reference_cpp():
+    """fp32 restatement within fp32 rounding of sampling.cpp:9-45 (T, top-k, top-p)."""
+    z = load_golden("verify.npz")
+    for c in range(5):
+        T, k, p = z[f"p{c}.args"].tolist()
+        got = osamp.probs_from_logits(z[f"p{c}.z"], T, int(k), p)
+        np.testing.assert_allclose(got, z[f"p{c}.p"], rtol=2e-6, atol=1e-9)
+
+
+def test_philox_matches_numpy():
+    """Salmon et al. Philox4x64-10 against numpy.random.Philox: numpy increments the
+    counter before producing a block, so counter c-1 in numpy == block c here."""
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        ctr = rng.integers(1, 2**63, 4, dtype=np.uint64)
+        key = rng.integers(0, 2**63, 2, dtype=np.uint64)
+        want = np.random.Philox(counter=[int(ctr[0]) - 1, *map(int, ctr[1:])], key=list(map(int, key))).random_raw(4)
+        np.testing.assert_array_equal(core.philox4x64_10(ctr, key), want)
+    # carry across the low counter word
+    want = np.random.Philox(counter=np.array([2**64 - 1, 6, 0, 0], dtype=np.uint64), key=[9, 0]).random_raw(4)
+    np.testing.assert_array_equal(core.philox4x64_10([0, 7, 0, 0], [9, 0]), want)
+
+
+def test_uniform_stream_layout():
+    """uniform i of (seed, round, purpose) = word i%4 of block (i//4, round, purpose, 0),
+    converted like numpy's Generator.random (53-bit)."""
+    seed, rnd, purpose = 1234, 77, 3
+    u = core.uniforms(seed, rnd, purpose, 0, 12)
+    for i in (1, 5, 11):
+        blk = core.philox4x64_10([i // 4, rnd, purpose, 0], [seed, 0])
+        assert u[i] == (int(blk[i % 4]) >> 11) * (1.0 / 9007199254740992.0)
+    g = np.random.Generator(np.random.Philox(counter=[0, rnd, purpose, 0], key=[seed, 0]))
+    np.testing.assert_array_equal(core.uniforms(seed, rnd, purpose, 4, 8), g.random(8))
+    s = core.UniformStream(seed, rnd, purpose)
+    assert [s.random() for _ in range(3)] == u[:3].tolist()
+    np.testing.assert_array_equal(s.random(4), u[3:7])
+
+
+@pytest.mark.skipif(not refcpp.available(), reason="reference build absent")
+@pytest.mark.parametrize("D,base", [(8, 1e4), (128, 1e6)])
+def test_rope_table_reproduces_reference_rope(D, base):
+    """Rotating a unit vector e_i by the reference ops::rope reveals (cos, sin) of
+    every pair; the oracle's host table must equal them bit for bit."""
+    positions = np.array([0, 1, 7, 511, 4095], dtype=np.int32)
+    half = D // 2
+    ct, st = core.rope_table(4096, D, base)
+    for i in range(half):
+        x = np.zeros((len(positions), 1, D), dtype=np.float32)
+        x[:, 0, i] = 1.0
+        refcpp.lib().wcref_rope(x.ctypes.data, len(positions), 1, D, positions.ctypes.data, base)
+        np.testing.assert_array_equal(x[:, 0, i], ct[positions, i])
+        np.testing.assert_array_equal(x[:, 0, i + half], st[positions, i])
