@@ -110,6 +110,97 @@ int wc_kv_compact(void* const* k_layers, void* const* v_layers, int n_layers, in
                   int row_bytes, const int32_t* start_dev, const int32_t* keep_dev, const int32_t* n_keep_dev,
                   int max_keep, int32_t* offset_dev, int32_t* status_dev, wc_stream_t stream);
 
+/* ------------------------------------------------------------------ drafter step */
+
+#define WC_MAX_DRAFTER_LAYERS 4
+#define WC_MAX_FEATURES 3
+#define WC_MAX_STEP_ROWS 16 /* rows per drafter launch; longer inputs are tiled by the host */
+
+/* DrafterConfig fields the kernels need (python/woodcock/drafter.py:33-49;
+ * include/woodcock/drafter.h:16-24). */
+typedef struct wc_drafter_dims {
+  int32_t hidden, num_layers, heads, kv_heads, head_dim, inter, target_hidden, num_features, head_rows;
+  float eps;
+  int32_t window; /* 0 = full attention */
+} wc_drafter_dims;
+
+/* One decoder layer's device weights, bf16 row-major [out][in] (nn.Linear layout).
+ * aux_norm / aux_q / aux_k / aux_v are NULL for layers without the token stream. */
+typedef struct wc_layer_weights {
+  const void *in_norm, *post_norm, *aux_norm;
+  const void *q, *k, *v, *o, *aux_q, *aux_k, *aux_v, *q_norm, *k_norm, *gate, *up, *down;
+} wc_layer_weights;
+
+typedef struct wc_drafter_weights {
+  const void* embed;                          /* [vocab][hidden] */
+  const void* fc;                             /* [hidden][num_features * target_hidden] */
+  const void* feature_norm[WC_MAX_FEATURES];  /* [target_hidden] each, NULL = feature_norm off */
+  const void* final_norm;                     /* [hidden] */
+  const void* head;                           /* [head_rows][hidden]: the restricted rows, gathered */
+  const int32_t* d2t;                         /* [head_rows] head row -> token id; NULL = identity */
+  const float* rope_cos;                      /* [rope_max_pos][head_dim/2] host recipe (wc_rope_table) */
+  const float* rope_sin;
+  int32_t rope_max_pos;
+  wc_layer_weights layers[WC_MAX_DRAFTER_LAYERS];
+} wc_drafter_weights;
+
+/* Stochastic drafting: Gumbel-max over the head rows, uniforms from the
+ * Philox4x64-10 stream (seed, *round_dev, purpose + row). */
+typedef struct wc_gumbel {
+  uint64_t seed;
+  const int32_t* round_dev;
+  int32_t purpose;
+  float temperature;
+} wc_gumbel;
+
+/* cos/sin table of the rotate-half RoPE with the reference recipe:
+ * inv_i = powf(base, -2i/D), angle = (float)pos * inv_i (src/backends/cpu_ops.cpp:61-77).
+ * Host memory, [max_pos][D/2] each. */
+int wc_rope_table(float* cos_out, float* sin_out, int max_pos, int head_dim, float base);
+
+/* Device workspace for wc_drafter_fuse / wc_drafter_forward / wc_draft_head. */
+size_t wc_drafter_workspace_bytes(const wc_drafter_dims* dims);
+
+/* g[r] = fc(concat_f RMS_f(tap_f[row r])) for r < rows (device count *n_rows_dev
+ * when not NULL).  taps: num_features device pointers, [.][tap_ld] of tap_dtype;
+ * tap_rows_dev (optional) gathers tap rows (e.g. the accepted path, keep).
+ * Replaces Drafter.fuse (python/woodcock/drafter.py:149-153; src/core/drafter.cpp:75-89). */
+int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps, int tap_dtype,
+                    int64_t tap_ld, const int32_t* tap_rows_dev, int rows, const int32_t* n_rows_dev, float* g_out,
+                    int64_t g_ld, void* workspace, wc_stream_t stream);
+
+/* One drafting forward over `rows` tokens appended at cache offset
+ * *offset_dev + offset_add: every layer (dual-stream layer 0, GQA attention
+ * with q/k RMSNorm and rotate-half RoPE, SwiGLU MLP), then the final RMSNorm.
+ *   tokens_dev [rows]; feat [rows][feat_ld] fp32 (feat_row_dev optionally
+ *   gathers one feature row: row *feat_row_dev + feat_row_add);
+ *   k_cache/v_cache: num_layers device pointers [kv_heads][capacity][head_dim]
+ *   of kv_dtype; positions_dev [rows] (NULL = offset + r); mask_dev
+ *   [rows][mask_ld] uint8 over cache slots (NULL = causal, sliding window
+ *   when dims->window > 0); n_rows_dev: device row count (rows <= WC_MAX_STEP_ROWS).
+ *   Writes hidden_out / out_out [rows][hidden] fp32; when advance_dev is not
+ *   NULL, *advance_dev = offset + rows after the last layer.
+ * Replaces Drafter.__call__ (python/woodcock/drafter.py:164-191) and
+ * Drafter::forward (src/core/drafter.cpp:91-136). */
+int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w, const int32_t* tokens_dev,
+                       const float* feat, int64_t feat_ld, const int32_t* feat_row_dev, int feat_row_add, int rows,
+                       const int32_t* n_rows_dev, void* const* k_cache, void* const* v_cache, int kv_dtype,
+                       int capacity, const int32_t* offset_dev, int offset_add, const int32_t* positions_dev,
+                       const uint8_t* mask_dev, int64_t mask_ld, float* hidden_out, float* out_out,
+                       int32_t* advance_dev, void* workspace, wc_stream_t stream);
+
+/* Draft head + argmax + d2t over `rows` output rows: logits z = out . head^T
+ * (written when logits_out is not NULL, [rows][head_rows] fp32), token_out[r] =
+ * d2t[argmax_r z] (lowest row wins a tie), row_out[r] = the row.  With gumbel,
+ * the argmax is of z/T + Gumbel noise (a draw from softmax(z/T)).
+ * out_row_dev optionally selects input row *out_row_dev + out_row_add (rows = 1).
+ * Replaces Drafter.logits + mx.argmax + Drafter.token_ids
+ * (python/woodcock/drafter.py:204-215; python/woodcock/spec.py:346). */
+int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* out_rows, int64_t out_ld,
+                  const int32_t* out_row_dev, int out_row_add, int rows, float* logits_out, int64_t logits_ld,
+                  int32_t* token_out, int32_t* row_out, const wc_gumbel* gumbel, void* workspace,
+                  wc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -195,6 +195,11 @@ def test_invalid_arguments_raise(cuda):
         S.verify_chain_greedy(torch.zeros(3, 10), [1, 2])  # host tensor: no CPU fallback
     with pytest.raises(ValueError):
         S.verify_chain_greedy(torch.zeros(3, 10, device=cuda, dtype=torch.float16), [1, 2])
-    bad = S.DraftTree(tokens=[0, 1], parents=[-1, 5], depth=[0, 1])
+    # a parent index outside the tree, seen only on the device: the kernel's own
+    # check flags the verdict, which the host read turns into ValueError
+    from woodcock_amd.runtime import read_verdict
+
+    v = S.verify_tree_greedy_dev(torch.zeros(2, 10, device=cuda), torch.tensor([0, 1], dtype=torch.int32, device=cuda),
+                                 torch.tensor([-1, 5], dtype=torch.int32, device=cuda))
     with pytest.raises(ValueError):
-        S.verify_tree_greedy(torch.zeros(2, 10, device=cuda), bad)
+        read_verdict(v)

@@ -46,6 +46,40 @@ P = C.c_void_p
 I32 = C.c_int32
 I64 = C.c_int64
 
+WC_MAX_DRAFTER_LAYERS = 4
+WC_MAX_FEATURES = 3
+WC_MAX_STEP_ROWS = 16
+
+
+class DrafterDims(C.Structure):
+    """Mirror of wc_drafter_dims."""
+
+    _fields_ = [(n, C.c_int32) for n in ("hidden", "num_layers", "heads", "kv_heads", "head_dim", "inter",
+                                          "target_hidden", "num_features", "head_rows")] + \
+               [("eps", C.c_float), ("window", C.c_int32)]
+
+
+class LayerWeights(C.Structure):
+    """Mirror of wc_layer_weights (device pointers)."""
+
+    _fields_ = [(n, C.c_void_p) for n in ("in_norm", "post_norm", "aux_norm", "q", "k", "v", "o", "aux_q", "aux_k",
+                                          "aux_v", "q_norm", "k_norm", "gate", "up", "down")]
+
+
+class DrafterWeights(C.Structure):
+    """Mirror of wc_drafter_weights (device pointers)."""
+
+    _fields_ = [("embed", C.c_void_p), ("fc", C.c_void_p), ("feature_norm", C.c_void_p * WC_MAX_FEATURES),
+                ("final_norm", C.c_void_p), ("head", C.c_void_p), ("d2t", C.c_void_p), ("rope_cos", C.c_void_p),
+                ("rope_sin", C.c_void_p), ("rope_max_pos", C.c_int32),
+                ("layers", LayerWeights * WC_MAX_DRAFTER_LAYERS)]
+
+
+class Gumbel(C.Structure):
+    """Mirror of wc_gumbel."""
+
+    _fields_ = [("seed", C.c_uint64), ("round_dev", C.c_void_p), ("purpose", C.c_int32), ("temperature", C.c_float)]
+
 _SIGS = {
     "wc_version": ([], C.c_int),
     "wc_last_error": ([], C.c_char_p),
@@ -55,6 +89,12 @@ _SIGS = {
     "wc_verify_chain_greedy": ([P, C.c_int, C.c_int, I64, P, P, P, P], C.c_int),
     "wc_verify_tree_greedy": ([P, C.c_int, C.c_int, I64, P, P, P, P, P], C.c_int),
     "wc_kv_compact": ([P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, C.c_int, P, P, P], C.c_int),
+    "wc_rope_table": ([P, P, C.c_int, C.c_int, C.c_float], C.c_int),
+    "wc_drafter_workspace_bytes": ([P], C.c_size_t),
+    "wc_drafter_fuse": ([P, P, P, C.c_int, I64, P, C.c_int, P, P, I64, P, P], C.c_int),
+    "wc_drafter_forward": ([P, P, P, P, I64, P, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int, P, C.c_int, P, P, I64,
+                            P, P, P, P, P], C.c_int),
+    "wc_draft_head": ([P, P, P, I64, P, C.c_int, C.c_int, P, I64, P, P, P, P, P], C.c_int),
 }
 
 _lib = None

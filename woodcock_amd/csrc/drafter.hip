@@ -1,0 +1,741 @@
+// drafter.hip -- the EAGLE-3 drafter step on gfx950.
+//
+// One decoder layer (python/woodcock/drafter.py:164-191; src/core/drafter.cpp:91-136)
+// is five launches, all stream-ordered on the caller's stream:
+//   1. QKV    : dual-input streaming GEMV  q,k,v = W.RMS(h) + W_aux.RMS(e(x))
+//   2. attend : q/k RMSNorm + RoPE + KV append + split-KV GQA attention,
+//               last-arriving block per kv head merges the splits
+//   3. o_proj : GEMV with residual epilogue          h1 = h + W_o.o
+//   4. gate/up: paired-row GEMV, SiLU(gate)*up epilogue
+//   5. down   : GEMV with residual epilogue, last block applies the final
+//               RMSNorm (out) and advances the cache offset
+// plus the fc fusion (drafter.py:149-153) and the draft head with a fused
+// argmax / Gumbel-max and d2t map (drafter.py:204-215, spec.py:346).
+// Every round-varying integer (offset, row counts, gathered rows, tokens) is
+// read from device memory.
+#include "gemv.h"
+
+namespace wc {
+
+// ------------------------------------------------------------------ workspace
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnChunk = 32;  // keys staged per iteration
+constexpr int kMaxQV = 64;      // query vectors (rows x GQA group) per attention block
+constexpr int kMaxSplits = 32;
+constexpr int kMaxKvHeads = 64;
+
+struct DrafterWs {
+  unsigned int* counters;  // [0] head, [1] final, [2 + kh] attention
+  unsigned long long* slots;
+  float* qkv;
+  float* attn;
+  float* h1;
+  float* act;
+  float* partial;
+  size_t bytes;
+};
+
+static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
+  DrafterWs w{};
+  char* p = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* q = p ? p + off : nullptr;
+    off = align256(off + bytes);
+    return q;
+  };
+  const size_t R = WC_MAX_STEP_ROWS;
+  const size_t nqkv = static_cast<size_t>(d.heads + 2 * d.kv_heads) * d.head_dim;
+  w.counters = reinterpret_cast<unsigned int*>(take(4 * (2 + kMaxKvHeads)));
+  w.slots = reinterpret_cast<unsigned long long*>(take(8 * R));
+  w.qkv = reinterpret_cast<float*>(take(4 * R * nqkv));
+  w.attn = reinterpret_cast<float*>(take(4 * R * d.heads * d.head_dim));
+  w.h1 = reinterpret_cast<float*>(take(4 * R * d.hidden));
+  w.act = reinterpret_cast<float*>(take(4 * R * d.inter));
+  w.partial = reinterpret_cast<float*>(take(4 * static_cast<size_t>(d.kv_heads) * kMaxSplits * kMaxQV *
+                                            (d.head_dim + 2)));
+  w.bytes = off;
+  return w;
+}
+
+// ------------------------------------------------------------------ attention
+
+struct AttnArgs {
+  const float* qkv;  // [rows][ld_qkv] raw q | k | v
+  int64_t ld_qkv;
+  int H, Hk, rows;
+  const int32_t* n_rows_dev;
+  const uint16_t *q_gain, *k_gain;
+  float eps, scale;
+  const float *rope_cos, *rope_sin;
+  int rope_max;
+  const int32_t* positions;  // [rows] or NULL
+  void *kc, *vc;             // [Hk][cap][D]
+  int cap;
+  const int32_t* offset_dev;
+  int offset_add;
+  const uint8_t* mask;  // [rows][mask_ld] or NULL
+  int64_t mask_ld;
+  int window;
+  float* partial;  // [Hk][S][kMaxQV][D+2]
+  unsigned int* counters;
+  float* out;  // [rows][H*D]
+  int64_t ld_out;
+};
+
+template <typename KT>
+__device__ __forceinline__ float kv_load(const KT* p, int64_t i);
+template <>
+__device__ __forceinline__ float kv_load<float>(const float* p, int64_t i) {
+  return p[i];
+}
+template <>
+__device__ __forceinline__ float kv_load<uint16_t>(const uint16_t* p, int64_t i) {
+  return bf16_to_float(p[i]);
+}
+// store to the cache, return the stored value as read back (bf16 rounding)
+template <typename KT>
+__device__ __forceinline__ float kv_store(KT* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ float kv_store<float>(float* p, int64_t i, float v) {
+  p[i] = v;
+  return v;
+}
+template <>
+__device__ __forceinline__ float kv_store<uint16_t>(uint16_t* p, int64_t i, float v) {
+  const uint16_t b = float_to_bf16(v);
+  p[i] = b;
+  return bf16_to_float(b);
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if ((threadIdx.x % kWave) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) t += red[w];
+  return t;
+}
+
+// Normalise (gain) and rotate one head vector src[D] at position pos into dst[D]
+// (LDS).  Executed by one wave; D <= 256.
+template <int D>
+__device__ __forceinline__ void norm_rope_vec(const float* src, const uint16_t* gain, float eps, const float* ct,
+                                              const float* st, int pos, float* dst) {
+  const int lane = threadIdx.x % kWave;
+  constexpr int EPL = (D + kWave - 1) / kWave;
+  float x[EPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int i = lane + e * kWave;
+    x[e] = i < D ? src[i] : 0.f;
+    ss = fmaf(x[e], x[e], ss);
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int i = lane + e * kWave;
+    if (i < D) dst[i] = x[e] * inv * bf16_to_float(gain[i]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  constexpr int half = D / 2;
+  float r1[EPL], r2[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int i = lane + e * kWave;
+    if (i < half) {
+      const float c = ct[static_cast<int64_t>(pos) * half + i], s = st[static_cast<int64_t>(pos) * half + i];
+      const float x1 = dst[i], x2 = dst[i + half];
+      r1[e] = x1 * c - x2 * s;
+      r2[e] = x2 * c + x1 * s;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    const int i = lane + e * kWave;
+    if (i < half) {
+      dst[i] = r1[e];
+      dst[i + half] = r2[e];
+    }
+  }
+}
+
+template <int D, typename KT>
+__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
+  extern __shared__ float lds[];
+  constexpr int ACC = (kMaxQV * D + kAttnThreads - 1) / kAttnThreads;
+  const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
+  const int rep = a.H / a.Hk;
+  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
+  const int offset = *a.offset_dev + a.offset_add;
+  const int T = offset + nr;
+  const int QV = nr * rep;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int nw = kAttnThreads / kWave;
+
+  float* qs = lds;                       // [QV][D]
+  float* ks = qs + QV * D;               // [kAttnChunk][D]
+  float* vs = ks + kAttnChunk * D;       // [kAttnChunk][D]
+  float* sc = vs + kAttnChunk * D;       // [QV][kAttnChunk]
+  __shared__ float s_m[kMaxQV], s_l[kMaxQV], s_alpha[kMaxQV];
+
+  KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
+  KT* vc = static_cast<KT*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
+  const int per = (T + S - 1) / S;
+  const int kb = min(T, split * per), ke = min(T, kb + per);
+
+  // q vectors of this kv head's group: normalised + rotated, in LDS
+  for (int v = wave; v < QV; v += nw) {
+    const int l = v / rep, h = kh * rep + v % rep;
+    int pos = a.positions ? a.positions[l] : offset + l;
+    pos = min(max(pos, 0), a.rope_max - 1);
+    norm_rope_vec<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, a.eps, a.rope_cos, a.rope_sin, pos, qs + v * D);
+  }
+  // new keys / values whose slot falls in this block's range: norm + rope, append
+  for (int l = wave; l < nr; l += nw) {
+    const int t = offset + l;
+    if (t < kb || t >= ke) continue;
+    int pos = a.positions ? a.positions[l] : offset + l;
+    pos = min(max(pos, 0), a.rope_max - 1);
+    float* tmp = ks + wave * D;  // scratch row (ks is free until the key loop; kAttnChunk >= waves)
+    norm_rope_vec<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, a.eps, a.rope_cos, a.rope_sin, pos, tmp);
+    for (int i = lane; i < D; i += kWave) {
+      kv_store<KT>(kc, static_cast<int64_t>(t) * D + i, tmp[i]);
+      kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, a.qkv[l * a.ld_qkv + (a.H + a.Hk + kh) * D + i]);
+    }
+  }
+  if (threadIdx.x < kMaxQV) {
+    s_m[threadIdx.x] = -INFINITY;
+    s_l[threadIdx.x] = 0.f;
+  }
+  __threadfence_block();
+  __syncthreads();
+
+  float acc[ACC];
+#pragma unroll
+  for (int e = 0; e < ACC; ++e) acc[e] = 0.f;
+
+  for (int c0 = kb; c0 < ke; c0 += kAttnChunk) {
+    const int n = min(kAttnChunk, ke - c0);
+    for (int e = threadIdx.x; e < n * D; e += kAttnThreads) {
+      ks[e] = kv_load<KT>(kc, static_cast<int64_t>(c0) * D + e);
+      vs[e] = kv_load<KT>(vc, static_cast<int64_t>(c0) * D + e);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < QV * n; e += kAttnThreads) {
+      const int v = e / n, j = e - v * n;
+      const int l = v / rep, t = c0 + j;
+      bool vis;
+      if (a.mask)
+        vis = a.mask[l * a.mask_ld + t] != 0;
+      else
+        vis = t <= offset + l && (a.window <= 0 || t > offset + l - a.window);
+      float s = -INFINITY;
+      if (vis) {
+        float d = 0.f;
+        const float* q = qs + v * D;
+        const float* k = ks + j * D;
+#pragma unroll 8
+        for (int i = 0; i < D; ++i) d = fmaf(q[i], k[i], d);
+        s = a.scale * d;
+      }
+      sc[v * kAttnChunk + j] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x < QV) {
+      const int v = threadIdx.x;
+      const float m_old = s_m[v];
+      float m_new = m_old;
+      for (int j = 0; j < n; ++j) m_new = fmaxf(m_new, sc[v * kAttnChunk + j]);
+      float alpha = 1.f, lsum = 0.f;
+      if (m_new != -INFINITY) {
+        alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
+        for (int j = 0; j < n; ++j) {
+          const float s = sc[v * kAttnChunk + j];
+          const float p = s == -INFINITY ? 0.f : expf(s - m_new);
+          sc[v * kAttnChunk + j] = p;
+          lsum += p;
+        }
+      } else {
+        for (int j = 0; j < n; ++j) sc[v * kAttnChunk + j] = 0.f;
+      }
+      s_m[v] = m_new;
+      s_l[v] = s_l[v] * alpha + lsum;
+      s_alpha[v] = alpha;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < ACC; ++e) {
+      const int idx = threadIdx.x + e * kAttnThreads;
+      if (idx < QV * D) {
+        const int v = idx / D, i = idx - v * D;
+        float o = acc[e] * s_alpha[v];
+        for (int j = 0; j < n; ++j) o = fmaf(sc[v * kAttnChunk + j], vs[j * D + i], o);
+        acc[e] = o;
+      }
+    }
+    __syncthreads();
+  }
+
+  // publish this split's (m, l, o)
+  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * kMaxQV * (D + 2);
+#pragma unroll
+  for (int e = 0; e < ACC; ++e) {
+    const int idx = threadIdx.x + e * kAttnThreads;
+    if (idx < QV * D) {
+      const int v = idx / D, i = idx - v * D;
+      part[v * (D + 2) + 2 + i] = acc[e];
+    }
+  }
+  if (threadIdx.x < QV) {
+    part[threadIdx.x * (D + 2)] = s_m[threadIdx.x];
+    part[threadIdx.x * (D + 2) + 1] = s_l[threadIdx.x];
+  }
+  if (!last_block_done(&a.counters[kh], S)) return;
+
+  // merge the splits of this kv head
+  const float* base = a.partial + static_cast<int64_t>(kh) * S * kMaxQV * (D + 2);
+  for (int idx = threadIdx.x; idx < QV * D; idx += kAttnThreads) {
+    const int v = idx / D, i = idx - v * D;
+    float M = -INFINITY;
+    for (int s = 0; s < S; ++s) M = fmaxf(M, base[(s * kMaxQV + v) * (D + 2)]);
+    float num = 0.f, den = 0.f;
+    for (int s = 0; s < S; ++s) {
+      const float* p = base + (s * kMaxQV + v) * (D + 2);
+      if (p[0] == -INFINITY) continue;
+      const float wgt = expf(p[0] - M);
+      den = fmaf(p[1], wgt, den);
+      num = fmaf(p[2 + i], wgt, num);
+    }
+    const int l = v / rep, h = kh * rep + v % rep;
+    a.out[l * a.ld_out + h * D + i] = num / den;
+  }
+  if (threadIdx.x == 0) atomic_store_u32(&a.counters[kh], 0u);
+}
+
+template <int D, typename KT>
+static int launch_attention_t(const AttnArgs& a, int splits, int qv_max, hipStream_t stream) {
+  const size_t lds = sizeof(float) * (static_cast<size_t>(qv_max) * D + 2 * kAttnChunk * D +
+                                      static_cast<size_t>(qv_max) * kAttnChunk);
+  static bool attr_set = false;
+  if (lds > 64 * 1024 && !attr_set) {
+    WC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention<D, KT>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((k_attention<D, KT>), dim3(splits, a.Hk), dim3(kAttnThreads), lds, stream, a);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, int qv_max, hipStream_t s) {
+#define WC_ATT(DD)                                                                                  \
+  case DD:                                                                                          \
+    return kv_dtype == WC_BF16 ? launch_attention_t<DD, uint16_t>(a, splits, qv_max, s)            \
+                               : launch_attention_t<DD, float>(a, splits, qv_max, s);
+  switch (D) {
+    WC_ATT(8)
+    WC_ATT(16)
+    WC_ATT(32)
+    WC_ATT(64)
+    WC_ATT(128)
+    WC_ATT(256)
+    default:
+      return set_error(WC_E_UNSUPPORTED, "head_dim %d not supported (8, 16, 32, 64, 128, 256)", D);
+  }
+#undef WC_ATT
+}
+
+// ------------------------------------------------------------------ GEMV launch
+
+template <int R, bool PAIR>
+static int launch_gemv_r(const GemvArgs& a, hipStream_t s) {
+  const int blocks = (a.N + kGemvWaves * R - 1) / (kGemvWaves * R);
+  const dim3 grid(blocks), block(kGemvThreads);
+#define WC_GEMV(MMV) \
+  hipLaunchKernelGGL((k_gemv<R, MMV, PAIR, 4>), grid, block, kGemvLdsBytes, s, a)
+  if (a.M <= 1)
+    WC_GEMV(1);
+  else if (a.M <= 2)
+    WC_GEMV(2);
+  else if (a.M <= 4)
+    WC_GEMV(4);
+  else if (a.M <= 8)
+    WC_GEMV(8);
+  else
+    WC_GEMV(16);
+#undef WC_GEMV
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+static int launch_gemv(const GemvArgs& a, int R, hipStream_t s) {
+  if (a.M < 1 || a.M > kMaxM) return set_error(WC_E_INVALID, "gemv: rows %d not in 1..%d", a.M, kMaxM);
+  if (a.epi == kEpiSiluPair) return R >= 2 ? launch_gemv_r<2, true>(a, s) : launch_gemv_r<1, true>(a, s);
+  return R >= 2 ? launch_gemv_r<2, false>(a, s) : launch_gemv_r<1, false>(a, s);
+}
+
+static GemvArgs gemv_defaults() {
+  GemvArgs g{};
+  g.n_seg = 1;
+  g.seg_start[0] = 0;
+  return g;
+}
+
+static const uint16_t* u16(const void* p) { return static_cast<const uint16_t*>(p); }
+
+static int check_dims(const wc_drafter_dims* d) {
+  WC_REQUIRE(d != nullptr, "dims is NULL");
+  WC_REQUIRE(d->hidden > 0 && d->hidden % 8 == 0, "hidden_size must be a positive multiple of 8");
+  WC_REQUIRE(d->heads > 0 && d->kv_heads > 0 && d->heads % d->kv_heads == 0, "heads must be a multiple of kv_heads");
+  WC_REQUIRE(d->kv_heads <= kMaxKvHeads, "at most %d kv heads", kMaxKvHeads);
+  WC_REQUIRE(d->head_dim > 0 && d->head_dim % 8 == 0, "head_dim must be a positive multiple of 8");
+  WC_REQUIRE(d->inter > 0 && d->inter % 8 == 0, "intermediate_size must be a positive multiple of 8");
+  WC_REQUIRE(d->target_hidden > 0 && d->target_hidden % 8 == 0, "target_hidden_size must be a multiple of 8");
+  WC_REQUIRE(d->num_features >= 1 && d->num_features <= WC_MAX_FEATURES, "num_features must be in 1..%d",
+             WC_MAX_FEATURES);
+  WC_REQUIRE(d->num_layers >= 1 && d->num_layers <= WC_MAX_DRAFTER_LAYERS, "num_layers must be in 1..%d",
+             WC_MAX_DRAFTER_LAYERS);
+  WC_REQUIRE(d->head_rows >= 1, "head_rows must be positive");
+  return WC_OK;
+}
+
+static bool al16(const void* p) { return aligned(p, 16); }
+
+}  // namespace wc
+
+using namespace wc;
+
+extern "C" {
+
+int wc_rope_table(float* cos_out, float* sin_out, int max_pos, int head_dim, float base) {
+  WC_REQUIRE(cos_out && sin_out, "wc_rope_table: NULL output");
+  WC_REQUIRE(max_pos > 0 && head_dim > 0 && head_dim % 2 == 0, "wc_rope_table: bad sizes");
+  const int half = head_dim / 2;
+  for (int i = 0; i < half; ++i) {
+    const float inv = powf(base, -2.f * static_cast<float>(i) / static_cast<float>(head_dim));
+    for (int p = 0; p < max_pos; ++p) {
+      const float ang = static_cast<float>(p) * inv;
+      cos_out[static_cast<int64_t>(p) * half + i] = cosf(ang);
+      sin_out[static_cast<int64_t>(p) * half + i] = sinf(ang);
+    }
+  }
+  return WC_OK;
+}
+
+size_t wc_drafter_workspace_bytes(const wc_drafter_dims* dims) {
+  if (!dims) return 0;
+  return drafter_ws(*dims, nullptr).bytes;
+}
+
+int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps, int tap_dtype,
+                    int64_t tap_ld, const int32_t* tap_rows_dev, int rows, const int32_t* n_rows_dev, float* g_out,
+                    int64_t g_ld, void* workspace, wc_stream_t stream) {
+  if (int rc = check_dims(dims)) return rc;
+  WC_REQUIRE(w && taps && g_out, "wc_drafter_fuse: NULL argument");
+  WC_REQUIRE(w->fc && al16(w->fc), "wc_drafter_fuse: fc weight missing or not 16-byte aligned");
+  WC_REQUIRE(tap_dtype == WC_F32 || tap_dtype == WC_BF16, "wc_drafter_fuse: tap dtype must be f32 or bf16");
+  WC_REQUIRE(tap_ld >= dims->target_hidden && g_ld >= dims->hidden, "wc_drafter_fuse: bad row stride");
+  WC_REQUIRE(rows >= 1, "wc_drafter_fuse: rows must be positive");
+  WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
+             "wc_drafter_fuse: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  const int nf = dims->num_features, Dt = dims->target_hidden;
+  for (int t0 = 0; t0 < rows; t0 += WC_MAX_STEP_ROWS) {
+    const int tr = std::min(WC_MAX_STEP_ROWS, rows - t0);
+    GemvArgs g = gemv_defaults();
+    g.n_in = nf;
+    for (int f = 0; f < nf; ++f) {
+      WC_REQUIRE(taps[f] != nullptr, "wc_drafter_fuse: tap %d is NULL", f);
+      g.in[f].x = static_cast<const char*>(taps[f]) + (tap_rows_dev ? 0 : t0 * tap_ld * (tap_dtype ? 2 : 4));
+      g.in[f].ld = tap_ld;
+      g.in[f].dtype = tap_dtype;
+      g.in[f].row_idx = tap_rows_dev ? tap_rows_dev + t0 : nullptr;
+      g.in[f].gain = u16(w->feature_norm[f]);  // NULL: feature_norm off (drafter.py:151-152)
+      g.in[f].K = Dt;
+      g.ldw[f] = static_cast<int64_t>(nf) * Dt;
+      g.w[0][f] = u16(w->fc) + static_cast<int64_t>(f) * Dt;
+    }
+    g.N = dims->hidden;
+    g.seg_start[1] = g.N;
+    g.M = tr;
+    g.m_dev = n_rows_dev;
+    g.eps = dims->eps;
+    g.epi = kEpiStore;
+    g.y = g_out + t0 * g_ld;
+    g.ldy = g_ld;
+    if (int rc = launch_gemv(g, 1, s)) return rc;
+  }
+  return WC_OK;
+}
+
+int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w, const int32_t* tokens_dev,
+                       const float* feat, int64_t feat_ld, const int32_t* feat_row_dev, int feat_row_add, int rows,
+                       const int32_t* n_rows_dev, void* const* k_cache, void* const* v_cache, int kv_dtype,
+                       int capacity, const int32_t* offset_dev, int offset_add, const int32_t* positions_dev,
+                       const uint8_t* mask_dev, int64_t mask_ld, float* hidden_out, float* out_out,
+                       int32_t* advance_dev, void* workspace, wc_stream_t stream) {
+  if (int rc = check_dims(dims)) return rc;
+  const wc_drafter_dims& d = *dims;
+  WC_REQUIRE(w && tokens_dev && feat && hidden_out && out_out && workspace && offset_dev && k_cache && v_cache,
+             "wc_drafter_forward: NULL argument");
+  WC_REQUIRE(al16(workspace), "wc_drafter_forward: workspace must be 16-byte aligned");
+  WC_REQUIRE(rows >= 1, "wc_drafter_forward: rows must be positive");
+  WC_REQUIRE(kv_dtype == WC_F32 || kv_dtype == WC_BF16, "wc_drafter_forward: kv dtype must be f32 or bf16");
+  WC_REQUIRE(feat_ld >= d.hidden, "wc_drafter_forward: feature row stride smaller than hidden_size");
+  WC_REQUIRE(feat_row_dev == nullptr || rows == 1, "wc_drafter_forward: a gathered feature row needs rows == 1");
+  WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
+             "wc_drafter_forward: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
+  WC_REQUIRE(mask_dev == nullptr || mask_ld >= rows, "wc_drafter_forward: mask row stride too small");
+  WC_REQUIRE(w->embed && al16(w->embed) && w->final_norm && w->rope_cos && w->rope_sin && w->rope_max_pos > 0,
+             "wc_drafter_forward: embedding / final norm / rope table missing");
+  WC_REQUIRE(w->rope_max_pos >= capacity, "wc_drafter_forward: rope table (%d positions) shorter than capacity %d",
+             w->rope_max_pos, capacity);
+  const int H = d.heads, Hk = d.kv_heads, D = d.head_dim, rep = H / Hk;
+  const int tile_rows = std::min(WC_MAX_STEP_ROWS, kMaxQV / rep);
+  WC_REQUIRE(tile_rows >= 1, "wc_drafter_forward: GQA group of %d heads too large", rep);
+  WC_REQUIRE(n_rows_dev == nullptr || rows <= tile_rows,
+             "wc_drafter_forward: a device row count needs rows <= %d for this head grouping", tile_rows);
+  for (int li = 0; li < d.num_layers; ++li) {
+    const wc_layer_weights& L = w->layers[li];
+    WC_REQUIRE(L.in_norm && L.post_norm && L.q && L.k && L.v && L.o && L.q_norm && L.k_norm && L.gate && L.up &&
+                   L.down && k_cache[li] && v_cache[li],
+               "wc_drafter_forward: layer %d has a NULL weight or cache", li);
+    WC_REQUIRE(al16(L.q) && al16(L.k) && al16(L.v) && al16(L.o) && al16(L.gate) && al16(L.up) && al16(L.down),
+               "wc_drafter_forward: layer %d weights must be 16-byte aligned", li);
+    if (L.aux_norm)
+      WC_REQUIRE(L.aux_q && L.aux_k && L.aux_v && al16(L.aux_q) && al16(L.aux_k) && al16(L.aux_v),
+                 "wc_drafter_forward: layer %d aux projections missing", li);
+  }
+  const DrafterWs ws = drafter_ws(d, workspace);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  const int nqkv = (H + 2 * Hk) * D;
+  const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunk - 1) / kAttnChunk));
+
+  for (int t0 = 0; t0 < rows; t0 += tile_rows) {
+    const int tr = std::min(tile_rows, rows - t0);
+    const bool last_tile = t0 + tr >= rows;
+    for (int li = 0; li < d.num_layers; ++li) {
+      const wc_layer_weights& L = w->layers[li];
+      const bool last_layer = li == d.num_layers - 1;
+      // residual-stream input of this layer: the feature (layer 0) or the previous layer's output
+      InSeg xin{};
+      xin.dtype = WC_F32;
+      xin.K = d.hidden;
+      if (li == 0) {
+        xin.x = feat + (feat_row_dev ? 0 : t0 * feat_ld);
+        xin.ld = feat_ld;
+        xin.row_idx = feat_row_dev;
+        xin.row_add = feat_row_dev ? feat_row_add : 0;
+      } else {
+        xin.x = hidden_out + t0 * d.hidden;
+        xin.ld = d.hidden;
+      }
+
+      // 1. QKV (dual stream on layers with the token embedding)
+      GemvArgs q = gemv_defaults();
+      q.in[0] = xin;
+      q.in[0].gain = u16(L.in_norm);
+      q.ldw[0] = d.hidden;
+      q.w[0][0] = u16(L.q);
+      q.w[1][0] = u16(L.k);
+      q.w[2][0] = u16(L.v);
+      q.n_in = 1;
+      if (L.aux_norm) {
+        InSeg e{};
+        e.x = w->embed;
+        e.ld = d.hidden;
+        e.dtype = WC_BF16;
+        e.row_idx = tokens_dev + t0;
+        e.gain = u16(L.aux_norm);
+        e.K = d.hidden;
+        q.in[1] = e;
+        q.ldw[1] = d.hidden;
+        q.w[0][1] = u16(L.aux_q);
+        q.w[1][1] = u16(L.aux_k);
+        q.w[2][1] = u16(L.aux_v);
+        q.n_in = 2;
+      }
+      q.n_seg = 3;
+      q.seg_start[1] = H * D;
+      q.seg_start[2] = (H + Hk) * D;
+      q.seg_start[3] = nqkv;
+      q.N = nqkv;
+      q.M = tr;
+      q.m_dev = n_rows_dev;
+      q.eps = d.eps;
+      q.epi = kEpiStore;
+      q.y = ws.qkv;
+      q.ldy = nqkv;
+      if (int rc = launch_gemv(q, 1, s)) return rc;
+
+      // 2. attention with q/k norm, RoPE and the KV append
+      AttnArgs at{};
+      at.qkv = ws.qkv;
+      at.ld_qkv = nqkv;
+      at.H = H;
+      at.Hk = Hk;
+      at.rows = tr;
+      at.n_rows_dev = n_rows_dev;
+      at.q_gain = u16(L.q_norm);
+      at.k_gain = u16(L.k_norm);
+      at.eps = d.eps;
+      at.scale = 1.f / sqrtf(static_cast<float>(D));
+      at.rope_cos = w->rope_cos;
+      at.rope_sin = w->rope_sin;
+      at.rope_max = w->rope_max_pos;
+      at.positions = positions_dev ? positions_dev + t0 : nullptr;
+      at.kc = k_cache[li];
+      at.vc = v_cache[li];
+      at.cap = capacity;
+      at.offset_dev = offset_dev;
+      at.offset_add = offset_add + t0;
+      at.mask = mask_dev ? mask_dev + t0 * mask_ld : nullptr;
+      at.mask_ld = mask_ld;
+      at.window = d.window;
+      at.partial = ws.partial;
+      at.counters = ws.counters + 2;
+      at.out = ws.attn;
+      at.ld_out = H * D;
+      if (int rc = launch_attention(at, D, kv_dtype, splits, tr * rep, s)) return rc;
+
+      // 3. o_proj with the residual: h1 = h + W_o . o
+      GemvArgs o = gemv_defaults();
+      o.in[0].x = ws.attn;
+      o.in[0].ld = H * D;
+      o.in[0].dtype = WC_F32;
+      o.in[0].K = H * D;
+      o.n_in = 1;
+      o.ldw[0] = H * D;
+      o.w[0][0] = u16(L.o);
+      o.N = d.hidden;
+      o.seg_start[1] = o.N;
+      o.M = tr;
+      o.m_dev = n_rows_dev;
+      o.eps = d.eps;
+      o.epi = kEpiResidual;
+      o.res = static_cast<const float*>(xin.x);
+      o.ldres = xin.ld;
+      o.res_row_idx = xin.row_idx;
+      o.res_row_add = xin.row_add;
+      o.y = ws.h1;
+      o.ldy = d.hidden;
+      if (int rc = launch_gemv(o, 1, s)) return rc;
+
+      // 4. gate / up with SiLU(gate) * up
+      GemvArgs gu = gemv_defaults();
+      gu.in[0].x = ws.h1;
+      gu.in[0].ld = d.hidden;
+      gu.in[0].dtype = WC_F32;
+      gu.in[0].gain = u16(L.post_norm);
+      gu.in[0].K = d.hidden;
+      gu.n_in = 1;
+      gu.ldw[0] = d.hidden;
+      gu.w[0][0] = u16(L.gate);
+      gu.w[1][0] = u16(L.up);
+      gu.N = d.inter;
+      gu.M = tr;
+      gu.m_dev = n_rows_dev;
+      gu.eps = d.eps;
+      gu.epi = kEpiSiluPair;
+      gu.y = ws.act;
+      gu.ldy = d.inter;
+      if (int rc = launch_gemv(gu, 1, s)) return rc;
+
+      // 5. down with the residual; the last layer also writes out = RMSNorm(h)
+      GemvArgs dn = gemv_defaults();
+      dn.in[0].x = ws.act;
+      dn.in[0].ld = d.inter;
+      dn.in[0].dtype = WC_F32;
+      dn.in[0].K = d.inter;
+      dn.n_in = 1;
+      dn.ldw[0] = d.inter;
+      dn.w[0][0] = u16(L.down);
+      dn.N = d.hidden;
+      dn.seg_start[1] = dn.N;
+      dn.M = tr;
+      dn.m_dev = n_rows_dev;
+      dn.eps = d.eps;
+      dn.epi = kEpiResidual;
+      dn.res = ws.h1;
+      dn.ldres = d.hidden;
+      dn.y = hidden_out + t0 * d.hidden;
+      dn.ldy = d.hidden;
+      if (last_layer) {
+        dn.fin_counter = ws.counters + 1;
+        dn.fin_gain = u16(w->final_norm);
+        dn.fin_out = out_out + t0 * d.hidden;
+        dn.ld_fin = d.hidden;
+        if (advance_dev && last_tile) {
+          dn.adv_dst = advance_dev;
+          dn.adv_src = offset_dev;
+          dn.adv_add = offset_add + t0;
+        }
+      }
+      if (int rc = launch_gemv(dn, 1, s)) return rc;
+    }
+  }
+  return WC_OK;
+}
+
+int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* out_rows, int64_t out_ld,
+                  const int32_t* out_row_dev, int out_row_add, int rows, float* logits_out, int64_t logits_ld,
+                  int32_t* token_out, int32_t* row_out, const wc_gumbel* gumbel, void* workspace,
+                  wc_stream_t stream) {
+  if (int rc = check_dims(dims)) return rc;
+  WC_REQUIRE(w && w->head && out_rows && token_out && workspace, "wc_draft_head: NULL argument");
+  WC_REQUIRE(al16(w->head) && al16(workspace), "wc_draft_head: head weight / workspace must be 16-byte aligned");
+  WC_REQUIRE(rows >= 1, "wc_draft_head: rows must be positive");
+  WC_REQUIRE(out_row_dev == nullptr || rows == 1, "wc_draft_head: a gathered input row needs rows == 1");
+  WC_REQUIRE(out_ld >= dims->hidden, "wc_draft_head: input row stride smaller than hidden_size");
+  WC_REQUIRE(logits_out == nullptr || logits_ld >= dims->head_rows, "wc_draft_head: logits row stride too small");
+  WC_REQUIRE(gumbel == nullptr || (gumbel->round_dev && gumbel->temperature > 0.f),
+             "wc_draft_head: gumbel needs a round counter and a positive temperature");
+  const DrafterWs ws = drafter_ws(*dims, workspace);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  for (int t0 = 0; t0 < rows; t0 += WC_MAX_STEP_ROWS) {
+    const int tr = std::min(WC_MAX_STEP_ROWS, rows - t0);
+    GemvArgs h = gemv_defaults();
+    h.in[0].x = out_rows + (out_row_dev ? 0 : t0 * out_ld);
+    h.in[0].ld = out_ld;
+    h.in[0].dtype = WC_F32;
+    h.in[0].row_idx = out_row_dev;
+    h.in[0].row_add = out_row_dev ? out_row_add : 0;
+    h.in[0].K = dims->hidden;
+    h.n_in = 1;
+    h.ldw[0] = dims->hidden;
+    h.w[0][0] = u16(w->head);
+    h.N = dims->head_rows;
+    h.seg_start[1] = h.N;
+    h.M = tr;
+    h.eps = dims->eps;
+    h.epi = kEpiArgmax;
+    h.y = logits_out ? logits_out + t0 * logits_ld : nullptr;
+    h.ldy = logits_ld;
+    h.slots = ws.slots;
+    h.counter = ws.counters;
+    h.d2t = w->d2t;
+    h.tok_out = token_out + t0;
+    h.row_out = row_out ? row_out + t0 : nullptr;
+    if (gumbel) {
+      h.use_gumbel = 1;
+      h.gumbel.seed = gumbel->seed;
+      h.gumbel.round_dev = gumbel->round_dev;
+      h.gumbel.purpose = gumbel->purpose + t0;
+      h.gumbel.inv_temperature = 1.f / gumbel->temperature;
+    }
+    if (int rc = launch_gemv(h, dims->head_rows >= 8192 ? 2 : 1, s)) return rc;
+  }
+  return WC_OK;
+}
+
+}  // extern "C"

@@ -6,6 +6,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <string>
 
 #include "../../include/woodcock_hip.h"
@@ -128,9 +129,9 @@ __device__ __forceinline__ void atomic_store_u32(unsigned int* p, unsigned int v
 // re-launchable without a host-side clear.
 __device__ __forceinline__ bool last_block_done(unsigned int* counter, unsigned int total) {
   __shared__ bool s_last;
+  __threadfence();  // every thread releases its own writes (device scope: other XCDs' L2s)
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();  // release this block's writes (device scope)
     unsigned int prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     s_last = (prev == total - 1);
   }
