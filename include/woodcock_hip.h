@@ -120,6 +120,7 @@ int wc_kv_compact(void* const* k_layers, void* const* v_layers, int n_layers, in
  * include/woodcock/drafter.h:16-24). */
 typedef struct wc_drafter_dims {
   int32_t hidden, num_layers, heads, kv_heads, head_dim, inter, target_hidden, num_features, head_rows;
+  int32_t vocab; /* embedding rows: token ids read on the device are clamped to [0, vocab) */
   float eps;
   int32_t window; /* 0 = full attention */
 } wc_drafter_dims;

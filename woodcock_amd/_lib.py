@@ -55,7 +55,7 @@ class DrafterDims(C.Structure):
     """Mirror of wc_drafter_dims."""
 
     _fields_ = [(n, C.c_int32) for n in ("hidden", "num_layers", "heads", "kv_heads", "head_dim", "inter",
-                                          "target_hidden", "num_features", "head_rows")] + \
+                                          "target_hidden", "num_features", "head_rows", "vocab")] + \
                [("eps", C.c_float), ("window", C.c_int32)]
 
 

@@ -177,7 +177,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   const int rep = a.H / a.Hk;
   const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
   const int offset = *a.offset_dev + a.offset_add;
-  const int T = offset + nr;
+  const int T = min(offset + nr, a.cap);  // never past the cache capacity
   const int QV = nr * rep;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int nw = kAttnThreads / kWave;
@@ -406,6 +406,7 @@ static int check_dims(const wc_drafter_dims* d) {
   WC_REQUIRE(d->num_layers >= 1 && d->num_layers <= WC_MAX_DRAFTER_LAYERS, "num_layers must be in 1..%d",
              WC_MAX_DRAFTER_LAYERS);
   WC_REQUIRE(d->head_rows >= 1, "head_rows must be positive");
+  WC_REQUIRE(d->vocab >= 1, "vocab must be positive");
   return WC_OK;
 }
 
@@ -556,6 +557,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
         e.ld = d.hidden;
         e.dtype = WC_BF16;
         e.row_idx = tokens_dev + t0;
+        e.max_row = d.vocab;
         e.gain = u16(L.aux_norm);
         e.K = d.hidden;
         q.in[1] = e;

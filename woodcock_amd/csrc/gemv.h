@@ -39,6 +39,7 @@ struct InSeg {
   int row_add;
   const uint16_t* gain;    // RMSNorm gain [K] (bf16) or NULL: no norm
   int K;                   // multiple of 8
+  int max_row;             // > 0: gathered rows are clamped to [0, max_row)
 };
 
 enum Epi { kEpiStore = 0, kEpiResidual = 1, kEpiSiluPair = 2, kEpiArgmax = 3 };
@@ -103,7 +104,11 @@ __device__ __forceinline__ float load_in(const InSeg& s, int64_t row, int k) {
   return s.dtype == WC_BF16 ? bf16_to_float(static_cast<const uint16_t*>(s.x)[i]) : static_cast<const float*>(s.x)[i];
 }
 
-__device__ __forceinline__ int in_row(const InSeg& s, int m) { return (s.row_idx ? s.row_idx[m] : m) + s.row_add; }
+__device__ __forceinline__ int in_row(const InSeg& s, int m) {
+  int r = (s.row_idx ? s.row_idx[m] : m) + s.row_add;
+  if (s.max_row > 0) r = min(max(r, 0), s.max_row - 1);
+  return r;
+}
 
 // Philox4x64-10 (Salmon et al., SC'11): same stream as the host oracle.
 __device__ __forceinline__ void philox4x64(unsigned long long c[4], unsigned long long k0, unsigned long long k1) {

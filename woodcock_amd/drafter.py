@@ -70,7 +70,8 @@ class Drafter:
         c = self.cfg
         self.dims = _lib.DrafterDims(c.hidden_size, c.num_layers, c.num_heads, c.num_kv_heads, c.head_dim,
                                      c.intermediate_size, c.target_hidden_size, c.num_features,
-                                     self._head.shape[0], c.rms_norm_eps, int(c.window or 0))
+                                     self._head.shape[0], self.w["embed_tokens.weight"].shape[0],
+                                     c.rms_norm_eps, int(c.window or 0))
         self._ensure_rope(rope_positions)
         W = _lib.DrafterWeights()
         W.embed = self.w["embed_tokens.weight"].data_ptr()
