@@ -231,3 +231,29 @@ def test_gumbel_draws_follow_softmax(cuda):
     a = d.draft(out, gumbel=(11, rnd, 5, T)).item()
     b = d.draft(out, gumbel=(11, rnd, 5, T)).item()
     assert a == b
+
+
+@pytest.mark.parametrize("head_dim,heads,kv_heads", [(8, 4, 2), (32, 4, 1), (64, 4, 2), (128, 4, 4), (256, 2, 1)])
+def test_head_dim_sweep_multi_row_forward(cuda, head_dim, heads, kv_heads):
+    """Every instantiated head_dim / GQA grouping, 1-row and 3-row forwards with
+    appends, against the oracle (fp32 cache, 1e-5)."""
+    from woodcock_amd.config import DrafterConfig
+    from woodcock_amd.drafter import Drafter
+    from woodcock_amd.synthetic import random_drafter, to_bits
+
+    cfg = DrafterConfig(hidden_size=128, num_layers=1, num_heads=heads, num_kv_heads=kv_heads, head_dim=head_dim,
+                        intermediate_size=192, vocab_size=300, target_hidden_size=64, rope_theta=1e6)
+    w = random_drafter(cfg, seed=head_dim, device=cuda)
+    d = Drafter(cfg, dict(w), cuda, torch.float32)
+    od = core.Drafter(cfg.as_dict(), {k: to_bits(v) for k, v in w.items()})
+    cache, oc = d.make_cache(64), od.make_cache(64)
+    rng = np.random.default_rng(head_dim)
+    for L in (5, 1, 3, 1):
+        toks = rng.integers(0, cfg.vocab_size, L)
+        feat = rng.standard_normal((L, cfg.hidden_size)).astype(np.float32)
+        hid, out = d(torch.from_numpy(toks), torch.from_numpy(feat).to(cuda), cache)
+        ohid, oout = od.forward(toks, feat, oc)
+        assert _rel(hid.cpu().numpy(), ohid) <= 1e-5, L
+        assert _rel(out.cpu().numpy(), oout) <= 1e-5, L
+        n = oc.offset
+        assert _rel(cache[0].keys[0, :, :n].cpu().numpy(), oc.keys_f32(0)[:, :n]) <= 1e-5, L

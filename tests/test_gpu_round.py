@@ -1,0 +1,163 @@
+"""The fused greedy chain round (python/woodcock/spec.py:331-374) on the GPU vs an
+oracle round built from the CPU drafter restatement, round after round:
+identical drafted tokens, accepted lengths and accepted tokens; root outputs
+and drafter caches within the fp32 tolerance; exactly one host sync per
+round; a captured HIP graph replays to the same results as eager rounds."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from oracle import sampling as osamp
+
+pytestmark = pytest.mark.gpu
+
+K = 4
+
+
+def small_cfg():
+    from woodcock_amd.config import DrafterConfig
+
+    return DrafterConfig(hidden_size=256, num_layers=1, num_heads=4, num_kv_heads=2, head_dim=64,
+                         intermediate_size=512, vocab_size=4096, target_hidden_size=192, rope_theta=1e6)
+
+
+def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256):
+    from woodcock_amd.drafter import Drafter
+    from woodcock_amd.spec import ChainRound
+    from woodcock_amd.synthetic import SyntheticTarget, draft_vocab, random_drafter, to_bits
+
+    cfg = small_cfg()
+    ids = draft_vocab(cfg.vocab_size, 1024, seed=seed)
+    w = random_drafter(cfg, seed=seed, device=cuda, head_rows=1024)
+    d = Drafter(cfg, dict(w), cuda, kv_dtype)
+    d._vocab_ids = torch.from_numpy(ids).to(cuda)
+    d._build_structs(d._rope[0].shape[0])
+    rnd = ChainRound(d, K, cap)
+    od = core.Drafter(cfg.as_dict(), {k: to_bits(v) for k, v in w.items()})
+    od.d2t = ids
+    oc = od.make_cache(cap, kv_bf16=kv_dtype == torch.bfloat16)
+    g = torch.Generator(device=cuda).manual_seed(seed)
+    c = rnd.cache[0]
+    c.keys[0, :, :ctx] = torch.randn(c.keys[0, :, :ctx].shape, generator=g, device=cuda).to(kv_dtype)
+    c.values[0, :, :ctx] = torch.randn(c.values[0, :, :ctx].shape, generator=g, device=cuda).to(kv_dtype)
+    if kv_dtype == torch.bfloat16:
+        oc.k[0][:] = to_bits(c.keys[0])
+        oc.v[0][:] = to_bits(c.values[0])
+    else:
+        oc.k[0][:] = c.keys[0].cpu().numpy()
+        oc.v[0][:] = c.values[0].cpu().numpy()
+    oc.offset = ctx
+    root = torch.randn(1, cfg.hidden_size, generator=g, device=cuda)
+    root = root / root.pow(2).mean().sqrt()
+    rnd.set_root(ctx, root)
+    target = SyntheticTarget(K, cfg.vocab_size, cfg.target_hidden_size, device=cuda, seed=seed + 1)
+    return cfg, d, rnd, od, oc, target, root.cpu().numpy()
+
+
+def oracle_round(od, oc, root_out, root_fb, logits, taps):
+    drafts, out, fb = [], root_out, root_fb
+    base = oc.offset
+    for k in range(K):
+        z = od.logits(out)
+        drafts.append(int(od.d2t[core.argmax(z[0])]))
+        if k < K - 1:
+            hid, out = od.forward([drafts[-1]], fb, oc)
+            fb = od.feedback(hid, out)
+    oc.offset = base
+    a, nxt = osamp.verify_chain_greedy(logits, drafts)
+    acc = drafts[:a] + [nxt]
+    g = od.fuse([t[: a + 1] for t in taps])
+    hid, out = od.forward(acc, g, oc)
+    return drafts, a, acc, out[-1:], od.feedback(hid[-1:], out[-1:])
+
+
+def gpu_round(rnd, target, n_agree):
+    rnd.enqueue_draft()
+    target.plant(rnd.drafts, n_agree)
+    rnd.enqueue_verify(target.logits)
+    rnd.enqueue_commit(target.taps)
+    rnd.enqueue_readback()
+    return rnd.finish()
+
+
+def _rel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)).max() / np.abs(b).max())
+
+
+def test_rounds_match_oracle_round(cuda):
+    cfg, d, rnd, od, oc, target, root = setup(cuda, 1)
+    root_out = root_fb = root
+    pattern = [2, 0, 4, 1, 3, 2, 4, 0]
+    for r, n_agree in enumerate(pattern):
+        res = gpu_round(rnd, target, n_agree)
+        logits = target.logits.cpu().numpy()
+        taps = [t.float().cpu().numpy() for t in target.taps]
+        drafts, a, acc, root_out, root_fb = oracle_round(od, oc, root_out, root_fb, logits, taps)
+        assert rnd.drafts.tolist() == drafts, f"round {r}"
+        assert res.n_accepted == a == n_agree, f"round {r}"
+        assert res.tokens == acc, f"round {r}"
+        assert _rel(rnd.upd_out[a].cpu().numpy(), root_out[0]) <= 1e-5, f"round {r}"
+        n = oc.offset
+        assert rnd.committed() == n
+        k_gpu = rnd.cache[0].keys[0, :, :n].float().cpu().numpy()
+        assert _rel(k_gpu, oc.keys_f32(0)[:, :n]) <= 1e-5, f"round {r}"
+    assert rnd.syncs == len(pattern)
+
+
+def test_enqueue_never_synchronises(cuda):
+    """Everything between two verdict reads is asynchronous: torch's sync debug
+    mode raises on any implicit host synchronisation while a round is enqueued."""
+    cfg, d, rnd, od, oc, target, root = setup(cuda, 2)
+    gpu_round(rnd, target, 1)  # warm-up (workspaces, attributes)
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        rnd.enqueue_draft()
+        target.plant(rnd.drafts, 2)
+        rnd.enqueue_verify(target.logits)
+        rnd.enqueue_commit(target.taps)
+        rnd.enqueue_readback()
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    res = rnd.finish()
+    assert res.n_accepted == 2
+
+
+def test_graph_replay_equals_eager_rounds(cuda):
+    """One captured graph per round shape, replayed with host work in between;
+    every replay matches the eager round bit for bit."""
+    pattern = [2, 3, 0, 4, 2, 1]
+    _, _, eager, _, _, te, _ = setup(cuda, 3)
+    eager_res = [gpu_round(eager, te, n) for n in pattern]
+    eager_k = eager.cache[0].keys.clone()
+
+    _, _, rnd, _, _, tg, _ = setup(cuda, 3)
+    gpu_round(rnd, tg, 2)  # warm-up outside capture
+    _, _, rnd, _, _, tg, _ = setup(cuda, 3)  # fresh identical state
+    n_agree = torch.zeros(1, dtype=torch.int32)
+    graphs = {}
+    s = torch.cuda.Stream()
+    results = []
+    for n in pattern:
+        if n not in graphs:
+            s.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            # capture without executing: the state must not move
+            snap = (rnd.state.clone(), rnd.verdict.clone(), rnd.upd_out.clone(), rnd.upd_hid.clone(),
+                    rnd.cache[0].keys.clone(), rnd.cache[0].values.clone(), tg.logits.clone())
+            with torch.cuda.graph(g, stream=s):
+                rnd.enqueue_draft()
+                tg.plant(rnd.drafts, n)
+                rnd.enqueue_verify(tg.logits)
+                rnd.enqueue_commit(tg.taps)
+                rnd.enqueue_readback()
+            torch.cuda.synchronize()
+            assert torch.equal(snap[0], rnd.state) and torch.equal(snap[4], rnd.cache[0].keys)
+            graphs[n] = g
+        graphs[n].replay()
+        results.append(rnd.finish())
+        _ = torch.ones(3, device=cuda).sum().item()  # eager work between replays
+    for r, (a, b) in enumerate(zip(results, eager_res)):
+        assert (a.n_accepted, a.tokens) == (b.n_accepted, b.tokens), f"replay {r}"
+    assert torch.equal(rnd.cache[0].keys, eager_k)
+    del n_agree

@@ -20,13 +20,17 @@ namespace wc {
 // ------------------------------------------------------------------ workspace
 
 constexpr int kAttnThreads = 256;
-constexpr int kAttnChunk = 32;  // keys staged per iteration
+constexpr int kAttnChunkMax = 32;  // keys staged per iteration (fewer for head_dim 256)
+template <int D>
+constexpr int attn_chunk() { return D >= 256 ? 16 : kAttnChunkMax; }
 constexpr int kMaxQV = 64;      // query vectors (rows x GQA group) per attention block
 constexpr int kMaxSplits = 32;
 constexpr int kMaxKvHeads = 64;
 
 struct DrafterWs {
-  unsigned int* counters;  // [0] head, [1] final, [2 + kh] attention
+  unsigned int* head_ctr;  // tree counters (kTreeCounterBytes each)
+  unsigned int* fin_ctr;
+  unsigned int* attn_ctr;  // [kv_heads] tree counters
   unsigned long long* slots;
   float* qkv;
   float* attn;
@@ -49,8 +53,10 @@ static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
   };
   const size_t R = WC_MAX_STEP_ROWS;
   const size_t nqkv = static_cast<size_t>(d.heads + 2 * d.kv_heads) * d.head_dim;
-  w.counters = reinterpret_cast<unsigned int*>(take(4 * (2 + kMaxKvHeads)));
-  w.slots = reinterpret_cast<unsigned long long*>(take(8 * R));
+  w.head_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
+  w.fin_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
+  w.attn_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes * static_cast<size_t>(d.kv_heads)));
+  w.slots = reinterpret_cast<unsigned long long*>(take(8 * R * kSlots * kSlotStride));
   w.qkv = reinterpret_cast<float*>(take(4 * R * nqkv));
   w.attn = reinterpret_cast<float*>(take(4 * R * d.heads * d.head_dim));
   w.h1 = reinterpret_cast<float*>(take(4 * R * d.hidden));
@@ -81,7 +87,7 @@ struct AttnArgs {
   int64_t mask_ld;
   int window;
   float* partial;  // [Hk][S][kMaxQV][D+2]
-  unsigned int* counters;
+  unsigned int* counters;  // [Hk] tree counters
   float* out;  // [rows][H*D]
   int64_t ld_out;
 };
@@ -121,50 +127,44 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-// Normalise (gain) and rotate one head vector src[D] at position pos into dst[D]
-// (LDS).  Executed by one wave; D <= 256.
+// Normalise (gain) and rotate one head vector src[D] at position pos
+// (rotate-half RoPE, src/backends/cpu_ops.cpp:61-77).  Executed by one wave:
+// lane j owns the pairs (p, p + D/2) for p = j, j + 64, ..., so every value a
+// lane returns was computed by that lane alone -- no cross-lane LDS traffic.
+// lo[e] / hi[e] are elements p and p + D/2 of pair p = lane + 64 e (valid when
+// p < D/2).
 template <int D>
-__device__ __forceinline__ void norm_rope_vec(const float* src, const uint16_t* gain, float eps, const float* ct,
-                                              const float* st, int pos, float* dst) {
+struct PairRegs {
+  static constexpr int kHalf = D / 2;
+  static constexpr int kPPL = (kHalf + kWave - 1) / kWave;
+  float lo[kPPL], hi[kPPL];
+};
+
+template <int D>
+__device__ __forceinline__ void norm_rope_pairs(const float* src, const uint16_t* gain, float eps, const float* ct,
+                                                const float* st, int pos, PairRegs<D>& r) {
   const int lane = threadIdx.x % kWave;
-  constexpr int EPL = (D + kWave - 1) / kWave;
-  float x[EPL];
+  constexpr int half = PairRegs<D>::kHalf, PPL = PairRegs<D>::kPPL;
   float ss = 0.f;
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const int i = lane + e * kWave;
-    x[e] = i < D ? src[i] : 0.f;
-    ss = fmaf(x[e], x[e], ss);
+  for (int e = 0; e < PPL; ++e) {
+    const int p = lane + e * kWave;
+    r.lo[e] = p < half ? src[p] : 0.f;
+    r.hi[e] = p < half ? src[p + half] : 0.f;
+    ss = fmaf(r.lo[e], r.lo[e], ss);
+    ss = fmaf(r.hi[e], r.hi[e], ss);
   }
   ss = wave_sum(ss);
   const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
 #pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const int i = lane + e * kWave;
-    if (i < D) dst[i] = x[e] * inv * bf16_to_float(gain[i]);
-  }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  constexpr int half = D / 2;
-  float r1[EPL], r2[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const int i = lane + e * kWave;
-    if (i < half) {
-      const float c = ct[static_cast<int64_t>(pos) * half + i], s = st[static_cast<int64_t>(pos) * half + i];
-      const float x1 = dst[i], x2 = dst[i + half];
-      r1[e] = x1 * c - x2 * s;
-      r2[e] = x2 * c + x1 * s;
-    }
-  }
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) {
-    const int i = lane + e * kWave;
-    if (i < half) {
-      dst[i] = r1[e];
-      dst[i + half] = r2[e];
+  for (int e = 0; e < PPL; ++e) {
+    const int p = lane + e * kWave;
+    if (p < half) {
+      const float x1 = r.lo[e] * inv * bf16_to_float(gain[p]);
+      const float x2 = r.hi[e] * inv * bf16_to_float(gain[p + half]);
+      const float c = ct[static_cast<int64_t>(pos) * half + p], sn = st[static_cast<int64_t>(pos) * half + p];
+      r.lo[e] = x1 * c - x2 * sn;
+      r.hi[e] = x2 * c + x1 * sn;
     }
   }
 }
@@ -172,6 +172,7 @@ __device__ __forceinline__ void norm_rope_vec(const float* src, const uint16_t* 
 template <int D, typename KT>
 __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   extern __shared__ float lds[];
+  constexpr int kAttnChunk = attn_chunk<D>();
   constexpr int ACC = (kMaxQV * D + kAttnThreads - 1) / kAttnThreads;
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
   const int rep = a.H / a.Hk;
@@ -198,7 +199,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
     const int l = v / rep, h = kh * rep + v % rep;
     int pos = a.positions ? a.positions[l] : offset + l;
     pos = min(max(pos, 0), a.rope_max - 1);
-    norm_rope_vec<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, a.eps, a.rope_cos, a.rope_sin, pos, qs + v * D);
+    PairRegs<D> r;
+    norm_rope_pairs<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, a.eps, a.rope_cos, a.rope_sin, pos, r);
+#pragma unroll
+    for (int e = 0; e < PairRegs<D>::kPPL; ++e) {
+      const int p = lane + e * kWave;
+      if (p < D / 2) {
+        qs[v * D + p] = r.lo[e];
+        qs[v * D + p + D / 2] = r.hi[e];
+      }
+    }
   }
   // new keys / values whose slot falls in this block's range: norm + rope, append
   for (int l = wave; l < nr; l += nw) {
@@ -206,12 +216,18 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
     if (t < kb || t >= ke) continue;
     int pos = a.positions ? a.positions[l] : offset + l;
     pos = min(max(pos, 0), a.rope_max - 1);
-    float* tmp = ks + wave * D;  // scratch row (ks is free until the key loop; kAttnChunk >= waves)
-    norm_rope_vec<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, a.eps, a.rope_cos, a.rope_sin, pos, tmp);
-    for (int i = lane; i < D; i += kWave) {
-      kv_store<KT>(kc, static_cast<int64_t>(t) * D + i, tmp[i]);
-      kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, a.qkv[l * a.ld_qkv + (a.H + a.Hk + kh) * D + i]);
+    PairRegs<D> r;
+    norm_rope_pairs<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, a.eps, a.rope_cos, a.rope_sin, pos, r);
+#pragma unroll
+    for (int e = 0; e < PairRegs<D>::kPPL; ++e) {
+      const int p = lane + e * kWave;
+      if (p < D / 2) {
+        kv_store<KT>(kc, static_cast<int64_t>(t) * D + p, r.lo[e]);
+        kv_store<KT>(kc, static_cast<int64_t>(t) * D + p + D / 2, r.hi[e]);
+      }
     }
+    for (int i = lane; i < D; i += kWave)
+      kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, a.qkv[l * a.ld_qkv + (a.H + a.Hk + kh) * D + i]);
   }
   if (threadIdx.x < kMaxQV) {
     s_m[threadIdx.x] = -INFINITY;
@@ -293,44 +309,66 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
     const int idx = threadIdx.x + e * kAttnThreads;
     if (idx < QV * D) {
       const int v = idx / D, i = idx - v * D;
-      part[v * (D + 2) + 2 + i] = acc[e];
+      publish_f32(&part[v * (D + 2) + 2 + i], acc[e]);
     }
   }
   if (threadIdx.x < QV) {
-    part[threadIdx.x * (D + 2)] = s_m[threadIdx.x];
-    part[threadIdx.x * (D + 2) + 1] = s_l[threadIdx.x];
+    publish_f32(&part[threadIdx.x * (D + 2)], s_m[threadIdx.x]);
+    publish_f32(&part[threadIdx.x * (D + 2) + 1], s_l[threadIdx.x]);
   }
-  if (!last_block_done(&a.counters[kh], S)) return;
+  if (!last_block_done(a.counters + kh * (kTreeCounterBytes / 4), S, split)) return;
 
-  // merge the splits of this kv head
+  // merge the splits of this kv head: one thread per query vector loads every
+  // split's (m, l) back to back and forms the merge weights, then every thread
+  // combines its (vector, element) outputs
+  __shared__ float s_w[kMaxSplits * kMaxQV], s_den[kMaxQV];
   const float* base = a.partial + static_cast<int64_t>(kh) * S * kMaxQV * (D + 2);
+  if (threadIdx.x < QV) {
+    const int v = threadIdx.x;
+    float ms[kMaxSplits], ls[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+      if (s < S) {
+        ms[s] = fetch_f32(&base[(s * kMaxQV + v) * (D + 2)]);
+        ls[s] = fetch_f32(&base[(s * kMaxQV + v) * (D + 2) + 1]);
+      }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s)
+      if (s < S) M = fmaxf(M, ms[s]);
+    float den = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) {
+      if (s < S) {
+        const float wgt = ms[s] == -INFINITY ? 0.f : expf(ms[s] - M);
+        s_w[s * kMaxQV + v] = wgt;
+        den = fmaf(ls[s], wgt, den);
+      }
+    }
+    s_den[v] = den;
+  }
+  __syncthreads();
   for (int idx = threadIdx.x; idx < QV * D; idx += kAttnThreads) {
     const int v = idx / D, i = idx - v * D;
-    float M = -INFINITY;
-    for (int s = 0; s < S; ++s) M = fmaxf(M, base[(s * kMaxQV + v) * (D + 2)]);
-    float num = 0.f, den = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float* p = base + (s * kMaxQV + v) * (D + 2);
-      if (p[0] == -INFINITY) continue;
-      const float wgt = expf(p[0] - M);
-      den = fmaf(p[1], wgt, den);
-      num = fmaf(p[2 + i], wgt, num);
-    }
+    float num = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < S; ++s) num = fmaf(s_w[s * kMaxQV + v], fetch_f32(&base[(s * kMaxQV + v) * (D + 2) + 2 + i]), num);
     const int l = v / rep, h = kh * rep + v % rep;
-    a.out[l * a.ld_out + h * D + i] = num / den;
+    a.out[l * a.ld_out + h * D + i] = num / s_den[v];
   }
-  if (threadIdx.x == 0) atomic_store_u32(&a.counters[kh], 0u);
 }
 
 template <int D, typename KT>
 static int launch_attention_t(const AttnArgs& a, int splits, int qv_max, hipStream_t stream) {
-  const size_t lds = sizeof(float) * (static_cast<size_t>(qv_max) * D + 2 * kAttnChunk * D +
-                                      static_cast<size_t>(qv_max) * kAttnChunk);
-  static bool attr_set = false;
-  if (lds > 64 * 1024 && !attr_set) {
+  constexpr int CH = attn_chunk<D>();
+  const size_t lds = sizeof(float) * (static_cast<size_t>(qv_max) * D + 2 * CH * D +
+                                      static_cast<size_t>(qv_max) * CH);
+  static size_t attr_bytes = 64 * 1024;  // default dynamic-LDS limit
+  if (lds > attr_bytes) {
     WC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention<D, KT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-    attr_set = true;
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    attr_bytes = lds;
   }
   hipLaunchKernelGGL((k_attention<D, KT>), dim3(splits, a.Hk), dim3(kAttnThreads), lds, stream, a);
   WC_LAUNCHED();
@@ -357,31 +395,64 @@ static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, 
 
 // ------------------------------------------------------------------ GEMV launch
 
-template <int R, bool PAIR>
-static int launch_gemv_r(const GemvArgs& a, hipStream_t s) {
-  const int blocks = (a.N + kGemvWaves * R - 1) / (kGemvWaves * R);
-  const dim3 grid(blocks), block(kGemvThreads);
-#define WC_GEMV(MMV) \
-  hipLaunchKernelGGL((k_gemv<R, MMV, PAIR, 4>), grid, block, kGemvLdsBytes, s, a)
-  if (a.M <= 1)
-    WC_GEMV(1);
-  else if (a.M <= 2)
-    WC_GEMV(2);
-  else if (a.M <= 4)
-    WC_GEMV(4);
-  else if (a.M <= 8)
-    WC_GEMV(8);
+template <int R, bool PAIR, int NIN>
+static int launch_gemv1(const GemvArgs& a, int steps, hipStream_t s) {
+  const dim3 grid((a.N + kGemvWaves * R - 1) / (kGemvWaves * R)), block(kGemvThreads);
+#define WC_G1(SV) hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, SV>), grid, block, 0, s, a)
+  if (steps <= 2)
+    WC_G1(2);
+  else if (steps <= 4)
+    WC_G1(4);
+  else if (steps <= 8)
+    WC_G1(8);
+  else if (steps <= 12)
+    WC_G1(12);
+  else if (steps <= 16)
+    WC_G1(16);
+  else if (steps <= 20)
+    WC_G1(20);
   else
-    WC_GEMV(16);
-#undef WC_GEMV
+    WC_G1(24);
+#undef WC_G1
   WC_LAUNCHED();
   return WC_OK;
 }
 
+template <bool PAIR>
+static int launch_gemvm(GemvArgs a, int max_k, hipStream_t s) {
+  const dim3 grid((a.N + kGemvWaves - 1) / kGemvWaves), block(kGemvThreads);
+  const int kr = (max_k + 511) / 512 * 512;
+  a.lds_floats = std::min(kGemvLdsBytes / 4, a.M * kr);
+  const size_t lds = sizeof(float) * static_cast<size_t>(a.lds_floats);
+#define WC_GM(MMV) hipLaunchKernelGGL((k_gemvm<1, MMV, PAIR, 4>), grid, block, lds, s, a)
+  if (a.M <= 2)
+    WC_GM(2);
+  else if (a.M <= 4)
+    WC_GM(4);
+  else if (a.M <= 8)
+    WC_GM(8);
+  else
+    WC_GM(16);
+#undef WC_GM
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+// M = 1 goes to the register-resident kernel (R rows per wave), M > 1 to the LDS-staged one.
 static int launch_gemv(const GemvArgs& a, int R, hipStream_t s) {
   if (a.M < 1 || a.M > kMaxM) return set_error(WC_E_INVALID, "gemv: rows %d not in 1..%d", a.M, kMaxM);
-  if (a.epi == kEpiSiluPair) return R >= 2 ? launch_gemv_r<2, true>(a, s) : launch_gemv_r<1, true>(a, s);
-  return R >= 2 ? launch_gemv_r<2, false>(a, s) : launch_gemv_r<1, false>(a, s);
+  int max_k = 0;
+  for (int i = 0; i < a.n_in; ++i) max_k = std::max(max_k, a.in[i].K);
+  const int steps = (max_k + 511) / 512;
+  const bool pair = a.epi == kEpiSiluPair;
+  if (a.M == 1 && steps <= kMaxSteps1) {
+    if (pair) return a.n_in == 1 ? launch_gemv1<1, true, 1>(a, steps, s) : launch_gemvm<true>(a, max_k, s);
+    if (R >= 2 && a.n_in == 1) return launch_gemv1<2, false, 1>(a, steps, s);
+    if (a.n_in == 1) return launch_gemv1<1, false, 1>(a, steps, s);
+    if (a.n_in == 2) return launch_gemv1<1, false, 2>(a, steps, s);
+    return launch_gemv1<1, false, 3>(a, steps, s);
+  }
+  return pair ? launch_gemvm<true>(a, max_k, s) : launch_gemvm<false>(a, max_k, s);
 }
 
 static GemvArgs gemv_defaults() {
@@ -446,6 +517,7 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
   WC_REQUIRE(w->fc && al16(w->fc), "wc_drafter_fuse: fc weight missing or not 16-byte aligned");
   WC_REQUIRE(tap_dtype == WC_F32 || tap_dtype == WC_BF16, "wc_drafter_fuse: tap dtype must be f32 or bf16");
   WC_REQUIRE(tap_ld >= dims->target_hidden && g_ld >= dims->hidden, "wc_drafter_fuse: bad row stride");
+  WC_REQUIRE(tap_ld % 8 == 0 && g_ld % 4 == 0, "wc_drafter_fuse: row strides must be multiples of 8 (taps) / 4");
   WC_REQUIRE(rows >= 1, "wc_drafter_fuse: rows must be positive");
   WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
              "wc_drafter_fuse: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
@@ -456,7 +528,7 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
     GemvArgs g = gemv_defaults();
     g.n_in = nf;
     for (int f = 0; f < nf; ++f) {
-      WC_REQUIRE(taps[f] != nullptr, "wc_drafter_fuse: tap %d is NULL", f);
+      WC_REQUIRE(taps[f] != nullptr && al16(taps[f]), "wc_drafter_fuse: tap %d is NULL or not 16-byte aligned", f);
       g.in[f].x = static_cast<const char*>(taps[f]) + (tap_rows_dev ? 0 : t0 * tap_ld * (tap_dtype ? 2 : 4));
       g.in[f].ld = tap_ld;
       g.in[f].dtype = tap_dtype;
@@ -492,7 +564,9 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
   WC_REQUIRE(al16(workspace), "wc_drafter_forward: workspace must be 16-byte aligned");
   WC_REQUIRE(rows >= 1, "wc_drafter_forward: rows must be positive");
   WC_REQUIRE(kv_dtype == WC_F32 || kv_dtype == WC_BF16, "wc_drafter_forward: kv dtype must be f32 or bf16");
-  WC_REQUIRE(feat_ld >= d.hidden, "wc_drafter_forward: feature row stride smaller than hidden_size");
+  WC_REQUIRE(feat_ld >= d.hidden && feat_ld % 4 == 0,
+             "wc_drafter_forward: feature row stride must be >= hidden_size and a multiple of 4");
+  WC_REQUIRE(al16(feat) && al16(hidden_out) && al16(out_out), "wc_drafter_forward: buffers must be 16-byte aligned");
   WC_REQUIRE(feat_row_dev == nullptr || rows == 1, "wc_drafter_forward: a gathered feature row needs rows == 1");
   WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
              "wc_drafter_forward: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
@@ -520,7 +594,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
   const DrafterWs ws = drafter_ws(d, workspace);
   auto s = reinterpret_cast<hipStream_t>(stream);
   const int nqkv = (H + 2 * Hk) * D;
-  const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunk - 1) / kAttnChunk));
+  const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunkMax - 1) / kAttnChunkMax));
 
   for (int t0 = 0; t0 < rows; t0 += tile_rows) {
     const int tr = std::min(tile_rows, rows - t0);
@@ -605,7 +679,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       at.mask_ld = mask_ld;
       at.window = d.window;
       at.partial = ws.partial;
-      at.counters = ws.counters + 2;
+      at.counters = ws.attn_ctr;
       at.out = ws.attn;
       at.ld_out = H * D;
       if (int rc = launch_attention(at, D, kv_dtype, splits, tr * rep, s)) return rc;
@@ -673,7 +747,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       dn.y = hidden_out + t0 * d.hidden;
       dn.ldy = d.hidden;
       if (last_layer) {
-        dn.fin_counter = ws.counters + 1;
+        dn.fin_counter = ws.fin_ctr;
         dn.fin_gain = u16(w->final_norm);
         dn.fin_out = out_out + t0 * d.hidden;
         dn.ld_fin = d.hidden;
@@ -698,7 +772,8 @@ int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, cons
   WC_REQUIRE(al16(w->head) && al16(workspace), "wc_draft_head: head weight / workspace must be 16-byte aligned");
   WC_REQUIRE(rows >= 1, "wc_draft_head: rows must be positive");
   WC_REQUIRE(out_row_dev == nullptr || rows == 1, "wc_draft_head: a gathered input row needs rows == 1");
-  WC_REQUIRE(out_ld >= dims->hidden, "wc_draft_head: input row stride smaller than hidden_size");
+  WC_REQUIRE(out_ld >= dims->hidden && out_ld % 4 == 0 && al16(out_rows),
+             "wc_draft_head: input rows must be 16-byte aligned with a stride >= hidden_size, multiple of 4");
   WC_REQUIRE(logits_out == nullptr || logits_ld >= dims->head_rows, "wc_draft_head: logits row stride too small");
   WC_REQUIRE(gumbel == nullptr || (gumbel->round_dev && gumbel->temperature > 0.f),
              "wc_draft_head: gumbel needs a round counter and a positive temperature");
@@ -724,7 +799,7 @@ int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, cons
     h.y = logits_out ? logits_out + t0 * logits_ld : nullptr;
     h.ldy = logits_ld;
     h.slots = ws.slots;
-    h.counter = ws.counters;
+    h.counter = ws.head_ctr;
     h.d2t = w->d2t;
     h.tok_out = token_out + t0;
     h.row_out = row_out ? row_out + t0 : nullptr;

@@ -3,21 +3,27 @@
 //   y[m][n] = sum_s sum_k W_s[n][k] * xhat_s[m][k]        for m < M, n < N
 //   xhat_s[m] = RMSNorm(x_s[m]) * gain_s   (or x_s[m] when the segment has no gain)
 //
-// Design (HBM-streaming, one pass over W):
-//   - a 256-thread block = 4 waves; each wave owns R consecutive output rows
-//     (x2 physical rows for the gate/up pair epilogue); every lane reads 8
-//     consecutive bf16 weights (one 128-bit load) per 512-wide K step, so each
-//     load instruction of a wave covers 1 KB of one weight row, fully coalesced;
-//   - the (normalised) fp32 inputs of all M rows are staged in LDS once per
-//     block and K chunk; the RMSNorm sum of squares is a block reduction over
-//     the same rows (fp32), applied as x * inv * gain like the reference
-//     (src/backends/cpu_ops.cpp:50-59);
-//   - U K-steps of every row are loaded before the first FMA so each lane
-//     keeps R*U 128-bit loads in flight;
-//   - fp32 accumulation, wave reduction with cross-lane shuffles.
+// The weights are read exactly once, with 128-bit loads: a 256-thread block is
+// 4 waves, each wave owns R consecutive output rows (x2 physical rows for the
+// gate/up pair epilogue), and lane j reads bf16 k = 8j..8j+7 of every 512-wide
+// step, so one load instruction of a wave covers 1 KB of one weight row.
+//
+// M = 1 (the draft step): k_gemv1 keeps everything in registers.  Every weight
+// load of every input segment is issued first; the lane then loads its own x
+// slices (the same k positions as its weights), and the RMSNorm sum of squares
+// is a wave reduction -- a wave's lanes tile the whole row -- so there is no
+// LDS and no barrier between the first weight byte requested and the FMAs.
+// The norm scale is applied after the dot product (sum W (x g) * inv).
+//
+// M > 1 (the update over a+1 accepted tokens): k_gemvm stages x * gain of all
+// rows in LDS per K chunk with 128-bit accesses, accumulating the sums of
+// squares in the same pass, requests the first weight group before staging,
+// and applies each row's 1/rms to the partial dot products at the end.
+//
 // Epilogues: plain store, residual add, SiLU(gate)*up of paired rows
-// (cpu_ops.cpp:79-84), and argmax over the rows (packed-key device atomics)
-// with a last-block finalisation that maps the winning row through d2t.
+// (cpu_ops.cpp:79-84), argmax over rows (packed (value, lowest index) keys,
+// device-scope atomicMax spread over kSlots addresses, last block maps the winner
+// through d2t), and a last-block final RMSNorm of the produced rows.
 #pragma once
 
 #include "wc_common.h"
@@ -30,6 +36,9 @@ constexpr int kMaxM = 16;
 constexpr int kMaxIn = 3;
 constexpr int kMaxSeg = 3;
 constexpr int kGemvLdsBytes = 48 * 1024;
+constexpr int kSlots = 32;       // argmax atomics are spread over kSlots addresses per row
+constexpr int kSlotStride = 16;  // uint64s between slots: one 128-byte line each
+constexpr int kMaxSteps1 = 24;   // M=1 kernel: up to 24 x 512 = 12288 inputs per segment
 
 struct InSeg {
   const void* x;           // [rows][ld] fp32 or bf16
@@ -63,6 +72,7 @@ struct GemvArgs {
   const int32_t* m_dev;                    // optional device row count (<= M)
   float eps;
   int epi;
+  int lds_floats;                          // dynamic LDS of the M>1 kernel
   float* y;                                // [M][ldy] (store / residual / pair; optional for argmax)
   int64_t ldy;
   const float* res;                        // residual [M][ldres]
@@ -70,8 +80,8 @@ struct GemvArgs {
   const int32_t* res_row_idx;              // optional: residual row m is res_row_idx[m] + res_row_add
   int res_row_add;
   // argmax epilogue
-  unsigned long long* slots;               // [M] packed keys, zero on entry, zeroed on exit
-  unsigned int* counter;                   // zero on entry, zeroed on exit
+  unsigned long long* slots;               // [M][kSlots] keys (stride kSlotStride), zero on entry and exit
+  unsigned int* counter;                   // tree counter (kTreeCounterBytes), zero on entry and exit
   const int32_t* d2t;                      // head row -> token id (NULL = identity)
   int32_t* tok_out;                        // [M] token ids
   int32_t* row_out;                        // [M] winning rows (optional)
@@ -136,46 +146,232 @@ __device__ __forceinline__ double philox_uniform(unsigned long long seed, unsign
   return static_cast<double>(c[i & 3] >> 11) * (1.0 / 9007199254740992.0);
 }
 
-// Stage rows [0, m) x chunk [c0, c0+kc) of input segment s into LDS as x*inv*gain.
-__device__ __forceinline__ void stage_chunk(const InSeg& s, int m, int c0, int kc, int ldk, const float* inv,
-                                            float* xs) {
-  for (int mi = 0; mi < m; ++mi) {
-    const int64_t row = in_row(s, mi);
-    for (int k = threadIdx.x; k < kc; k += kGemvThreads) {
-      float v = load_in(s, row, c0 + k);
-      if (s.gain) v = v * inv[mi] * bf16_to_float(s.gain[c0 + k]);
-      xs[mi * ldk + k] = v;
+// (segment, offset) of logical row n; PAIR rows live in segments 0 and 1 at offset n
+template <bool PAIR>
+__device__ __forceinline__ void row_segment(const GemvArgs& a, int n, int p, int& seg, int& off) {
+  if (PAIR) {
+    seg = p;
+    off = n;
+    return;
+  }
+  seg = 0;
+  for (int j = 1; j < a.n_seg; ++j)
+    if (n >= a.seg_start[j]) seg = j;
+  off = n - a.seg_start[seg];
+}
+
+// ------------------------------------------------------------------ shared epilogues
+
+// Store / residual / pair epilogue for one output value; published (device
+// coherent) when a last-block epilogue will read it back.
+template <bool PAIR>
+__device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, float g, float u) {
+  float v = g;
+  if (PAIR) {
+    v = g / (1.f + expf(-g)) * u;
+  } else if (a.epi == kEpiResidual) {
+    const int64_t rr = (a.res_row_idx ? a.res_row_idx[mi] : mi) + a.res_row_add;
+    v = a.res[rr * a.ldres + n] + v;
+  }
+  float* dst = a.y + mi * a.ldy + n;
+  if (a.fin_counter)
+    publish_f32(dst, v);
+  else
+    *dst = v;
+}
+
+// Last block: final RMSNorm of the m produced rows (read back coherently) and the offset advance.
+__device__ __forceinline__ void fin_epilogue(const GemvArgs& a, int m, float* s_red) {
+  if (!last_block_done(a.fin_counter, gridDim.x)) return;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (a.fin_gain) {
+    for (int mi = 0; mi < m; ++mi) {
+      float ss = 0.f;
+      for (int k = threadIdx.x; k < a.N; k += kGemvThreads) {
+        const float v = fetch_f32(a.y + mi * a.ldy + k);
+        ss = fmaf(v, v, ss);
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_red[wave] = ss;
+      __syncthreads();
+      float t = 0.f;
+      for (int w = 0; w < kGemvWaves; ++w) t += s_red[w];
+      const float inv = 1.f / sqrtf(t / static_cast<float>(a.N) + a.eps);
+      for (int k = threadIdx.x; k < a.N; k += kGemvThreads)
+        a.fin_out[mi * a.ld_fin + k] = fetch_f32(a.y + mi * a.ldy + k) * inv * bf16_to_float(a.fin_gain[k]);
+      __syncthreads();
     }
+  }
+  if (threadIdx.x == 0 && a.adv_dst) *a.adv_dst = *a.adv_src + a.adv_add + m;
+}
+
+// Draft-head value of row n for input row mi (optional logits store, Gumbel noise).
+__device__ __forceinline__ unsigned long long head_key(const GemvArgs& a, int mi, int n, float z) {
+  if (a.y) a.y[mi * a.ldy + n] = z;
+  if (a.use_gumbel) {
+    // Gumbel-max draw: argmax z/T - log(-log u) is a draw from softmax(z/T)
+    // (python/woodcock/sampling.py:196-203 with one uniform per head row)
+    const double u = philox_uniform(a.gumbel.seed, static_cast<unsigned long long>(*a.gumbel.round_dev),
+                                    a.gumbel.purpose + mi, static_cast<unsigned long long>(n));
+    z = static_cast<float>(static_cast<double>(z) * a.gumbel.inv_temperature - log(-log(u)));
+  }
+  return argmax_key(z, n);
+}
+
+// Block keys -> spread device atomics -> last block: winner row -> d2t token.
+template <int MM>
+__device__ __forceinline__ void argmax_epilogue(const GemvArgs& a, int m, unsigned long long (*s_key)[MM]) {
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) < m) {
+    unsigned long long best = 0;
+    for (int w = 0; w < kGemvWaves; ++w) best = s_key[w][threadIdx.x] > best ? s_key[w][threadIdx.x] : best;
+    if (best) atomic_max_u64(&a.slots[(threadIdx.x * kSlots + blockIdx.x % kSlots) * kSlotStride], best);
+  }
+  if (!last_block_done(a.counter, gridDim.x)) return;
+  if (static_cast<int>(threadIdx.x) < m) {
+    unsigned long long best = 0;
+    for (int j = 0; j < kSlots; ++j) {
+      unsigned long long* sl = &a.slots[(threadIdx.x * kSlots + j) * kSlotStride];
+      const unsigned long long k = atomic_load_u64(sl);
+      best = k > best ? k : best;
+      if (k) atomic_store_u64(sl, 0ull);
+    }
+    const int row = argmax_key_index(best);
+    a.tok_out[threadIdx.x] = a.d2t ? a.d2t[row] : row;
+    if (a.row_out) a.row_out[threadIdx.x] = row;
   }
 }
 
-// inv[mi] = 1 / sqrt(mean(x^2) + eps) for rows [0, m) of segment s (block reduction).
-__device__ __forceinline__ void row_inv_norms(const InSeg& s, int m, float eps, float* inv, float* red) {
-  for (int mi = 0; mi < m; ++mi) {
-    const int64_t row = in_row(s, mi);
-    float ss = 0.f;
-    for (int k = threadIdx.x; k < s.K; k += kGemvThreads) {
-      const float v = load_in(s, row, k);
-      ss = fmaf(v, v, ss);
+// ------------------------------------------------------------------ M = 1
+
+template <int R, bool PAIR, int NIN, int S>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
+  constexpr int P = PAIR ? 2 : 1;
+  __shared__ float s_red[kGemvWaves];
+  __shared__ unsigned long long s_key[kGemvWaves][1];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+  const int m = a.m_dev ? min(max(*a.m_dev, 0), 1) : 1;
+
+  // 1. every weight load of every input segment, first
+  uint4 w[NIN][R][P][S];
+  bool valid[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = row0 + r;
+    valid[r] = n < a.N && m > 0;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      int seg, off;
+      row_segment<PAIR>(a, n, p, seg, off);
+#pragma unroll
+      for (int s = 0; s < NIN; ++s) {
+        const uint16_t* wr = valid[r] ? a.w[seg][s] + static_cast<int64_t>(off) * a.ldw[s] : nullptr;
+        const int K = a.in[s].K;
+#pragma unroll
+        for (int u = 0; u < S; ++u) {
+          const int k = u * kWave * 8 + lane * 8;
+          w[s][r][p][u] = (valid[r] && k < K) ? *reinterpret_cast<const uint4*>(wr + k) : make_uint4(0, 0, 0, 0);
+        }
+      }
     }
-    ss = wave_sum(ss);
-    if ((threadIdx.x % kWave) == 0) red[threadIdx.x / kWave] = ss;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float t = 0.f;
-      for (int w = 0; w < kGemvWaves; ++w) t += red[w];
-      inv[mi] = 1.f / sqrtf(t / static_cast<float>(s.K) + eps);
-    }
-    __syncthreads();
   }
+
+  // 2. this lane's input slices, the per-segment norm, the dot products
+  float acc[R][P];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int p = 0; p < P; ++p) acc[r][p] = 0.f;
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const InSeg& seg = a.in[s];
+    const int64_t row = m > 0 ? in_row(seg, 0) : 0;
+    float part[R][P];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) part[r][p] = 0.f;
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int k = u * kWave * 8 + lane * 8;
+      if (k < seg.K && m > 0) {
+        float4 x0, x1;
+        if (seg.dtype == WC_BF16) {
+          const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + row * seg.ld + k);
+          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
+        } else {
+          const float* xp = static_cast<const float*>(seg.x) + row * seg.ld + k;
+          x0 = *reinterpret_cast<const float4*>(xp);
+          x1 = *reinterpret_cast<const float4*>(xp + 4);
+        }
+        if (seg.gain) {
+          ss = fmaf(x0.x, x0.x, ss); ss = fmaf(x0.y, x0.y, ss); ss = fmaf(x0.z, x0.z, ss); ss = fmaf(x0.w, x0.w, ss);
+          ss = fmaf(x1.x, x1.x, ss); ss = fmaf(x1.y, x1.y, ss); ss = fmaf(x1.z, x1.z, ss); ss = fmaf(x1.w, x1.w, ss);
+          const uint4 g = *reinterpret_cast<const uint4*>(seg.gain + k);
+          x0.x *= bf16_lo(g.x); x0.y *= bf16_hi(g.x); x0.z *= bf16_lo(g.y); x0.w *= bf16_hi(g.y);
+          x1.x *= bf16_lo(g.z); x1.y *= bf16_hi(g.z); x1.z *= bf16_lo(g.w); x1.w *= bf16_hi(g.w);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int p = 0; p < P; ++p) part[r][p] += dot8(w[s][r][p][u], x0, x1);
+      }
+    }
+    float inv = 1.f;
+    if (seg.gain) inv = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(seg.K) + a.eps);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) acc[r][p] = fmaf(part[r][p], inv, acc[r][p]);
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int p = 0; p < P; ++p) acc[r][p] = wave_sum(acc[r][p]);
+
+  // 3. epilogues
+  if (a.epi != kEpiArgmax) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (valid[r]) store_out<PAIR>(a, 0, row0 + r, acc[r][0], acc[r][P - 1]);
+    }
+    if (a.fin_counter) fin_epilogue(a, m, s_red);
+    return;
+  }
+  if (lane == 0) {
+    unsigned long long best = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (!valid[r]) continue;
+      const unsigned long long key = head_key(a, 0, row0 + r, acc[r][0]);
+      best = key > best ? key : best;
+    }
+    s_key[wave][0] = best;
+  }
+  argmax_epilogue<1>(a, m, s_key);
+}
+
+// ------------------------------------------------------------------ M > 1
+
+// Four consecutive inputs of segment s, row `row`, from k (k % 4 == 0).
+__device__ __forceinline__ float4 load4(const InSeg& s, int64_t row, int k) {
+  if (s.dtype == WC_BF16) {
+    const uint2 h = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(s.x) + row * s.ld + k);
+    return make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+  }
+  return *reinterpret_cast<const float4*>(static_cast<const float*>(s.x) + row * s.ld + k);
 }
 
 template <int R, int MM, bool PAIR, int U>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(kGemvThreads) void k_gemvm(GemvArgs a) {
   constexpr int P = PAIR ? 2 : 1;
   extern __shared__ float smem[];
-  __shared__ float s_inv[kMaxIn][kMaxM];
   __shared__ float s_red[kGemvWaves];
+  __shared__ float s_ss[kGemvWaves][MM];
   __shared__ unsigned long long s_key[kGemvWaves][MM];
 
   int m = a.M;
@@ -183,28 +379,34 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
 
-  // per-segment RMS norms of every input row
-  for (int s = 0; s < a.n_in; ++s)
-    if (a.in[s].gain) row_inv_norms(a.in[s], m, a.eps, s_inv[s], s_red);
-
-  // (segment, offset) of this wave's rows; physical row p of a PAIR row n is row n of segment p
   int rseg[R][P], roff[R][P];
   bool valid[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int n = row0 + r;
-    valid[r] = n < a.N;
+    valid[r] = row0 + r < a.N;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      int seg = p, off = n;
-      if (!PAIR) {
-        seg = 0;
-        for (int j = 1; j < a.n_seg; ++j)
-          if (n >= a.seg_start[j]) seg = j;
-        off = n - a.seg_start[seg];
-      }
-      rseg[r][p] = seg;
-      roff[r][p] = off;
+    for (int p = 0; p < P; ++p) row_segment<PAIR>(a, row0 + r, p, rseg[r][p], roff[r][p]);
+  }
+
+  int kcap = a.lds_floats / (m > 0 ? m : 1);
+  kcap = kcap / 512 * 512;
+  if (kcap < 512) kcap = 512;
+
+  // the first weight group of segment 0 is requested before any staging
+  uint4 w[R][P][U];
+  {
+    const int kc0 = min(kcap, a.in[0].K);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int kk = lane * 8 + u * kWave * 8;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          w[r][p][u] = (valid[r] && kk < kc0)
+                           ? *reinterpret_cast<const uint4*>(a.w[rseg[r][p]][0] +
+                                                             static_cast<int64_t>(roff[r][p]) * a.ldw[0] + kk)
+                           : make_uint4(0, 0, 0, 0);
     }
   }
 
@@ -216,7 +418,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
       for (int mi = 0; mi < MM; ++mi) acc[r][p][mi] = 0.f;
 
-  const int lds_floats = kGemvLdsBytes / 4;
+  bool prefetched = true;
   for (int s = 0; s < a.n_in; ++s) {
     const InSeg seg = a.in[s];
     const uint16_t* wrow[R][P];
@@ -225,26 +427,53 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
       for (int p = 0; p < P; ++p)
         wrow[r][p] = valid[r] ? a.w[rseg[r][p]][s] + static_cast<int64_t>(roff[r][p]) * a.ldw[s] : nullptr;
-    int kcap = lds_floats / (m > 0 ? m : 1);
-    kcap = kcap / 512 * 512;
-    if (kcap < 512) kcap = 512;
+    float part[R][P][MM], ssp[MM];
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      ssp[mi] = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int p = 0; p < P; ++p) part[r][p][mi] = 0.f;
+    }
     for (int c0 = 0; c0 < seg.K; c0 += kcap) {
       const int kc = min(kcap, seg.K - c0);
       __syncthreads();  // previous chunk fully consumed
-      stage_chunk(seg, m, c0, kc, kc, s_inv[s], smem);
+      // stage x * gain (the norm scale is applied after the dot product) and
+      // accumulate the sums of squares in the same pass
+#pragma unroll
+      for (int mi = 0; mi < MM; ++mi) {
+        if (mi < m) {
+          const int64_t row = in_row(seg, mi);
+          for (int k = threadIdx.x * 4; k < kc; k += kGemvThreads * 4) {
+            float4 v = load4(seg, row, c0 + k);
+            if (seg.gain) {
+              ssp[mi] = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ssp[mi]))));
+              const uint2 g = *reinterpret_cast<const uint2*>(seg.gain + c0 + k);
+              v.x *= bf16_lo(g.x);
+              v.y *= bf16_hi(g.x);
+              v.z *= bf16_lo(g.y);
+              v.w *= bf16_hi(g.y);
+            }
+            *reinterpret_cast<float4*>(smem + mi * kc + k) = v;
+          }
+        }
+      }
       __syncthreads();
       for (int k = lane * 8; k < kc; k += kWave * 8 * U) {
-        uint4 w[R][P][U];
+        if (!prefetched) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int kk = k + u * kWave * 8;
+          for (int u = 0; u < U; ++u) {
+            const int kk = k + u * kWave * 8;
 #pragma unroll
-          for (int r = 0; r < R; ++r)
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int p = 0; p < P; ++p)
-              w[r][p][u] = (valid[r] && kk < kc) ? *reinterpret_cast<const uint4*>(wrow[r][p] + c0 + kk)
-                                                 : make_uint4(0, 0, 0, 0);
+              for (int p = 0; p < P; ++p)
+                w[r][p][u] = (valid[r] && kk < kc) ? *reinterpret_cast<const uint4*>(wrow[r][p] + c0 + kk)
+                                                   : make_uint4(0, 0, 0, 0);
+          }
         }
+        prefetched = false;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int kk = k + u * kWave * 8;
@@ -257,12 +486,35 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
                 for (int r = 0; r < R; ++r)
 #pragma unroll
-                  for (int p = 0; p < P; ++p) acc[r][p][mi] += dot8(w[r][p][u], x0, x1);
+                  for (int p = 0; p < P; ++p) part[r][p][mi] += dot8(w[r][p][u], x0, x1);
               }
             }
           }
         }
       }
+    }
+    // per-row 1/rms of this segment (block reduction), applied to the partial sums
+    if (seg.gain) {
+#pragma unroll
+      for (int mi = 0; mi < MM; ++mi) {
+        const float t = wave_sum(ssp[mi]);
+        if (lane == 0) s_ss[wave][mi] = t;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      float inv = 1.f;
+      if (seg.gain) {
+        float t = 0.f;
+#pragma unroll
+        for (int q = 0; q < kGemvWaves; ++q) t += s_ss[q][mi];
+        inv = 1.f / sqrtf(t / static_cast<float>(seg.K) + a.eps);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int p = 0; p < P; ++p) acc[r][p][mi] = fmaf(part[r][p][mi], inv, acc[r][p][mi]);
     }
   }
 
@@ -278,52 +530,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if (!valid[r]) continue;
-        const int n = row0 + r;
 #pragma unroll
-        for (int mi = 0; mi < MM; ++mi) {
-          if (mi >= m) continue;
-          float v = acc[r][0][mi];
-          if (PAIR) {
-            const float g = acc[r][0][mi], u = acc[r][P - 1][mi];
-            v = g / (1.f + expf(-g)) * u;
-          } else if (a.epi == kEpiResidual) {
-            const int64_t rr = (a.res_row_idx ? a.res_row_idx[mi] : mi) + a.res_row_add;
-            v = a.res[rr * a.ldres + n] + v;
-          }
-          a.y[mi * a.ldy + n] = v;
-        }
+        for (int mi = 0; mi < MM; ++mi)
+          if (mi < m) store_out<PAIR>(a, mi, row0 + r, acc[r][0][mi], acc[r][P - 1][mi]);
       }
     }
-    // optional last-block epilogue: final RMSNorm of the produced rows, offset advance
-    if (a.fin_counter) {
-      if (!last_block_done(a.fin_counter, gridDim.x)) return;
-      if (a.fin_gain) {
-        for (int mi = 0; mi < m; ++mi) {
-          float ss = 0.f;
-          for (int k = threadIdx.x; k < a.N; k += kGemvThreads) {
-            const float v = a.y[mi * a.ldy + k];
-            ss = fmaf(v, v, ss);
-          }
-          ss = wave_sum(ss);
-          if (lane == 0) s_red[wave] = ss;
-          __syncthreads();
-          float t = 0.f;
-          for (int w = 0; w < kGemvWaves; ++w) t += s_red[w];
-          const float inv = 1.f / sqrtf(t / static_cast<float>(a.N) + a.eps);
-          for (int k = threadIdx.x; k < a.N; k += kGemvThreads)
-            a.fin_out[mi * a.ld_fin + k] = a.y[mi * a.ldy + k] * inv * bf16_to_float(a.fin_gain[k]);
-          __syncthreads();
-        }
-      }
-      if (threadIdx.x == 0) {
-        if (a.adv_dst) *a.adv_dst = *a.adv_src + a.adv_add + m;
-        atomic_store_u32(a.fin_counter, 0u);
-      }
-    }
+    if (a.fin_counter) fin_epilogue(a, m, s_red);
     return;
   }
-
-  // ---- argmax epilogue (draft head): per-wave keys -> per-block -> device atomics
   if (lane == 0) {
 #pragma unroll
     for (int mi = 0; mi < MM; ++mi) {
@@ -331,37 +545,13 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvArgs a) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         if (!valid[r] || mi >= m) continue;
-        const int n = row0 + r;
-        float z = acc[r][0][mi];
-        if (a.y) a.y[mi * a.ldy + n] = z;
-        if (a.use_gumbel) {
-          // Gumbel-max draw: argmax z/T - log(-log u) == a draw from softmax(z/T)
-          // (python/woodcock/sampling.py:196-203 with one uniform per head row)
-          const double u = philox_uniform(a.gumbel.seed, static_cast<unsigned long long>(*a.gumbel.round_dev),
-                                          a.gumbel.purpose + mi, static_cast<unsigned long long>(n));
-          z = static_cast<float>(static_cast<double>(z) * a.gumbel.inv_temperature - log(-log(u)));
-        }
-        const unsigned long long key = argmax_key(z, n);
+        const unsigned long long key = head_key(a, mi, row0 + r, acc[r][0][mi]);
         best = key > best ? key : best;
       }
       s_key[wave][mi] = best;
     }
   }
-  __syncthreads();
-  if (threadIdx.x < MM && static_cast<int>(threadIdx.x) < m) {
-    unsigned long long best = 0;
-    for (int w = 0; w < kGemvWaves; ++w) best = s_key[w][threadIdx.x] > best ? s_key[w][threadIdx.x] : best;
-    atomic_max_u64(&a.slots[threadIdx.x], best);
-  }
-  if (!last_block_done(a.counter, gridDim.x)) return;
-  if (threadIdx.x < MM && static_cast<int>(threadIdx.x) < m) {
-    const unsigned long long k = atomic_load_u64(&a.slots[threadIdx.x]);
-    atomic_store_u64(&a.slots[threadIdx.x], 0ull);
-    const int row = argmax_key_index(k);
-    a.tok_out[threadIdx.x] = a.d2t ? a.d2t[row] : row;
-    if (a.row_out) a.row_out[threadIdx.x] = row;
-  }
-  if (threadIdx.x == 0) atomic_store_u32(a.counter, 0u);
+  argmax_epilogue<MM>(a, m, s_key);
 }
 
 }  // namespace wc

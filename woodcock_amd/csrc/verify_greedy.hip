@@ -138,7 +138,6 @@ __global__ __launch_bounds__(kArgBlock) void k_argmax_verify(
       verdict->status = any_bad ? WC_E_INVALID : 0;
     }
   }
-  if (c == 0) atomic_store_u32(counter, 0u);
 }
 
 static int launch_argmax_verify(const float* logits, int rows, int vocab, int64_t ld, int mode, const int32_t* drafts,
@@ -150,7 +149,7 @@ static int launch_argmax_verify(const float* logits, int rows, int vocab, int64_
   WC_REQUIRE(vocab >= 1, "vocab must be positive (got %d)", vocab);
   WC_REQUIRE(ld >= vocab, "row stride %lld smaller than vocab %d", static_cast<long long>(ld), vocab);
   auto* slots = static_cast<unsigned long long*>(workspace);
-  auto* counter = reinterpret_cast<unsigned int*>(static_cast<char*>(workspace) + kCounterOff) + kCtrArgmax;
+  auto* counter = verify_counter(workspace, kCtrArgmax);
   const dim3 grid((vocab + kArgChunk - 1) / kArgChunk, rows);
   const bool vec = aligned(logits, 16) && (ld % 4) == 0;
   if (vec)

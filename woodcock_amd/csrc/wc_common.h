@@ -40,13 +40,12 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 
 // ------------------------------------------------------------------ workspace layout
 // The verify kernels share one small zero-initialised workspace:
-//   [0, 8*WC_MAX_NODES)            per-row argmax slots (uint64 keys)
-//   [+0, +64)                      completion counters (uint32), one per kernel family
+//   [0, 8*WC_MAX_NODES)                  per-row argmax slots (uint64 keys)
+//   then kNumCounters tree counters      (kTreeCounterBytes each, see last_block_done)
 constexpr size_t kSlotBytes = 8 * WC_MAX_NODES;
 constexpr size_t kCounterOff = kSlotBytes;
-constexpr int kNumCounters = 16;
-constexpr size_t kVerifyWorkspace = kCounterOff + 4 * kNumCounters + 64;
-enum Counter { kCtrArgmax = 0, kCtrStochastic = 1, kCtrHead = 2 };
+constexpr int kNumCounters = 4;
+enum Counter { kCtrArgmax = 0, kCtrStochastic = 1 };
 
 // ------------------------------------------------------------------ device helpers
 
@@ -121,23 +120,69 @@ __device__ __forceinline__ void atomic_store_u32(unsigned int* p, unsigned int v
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// "Last block done" handshake: every block calls this once after publishing its
-// partial results (all threads of the block must call it).  Returns true in
-// exactly one block -- the last to arrive -- after an acquire fence, so that
-// block sees every other block's published writes.  That block must reset
-// *counter to 0 (atomic_store_u32) before it exits, which makes the kernel
-// re-launchable without a host-side clear.
-__device__ __forceinline__ bool last_block_done(unsigned int* counter, unsigned int total) {
+// Device-coherent publish / fetch of single words: agent-scope atomic stores and
+// loads (sc1 on gfx950), visible across the XCDs of the GPU without an L2
+// write-back or invalidate.
+__device__ __forceinline__ void publish_f32(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<unsigned int*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fetch_f32(const float* p) {
+  return __uint_as_float(
+      __hip_atomic_load(reinterpret_cast<const unsigned int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// "Last block done" handshake.  Every block calls this once (all threads) after
+// handing its partial results over with publish_*() or device-scope RMW atomics;
+// returns true in exactly one block, the last to arrive, which then reads them
+// with fetch_*() / atomic loads.  Each thread first waits until its own
+// published stores and atomics have completed, the block barriers, and relaxed
+// RMWs on counters order the blocks -- no cache write-back or invalidate is
+// involved.  Plain stores are NOT handed over (they become visible at the end
+// of the kernel).
+//
+// The counters form a two-level tree so that no address takes more than
+// ~total/64 RMWs: block b increments group counter b % G; the block completing
+// a group increments the root; the block completing the root is the last.
+// Every counter sits on its own 128-byte line and is reset by the block that
+// completes it, so the kernel can be replayed without a host-side clear.
+constexpr int kTreeGroups = 64;
+constexpr int kCounterStride = 32;  // uints: one 128-byte line per counter
+constexpr size_t kTreeCounterBytes = 4 * kCounterStride * (kTreeGroups + 1);
+
+constexpr size_t kVerifyWorkspace = kCounterOff + kNumCounters * kTreeCounterBytes;
+inline unsigned int* verify_counter(void* ws, int which) {
+  return reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + kCounterOff + which * kTreeCounterBytes);
+}
+
+__device__ __forceinline__ unsigned int linear_block() { return blockIdx.y * gridDim.x + blockIdx.x; }
+
+// idx: this block's index among the `total` blocks counted on ctr.
+__device__ __forceinline__ bool last_block_done(unsigned int* ctr, unsigned int total, unsigned int idx) {
   __shared__ bool s_last;
-  __threadfence();  // every thread releases its own writes (device scope: other XCDs' L2s)
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned int prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (prev == total - 1);
+    const unsigned int G = total < kTreeGroups ? total : kTreeGroups;
+    const unsigned int g = idx % G;
+    const unsigned int gsize = total / G + (g < total % G ? 1u : 0u);
+    unsigned int* leaf = ctr + kCounterStride * (1 + g);
+    bool last = false;
+    if (__hip_atomic_fetch_add(leaf, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gsize - 1) {
+      __hip_atomic_store(leaf, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1) {
+        __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = true;
+      }
+    }
+    s_last = last;
   }
   __syncthreads();
-  if (s_last) __threadfence();  // acquire the other blocks' writes
   return s_last;
+}
+
+__device__ __forceinline__ bool last_block_done(unsigned int* ctr, unsigned int total) {
+  return last_block_done(ctr, total, linear_block());
 }
 
 }  // namespace wc

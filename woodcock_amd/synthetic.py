@@ -79,3 +79,39 @@ def draft_vocab(vocab: int, k: int, seed: int = 0, always=()) -> np.ndarray:
     rng = np.random.default_rng(seed)
     counts = rng.zipf(1.2, size=vocab).astype(np.int64)
     return top_ids(counts, k, set(int(a) for a in always if a < vocab))
+
+
+class SyntheticTarget:
+    """Stand-in for the verify-width target forward (out of scope here): fixed
+    target logits [K+1, V] fp32 ~ N(0, scale^2) and feature taps [K+1, Dt].
+
+    ``plant(drafts_dev, n_agree)`` makes rows i < n_agree take the drafted token
+    d_{i+1} as their argmax and keeps row n_agree away from d_{n_agree+1}, so a
+    greedy verify accepts exactly n_agree drafts.  It runs as device ops on
+    device-resident drafts (capturable in a graph) and restores the previous
+    round's plant first."""
+
+    BIG, BLOCK = 1.0e4, -1.0e4
+
+    def __init__(self, k: int, vocab: int, target_hidden: int, num_features: int = 3, device="cuda", seed: int = 0,
+                 scale: float = 3.0, tap_dtype=torch.bfloat16):
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        self.logits = scale * torch.randn(k + 1, vocab, generator=g, device=device, dtype=torch.float32)
+        self.taps = [torch.randn(k + 1, target_hidden, generator=g, device=device, dtype=torch.float32).to(tap_dtype)
+                     for _ in range(num_features)]
+        self.k = k
+        dev = self.logits.device
+        self._rows = torch.arange(k, device=dev)
+        self._prev_idx = torch.zeros(k, dtype=torch.long, device=dev)
+        self._prev_val = self.logits[self._rows, self._prev_idx].clone()
+        self._big = torch.full((k,), self.BIG, device=dev)
+        self._block = torch.full((k,), self.BLOCK, device=dev)
+
+    def plant(self, drafts_dev: torch.Tensor, n_agree: int) -> None:
+        rows = self._rows
+        self.logits.index_put_((rows, self._prev_idx), self._prev_val)  # undo the previous plant
+        self._prev_idx.copy_(drafts_dev[: self.k].long())
+        self._prev_val.copy_(self.logits[rows, self._prev_idx])
+        vals = torch.where(rows < n_agree, self._big, torch.where(rows == n_agree, self._block, self._prev_val))
+        self.logits.index_put_((rows, self._prev_idx), vals)
