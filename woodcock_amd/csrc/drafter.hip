@@ -1,10 +1,10 @@
 // drafter.hip -- the EAGLE-3 drafter step on gfx950.
 //
 // One decoder layer (python/woodcock/drafter.py:164-191; src/core/drafter.cpp:91-136)
-// is five launches, all stream-ordered on the caller's stream:
+// is six launches, all stream-ordered on the caller's stream:
 //   1. QKV    : dual-input streaming GEMV  q,k,v = W.RMS(h) + W_aux.RMS(e(x))
 //   2. attend : q/k RMSNorm + RoPE + KV append + split-KV GQA attention,
-//               last-arriving block per kv head merges the splits
+//               then a merge launch combines the splits
 //   3. o_proj : GEMV with residual epilogue          h1 = h + W_o.o
 //   4. gate/up: paired-row GEMV, SiLU(gate)*up epilogue
 //   5. down   : GEMV with residual epilogue, last block applies the final
@@ -30,7 +30,6 @@ constexpr int kMaxKvHeads = 64;
 struct DrafterWs {
   unsigned int* head_ctr;  // tree counters (kTreeCounterBytes each)
   unsigned int* fin_ctr;
-  unsigned int* attn_ctr;  // [kv_heads] tree counters
   unsigned long long* slots;
   float* qkv;
   float* attn;
@@ -55,7 +54,6 @@ static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
   const size_t nqkv = static_cast<size_t>(d.heads + 2 * d.kv_heads) * d.head_dim;
   w.head_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
   w.fin_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
-  w.attn_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes * static_cast<size_t>(d.kv_heads)));
   w.slots = reinterpret_cast<unsigned long long*>(take(8 * R * kSlots * kSlotStride));
   w.qkv = reinterpret_cast<float*>(take(4 * R * nqkv));
   w.attn = reinterpret_cast<float*>(take(4 * R * d.heads * d.head_dim));
@@ -87,7 +85,6 @@ struct AttnArgs {
   int64_t mask_ld;
   int window;
   float* partial;  // [Hk][S][kMaxQV][D+2]
-  unsigned int* counters;  // [Hk] tree counters
   float* out;  // [rows][H*D]
   int64_t ld_out;
 };
@@ -127,66 +124,162 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   return t;
 }
 
-// Normalise (gain) and rotate one head vector src[D] at position pos
-// (rotate-half RoPE, src/backends/cpu_ops.cpp:61-77).  Executed by one wave:
-// lane j owns the pairs (p, p + D/2) for p = j, j + 64, ..., so every value a
-// lane returns was computed by that lane alone -- no cross-lane LDS traffic.
-// lo[e] / hi[e] are elements p and p + D/2 of pair p = lane + 64 e (valid when
-// p < D/2).
+// One head vector held by one wave for q/k RMSNorm + rotate-half RoPE
+// (src/backends/cpu_ops.cpp:61-77): lane j owns the pairs (p, p + D/2) for
+// p = j, j + 64, ..., so every value a lane produces was computed by that lane
+// alone.  Loads go to clamped addresses (always in bounds) and lanes with
+// p >= D/2 are masked when the values are used, so a load never sits behind a
+// branch.
 template <int D>
-struct PairRegs {
+struct HeadVec {
   static constexpr int kHalf = D / 2;
   static constexpr int kPPL = (kHalf + kWave - 1) / kWave;
   float lo[kPPL], hi[kPPL];
+  uint16_t glo[kPPL], ghi[kPPL];  // raw bf16 gains, widened where used
+  float c[kPPL], sn[kPPL];        // RoPE row of the vector's position
 };
 
 template <int D>
-__device__ __forceinline__ void norm_rope_pairs(const float* src, const uint16_t* gain, float eps, const float* ct,
-                                                const float* st, int pos, PairRegs<D>& r) {
+__device__ __forceinline__ void head_vec_load(const float* src, const uint16_t* gain, HeadVec<D>& r) {
   const int lane = threadIdx.x % kWave;
-  constexpr int half = PairRegs<D>::kHalf, PPL = PairRegs<D>::kPPL;
+  constexpr int half = HeadVec<D>::kHalf;
+#pragma unroll
+  for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+    const int p = min(lane + e * kWave, half - 1);
+    r.lo[e] = src[p];
+    r.hi[e] = src[p + half];
+    r.glo[e] = gain[p];
+    r.ghi[e] = gain[p + half];
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void head_vec_rope_load(const float* ct, const float* st, int pos, HeadVec<D>& r) {
+  const int lane = threadIdx.x % kWave;
+  constexpr int half = HeadVec<D>::kHalf;
+#pragma unroll
+  for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+    const int p = min(lane + e * kWave, half - 1);
+    r.c[e] = ct[static_cast<int64_t>(pos) * half + p];
+    r.sn[e] = st[static_cast<int64_t>(pos) * half + p];
+  }
+}
+
+// Normalise and rotate in place (after head_vec_load and head_vec_rope_load).
+template <int D>
+__device__ __forceinline__ void head_vec_norm_rope(HeadVec<D>& r, float eps) {
+  const int lane = threadIdx.x % kWave;
+  constexpr int half = HeadVec<D>::kHalf, PPL = HeadVec<D>::kPPL;
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < PPL; ++e) {
-    const int p = lane + e * kWave;
-    r.lo[e] = p < half ? src[p] : 0.f;
-    r.hi[e] = p < half ? src[p + half] : 0.f;
+    if (lane + e * kWave >= half) r.lo[e] = r.hi[e] = 0.f;
     ss = fmaf(r.lo[e], r.lo[e], ss);
     ss = fmaf(r.hi[e], r.hi[e], ss);
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
 #pragma unroll
   for (int e = 0; e < PPL; ++e) {
-    const int p = lane + e * kWave;
-    if (p < half) {
-      const float x1 = r.lo[e] * inv * bf16_to_float(gain[p]);
-      const float x2 = r.hi[e] * inv * bf16_to_float(gain[p + half]);
-      const float c = ct[static_cast<int64_t>(pos) * half + p], sn = st[static_cast<int64_t>(pos) * half + p];
-      r.lo[e] = x1 * c - x2 * sn;
-      r.hi[e] = x2 * c + x1 * sn;
+    const float x1 = r.lo[e] * inv * bf16_to_float(r.glo[e]);
+    const float x2 = r.hi[e] * inv * bf16_to_float(r.ghi[e]);
+    r.lo[e] = x1 * r.c[e] - x2 * r.sn[e];
+    r.hi[e] = x2 * r.c[e] + x1 * r.sn[e];
+  }
+}
+
+// Key/value chunk staging: CH rows x D elements of one kv head, read as
+// 16-byte vectors (VE cache elements each), kNL vectors per thread per tensor.
+template <int D, typename KT>
+struct KvChunk {
+  static constexpr int kCH = attn_chunk<D>();
+  static constexpr int kVE = 16 / static_cast<int>(sizeof(KT));
+  static constexpr int kNL = (kCH * D / kVE + kAttnThreads - 1) / kAttnThreads;
+  uint4 k[kNL], v[kNL];
+};
+
+// Issue the loads of rows [c0, c0 + CH) (clamped into the cache; rows past the
+// chunk's end are loaded and ignored).
+template <int D, typename KT>
+__device__ __forceinline__ void kv_chunk_load(const KT* kc, const KT* vc, int cap, int c0, KvChunk<D, KT>& r) {
+  using C = KvChunk<D, KT>;
+  const uint4* k4 = reinterpret_cast<const uint4*>(kc);
+  const uint4* v4 = reinterpret_cast<const uint4*>(vc);
+  const int64_t last = static_cast<int64_t>(cap) * D / C::kVE - 1;
+#pragma unroll
+  for (int i = 0; i < C::kNL; ++i) {
+    const int64_t e = min(static_cast<int64_t>(c0) * D / C::kVE + threadIdx.x + i * kAttnThreads, last);
+    r.k[i] = k4[e];
+    r.v[i] = v4[e];
+  }
+}
+
+template <typename KT>
+__device__ __forceinline__ void unpack16(const uint4 q, float* out);
+template <>
+__device__ __forceinline__ void unpack16<uint16_t>(const uint4 q, float* out) {
+  out[0] = bf16_lo(q.x); out[1] = bf16_hi(q.x); out[2] = bf16_lo(q.y); out[3] = bf16_hi(q.y);
+  out[4] = bf16_lo(q.z); out[5] = bf16_hi(q.z); out[6] = bf16_lo(q.w); out[7] = bf16_hi(q.w);
+}
+template <>
+__device__ __forceinline__ void unpack16<float>(const uint4 q, float* out) {
+  out[0] = __uint_as_float(q.x); out[1] = __uint_as_float(q.y);
+  out[2] = __uint_as_float(q.z); out[3] = __uint_as_float(q.w);
+}
+
+// Write the n staged rows of chunk c0 into LDS; rows at or past `offset` are
+// this launch's appended rows and come from nk / nv instead of the loads.
+template <int D, typename KT>
+__device__ __forceinline__ void kv_chunk_fill(const KvChunk<D, KT>& r, int c0, int n, int offset, const float* nk,
+                                              const float* nv, float* ks, float* vs) {
+  using C = KvChunk<D, KT>;
+#pragma unroll
+  for (int i = 0; i < C::kNL; ++i) {
+    const int e = threadIdx.x + i * kAttnThreads;
+    const int el = e * C::kVE;  // element index within the chunk
+    if (el >= n * D) continue;
+    const int t = c0 + el / D;
+    if (t < offset) {
+      unpack16<KT>(r.k[i], ks + el);
+      unpack16<KT>(r.v[i], vs + el);
+    } else {
+      const int src = (t - offset) * D + el % D;
+#pragma unroll
+      for (int j = 0; j < C::kVE; ++j) {
+        ks[el + j] = nk[src + j];
+        vs[el + j] = nv[src + j];
+      }
     }
   }
 }
 
+// One block per (split, kv head).  The block's key range [kb, ke) of the
+// visible rows [0, T) is staged in chunks; the q vectors of the head group are
+// normalised and rotated into LDS; rows appended by this launch (t >= offset)
+// whose slot lies in [kb, ke) are normalised/rotated and written to the cache
+// by this block, which also takes them from LDS rather than reading them back.
+// Every load that does not depend on another is issued before the first wait:
+// q / new-row sources and gains, then the first chunk, then the RoPE rows.
 template <int D, typename KT>
 __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   extern __shared__ float lds[];
-  constexpr int kAttnChunk = attn_chunk<D>();
+  constexpr int CH = attn_chunk<D>();
   constexpr int ACC = (kMaxQV * D + kAttnThreads - 1) / kAttnThreads;
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
   const int rep = a.H / a.Hk;
   const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
   const int offset = *a.offset_dev + a.offset_add;
   const int T = min(offset + nr, a.cap);  // never past the cache capacity
-  const int QV = nr * rep;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int nw = kAttnThreads / kWave;
+  const int QV = nr * rep, QVb = a.rows * rep;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
+  constexpr int nw = kAttnThreads / kWave;
 
-  float* qs = lds;                       // [QV][D]
-  float* ks = qs + QV * D;               // [kAttnChunk][D]
-  float* vs = ks + kAttnChunk * D;       // [kAttnChunk][D]
-  float* sc = vs + kAttnChunk * D;       // [QV][kAttnChunk]
+  float* qs = lds;                 // [QVb][D]
+  float* ks = qs + QVb * D;        // [CH][D]
+  float* vs = ks + CH * D;         // [CH][D]
+  float* sc = vs + CH * D;         // [QVb][CH]
+  float* nk = sc + QVb * CH;       // [rows][D] appended keys (cache-rounded)
+  float* nv = nk + a.rows * D;     // [rows][D] appended values (cache-rounded)
   __shared__ float s_m[kMaxQV], s_l[kMaxQV], s_alpha[kMaxQV];
 
   KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
@@ -194,59 +287,98 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   const int per = (T + S - 1) / S;
   const int kb = min(T, split * per), ke = min(T, kb + per);
 
-  // q vectors of this kv head's group: normalised + rotated, in LDS
-  for (int v = wave; v < QV; v += nw) {
-    const int l = v / rep, h = kh * rep + v % rep;
-    int pos = a.positions ? a.positions[l] : offset + l;
-    pos = min(max(pos, 0), a.rope_max - 1);
-    PairRegs<D> r;
-    norm_rope_pairs<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, a.eps, a.rope_cos, a.rope_sin, pos, r);
+  // first q vector and first appended row of this wave: sources and gains
+  const int v0 = wave, l0 = nw - 1 - wave;  // appended rows from the last wave down
+  // (loaded unconditionally from clamped rows so that no load sits in a branch)
+  HeadVec<D> qv0, kv0;
+  {
+    const int v = min(v0, QVb - 1), l = v / rep, h = kh * rep + v % rep;
+    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, qv0);
+  }
+  const bool app0 = l0 < nr && offset + l0 >= kb && offset + l0 < ke;
+  constexpr int VPL = (D + kWave - 1) / kWave;
+  float vv0[VPL];
+  {
+    const int l = min(l0, a.rows - 1);
+    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, kv0);
+    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
 #pragma unroll
-    for (int e = 0; e < PairRegs<D>::kPPL; ++e) {
+    for (int e = 0; e < VPL; ++e) vv0[e] = vsrc[min(lane + e * kWave, D - 1)];
+  }
+  // first chunk
+  KvChunk<D, KT> ch;
+  kv_chunk_load<D, KT>(kc, vc, a.cap, kb, ch);
+
+  auto row_pos = [&](int l) {
+    const int pos = a.positions ? a.positions[l] : offset + l;
+    return min(max(pos, 0), a.rope_max - 1);
+  };
+  auto put_q = [&](int v, HeadVec<D>& r) {
+    head_vec_norm_rope<D>(r, a.eps);
+#pragma unroll
+    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
       const int p = lane + e * kWave;
       if (p < D / 2) {
         qs[v * D + p] = r.lo[e];
         qs[v * D + p + D / 2] = r.hi[e];
       }
     }
-  }
-  // new keys / values whose slot falls in this block's range: norm + rope, append
-  for (int l = wave; l < nr; l += nw) {
+  };
+  auto put_kv = [&](int l, HeadVec<D>& r, const float* vv) {
     const int t = offset + l;
-    if (t < kb || t >= ke) continue;
-    int pos = a.positions ? a.positions[l] : offset + l;
-    pos = min(max(pos, 0), a.rope_max - 1);
-    PairRegs<D> r;
-    norm_rope_pairs<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, a.eps, a.rope_cos, a.rope_sin, pos, r);
+    head_vec_norm_rope<D>(r, a.eps);
 #pragma unroll
-    for (int e = 0; e < PairRegs<D>::kPPL; ++e) {
+    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
       const int p = lane + e * kWave;
       if (p < D / 2) {
-        kv_store<KT>(kc, static_cast<int64_t>(t) * D + p, r.lo[e]);
-        kv_store<KT>(kc, static_cast<int64_t>(t) * D + p + D / 2, r.hi[e]);
+        nk[l * D + p] = kv_store<KT>(kc, static_cast<int64_t>(t) * D + p, r.lo[e]);
+        nk[l * D + p + D / 2] = kv_store<KT>(kc, static_cast<int64_t>(t) * D + p + D / 2, r.hi[e]);
       }
     }
-    for (int i = lane; i < D; i += kWave)
-      kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, a.qkv[l * a.ld_qkv + (a.H + a.Hk + kh) * D + i]);
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) {
+      const int i = lane + e * kWave;
+      if (i < D) nv[l * D + i] = kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, vv[e]);
+    }
+  };
+
+  head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(min(v0, QVb - 1) / rep), qv0);
+  head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(min(l0, a.rows - 1)), kv0);
+  if (v0 < QV) put_q(v0, qv0);
+  if (app0) put_kv(l0, kv0, vv0);
+  for (int v = v0 + nw; v < QV; v += nw) {
+    HeadVec<D> r;
+    const int l = v / rep, h = kh * rep + v % rep;
+    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, r);
+    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
+    put_q(v, r);
+  }
+  for (int l = l0 + nw; l < nr; l += nw) {
+    if (offset + l < kb || offset + l >= ke) continue;
+    HeadVec<D> r;
+    float vv[VPL];
+    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, r);
+    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
+#pragma unroll
+    for (int e = 0; e < VPL; ++e) vv[e] = vsrc[min(lane + e * kWave, D - 1)];
+    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
+    put_kv(l, r, vv);
   }
   if (threadIdx.x < kMaxQV) {
     s_m[threadIdx.x] = -INFINITY;
     s_l[threadIdx.x] = 0.f;
   }
-  __threadfence_block();
   __syncthreads();
 
   float acc[ACC];
 #pragma unroll
   for (int e = 0; e < ACC; ++e) acc[e] = 0.f;
 
-  for (int c0 = kb; c0 < ke; c0 += kAttnChunk) {
-    const int n = min(kAttnChunk, ke - c0);
-    for (int e = threadIdx.x; e < n * D; e += kAttnThreads) {
-      ks[e] = kv_load<KT>(kc, static_cast<int64_t>(c0) * D + e);
-      vs[e] = kv_load<KT>(vc, static_cast<int64_t>(c0) * D + e);
-    }
+  for (int c0 = kb; c0 < ke; c0 += CH) {
+    const int n = min(CH, ke - c0);
+    kv_chunk_fill<D, KT>(ch, c0, n, offset, nk, nv, ks, vs);
     __syncthreads();
+    if (c0 + CH < ke) kv_chunk_load<D, KT>(kc, vc, a.cap, c0 + CH, ch);  // next chunk in flight
     for (int e = threadIdx.x; e < QV * n; e += kAttnThreads) {
       const int v = e / n, j = e - v * n;
       const int l = v / rep, t = c0 + j;
@@ -258,31 +390,37 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
       float s = -INFINITY;
       if (vis) {
         float d = 0.f;
-        const float* q = qs + v * D;
-        const float* k = ks + j * D;
-#pragma unroll 8
-        for (int i = 0; i < D; ++i) d = fmaf(q[i], k[i], d);
+        const float4* q = reinterpret_cast<const float4*>(qs + v * D);
+        const float4* k = reinterpret_cast<const float4*>(ks + j * D);
+#pragma unroll 4
+        for (int i = 0; i < D / 4; ++i) {
+          const float4 x = q[i], y = k[i];
+          d = fmaf(x.x, y.x, d);
+          d = fmaf(x.y, y.y, d);
+          d = fmaf(x.z, y.z, d);
+          d = fmaf(x.w, y.w, d);
+        }
         s = a.scale * d;
       }
-      sc[v * kAttnChunk + j] = s;
+      sc[v * CH + j] = s;
     }
     __syncthreads();
     if (threadIdx.x < QV) {
       const int v = threadIdx.x;
       const float m_old = s_m[v];
       float m_new = m_old;
-      for (int j = 0; j < n; ++j) m_new = fmaxf(m_new, sc[v * kAttnChunk + j]);
+      for (int j = 0; j < n; ++j) m_new = fmaxf(m_new, sc[v * CH + j]);
       float alpha = 1.f, lsum = 0.f;
       if (m_new != -INFINITY) {
         alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
         for (int j = 0; j < n; ++j) {
-          const float s = sc[v * kAttnChunk + j];
-          const float p = s == -INFINITY ? 0.f : expf(s - m_new);
-          sc[v * kAttnChunk + j] = p;
+          const float sv = sc[v * CH + j];
+          const float p = sv == -INFINITY ? 0.f : expf(sv - m_new);
+          sc[v * CH + j] = p;
           lsum += p;
         }
       } else {
-        for (int j = 0; j < n; ++j) sc[v * kAttnChunk + j] = 0.f;
+        for (int j = 0; j < n; ++j) sc[v * CH + j] = 0.f;
       }
       s_m[v] = m_new;
       s_l[v] = s_l[v] * alpha + lsum;
@@ -295,75 +433,78 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
       if (idx < QV * D) {
         const int v = idx / D, i = idx - v * D;
         float o = acc[e] * s_alpha[v];
-        for (int j = 0; j < n; ++j) o = fmaf(sc[v * kAttnChunk + j], vs[j * D + i], o);
+        for (int j = 0; j < n; ++j) o = fmaf(sc[v * CH + j], vs[j * D + i], o);
         acc[e] = o;
       }
     }
     __syncthreads();
   }
 
-  // publish this split's (m, l, o)
+  // this split's (m, l, o); an empty range leaves m = -inf, l = 0
   float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * kMaxQV * (D + 2);
 #pragma unroll
   for (int e = 0; e < ACC; ++e) {
     const int idx = threadIdx.x + e * kAttnThreads;
     if (idx < QV * D) {
       const int v = idx / D, i = idx - v * D;
-      publish_f32(&part[v * (D + 2) + 2 + i], acc[e]);
+      part[v * (D + 2) + 2 + i] = acc[e];
     }
   }
   if (threadIdx.x < QV) {
-    publish_f32(&part[threadIdx.x * (D + 2)], s_m[threadIdx.x]);
-    publish_f32(&part[threadIdx.x * (D + 2) + 1], s_l[threadIdx.x]);
+    part[threadIdx.x * (D + 2)] = s_m[threadIdx.x];
+    part[threadIdx.x * (D + 2) + 1] = s_l[threadIdx.x];
   }
-  if (!last_block_done(a.counters + kh * (kTreeCounterBytes / 4), S, split)) return;
+}
 
-  // merge the splits of this kv head: one thread per query vector loads every
-  // split's (m, l) back to back and forms the merge weights, then every thread
-  // combines its (vector, element) outputs
-  __shared__ float s_w[kMaxSplits * kMaxQV], s_den[kMaxQV];
-  const float* base = a.partial + static_cast<int64_t>(kh) * S * kMaxQV * (D + 2);
-  if (threadIdx.x < QV) {
-    const int v = threadIdx.x;
-    float ms[kMaxSplits], ls[kMaxSplits];
+// Merge the splits: one block per (vector, kv head).  Every load -- the
+// splits' (m, l) and this vector's partial outputs -- is issued up front from
+// addresses that do not depend on the row count; the block then exits if its
+// vector is past the live rows.  Runs after k_attention (stream order), so
+// plain loads see the partials.
+template <int D>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) {
+  constexpr int kPer = (D + kAttnThreads - 1) / kAttnThreads;  // elements per thread (D <= 256: 1)
+  static_assert(kPer == 1, "head_dim up to the block size");
+  __shared__ float s_w[kMaxSplits], s_lsum[kMaxSplits];
+  const int v = blockIdx.x, kh = blockIdx.y;
+  const int rep = a.H / a.Hk;
+  const int t = threadIdx.x;
+  const float* base = a.partial + static_cast<int64_t>(kh) * S * kMaxQV * (D + 2) + v * (D + 2);
+  constexpr int64_t kSplitStride = static_cast<int64_t>(kMaxQV) * (D + 2);
+  const int i = min(t, D - 1);
+  float o[kMaxSplits];
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) {
-      if (s < S) {
-        ms[s] = fetch_f32(&base[(s * kMaxQV + v) * (D + 2)]);
-        ls[s] = fetch_f32(&base[(s * kMaxQV + v) * (D + 2) + 1]);
-      }
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s)
-      if (s < S) M = fmaxf(M, ms[s]);
-    float den = 0.f;
-#pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) {
-      if (s < S) {
-        const float wgt = ms[s] == -INFINITY ? 0.f : expf(ms[s] - M);
-        s_w[s * kMaxQV + v] = wgt;
-        den = fmaf(ls[s], wgt, den);
-      }
-    }
-    s_den[v] = den;
+  for (int sp = 0; sp < kMaxSplits; ++sp) o[sp] = base[min(sp, S - 1) * kSplitStride + 2 + i];
+  if (t < S) {
+    s_w[t] = base[t * kSplitStride];
+    s_lsum[t] = base[t * kSplitStride + 1];
   }
+  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
+  if (v >= nr * rep) return;  // uniform per block
   __syncthreads();
-  for (int idx = threadIdx.x; idx < QV * D; idx += kAttnThreads) {
-    const int v = idx / D, i = idx - v * D;
-    float num = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < S; ++s) num = fmaf(s_w[s * kMaxQV + v], fetch_f32(&base[(s * kMaxQV + v) * (D + 2) + 2 + i]), num);
+  float M = -INFINITY;
+  for (int sp = 0; sp < S; ++sp) M = fmaxf(M, s_w[sp]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int sp = 0; sp < kMaxSplits; ++sp) {
+    if (sp < S) {
+      const float ms = s_w[sp];
+      const float wgt = ms == -INFINITY ? 0.f : expf(ms - M);
+      den = fmaf(s_lsum[sp], wgt, den);
+      num = fmaf(wgt, o[sp], num);
+    }
+  }
+  if (t < D) {
     const int l = v / rep, h = kh * rep + v % rep;
-    a.out[l * a.ld_out + h * D + i] = num / s_den[v];
+    a.out[l * a.ld_out + h * D + t] = num / den;
   }
 }
 
 template <int D, typename KT>
-static int launch_attention_t(const AttnArgs& a, int splits, int qv_max, hipStream_t stream) {
+static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream) {
   constexpr int CH = attn_chunk<D>();
-  const size_t lds = sizeof(float) * (static_cast<size_t>(qv_max) * D + 2 * CH * D +
-                                      static_cast<size_t>(qv_max) * CH);
+  const size_t qvb = static_cast<size_t>(a.rows) * (a.H / a.Hk);
+  const size_t lds = sizeof(float) * (qvb * D + 2 * CH * D + qvb * CH + 2 * static_cast<size_t>(a.rows) * D);
   static size_t attr_bytes = 64 * 1024;  // default dynamic-LDS limit
   if (lds > attr_bytes) {
     WC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention<D, KT>),
@@ -372,14 +513,17 @@ static int launch_attention_t(const AttnArgs& a, int splits, int qv_max, hipStre
   }
   hipLaunchKernelGGL((k_attention<D, KT>), dim3(splits, a.Hk), dim3(kAttnThreads), lds, stream, a);
   WC_LAUNCHED();
+  hipLaunchKernelGGL((k_attn_merge<D>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, stream, a,
+                     splits);
+  WC_LAUNCHED();
   return WC_OK;
 }
 
-static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, int qv_max, hipStream_t s) {
+static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, hipStream_t s) {
 #define WC_ATT(DD)                                                                                  \
   case DD:                                                                                          \
-    return kv_dtype == WC_BF16 ? launch_attention_t<DD, uint16_t>(a, splits, qv_max, s)            \
-                               : launch_attention_t<DD, float>(a, splits, qv_max, s);
+    return kv_dtype == WC_BF16 ? launch_attention_t<DD, uint16_t>(a, splits, s)                   \
+                               : launch_attention_t<DD, float>(a, splits, s);
   switch (D) {
     WC_ATT(8)
     WC_ATT(16)
@@ -395,27 +539,80 @@ static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, 
 
 // ------------------------------------------------------------------ GEMV launch
 
-template <int R, bool PAIR, int NIN>
-static int launch_gemv1(const GemvArgs& a, int steps, hipStream_t s) {
-  const dim3 grid((a.N + kGemvWaves * R - 1) / (kGemvWaves * R)), block(kGemvThreads);
-#define WC_G1(SV) hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, SV>), grid, block, 0, s, a)
-  if (steps <= 2)
-    WC_G1(2);
-  else if (steps <= 4)
-    WC_G1(4);
-  else if (steps <= 8)
-    WC_G1(8);
-  else if (steps <= 12)
-    WC_G1(12);
-  else if (steps <= 16)
-    WC_G1(16);
-  else if (steps <= 20)
-    WC_G1(20);
-  else
-    WC_G1(24);
-#undef WC_G1
-  WC_LAUNCHED();
-  return WC_OK;
+// Weight registers per lane are 4 * R * P * NIN * S; variants above the budget
+// are not instantiated (they would spill) and report false to the dispatcher.
+constexpr int kGemv1Budget = 24;
+constexpr size_t kGemvxMaxLds = 96 * 1024;
+
+template <int R, bool PAIR, int NIN, int S, int XB>
+static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
+  if constexpr (R * (PAIR ? 2 : 1) * NIN * S > kGemv1Budget) {
+    return false;
+  } else {
+    const dim3 grid((a.N + kGemvWaves * R - 1) / (kGemvWaves * R)), block(kGemvThreads);
+    hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, S, XB>), grid, block, 0, s, a);
+    return true;
+  }
+}
+
+template <int R, bool PAIR, int NIN, int XB>
+static bool launch_gemv1(const GemvArgs& a, int steps, hipStream_t s) {
+  if (steps <= 4) return launch_gemv1_s<R, PAIR, NIN, 4, XB>(a, s);
+  if (steps <= 8) return launch_gemv1_s<R, PAIR, NIN, 8, XB>(a, s);
+  if (steps <= 12) return launch_gemv1_s<R, PAIR, NIN, 12, XB>(a, s);
+  return false;
+}
+
+// Largest rows-per-wave that keeps at least 512 blocks and fits the budget.
+template <bool PAIR, int NIN, int XB>
+static bool launch_gemv1_r(const GemvArgs& a, int steps, hipStream_t s) {
+  if (a.N >= 4 * kGemvWaves * 512 && launch_gemv1<4, PAIR, NIN, XB>(a, steps, s)) return true;
+  if (a.N >= 2 * kGemvWaves * 512 && launch_gemv1<2, PAIR, NIN, XB>(a, steps, s)) return true;
+  return launch_gemv1<1, PAIR, NIN, XB>(a, steps, s);
+}
+
+// Few-row kernel: x staged in LDS; same register budget for the weights.
+template <int R, bool PAIR, int NIN, int S, int XB, int MM>
+static bool launch_gemvx_s(const GemvArgs& a, size_t lds, hipStream_t s) {
+  if constexpr (R * (PAIR ? 2 : 1) * NIN * S > kGemv1Budget) {
+    return false;
+  } else {
+    const void* fn = reinterpret_cast<const void*>(&k_gemvx<R, PAIR, NIN, S, XB, MM>);
+    static size_t attr_bytes = 64 * 1024;  // default dynamic-LDS limit
+    if (lds > attr_bytes) {
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)) != hipSuccess)
+        return false;
+      attr_bytes = lds;
+    }
+    const dim3 grid((a.N + kGemvWaves * R - 1) / (kGemvWaves * R)), block(kGemvThreads);
+    hipLaunchKernelGGL((k_gemvx<R, PAIR, NIN, S, XB, MM>), grid, block, lds, s, a);
+    return true;
+  }
+}
+
+template <int R, bool PAIR, int NIN, int XB, int MM>
+static bool launch_gemvx_m(const GemvArgs& a, int steps, hipStream_t s) {
+  const int S = steps <= 4 ? 4 : steps <= 8 ? 8 : 12;
+  size_t lds = 0;
+  for (int i = 0; i < NIN; ++i) lds += static_cast<size_t>(a.M) * S * 512 * ((XB >> i) & 1 ? 2 : 4);
+  if (lds > kGemvxMaxLds) return false;
+  if (steps <= 4) return launch_gemvx_s<R, PAIR, NIN, 4, XB, MM>(a, lds, s);
+  if (steps <= 8) return launch_gemvx_s<R, PAIR, NIN, 8, XB, MM>(a, lds, s);
+  if (steps <= 12) return launch_gemvx_s<R, PAIR, NIN, 12, XB, MM>(a, lds, s);
+  return false;
+}
+
+template <bool PAIR, int NIN, int XB>
+static bool launch_gemvx(const GemvArgs& a, int steps, hipStream_t s) {
+  if (a.M <= 4) {
+    if (a.N >= 2 * kGemvWaves * 512 && launch_gemvx_m<2, PAIR, NIN, XB, 4>(a, steps, s)) return true;
+    return launch_gemvx_m<1, PAIR, NIN, XB, 4>(a, steps, s);
+  }
+  if (a.M <= 8) {
+    if (a.N >= 2 * kGemvWaves * 512 && launch_gemvx_m<2, PAIR, NIN, XB, 8>(a, steps, s)) return true;
+    return launch_gemvx_m<1, PAIR, NIN, XB, 8>(a, steps, s);
+  }
+  return false;
 }
 
 template <bool PAIR>
@@ -438,19 +635,49 @@ static int launch_gemvm(GemvArgs a, int max_k, hipStream_t s) {
   return WC_OK;
 }
 
-// M = 1 goes to the register-resident kernel (R rows per wave), M > 1 to the LDS-staged one.
-static int launch_gemv(const GemvArgs& a, int R, hipStream_t s) {
+// Every K a multiple of 512 (up to 6144): one row goes to the register-resident
+// kernel, 2..8 rows to the LDS-staged few-row kernel; anything else to the
+// chunked LDS kernel.
+static int launch_gemv(const GemvArgs& a, int /*R hint*/, hipStream_t s) {
   if (a.M < 1 || a.M > kMaxM) return set_error(WC_E_INVALID, "gemv: rows %d not in 1..%d", a.M, kMaxM);
   int max_k = 0;
-  for (int i = 0; i < a.n_in; ++i) max_k = std::max(max_k, a.in[i].K);
-  const int steps = (max_k + 511) / 512;
+  bool k512 = true;
+  int xb = 0;
+  for (int i = 0; i < a.n_in; ++i) {
+    max_k = std::max(max_k, a.in[i].K);
+    k512 = k512 && a.in[i].K % 512 == 0;
+    if (a.in[i].dtype == WC_BF16) xb |= 1 << i;
+  }
+  const int steps = max_k / 512;
   const bool pair = a.epi == kEpiSiluPair;
-  if (a.M == 1 && steps <= kMaxSteps1) {
-    if (pair) return a.n_in == 1 ? launch_gemv1<1, true, 1>(a, steps, s) : launch_gemvm<true>(a, max_k, s);
-    if (R >= 2 && a.n_in == 1) return launch_gemv1<2, false, 1>(a, steps, s);
-    if (a.n_in == 1) return launch_gemv1<1, false, 1>(a, steps, s);
-    if (a.n_in == 2) return launch_gemv1<1, false, 2>(a, steps, s);
-    return launch_gemv1<1, false, 3>(a, steps, s);
+  bool done = false;
+  if (a.M > 1 && k512) {
+    if (pair && a.n_in == 1 && xb == 0)
+      done = launch_gemvx<true, 1, 0>(a, steps, s);
+    else if (!pair && a.n_in == 1 && xb == 0)
+      done = launch_gemvx<false, 1, 0>(a, steps, s);
+    else if (!pair && a.n_in == 2 && xb == 2)
+      done = launch_gemvx<false, 2, 2>(a, steps, s);
+    else if (!pair && a.n_in == 3 && xb == 0)
+      done = launch_gemvx<false, 3, 0>(a, steps, s);
+    else if (!pair && a.n_in == 3 && xb == 7)
+      done = launch_gemvx<false, 3, 7>(a, steps, s);
+  }
+  if (a.M == 1 && k512) {
+    if (pair && a.n_in == 1 && xb == 0)
+      done = launch_gemv1_r<true, 1, 0>(a, steps, s);
+    else if (!pair && a.n_in == 1 && xb == 0)
+      done = launch_gemv1_r<false, 1, 0>(a, steps, s);
+    else if (!pair && a.n_in == 2 && xb == 2)
+      done = launch_gemv1_r<false, 2, 2>(a, steps, s);
+    else if (!pair && a.n_in == 3 && xb == 0)
+      done = launch_gemv1_r<false, 3, 0>(a, steps, s);
+    else if (!pair && a.n_in == 3 && xb == 7)
+      done = launch_gemv1_r<false, 3, 7>(a, steps, s);
+  }
+  if (done) {
+    WC_LAUNCHED();
+    return WC_OK;
   }
   return pair ? launch_gemvm<true>(a, max_k, s) : launch_gemvm<false>(a, max_k, s);
 }
@@ -587,6 +814,8 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
                "wc_drafter_forward: layer %d has a NULL weight or cache", li);
     WC_REQUIRE(al16(L.q) && al16(L.k) && al16(L.v) && al16(L.o) && al16(L.gate) && al16(L.up) && al16(L.down),
                "wc_drafter_forward: layer %d weights must be 16-byte aligned", li);
+    WC_REQUIRE(al16(k_cache[li]) && al16(v_cache[li]), "wc_drafter_forward: layer %d cache must be 16-byte aligned",
+               li);
     if (L.aux_norm)
       WC_REQUIRE(L.aux_q && L.aux_k && L.aux_v && al16(L.aux_q) && al16(L.aux_k) && al16(L.aux_v),
                  "wc_drafter_forward: layer %d aux projections missing", li);
@@ -679,10 +908,9 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       at.mask_ld = mask_ld;
       at.window = d.window;
       at.partial = ws.partial;
-      at.counters = ws.attn_ctr;
       at.out = ws.attn;
       at.ld_out = H * D;
-      if (int rc = launch_attention(at, D, kv_dtype, splits, tr * rep, s)) return rc;
+      if (int rc = launch_attention(at, D, kv_dtype, splits, s)) return rc;
 
       // 3. o_proj with the residual: h1 = h + W_o . o
       GemvArgs o = gemv_defaults();

@@ -160,19 +160,46 @@ __device__ __forceinline__ void row_segment(const GemvArgs& a, int n, int p, int
   off = n - a.seg_start[seg];
 }
 
+// Weight row pointer of logical row n (pair member p) for input segment s,
+// resolved with constant indices only so that a wave-uniform n keeps the whole
+// lookup in scalar registers.
+template <bool PAIR>
+__device__ __forceinline__ const uint16_t* row_ptr(const GemvArgs& a, int n, int p, int s) {
+  if (PAIR) return (p ? a.w[1][s] : a.w[0][s]) + static_cast<int64_t>(n) * a.ldw[s];
+  const uint16_t* base = a.w[0][s];
+  int start = 0;
+#pragma unroll
+  for (int j = 1; j < kMaxSeg; ++j)
+    if (j < a.n_seg && n >= a.seg_start[j]) {
+      base = a.w[j][s];
+      start = a.seg_start[j];
+    }
+  return base + static_cast<int64_t>(n - start) * a.ldw[s];
+}
+
 // ------------------------------------------------------------------ shared epilogues
 
-// Store / residual / pair epilogue for one output value; published (device
-// coherent) when a last-block epilogue will read it back.
+// Residual input of output (mi, n), in two steps so that kernels can request
+// every row index first and every value later, none waiting on another:
+// res_row() the residual row of input row mi, res_at() the value (0 when the
+// epilogue has no residual).  Addresses are wave-uniform: every lane reads.
+__device__ __forceinline__ int res_row(const GemvArgs& a, int mi) {
+  return (a.epi == kEpiResidual && a.res_row_idx ? a.res_row_idx[mi] : mi) + a.res_row_add;
+}
+__device__ __forceinline__ float res_at(const GemvArgs& a, int row, int n) {
+  return a.epi == kEpiResidual ? a.res[static_cast<int64_t>(row) * a.ldres + n] : 0.f;
+}
+__device__ __forceinline__ float res_value(const GemvArgs& a, int mi, int n) { return res_at(a, res_row(a, mi), n); }
+
+// Store / residual / pair epilogue for one output value (res from res_value);
+// published (device coherent) when a last-block epilogue will read it back.
 template <bool PAIR>
-__device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, float g, float u) {
+__device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, float g, float u, float res) {
   float v = g;
-  if (PAIR) {
+  if (PAIR)
     v = g / (1.f + expf(-g)) * u;
-  } else if (a.epi == kEpiResidual) {
-    const int64_t rr = (a.res_row_idx ? a.res_row_idx[mi] : mi) + a.res_row_add;
-    v = a.res[rr * a.ldres + n] + v;
-  }
+  else if (a.epi == kEpiResidual)
+    v = res + v;
   float* dst = a.y + mi * a.ldy + n;
   if (a.fin_counter)
     publish_f32(dst, v);
@@ -184,25 +211,49 @@ __device__ __forceinline__ void store_out(const GemvArgs& a, int mi, int n, floa
 __device__ __forceinline__ void fin_epilogue(const GemvArgs& a, int m, float* s_red) {
   if (!last_block_done(a.fin_counter, gridDim.x)) return;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int adv = (threadIdx.x == 0 && a.adv_dst) ? *a.adv_src : 0;  // issued early, used last
   if (a.fin_gain) {
+    constexpr int kPer = 16;  // rows up to 16 * 256 = 4096 wide are held in registers
     for (int mi = 0; mi < m; ++mi) {
+      const float* yr = a.y + mi * a.ldy;
       float ss = 0.f;
-      for (int k = threadIdx.x; k < a.N; k += kGemvThreads) {
-        const float v = fetch_f32(a.y + mi * a.ldy + k);
-        ss = fmaf(v, v, ss);
+      float v[kPer];
+      const bool small = a.N <= kPer * kGemvThreads;
+      if (small) {
+        // all loads issued back to back from clamped addresses, masked after
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) v[j] = fetch_f32(yr + min(static_cast<int>(threadIdx.x) + j * kGemvThreads, a.N - 1));
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+          if (static_cast<int>(threadIdx.x) + j * kGemvThreads >= a.N) v[j] = 0.f;
+          ss = fmaf(v[j], v[j], ss);
+        }
+      } else {
+        for (int k = threadIdx.x; k < a.N; k += kGemvThreads) {
+          const float x = fetch_f32(yr + k);
+          ss = fmaf(x, x, ss);
+        }
       }
-      ss = wave_sum(ss);
+      ss = wave_sum_dpp(ss);
       if (lane == 0) s_red[wave] = ss;
       __syncthreads();
       float t = 0.f;
       for (int w = 0; w < kGemvWaves; ++w) t += s_red[w];
       const float inv = 1.f / sqrtf(t / static_cast<float>(a.N) + a.eps);
-      for (int k = threadIdx.x; k < a.N; k += kGemvThreads)
-        a.fin_out[mi * a.ld_fin + k] = fetch_f32(a.y + mi * a.ldy + k) * inv * bf16_to_float(a.fin_gain[k]);
+      if (small) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+          const int k = threadIdx.x + j * kGemvThreads;
+          if (k < a.N) a.fin_out[mi * a.ld_fin + k] = v[j] * inv * bf16_to_float(a.fin_gain[k]);
+        }
+      } else {
+        for (int k = threadIdx.x; k < a.N; k += kGemvThreads)
+          a.fin_out[mi * a.ld_fin + k] = fetch_f32(yr + k) * inv * bf16_to_float(a.fin_gain[k]);
+      }
       __syncthreads();
     }
   }
-  if (threadIdx.x == 0 && a.adv_dst) *a.adv_dst = *a.adv_src + a.adv_add + m;
+  if (threadIdx.x == 0 && a.adv_dst) *a.adv_dst = adv + a.adv_add + m;
 }
 
 // Draft-head value of row n for input row mi (optional logits store, Gumbel noise).
@@ -228,116 +279,153 @@ __device__ __forceinline__ void argmax_epilogue(const GemvArgs& a, int m, unsign
     if (best) atomic_max_u64(&a.slots[(threadIdx.x * kSlots + blockIdx.x % kSlots) * kSlotStride], best);
   }
   if (!last_block_done(a.counter, gridDim.x)) return;
-  if (static_cast<int>(threadIdx.x) < m) {
-    unsigned long long best = 0;
-    for (int j = 0; j < kSlots; ++j) {
-      unsigned long long* sl = &a.slots[(threadIdx.x * kSlots + j) * kSlotStride];
-      const unsigned long long k = atomic_load_u64(sl);
-      best = k > best ? k : best;
-      if (k) atomic_store_u64(sl, 0ull);
+  // thread (row, slot): every slot read in parallel, then a max over the 32
+  // lanes of the row's slots (kSlots == 32 lanes, half a wave)
+  static_assert(kSlots == 32, "one half-wave per row");
+  const int j = threadIdx.x % kSlots;
+  for (int mi = threadIdx.x / kSlots; mi < m; mi += kGemvThreads / kSlots) {
+    unsigned long long* sl = &a.slots[(mi * kSlots + j) * kSlotStride];
+    unsigned long long best = atomic_load_u64(sl);
+    atomic_store_u64(sl, 0ull);
+#pragma unroll
+    for (int o = kSlots / 2; o > 0; o >>= 1) {
+      const unsigned long long other = __shfl_xor(best, o);
+      best = other > best ? other : best;
     }
-    const int row = argmax_key_index(best);
-    a.tok_out[threadIdx.x] = a.d2t ? a.d2t[row] : row;
-    if (a.row_out) a.row_out[threadIdx.x] = row;
+    if (j == 0) {
+      const int row = argmax_key_index(best);
+      a.tok_out[mi] = a.d2t ? a.d2t[row] : row;
+      if (a.row_out) a.row_out[mi] = row;
+    }
   }
 }
 
 // ------------------------------------------------------------------ M = 1
 
-template <int R, bool PAIR, int NIN, int S>
+// Fast path for one input row when every segment's K is a multiple of 512.
+// Load order is x slices, then gains, then weights, so the norm (which needs
+// only the L2-resident x) waits for nothing the weight stream is carrying, and
+// the dot products retire the weight loads in the order they were issued.
+// XB: bit s set = input segment s is bf16.  S: max 512-wide steps per segment.
+template <int R, bool PAIR, int NIN, int S, int XB>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
   constexpr int P = PAIR ? 2 : 1;
   __shared__ float s_red[kGemvWaves];
   __shared__ unsigned long long s_key[kGemvWaves][1];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int m = a.m_dev ? min(max(*a.m_dev, 0), 1) : 1;
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+  const int rrow = res_row(a, 0);
 
-  // 1. every weight load of every input segment, first
-  uint4 w[NIN][R][P][S];
-  bool valid[R];
+  // Every load below is unconditional (addresses clamped into the operands), so
+  // the compiler issues them back to back with no branch or merge between them;
+  // out-of-range steps are zeroed in the x slices, and out-of-range rows are
+  // never stored.
+  // 1. x slices, kept raw until the weights are in flight
+  uint4 xq[NIN][S][2];
+  int steps[NIN];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int n = row0 + r;
-    valid[r] = n < a.N && m > 0;
+  for (int s = 0; s < NIN; ++s) {
+    const InSeg& seg = a.in[s];
+    steps[s] = seg.K / (kWave * 8);
+    const int64_t row = m > 0 ? in_row(seg, 0) : 0;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      int seg, off;
-      row_segment<PAIR>(a, n, p, seg, off);
-#pragma unroll
-      for (int s = 0; s < NIN; ++s) {
-        const uint16_t* wr = valid[r] ? a.w[seg][s] + static_cast<int64_t>(off) * a.ldw[s] : nullptr;
-        const int K = a.in[s].K;
-#pragma unroll
-        for (int u = 0; u < S; ++u) {
-          const int k = u * kWave * 8 + lane * 8;
-          w[s][r][p][u] = (valid[r] && k < K) ? *reinterpret_cast<const uint4*>(wr + k) : make_uint4(0, 0, 0, 0);
-        }
+    for (int u = 0; u < S; ++u) {
+      const int k = min(u, steps[s] - 1) * kWave * 8 + lane * 8;
+      if (XB & (1 << s)) {
+        xq[s][u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + row * seg.ld + k);
+      } else {
+        const float* xp = static_cast<const float*>(seg.x) + row * seg.ld + k;
+        xq[s][u][0] = *reinterpret_cast<const uint4*>(xp);
+        xq[s][u][1] = *reinterpret_cast<const uint4*>(xp + 4);
       }
     }
   }
-
-  // 2. this lane's input slices, the per-segment norm, the dot products
+  // 2. gains (a segment without one reads its weight row 0 and ignores it)
+  uint4 gr[NIN][S];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const uint16_t* gp = a.in[s].gain ? a.in[s].gain : a.w[0][s];
+#pragma unroll
+    for (int u = 0; u < S; ++u)
+      gr[s][u] = *reinterpret_cast<const uint4*>(gp + min(u, steps[s] - 1) * kWave * 8 + lane * 8);
+  }
+  // 3. weights of this wave's rows
+  uint4 w[NIN][R][P][S];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(row0 + r, a.N - 1);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+#pragma unroll
+      for (int s = 0; s < NIN; ++s) {
+        const uint16_t* wr = row_ptr<PAIR>(a, n, p, s) + lane * 8;
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+          w[s][r][p][u] = *reinterpret_cast<const uint4*>(wr + min(u, steps[s] - 1) * kWave * 8);
+      }
+    }
+  }
+  float resv[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) resv[r] = res_at(a, rrow, min(row0 + r, a.N - 1));
+  // 4. per-segment 1/rms and x * gain (waits only for x and gain)
+  float4 xr[NIN][S][2];
+  float inv[NIN];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const bool gain = a.in[s].gain != nullptr;
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      float4 x0, x1;
+      if (XB & (1 << s)) {
+        const uint4 h = xq[s][u][0];
+        x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+        x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
+      } else {
+        x0 = make_float4(__uint_as_float(xq[s][u][0].x), __uint_as_float(xq[s][u][0].y),
+                         __uint_as_float(xq[s][u][0].z), __uint_as_float(xq[s][u][0].w));
+        x1 = make_float4(__uint_as_float(xq[s][u][1].x), __uint_as_float(xq[s][u][1].y),
+                         __uint_as_float(xq[s][u][1].z), __uint_as_float(xq[s][u][1].w));
+      }
+      if (u >= steps[s]) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+      ss = fmaf(x0.x, x0.x, ss); ss = fmaf(x0.y, x0.y, ss); ss = fmaf(x0.z, x0.z, ss); ss = fmaf(x0.w, x0.w, ss);
+      ss = fmaf(x1.x, x1.x, ss); ss = fmaf(x1.y, x1.y, ss); ss = fmaf(x1.z, x1.z, ss); ss = fmaf(x1.w, x1.w, ss);
+      if (gain) {
+        const uint4 g = gr[s][u];
+        x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
+        x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
+      }
+      xr[s][u][0] = x0;
+      xr[s][u][1] = x1;
+    }
+    inv[s] = gain ? 1.f / sqrtf(wave_sum_dpp(ss) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+  }
+  // 5. dot products in weight-issue order
   float acc[R][P];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int p = 0; p < P; ++p) acc[r][p] = 0.f;
+    for (int p = 0; p < P; ++p) {
+      float t = 0.f;
 #pragma unroll
-  for (int s = 0; s < NIN; ++s) {
-    const InSeg& seg = a.in[s];
-    const int64_t row = m > 0 ? in_row(seg, 0) : 0;
-    float part[R][P];
+      for (int s = 0; s < NIN; ++s) {
+        float part = 0.f;
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int p = 0; p < P; ++p) part[r][p] = 0.f;
-    float ss = 0.f;
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int k = u * kWave * 8 + lane * 8;
-      if (k < seg.K && m > 0) {
-        float4 x0, x1;
-        if (seg.dtype == WC_BF16) {
-          const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + row * seg.ld + k);
-          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
-          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
-        } else {
-          const float* xp = static_cast<const float*>(seg.x) + row * seg.ld + k;
-          x0 = *reinterpret_cast<const float4*>(xp);
-          x1 = *reinterpret_cast<const float4*>(xp + 4);
-        }
-        if (seg.gain) {
-          ss = fmaf(x0.x, x0.x, ss); ss = fmaf(x0.y, x0.y, ss); ss = fmaf(x0.z, x0.z, ss); ss = fmaf(x0.w, x0.w, ss);
-          ss = fmaf(x1.x, x1.x, ss); ss = fmaf(x1.y, x1.y, ss); ss = fmaf(x1.z, x1.z, ss); ss = fmaf(x1.w, x1.w, ss);
-          const uint4 g = *reinterpret_cast<const uint4*>(seg.gain + k);
-          x0.x *= bf16_lo(g.x); x0.y *= bf16_hi(g.x); x0.z *= bf16_lo(g.y); x0.w *= bf16_hi(g.y);
-          x1.x *= bf16_lo(g.z); x1.y *= bf16_hi(g.z); x1.z *= bf16_lo(g.w); x1.w *= bf16_hi(g.w);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int p = 0; p < P; ++p) part[r][p] += dot8(w[s][r][p][u], x0, x1);
+        for (int u = 0; u < S; ++u) part += dot8(w[s][r][p][u], xr[s][u][0], xr[s][u][1]);
+        t = fmaf(part, inv[s], t);
       }
+      acc[r][p] = wave_sum_dpp(t);
     }
-    float inv = 1.f;
-    if (seg.gain) inv = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(seg.K) + a.eps);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int p = 0; p < P; ++p) acc[r][p] = fmaf(part[r][p], inv, acc[r][p]);
-  }
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int p = 0; p < P; ++p) acc[r][p] = wave_sum(acc[r][p]);
 
-  // 3. epilogues
+  // 6. epilogues
   if (a.epi != kEpiArgmax) {
     if (lane == 0) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        if (valid[r]) store_out<PAIR>(a, 0, row0 + r, acc[r][0], acc[r][P - 1]);
+        if (row0 + r < a.N && m > 0) store_out<PAIR>(a, 0, row0 + r, acc[r][0], acc[r][P - 1], resv[r]);
     }
     if (a.fin_counter) fin_epilogue(a, m, s_red);
     return;
@@ -346,13 +434,209 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
     unsigned long long best = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (!valid[r]) continue;
+      if (row0 + r >= a.N || m == 0) continue;
       const unsigned long long key = head_key(a, 0, row0 + r, acc[r][0]);
       best = key > best ? key : best;
     }
     s_key[wave][0] = best;
   }
   argmax_epilogue<1>(a, m, s_key);
+}
+
+// ------------------------------------------------------------------ 2..MM rows, x staged in LDS
+
+// Few input rows (M <= MM) with every segment's K a multiple of 512.  The x
+// rows are copied HBM/L2 -> LDS by direct-to-LDS loads (no registers, no wait
+// before the weight loads are issued), gains and the wave's weight rows go to
+// registers, and every wave reduces the sums of squares of all rows itself
+// while it streams x from LDS, so no block-wide reduction is needed.
+// LDS: per segment s, rows 0..M-1 of S * 512 elements each (fp32, or bf16 when
+// XB bit s is set).
+template <int R, bool PAIR, int NIN, int S, int XB, int MM>
+__global__ __launch_bounds__(kGemvThreads) void k_gemvx(GemvArgs a) {
+  constexpr int P = PAIR ? 2 : 1;
+  extern __shared__ float smem[];
+  __shared__ float s_red[kGemvWaves];
+  __shared__ unsigned long long s_key[kGemvWaves][MM];
+  char* xs = reinterpret_cast<char*>(smem);
+  const int lane = threadIdx.x % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int m = a.m_dev ? min(max(*a.m_dev, 0), a.M) : a.M;
+  const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+
+  int steps[NIN];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) steps[s] = a.in[s].K / (kWave * 8);
+
+  // gathered row indices first: the x copies below must not wait on them one by one
+  int xrow_idx[NIN][MM];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s)
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) xrow_idx[s][mi] = in_row(a.in[s], min(mi, a.M - 1));
+  int rrow[MM];
+#pragma unroll
+  for (int mi = 0; mi < MM; ++mi) rrow[mi] = res_row(a, min(mi, a.M - 1));
+
+  // 1. x rows -> LDS: each 1 KB piece (one wave-wide 16-byte load) of row mi,
+  //    segment s, is issued by wave (piece index % waves); rows past m skipped
+  {
+    int seg_off = 0;
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      const InSeg& seg = a.in[s];
+      const int bpe = (XB >> s) & 1 ? 2 : 4;                  // bytes per element
+      const int pieces_per_row = S * 512 * bpe / 1024;        // 1 KB pieces
+#pragma unroll
+      for (int mi = 0; mi < MM; ++mi) {
+        if (mi >= m) continue;
+        const int64_t row = xrow_idx[s][mi];
+        const char* xrow = static_cast<const char*>(seg.x) + row * seg.ld * bpe;
+        const int row_bytes = seg.K * bpe;
+#pragma unroll
+        for (int pc = 0; pc < pieces_per_row; ++pc) {
+          if ((mi * pieces_per_row + pc) % kGemvWaves != wave) continue;
+          const int gb = min(pc * 1024, row_bytes - 1024) + lane * 16;  // clamped into the row
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xrow + gb),
+                                           xs + seg_off + mi * S * 512 * bpe + pc * 1024, 16, 0, 0);
+        }
+      }
+      seg_off += a.M * S * 512 * bpe;
+    }
+  }
+  // 2. gains and weights to registers (loads only, nothing waits on them yet)
+  uint4 gr[NIN][S];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const uint16_t* gp = a.in[s].gain ? a.in[s].gain : a.w[0][s];
+#pragma unroll
+    for (int u = 0; u < S; ++u)
+      gr[s][u] = *reinterpret_cast<const uint4*>(gp + min(u, steps[s] - 1) * kWave * 8 + lane * 8);
+  }
+  uint4 w[NIN][R][P][S];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(row0 + r, a.N - 1);
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int s = 0; s < NIN; ++s) {
+        const uint16_t* wr = row_ptr<PAIR>(a, n, p, s) + lane * 8;
+#pragma unroll
+        for (int u = 0; u < S; ++u)
+          w[s][r][p][u] = *reinterpret_cast<const uint4*>(wr + min(u, steps[s] - 1) * kWave * 8);
+      }
+  }
+  float resv[R][MM];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) resv[r][mi] = res_at(a, rrow[mi], min(row0 + r, a.N - 1));
+  // 3. the LDS copies are the oldest loads: wait for them only, then barrier
+  constexpr int kRegLoads = NIN * S + NIN * R * P * S;
+  static_assert(kRegLoads < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((kRegLoads & 0xf) | ((kRegLoads >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+  __syncthreads();
+
+  // 4. dot products and per-row sums of squares
+  float acc[R][P][MM];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int mi = 0; mi < MM; ++mi) acc[r][p][mi] = 0.f;
+  int seg_off = 0;
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const bool bf = (XB >> s) & 1;
+    const int bpe = bf ? 2 : 4;
+    const bool gain = a.in[s].gain != nullptr;
+    float part[R][P][MM], ss[MM];
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      ss[mi] = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int p = 0; p < P; ++p) part[r][p][mi] = 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      if (u >= steps[s]) continue;  // (continue, not break: keeps the loop fully unrolled)
+      const uint4 g = gr[s][u];
+#pragma unroll
+      for (int mi = 0; mi < MM; ++mi) {
+        if (mi >= m) continue;
+        const char* xp = xs + seg_off + mi * S * 512 * bpe + (u * 512 + lane * 8) * bpe;
+        float4 x0, x1;
+        if (bf) {
+          const uint4 h = *reinterpret_cast<const uint4*>(xp);
+          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
+        } else {
+          x0 = *reinterpret_cast<const float4*>(xp);
+          x1 = *reinterpret_cast<const float4*>(xp + 16);
+        }
+        if (gain) {
+          float t = ss[mi];
+          t = fmaf(x0.x, x0.x, t); t = fmaf(x0.y, x0.y, t); t = fmaf(x0.z, x0.z, t); t = fmaf(x0.w, x0.w, t);
+          t = fmaf(x1.x, x1.x, t); t = fmaf(x1.y, x1.y, t); t = fmaf(x1.z, x1.z, t); t = fmaf(x1.w, x1.w, t);
+          ss[mi] = t;
+          x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
+          x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int p = 0; p < P; ++p) part[r][p][mi] += dot8(w[s][r][p][u], x0, x1);
+      }
+    }
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      const float inv = gain ? 1.f / sqrtf(wave_sum_dpp(ss[mi]) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int p = 0; p < P; ++p) acc[r][p][mi] = fmaf(part[r][p][mi], inv, acc[r][p][mi]);
+    }
+    seg_off += a.M * S * 512 * bpe;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+      for (int mi = 0; mi < MM; ++mi) acc[r][p][mi] = wave_sum_dpp(acc[r][p][mi]);
+
+  // 5. epilogues
+  if (a.epi != kEpiArgmax) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (row0 + r >= a.N) continue;
+#pragma unroll
+        for (int mi = 0; mi < MM; ++mi)
+          if (mi < m) store_out<PAIR>(a, mi, row0 + r, acc[r][0][mi], acc[r][P - 1][mi], resv[r][mi]);
+      }
+    }
+    if (a.fin_counter) fin_epilogue(a, m, s_red);
+    return;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      unsigned long long best = 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (row0 + r >= a.N || mi >= m) continue;
+        const unsigned long long key = head_key(a, mi, row0 + r, acc[r][0][mi]);
+        best = key > best ? key : best;
+      }
+      s_key[wave][mi] = best;
+    }
+  }
+  argmax_epilogue<MM>(a, m, s_key);
 }
 
 // ------------------------------------------------------------------ M > 1
@@ -532,7 +816,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemvm(GemvArgs a) {
         if (!valid[r]) continue;
 #pragma unroll
         for (int mi = 0; mi < MM; ++mi)
-          if (mi < m) store_out<PAIR>(a, mi, row0 + r, acc[r][0][mi], acc[r][P - 1][mi]);
+          if (mi < m) store_out<PAIR>(a, mi, row0 + r, acc[r][0][mi], acc[r][P - 1][mi], res_value(a, mi, row0 + r));
       }
     }
     if (a.fin_counter) fin_epilogue(a, m, s_red);

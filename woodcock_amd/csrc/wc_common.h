@@ -63,6 +63,24 @@ __device__ __forceinline__ double wave_sum(double v) {
   return v;
 }
 
+// Wave-wide sum with DPP lane moves (VALU, no LDS round trip): pairwise and
+// quad exchanges, two rotations complete each 16-lane row, the row broadcasts
+// of lanes 15 and 31 fold the four rows into lane 63, which is read back
+// uniformly.  Same value on every lane on return.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_move<0xB1>(v);        // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);        // quad_perm [2,3,0,1]
+  v += dpp_move<0x124>(v);       // row_ror:4
+  v += dpp_move<0x128>(v);       // row_ror:8
+  v += dpp_move<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_move<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = kWave / 2; m > 0; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
