@@ -227,8 +227,38 @@ def bench_gpu(args):
             _lib.call("wc_kv_compact", kp_, vp_, len(tc), 8, tc[0].capacity, 256, ptr(karr[i, 1:2]),
                       ptr(karr[i, 2:8]), ptr(karr[i, 0:1]), 6, ptr(koff[i:i + 1]), None, s())
 
+    # config 2: stochastic accept/reject at k=5 -- target softmax [6,151936], draft softmax
+    # [5,16384] and the rule over device probabilities
+    from woodcock_amd.synthetic import draw_rows, stochastic_workload
+
+    s_lg, s_dl, s_d2t = stochastic_workload(5, cfg.vocab_size, 16384, seed=args.seed + 5)
+    s_tl = torch.from_numpy(s_lg).to(out1.device)
+    s_dlg = torch.from_numpy(s_dl).to(out1.device)
+    s_d2 = torch.from_numpy(s_d2t).to(out1.device)
+    s_p = torch.empty_like(s_tl)
+    s_q = torch.empty_like(s_dlg)
+    from woodcock_amd.sampling import probs_from_logits as _probs
+
+    _probs(s_dlg, 1.0, out=s_q)
+    s_rows = draw_rows(s_q.cpu().numpy(), 1, np.random.default_rng(args.seed))[0]
+    s_dr = torch.from_numpy(s_d2t[s_rows]).to(out1.device)
+    s_round = torch.zeros(1, dtype=torch.int32, device=out1.device)
+    s_u = _lib.Uniforms(args.seed, ptr(s_round), 0)
+    s_verd = torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, device=out1.device)
+    sws = ptr(rnd.vws)
+
+    def stochastic():
+        for _ in range(REP):
+            _lib.call("wc_probs_from_logits", ptr(s_tl), 6, s_tl.shape[1], s_tl.stride(0), 1.0, ptr(s_p),
+                      s_p.stride(0), sws, s())
+            _lib.call("wc_probs_from_logits", ptr(s_dlg), 5, s_dlg.shape[1], s_dlg.stride(0), 1.0, ptr(s_q),
+                      s_q.stride(0), sws, s())
+            _lib.call("wc_verify_chain_stochastic", ptr(s_p), 6, s_p.shape[1], s_p.stride(0), ptr(s_q), 16384,
+                      s_q.stride(0), ptr(s_d2), ptr(s_dr), None, C.byref(s_u), ptr(s_verd), sws, s())
+
     comps = {}
-    for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts)):
+    for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
+                     ("stochastic", stochastic)):
         fn()
         torch.cuda.synchronize()
         g = capture(fn)
@@ -252,6 +282,7 @@ def bench_gpu(args):
         "head_us": comps["head"],
         "verify_accept_us": comps["verify"],
         "kv_compact_us": comps["compact"],
+        "stochastic_us": comps["stochastic"],
         "head_bytes": head_bytes,
         "step_bytes": step_bytes,
         "compact_bytes_avg": compact_bytes,
@@ -364,6 +395,7 @@ def main():
             "draft_step_hbm_frac": round(step_gbs / PEAK_HBM_GBS, 4),
             "verify_accept_us_k5": round(r["verify_accept_us"], 2),
             "kv_compact_us_config3": round(r["kv_compact_us"], 2),
+            "verify_stochastic_us_config2_k5": round(r["stochastic_us"], 2),
             "head_gemv_us": round(r["head_us"], 2),
         },
         "roofline": {

@@ -92,6 +92,46 @@ int wc_verify_tree_greedy(const float* logits, int rows, int vocab, int64_t ld, 
                           const int32_t* tree_parents_dev, wc_verdict* verdict_dev, void* workspace,
                           wc_stream_t stream);
 
+/* ------------------------------------------------------------------ stochastic verification */
+
+/* Counter-based uniforms: value j of a round is Philox4x64-10 (Salmon et al.,
+ * SC'11) with counter (j/4, *round_dev, purpose, 0) and key (seed, 0), word j%4,
+ * top 53 bits / 2^53.  Stands in for the np.random.Generator the reference
+ * threads through the verification rules (python/woodcock/sampling.py:69-82,143-193). */
+typedef struct wc_uniforms {
+  uint64_t seed;
+  const int32_t* round_dev;
+  int32_t purpose;
+} wc_uniforms;
+
+/* out[r] = softmax(logits[r] / max(T, 1e-6)) in fp32 for r < rows (width n,
+ * row strides ld / ld_out floats; rows <= WC_MAX_NODES).  Top-k / top-p are not
+ * implemented (no configuration uses them).  Replaces probs_from_logits
+ * (python/woodcock/sampling.py:39-55; src/sampling/sampling.cpp:9-45) and the
+ * draft distribution of SpeculativeDecoder._draft_dist (python/woodcock/spec.py:113-125). */
+int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float temperature, float* out,
+                         int64_t ld_out, void* workspace, wc_stream_t stream);
+
+/* Stochastic chain verification (Leviathan et al. 2023 / Chen et al. 2023) with
+ * fp64 decisions: p [rows][ld_p] target probabilities at [x_n, d_1..d_K]
+ * (rows = K+1), q [K][ld_q] the draft distributions the drafts were drawn from,
+ * over the head rows (head_rows wide), d2t_dev [head_rows] the ascending target
+ * id of each head row (NULL = identity), draft_rows_dev [K] the drafts' head
+ * rows (NULL = looked up in d2t).  q is scattered to the vocabulary and
+ * renormalised in fp64; q(d_i) <= 0 rejects without a uniform, else
+ * u < min(1, p(d_i)/q(d_i)) accepts; the next token is drawn from
+ * norm(max(p - q, 0)) at the first rejection (p when that mass is <= 1e-12), or
+ * from p_K.  Writes n_accepted, next, tokens, keep = 0..a and n_uniforms;
+ * status = WC_E_INVALID for a draft outside the vocabulary or a d2t that is not
+ * strictly ascending.  Replaces verify_chain_stochastic
+ * (python/woodcock/sampling.py:69-82, 182-193) as the engine runs it
+ * (verify_tree_stochastic on a chain, python/woodcock/spec.py:316-324,
+ * sampling.py:143-177; src/sampling/sampling.cpp:116-141). */
+int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p, const float* q, int head_rows,
+                               int64_t ld_q, const int32_t* d2t_dev, const int32_t* draft_tokens_dev,
+                               const int32_t* draft_rows_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
+                               void* workspace, wc_stream_t stream);
+
 /* ------------------------------------------------------------------ KV compaction */
 
 /* In-place gather of the accepted entries of the last verify block, in every

@@ -1,0 +1,214 @@
+"""Stochastic chain verification and the temperature softmax on the GPU.
+
+- probabilities: GPU softmax(logits / T) against the oracle's fp32 restatement
+  of probs_from_logits (python/woodcock/sampling.py:39-45), rtol 2e-6;
+- decisions: the accept/reject walk, the uniform count and the emitted token
+  equal the oracle's engine-level round (verify_tree_stochastic on the chain,
+  python/woodcock/spec.py:316-324) fed the same fp32 p and q and the same
+  Philox uniforms, round by round, on the full-vocabulary workload (Zipf target,
+  16384-row draft vocabulary);
+- the law: first emitted token over 10^5 rounds against p row 0 (chi-square),
+  and the exact three-token Markov law of the reference's distribution tests
+  (tests/test_sampling.py:33-92) with the GPU rule in the loop;
+- special cases: a draft outside the draft vocabulary (q = 0, no uniform), p == q
+  (every draft accepted, the bonus token from p_K), K = 0, invalid inputs.
+"""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+from scipy.stats import chisquare
+
+from oracle import core
+from oracle import sampling as S
+from woodcock_amd import _lib
+from woodcock_amd.runtime import new_verdict, ptr
+from woodcock_amd.sampling import PhiloxStream, probs_from_logits, verify_chain_stochastic, verify_chain_stochastic_dev
+from woodcock_amd.synthetic import draw_rows, stochastic_workload
+
+pytestmark = pytest.mark.gpu
+
+K, V, H = 5, 151936, 16384
+SEED = 1234
+
+
+@pytest.fixture(scope="module")
+def workload(cuda):
+    lg, dl, d2t = stochastic_workload(K, V, H, seed=3)
+    dev = torch.device("cuda", 0)
+    tl, dlg, d2 = torch.from_numpy(lg).to(dev), torch.from_numpy(dl).to(dev), torch.from_numpy(d2t).to(dev)
+    p = probs_from_logits(tl, 1.0)
+    q = probs_from_logits(dlg, 1.0)
+    torch.cuda.synchronize()
+    return lg, dl, d2t, tl, dlg, d2, p, q
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7, 1e-7])
+def test_probs_match_oracle(workload, temperature):
+    lg, dl, _, tl, dlg, _, _, _ = workload
+    for host, dev in ((lg, tl), (dl, dlg)):
+        got = probs_from_logits(dev, temperature).cpu().numpy()
+        want = S.probs_from_logits(host, temperature)
+        np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-12)
+        np.testing.assert_allclose(got.sum(-1), 1.0, rtol=1e-5)
+
+
+def test_probs_small_width_and_stride(cuda):
+    dev = torch.device("cuda", 0)
+    x = torch.randn(3, 40, device=dev) * 4
+    out = torch.full((3, 40), -1.0, device=dev)
+    probs_from_logits(x[:, :37], 1.3, out=out[:, :37])
+    want = S.probs_from_logits(x[:, :37].cpu().numpy(), 1.3)
+    np.testing.assert_allclose(out[:, :37].cpu().numpy(), want, rtol=2e-6, atol=1e-12)
+    assert (out[:, 37:] == -1).all()
+
+
+def _oracle_round(p_np, q_np, d2t, drafts, rnd):
+    st = core.UniformStream(SEED, rnd)
+    n, nxt = S.chain_stochastic_round(p_np, q_np, d2t, list(drafts), st)
+    return n, nxt, st.pos
+
+
+def test_rounds_equal_oracle(workload):
+    lg, dl, d2t, tl, dlg, d2, p, q = workload
+    dev = p.device
+    p_np, q_np = p.cpu().numpy(), q.cpu().numpy()
+    rng = np.random.default_rng(7)
+    rows = draw_rows(q_np, 150, rng)
+    drafts = d2t[rows]
+    # a few rounds with drafts outside the draft vocabulary (q = 0: rejected, no uniform)
+    outside = np.setdiff1d(np.arange(V), d2t)
+    drafts[::17, 1] = outside[rng.integers(0, len(outside), size=len(drafts[::17]))]
+    rounds = torch.arange(len(drafts), dtype=torch.int32, device=dev)
+    dd = torch.from_numpy(drafts).to(dev)
+    verd = torch.zeros(len(drafts), _lib.VERDICT_INTS, dtype=torch.int32, device=dev)
+    for r in range(len(drafts)):
+        u = _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0)
+        verify_chain_stochastic_dev(p, q, dd[r], u, d2, verdict=verd[r])
+    verd = verd.cpu().numpy()
+    assert (verd[:, _lib.V_STATUS] == 0).all()
+    seen = set()
+    for r in range(len(drafts)):
+        n, nxt, nu = _oracle_round(p_np, q_np, d2t, drafts[r], r)
+        got = (int(verd[r, _lib.V_N_ACCEPTED]), int(verd[r, _lib.V_NEXT]), int(verd[r, _lib.V_N_UNIFORMS]))
+        assert got == (n, nxt, nu), (r, drafts[r], got, (n, nxt, nu))
+        toks = verd[r, _lib.V_TOKENS:_lib.V_TOKENS + n + 1].tolist()
+        assert toks == list(drafts[r][:n]) + [nxt]
+        assert verd[r, _lib.V_KEEP:_lib.V_KEEP + n + 1].tolist() == list(range(n + 1))
+        seen.add(n)
+    assert len(seen) >= 3, seen  # rejections at several depths are exercised
+
+
+def test_first_token_law_1e5_rounds(workload):
+    """The first emitted token is distributed as p row 0 (the defining property
+    of speculative sampling), over 10^5 rounds of the full-size rule."""
+    lg, dl, d2t, tl, dlg, d2, p, q = workload
+    dev = p.device
+    R = 100_000
+    q_np = q.cpu().numpy()
+    rows = draw_rows(q_np, R, np.random.default_rng(11))
+    dd = torch.from_numpy(d2t[rows]).to(dev)
+    rounds = torch.arange(R, dtype=torch.int32, device=dev)
+    verd = torch.zeros(R, _lib.VERDICT_INTS, dtype=torch.int32, device=dev)
+    rr = torch.from_numpy(rows).to(dev)
+    for r in range(R):
+        u = _lib.Uniforms(SEED + 1, ptr(rounds[r:r + 1]), 0)
+        verify_chain_stochastic_dev(p, q, dd[r], u, d2, draft_rows=rr[r], verdict=verd[r])
+    v = verd.cpu().numpy()
+    assert (v[:, _lib.V_STATUS] == 0).all()
+    first = v[:, _lib.V_TOKENS]
+    p0 = p[0].double().cpu().numpy()
+    top = np.argsort(-p0)[:60]
+    counts = np.array([(first == t).sum() for t in top] + [(~np.isin(first, top)).sum()], np.float64)
+    exp = np.concatenate([p0[top], [1.0 - p0[top].sum()]]) * R
+    assert chisquare(counts, exp * counts.sum() / exp.sum()).pvalue > 1e-3
+    # the accepted-length histogram is non-trivial
+    assert len(np.unique(v[:, _lib.V_N_ACCEPTED])) >= 4
+
+
+# ------------------------------------------------------------------ exact Markov law (tests/test_sampling.py:33-92)
+
+MV, N_EMIT = 5, 3
+
+
+def _markov(seed, sharp):
+    return np.random.default_rng(seed).dirichlet(np.full(MV, sharp), size=MV)
+
+
+MP = _markov(1, 0.7)
+MQ = 0.5 * _markov(2, 0.7) + 0.5 * MP
+
+
+def test_markov_exact_law_with_gpu_rule(cuda):
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(0)
+    Kc = 3
+    trials = 6000
+    counts = np.zeros(MV ** N_EMIT)
+    stream = PhiloxStream(seed=77)
+    Pt = torch.from_numpy(MP.astype(np.float32)).to(dev)
+    Qt = torch.from_numpy(MQ.astype(np.float32)).to(dev)
+    for _ in range(trials):
+        out = []
+        while len(out) < N_EMIT:
+            prev = out[-1] if out else 0
+            toks, cur = [], prev
+            for _ in range(Kc):
+                x = int(rng.choice(MV, p=MQ[cur]))
+                toks.append(x)
+                cur = x
+            ctx = [prev] + toks
+            p = Pt[ctx]
+            q = Qt[ctx[:-1]]
+            n, nxt = verify_chain_stochastic(p, q, toks, stream)
+            out.extend(toks[:n] + [nxt])
+        counts[np.ravel_multi_index(tuple(out[:N_EMIT]), (MV,) * N_EMIT)] += 1
+    law = np.zeros((MV,) * N_EMIT)
+    for seq in itertools.product(range(MV), repeat=N_EMIT):
+        pr, prev = 1.0, 0
+        for t in seq:
+            pr *= MP[prev, t]
+            prev = t
+        law[seq] = pr
+    exp = law.ravel() * counts.sum()
+    keep = exp > 0
+    assert chisquare(counts[keep], exp[keep] * counts[keep].sum() / exp[keep].sum()).pvalue > 1e-3
+
+
+# ------------------------------------------------------------------ special cases
+
+def test_equal_distributions_accept_all_and_sample_bonus(cuda):
+    dev = torch.device("cuda", 0)
+    p = torch.softmax(torch.randn(4, 300, device=dev), -1)
+    q = p[:3].clone()
+    drafts = [int(torch.argmax(p[i])) for i in range(3)]
+    for r in range(20):
+        st = PhiloxStream(seed=5, round=r)
+        n, nxt = verify_chain_stochastic(p, q, drafts, st)
+        ost = core.UniformStream(5, r)
+        want = S.chain_stochastic_round(p.cpu().numpy(), q.cpu().numpy(), None, drafts, ost)
+        assert (n, nxt) == want and n == 3
+
+
+def test_no_drafts_samples_p0(cuda):
+    dev = torch.device("cuda", 0)
+    p = torch.softmax(torch.randn(1, 1000, device=dev) * 2, -1)
+    for r in range(10):
+        n, nxt = verify_chain_stochastic(p, torch.empty(0, 1, device=dev), [], PhiloxStream(seed=9, round=r))
+        want = S.sample(p[0].cpu().numpy().astype(np.float64), core.UniformStream(9, r))
+        assert (n, nxt) == (0, want)
+
+
+def test_invalid_inputs_raise(cuda):
+    dev = torch.device("cuda", 0)
+    p = torch.softmax(torch.randn(3, 100, device=dev), -1)
+    q = torch.softmax(torch.randn(2, 10, device=dev), -1)
+    bad_d2t = torch.tensor([5, 3, 7, 9, 11, 12, 13, 14, 15, 16], dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError):
+        verify_chain_stochastic(p, q, [5, 7], PhiloxStream(seed=1), d2t=bad_d2t)
+    ok_d2t = torch.arange(10, dtype=torch.int32, device=dev) * 3
+    with pytest.raises(ValueError):
+        verify_chain_stochastic(p, q, [5, 100], PhiloxStream(seed=1), d2t=ok_d2t)
+    with pytest.raises(ValueError):
+        verify_chain_stochastic(p, q, [5], PhiloxStream(seed=1), d2t=ok_d2t)

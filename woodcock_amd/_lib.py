@@ -80,6 +80,12 @@ class Gumbel(C.Structure):
 
     _fields_ = [("seed", C.c_uint64), ("round_dev", C.c_void_p), ("purpose", C.c_int32), ("temperature", C.c_float)]
 
+class Uniforms(C.Structure):
+    """Mirror of wc_uniforms."""
+
+    _fields_ = [("seed", C.c_uint64), ("round_dev", C.c_void_p), ("purpose", C.c_int32)]
+
+
 _SIGS = {
     "wc_version": ([], C.c_int),
     "wc_last_error": ([], C.c_char_p),
@@ -95,6 +101,8 @@ _SIGS = {
     "wc_drafter_forward": ([P, P, P, P, I64, P, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int, P, C.c_int, P, P, I64,
                             P, P, P, P, P], C.c_int),
     "wc_draft_head": ([P, P, P, I64, P, C.c_int, C.c_int, P, I64, P, P, P, P, P], C.c_int),
+    "wc_probs_from_logits": ([P, C.c_int, C.c_int, I64, C.c_float, P, I64, P, P], C.c_int),
+    "wc_verify_chain_stochastic": ([P, C.c_int, C.c_int, I64, P, C.c_int, I64, P, P, P, P, P, P, P], C.c_int),
 }
 
 _lib = None

@@ -120,32 +120,6 @@ __device__ __forceinline__ int in_row(const InSeg& s, int m) {
   return r;
 }
 
-// Philox4x64-10 (Salmon et al., SC'11): same stream as the host oracle.
-__device__ __forceinline__ void philox4x64(unsigned long long c[4], unsigned long long k0, unsigned long long k1) {
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    if (r) {
-      k0 += 0x9E3779B97F4A7C15ull;
-      k1 += 0xBB67AE8584CAA73Bull;
-    }
-    const unsigned long long lo0 = 0xD2E7470EE14C6C93ull * c[0], hi0 = __umul64hi(0xD2E7470EE14C6C93ull, c[0]);
-    const unsigned long long lo1 = 0xCA5A826395121157ull * c[2], hi1 = __umul64hi(0xCA5A826395121157ull, c[2]);
-    const unsigned long long n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
-    c[0] = n0;
-    c[1] = lo1;
-    c[2] = n2;
-    c[3] = lo0;
-  }
-}
-
-// uniform i of (seed, round, purpose): counter (i/4, round, purpose, 0), key (seed, 0), word i%4
-__device__ __forceinline__ double philox_uniform(unsigned long long seed, unsigned long long round, int purpose,
-                                                 unsigned long long i) {
-  unsigned long long c[4] = {i >> 2, round, static_cast<unsigned long long>(purpose), 0ull};
-  philox4x64(c, seed, 0ull);
-  return static_cast<double>(c[i & 3] >> 11) * (1.0 / 9007199254740992.0);
-}
-
 // (segment, offset) of logical row n; PAIR rows live in segments 0 and 1 at offset n
 template <bool PAIR>
 __device__ __forceinline__ void row_segment(const GemvArgs& a, int n, int p, int& seg, int& off) {

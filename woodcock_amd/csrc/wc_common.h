@@ -39,9 +39,10 @@ const char* last_error();
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // ------------------------------------------------------------------ workspace layout
-// The verify kernels share one small zero-initialised workspace:
+// The verify kernels share one zero-initialised workspace:
 //   [0, 8*WC_MAX_NODES)                  per-row argmax slots (uint64 keys)
 //   then kNumCounters tree counters      (kTreeCounterBytes each, see last_block_done)
+//   then the stochastic / softmax scratch (kStochRowOff ... kVerifyWorkspace)
 constexpr size_t kSlotBytes = 8 * WC_MAX_NODES;
 constexpr size_t kCounterOff = kSlotBytes;
 constexpr int kNumCounters = 4;
@@ -112,6 +113,32 @@ __device__ __forceinline__ int argmax_key_index(unsigned long long k) {
   return 0x7fffffff - static_cast<int>(static_cast<uint32_t>(k & 0xffffffffu));
 }
 
+// Philox4x64-10 (Salmon et al., SC'11): same stream as the host oracle.
+__device__ __forceinline__ void philox4x64(unsigned long long c[4], unsigned long long k0, unsigned long long k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += 0x9E3779B97F4A7C15ull;
+      k1 += 0xBB67AE8584CAA73Bull;
+    }
+    const unsigned long long lo0 = 0xD2E7470EE14C6C93ull * c[0], hi0 = __umul64hi(0xD2E7470EE14C6C93ull, c[0]);
+    const unsigned long long lo1 = 0xCA5A826395121157ull * c[2], hi1 = __umul64hi(0xCA5A826395121157ull, c[2]);
+    const unsigned long long n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0;
+    c[1] = lo1;
+    c[2] = n2;
+    c[3] = lo0;
+  }
+}
+
+// uniform i of (seed, round, purpose): counter (i/4, round, purpose, 0), key (seed, 0), word i%4
+__device__ __forceinline__ double philox_uniform(unsigned long long seed, unsigned long long round, int purpose,
+                                                 unsigned long long i) {
+  unsigned long long c[4] = {i >> 2, round, static_cast<unsigned long long>(purpose), 0ull};
+  philox4x64(c, seed, 0ull);
+  return static_cast<double>(c[i & 3] >> 11) * (1.0 / 9007199254740992.0);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_float(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
@@ -168,7 +195,19 @@ constexpr int kTreeGroups = 64;
 constexpr int kCounterStride = 32;  // uints: one 128-byte line per counter
 constexpr size_t kTreeCounterBytes = 4 * kCounterStride * (kTreeGroups + 1);
 
-constexpr size_t kVerifyWorkspace = kCounterOff + kNumCounters * kTreeCounterBytes;
+// Stochastic verification and probability kernels, after the counters:
+//   per verify row (Q = draft mass, p(x), q(x) at the drafted token) as fp64,
+//   per vocabulary chunk (residual mass, target mass) as fp64,
+//   per (row, chunk) (max, sum of exp) of the softmax kernels as fp32.
+constexpr int kVocabChunk = 4096;
+constexpr int kMaxVocabChunks = 512;  // vocabularies up to 2,097,152 entries
+constexpr size_t kStochRowOff = kCounterOff + kNumCounters * kTreeCounterBytes;
+constexpr size_t kStochRowBytes = 8 * 4 * WC_MAX_NODES;
+constexpr size_t kStochChunkOff = kStochRowOff + kStochRowBytes;
+constexpr size_t kStochChunkBytes = 8 * 2 * kMaxVocabChunks;
+constexpr size_t kProbsOff = kStochChunkOff + kStochChunkBytes;
+constexpr size_t kProbsBytes = 4 * 2 * static_cast<size_t>(WC_MAX_NODES) * kMaxVocabChunks;
+constexpr size_t kVerifyWorkspace = kProbsOff + kProbsBytes;
 inline unsigned int* verify_counter(void* ws, int which) {
   return reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + kCounterOff + which * kTreeCounterBytes);
 }

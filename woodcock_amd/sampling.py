@@ -1,12 +1,19 @@
 """Speculative verification rules on the GPU (python/woodcock/sampling.py API).
 
 Greedy rules run as one fused kernel (target argmax + acceptance) that writes a
-device-side ``wc_verdict``; the host-facing functions read it back (one copy)
-and return the reference's ``(n, next)`` / ``(path, next)`` tuples.  The
+device-side ``wc_verdict``; the stochastic chain rule runs as two launches over
+device probabilities.  The host-facing functions read the verdict back (one
+copy) and return the reference's ``(n, next)`` / ``(path, next)`` tuples.  The
 ``*_dev`` variants leave the verdict on the device for a fused round.
+
+Randomness: where the reference threads a numpy Generator through the rules,
+these take a ``PhiloxStream`` -- (seed, round, purpose) of the counter-based
+stream the kernels read; uniform j of a round is consumed in the reference's
+order (sampling.py:79,165,193).
 """
 from __future__ import annotations
 
+import ctypes as C
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -141,3 +148,86 @@ def verify_tree_greedy(target_logits: torch.Tensor, tree: DraftTree) -> tuple[li
         raise ValueError(f"at most {_lib.WC_MAX_NODES} tree nodes per round")
     v = read_verdict(verify_tree_greedy_dev(lg, i32(tree.tokens, lg.device), i32(tree.parents, lg.device)))
     return [int(v.keep[1 + i]) for i in range(v.n_accepted)], int(v.next)
+
+
+# ------------------------------------------------------------------ stochastic rules
+
+@dataclass
+class PhiloxStream:
+    """Uniform source of the stochastic kernels: round ``round`` of Philox4x64-10
+    under ``seed``, sub-stream ``purpose``.  ``round_dev`` (int32 [1] on the
+    device) is what the kernels read, so a captured graph advances by updating it."""
+
+    seed: int
+    round: int = 0
+    purpose: int = 0
+    round_dev: torch.Tensor | None = None
+
+    def device_round(self, device) -> torch.Tensor:
+        if self.round_dev is None or self.round_dev.device != device:
+            self.round_dev = i32([self.round], device)
+        else:
+            self.round_dev.fill_(self.round)
+        return self.round_dev
+
+    def struct(self, round_dev: torch.Tensor) -> _lib.Uniforms:
+        return _lib.Uniforms(self.seed, ptr(round_dev), self.purpose)
+
+
+def probs_from_logits(logits: torch.Tensor, sp: SamplingParams | float, out: torch.Tensor | None = None
+                      ) -> torch.Tensor:
+    """Warped float32 distribution over the last axis (python/woodcock/sampling.py:39-55):
+    softmax(logits / max(T, 1e-6)).  Top-k / top-p raise: no configuration uses them."""
+    t = sp if isinstance(sp, (int, float)) else sp.temperature
+    if not isinstance(sp, (int, float)) and (sp.top_k or sp.top_p < 1.0):
+        raise NotImplementedError("top-k / top-p warping is not implemented on the GPU")
+    lg = _logits_2d(logits)
+    out = torch.empty_like(lg) if out is None else out
+    if out.shape != lg.shape or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be a float32 tensor shaped like logits")
+    _lib.call("wc_probs_from_logits", ptr(lg), lg.shape[0], lg.shape[1], lg.stride(0), float(t), ptr(out),
+              out.stride(0), ptr(workspace(lg.device)), stream_ptr())
+    return out
+
+
+def verify_chain_stochastic_dev(p: torch.Tensor, q: torch.Tensor, draft_tokens: torch.Tensor,
+                                rng: _lib.Uniforms, d2t: torch.Tensor | None = None,
+                                draft_rows: torch.Tensor | None = None,
+                                verdict: torch.Tensor | None = None) -> torch.Tensor:
+    """Enqueue the stochastic chain rule; p (K+1, V) target probabilities, q (K, H)
+    draft probabilities over the H head rows (d2t maps row -> token; None = identity)."""
+    p2 = _logits_2d(p)
+    rows, vocab = p2.shape
+    K = rows - 1
+    if draft_tokens.numel() != K:
+        raise ValueError(f"{rows} probability rows need {K} draft tokens, got {draft_tokens.numel()}")
+    if K > 0:
+        q2 = _logits_2d(q)
+        if q2.shape[0] < K:
+            raise ValueError(f"q has {q2.shape[0]} rows, {K} needed")
+        head_rows, ldq, qp = q2.shape[1], q2.stride(0), ptr(q2)
+    else:
+        head_rows, ldq, qp = 1, 1, None
+    if d2t is not None and d2t.numel() != head_rows:
+        raise ValueError(f"d2t has {d2t.numel()} entries for {head_rows} draft rows")
+    verdict = new_verdict(p2.device) if verdict is None else verdict
+    _lib.call("wc_verify_chain_stochastic", ptr(p2), rows, vocab, p2.stride(0), qp, head_rows, ldq,
+              ptr(d2t) if d2t is not None else None, ptr(draft_tokens) if K > 0 else None,
+              ptr(draft_rows) if draft_rows is not None else None, C.byref(rng), ptr(verdict),
+              ptr(workspace(p2.device)), stream_ptr())
+    return verdict
+
+
+def verify_chain_stochastic(p: torch.Tensor, q: torch.Tensor, draft_tokens, rng: PhiloxStream,
+                            d2t: torch.Tensor | None = None) -> tuple[int, int]:
+    """p (K+1, V) target probabilities, q (K, H) draft probabilities the tokens were
+    drawn from -> (n_accepted, next_token) (python/woodcock/sampling.py:69-82).
+    Advances ``rng.round`` by one."""
+    p2 = _logits_2d(p)
+    dev = p2.device
+    d = draft_tokens if isinstance(draft_tokens, torch.Tensor) else i32(list(draft_tokens), dev)
+    rd = rng.device_round(dev)
+    u = rng.struct(rd)
+    v = read_verdict(verify_chain_stochastic_dev(p2, q, d.to(dev, torch.int32), u, d2t))
+    rng.round += 1
+    return int(v.n_accepted), int(v.next)

@@ -115,3 +115,33 @@ class SyntheticTarget:
         self._prev_val.copy_(self.logits[rows, self._prev_idx])
         vals = torch.where(rows < n_agree, self._big, torch.where(rows == n_agree, self._block, self._prev_val))
         self.logits.index_put_((rows, self._prev_idx), vals)
+
+
+def stochastic_workload(k: int, vocab: int, head_rows: int, seed: int = 0, zipf_s: float = 1.1,
+                        noise: float = 0.5, always=()):
+    """Accept/reject workload (host numpy): target logits [k+1, vocab] fp32 =
+    log of a Zipf(s) law over a seeded permutation per row; a head_rows-entry
+    ascending draft vocabulary d2t; draft logits [k, head_rows] fp32 =
+    log p_i[d2t] + N(0, noise^2), so q_i = softmax of them is close to but not
+    equal to p_i restricted to the draft vocabulary."""
+    rng = np.random.default_rng(seed)
+    ranks = np.arange(1, vocab + 1, dtype=np.float64)
+    law = ranks ** -zipf_s
+    law /= law.sum()
+    logits = np.empty((k + 1, vocab), np.float32)
+    for i in range(k + 1):
+        logits[i, rng.permutation(vocab)] = np.log(law).astype(np.float32)
+    # the draft vocabulary: row 0's likeliest half plus seeded draft_vocab ids
+    top = np.argsort(-logits[0])[: head_rows // 2]
+    rest = np.setdiff1d(draft_vocab(vocab, head_rows, seed=seed, always=always), top)
+    d2t = np.sort(np.concatenate([top, rest[: head_rows - len(top)]])).astype(np.int32)
+    draft_logits = (logits[:k][:, d2t] + noise * rng.standard_normal((k, len(d2t)))).astype(np.float32)
+    return logits, draft_logits, d2t
+
+
+def draw_rows(q_rows: np.ndarray, n: int, rng: np.random.Generator) -> np.ndarray:
+    """n independent draws of a head row from each distribution q_rows[i] -> [n, K] int32."""
+    c = np.cumsum(np.asarray(q_rows, np.float64), axis=-1)
+    u = rng.random((n, q_rows.shape[0])) * c[:, -1]
+    return np.stack([np.minimum(np.searchsorted(c[i], u[:, i], side="right"), c.shape[1] - 1)
+                     for i in range(q_rows.shape[0])], axis=1).astype(np.int32)
