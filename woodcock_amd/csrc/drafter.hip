@@ -262,7 +262,7 @@ __device__ __forceinline__ void kv_chunk_fill(const KvChunk<D, KT>& r, int c0, i
 // q / new-row sources and gains, then the first chunk, then the RoPE rows.
 template <int D, typename KT>
 __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
-  extern __shared__ float lds[];
+  extern __shared__ __attribute__((aligned(16))) float lds[];  // 16-byte aligned for b128 accesses
   constexpr int CH = attn_chunk<D>();
   constexpr int ACC = (kMaxQV * D + kAttnThreads - 1) / kAttnThreads;
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
@@ -542,7 +542,9 @@ static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, 
 // Weight registers per lane are 4 * R * P * NIN * S; variants above the budget
 // are not instantiated (they would spill) and report false to the dispatcher.
 constexpr int kGemv1Budget = 24;
-constexpr size_t kGemvxMaxLds = 96 * 1024;
+constexpr size_t kCuLds = 160 * 1024 - 2048;       // LDS per CU on gfx950, less the kernels' static LDS
+constexpr int kGemvxBudget = 32;                   // weight vectors per lane of the few-row kernel
+constexpr size_t kGemvxMaxLds = 144 * 1024;        // dynamic LDS of the few-row GEMV, at most
 
 template <int R, bool PAIR, int NIN, int S, int XB>
 static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
@@ -574,7 +576,7 @@ static bool launch_gemv1_r(const GemvArgs& a, int steps, hipStream_t s) {
 // Few-row kernel: x staged in LDS; same register budget for the weights.
 template <int R, bool PAIR, int NIN, int S, int XB, int MM>
 static bool launch_gemvx_s(const GemvArgs& a, size_t lds, hipStream_t s) {
-  if constexpr (R * (PAIR ? 2 : 1) * NIN * S > kGemv1Budget) {
+  if constexpr (R * (PAIR ? 2 : 1) * NIN * S > kGemvxBudget) {
     return false;
   } else {
     const void* fn = reinterpret_cast<const void*>(&k_gemvx<R, PAIR, NIN, S, XB, MM>);
@@ -593,8 +595,7 @@ static bool launch_gemvx_s(const GemvArgs& a, size_t lds, hipStream_t s) {
 template <int R, bool PAIR, int NIN, int XB, int MM>
 static bool launch_gemvx_m(const GemvArgs& a, int steps, hipStream_t s) {
   const int S = steps <= 4 ? 4 : steps <= 8 ? 8 : 12;
-  size_t lds = 0;
-  for (int i = 0; i < NIN; ++i) lds += static_cast<size_t>(a.M) * S * 512 * ((XB >> i) & 1 ? 2 : 4);
+  const size_t lds = static_cast<size_t>(NIN) * a.M * S * 512 * 4;
   if (lds > kGemvxMaxLds) return false;
   if (steps <= 4) return launch_gemvx_s<R, PAIR, NIN, 4, XB, MM>(a, lds, s);
   if (steps <= 8) return launch_gemvx_s<R, PAIR, NIN, 8, XB, MM>(a, lds, s);
@@ -602,16 +603,28 @@ static bool launch_gemvx_m(const GemvArgs& a, int steps, hipStream_t s) {
   return false;
 }
 
+// Rows per wave: the fewest that keep every block resident at once (the LDS
+// footprint sets how many blocks fit on a CU), within the register budget.
+template <bool PAIR, int NIN, int XB, int MM>
+static bool launch_gemvx_r(const GemvArgs& a, int steps, hipStream_t s) {
+  const int S = steps <= 4 ? 4 : steps <= 8 ? 8 : 12;
+  const size_t lds = static_cast<size_t>(NIN) * a.M * S * 512 * 4;
+  const int per_cu = std::max<int>(1, static_cast<int>(kCuLds / std::max<size_t>(lds, 1)));
+  const long resident = 256L * std::min(per_cu, 4);
+  if ((a.N + kGemvWaves - 1) / kGemvWaves <= resident && launch_gemvx_m<1, PAIR, NIN, XB, MM>(a, steps, s))
+    return true;
+  if ((a.N + 2 * kGemvWaves - 1) / (2 * kGemvWaves) <= resident && launch_gemvx_m<2, PAIR, NIN, XB, MM>(a, steps, s))
+    return true;
+  if (launch_gemvx_m<4, PAIR, NIN, XB, MM>(a, steps, s)) return true;
+  if (launch_gemvx_m<2, PAIR, NIN, XB, MM>(a, steps, s)) return true;
+  return launch_gemvx_m<1, PAIR, NIN, XB, MM>(a, steps, s);
+}
+
 template <bool PAIR, int NIN, int XB>
 static bool launch_gemvx(const GemvArgs& a, int steps, hipStream_t s) {
-  if (a.M <= 4) {
-    if (a.N >= 2 * kGemvWaves * 512 && launch_gemvx_m<2, PAIR, NIN, XB, 4>(a, steps, s)) return true;
-    return launch_gemvx_m<1, PAIR, NIN, XB, 4>(a, steps, s);
-  }
-  if (a.M <= 8) {
-    if (a.N >= 2 * kGemvWaves * 512 && launch_gemvx_m<2, PAIR, NIN, XB, 8>(a, steps, s)) return true;
-    return launch_gemvx_m<1, PAIR, NIN, XB, 8>(a, steps, s);
-  }
+  if (a.M <= 2) return launch_gemvx_r<PAIR, NIN, XB, 2>(a, steps, s);
+  if (a.M <= 4) return launch_gemvx_r<PAIR, NIN, XB, 4>(a, steps, s);
+  if (a.M <= 8) return launch_gemvx_r<PAIR, NIN, XB, 8>(a, steps, s);
   return false;
 }
 

@@ -419,30 +419,37 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
 
 // ------------------------------------------------------------------ 2..MM rows, x staged in LDS
 
-// Few input rows (M <= MM) with every segment's K a multiple of 512.  The x
-// rows are copied HBM/L2 -> LDS by direct-to-LDS loads (no registers, no wait
-// before the weight loads are issued), gains and the wave's weight rows go to
-// registers, and every wave reduces the sums of squares of all rows itself
-// while it streams x from LDS, so no block-wide reduction is needed.
-// LDS: per segment s, rows 0..M-1 of S * 512 elements each (fp32, or bf16 when
-// XB bit s is set).
+// Few input rows (M <= MM) with every segment's K a multiple of 512.
+//   1. the wave's weight rows are requested first (all of them);
+//   2. fp32 x rows are copied HBM/L2 -> LDS by direct-to-LDS loads, bf16 rows
+//      (the embedding gather) and the gains go to registers;
+//   3. after the barrier (weights and copies in), the block writes x * gain
+//      as fp32 into LDS once and reduces the per-row sums of squares;
+//   4. each wave runs its weights against x from LDS, widening each weight
+//      vector from bf16 once for all rows.
+// Row addressing uses the host row count M, so nothing waits on the device
+// count m before the loads are issued; m only masks compute and stores.
+// LDS: fp32 [NIN][M][S * 512] (x * gain).
 template <int R, bool PAIR, int NIN, int S, int XB, int MM>
 __global__ __launch_bounds__(kGemvThreads) void k_gemvx(GemvArgs a) {
   constexpr int P = PAIR ? 2 : 1;
-  extern __shared__ float smem[];
+  constexpr int C = S / 4;  // 2048-element chunks of a row: thread t owns elements c*2048 + t*8 .. +8
+  static_assert(S % 4 == 0, "steps in multiples of 4");
+  extern __shared__ __attribute__((aligned(16))) float smem[];  // 16-byte aligned: b128 LDS accesses and LDS DMA
   __shared__ float s_red[kGemvWaves];
+  __shared__ float s_ss[kGemvWaves][NIN * MM];
   __shared__ unsigned long long s_key[kGemvWaves][MM];
-  char* xs = reinterpret_cast<char*>(smem);
   const int lane = threadIdx.x % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int m = a.m_dev ? min(max(*a.m_dev, 0), a.M) : a.M;
   const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
+  const int row_len = S * 512;  // LDS row stride (floats)
 
   int steps[NIN];
 #pragma unroll
   for (int s = 0; s < NIN; ++s) steps[s] = a.in[s].K / (kWave * 8);
 
-  // gathered row indices first: the x copies below must not wait on them one by one
+  // 0. gathered row indices (before anything that would wait on them one by one)
   int xrow_idx[NIN][MM];
 #pragma unroll
   for (int s = 0; s < NIN; ++s)
@@ -452,41 +459,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemvx(GemvArgs a) {
 #pragma unroll
   for (int mi = 0; mi < MM; ++mi) rrow[mi] = res_row(a, min(mi, a.M - 1));
 
-  // 1. x rows -> LDS: each 1 KB piece (one wave-wide 16-byte load) of row mi,
-  //    segment s, is issued by wave (piece index % waves); rows past m skipped
-  {
-    int seg_off = 0;
-#pragma unroll
-    for (int s = 0; s < NIN; ++s) {
-      const InSeg& seg = a.in[s];
-      const int bpe = (XB >> s) & 1 ? 2 : 4;                  // bytes per element
-      const int pieces_per_row = S * 512 * bpe / 1024;        // 1 KB pieces
-#pragma unroll
-      for (int mi = 0; mi < MM; ++mi) {
-        if (mi >= m) continue;
-        const int64_t row = xrow_idx[s][mi];
-        const char* xrow = static_cast<const char*>(seg.x) + row * seg.ld * bpe;
-        const int row_bytes = seg.K * bpe;
-#pragma unroll
-        for (int pc = 0; pc < pieces_per_row; ++pc) {
-          if ((mi * pieces_per_row + pc) % kGemvWaves != wave) continue;
-          const int gb = min(pc * 1024, row_bytes - 1024) + lane * 16;  // clamped into the row
-          __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xrow + gb),
-                                           xs + seg_off + mi * S * 512 * bpe + pc * 1024, 16, 0, 0);
-        }
-      }
-      seg_off += a.M * S * 512 * bpe;
-    }
-  }
-  // 2. gains and weights to registers (loads only, nothing waits on them yet)
-  uint4 gr[NIN][S];
-#pragma unroll
-  for (int s = 0; s < NIN; ++s) {
-    const uint16_t* gp = a.in[s].gain ? a.in[s].gain : a.w[0][s];
-#pragma unroll
-    for (int u = 0; u < S; ++u)
-      gr[s][u] = *reinterpret_cast<const uint4*>(gp + min(u, steps[s] - 1) * kWave * 8 + lane * 8);
-  }
+  // 1. the wave's weight rows first: the stream starts at once
   uint4 w[NIN][R][P][S];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -501,18 +474,118 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemvx(GemvArgs a) {
           w[s][r][p][u] = *reinterpret_cast<const uint4*>(wr + min(u, steps[s] - 1) * kWave * 8);
       }
   }
+
+  // 2a. fp32 rows -> LDS in 1 KB pieces (one wave-wide 16-byte load each); wave w
+  //     issues pieces w, w+4, ... of every row.  Branch-free: every one of the
+  //     M rows is copied (rows past the device row count are never used).
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    if ((XB >> s) & 1) continue;
+    const InSeg& seg = a.in[s];
+    constexpr int kPieces = S * 512 * 4 / 1024;
+    static_assert(kPieces % kGemvWaves == 0, "pieces per row split evenly over the waves");
+    const int row_bytes = seg.K * 4;
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      if (mi >= a.M) continue;
+      const int slot = mi;
+      const char* xrow = static_cast<const char*>(seg.x) + static_cast<int64_t>(xrow_idx[s][mi]) * seg.ld * 4;
+#pragma unroll
+      for (int k = 0; k < kPieces / kGemvWaves; ++k) {
+        const int pc = k * kGemvWaves + wave;
+        const int gb = min(pc * 1024, row_bytes - 1024) + lane * 16;  // clamped into the row
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(xrow + gb),
+                                         smem + (s * a.M + slot) * row_len + pc * 256, 16, 0, 0);
+      }
+    }
+  }
+  // 2b. bf16 rows -> registers (8 elements per thread and chunk), gains of the
+  //     thread's elements
+  uint4 xb[NIN][MM][C];
+  uint4 gq[NIN][C];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const InSeg& seg = a.in[s];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int e = min(c * 2048 + static_cast<int>(threadIdx.x) * 8, seg.K - 8);
+      const uint16_t* gp = seg.gain ? seg.gain : a.w[0][s];
+      gq[s][c] = *reinterpret_cast<const uint4*>(gp + e);
+      if ((XB >> s) & 1) {
+#pragma unroll
+        for (int mi = 0; mi < MM; ++mi)
+          xb[s][mi][c] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) +
+                                                         static_cast<int64_t>(xrow_idx[s][mi]) * seg.ld + e);
+      }
+    }
+  }
   float resv[R][MM];
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int mi = 0; mi < MM; ++mi) resv[r][mi] = res_at(a, rrow[mi], min(row0 + r, a.N - 1));
-  // 3. the LDS copies are the oldest loads: wait for them only, then barrier
-  constexpr int kRegLoads = NIN * S + NIN * R * P * S;
-  static_assert(kRegLoads < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((kRegLoads & 0xf) | ((kRegLoads >> 4) << 14) | (0x7 << 4) | (0xf << 8));
+
+  // the copies land before the barrier (the compiler waits for every load here,
+  // the weights included: they were requested first and arrive with the copies)
   __syncthreads();
 
-  // 4. dot products and per-row sums of squares
+  // 3. x * gain into LDS (fp32, in place for fp32 rows) and per-row sums of squares
+  float ss[NIN][MM];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s) {
+    const bool bf = (XB >> s) & 1;
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      ss[s][mi] = 0.f;
+      if (mi >= m) continue;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int e = c * 2048 + static_cast<int>(threadIdx.x) * 8;
+        if (e >= a.in[s].K) continue;
+        float* xp = smem + (s * a.M + mi) * row_len + e;
+        float x[8];
+        if (bf) {
+          const uint4 h = xb[s][mi][c];
+          x[0] = bf16_lo(h.x); x[1] = bf16_hi(h.x); x[2] = bf16_lo(h.y); x[3] = bf16_hi(h.y);
+          x[4] = bf16_lo(h.z); x[5] = bf16_hi(h.z); x[6] = bf16_lo(h.w); x[7] = bf16_hi(h.w);
+        } else {
+          const float4 v0 = *reinterpret_cast<const float4*>(xp), v1 = *reinterpret_cast<const float4*>(xp + 4);
+          x[0] = v0.x; x[1] = v0.y; x[2] = v0.z; x[3] = v0.w; x[4] = v1.x; x[5] = v1.y; x[6] = v1.z; x[7] = v1.w;
+        }
+        float t = ss[s][mi];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t = fmaf(x[j], x[j], t);
+        ss[s][mi] = t;
+        if (a.in[s].gain) {
+          const uint4 g = gq[s][c];
+          x[0] *= bf16_lo(g.x); x[1] *= bf16_hi(g.x); x[2] *= bf16_lo(g.y); x[3] *= bf16_hi(g.y);
+          x[4] *= bf16_lo(g.z); x[5] *= bf16_hi(g.z); x[6] *= bf16_lo(g.w); x[7] *= bf16_hi(g.w);
+        }
+        *reinterpret_cast<float4*>(xp) = make_float4(x[0], x[1], x[2], x[3]);
+        *reinterpret_cast<float4*>(xp + 4) = make_float4(x[4], x[5], x[6], x[7]);
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < NIN; ++s)
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      const float t = wave_sum_dpp(ss[s][mi]);
+      if (lane == 0) s_ss[wave][s * MM + mi] = t;
+    }
+  lds_barrier();
+  float inv[NIN][MM];
+#pragma unroll
+  for (int s = 0; s < NIN; ++s)
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      float t = 0.f;
+#pragma unroll
+      for (int q = 0; q < kGemvWaves; ++q) t += s_ss[q][s * MM + mi];
+      inv[s][mi] = a.in[s].gain ? 1.f / sqrtf(t / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+    }
+
+  // 4. dot products: each weight vector widened once, then used for every row
   float acc[R][P][MM];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -520,61 +593,52 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemvx(GemvArgs a) {
     for (int p = 0; p < P; ++p)
 #pragma unroll
       for (int mi = 0; mi < MM; ++mi) acc[r][p][mi] = 0.f;
-  int seg_off = 0;
 #pragma unroll
   for (int s = 0; s < NIN; ++s) {
-    const bool bf = (XB >> s) & 1;
-    const int bpe = bf ? 2 : 4;
-    const bool gain = a.in[s].gain != nullptr;
-    float part[R][P][MM], ss[MM];
+    float part[R][P][MM];
 #pragma unroll
-    for (int mi = 0; mi < MM; ++mi) {
-      ss[mi] = 0.f;
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int mi = 0; mi < MM; ++mi) part[r][p][mi] = 0.f;
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      if (u >= steps[s]) continue;
+      float wf[R][P][8];
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int p = 0; p < P; ++p) part[r][p][mi] = 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      if (u >= steps[s]) continue;  // (continue, not break: keeps the loop fully unrolled)
-      const uint4 g = gr[s][u];
+        for (int p = 0; p < P; ++p) {
+          const uint4 q = w[s][r][p][u];
+          wf[r][p][0] = bf16_lo(q.x); wf[r][p][1] = bf16_hi(q.x); wf[r][p][2] = bf16_lo(q.y);
+          wf[r][p][3] = bf16_hi(q.y); wf[r][p][4] = bf16_lo(q.z); wf[r][p][5] = bf16_hi(q.z);
+          wf[r][p][6] = bf16_lo(q.w); wf[r][p][7] = bf16_hi(q.w);
+        }
 #pragma unroll
       for (int mi = 0; mi < MM; ++mi) {
         if (mi >= m) continue;
-        const char* xp = xs + seg_off + mi * S * 512 * bpe + (u * 512 + lane * 8) * bpe;
-        float4 x0, x1;
-        if (bf) {
-          const uint4 h = *reinterpret_cast<const uint4*>(xp);
-          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
-          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
-        } else {
-          x0 = *reinterpret_cast<const float4*>(xp);
-          x1 = *reinterpret_cast<const float4*>(xp + 16);
-        }
-        if (gain) {
-          float t = ss[mi];
-          t = fmaf(x0.x, x0.x, t); t = fmaf(x0.y, x0.y, t); t = fmaf(x0.z, x0.z, t); t = fmaf(x0.w, x0.w, t);
-          t = fmaf(x1.x, x1.x, t); t = fmaf(x1.y, x1.y, t); t = fmaf(x1.z, x1.z, t); t = fmaf(x1.w, x1.w, t);
-          ss[mi] = t;
-          x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
-          x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
-        }
+        const float* xp = smem + (s * a.M + mi) * row_len + u * 512 + lane * 8;
+        const float4 x0 = *reinterpret_cast<const float4*>(xp), x1 = *reinterpret_cast<const float4*>(xp + 4);
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int p = 0; p < P; ++p) part[r][p][mi] += dot8(w[s][r][p][u], x0, x1);
+          for (int p = 0; p < P; ++p) {
+            float t = part[r][p][mi];
+            t = fmaf(wf[r][p][0], x0.x, t); t = fmaf(wf[r][p][1], x0.y, t);
+            t = fmaf(wf[r][p][2], x0.z, t); t = fmaf(wf[r][p][3], x0.w, t);
+            t = fmaf(wf[r][p][4], x1.x, t); t = fmaf(wf[r][p][5], x1.y, t);
+            t = fmaf(wf[r][p][6], x1.z, t); t = fmaf(wf[r][p][7], x1.w, t);
+            part[r][p][mi] = t;
+          }
       }
     }
 #pragma unroll
-    for (int mi = 0; mi < MM; ++mi) {
-      const float inv = gain ? 1.f / sqrtf(wave_sum_dpp(ss[mi]) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+      for (int p = 0; p < P; ++p)
 #pragma unroll
-        for (int p = 0; p < P; ++p) acc[r][p][mi] = fmaf(part[r][p][mi], inv, acc[r][p][mi]);
-    }
-    seg_off += a.M * S * 512 * bpe;
+        for (int mi = 0; mi < MM; ++mi) acc[r][p][mi] = fmaf(part[r][p][mi], inv[s][mi], acc[r][p][mi]);
   }
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -627,7 +691,7 @@ __device__ __forceinline__ float4 load4(const InSeg& s, int64_t row, int k) {
 template <int R, int MM, bool PAIR, int U>
 __global__ __launch_bounds__(kGemvThreads) void k_gemvm(GemvArgs a) {
   constexpr int P = PAIR ? 2 : 1;
-  extern __shared__ float smem[];
+  extern __shared__ __attribute__((aligned(16))) float smem[];  // 16-byte aligned: b128 LDS accesses and LDS DMA
   __shared__ float s_red[kGemvWaves];
   __shared__ float s_ss[kGemvWaves][MM];
   __shared__ unsigned long long s_key[kGemvWaves][MM];
