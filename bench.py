@@ -256,14 +256,53 @@ def bench_gpu(args):
             _lib.call("wc_verify_chain_stochastic", ptr(s_p), 6, s_p.shape[1], s_p.stride(0), ptr(s_q), 16384,
                       s_q.stride(0), ptr(s_d2), ptr(s_dr), None, C.byref(s_u), ptr(s_verd), sws, s())
 
+    # config 5: one Qwen3-1.7B target layer over a 60-node draft tree (depth <= 6) at context
+    # 2048 with the tree mask, then the greedy tree verify over [60, 151936] logits
+    from woodcock_amd.cache import KVCache
+    from woodcock_amd.sampling import tree_attention_mask, DraftTree
+    from woodcock_amd.target import TargetConfig, TargetLayer, random_layer
+
+    tcfg = TargetConfig()
+    trng = np.random.default_rng(args.seed + 9)
+    parents, depth = [-1], [0]
+    while len(parents) < 60:
+        p_ = int(trng.integers(0, len(parents)))
+        if depth[p_] < 6:
+            parents.append(p_)
+            depth.append(depth[p_] + 1)
+    tree = DraftTree([int(t) for t in trng.integers(0, cfg.vocab_size, 60)], parents, depth)
+    tl = TargetLayer(tcfg, random_layer(tcfg, seed=args.seed, device=out1.device), out1.device, max_rows=60)
+    tcache = KVCache(tcfg.num_kv_heads, tcfg.head_dim, 2048 + 64, torch.bfloat16, out1.device)
+    tcache.keys.normal_()
+    tcache.values.normal_()
+    tx = torch.randn(60, tcfg.hidden_size, device=out1.device)
+    toff = torch.tensor([2048], dtype=torch.int32, device=out1.device)
+    tpos = torch.tensor([2048 + dd for dd in depth], dtype=torch.int32, device=out1.device)
+    tmask = torch.from_numpy(tree_attention_mask(tree, 2048).astype(np.uint8)).to(out1.device)
+    tl(tx, tcache, toff, tpos, tmask)  # rope table, workspace touched before capture
+
+    def target_layers():
+        for _ in range(REP // 4):
+            tl(tx, tcache, toff, tpos, tmask)
+
+    tlog = torch.randn(60, cfg.vocab_size, device=out1.device) * 3
+    ttok = torch.tensor(tree.tokens, dtype=torch.int32, device=out1.device)
+    tpar = torch.tensor(tree.parents, dtype=torch.int32, device=out1.device)
+
+    def tree_verifies():
+        for _ in range(REP):
+            _lib.call("wc_verify_tree_greedy", ptr(tlog), 60, cfg.vocab_size, tlog.stride(0), ptr(ttok), ptr(tpar),
+                      ptr(vverd), ptr(rnd.vws), s())
+
     comps = {}
+    reps = {"target_layer": REP // 4}
     for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
-                     ("stochastic", stochastic)):
+                     ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies)):
         fn()
         torch.cuda.synchronize()
         g = capture(fn)
         t = gpu_time_graphs([g], max(5, args.steps // 10))
-        comps[name] = float(np.median(t)) / REP
+        comps[name] = float(np.median(t)) / reps.get(name, REP)
     rewind()
     torch.cuda.synchronize()
 
@@ -283,6 +322,8 @@ def bench_gpu(args):
         "verify_accept_us": comps["verify"],
         "kv_compact_us": comps["compact"],
         "stochastic_us": comps["stochastic"],
+        "target_layer_us": comps["target_layer"],
+        "tree_verify_us": comps["tree_verify"],
         "head_bytes": head_bytes,
         "step_bytes": step_bytes,
         "compact_bytes_avg": compact_bytes,
@@ -396,6 +437,9 @@ def main():
             "verify_accept_us_k5": round(r["verify_accept_us"], 2),
             "kv_compact_us_config3": round(r["kv_compact_us"], 2),
             "verify_stochastic_us_config2_k5": round(r["stochastic_us"], 2),
+            "target_layer_us_config5_m60_ctx2048": round(r["target_layer_us"], 2),
+            "target_layer_hbm_frac_config5": round(100_663_296 / (r["target_layer_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "verify_tree_greedy_us_config5_n60": round(r["tree_verify_us"], 2),
             "head_gemv_us": round(r["head_us"], 2),
         },
         "roofline": {

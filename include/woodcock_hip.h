@@ -242,6 +242,30 @@ int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, cons
                   int32_t* token_out, int32_t* row_out, const wc_gumbel* gumbel, void* workspace,
                   wc_stream_t stream);
 
+/* ------------------------------------------------------------------ verify-width target layer */
+
+/* Device workspace for wc_target_layer with up to max_rows rows. */
+size_t wc_target_workspace_bytes(const wc_drafter_dims* dims, int max_rows);
+
+/* One Qwen3 decoder layer over a verify block of `rows` <= 64 tokens, in place
+ * on the fp32 residual stream x [rows][hidden]:
+ *   h = x + W_o . attn(q_norm(W_q xn), k_norm(W_k xn), W_v xn), xn = RMS_in(x);
+ *   x = h + W_down . (silu(W_gate hn) * W_up hn), hn = RMS_post(h);
+ * RoPE at positions_dev [rows] (NULL = offset + r) from the cos/sin table
+ * (wc_rope_table), mask_dev [rows][mask_ld] uint8 over cache slots (NULL =
+ * causal; the tree mask of a draft tree), K/V of the block appended at
+ * *offset_dev in k_cache / v_cache [kv_heads][capacity][head_dim] of kv_dtype.
+ * The caller advances the offset after the last layer.  dims supplies hidden,
+ * heads, kv_heads, head_dim, inter, eps and window; hidden, heads*head_dim and
+ * inter must be multiples of 256; the aux fields of L are ignored.
+ * Replaces _block_forward (python/woodcock/target.py:142-156) as called by
+ * Target.__call__ with positions and a mask (target.py:82-116), and the layer
+ * loop of Qwen3::forward (src/core/qwen3.cpp:86-111). */
+int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, const float* rope_cos,
+                    const float* rope_sin, int rope_max_pos, float* x, int rows, const int32_t* positions_dev,
+                    const uint8_t* mask_dev, int64_t mask_ld, void* k_cache, void* v_cache, int kv_dtype,
+                    int capacity, const int32_t* offset_dev, void* workspace, wc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,19 +13,13 @@
 // argmax / Gumbel-max and d2t map (drafter.py:204-215, spec.py:346).
 // Every round-varying integer (offset, row counts, gathered rows, tokens) is
 // read from device memory.
+#include "attention.h"
 #include "gemv.h"
 
 namespace wc {
 
 // ------------------------------------------------------------------ workspace
 
-constexpr int kAttnThreads = 256;
-constexpr int kAttnChunkMax = 32;  // keys staged per iteration (fewer for head_dim 256)
-template <int D>
-constexpr int attn_chunk() { return D >= 256 ? 16 : kAttnChunkMax; }
-constexpr int kMaxQV = 64;      // query vectors (rows x GQA group) per attention block
-constexpr int kMaxSplits = 32;
-constexpr int kMaxKvHeads = 64;
 
 struct DrafterWs {
   unsigned int* head_ctr;  // tree counters (kTreeCounterBytes each)
@@ -63,478 +57,6 @@ static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
                                             (d.head_dim + 2)));
   w.bytes = off;
   return w;
-}
-
-// ------------------------------------------------------------------ attention
-
-struct AttnArgs {
-  const float* qkv;  // [rows][ld_qkv] raw q | k | v
-  int64_t ld_qkv;
-  int H, Hk, rows;
-  const int32_t* n_rows_dev;
-  const uint16_t *q_gain, *k_gain;
-  float eps, scale;
-  const float *rope_cos, *rope_sin;
-  int rope_max;
-  const int32_t* positions;  // [rows] or NULL
-  void *kc, *vc;             // [Hk][cap][D]
-  int cap;
-  const int32_t* offset_dev;
-  int offset_add;
-  const uint8_t* mask;  // [rows][mask_ld] or NULL
-  int64_t mask_ld;
-  int window;
-  float* partial;  // [Hk][S][kMaxQV][D+2]
-  float* out;  // [rows][H*D]
-  int64_t ld_out;
-};
-
-template <typename KT>
-__device__ __forceinline__ float kv_load(const KT* p, int64_t i);
-template <>
-__device__ __forceinline__ float kv_load<float>(const float* p, int64_t i) {
-  return p[i];
-}
-template <>
-__device__ __forceinline__ float kv_load<uint16_t>(const uint16_t* p, int64_t i) {
-  return bf16_to_float(p[i]);
-}
-// store to the cache, return the stored value as read back (bf16 rounding)
-template <typename KT>
-__device__ __forceinline__ float kv_store(KT* p, int64_t i, float v);
-template <>
-__device__ __forceinline__ float kv_store<float>(float* p, int64_t i, float v) {
-  p[i] = v;
-  return v;
-}
-template <>
-__device__ __forceinline__ float kv_store<uint16_t>(uint16_t* p, int64_t i, float v) {
-  const uint16_t b = float_to_bf16(v);
-  p[i] = b;
-  return bf16_to_float(b);
-}
-
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x % kWave) == 0) red[threadIdx.x / kWave] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int w = 0; w < static_cast<int>(blockDim.x) / kWave; ++w) t += red[w];
-  return t;
-}
-
-// One head vector held by one wave for q/k RMSNorm + rotate-half RoPE
-// (src/backends/cpu_ops.cpp:61-77): lane j owns the pairs (p, p + D/2) for
-// p = j, j + 64, ..., so every value a lane produces was computed by that lane
-// alone.  Loads go to clamped addresses (always in bounds) and lanes with
-// p >= D/2 are masked when the values are used, so a load never sits behind a
-// branch.
-template <int D>
-struct HeadVec {
-  static constexpr int kHalf = D / 2;
-  static constexpr int kPPL = (kHalf + kWave - 1) / kWave;
-  float lo[kPPL], hi[kPPL];
-  uint16_t glo[kPPL], ghi[kPPL];  // raw bf16 gains, widened where used
-  float c[kPPL], sn[kPPL];        // RoPE row of the vector's position
-};
-
-template <int D>
-__device__ __forceinline__ void head_vec_load(const float* src, const uint16_t* gain, HeadVec<D>& r) {
-  const int lane = threadIdx.x % kWave;
-  constexpr int half = HeadVec<D>::kHalf;
-#pragma unroll
-  for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
-    const int p = min(lane + e * kWave, half - 1);
-    r.lo[e] = src[p];
-    r.hi[e] = src[p + half];
-    r.glo[e] = gain[p];
-    r.ghi[e] = gain[p + half];
-  }
-}
-
-template <int D>
-__device__ __forceinline__ void head_vec_rope_load(const float* ct, const float* st, int pos, HeadVec<D>& r) {
-  const int lane = threadIdx.x % kWave;
-  constexpr int half = HeadVec<D>::kHalf;
-#pragma unroll
-  for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
-    const int p = min(lane + e * kWave, half - 1);
-    r.c[e] = ct[static_cast<int64_t>(pos) * half + p];
-    r.sn[e] = st[static_cast<int64_t>(pos) * half + p];
-  }
-}
-
-// Normalise and rotate in place (after head_vec_load and head_vec_rope_load).
-template <int D>
-__device__ __forceinline__ void head_vec_norm_rope(HeadVec<D>& r, float eps) {
-  const int lane = threadIdx.x % kWave;
-  constexpr int half = HeadVec<D>::kHalf, PPL = HeadVec<D>::kPPL;
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < PPL; ++e) {
-    if (lane + e * kWave >= half) r.lo[e] = r.hi[e] = 0.f;
-    ss = fmaf(r.lo[e], r.lo[e], ss);
-    ss = fmaf(r.hi[e], r.hi[e], ss);
-  }
-  ss = wave_sum_dpp(ss);
-  const float inv = 1.f / sqrtf(ss / static_cast<float>(D) + eps);
-#pragma unroll
-  for (int e = 0; e < PPL; ++e) {
-    const float x1 = r.lo[e] * inv * bf16_to_float(r.glo[e]);
-    const float x2 = r.hi[e] * inv * bf16_to_float(r.ghi[e]);
-    r.lo[e] = x1 * r.c[e] - x2 * r.sn[e];
-    r.hi[e] = x2 * r.c[e] + x1 * r.sn[e];
-  }
-}
-
-// Key/value chunk staging: CH rows x D elements of one kv head, read as
-// 16-byte vectors (VE cache elements each), kNL vectors per thread per tensor.
-template <int D, typename KT>
-struct KvChunk {
-  static constexpr int kCH = attn_chunk<D>();
-  static constexpr int kVE = 16 / static_cast<int>(sizeof(KT));
-  static constexpr int kNL = (kCH * D / kVE + kAttnThreads - 1) / kAttnThreads;
-  uint4 k[kNL], v[kNL];
-};
-
-// Issue the loads of rows [c0, c0 + CH) (clamped into the cache; rows past the
-// chunk's end are loaded and ignored).
-template <int D, typename KT>
-__device__ __forceinline__ void kv_chunk_load(const KT* kc, const KT* vc, int cap, int c0, KvChunk<D, KT>& r) {
-  using C = KvChunk<D, KT>;
-  const uint4* k4 = reinterpret_cast<const uint4*>(kc);
-  const uint4* v4 = reinterpret_cast<const uint4*>(vc);
-  const int64_t last = static_cast<int64_t>(cap) * D / C::kVE - 1;
-#pragma unroll
-  for (int i = 0; i < C::kNL; ++i) {
-    const int64_t e = min(static_cast<int64_t>(c0) * D / C::kVE + threadIdx.x + i * kAttnThreads, last);
-    r.k[i] = k4[e];
-    r.v[i] = v4[e];
-  }
-}
-
-template <typename KT>
-__device__ __forceinline__ void unpack16(const uint4 q, float* out);
-template <>
-__device__ __forceinline__ void unpack16<uint16_t>(const uint4 q, float* out) {
-  out[0] = bf16_lo(q.x); out[1] = bf16_hi(q.x); out[2] = bf16_lo(q.y); out[3] = bf16_hi(q.y);
-  out[4] = bf16_lo(q.z); out[5] = bf16_hi(q.z); out[6] = bf16_lo(q.w); out[7] = bf16_hi(q.w);
-}
-template <>
-__device__ __forceinline__ void unpack16<float>(const uint4 q, float* out) {
-  out[0] = __uint_as_float(q.x); out[1] = __uint_as_float(q.y);
-  out[2] = __uint_as_float(q.z); out[3] = __uint_as_float(q.w);
-}
-
-// Write the n staged rows of chunk c0 into LDS; rows at or past `offset` are
-// this launch's appended rows and come from nk / nv instead of the loads.
-template <int D, typename KT>
-__device__ __forceinline__ void kv_chunk_fill(const KvChunk<D, KT>& r, int c0, int n, int offset, const float* nk,
-                                              const float* nv, float* ks, float* vs) {
-  using C = KvChunk<D, KT>;
-#pragma unroll
-  for (int i = 0; i < C::kNL; ++i) {
-    const int e = threadIdx.x + i * kAttnThreads;
-    const int el = e * C::kVE;  // element index within the chunk
-    if (el >= n * D) continue;
-    const int t = c0 + el / D;
-    if (t < offset) {
-      unpack16<KT>(r.k[i], ks + el);
-      unpack16<KT>(r.v[i], vs + el);
-    } else {
-      const int src = (t - offset) * D + el % D;
-#pragma unroll
-      for (int j = 0; j < C::kVE; ++j) {
-        ks[el + j] = nk[src + j];
-        vs[el + j] = nv[src + j];
-      }
-    }
-  }
-}
-
-// One block per (split, kv head).  The block's key range [kb, ke) of the
-// visible rows [0, T) is staged in chunks; the q vectors of the head group are
-// normalised and rotated into LDS; rows appended by this launch (t >= offset)
-// whose slot lies in [kb, ke) are normalised/rotated and written to the cache
-// by this block, which also takes them from LDS rather than reading them back.
-// Every load that does not depend on another is issued before the first wait:
-// q / new-row sources and gains, then the first chunk, then the RoPE rows.
-template <int D, typename KT>
-__global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];  // 16-byte aligned for b128 accesses
-  constexpr int CH = attn_chunk<D>();
-  constexpr int ACC = (kMaxQV * D + kAttnThreads - 1) / kAttnThreads;
-  const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
-  const int rep = a.H / a.Hk;
-  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
-  const int offset = *a.offset_dev + a.offset_add;
-  const int T = min(offset + nr, a.cap);  // never past the cache capacity
-  const int QV = nr * rep, QVb = a.rows * rep;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
-  constexpr int nw = kAttnThreads / kWave;
-
-  float* qs = lds;                 // [QVb][D]
-  float* ks = qs + QVb * D;        // [CH][D]
-  float* vs = ks + CH * D;         // [CH][D]
-  float* sc = vs + CH * D;         // [QVb][CH]
-  float* nk = sc + QVb * CH;       // [rows][D] appended keys (cache-rounded)
-  float* nv = nk + a.rows * D;     // [rows][D] appended values (cache-rounded)
-  __shared__ float s_m[kMaxQV], s_l[kMaxQV], s_alpha[kMaxQV];
-
-  KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
-  KT* vc = static_cast<KT*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
-  const int per = (T + S - 1) / S;
-  const int kb = min(T, split * per), ke = min(T, kb + per);
-
-  // first q vector and first appended row of this wave: sources and gains
-  const int v0 = wave, l0 = nw - 1 - wave;  // appended rows from the last wave down
-  // (loaded unconditionally from clamped rows so that no load sits in a branch)
-  HeadVec<D> qv0, kv0;
-  {
-    const int v = min(v0, QVb - 1), l = v / rep, h = kh * rep + v % rep;
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, qv0);
-  }
-  const bool app0 = l0 < nr && offset + l0 >= kb && offset + l0 < ke;
-  constexpr int VPL = (D + kWave - 1) / kWave;
-  float vv0[VPL];
-  {
-    const int l = min(l0, a.rows - 1);
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, kv0);
-    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
-#pragma unroll
-    for (int e = 0; e < VPL; ++e) vv0[e] = vsrc[min(lane + e * kWave, D - 1)];
-  }
-  // first chunk
-  KvChunk<D, KT> ch;
-  kv_chunk_load<D, KT>(kc, vc, a.cap, kb, ch);
-
-  auto row_pos = [&](int l) {
-    const int pos = a.positions ? a.positions[l] : offset + l;
-    return min(max(pos, 0), a.rope_max - 1);
-  };
-  auto put_q = [&](int v, HeadVec<D>& r) {
-    head_vec_norm_rope<D>(r, a.eps);
-#pragma unroll
-    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
-      const int p = lane + e * kWave;
-      if (p < D / 2) {
-        qs[v * D + p] = r.lo[e];
-        qs[v * D + p + D / 2] = r.hi[e];
-      }
-    }
-  };
-  auto put_kv = [&](int l, HeadVec<D>& r, const float* vv) {
-    const int t = offset + l;
-    head_vec_norm_rope<D>(r, a.eps);
-#pragma unroll
-    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
-      const int p = lane + e * kWave;
-      if (p < D / 2) {
-        nk[l * D + p] = kv_store<KT>(kc, static_cast<int64_t>(t) * D + p, r.lo[e]);
-        nk[l * D + p + D / 2] = kv_store<KT>(kc, static_cast<int64_t>(t) * D + p + D / 2, r.hi[e]);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < VPL; ++e) {
-      const int i = lane + e * kWave;
-      if (i < D) nv[l * D + i] = kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, vv[e]);
-    }
-  };
-
-  head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(min(v0, QVb - 1) / rep), qv0);
-  head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(min(l0, a.rows - 1)), kv0);
-  if (v0 < QV) put_q(v0, qv0);
-  if (app0) put_kv(l0, kv0, vv0);
-  for (int v = v0 + nw; v < QV; v += nw) {
-    HeadVec<D> r;
-    const int l = v / rep, h = kh * rep + v % rep;
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, r);
-    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
-    put_q(v, r);
-  }
-  for (int l = l0 + nw; l < nr; l += nw) {
-    if (offset + l < kb || offset + l >= ke) continue;
-    HeadVec<D> r;
-    float vv[VPL];
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, r);
-    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
-#pragma unroll
-    for (int e = 0; e < VPL; ++e) vv[e] = vsrc[min(lane + e * kWave, D - 1)];
-    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
-    put_kv(l, r, vv);
-  }
-  if (threadIdx.x < kMaxQV) {
-    s_m[threadIdx.x] = -INFINITY;
-    s_l[threadIdx.x] = 0.f;
-  }
-  __syncthreads();
-
-  float acc[ACC];
-#pragma unroll
-  for (int e = 0; e < ACC; ++e) acc[e] = 0.f;
-
-  for (int c0 = kb; c0 < ke; c0 += CH) {
-    const int n = min(CH, ke - c0);
-    kv_chunk_fill<D, KT>(ch, c0, n, offset, nk, nv, ks, vs);
-    __syncthreads();
-    if (c0 + CH < ke) kv_chunk_load<D, KT>(kc, vc, a.cap, c0 + CH, ch);  // next chunk in flight
-    for (int e = threadIdx.x; e < QV * n; e += kAttnThreads) {
-      const int v = e / n, j = e - v * n;
-      const int l = v / rep, t = c0 + j;
-      bool vis;
-      if (a.mask)
-        vis = a.mask[l * a.mask_ld + t] != 0;
-      else
-        vis = t <= offset + l && (a.window <= 0 || t > offset + l - a.window);
-      float s = -INFINITY;
-      if (vis) {
-        float d = 0.f;
-        const float4* q = reinterpret_cast<const float4*>(qs + v * D);
-        const float4* k = reinterpret_cast<const float4*>(ks + j * D);
-#pragma unroll 4
-        for (int i = 0; i < D / 4; ++i) {
-          const float4 x = q[i], y = k[i];
-          d = fmaf(x.x, y.x, d);
-          d = fmaf(x.y, y.y, d);
-          d = fmaf(x.z, y.z, d);
-          d = fmaf(x.w, y.w, d);
-        }
-        s = a.scale * d;
-      }
-      sc[v * CH + j] = s;
-    }
-    __syncthreads();
-    if (threadIdx.x < QV) {
-      const int v = threadIdx.x;
-      const float m_old = s_m[v];
-      float m_new = m_old;
-      for (int j = 0; j < n; ++j) m_new = fmaxf(m_new, sc[v * CH + j]);
-      float alpha = 1.f, lsum = 0.f;
-      if (m_new != -INFINITY) {
-        alpha = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
-        for (int j = 0; j < n; ++j) {
-          const float sv = sc[v * CH + j];
-          const float p = sv == -INFINITY ? 0.f : expf(sv - m_new);
-          sc[v * CH + j] = p;
-          lsum += p;
-        }
-      } else {
-        for (int j = 0; j < n; ++j) sc[v * CH + j] = 0.f;
-      }
-      s_m[v] = m_new;
-      s_l[v] = s_l[v] * alpha + lsum;
-      s_alpha[v] = alpha;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < ACC; ++e) {
-      const int idx = threadIdx.x + e * kAttnThreads;
-      if (idx < QV * D) {
-        const int v = idx / D, i = idx - v * D;
-        float o = acc[e] * s_alpha[v];
-        for (int j = 0; j < n; ++j) o = fmaf(sc[v * CH + j], vs[j * D + i], o);
-        acc[e] = o;
-      }
-    }
-    __syncthreads();
-  }
-
-  // this split's (m, l, o); an empty range leaves m = -inf, l = 0
-  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * kMaxQV * (D + 2);
-#pragma unroll
-  for (int e = 0; e < ACC; ++e) {
-    const int idx = threadIdx.x + e * kAttnThreads;
-    if (idx < QV * D) {
-      const int v = idx / D, i = idx - v * D;
-      part[v * (D + 2) + 2 + i] = acc[e];
-    }
-  }
-  if (threadIdx.x < QV) {
-    part[threadIdx.x * (D + 2)] = s_m[threadIdx.x];
-    part[threadIdx.x * (D + 2) + 1] = s_l[threadIdx.x];
-  }
-}
-
-// Merge the splits: one block per (vector, kv head).  Every load -- the
-// splits' (m, l) and this vector's partial outputs -- is issued up front from
-// addresses that do not depend on the row count; the block then exits if its
-// vector is past the live rows.  Runs after k_attention (stream order), so
-// plain loads see the partials.
-template <int D>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) {
-  constexpr int kPer = (D + kAttnThreads - 1) / kAttnThreads;  // elements per thread (D <= 256: 1)
-  static_assert(kPer == 1, "head_dim up to the block size");
-  __shared__ float s_w[kMaxSplits], s_lsum[kMaxSplits];
-  const int v = blockIdx.x, kh = blockIdx.y;
-  const int rep = a.H / a.Hk;
-  const int t = threadIdx.x;
-  const float* base = a.partial + static_cast<int64_t>(kh) * S * kMaxQV * (D + 2) + v * (D + 2);
-  constexpr int64_t kSplitStride = static_cast<int64_t>(kMaxQV) * (D + 2);
-  const int i = min(t, D - 1);
-  float o[kMaxSplits];
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) o[sp] = base[min(sp, S - 1) * kSplitStride + 2 + i];
-  if (t < S) {
-    s_w[t] = base[t * kSplitStride];
-    s_lsum[t] = base[t * kSplitStride + 1];
-  }
-  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
-  if (v >= nr * rep) return;  // uniform per block
-  __syncthreads();
-  float M = -INFINITY;
-  for (int sp = 0; sp < S; ++sp) M = fmaxf(M, s_w[sp]);
-  float num = 0.f, den = 0.f;
-#pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) {
-    if (sp < S) {
-      const float ms = s_w[sp];
-      const float wgt = ms == -INFINITY ? 0.f : expf(ms - M);
-      den = fmaf(s_lsum[sp], wgt, den);
-      num = fmaf(wgt, o[sp], num);
-    }
-  }
-  if (t < D) {
-    const int l = v / rep, h = kh * rep + v % rep;
-    a.out[l * a.ld_out + h * D + t] = num / den;
-  }
-}
-
-template <int D, typename KT>
-static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream) {
-  constexpr int CH = attn_chunk<D>();
-  const size_t qvb = static_cast<size_t>(a.rows) * (a.H / a.Hk);
-  const size_t lds = sizeof(float) * (qvb * D + 2 * CH * D + qvb * CH + 2 * static_cast<size_t>(a.rows) * D);
-  static size_t attr_bytes = 64 * 1024;  // default dynamic-LDS limit
-  if (lds > attr_bytes) {
-    WC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention<D, KT>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-    attr_bytes = lds;
-  }
-  hipLaunchKernelGGL((k_attention<D, KT>), dim3(splits, a.Hk), dim3(kAttnThreads), lds, stream, a);
-  WC_LAUNCHED();
-  hipLaunchKernelGGL((k_attn_merge<D>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, stream, a,
-                     splits);
-  WC_LAUNCHED();
-  return WC_OK;
-}
-
-static int launch_attention(const AttnArgs& a, int D, int kv_dtype, int splits, hipStream_t s) {
-#define WC_ATT(DD)                                                                                  \
-  case DD:                                                                                          \
-    return kv_dtype == WC_BF16 ? launch_attention_t<DD, uint16_t>(a, splits, s)                   \
-                               : launch_attention_t<DD, float>(a, splits, s);
-  switch (D) {
-    WC_ATT(8)
-    WC_ATT(16)
-    WC_ATT(32)
-    WC_ATT(64)
-    WC_ATT(128)
-    WC_ATT(256)
-    default:
-      return set_error(WC_E_UNSUPPORTED, "head_dim %d not supported (8, 16, 32, 64, 128, 256)", D);
-  }
-#undef WC_ATT
 }
 
 // ------------------------------------------------------------------ GEMV launch
