@@ -95,8 +95,7 @@ def build_workload(seed=0):
     for c in rnd.cache:
         c.keys[0, :, :BASE_CTX] = torch.randn(c.keys[0, :, :BASE_CTX].shape, generator=g, device=dev).bfloat16()
         c.values[0, :, :BASE_CTX] = torch.randn(c.values[0, :, :BASE_CTX].shape, generator=g, device=dev).bfloat16()
-    root = torch.randn(1, cfg.hidden_size, generator=g, device=dev)
-    root = root / root.pow(2).mean().sqrt()
+    root = torch.randn(1, cfg.hidden_size, generator=g, device=dev)  # pre-norm hidden state of the last entry
     rnd.set_root(BASE_CTX, root)
     target = SyntheticTarget(K, cfg.vocab_size, cfg.target_hidden_size, device=dev, seed=seed + 2)
     init_state = rnd.state.clone()
@@ -178,22 +177,25 @@ def bench_gpu(args):
     REP = 32
     dims, W, ws, s = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws), stream_ptr
     dm = cfg.hidden_size
+    hid1 = rnd.upd_hid[0:1]
     out1 = rnd.upd_out[0:1]
     tok = rnd.drafts[0:1]
     hid_s = torch.empty(1, dm, device=out1.device)
-    out_s = torch.empty_like(hid_s)
 
     def heads():
         for _ in range(REP):
-            _lib.call("wc_draft_head", dims, W, ptr(out1), dm, None, 0, 1, None, 0, ptr(tok), None, None, ws, s())
+            _lib.call("wc_draft_head_norm", dims, W, ptr(hid1), dm, None, 0, ptr(out1), dm, None, 0, ptr(tok),
+                      None, None, ws, s())
 
     def steps():
-        # the reference's draft-step unit: head + argmax + one drafter layer, KV rolled back
+        # the reference's draft-step unit: (final norm +) head + argmax + one drafter layer, KV rolled back;
+        # the layer leaves its final norm to the next head, as in the chain
         for _ in range(REP):
-            _lib.call("wc_draft_head", dims, W, ptr(out1), dm, None, 0, 1, None, 0, ptr(tok), None, None, ws, s())
+            _lib.call("wc_draft_head_norm", dims, W, ptr(hid1), dm, None, 0, ptr(out1), dm, None, 0, ptr(tok),
+                      None, None, ws, s())
             _lib.call("wc_drafter_forward", dims, W, ptr(tok), ptr(out1), dm, None, 0, 1, None, rnd._kp, rnd._vp,
                       rnd._kvdt, rnd.cache[0].capacity, ptr(init_state[0:1]), 0, None, None, 0, ptr(hid_s),
-                      ptr(out_s), None, ws, s())
+                      None, None, ws, s())
 
     vlog = torch.randn(6, cfg.vocab_size, device=out1.device) * 3
     vdr = torch.randint(0, cfg.vocab_size, (5,), dtype=torch.int32, device=out1.device)
@@ -366,14 +368,15 @@ def cpu_baseline(gpu, seconds: float):
     while time.perf_counter() < t_end or len(times) < 2:
         oc.offset = BASE_CTX
         t0 = time.perf_counter()
-        out = fb = root
+        out = core.rmsnorm(root, od.w["norm.weight"], d.cfg.rms_norm_eps)
+        fb = od.feedback(root, out)
         drafts = []
         for k in range(K):
             z = od.logits(out)
             drafts.append(int(od.d2t[core.argmax(z[0])]))
             if k < K - 1:
                 hid, out = od.forward([drafts[-1]], fb, oc)
-                fb = out
+                fb = od.feedback(hid, out)
         oc.offset = BASE_CTX
         a, nxt = osamp.verify_chain_greedy(logits, drafts)
         acc = drafts[:a] + [nxt]

@@ -219,8 +219,9 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
  *   of kv_dtype; positions_dev [rows] (NULL = offset + r); mask_dev
  *   [rows][mask_ld] uint8 over cache slots (NULL = causal, sliding window
  *   when dims->window > 0); n_rows_dev: device row count (rows <= WC_MAX_STEP_ROWS).
- *   Writes hidden_out / out_out [rows][hidden] fp32; when advance_dev is not
- *   NULL, *advance_dev = offset + rows after the last layer.
+ *   Writes hidden_out / out_out [rows][hidden] fp32 (out_out = NULL leaves the
+ *   final RMSNorm to the consumer, e.g. wc_draft_head_norm); when advance_dev
+ *   is not NULL, *advance_dev = offset + rows after the last layer.
  * Replaces Drafter.__call__ (python/woodcock/drafter.py:164-191) and
  * Drafter::forward (src/core/drafter.cpp:91-136). */
 int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w, const int32_t* tokens_dev,
@@ -265,6 +266,20 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
                     const float* rope_sin, int rope_max_pos, float* x, int rows, const int32_t* positions_dev,
                     const uint8_t* mask_dev, int64_t mask_ld, void* k_cache, void* v_cache, int kv_dtype,
                     int capacity, const int32_t* offset_dev, void* workspace, wc_stream_t stream);
+
+/* wc_draft_head for one pre-norm hidden row: the final RMSNorm is applied on the
+ * fly (out = RMSNorm(hidden), drafter.py:190) and, when out_norm is not NULL,
+ * written to out_norm at the same row index (*row_dev + row_add, or 0) -- the
+ * drafter's `out` and, with post_norm, the next step's feedback
+ * (drafter.py:193-194).  Lets wc_drafter_forward skip its final norm
+ * (out_out = NULL) on the chain's critical path.  hidden_size must be a
+ * multiple of 512 when out_norm is given.  Replaces Drafter.norm +
+ * Drafter.logits + mx.argmax + Drafter.token_ids (drafter.py:190,204-215;
+ * spec.py:346). */
+int wc_draft_head_norm(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* hidden_rows,
+                       int64_t hidden_ld, const int32_t* row_dev, int row_add, float* out_norm, int64_t out_ld,
+                       float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
+                       const wc_gumbel* gumbel, void* workspace, wc_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -132,9 +132,16 @@ def test_qwen3_1p7b_draft_step_matches_oracle(cuda, kv_dtype, tol):
         oz = od.logits(oout)
         assert _rel(z, oz) <= tol, step
         tok_dev = d.draft(out).cpu().numpy()
+        # the fused final norm + head from the pre-norm hidden state
+        out_n = torch.full_like(out, float("nan"))
+        z_n = torch.full_like(z := torch.from_numpy(z).to(cuda), float("nan"))
+        tok_n = d.draft_from_hidden(hid, out=out_n, logits=z_n).cpu().numpy()
+        assert _rel(out_n.cpu().numpy(), oout) <= tol, step
+        assert _rel(z_n.cpu().numpy(), oz) <= tol, step
         top2 = np.sort(oz[0])[-2:]
         if top2[1] - top2[0] > 1e-3 * np.abs(oz).max():
             assert int(tok_dev[0]) == int(ids[int(np.argmax(oz[0]))]), step
+            assert int(tok_n[0]) == int(tok_dev[0]), step
         k_gpu = cache[0].keys[0, :, : oc.offset].float().cpu().numpy()
         assert _rel(k_gpu, oc.keys_f32(0)[:, : oc.offset]) <= max(tol, 1e-2 if kv_dtype == torch.bfloat16 else 0)
 

@@ -48,8 +48,7 @@ def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256):
         oc.k[0][:] = c.keys[0].cpu().numpy()
         oc.v[0][:] = c.values[0].cpu().numpy()
     oc.offset = ctx
-    root = torch.randn(1, cfg.hidden_size, generator=g, device=cuda)
-    root = root / root.pow(2).mean().sqrt()
+    root = torch.randn(1, cfg.hidden_size, generator=g, device=cuda)  # the root's pre-norm hidden state
     rnd.set_root(ctx, root)
     target = SyntheticTarget(K, cfg.vocab_size, cfg.target_hidden_size, device=cuda, seed=seed + 1)
     return cfg, d, rnd, od, oc, target, root.cpu().numpy()
@@ -69,7 +68,7 @@ def oracle_round(od, oc, root_out, root_fb, logits, taps):
     acc = drafts[:a] + [nxt]
     g = od.fuse([t[: a + 1] for t in taps])
     hid, out = od.forward(acc, g, oc)
-    return drafts, a, acc, out[-1:], od.feedback(hid[-1:], out[-1:])
+    return drafts, a, acc, out[-1:], od.feedback(hid[-1:], out[-1:]), hid[-1:]
 
 
 def gpu_round(rnd, target, n_agree):
@@ -87,17 +86,18 @@ def _rel(a, b):
 
 def test_rounds_match_oracle_round(cuda):
     cfg, d, rnd, od, oc, target, root = setup(cuda, 1)
-    root_out = root_fb = root
+    root_out = core.rmsnorm(root, od.w["norm.weight"], cfg.rms_norm_eps)
+    root_fb = od.feedback(root, root_out)
     pattern = [2, 0, 4, 1, 3, 2, 4, 0]
     for r, n_agree in enumerate(pattern):
         res = gpu_round(rnd, target, n_agree)
         logits = target.logits.cpu().numpy()
         taps = [t.float().cpu().numpy() for t in target.taps]
-        drafts, a, acc, root_out, root_fb = oracle_round(od, oc, root_out, root_fb, logits, taps)
+        drafts, a, acc, root_out, root_fb, root_hid = oracle_round(od, oc, root_out, root_fb, logits, taps)
         assert rnd.drafts.tolist() == drafts, f"round {r}"
         assert res.n_accepted == a == n_agree, f"round {r}"
         assert res.tokens == acc, f"round {r}"
-        assert _rel(rnd.upd_out[a].cpu().numpy(), root_out[0]) <= 1e-5, f"round {r}"
+        assert _rel(rnd.upd_hid[a].cpu().numpy(), root_hid[0]) <= 1e-5, f"round {r}"
         n = oc.offset
         assert rnd.committed() == n
         k_gpu = rnd.cache[0].keys[0, :, :n].float().cpu().numpy()

@@ -249,6 +249,103 @@ static bool al16(const void* p) { return aligned(p, 16); }
 
 using namespace wc;
 
+namespace wc {
+
+// One row's RMSNorm into y (one block): the general-shape path of the fused
+// final norm + head, for hidden sizes the one-row GEMV does not fuse.
+__global__ __launch_bounds__(256) void k_row_rmsnorm(const float* __restrict__ x, int64_t ld,
+                                                     const int32_t* __restrict__ row_dev, int row_add, int K,
+                                                     const uint16_t* __restrict__ gain, float eps,
+                                                     float* __restrict__ y, int64_t ldy) {
+  __shared__ float red[256 / kWave];
+  const int64_t row = row_dev ? static_cast<int64_t>(*row_dev + row_add) : 0;
+  const float* xr = x + row * ld;
+  float ss = 0.f;
+  for (int k = threadIdx.x; k < K; k += 256) ss = fmaf(xr[k], xr[k], ss);
+  ss = wave_sum_dpp(ss);
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < 256 / kWave; ++i) t += red[i];
+  const float inv = 1.f / sqrtf(t / static_cast<float>(K) + eps);
+  float* yr = y + row * ldy;
+  for (int k = threadIdx.x; k < K; k += 256) yr[k] = xr[k] * bf16_to_float(gain[k]) * inv;
+}
+
+// Draft head over `rows` input rows; with `norm`, the rows are pre-norm hidden
+// states and the final RMSNorm is applied on the fly (its normalised row is
+// written to xn_out when not NULL; one row).
+static int draft_head_impl(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* out_rows,
+                           int64_t out_ld, const int32_t* out_row_dev, int out_row_add, int rows, float* xn_out,
+                           int64_t ld_xn, float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
+                           const wc_gumbel* gumbel, void* workspace, wc_stream_t stream, bool norm) {
+  if (int rc = check_dims(dims)) return rc;
+  WC_REQUIRE(w && w->head && out_rows && token_out && workspace, "wc_draft_head: NULL argument");
+  WC_REQUIRE(xn_out == nullptr || (rows == 1 && ld_xn >= dims->hidden && ld_xn % 4 == 0 && al16(xn_out)),
+             "wc_draft_head_norm: the normalised row needs rows == 1 and a 16-byte aligned output, stride >= hidden");
+  WC_REQUIRE(al16(w->head) && al16(workspace), "wc_draft_head: head weight / workspace must be 16-byte aligned");
+  WC_REQUIRE(rows >= 1, "wc_draft_head: rows must be positive");
+  WC_REQUIRE(out_row_dev == nullptr || rows == 1, "wc_draft_head: a gathered input row needs rows == 1");
+  WC_REQUIRE(out_ld >= dims->hidden && out_ld % 4 == 0 && al16(out_rows),
+             "wc_draft_head: input rows must be 16-byte aligned with a stride >= hidden_size, multiple of 4");
+  WC_REQUIRE(logits_out == nullptr || logits_ld >= dims->head_rows, "wc_draft_head: logits row stride too small");
+  WC_REQUIRE(gumbel == nullptr || (gumbel->round_dev && gumbel->temperature > 0.f),
+             "wc_draft_head: gumbel needs a round counter and a positive temperature");
+  const DrafterWs ws = drafter_ws(*dims, workspace);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  if (norm && xn_out && dims->hidden % 512 != 0) {
+    // the one-row GEMV fuses the norm for hidden % 512 == 0 only: normalise
+    // into xn_out first and run the plain head on it
+    WC_REQUIRE(w->final_norm, "wc_draft_head_norm: final norm weight is NULL");
+    k_row_rmsnorm<<<1, 256, 0, s>>>(out_rows, out_ld, out_row_dev, out_row_add, dims->hidden, u16(w->final_norm),
+                                    dims->eps, xn_out, ld_xn);
+    WC_LAUNCHED();
+    return draft_head_impl(dims, w, xn_out, ld_xn, out_row_dev, out_row_add, 1, nullptr, 0, logits_out, logits_ld,
+                           token_out, row_out, gumbel, workspace, stream, false);
+  }
+  for (int t0 = 0; t0 < rows; t0 += WC_MAX_STEP_ROWS) {
+    const int tr = std::min(WC_MAX_STEP_ROWS, rows - t0);
+    GemvArgs h = gemv_defaults();
+    h.in[0].x = out_rows + (out_row_dev ? 0 : t0 * out_ld);
+    h.in[0].ld = out_ld;
+    h.in[0].dtype = WC_F32;
+    h.in[0].row_idx = out_row_dev;
+    h.in[0].row_add = out_row_dev ? out_row_add : 0;
+    h.in[0].K = dims->hidden;
+    h.in[0].gain = norm ? u16(w->final_norm) : nullptr;
+    h.n_in = 1;
+    h.xn_out = xn_out;
+    h.ld_xn = ld_xn;
+    h.ldw[0] = dims->hidden;
+    h.w[0][0] = u16(w->head);
+    h.N = dims->head_rows;
+    h.seg_start[1] = h.N;
+    h.M = tr;
+    h.eps = dims->eps;
+    h.epi = kEpiArgmax;
+    h.y = logits_out ? logits_out + t0 * logits_ld : nullptr;
+    h.ldy = logits_ld;
+    h.slots = ws.slots;
+    h.counter = ws.head_ctr;
+    h.d2t = w->d2t;
+    h.tok_out = token_out + t0;
+    h.row_out = row_out ? row_out + t0 : nullptr;
+    if (gumbel) {
+      h.use_gumbel = 1;
+      h.gumbel.seed = gumbel->seed;
+      h.gumbel.round_dev = gumbel->round_dev;
+      h.gumbel.purpose = gumbel->purpose + t0;
+      h.gumbel.inv_temperature = 1.f / gumbel->temperature;
+    }
+    if (int rc = launch_gemv(h, dims->head_rows >= 8192 ? 2 : 1, s)) return rc;
+  }
+  return WC_OK;
+}
+
+
+}  // namespace wc
+
 extern "C" {
 
 int wc_rope_table(float* cos_out, float* sin_out, int max_pos, int head_dim, float base) {
@@ -321,14 +418,15 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
                        int32_t* advance_dev, void* workspace, wc_stream_t stream) {
   if (int rc = check_dims(dims)) return rc;
   const wc_drafter_dims& d = *dims;
-  WC_REQUIRE(w && tokens_dev && feat && hidden_out && out_out && workspace && offset_dev && k_cache && v_cache,
+  WC_REQUIRE(w && tokens_dev && feat && hidden_out && workspace && offset_dev && k_cache && v_cache,
              "wc_drafter_forward: NULL argument");
   WC_REQUIRE(al16(workspace), "wc_drafter_forward: workspace must be 16-byte aligned");
   WC_REQUIRE(rows >= 1, "wc_drafter_forward: rows must be positive");
   WC_REQUIRE(kv_dtype == WC_F32 || kv_dtype == WC_BF16, "wc_drafter_forward: kv dtype must be f32 or bf16");
   WC_REQUIRE(feat_ld >= d.hidden && feat_ld % 4 == 0,
              "wc_drafter_forward: feature row stride must be >= hidden_size and a multiple of 4");
-  WC_REQUIRE(al16(feat) && al16(hidden_out) && al16(out_out), "wc_drafter_forward: buffers must be 16-byte aligned");
+  WC_REQUIRE(al16(feat) && al16(hidden_out) && (out_out == nullptr || al16(out_out)),
+             "wc_drafter_forward: buffers must be 16-byte aligned");
   WC_REQUIRE(feat_row_dev == nullptr || rows == 1, "wc_drafter_forward: a gathered feature row needs rows == 1");
   WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
              "wc_drafter_forward: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
@@ -509,12 +607,18 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       dn.ldres = d.hidden;
       dn.y = hidden_out + t0 * d.hidden;
       dn.ldy = d.hidden;
-      if (last_layer) {
+      // the last layer's last-block epilogue: the final RMSNorm (unless the
+      // caller leaves it to the consumer: out_out == NULL) and the offset advance
+      const bool fin = last_layer && out_out != nullptr;
+      const bool adv = last_layer && advance_dev && last_tile;
+      if (fin || adv) {
         dn.fin_counter = ws.fin_ctr;
-        dn.fin_gain = u16(w->final_norm);
-        dn.fin_out = out_out + t0 * d.hidden;
         dn.ld_fin = d.hidden;
-        if (advance_dev && last_tile) {
+        if (fin) {
+          dn.fin_gain = u16(w->final_norm);
+          dn.fin_out = out_out + t0 * d.hidden;
+        }
+        if (adv) {
           dn.adv_dst = advance_dev;
           dn.adv_src = offset_dev;
           dn.adv_add = offset_add + t0;
@@ -530,52 +634,19 @@ int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, cons
                   const int32_t* out_row_dev, int out_row_add, int rows, float* logits_out, int64_t logits_ld,
                   int32_t* token_out, int32_t* row_out, const wc_gumbel* gumbel, void* workspace,
                   wc_stream_t stream) {
-  if (int rc = check_dims(dims)) return rc;
-  WC_REQUIRE(w && w->head && out_rows && token_out && workspace, "wc_draft_head: NULL argument");
-  WC_REQUIRE(al16(w->head) && al16(workspace), "wc_draft_head: head weight / workspace must be 16-byte aligned");
-  WC_REQUIRE(rows >= 1, "wc_draft_head: rows must be positive");
-  WC_REQUIRE(out_row_dev == nullptr || rows == 1, "wc_draft_head: a gathered input row needs rows == 1");
-  WC_REQUIRE(out_ld >= dims->hidden && out_ld % 4 == 0 && al16(out_rows),
-             "wc_draft_head: input rows must be 16-byte aligned with a stride >= hidden_size, multiple of 4");
-  WC_REQUIRE(logits_out == nullptr || logits_ld >= dims->head_rows, "wc_draft_head: logits row stride too small");
-  WC_REQUIRE(gumbel == nullptr || (gumbel->round_dev && gumbel->temperature > 0.f),
-             "wc_draft_head: gumbel needs a round counter and a positive temperature");
-  const DrafterWs ws = drafter_ws(*dims, workspace);
-  auto s = reinterpret_cast<hipStream_t>(stream);
-  for (int t0 = 0; t0 < rows; t0 += WC_MAX_STEP_ROWS) {
-    const int tr = std::min(WC_MAX_STEP_ROWS, rows - t0);
-    GemvArgs h = gemv_defaults();
-    h.in[0].x = out_rows + (out_row_dev ? 0 : t0 * out_ld);
-    h.in[0].ld = out_ld;
-    h.in[0].dtype = WC_F32;
-    h.in[0].row_idx = out_row_dev;
-    h.in[0].row_add = out_row_dev ? out_row_add : 0;
-    h.in[0].K = dims->hidden;
-    h.n_in = 1;
-    h.ldw[0] = dims->hidden;
-    h.w[0][0] = u16(w->head);
-    h.N = dims->head_rows;
-    h.seg_start[1] = h.N;
-    h.M = tr;
-    h.eps = dims->eps;
-    h.epi = kEpiArgmax;
-    h.y = logits_out ? logits_out + t0 * logits_ld : nullptr;
-    h.ldy = logits_ld;
-    h.slots = ws.slots;
-    h.counter = ws.head_ctr;
-    h.d2t = w->d2t;
-    h.tok_out = token_out + t0;
-    h.row_out = row_out ? row_out + t0 : nullptr;
-    if (gumbel) {
-      h.use_gumbel = 1;
-      h.gumbel.seed = gumbel->seed;
-      h.gumbel.round_dev = gumbel->round_dev;
-      h.gumbel.purpose = gumbel->purpose + t0;
-      h.gumbel.inv_temperature = 1.f / gumbel->temperature;
-    }
-    if (int rc = launch_gemv(h, dims->head_rows >= 8192 ? 2 : 1, s)) return rc;
-  }
-  return WC_OK;
+  return wc::draft_head_impl(dims, w, out_rows, out_ld, out_row_dev, out_row_add, rows, nullptr, 0, logits_out,
+                             logits_ld, token_out, row_out, gumbel, workspace, stream, false);
+}
+
+int wc_draft_head_norm(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* hidden_rows,
+                       int64_t hidden_ld, const int32_t* row_dev, int row_add, float* out_norm, int64_t out_ld,
+                       float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
+                       const wc_gumbel* gumbel, void* workspace, wc_stream_t stream) {
+  WC_REQUIRE(dims && w && w->final_norm, "wc_draft_head_norm: final norm missing");
+  WC_REQUIRE(out_norm == nullptr || (out_ld >= dims->hidden && out_ld % 4 == 0 && wc::aligned(out_norm, 16)),
+             "wc_draft_head_norm: out rows must be 16-byte aligned with a stride >= hidden_size, multiple of 4");
+  return wc::draft_head_impl(dims, w, hidden_rows, hidden_ld, row_dev, row_add, 1, out_norm, out_ld, logits_out,
+                             logits_ld, token_out, row_out, gumbel, workspace, stream, true);
 }
 
 }  // extern "C"

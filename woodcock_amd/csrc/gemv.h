@@ -95,6 +95,10 @@ struct GemvArgs {
   const int32_t* adv_src;                  // *adv_dst = *adv_src + adv_add + (m rows) when adv_dst != NULL
   int adv_add;
   int32_t* adv_dst;
+  // one-row kernel: the normalised input segment 0 (x * gain / rms) written to
+  // xn_out at the input's row index by block 0 (the drafter output `out`)
+  float* xn_out;
+  int64_t ld_xn;
 };
 
 __device__ __forceinline__ float dot8(const uint4 w, const float4 a, const float4 b) {
@@ -376,6 +380,18 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
       xr[s][u][1] = x1;
     }
     inv[s] = gain ? 1.f / sqrtf(wave_sum_dpp(ss) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+  }
+  if (a.xn_out && blockIdx.x == 0 && wave == 0 && m > 0) {
+    float* xo = a.xn_out + static_cast<int64_t>(in_row(a.in[0], 0)) * a.ld_xn + lane * 8;
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      if (u >= steps[0]) continue;
+      const float4 x0 = xr[0][u][0], x1 = xr[0][u][1];
+      *reinterpret_cast<float4*>(xo + u * kWave * 8) =
+          make_float4(x0.x * inv[0], x0.y * inv[0], x0.z * inv[0], x0.w * inv[0]);
+      *reinterpret_cast<float4*>(xo + u * kWave * 8 + 4) =
+          make_float4(x1.x * inv[0], x1.y * inv[0], x1.z * inv[0], x1.w * inv[0]);
+    }
   }
   // 5. dot products in weight-issue order
   float acc[R][P];

@@ -242,6 +242,20 @@ class Drafter:
                   None if g is None else C.byref(g), ptr(self.ws), stream_ptr())
         return tok
 
+    def draft_from_hidden(self, hidden: torch.Tensor, out: torch.Tensor | None = None,
+                          logits: torch.Tensor | None = None) -> torch.Tensor:
+        """Final RMSNorm + head + argmax + d2t in one launch chain, for one row of
+        pre-norm hidden state (the drafter output is norm(hidden), python/woodcock/drafter.py:190);
+        the normalised row is written to `out` when given."""
+        h = _as_rows(hidden, self.cfg.hidden_size)
+        if h.dtype != torch.float32 or h.shape[0] != 1:
+            raise ValueError("hidden must be one float32 row")
+        tok = torch.empty(1, dtype=torch.int32, device=self.device)
+        _lib.call("wc_draft_head_norm", C.byref(self.dims), C.byref(self.wstruct), ptr(h), h.stride(0), None, 0,
+                  ptr(out), 0 if out is None else out.stride(0), ptr(logits),
+                  0 if logits is None else logits.stride(0), ptr(tok), None, None, ptr(self.ws), stream_ptr())
+        return tok
+
     @property
     def vocab_ids(self) -> torch.Tensor | None:
         return self._vocab_ids

@@ -3,8 +3,8 @@
 
 Everything between two host reads stays on the device:
 
-    head(root) -> d_1                                   (draft head + argmax + d2t)
-    for k in 1..K-1: drafter layer(d_k, fb) -> head -> d_{k+1}
+    head(RMSNorm(root)) -> d_1                          (final norm + draft head + argmax + d2t)
+    for k in 1..K-1: drafter layer(d_k, fb) -> head(RMSNorm(h)) -> d_{k+1}
     target logits at [x_n, d_1..d_K]                    (supplied by the target; out of scope here)
     fused target argmax + greedy accept -> verdict      (a, accepted tokens + next, keep)
     compact the target KV with keep (identity for a chain: offset only)
@@ -17,8 +17,10 @@ start), the accepted count, the gathered rows -- are read from device memory,
 so the same kernel sequence (or one captured HIP graph) serves every round.
 
 State invariants follow python/woodcock/spec.py:1-15: before a round the
-drafter cache holds real entries 0..n-1 and the root is the drafter output of
-entry n-1 (row n_keep-1 of the previous update).
+drafter cache holds real entries 0..n-1 and the root is the drafter's hidden
+state of entry n-1 (row n_keep-1 of the previous update); its output, the final
+RMSNorm of it, is formed by the head launch that consumes it, so no drafter
+pass of the round runs a norm of its own on the critical path.
 """
 from __future__ import annotations
 
@@ -77,11 +79,11 @@ class ChainRound:
 
     # ------------------------------------------------------------------ state
 
-    def set_root(self, n: int, root_out: torch.Tensor, root_hidden: torch.Tensor | None = None) -> None:
-        """Start state: n committed entries in the drafter cache, the root output
-        (drafter output of entry n-1) and its hidden state."""
-        self.upd_out[0].copy_(root_out.reshape(-1))
-        self.upd_hid[0].copy_((root_out if root_hidden is None else root_hidden).reshape(-1))
+    def set_root(self, n: int, root_hidden: torch.Tensor) -> None:
+        """Start state: n committed entries in the drafter cache and the root --
+        the drafter's pre-norm hidden state of entry n-1 (its output, the final
+        RMSNorm of it, is formed by the first head launch of the round)."""
+        self.upd_hid[0].copy_(root_hidden.reshape(-1))
         self.verdict.zero_()
         self.verdict[_lib.V_N_KEEP] = 1
         self.state.zero_()
@@ -102,21 +104,23 @@ class ChainRound:
         n_keep = ptr(self.verdict[_lib.V_N_KEEP:_lib.V_N_KEEP + 1])
         dm = d.cfg.hidden_size
         cap = self.cache[0].capacity
-        # d_1 from the root = update row n_keep - 1
-        _lib.call("wc_draft_head", dims, W, ptr(self.upd_out), dm, n_keep, -1, 1, None, 0, ptr(self.drafts[0:1]),
-                  None, None, ws, s)
+        # d_1 from the root = update row n_keep - 1; the head applies the final
+        # RMSNorm and leaves the root's output in upd_out (same row)
+        _lib.call("wc_draft_head_norm", dims, W, ptr(self.upd_hid), dm, n_keep, -1, ptr(self.upd_out), dm, None, 0,
+                  ptr(self.drafts[0:1]), None, None, ws, s)
         root_fb = self._fb_rows(self.upd_hid, self.upd_out)
         for k in range(1, self.K):
             if k == 1:
                 feat, frow, fadd = root_fb, n_keep, -1
             else:
                 feat, frow, fadd = self._fb_rows(self.step_hid, self.step_out)[k - 2:k - 1], None, 0
-            # the chain appends at n + k - 1 (contiguous positions, causal, python/woodcock/spec.py:349)
+            # the chain appends at n + k - 1 (contiguous positions, causal, python/woodcock/spec.py:349);
+            # the layer's final RMSNorm is left to the next head (out_out = NULL)
             _lib.call("wc_drafter_forward", dims, W, ptr(self.drafts[k - 1:k]), ptr(feat), dm, frow, fadd, 1, None,
                       self._kp, self._vp, self._kvdt, cap, ptr(self.state[S_N:S_N + 1]), k - 1, None, None, 0,
-                      ptr(self.step_hid[k - 1:k]), ptr(self.step_out[k - 1:k]), None, ws, s)
-            _lib.call("wc_draft_head", dims, W, ptr(self.step_out[k - 1:k]), dm, None, 0, 1, None, 0,
-                      ptr(self.drafts[k:k + 1]), None, None, ws, s)
+                      ptr(self.step_hid[k - 1:k]), None, None, ws, s)
+            _lib.call("wc_draft_head_norm", dims, W, ptr(self.step_hid[k - 1:k]), dm, None, 0,
+                      ptr(self.step_out[k - 1:k]), dm, None, 0, ptr(self.drafts[k:k + 1]), None, None, ws, s)
         # the speculative entries n..n+K-2 are simply overwritten later: the
         # drafter's committed count n is never advanced by the chain (spec.py:351-352)
 
@@ -144,7 +148,7 @@ class ChainRound:
         # appends the accepted entries at n and advances n in place (last kernel of the pass)
         V.call("wc_drafter_forward", dims, W, ptr(self.verdict[V.V_TOKENS:V.V_TOKENS + self.K + 1]), ptr(self.g), dm,
                None, 0, self.K + 1, ptr(n_keep), self._kp, self._vp, self._kvdt, self.cache[0].capacity,
-               ptr(self.state[S_N:S_N + 1]), 0, None, None, 0, ptr(self.upd_hid), ptr(self.upd_out),
+               ptr(self.state[S_N:S_N + 1]), 0, None, None, 0, ptr(self.upd_hid), None,
                ptr(self.state[S_N:S_N + 1]), ws, s)
 
     def enqueue_readback(self) -> None:
