@@ -206,7 +206,7 @@ def bench_gpu(args):
             _lib.call("wc_verify_chain_greedy", ptr(vlog), 6, cfg.vocab_size, vlog.stride(0), ptr(vdr), ptr(vverd),
                       ptr(rnd.vws), s())
 
-    # config 3 compaction: tree-path keeps with a ~ U{0..5} over a 6-slot verify window at 2048
+    # tree-path compaction: keeps with a ~ U{0..5} over a 6-slot verify window at 2048
     rng = np.random.default_rng(args.seed)
     keeps = []
     for _ in range(REP):
@@ -229,7 +229,7 @@ def bench_gpu(args):
             _lib.call("wc_kv_compact", kp_, vp_, len(tc), 8, tc[0].capacity, 256, ptr(karr[i, 1:2]),
                       ptr(karr[i, 2:8]), ptr(karr[i, 0:1]), 6, ptr(koff[i:i + 1]), None, s())
 
-    # config 2: stochastic accept/reject at k=5 -- target softmax [6,151936], draft softmax
+    # stochastic accept/reject at k=5 -- target softmax [6,151936], draft softmax
     # [5,16384] and the rule over device probabilities
     from woodcock_amd.synthetic import draw_rows, stochastic_workload
 
@@ -258,7 +258,7 @@ def bench_gpu(args):
             _lib.call("wc_verify_chain_stochastic", ptr(s_p), 6, s_p.shape[1], s_p.stride(0), ptr(s_q), 16384,
                       s_q.stride(0), ptr(s_d2), ptr(s_dr), None, C.byref(s_u), ptr(s_verd), sws, s())
 
-    # config 5: one Qwen3-1.7B target layer over a 60-node draft tree (depth <= 6) at context
+    # one Qwen3-1.7B target layer over a 60-node draft tree (depth <= 6) at context
     # 2048 with the tree mask, then the greedy tree verify over [60, 151936] logits
     from woodcock_amd.cache import KVCache
     from woodcock_amd.sampling import tree_attention_mask, DraftTree
@@ -339,6 +339,135 @@ def bench_gpu(args):
     }
 
 
+# ---------------------------------------------------------------- HBM traffic
+# The head GEMV's HBM bytes per launch come from two rocprofv3 counter passes
+# over `bench.py --pmc-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch),
+# each scaled by what the same counter reads for a plain copy kernel of known
+# size run in the same process.  `bench.py --pmc-summary FETCH_DIR WRITE_DIR`
+# turns the two counter CSVs into the committed summary that later runs read.
+HEAD_KERNEL = "k_gemv1<4, false, 1, 4, 0>"
+PROBE_HEADS = 16
+PROBE_COPIES = 4
+PROBE_COPY_FLOATS = 64 << 20  # 256 MiB read + 256 MiB written per copy
+TRAFFIC_SUMMARY = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "draft_head_gemv_16384x2048_hbm_traffic.md")
+
+
+def pmc_probe(seed=0):
+    """Launch only what the counter passes read: PROBE_HEADS head launches of the
+    benchmark workload, then PROBE_COPIES copies (torch.neg, fp32) of known size."""
+    import ctypes as C
+
+    import torch
+
+    from woodcock_amd import _lib
+    from woodcock_amd.runtime import ptr, stream_ptr
+
+    cfg, d, ids, rnd, target, init_state, root = build_workload(seed)
+    dims, W, ws = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws)
+    dm = cfg.hidden_size
+    x = torch.randn(PROBE_COPY_FLOATS, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(PROBE_HEADS):
+        _lib.call("wc_draft_head_norm", dims, W, ptr(rnd.upd_hid[0:1]), dm, None, 0, ptr(rnd.upd_out[0:1]), dm,
+                  None, 0, ptr(rnd.drafts[0:1]), None, None, ws, stream_ptr())
+    torch.cuda.synchronize()
+    for _ in range(PROBE_COPIES):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(f"pmc probe: {PROBE_HEADS} head launches, {PROBE_COPIES} copies of {4 * PROBE_COPY_FLOATS} bytes",
+          flush=True)
+
+
+def _counter_rows(d):
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {d}")
+    with open(files[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _per_dispatch(rows, counter):
+    """{dispatch id: (kernel name, value)} for one counter (summed over its instances)."""
+    out = {}
+    for r in rows:
+        if r["Counter_Name"] != counter:
+            continue
+        did = int(r["Dispatch_Id"])
+        name, v = out.get(did, (r["Kernel_Name"], 0.0))
+        out[did] = (name, v + float(r["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_dir, write_dir):
+    """Markdown summary of the two counter passes (printed; commit it under profiles/)."""
+    copy_bytes = 4 * PROBE_COPY_FLOATS
+    res = {}
+    for counter, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        disp = _per_dispatch(_counter_rows(d), counter)
+        order = sorted(disp)
+        head = [disp[i][1] for i in order if HEAD_KERNEL in disp[i][0]]
+        copies = [disp[i] for i in order[-PROBE_COPIES:]]
+        if len(head) != PROBE_HEADS or any("neg" not in n for n, _ in copies):
+            raise SystemExit(f"{counter}: expected {PROBE_HEADS} head dispatches and {PROBE_COPIES} trailing neg "
+                             f"copies, got {len(head)} / {[n[:60] for n, _ in copies]}")
+        copy_kib = float(np.mean([v for _, v in copies]))
+        factor = copy_bytes / (copy_kib * 1024.0)
+        res[counter] = (float(np.mean(head)), copy_kib, factor)
+    fetch = res["FETCH_SIZE"][0] * 1024.0 * res["FETCH_SIZE"][2]
+    write = res["WRITE_SIZE"][0] * 1024.0 * res["WRITE_SIZE"][2]
+    algo = 16384 * 2048 * 2 + 2048 * 4 + 2048 * 2
+    lines = [
+        "# Draft head GEMV + argmax (16384 x 2048 bf16): HBM traffic per launch",
+        "",
+        "Commands (from the repository root on the GPU host):",
+        "",
+        "```",
+        "cd /tmp && export TMPDIR=/tmp",
+        "timeout -s KILL 90 rocprofv3 --pmc FETCH_SIZE --output-format csv -d $R/gpurun_out/pmc_fetch -o pmc "
+        "-- python3 $R/bench.py --pmc-probe",
+        "timeout -s KILL 90 rocprofv3 --pmc WRITE_SIZE --output-format csv -d $R/gpurun_out/pmc_write -o pmc "
+        "-- python3 $R/bench.py --pmc-probe",
+        "python3 bench.py --pmc-summary gpurun_out/pmc_fetch gpurun_out/pmc_write",
+        "```",
+        "",
+        f"Probe: {PROBE_HEADS} launches of `{HEAD_KERNEL}` (the draft head with the fused final norm), then "
+        f"{PROBE_COPIES} launches of torch.neg over {copy_bytes >> 20} MiB fp32 (reads and writes {copy_bytes} "
+        "bytes each) as the calibration copy.",
+        "",
+        "| counter | head, KiB/dispatch (mean) | copy, KiB/dispatch (mean) | scale (copy bytes / counter bytes) "
+        "| head bytes/launch |",
+        "|---|---|---|---|---|",
+        f"| FETCH_SIZE | {res['FETCH_SIZE'][0]:.1f} | {res['FETCH_SIZE'][1]:.1f} | {res['FETCH_SIZE'][2]:.4f} "
+        f"| {fetch:.0f} |",
+        f"| WRITE_SIZE | {res['WRITE_SIZE'][0]:.1f} | {res['WRITE_SIZE'][1]:.1f} | {res['WRITE_SIZE'][2]:.4f} "
+        f"| {write:.0f} |",
+        "",
+        f"Algorithmic bytes per launch: {algo} (head weights 16384 x 2048 bf16, the fp32 input row, the final-norm "
+        f"gain); measured / algorithmic = {(fetch + write) / algo:.4f}.",
+        "",
+        f"traffic_bytes_per_launch: {fetch + write:.0f}",
+        "",
+    ]
+    print("\n".join(lines))
+
+
+def head_traffic():
+    """HBM bytes per head launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def cpu_baseline(gpu, seconds: float):
     """The oracle (C restatement, OpenMP over output rows) running the same round
     on the host's cores: K heads, K-1 layers, verify, update (fuse + M=3 layer).
@@ -399,7 +528,13 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the launches the counter passes read")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 counter passes over --pmc-probe (no GPU needed)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the round is a batch-1, single-device path "
               "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
@@ -409,6 +544,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_probe:
+        pmc_probe(args.seed)
+        return
     r = bench_gpu(args)
     head_gbs = r["head_bytes"] / (r["head_us"] * 1e-6) / 1e9
     step_gbs = r["step_bytes"] / (r["draft_step_us"] * 1e-6) / 1e9
@@ -438,11 +576,11 @@ def main():
             "draft_step_us": round(r["draft_step_us"], 2),
             "draft_step_hbm_frac": round(step_gbs / PEAK_HBM_GBS, 4),
             "verify_accept_us_k5": round(r["verify_accept_us"], 2),
-            "kv_compact_us_config3": round(r["kv_compact_us"], 2),
-            "verify_stochastic_us_config2_k5": round(r["stochastic_us"], 2),
-            "target_layer_us_config5_m60_ctx2048": round(r["target_layer_us"], 2),
-            "target_layer_hbm_frac_config5": round(100_663_296 / (r["target_layer_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-            "verify_tree_greedy_us_config5_n60": round(r["tree_verify_us"], 2),
+            "kv_compact_us_28l_ctx2048_window6": round(r["kv_compact_us"], 2),
+            "verify_stochastic_us_k5_vocab151936": round(r["stochastic_us"], 2),
+            "target_layer_us_qwen3_1p7b_m60_ctx2048": round(r["target_layer_us"], 2),
+            "target_layer_hbm_frac_m60": round(100_663_296 / (r["target_layer_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "verify_tree_greedy_us_n60": round(r["tree_verify_us"], 2),
             "head_gemv_us": round(r["head_us"], 2),
         },
         "roofline": {
@@ -452,7 +590,7 @@ def main():
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(head_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": head_traffic(),
         },
         "cpu_baseline": cpu,
     }

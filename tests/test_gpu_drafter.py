@@ -114,7 +114,7 @@ def _rel(a, b):
 
 @pytest.mark.parametrize("kv_dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-4)])
 def test_qwen3_1p7b_draft_step_matches_oracle(cuda, kv_dtype, tol):
-    """Config 1 drafter step at full shape: one layer at ctx 512 + the 16k head,
+    """Qwen3-1.7B drafter step at full shape: one layer at ctx 512 + the 16k head,
     GPU vs the oracle over identical bf16 weights and cache contents."""
     from woodcock_amd.config import qwen3_1p7b_drafter
 

@@ -53,8 +53,8 @@ def test_known_answer(cuda):
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float32, 128), (torch.bfloat16, 64),
                                      (torch.float32, 6)])
-def test_config3_rounds(cuda, dtype, D):
-    """Config 3: 28 layers x 8 kv heads, context 2048 + a verify window of 6; 1000
+def test_28_layer_tree_rounds(cuda, dtype, D):
+    """28 layers x 8 kv heads, context 2048 + a verify window of 6; 1000
     seeded rounds with a ~ U{0..5}; chain prefixes (identity: nothing moves) and
     tree paths (strictly increasing keep).  The verify window of every layer/head
     is compared byte for byte with the oracle; rows outside it must not change."""

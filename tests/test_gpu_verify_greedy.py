@@ -29,8 +29,8 @@ def planted_chain_logits(rng, K, V, n_match, scale=3.0):
     return lg, drafts
 
 
-def test_config1_chain_round(cuda):
-    """Config 1 verify: [5, 151936] fp32 ~N(0, 3^2), argmax planted for the first 2 positions."""
+def test_chain_round_k4_full_vocab(cuda):
+    """Chain verify at K=4: [5, 151936] fp32 ~N(0, 3^2), argmax planted for the first 2 positions."""
     from woodcock_amd import sampling as S
 
     rng = np.random.default_rng(1)
@@ -146,7 +146,7 @@ def test_tree_known_answer(cuda):
     assert S.verify_tree_greedy(torch.from_numpy(lg).to(cuda), tree) == ([2, 3], 3)
 
 
-def test_config5_shape_tree(cuda):
+def test_sixty_node_tree_full_vocab(cuda):
     """60-node tree, depth 6 / branching 4, over the full vocabulary; duplicate
     sibling tokens resolve to the first child in draw order."""
     from woodcock_amd import sampling as S
