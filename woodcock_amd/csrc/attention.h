@@ -35,7 +35,8 @@ struct AttnArgs {
   const uint8_t* mask;  // [rows][mask_ld] or NULL
   int64_t mask_ld;
   int window;
-  float* partial;  // [Hk][S][kMaxQV][D+2]
+  float* partial;  // [Hk][S][qv_ld][D+2]
+  int qv_ld;       // query vectors per (kv head, split) in `partial` (>= rows x group)
   float* out;  // [rows][H*D]
   int64_t ld_out;
 };
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   }
 
   // this split's (m, l, o); an empty range leaves m = -inf, l = 0
-  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * kMaxQV * (D + 2);
+  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * a.qv_ld * (D + 2);
 #pragma unroll
   for (int e = 0; e < ACC; ++e) {
     const int idx = threadIdx.x + e * kAttnThreads;
@@ -427,299 +428,6 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   if (threadIdx.x < QV) {
     part[threadIdx.x * (D + 2)] = s_m[threadIdx.x];
     part[threadIdx.x * (D + 2) + 1] = s_l[threadIdx.x];
-  }
-}
-
-// ------------------------------------------------------------------ MFMA attention (verify width)
-
-typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
-typedef float af32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
-}
-
-// 8 fp32 -> bf16 hi (round to nearest) and lo (the rounding remainder, rounded):
-// hi + lo equals x to ~2^-17 relative, so bf16 MFMA products keep fp32 accuracy.
-__device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo) {
-  float r[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = x[e] - static_cast<float>(static_cast<__bf16>(x[e]));
-  const uint4 h = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]),
-                             pack2_bf16(x[6], x[7]));
-  const uint4 l = make_uint4(pack2_bf16(r[0], r[1]), pack2_bf16(r[2], r[3]), pack2_bf16(r[4], r[5]),
-                             pack2_bf16(r[6], r[7]));
-  hi = __builtin_bit_cast(abf16x8, h);
-  lo = __builtin_bit_cast(abf16x8, l);
-}
-
-constexpr int kMfD = 128;                 // head_dim of the MFMA path
-constexpr int kMfCH = 32;                 // keys per chunk
-constexpr int kMfLdT = kMfCH + 8;         // row stride (bf16) of the transposed V chunk
-constexpr int kMfLdP = kMfCH + 4;         // row stride (fp32) of a wave's P tile
-
-// Same contract as k_attention for head_dim 128 and a bf16 cache, for blocks
-// of 16..64 query vectors: wave w owns query vectors 16w .. 16w+15.  Per chunk
-// of 32 keys: S = Q K^T by v_mfma_f32_16x16x32_bf16 (Q as bf16 hi + lo, K exact
-// in bf16), an online softmax in registers (a row's 16 lanes reduce by
-// shuffles), P through the wave's LDS tile into the A layout (hi + lo), and
-// O += P V against the chunk's transposed V.
-template <typename KT>
-__global__ __launch_bounds__(kAttnThreads) void k_attention_mfma(AttnArgs a) {
-  static_assert(sizeof(KT) == 2, "bf16 cache");
-  constexpr int D = kMfD, CH = kMfCH;
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
-  const int rep = a.H / a.Hk;
-  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
-  const int offset = *a.offset_dev + a.offset_add;
-  const int T = min(offset + nr, a.cap);
-  const int QV = nr * rep, QVb = a.rows * rep;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave), lane = threadIdx.x % kWave;
-  constexpr int nw = kAttnThreads / kWave;
-
-  float* qs = lds;                                   // [QVb][D] fp32
-  float* nk = qs + QVb * D;                          // [rows][D] appended keys (cache-rounded)
-  float* nv = nk + a.rows * D;                       // [rows][D]
-  float* pb = nv + a.rows * D;                       // [4 waves][16][kMfLdP] fp32
-  uint16_t* ksb = reinterpret_cast<uint16_t*>(pb + nw * 16 * kMfLdP);  // [CH][D] bf16
-  uint16_t* vst = ksb + CH * D;                      // [D][kMfLdT] bf16 (transposed)
-  __shared__ uint8_t s_mask[kMaxQV * kAttnChunkMax];
-
-  KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
-  KT* vc = static_cast<KT*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
-  const int per = (T + S - 1) / S;
-  const int kb = min(T, split * per), ke = min(T, kb + per);
-
-  // ---- prologue (as k_attention): q vectors normalised + rotated into LDS,
-  //      appended rows of this block's range normalised/rotated, cached, kept in LDS
-  const int v0 = wave, l0 = nw - 1 - wave;
-  HeadVec<D> qv0, kv0;
-  {
-    const int v = min(v0, QVb - 1), l = v / rep, h = kh * rep + v % rep;
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, qv0);
-  }
-  const bool app0 = l0 < nr && offset + l0 >= kb && offset + l0 < ke;
-  constexpr int VPL = (D + kWave - 1) / kWave;
-  float vv0[VPL];
-  {
-    const int l = min(l0, a.rows - 1);
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, kv0);
-    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
-#pragma unroll
-    for (int e = 0; e < VPL; ++e) vv0[e] = vsrc[min(lane + e * kWave, D - 1)];
-  }
-  KvChunk<D, KT> ch;
-  kv_chunk_load<D, KT>(kc, vc, a.cap, kb, ch);
-  auto row_pos = [&](int l) {
-    const int pos = a.positions ? a.positions[l] : offset + l;
-    return min(max(pos, 0), a.rope_max - 1);
-  };
-  auto put_q = [&](int v, HeadVec<D>& r) {
-    head_vec_norm_rope<D>(r, a.eps);
-#pragma unroll
-    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
-      const int p = lane + e * kWave;
-      if (p < D / 2) {
-        qs[v * D + p] = r.lo[e];
-        qs[v * D + p + D / 2] = r.hi[e];
-      }
-    }
-  };
-  auto put_kv = [&](int l, HeadVec<D>& r, const float* vv) {
-    const int t = offset + l;
-    head_vec_norm_rope<D>(r, a.eps);
-#pragma unroll
-    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
-      const int p = lane + e * kWave;
-      if (p < D / 2) {
-        nk[l * D + p] = kv_store<KT>(kc, static_cast<int64_t>(t) * D + p, r.lo[e]);
-        nk[l * D + p + D / 2] = kv_store<KT>(kc, static_cast<int64_t>(t) * D + p + D / 2, r.hi[e]);
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < VPL; ++e) {
-      const int i = lane + e * kWave;
-      if (i < D) nv[l * D + i] = kv_store<KT>(vc, static_cast<int64_t>(t) * D + i, vv[e]);
-    }
-  };
-  head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(min(v0, QVb - 1) / rep), qv0);
-  head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(min(l0, a.rows - 1)), kv0);
-  if (v0 < QV) put_q(v0, qv0);
-  if (app0) put_kv(l0, kv0, vv0);
-  for (int v = v0 + nw; v < QV; v += nw) {
-    HeadVec<D> r;
-    const int l = v / rep, h = kh * rep + v % rep;
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, r);
-    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
-    put_q(v, r);
-  }
-  for (int l = l0 + nw; l < nr; l += nw) {
-    if (offset + l < kb || offset + l >= ke) continue;
-    HeadVec<D> r;
-    float vv[VPL];
-    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, r);
-    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
-#pragma unroll
-    for (int e = 0; e < VPL; ++e) vv[e] = vsrc[min(lane + e * kWave, D - 1)];
-    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
-    put_kv(l, r, vv);
-  }
-  __syncthreads();
-
-  // ---- this wave's Q tile as MFMA A fragments: row lane%16, d = 32 s + 8 (lane/16) ..
-  const int qrow = wave * 16 + lane % 16;
-  abf16x8 qh[4], ql[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    float x[8];
-    const int d0 = st * 32 + (lane / 16) * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = qrow < QV ? qs[qrow * D + d0 + e] : 0.f;
-    split8(x, qh[st], ql[st]);
-  }
-  // softmax state of the lane's rows 16w + 4 (lane/16) + e
-  float m_r[4], l_r[4];
-  af32x4 o[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    m_r[e] = -INFINITY;
-    l_r[e] = 0.f;
-  }
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = af32x4{0.f, 0.f, 0.f, 0.f};
-  const bool tile_live = wave * 16 < QV;
-  float* pw = pb + wave * 16 * kMfLdP;
-
-  for (int c0 = kb; c0 < ke; c0 += CH) {
-    const int n = min(CH, ke - c0);
-    // chunk -> LDS: K as [key][d] bf16, V transposed [d][key]; keys past n zeroed
-    {
-      using C = KvChunk<D, KT>;
-#pragma unroll
-      for (int i = 0; i < C::kNL; ++i) {
-        const int el = (threadIdx.x + i * kAttnThreads) * 8;
-        const int j = el / D, d0 = el % D;
-        uint4 kq, vq;
-        if (j >= n) {
-          kq = vq = make_uint4(0, 0, 0, 0);
-        } else if (c0 + j < offset) {
-          kq = ch.k[i];
-          vq = ch.v[i];
-        } else {
-          const float* kr = nk + (c0 + j - offset) * D + d0;
-          const float* vr = nv + (c0 + j - offset) * D + d0;
-          kq = make_uint4(pack2_bf16(kr[0], kr[1]), pack2_bf16(kr[2], kr[3]), pack2_bf16(kr[4], kr[5]),
-                          pack2_bf16(kr[6], kr[7]));
-          vq = make_uint4(pack2_bf16(vr[0], vr[1]), pack2_bf16(vr[2], vr[3]), pack2_bf16(vr[4], vr[5]),
-                          pack2_bf16(vr[6], vr[7]));
-        }
-        *reinterpret_cast<uint4*>(ksb + j * D + d0) = kq;
-        const uint32_t vw[4] = {vq.x, vq.y, vq.z, vq.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vst[(d0 + 2 * e) * kMfLdT + j] = static_cast<uint16_t>(vw[e] & 0xffffu);
-          vst[(d0 + 2 * e + 1) * kMfLdT + j] = static_cast<uint16_t>(vw[e] >> 16);
-        }
-      }
-    }
-    if (a.mask) {
-      for (int e = threadIdx.x; e < nr * n; e += kAttnThreads) {
-        const int l = e / n, j = e - l * n;
-        s_mask[l * CH + j] = a.mask[static_cast<int64_t>(l) * a.mask_ld + c0 + j];
-      }
-    }
-    __syncthreads();
-    if (c0 + CH < ke) kv_chunk_load<D, KT>(kc, vc, a.cap, c0 + CH, ch);  // next chunk in flight
-
-    if (tile_live) {
-      // S = Q K^T for the 2 key tiles of the chunk
-      af32x4 sacc[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        sacc[kt] = af32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const abf16x8 b = __builtin_bit_cast(
-              abf16x8, *reinterpret_cast<const uint4*>(ksb + (kt * 16 + lane % 16) * D + st * 32 + (lane / 16) * 8));
-          sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[st], b, sacc[kt], 0, 0, 0);
-          sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[st], b, sacc[kt], 0, 0, 0);
-        }
-      }
-      // lane holds key kt*16 + lane%16 of rows 4 (lane/16) + e
-      float p[2][4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int v = wave * 16 + (lane / 16) * 4 + e;
-        const int l = min(v, QVb - 1) / rep;
-        float sv[2];
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int j = kt * 16 + lane % 16, t = c0 + j;
-          bool vis = j < n && v < QV;
-          if (vis) {
-            if (a.mask)
-              vis = s_mask[l * CH + j] != 0;
-            else
-              vis = t <= offset + l && (a.window <= 0 || t > offset + l - a.window);
-          }
-          sv[kt] = vis ? a.scale * sacc[kt][e] : -INFINITY;
-        }
-        float mx = fmaxf(sv[0], sv[1]);
-#pragma unroll
-        for (int msk = 1; msk < 16; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk));
-        const float m_new = fmaxf(m_r[e], mx);
-        float alpha = 1.f;
-        if (m_new != -INFINITY) alpha = m_r[e] == -INFINITY ? 0.f : expf(m_r[e] - m_new);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-          p[kt][e] = (m_new == -INFINITY || sv[kt] == -INFINITY) ? 0.f : expf(sv[kt] - m_new);
-        float rs = p[0][e] + p[1][e];
-#pragma unroll
-        for (int msk = 1; msk < 16; msk <<= 1) rs += __shfl_xor(rs, msk);
-        l_r[e] = l_r[e] * alpha + rs;
-        m_r[e] = m_new;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt][e] *= alpha;
-      }
-      // P through the wave's LDS tile into the A layout (row lane%16, keys 8 (lane/16) ..)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pw[((lane / 16) * 4 + e) * kMfLdP + kt * 16 + lane % 16] = p[kt][e];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-      float px[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) px[e] = pw[(lane % 16) * kMfLdP + (lane / 16) * 8 + e];
-      abf16x8 ph, pl;
-      split8(px, ph, pl);
-      // O += P V over the 8 d tiles
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const abf16x8 b = __builtin_bit_cast(
-            abf16x8, *reinterpret_cast<const uint4*>(vst + (dt * 16 + lane % 16) * kMfLdT + (lane / 16) * 8));
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, b, o[dt], 0, 0, 0);
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, b, o[dt], 0, 0, 0);
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- this split's (m, l, o) per query vector
-  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * kMaxQV * (D + 2);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int v = wave * 16 + (lane / 16) * 4 + e;
-    if (v >= QV) continue;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) part[v * (D + 2) + 2 + dt * 16 + lane % 16] = o[dt][e];
-    if (lane % 16 == 0) {
-      part[v * (D + 2)] = m_r[e];
-      part[v * (D + 2) + 1] = l_r[e];
-    }
   }
 }
 
@@ -738,8 +446,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) 
   const int v = blockIdx.x, kh = blockIdx.y;
   const int rep = a.H / a.Hk;
   const int t = threadIdx.x;
-  const float* base = a.partial + static_cast<int64_t>(kh) * S * kMaxQV * (D + 2) + v * (D + 2);
-  constexpr int64_t kSplitStride = static_cast<int64_t>(kMaxQV) * (D + 2);
+  const float* base = a.partial + static_cast<int64_t>(kh) * S * a.qv_ld * (D + 2) + v * (D + 2);
+  const int64_t kSplitStride = static_cast<int64_t>(a.qv_ld) * (D + 2);
   const int i = min(t, D - 1);
   float o[kMaxSplits];
 #pragma unroll
@@ -773,25 +481,6 @@ template <int D, typename KT>
 static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream) {
   constexpr int CH = attn_chunk<D>();
   const size_t qvb = static_cast<size_t>(a.rows) * (a.H / a.Hk);
-  if constexpr (D == kMfD && sizeof(KT) == 2) {
-    if (qvb >= 16) {  // verify-width blocks: the MFMA kernel
-      const size_t lds = sizeof(float) * (qvb * D + 2 * static_cast<size_t>(a.rows) * D +
-                                          static_cast<size_t>(kAttnThreads / kWave) * 16 * kMfLdP) +
-                         2 * (static_cast<size_t>(kMfCH) * D + static_cast<size_t>(D) * kMfLdT);
-      static size_t mf_attr = 64 * 1024;
-      if (lds > mf_attr) {
-        WC_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attention_mfma<KT>),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
-        mf_attr = lds;
-      }
-      hipLaunchKernelGGL(k_attention_mfma<KT>, dim3(splits, a.Hk), dim3(kAttnThreads), lds, stream, a);
-      WC_LAUNCHED();
-      hipLaunchKernelGGL((k_attn_merge<D>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, stream,
-                         a, splits);
-      WC_LAUNCHED();
-      return WC_OK;
-    }
-  }
   const size_t lds = sizeof(float) * (qvb * D + 2 * CH * D + qvb * CH + 2 * static_cast<size_t>(a.rows) * D);
   static size_t attr_bytes = 64 * 1024;  // default dynamic-LDS limit
   if (lds > attr_bytes) {

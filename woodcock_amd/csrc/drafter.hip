@@ -541,6 +541,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       at.mask_ld = mask_ld;
       at.window = d.window;
       at.partial = ws.partial;
+      at.qv_ld = kMaxQV;
       at.out = ws.attn;
       at.ld_out = H * D;
       if (int rc = launch_attention(at, D, kv_dtype, splits, s)) return rc;

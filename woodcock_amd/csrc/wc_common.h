@@ -82,6 +82,23 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Reductions over the 16 lanes of a DPP row (lanes 16r .. 16r + 15); every
+// lane of the row receives the result.
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_move<0x124>(v));  // row_ror:4
+  v = fmaxf(v, dpp_move<0x128>(v));  // row_ror:8
+  return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_move<0xB1>(v);
+  v += dpp_move<0x4E>(v);
+  v += dpp_move<0x124>(v);
+  v += dpp_move<0x128>(v);
+  return v;
+}
+
 // Workgroup barrier that orders LDS only: global loads in flight stay in flight
 // (the plain __syncthreads() fence would wait for every outstanding load).
 __device__ __forceinline__ void lds_barrier() {
