@@ -132,6 +132,51 @@ int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p
                                const int32_t* draft_rows_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
                                void* workspace, wc_stream_t stream);
 
+/* Stochastic tree verification, fp64 decisions: N = rows flattened nodes (node 0
+ * the root, parents[0] = -1, 0 <= parents[i] < i, children in ascending node
+ * order = draw order), p [N][ld_p] the target probabilities at every node,
+ * q [N][ld_q] the draft distribution each node's children were drawn from
+ * without replacement, over the head rows (rows of leaves unused), d2t_dev as
+ * above.  At each node the children are tested in draw order: q(x) <= 0
+ * rejects without a uniform, else u < min(1, p(x)/q(x)) accepts and the walk
+ * descends; a rejection sets p <- norm(max(p - q, 0)) (p / sum p when that mass
+ * is <= 1e-12), zeroes q(x) and renormalises q, stopping when q has no mass
+ * left; the next token is drawn from the current p where the walk stops.
+ * Writes the accepted path (keep = [0] + path), tokens, next and n_uniforms;
+ * status = WC_E_INVALID for an invalid tree, token or d2t.  Replaces
+ * verify_tree_stochastic (python/woodcock/sampling.py:143-193;
+ * src/sampling/sampling.cpp:116-141) as the engine calls it
+ * (python/woodcock/spec.py:316-324). */
+int wc_verify_tree_stochastic(const float* p, int rows, int vocab, int64_t ld_p, const float* q, int head_rows,
+                              int64_t ld_q, const int32_t* d2t_dev, const int32_t* tree_tokens_dev,
+                              const int32_t* tree_parents_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
+                              void* workspace, wc_stream_t stream);
+
+/* ------------------------------------------------------------------ tree helpers */
+
+/* Attention mask of a verify block holding a flattened draft tree: mask_out
+ * [n][ld] (ld >= prefix + n) gets 1 for the prefix columns [0, prefix) and for
+ * prefix + u when u is an ancestor of the row's node or the node itself, 0
+ * elsewhere; parents_dev [n] with parents[0] = -1 and parents[i] < i (the walk
+ * stops at a parent that breaks this).  Replaces tree_attention_mask
+ * (python/woodcock/sampling.py:118-128; src/sampling/sampling.cpp:85-93). */
+int wc_tree_mask(const int32_t* parents_dev, int n, int prefix, uint8_t* mask_out, int64_t ld, wc_stream_t stream);
+
+/* Gumbel-top-k draws without replacement from each of `rows` draft
+ * distributions q [rows][ld_q] over the head rows (renormalised in fp64; d2t_dev
+ * maps head rows to token ids, NULL = identity): every nonzero entry, in
+ * vocabulary order, consumes one uniform u of the stream (row r after the
+ * uniforms of rows < r, the first at index uniform_base) and gets the key
+ * log q(x) - log(-log u); tokens_out [rows][k_max] receives the min(k_r, nonzero
+ * count) largest keys' tokens in descending key order, counts_out [rows] (may be
+ * NULL) their number; k_dev [rows] per-row draw counts (NULL = k_max),
+ * k_max <= 16.  Replaces sample_without_replacement
+ * (python/woodcock/sampling.py:196-203) as tree drafting calls it per frontier
+ * node (python/woodcock/spec.py:238-249). */
+int wc_sample_without_replacement(const float* q, int rows, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
+                                  const int32_t* k_dev, int k_max, const wc_uniforms* rng, int64_t uniform_base,
+                                  int32_t* tokens_out, int32_t* counts_out, wc_stream_t stream);
+
 /* ------------------------------------------------------------------ KV compaction */
 
 /* In-place gather of the accepted entries of the last verify block, in every

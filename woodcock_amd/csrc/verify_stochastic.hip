@@ -291,6 +291,348 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ stochastic tree
+
+// wc_verify_tree_stochastic: recursive rejection down a draft tree whose
+// children were drawn without replacement (python/woodcock/sampling.py:143-177;
+// src/sampling/sampling.cpp:116-141).  At node v with children c_1, c_2, ...
+// (ascending node index = draw order): x = token(c); q(x) <= 0 rejects without
+// a uniform, else u < min(1, p(x) / q(x)) accepts and the walk moves to c; a
+// rejection replaces p by norm(max(p - q, 0)) (p / sum p when that mass is
+// <= 1e-12, sampling.py:182-187), zeroes q(x) and renormalises q by its new
+// mass s, stopping when s <= 0.  With no child accepted (or at a leaf) the next
+// token is drawn from the current p (sampling.py:190-193).
+//
+// After j rejections at v every entry is a fixed map of its own (p_i, q_i):
+//   p <- mode_k ? max(p - q, 0) / div_k : p / div_k,   q <- (i == x_k) ? 0 : q / s_k
+// for k = 1..j, so only the normalisers (div_k, s_k) need vocabulary-wide sums.
+// q is zero outside the head rows, so each rejection's sums run over the head
+// rows and the entries outside them contribute (sum of their p) / prod div_k.
+// One block walks the tree (k_tree_walk); a grid over the vocabulary then sums
+// the final distribution chunk by chunk and the last block locates the draw
+// (k_tree_sample).
+
+struct TreeState {
+  double q_mass;  // Q of the final node: the sum of its draft probabilities
+  int node, nsteps, n_uniforms, path_len, bad, pad[3];
+  int path[WC_MAX_NODES];
+  int x[WC_MAX_NODES];
+  int mode[WC_MAX_NODES];
+  double div[WC_MAX_NODES];
+  double s[WC_MAX_NODES];
+};
+static_assert(sizeof(TreeState) <= kTreeStateBytes, "tree state exceeds its workspace slot");
+
+struct TreeArgs {
+  const float* p;  // [rows][ld_p] target probabilities per node
+  int rows, vocab;
+  int64_t ld_p;
+  const float* q;  // [rows][ld_q] draft probabilities of each node's children, over the head rows
+  int head_rows;
+  int64_t ld_q;
+  const int32_t* d2t;  // [head_rows] ascending target ids, or NULL = identity
+  const int32_t* tokens;
+  const int32_t* parents;
+  unsigned long long seed;
+  const int32_t* round_dev;
+  int purpose;
+  TreeState* st;
+  double* chunk_data;  // [kMaxVocabChunks]
+  unsigned int* counter;
+  wc_verdict* verdict;
+};
+
+constexpr int kTwThreads = 1024;
+
+// The map of j rejections applied to one entry (token id tok): returns p, sets q.
+__device__ __forceinline__ double tree_chain(double p, double q, int tok, int j, const int* xs, const int* mode,
+                                             const double* div, const double* sv, double& q_out) {
+  for (int k = 0; k < j; ++k) {
+    p = mode[k] ? fmax(p - q, 0.0) / div[k] : p / div[k];
+    q = tok == xs[k] ? 0.0 : q / sv[k];
+  }
+  q_out = q;
+  return p;
+}
+
+__device__ __forceinline__ double block_sum_tw(double v, double* red) {
+  v = wave_sum(v);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int w = 0; w < kTwThreads / kWave; ++w) t += red[w];
+  return t;
+}
+
+__device__ __forceinline__ int head_row_of(const TreeArgs& a, int x) {
+  if (!a.d2t) return x < a.head_rows ? x : -1;
+  const int r = lower_bound_i32(a.d2t, a.head_rows, x);
+  return (r < a.head_rows && a.d2t[r] == x) ? r : -1;
+}
+
+__global__ __launch_bounds__(kTwThreads) void k_tree_walk(TreeArgs a) {
+  __shared__ double red[kTwThreads / kWave];
+  __shared__ int s_x[WC_MAX_NODES], s_mode[WC_MAX_NODES], s_path[WC_MAX_NODES];
+  __shared__ double s_div[WC_MAX_NODES], s_s[WC_MAX_NODES];
+  __shared__ int s_bad, s_acc, s_nu;
+  __shared__ unsigned long long s_kids;
+  const int t = threadIdx.x, N = a.rows;
+  const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
+  if (t == 0) {
+    s_bad = 0;
+    s_nu = 0;
+  }
+  __syncthreads();
+  {  // parents[0] = -1, 0 <= parents[i] < i, tokens inside the vocabulary, d2t ascending
+    int bad = 0;
+    for (int i = t; i < N; i += kTwThreads) {
+      const int par = a.parents[i], tok = a.tokens[i];
+      if (i == 0 ? par != -1 : (par < 0 || par >= i)) bad = 1;
+      if (tok < 0 || tok >= a.vocab) bad = 1;
+    }
+    if (a.d2t)
+      for (int r = t; r < a.head_rows; r += kTwThreads) {
+        const int x = a.d2t[r];
+        if (x < 0 || x >= a.vocab || (r + 1 < a.head_rows && a.d2t[r + 1] <= x)) bad = 1;
+      }
+    if (bad) s_bad = 1;
+  }
+  __syncthreads();
+  const bool bad = s_bad != 0;
+  int v = 0, plen = 0, j = 0;
+  double Q = 1.0;
+  while (!bad) {
+    if (t < kWave) {
+      const unsigned long long m = __ballot(t < N && a.parents[min(t, N - 1)] == v);
+      if (t == 0) s_kids = m;
+    }
+    __syncthreads();
+    unsigned long long kids = s_kids;
+    j = 0;
+    if (kids == 0) break;  // a leaf: the draw is from p[v]
+    // node sums: Q, the target mass on the head rows and on the whole vocabulary
+    const float* pr = a.p + static_cast<int64_t>(v) * a.ld_p;
+    const float* qr = a.q + static_cast<int64_t>(v) * a.ld_q;
+    double sq = 0.0, sph = 0.0, spa = 0.0;
+    for (int r = t; r < a.head_rows; r += kTwThreads) {
+      sq += static_cast<double>(qr[r]);
+      sph += static_cast<double>(pr[a.d2t ? a.d2t[r] : r]);
+    }
+    for (int i = t; i < a.vocab; i += kTwThreads) spa += static_cast<double>(pr[i]);
+    Q = block_sum_tw(sq, red);
+    const double p_head = block_sum_tw(sph, red);
+    const double p_out = block_sum_tw(spa, red) - p_head;  // mass where q = 0
+    double divprod = 1.0;
+    int accepted = -1;
+    while (kids != 0) {
+      const int c = __builtin_ctzll(kids);
+      kids &= kids - 1;
+      const int x = a.tokens[c];
+      if (t == 0) {  // the accept test at x after j rejections
+        const int rx = head_row_of(a, x);
+        const double q0 = (rx >= 0 && Q > 0.0) ? static_cast<double>(qr[rx]) / Q : 0.0;
+        double qx;
+        const double px = tree_chain(static_cast<double>(pr[x]), q0, x, j, s_x, s_mode, s_div, s_s, qx);
+        int acc = -1;
+        if (qx > 0.0) {
+          const double u = philox_uniform(a.seed, round, a.purpose, static_cast<unsigned long long>(s_nu++));
+          if (u < fmin(1.0, px / qx)) acc = c;
+        }
+        s_acc = acc;
+      }
+      __syncthreads();
+      accepted = s_acc;
+      if (accepted >= 0) break;
+      // rejection j + 1: residual mass, current p mass and the renormalising q mass
+      double z = 0.0, ps = 0.0, ss = 0.0;
+      for (int r = t; r < a.head_rows; r += kTwThreads) {
+        const int tok = a.d2t ? a.d2t[r] : r;
+        const double q0 = Q > 0.0 ? static_cast<double>(qr[r]) / Q : 0.0;
+        double qj;
+        const double pj = tree_chain(static_cast<double>(pr[tok]), q0, tok, j, s_x, s_mode, s_div, s_s, qj);
+        z += fmax(pj - qj, 0.0);
+        ps += pj;
+        ss += tok == x ? 0.0 : qj;
+      }
+      z = block_sum_tw(z, red);
+      ps = block_sum_tw(ps, red);
+      ss = block_sum_tw(ss, red);
+      const double outside = p_out / divprod;
+      const double zt = outside + z;
+      const bool normal = zt > 1e-12;
+      const double div = normal ? zt : outside + ps;
+      if (t == 0) {
+        s_x[j] = x;
+        s_mode[j] = normal ? 1 : 0;
+        s_div[j] = div;
+        s_s[j] = ss;
+      }
+      __syncthreads();
+      divprod *= div;
+      ++j;
+      if (ss <= 0.0) break;
+    }
+    if (accepted < 0) break;  // every child rejected: the draw is from the current p at v
+    if (t == 0) s_path[plen] = accepted;
+    ++plen;
+    v = accepted;
+    __syncthreads();
+  }
+  __syncthreads();
+  TreeState* st = a.st;
+  if (t == 0) {
+    st->q_mass = Q;
+    st->node = bad ? 0 : v;
+    st->nsteps = bad ? 0 : j;
+    st->n_uniforms = s_nu;
+    st->path_len = bad ? 0 : plen;
+    st->bad = bad ? 1 : 0;
+  }
+  if (t < WC_MAX_NODES) {
+    st->path[t] = s_path[t];
+    st->x[t] = s_x[t];
+    st->mode[t] = s_mode[t];
+    st->div[t] = s_div[t];
+    st->s[t] = s_s[t];
+  }
+}
+
+__global__ __launch_bounds__(kStThreads) void k_tree_sample(TreeArgs a) {
+  __shared__ double red[kStThreads / kWave];
+  __shared__ double qchunk[kVocabChunk];
+  __shared__ double s_tsum[kStThreads];
+  __shared__ int s_x[WC_MAX_NODES], s_mode[WC_MAX_NODES];
+  __shared__ double s_div[WC_MAX_NODES], s_s[WC_MAX_NODES];
+  __shared__ int s_chunk, s_idx;
+  const TreeState* st = a.st;
+  const int t = threadIdx.x;
+  const int v = st->node, j = st->nsteps;
+  const double Q = st->q_mass;
+  if (t < WC_MAX_NODES) {
+    s_x[t] = st->x[t];
+    s_mode[t] = st->mode[t];
+    s_div[t] = st->div[t];
+    s_s[t] = st->s[t];
+  }
+  const float* pr = a.p + static_cast<int64_t>(v) * a.ld_p;
+  const float* qr = a.q ? a.q + static_cast<int64_t>(v) * a.ld_q : nullptr;
+  // values of chunk c of the final distribution: q of the head rows in the chunk
+  // scattered into LDS (zero elsewhere), then the j-step map per entry
+  auto values = [&](int c, double (&val)[kPerThread]) {
+    const int x0 = c * kVocabChunk;
+    for (int k = t; k < kVocabChunk; k += kStThreads) qchunk[k] = 0.0;
+    __syncthreads();
+    if (j > 0 && qr && Q > 0.0) {
+      if (a.d2t) {
+        const int r0 = lower_bound_i32(a.d2t, a.head_rows, x0);
+        const int r1 = lower_bound_i32(a.d2t, a.head_rows, x0 + kVocabChunk);
+        for (int r = r0 + t; r < r1; r += kStThreads) qchunk[a.d2t[r] - x0] = static_cast<double>(qr[r]) / Q;
+      } else {
+        for (int k = t; k < kVocabChunk && x0 + k < a.head_rows; k += kStThreads)
+          qchunk[k] = static_cast<double>(qr[x0 + k]) / Q;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      const int k = t * kPerThread + e, x = x0 + k;
+      double qo;
+      val[e] = x < a.vocab ? tree_chain(static_cast<double>(pr[x]), qchunk[k], x, j, s_x, s_mode, s_div, s_s, qo)
+                           : 0.0;
+    }
+  };
+  const int c = blockIdx.x, nchunks = gridDim.x;
+  double val[kPerThread];
+  values(c, val);
+  double sum = 0.0;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) sum += val[e];
+  sum = block_sum_f64(sum, red);
+  if (t == 0)
+    atomic_store_u64(reinterpret_cast<unsigned long long*>(a.chunk_data + c),
+                     static_cast<unsigned long long>(__double_as_longlong(sum)));
+  if (!last_block_done(a.counter, nchunks, c)) return;
+
+  // ---- last block: the total, the chunk holding u * total, then the entry
+  double cm[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int k = t + h * kStThreads;
+    const unsigned long long* cd = reinterpret_cast<const unsigned long long*>(a.chunk_data + min(k, nchunks - 1));
+    cm[h] = k < nchunks ? __longlong_as_double(static_cast<long long>(atomic_load_u64(cd))) : 0.0;
+  }
+  const double total = block_sum_f64(cm[0] + cm[1], red);
+  const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
+  const int nu = st->n_uniforms;
+  const double target = philox_uniform(a.seed, round, a.purpose, static_cast<unsigned long long>(nu)) * total;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int k = t + h * kStThreads;
+    if (k < nchunks) qchunk[k] = cm[h];
+  }
+  __syncthreads();
+  if (t == 0) {
+    double run = 0.0;
+    int cs = nchunks - 1;
+    for (int k = 0; k < nchunks; ++k) {
+      if (run + qchunk[k] > target) {
+        cs = k;
+        break;
+      }
+      run += qchunk[k];
+    }
+    s_chunk = cs;
+    red[0] = run;
+    s_idx = kVocabChunk;
+  }
+  __syncthreads();
+  const int cs = s_chunk;
+  const double before = red[0];
+  __syncthreads();
+  values(cs, val);
+  double tsum = 0.0;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) tsum += val[e];
+  s_tsum[t] = tsum;
+  __syncthreads();
+  if (t == 0) {
+    double run = before;
+    for (int k = 0; k < kStThreads; ++k) {
+      const double w = s_tsum[k];
+      s_tsum[k] = run;
+      run += w;
+    }
+  }
+  __syncthreads();
+  double run = s_tsum[t];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    run += val[e];
+    if (run > target) {
+      atomicMin(&s_idx, t * kPerThread + e);
+      break;
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    const int x = min(cs * kVocabChunk + s_idx, a.vocab - 1);  // searchsorted clamp (sampling.py:193)
+    const int plen = st->path_len;
+    wc_verdict* out = a.verdict;
+    out->keep[0] = 0;
+    for (int k = 0; k < plen; ++k) {
+      out->tokens[k] = a.tokens[st->path[k]];
+      out->keep[k + 1] = st->path[k];
+    }
+    out->tokens[plen] = x;
+    out->n_accepted = plen;
+    out->next = x;
+    out->n_keep = plen + 1;
+    out->n_uniforms = nu + 1;
+    out->status = st->bad ? WC_E_INVALID : 0;
+  }
+}
+
 // ------------------------------------------------------------------ softmax
 
 struct ProbsArgs {
@@ -440,6 +782,49 @@ int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p
   hipLaunchKernelGGL(k_stoch_rows, dim3(rows), dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
   hipLaunchKernelGGL(k_stoch_sample, dim3((vocab + kVocabChunk - 1) / kVocabChunk), dim3(kStThreads), 0, s, a);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_verify_tree_stochastic(const float* p, int rows, int vocab, int64_t ld_p, const float* q, int head_rows,
+                              int64_t ld_q, const int32_t* d2t_dev, const int32_t* tree_tokens_dev,
+                              const int32_t* tree_parents_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
+                              void* workspace, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(p && tree_tokens_dev && tree_parents_dev && verdict_dev && rng && rng->round_dev,
+             "wc_verify_tree_stochastic: NULL buffer");
+  WC_REQUIRE(workspace && aligned(workspace, 16), "wc_verify_tree_stochastic: workspace is NULL or misaligned");
+  WC_REQUIRE(rows >= 1 && rows <= WC_MAX_NODES, "wc_verify_tree_stochastic: rows must be in 1..%d (got %d)",
+             WC_MAX_NODES, rows);
+  WC_REQUIRE(vocab >= 1 && vocab <= kVocabChunk * kMaxVocabChunks, "wc_verify_tree_stochastic: vocab %d out of range",
+             vocab);
+  WC_REQUIRE(ld_p >= vocab, "wc_verify_tree_stochastic: p row stride smaller than vocab");
+  WC_REQUIRE(rows == 1 || (q && head_rows >= 1 && ld_q >= head_rows),
+             "wc_verify_tree_stochastic: bad draft distribution buffer / width / stride");
+  WC_REQUIRE(d2t_dev != nullptr || head_rows <= vocab,
+             "wc_verify_tree_stochastic: without d2t the draft distribution must not exceed the vocabulary");
+  TreeArgs a{};
+  a.p = p;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.ld_p = ld_p;
+  a.q = q;
+  a.head_rows = rows == 1 ? 0 : head_rows;
+  a.ld_q = ld_q;
+  a.d2t = d2t_dev;
+  a.tokens = tree_tokens_dev;
+  a.parents = tree_parents_dev;
+  a.seed = rng->seed;
+  a.round_dev = rng->round_dev;
+  a.purpose = rng->purpose;
+  a.st = reinterpret_cast<TreeState*>(static_cast<char*>(workspace) + kTreeStateOff);
+  a.chunk_data = reinterpret_cast<double*>(static_cast<char*>(workspace) + kStochChunkOff);
+  a.counter = verify_counter(workspace, kCtrTree);
+  a.verdict = verdict_dev;
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_tree_walk, dim3(1), dim3(kTwThreads), 0, s, a);
+  WC_LAUNCHED();
+  hipLaunchKernelGGL(k_tree_sample, dim3((vocab + kVocabChunk - 1) / kVocabChunk), dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
   return WC_OK;
 }

@@ -46,7 +46,7 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 constexpr size_t kSlotBytes = 8 * WC_MAX_NODES;
 constexpr size_t kCounterOff = kSlotBytes;
 constexpr int kNumCounters = 4;
-enum Counter { kCtrArgmax = 0, kCtrStochastic = 1 };
+enum Counter { kCtrArgmax = 0, kCtrStochastic = 1, kCtrTree = 2 };
 
 // ------------------------------------------------------------------ device helpers
 
@@ -232,7 +232,9 @@ constexpr size_t kStochChunkOff = kStochRowOff + kStochRowBytes;
 constexpr size_t kStochChunkBytes = 8 * 2 * kMaxVocabChunks;
 constexpr size_t kProbsOff = kStochChunkOff + kStochChunkBytes;
 constexpr size_t kProbsBytes = 4 * 2 * static_cast<size_t>(WC_MAX_NODES) * kMaxVocabChunks;
-constexpr size_t kVerifyWorkspace = kProbsOff + kProbsBytes;
+constexpr size_t kTreeStateOff = kProbsOff + kProbsBytes;  // stochastic tree walk state
+constexpr size_t kTreeStateBytes = 4096;
+constexpr size_t kVerifyWorkspace = kTreeStateOff + kTreeStateBytes;
 inline unsigned int* verify_counter(void* ws, int which) {
   return reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + kCounterOff + which * kTreeCounterBytes);
 }

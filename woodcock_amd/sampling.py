@@ -231,3 +231,80 @@ def verify_chain_stochastic(p: torch.Tensor, q: torch.Tensor, draft_tokens, rng:
     v = read_verdict(verify_chain_stochastic_dev(p2, q, d.to(dev, torch.int32), u, d2t))
     rng.round += 1
     return int(v.n_accepted), int(v.next)
+
+
+def verify_tree_stochastic_dev(p: torch.Tensor, q: torch.Tensor | None, tree_tokens: torch.Tensor,
+                               tree_parents: torch.Tensor, rng: _lib.Uniforms, d2t: torch.Tensor | None = None,
+                               verdict: torch.Tensor | None = None) -> torch.Tensor:
+    """Enqueue the stochastic tree rule; p (N, V) target probabilities per node,
+    q (N, H) the draft distribution each node's children were drawn from, over
+    the H head rows (rows of leaves unused; d2t maps row -> token, None = identity)."""
+    p2 = _logits_2d(p)
+    N, vocab = p2.shape
+    if tree_tokens.numel() != N or tree_parents.numel() != N:
+        raise ValueError(f"{N} probability rows need {N} tree tokens and parents")
+    if N > 1:
+        if q is None:
+            raise ValueError("q is required for a tree with children")
+        q2 = _logits_2d(q)
+        if q2.shape[0] < N:
+            raise ValueError(f"q has {q2.shape[0]} rows, {N} needed")
+        head_rows, ldq, qp = q2.shape[1], q2.stride(0), ptr(q2)
+    else:
+        head_rows, ldq, qp = 1, 1, None
+    if d2t is not None and d2t.numel() != head_rows:
+        raise ValueError(f"d2t has {d2t.numel()} entries for {head_rows} draft rows")
+    verdict = new_verdict(p2.device) if verdict is None else verdict
+    _lib.call("wc_verify_tree_stochastic", ptr(p2), N, vocab, p2.stride(0), qp, head_rows, ldq,
+              ptr(d2t) if d2t is not None else None, ptr(tree_tokens), ptr(tree_parents), C.byref(rng),
+              ptr(verdict), ptr(workspace(p2.device)), stream_ptr())
+    return verdict
+
+
+def verify_tree_stochastic(p: torch.Tensor, q: torch.Tensor | None, tree: DraftTree, rng: PhiloxStream,
+                           d2t: torch.Tensor | None = None) -> tuple[list[int], int]:
+    """Recursive rejection down the tree (python/woodcock/sampling.py:143-177):
+    -> (accepted node path, next token).  Advances ``rng.round`` by one."""
+    p2 = _logits_2d(p)
+    dev = p2.device
+    rd = rng.device_round(dev)
+    v = read_verdict(verify_tree_stochastic_dev(p2, q, i32(tree.tokens, dev), i32(tree.parents, dev),
+                                                rng.struct(rd), d2t))
+    rng.round += 1
+    if v.status != 0:
+        raise ValueError("invalid tree, token or d2t")
+    return [int(v.keep[1 + i]) for i in range(v.n_accepted)], int(v.next)
+
+
+def tree_attention_mask_dev(parents: torch.Tensor, prefix_len: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """(N, prefix_len + N) uint8 mask on the device: the prefix plus each node's
+    ancestors (python/woodcock/sampling.py:118-128)."""
+    n = parents.numel()
+    out = torch.empty(n, prefix_len + n, dtype=torch.uint8, device=parents.device) if out is None else out
+    if out.dtype != torch.uint8 or out.shape[0] != n or out.shape[1] < prefix_len + n or out.stride(1) != 1:
+        raise ValueError("out must be a uint8 (N, >= prefix_len + N) tensor")
+    _lib.call("wc_tree_mask", ptr(parents), n, prefix_len, ptr(out), out.stride(0), stream_ptr())
+    return out
+
+
+def sample_without_replacement_dev(q: torch.Tensor, k: int | torch.Tensor, rng: _lib.Uniforms,
+                                   d2t: torch.Tensor | None = None, uniform_base: int = 0
+                                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Gumbel-top-k per row of q (rows, H) over the head rows
+    (python/woodcock/sampling.py:196-203): -> (tokens (rows, k_max), counts (rows,)).
+    Row r consumes one uniform per nonzero entry after those of rows < r."""
+    q2 = _logits_2d(q)
+    rows, H = q2.shape
+    if isinstance(k, torch.Tensor):
+        k_dev, k_max = k.to(q2.device, torch.int32).contiguous(), int(k.max())
+    else:
+        k_dev, k_max = None, int(k)
+    if d2t is not None and d2t.numel() != H:
+        raise ValueError(f"d2t has {d2t.numel()} entries for {H} draft rows")
+    toks = torch.full((rows, k_max), -1, dtype=torch.int32, device=q2.device)
+    counts = torch.zeros(rows, dtype=torch.int32, device=q2.device)
+    _lib.call("wc_sample_without_replacement", ptr(q2), rows, H, q2.stride(0), ptr(d2t) if d2t is not None else None,
+              ptr(k_dev) if k_dev is not None else None, k_max, C.byref(rng), int(uniform_base), ptr(toks),
+              ptr(counts), stream_ptr())
+    return toks, counts
+
