@@ -189,6 +189,60 @@ def test_update_rows_with_device_count(cuda):
             c.offset = cache_off + n
 
 
+def test_qwen3_4b_step_and_update_match_oracle(cuda):
+    """Qwen3-4B drafter width (hidden 2560, 32 q / 8 kv heads, SwiGLU 9728, fc
+    7680 -> 2560, the 16k head) at drafter context 4096 with a bf16 cache: two
+    draft steps (layer + fused final norm and head) and a 5-row update pass
+    (fuse + forward), GPU vs the oracle over identical weights and cache."""
+    import ctypes as C
+
+    from woodcock_amd import _lib
+    from woodcock_amd.config import qwen3_4b_drafter
+    from woodcock_amd.runtime import ptr, stream_ptr
+
+    cfg = qwen3_4b_drafter()
+    dm = cfg.hidden_size
+    d, od, cache, oc, ids = _oracle_step_setup(cfg, 6, cuda, 4096, torch.bfloat16)
+    rng = np.random.default_rng(6)
+    tol = 1e-4
+    for step in range(2):
+        tok = int(rng.integers(0, cfg.vocab_size))
+        feat = rng.standard_normal((1, dm)).astype(np.float32)
+        hid, out = d(torch.tensor([tok]), torch.from_numpy(feat).to(cuda), cache)
+        ohid, oout = od.forward([tok], feat, oc)
+        assert _rel(hid.cpu().numpy(), ohid) <= tol, step
+        out_n = torch.full_like(out, float("nan"))
+        z = torch.full((1, 16384), float("nan"), device=cuda)
+        tk = d.draft_from_hidden(hid, out=out_n, logits=z).cpu().numpy()
+        oz = od.logits(oout)
+        assert _rel(out_n.cpu().numpy(), oout) <= tol, step
+        assert _rel(z.cpu().numpy(), oz) <= tol, step
+        top2 = np.sort(oz[0])[-2:]
+        if top2[1] - top2[0] > 1e-3 * np.abs(oz).max():
+            assert int(tk[0]) == int(ids[int(np.argmax(oz[0]))]), step
+    # update pass over 5 accepted rows
+    taps = [rng.standard_normal((5, dm)).astype(np.float32) for _ in range(3)]
+    toks = rng.integers(0, cfg.vocab_size, 5).astype(np.int32)
+    off = cache[0].offset
+    nrow = torch.tensor([5, off], dtype=torch.int32, device=cuda)
+    g = torch.empty(5, dm, device=cuda)
+    tp = [torch.from_numpy(t).to(cuda) for t in taps]
+    arr = (C.c_void_p * 3)(*[t.data_ptr() for t in tp])
+    _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr, _lib.WC_F32, dm, None, 5, ptr(nrow[0:1]),
+              ptr(g), dm, ptr(d.ws), stream_ptr())
+    hid = torch.empty(5, dm, device=cuda)
+    kp = (C.c_void_p * 1)(cache[0].keys.data_ptr())
+    vp = (C.c_void_p * 1)(cache[0].values.data_ptr())
+    tk = torch.from_numpy(toks).to(cuda)
+    _lib.call("wc_drafter_forward", C.byref(d.dims), C.byref(d.wstruct), ptr(tk), ptr(g), dm, None, 0, 5,
+              ptr(nrow[0:1]), kp, vp, _lib.WC_BF16, cache[0].capacity, ptr(nrow[1:2]), 0, None, None, 0, ptr(hid),
+              None, None, ptr(d.ws), stream_ptr())
+    og = od.fuse(taps)
+    ohid, _ = od.forward(toks, og, oc)
+    assert _rel(g.cpu().numpy(), og) <= 1e-5
+    assert _rel(hid.cpu().numpy(), ohid) <= tol
+
+
 def test_restricted_head_equals_gathered_full_head(cuda):
     """tests/test_vocab.py:37-47 on the GPU: bit-exact rows, token_ids maps rows."""
     from woodcock_amd.config import tiny_drafter

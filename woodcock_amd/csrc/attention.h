@@ -16,6 +16,19 @@ constexpr int kMaxQV = 64;      // query vectors (rows x GQA group) per attentio
 constexpr int kMaxSplits = 32;
 constexpr int kMaxKvHeads = 64;
 
+// ------------------------------------------------------------------ fragment-major activations
+// Element (m, k) of a block of 64 fp32 rows, split into bf16 hi (round to
+// nearest) and lo (the rounding remainder), stored where one lane's 16-byte A
+// fragment of v_mfma_f32_16x16x32_bf16 reads it: 32-wide k step s = k / 32,
+// row tile m / 16, part h (0 hi, 1 lo), lane (m % 16) + 16 ((k % 32) / 8),
+// element k % 8.  One k step of all four row tiles is a contiguous 8 KB run.
+constexpr int kXaRowTiles = 4;
+constexpr int kXaStepElems = kXaRowTiles * 2 * 512;  // bf16 per k step
+__device__ __forceinline__ int64_t xa_index(int m, int k, int h) {
+  return (static_cast<int64_t>(k >> 5) * kXaRowTiles + (m >> 4)) * 1024 + h * 512 +
+         ((m & 15) + 16 * ((k & 31) >> 3)) * 8 + (k & 7);
+}
+
 // ------------------------------------------------------------------ attention
 
 struct AttnArgs {
@@ -38,6 +51,7 @@ struct AttnArgs {
   float* partial;  // [Hk][S][qv_ld][D+2]
   int qv_ld;       // query vectors per (kv head, split) in `partial` (>= rows x group)
   float* out;  // [rows][H*D]
+  uint16_t* xa_out;  // optional: the output also as fragment-major bf16 hi / lo (see xa_index), or NULL
   int64_t ld_out;
 };
 
@@ -473,7 +487,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) 
     if (sp < S) num = fmaf(s_w[sp], o[sp], num);
   if (t < D) {
     const int l = v / rep, h = kh * rep + v % rep;
-    a.out[l * a.ld_out + h * D + t] = num / s_den;
+    const float y = num / s_den;
+    a.out[l * a.ld_out + h * D + t] = y;
+    if (a.xa_out) {
+      const __bf16 hi = static_cast<__bf16>(y);
+      a.xa_out[xa_index(l, h * D + t, 0)] = __builtin_bit_cast(uint16_t, hi);
+      a.xa_out[xa_index(l, h * D + t, 1)] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y - static_cast<float>(hi)));
+    }
   }
 }
 

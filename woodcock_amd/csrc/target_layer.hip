@@ -8,236 +8,405 @@
 // block's K/V at the cache offset.
 //
 // The projections are skinny GEMMs (M <= 64 rows against weight matrices of
-// 2048..12288 rows): bf16 MFMA (v_mfma_f32_16x16x32_bf16) with the fp32
-// activations split into bf16 hi + lo parts (x = hi + lo to ~2^-17 relative),
-// so the products keep fp32-level accuracy.  Each block owns 128 output
-// features and one 256-wide K chunk (split-K, so every CU gets work and the
-// activations are read ~N/128 times, not once per row); a second launch sums
-// the K chunks in a fixed order (deterministic), applies the RMSNorm scale and
-// the epilogue (store, residual, SiLU(gate) * up).
+// 2048..12288 rows), HBM-bound on the weight stream: bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16) with the fp32 activations split into bf16 hi + lo
+// parts (x = hi + lo to ~2^-17 relative) so the products keep fp32-level
+// accuracy.  The activations are written once, already split and in MFMA
+// fragment order (xa_index), by whoever produces them -- a prep kernel for the
+// layer input, the attention merge, the o_proj and gate/up epilogues -- with
+// the next RMSNorm's gain folded in and per-row sums of squares on the side
+// (the norm's 1/rms scales the products afterwards).  k_mm_stream streams the
+// weights straight into B fragments eight k steps ahead while a three-slot LDS
+// ring hands each k step of activations to the block's four waves; blocks
+// split K when the projection is too narrow to fill the GPU, and the last
+// block of a column range sums the partials in a fixed order and runs the
+// epilogue (store, residual, SiLU(gate) * up, next activations).
 #include "attention.h"
 
 namespace wc {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
+typedef float af32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMmThreads = 256;           // 4 waves
-constexpr int kMmNT = 128;                // output features per block: 4 waves x 2 tiles of 16
-constexpr int kMmKC = 256;                // K per block: 8 MFMA steps of 32
-constexpr int kMmMaxRows = 64;            // 4 row tiles of 16
-constexpr int kMmLdsRow = kMmKC * 2 + 16; // bytes per LDS row of bf16 (16 B pad against bank conflicts)
-constexpr int kMmMaxSeg = 3;
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+}
 
-struct MmArgs {
-  const float* x;  // [M][ldx] fp32 rows
+// 8 fp32 -> bf16 hi (round to nearest) and lo (the rounding remainder, rounded):
+// hi + lo equals x to ~2^-17 relative, so bf16 MFMA products keep fp32 accuracy.
+__device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& lo) {
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = x[e] - static_cast<float>(static_cast<__bf16>(x[e]));
+  hi = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
+  lo = make_uint4(pack2_bf16(r[0], r[1]), pack2_bf16(r[2], r[3]), pack2_bf16(r[4], r[5]), pack2_bf16(r[6], r[7]));
+}
+__device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo) {
+  uint4 h, l;
+  split8(x, h, l);
+  hi = __builtin_bit_cast(abf16x8, h);
+  lo = __builtin_bit_cast(abf16x8, l);
+}
+
+// ------------------------------------------------------------------ activation prep
+// x [M][ldx] fp32 (times gain when given) -> fragment-major hi / lo, plus the
+// rows' sums of squares of x per 256-wide k block: ss [K / 256][64].  Block b
+// covers k [256 b, 256 b + 256) of all 64 rows (rows >= M are zero); thread t
+// row t / 4, k [256 b + 64 (t % 4), + 64).
+struct XaPrepArgs {
+  const float* x;
   int64_t ldx;
-  const uint16_t* gain;  // [K] bf16 RMSNorm gain, or NULL (no norm)
-  const uint16_t* w[kMmMaxSeg];  // per output segment: [rows][K] bf16
-  int seg_start[kMmMaxSeg + 1];  // output feature boundaries (multiples of kMmNT)
-  int n_seg;
-  int M, N, K, kchunks;
-  float* part;  // [kchunks][M][N]
-  float* ss;    // [kchunks][M] sums of squares of x over each chunk (with a gain)
+  int M, K;
+  const uint16_t* gain;
+  uint16_t* xa;
+  float* ss;
 };
 
-__device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
-  const __bf16 x = static_cast<__bf16>(a), y = static_cast<__bf16>(b);
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, x)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, y)) << 16);
-}
-
-// Block (n tile, K chunk): partial products of its 128 features over its chunk.
-template <int MT>
-__global__ __launch_bounds__(kMmThreads) void k_mm_partial(MmArgs a) {
-  __shared__ __attribute__((aligned(16))) unsigned char s_hi[kMmMaxRows * kMmLdsRow];
-  __shared__ __attribute__((aligned(16))) unsigned char s_lo[kMmMaxRows * kMmLdsRow];
-  const int lane = threadIdx.x % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int nb = blockIdx.x * kMmNT, kc = blockIdx.y, k0 = kc * kMmKC;
-
-  // 1. this wave's weights: 2 tiles of 16 features x 8 steps, one 16-byte
-  //    fragment per lane each (feature lane%16, k group lane/16)
-  int seg = 0;
+__global__ __launch_bounds__(256) void k_xa_prep(XaPrepArgs a) {
+  const int t = threadIdx.x, m = t / 4, k0 = blockIdx.x * 256 + (t % 4) * 64;
+  const bool live = m < a.M;
+  const float* xr = a.x + static_cast<int64_t>(min(m, a.M - 1)) * a.ldx + k0;
+  float4 xv[16];
 #pragma unroll
-  for (int j = 1; j < kMmMaxSeg; ++j)
-    if (j < a.n_seg && nb >= a.seg_start[j]) seg = j;
-  const uint16_t* wbase = seg == 0 ? a.w[0] : seg == 1 ? a.w[1] : a.w[2];
-  const int sbeg = seg == 0 ? a.seg_start[0] : seg == 1 ? a.seg_start[1] : a.seg_start[2];
-  uint4 wf[2][8];
+  for (int i = 0; i < 16; ++i) xv[i] = *reinterpret_cast<const float4*>(xr + 4 * i);
+  uint4 gv[8];
+  if (a.gain) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = min(nb + wave * 32 + j * 16 + lane % 16, a.N - 1) - sbeg;
-    const uint16_t* wr = wbase + static_cast<int64_t>(n) * a.K + k0 + (lane / 16) * 8;
-#pragma unroll
-    for (int s = 0; s < 8; ++s) wf[j][s] = *reinterpret_cast<const uint4*>(wr + s * 32);
+    for (int i = 0; i < 8; ++i) gv[i] = *reinterpret_cast<const uint4*>(a.gain + k0 + 8 * i);
   }
-
-  // 2. activation chunk -> LDS as bf16 hi / lo of x * gain; thread t owns row
-  //    t/4, columns (t%4)*64 .. +64 of the chunk
-  {
-    const int r = threadIdx.x / 4, q = threadIdx.x % 4;
-    const bool live = r < a.M;
-    const float* xr = a.x + static_cast<int64_t>(min(r, a.M - 1)) * a.ldx + k0 + q * 64;
-    float4 xv[16];
+  float ss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) xv[i] = *reinterpret_cast<const float4*>(xr + 4 * i);
-    uint4 gv[8];
+  for (int g = 0; g < 8; ++g) {
+    float v[8] = {xv[2 * g].x, xv[2 * g].y, xv[2 * g].z, xv[2 * g].w,
+                  xv[2 * g + 1].x, xv[2 * g + 1].y, xv[2 * g + 1].z, xv[2 * g + 1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (!live) v[e] = 0.f;
+      ss = fmaf(v[e], v[e], ss);
+    }
     if (a.gain) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) gv[i] = *reinterpret_cast<const uint4*>(a.gain + k0 + q * 64 + 8 * i);
+      const uint4 q = gv[g];
+      v[0] *= bf16_lo(q.x); v[1] *= bf16_hi(q.x); v[2] *= bf16_lo(q.y); v[3] *= bf16_hi(q.y);
+      v[4] *= bf16_lo(q.z); v[5] *= bf16_hi(q.z); v[6] *= bf16_lo(q.w); v[7] *= bf16_hi(q.w);
     }
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v[8] = {xv[2 * i].x, xv[2 * i].y, xv[2 * i].z, xv[2 * i].w,
-                    xv[2 * i + 1].x, xv[2 * i + 1].y, xv[2 * i + 1].z, xv[2 * i + 1].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        if (!live) v[e] = 0.f;
-        ss = fmaf(v[e], v[e], ss);
-      }
-      if (a.gain) {
-        const uint4 g = gv[i];
-        v[0] *= bf16_lo(g.x); v[1] *= bf16_hi(g.x); v[2] *= bf16_lo(g.y); v[3] *= bf16_hi(g.y);
-        v[4] *= bf16_lo(g.z); v[5] *= bf16_hi(g.z); v[6] *= bf16_lo(g.w); v[7] *= bf16_hi(g.w);
-      }
-      float lo[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lo[e] = v[e] - static_cast<float>(static_cast<__bf16>(v[e]));
-      const uint4 hq = make_uint4(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]), pack_bf16(v[4], v[5]),
-                                  pack_bf16(v[6], v[7]));
-      const uint4 lq = make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]), pack_bf16(lo[4], lo[5]),
-                                  pack_bf16(lo[6], lo[7]));
-      const int off = r * kMmLdsRow + (q * 64 + 8 * i) * 2;
-      *reinterpret_cast<uint4*>(s_hi + off) = hq;
-      *reinterpret_cast<uint4*>(s_lo + off) = lq;
-    }
-    // the row's four threads are adjacent lanes: combine, one of them records
-    ss += __shfl_xor(ss, 1);
-    ss += __shfl_xor(ss, 2);
-    if (a.gain && q == 0 && live && blockIdx.x == 0) a.ss[static_cast<int64_t>(kc) * a.M + r] = ss;
+    uint4 hi, lo;
+    split8(v, hi, lo);
+    *reinterpret_cast<uint4*>(a.xa + xa_index(m, k0 + 8 * g, 0)) = hi;
+    *reinterpret_cast<uint4*>(a.xa + xa_index(m, k0 + 8 * g, 1)) = lo;
   }
-  lds_barrier();
-
-  // 3. MFMA: rows tile i (MT of them) x features tile j (2), 8 steps, hi and lo
-  f32x4 acc[2][MT];
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const int off = (i * 16 + lane % 16) * kMmLdsRow + (s * 32 + (lane / 16) * 8) * 2;
-      const bf16x8 ah = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(s_hi + off));
-      const bf16x8 al = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(s_lo + off));
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const bf16x8 b = __builtin_bit_cast(bf16x8, wf[j][s]);
-        acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, b, acc[j][i], 0, 0, 0);
-        acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, b, acc[j][i], 0, 0, 0);
-      }
-    }
-  }
-
-  // 4. partials: lane holds feature lane%16, rows (lane/16)*4 + e of each tile
-  float* pp = a.part + static_cast<int64_t>(kc) * a.M * a.N;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int n = nb + wave * 32 + j * 16 + lane % 16;
-    if (n >= a.N) continue;
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = i * 16 + (lane / 16) * 4 + e;
-        if (m < a.M) pp[static_cast<int64_t>(m) * a.N + n] = acc[j][i][e];
-      }
-  }
+  ss += __shfl_xor(ss, 1);
+  ss += __shfl_xor(ss, 2);
+  if (t % 4 == 0) a.ss[blockIdx.x * 64 + m] = ss;
 }
 
-enum MmEpi { kMmStore = 0, kMmResidual = 1, kMmSiluPair = 2 };
+// ------------------------------------------------------------------ streaming skinny GEMM
 
-struct MmReduceArgs {
-  const float* part;
-  const float* ss;  // NULL: no norm
-  int M, N, K, kchunks;
+enum SkEpi { kSkRaw = 0, kSkStore = 1, kSkResidual = 2, kSkSiluPair = 3 };
+constexpr int kSkMaxSeg = 3;
+constexpr int kSkP = 8;            // k steps of weights / activations in flight
+constexpr int kSkCtrStride = 32;   // one 128-byte line per column-range counter
+
+struct SkArgs {
+  const uint16_t* xa;  // fragment-major activations, K / 32 steps
+  const float* ss;     // row scale: inv = 1 / sqrt(sum_p ss[p][m] / ss_k + eps); NULL = 1
+  int n_ss, ss_k;
   float eps;
+  const uint16_t* w[kSkMaxSeg];  // weight segments [rows][K] bf16
+  int seg_start[kSkMaxSeg + 1];
+  int n_seg;
+  int M, N, K, ks;  // N weight rows (SiLU pair: gate rows then up rows); ks = K splits
   int epi;
-  float* out;  // [M][ldo]
+  float* out;  // [M][ldo] (N columns, N / 2 for the pair); may be NULL for the pair
   int64_t ldo;
   const float* res;  // residual [M][ldr]
   int64_t ldr;
+  uint16_t* xa_next;         // optional: the output as the next projection's activations
+  const uint16_t* gain_next; // its RMSNorm gain (NULL = none)
+  float* ss_next;            // with xa_next: per-row sums of squares of the output, [gridDim.x][64]
+  float* part;               // ks > 1: [ks][64][cols] partials
+  unsigned int* ctr;         // ks > 1: one counter per column range
 };
 
-// Sum the K chunks in order, scale by the row's 1/rms, epilogue.  Block
-// (feature range, row); for the SiLU pair the features are [gate | up] halves.
-__global__ __launch_bounds__(256) void k_mm_reduce(MmReduceArgs a) {
-  __shared__ float s_inv;
-  const int m = blockIdx.y;
-  if (threadIdx.x == 0) {
-    float inv = 1.f;
-    if (a.ss) {
-      float t = 0.f;
-      for (int c = 0; c < a.kchunks; ++c) t += a.ss[static_cast<int64_t>(c) * a.M + m];
-      inv = 1.f / sqrtf(t / static_cast<float>(a.K) + a.eps);
+// Block (column range cb, K split kz), 4 waves.  TW = tiles of 16 weight rows
+// per wave (block columns FB = 64 TW); wave w owns tiles w TW .. w TW + TW - 1
+// (the SiLU pair: wave w's gate tile and up tile of act features 64 cb + 16 w ..).
+template <int MT, int TW>
+__global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
+  constexpr int FB = 64 * TW;
+  constexpr int AQ = MT * 128;                // uint4 of activations per k step
+  constexpr int AR = (AQ + 255) / 256;        // per thread
+  constexpr int LDC = FB + 4;
+  __shared__ __attribute__((aligned(16))) uint4 s_a[3][AQ];
+  __shared__ float s_c[64 * LDC];
+  __shared__ float s_inv[64];
+  __shared__ bool s_last;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int cb = blockIdx.x, kz = blockIdx.y;
+  const bool pair = a.epi == kSkSiluPair;
+
+  const uint16_t* wp[TW];
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    int row = pair ? (j == 0 ? 0 : a.N / 2) + cb * 64 + wave * 16 + lane % 16
+                   : cb * FB + (wave * TW + j) * 16 + lane % 16;
+    row = min(row, a.N - 1);
+    int seg = 0;
+#pragma unroll
+    for (int q = 1; q < kSkMaxSeg; ++q)
+      if (q < a.n_seg && row >= a.seg_start[q]) seg = q;
+    const uint16_t* base = seg == 0 ? a.w[0] : seg == 1 ? a.w[1] : a.w[2];
+    const int s0r = seg == 0 ? a.seg_start[0] : seg == 1 ? a.seg_start[1] : a.seg_start[2];
+    wp[j] = base + static_cast<int64_t>(row - s0r) * a.K + (lane / 16) * 8;
+  }
+  const int S = a.K / 32, per = (S + a.ks - 1) / a.ks;
+  const int s0 = min(S, kz * per), ns = min(S, s0 + per) - s0;
+
+  af32x4 acc[TW][MT];
+#pragma unroll
+  for (int j = 0; j < TW; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[j][i] = af32x4{0.f, 0.f, 0.f, 0.f};
+  // P steps of weights and activations in flight; the activations of step i
+  // are staged in LDS slot i % 3 just before step i's barrier (the barrier of
+  // step i - 1 guarantees every wave is done with the slot, last read by step
+  // i - 3).  Native vectors (not the uint4 struct) keep the buffers in registers.
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  uint4 wb[kSkP][TW];
+  u32x4v ab[kSkP][AR];
+#pragma unroll
+  for (int u = 0; u < kSkP; ++u) {
+    if (u < ns) {
+#pragma unroll
+      for (int j_ = 0; j_ < TW; ++j_) wb[u][j_] = *reinterpret_cast<const uint4*>(wp[j_] + static_cast<int64_t>(s0 + u) * 32);
+      const uint4* ap_ = reinterpret_cast<const uint4*>(a.xa + static_cast<int64_t>(s0 + u) * kXaStepElems);
+#pragma unroll
+      for (int r_ = 0; r_ < AR; ++r_) ab[u][r_] = reinterpret_cast<const u32x4v*>(ap_)[(t + r_ * 256) % AQ];
     }
-    s_inv = inv;
+  }
+  for (int b = 0; b < ns; b += kSkP) {
+#pragma unroll
+    for (int u = 0; u < kSkP; ++u) {
+      const int i = b + u;
+      if (i < ns) {
+        const int slot = i % 3;
+#pragma unroll
+        for (int r_ = 0; r_ < AR; ++r_) reinterpret_cast<u32x4v*>(s_a[slot])[(t + r_ * 256) % AQ] = ab[u][r_];
+        lds_barrier();
+        abf16x8 ah[MT], al[MT];
+#pragma unroll
+        for (int q = 0; q < MT; ++q) {
+          ah[q] = __builtin_bit_cast(abf16x8, s_a[slot][(2 * q) * 64 + lane]);
+          al[q] = __builtin_bit_cast(abf16x8, s_a[slot][(2 * q + 1) * 64 + lane]);
+        }
+#pragma unroll
+        for (int q = 0; q < MT; ++q)
+#pragma unroll
+          for (int j = 0; j < TW; ++j)
+            acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[q], __builtin_bit_cast(abf16x8, wb[u][j]),
+                                                                acc[j][q], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < MT; ++q)
+#pragma unroll
+          for (int j = 0; j < TW; ++j)
+            acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[q], __builtin_bit_cast(abf16x8, wb[u][j]),
+                                                                acc[j][q], 0, 0, 0);
+        if (i + kSkP < ns) {
+#pragma unroll
+          for (int j_ = 0; j_ < TW; ++j_) wb[u][j_] = *reinterpret_cast<const uint4*>(wp[j_] + static_cast<int64_t>(s0 + i + kSkP) * 32);
+          const uint4* ap_ = reinterpret_cast<const uint4*>(a.xa + static_cast<int64_t>(s0 + i + kSkP) * kXaStepElems);
+#pragma unroll
+          for (int r_ = 0; r_ < AR; ++r_) ab[u][r_] = reinterpret_cast<const u32x4v*>(ap_)[(t + r_ * 256) % AQ];
+        }
+      }
+    }
+  }
+
+  // the block's tile -> LDS: row i 16 + 4 (lane / 16) + e, column (w TW + j) 16 + lane % 16
+#pragma unroll
+  for (int j = 0; j < TW; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        s_c[(i * 16 + (lane / 16) * 4 + e) * LDC + (wave * TW + j) * 16 + lane % 16] = acc[j][i][e];
+  __syncthreads();
+
+  const int m = t / 4, g = t % 4;  // epilogue: row m, column quarter g
+  constexpr int CQ = FB / 4;
+  const int n0 = pair ? cb * 64 + g * 16 : cb * FB + g * CQ;  // first output column of this thread
+  if (a.ks > 1) {
+    // publish this split's tile (a wave per row, lanes along the columns, so
+    // every store is one contiguous run); the last split of the column range
+    // sums the ks tiles in a fixed order
+    const int cols = gridDim.x * FB;
+    float* base = a.part + static_cast<int64_t>(cb) * FB;
+    for (int r = wave; r < a.M; r += 4)
+#pragma unroll
+      for (int c = lane; c < FB; c += kWave)
+        publish_f32(base + (static_cast<int64_t>(kz) * 64 + r) * cols + c, s_c[r * LDC + c]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+      unsigned int* ctr = a.ctr + cb * kSkCtrStride;
+      const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        static_cast<unsigned int>(a.ks - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // element e = t + 256 i of the row-major M x FB tile, 16 elements and two
+    // splits per round
+    constexpr int EPT = 64 * FB / 256, EH = EPT > 16 ? 16 : EPT;
+#pragma unroll
+    for (int i0 = 0; i0 < EPT; i0 += EH) {
+      float v[EH];
+#pragma unroll
+      for (int i = 0; i < EH; ++i) v[i] = 0.f;
+      for (int z = 0; z < a.ks; z += 2) {
+        float u0[EH], u1[EH];
+#pragma unroll
+        for (int i = 0; i < EH; ++i) {
+          const int e = t + 256 * (i0 + i), r = min(e / FB, a.M - 1), c = e % FB;
+          const float* q = base + (static_cast<int64_t>(z) * 64 + r) * cols + c;
+          u0[i] = fetch_f32(q);
+          u1[i] = z + 1 < a.ks ? fetch_f32(q + 64 * static_cast<int64_t>(cols)) : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < EH; ++i) v[i] += u0[i] + u1[i];
+      }
+#pragma unroll
+      for (int i = 0; i < EH; ++i) {
+        const int e = t + 256 * (i0 + i);
+        s_c[(e / FB) * LDC + e % FB] = v[i];
+      }
+    }
+    __syncthreads();
+  }
+  // epilogue operands in one batch: the row scale's partial sums of squares
+  // (thread t sums parts t % 4 + 4 q of row t / 4), residuals, next gains
+  constexpr int kSsMax = 16;  // row-scale parts <= 64
+  const int mr = min(m, a.M - 1);
+  float ssv[kSsMax], resv[CQ];
+  uint16_t gnv[CQ];
+#pragma unroll
+  for (int q = 0; q < kSsMax; ++q) {
+    const int pp = g + 4 * q;
+    ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + m] : 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < CQ; ++c) {
+    resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + n0 + c] : 0.f;
+    gnv[c] = (a.xa_next && a.gain_next && (!pair || c < 16)) ? a.gain_next[n0 + min(c, pair ? 15 : CQ - 1)] : 0;
+  }
+  {
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < kSsMax; ++q) tot += ssv[q];
+    tot += __shfl_xor(tot, 1);
+    tot += __shfl_xor(tot, 2);
+    if (g == 0) s_inv[m] = a.ss ? 1.f / sqrtf(tot / static_cast<float>(a.ss_k) + a.eps) : 1.f;
   }
   __syncthreads();
-  const float inv = s_inv;
-  const int nout = a.epi == kMmSiluPair ? a.N / 2 : a.N;
-  const int n = blockIdx.x * 256 + threadIdx.x;
-  if (n >= nout) return;
-  const int64_t stride = static_cast<int64_t>(a.M) * a.N;
-  const float* p = a.part + static_cast<int64_t>(m) * a.N + n;
-  float y = 0.f, u = 0.f;
-  for (int c = 0; c < a.kchunks; ++c) {
-    y += p[c * stride];
-    if (a.epi == kMmSiluPair) u += p[c * stride + nout];
+  if (m >= a.M) return;
+  const float inv = s_inv[m];
+  // this thread's outputs: 8-wide groups of consecutive output columns
+  constexpr int NC = CQ < 16 ? CQ : 16;  // the pair's outputs per thread
+  float ss = 0.f;
+#pragma unroll
+  for (int c0 = 0; c0 < CQ; c0 += 8) {
+    if (pair && c0 >= NC) continue;
+    float z[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = c0 + e;
+      float y;
+      if (pair) {
+        const int af = g * 16 + c;  // act feature within the block
+        const int gc = (af / 16) * 32 + af % 16;
+        const float gv = s_c[m * LDC + gc] * inv, uv = s_c[m * LDC + gc + 16] * inv;
+        y = gv / (1.f + expf(-gv)) * uv;
+      } else {
+        const float sv = s_c[m * LDC + g * CQ + c];
+        y = (a.epi == kSkRaw ? sv : sv * inv) + resv[c];
+      }
+      z[e] = y;
+    }
+    if (a.out) {
+      float* op = a.out + static_cast<int64_t>(m) * a.ldo + n0 + c0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) op[e] = z[e];
+    }
+    if (a.xa_next) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        ss = fmaf(z[e], z[e], ss);
+        if (a.gain_next) z[e] *= bf16_to_float(gnv[c0 + e]);
+      }
+      uint4 hi, lo;
+      split8(z, hi, lo);
+      *reinterpret_cast<uint4*>(a.xa_next + xa_index(m, n0 + c0, 0)) = hi;
+      *reinterpret_cast<uint4*>(a.xa_next + xa_index(m, n0 + c0, 1)) = lo;
+    }
   }
-  y *= inv;
-  float v;
-  if (a.epi == kMmSiluPair) {
-    u *= inv;
-    v = y / (1.f + expf(-y)) * u;
-  } else if (a.epi == kMmResidual) {
-    v = a.res[static_cast<int64_t>(m) * a.ldr + n] + y;
-  } else {
-    v = y;
+  if (a.xa_next && a.ss_next) {
+    ss += __shfl_xor(ss, 1);
+    ss += __shfl_xor(ss, 2);
+    if (g == 0) a.ss_next[cb * 64 + m] = ss;
   }
-  a.out[static_cast<int64_t>(m) * a.ldo + n] = v;
 }
 
-static int launch_mm_partial(const MmArgs& g, hipStream_t s) {
-  WC_REQUIRE(g.M >= 1 && g.M <= kMmMaxRows, "target layer: rows must be in 1..%d", kMmMaxRows);
-  WC_REQUIRE(g.K % kMmKC == 0, "target layer: K %d must be a multiple of %d", g.K, kMmKC);
-  for (int j = 0; j < g.n_seg; ++j)
-    WC_REQUIRE(g.seg_start[j] % kMmNT == 0, "target layer: projection widths must be multiples of %d", kMmNT);
-  const dim3 grid((g.N + kMmNT - 1) / kMmNT, g.kchunks);
+struct GemmPlan {
+  int tw, cols, ks;
+};
+
+// Column ranges of 64 TW weight rows (TW = 2 for the SiLU pair and wide
+// projections), K split into at most 6 parts so that about 192-256 blocks run
+// with >= 16 k steps each (split-K partials cost 8 ks M bytes per weight row
+// against 2 K bytes of weights).
+static GemmPlan plan_gemm(int n_rows, int K, bool pair) {
+  GemmPlan p{};
+  p.tw = (pair || n_rows >= 8192) ? 2 : 1;
+  p.cols = pair ? n_rows / 2 / 64 : n_rows / (64 * p.tw);
+  const int steps = K / 32;
+  p.ks = std::max(1, std::min(std::min(6, steps / 16), (224 + p.cols - 1) / p.cols));
+  return p;
+}
+
+template <int TW>
+static int launch_stream_t(const SkArgs& g, const GemmPlan& p, hipStream_t s) {
+  const dim3 grid(p.cols, p.ks);
   switch ((g.M + 15) / 16) {
-    case 1: hipLaunchKernelGGL(k_mm_partial<1>, grid, dim3(kMmThreads), 0, s, g); break;
-    case 2: hipLaunchKernelGGL(k_mm_partial<2>, grid, dim3(kMmThreads), 0, s, g); break;
-    case 3: hipLaunchKernelGGL(k_mm_partial<3>, grid, dim3(kMmThreads), 0, s, g); break;
-    default: hipLaunchKernelGGL(k_mm_partial<4>, grid, dim3(kMmThreads), 0, s, g); break;
+    case 1: hipLaunchKernelGGL((k_mm_stream<1, TW>), grid, dim3(256), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((k_mm_stream<2, TW>), grid, dim3(256), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((k_mm_stream<3, TW>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((k_mm_stream<4, TW>), grid, dim3(256), 0, s, g); break;
   }
   WC_LAUNCHED();
   return WC_OK;
 }
 
-static int launch_mm(const MmArgs& g, const MmReduceArgs& r, hipStream_t s) {
-  if (int rc = launch_mm_partial(g, s)) return rc;
-  const int nout = r.epi == kMmSiluPair ? r.N / 2 : r.N;
-  hipLaunchKernelGGL(k_mm_reduce, dim3((nout + 255) / 256, r.M), dim3(256), 0, s, r);
+static int launch_stream(SkArgs g, const GemmPlan& p, hipStream_t s) {
+  WC_REQUIRE(g.M >= 1 && g.M <= 64, "target layer: rows must be in 1..64");
+  WC_REQUIRE(g.K % 256 == 0, "target layer: K %d must be a multiple of 256", g.K);
+  WC_REQUIRE(g.n_ss <= 64, "target layer: at most 64 row-scale parts");
+  g.ks = p.ks;
+  return p.tw == 2 ? launch_stream_t<2>(g, p, s) : launch_stream_t<1>(g, p, s);
+}
+
+static int launch_xa_prep(const float* x, int64_t ldx, int M, int K, const uint16_t* gain, uint16_t* xa, float* ss,
+                          hipStream_t s) {
+  XaPrepArgs a{x, ldx, M, K, gain, xa, ss};
+  hipLaunchKernelGGL(k_xa_prep, dim3(K / 256), dim3(256), 0, s, a);
   WC_LAUNCHED();
   return WC_OK;
 }
 
 // ------------------------------------------------------------------ QKV epilogue
-// The QKV projection's reduce kernel, for head_dim 128: per (row, 256 output
-// features = two heads) it sums the K chunks, applies RMS_in, then for q and k
+// The QKV projection's epilogue, for head_dim 128: per (row, 256 output
+// features = two heads) it applies RMS_in to the projection sums, then for q and k
 // heads the per-head RMSNorm (q_norm / k_norm gains) and rotate-half RoPE at
 // the row's position (src/backends/cpu_ops.cpp:61-77), in the order
 // x1 = x inv g, lo' = x1 c - x2 s, hi' = x2 c + x1 s.  q lands in q_out; the
@@ -246,9 +415,9 @@ static int launch_mm(const MmArgs& g, const MmReduceArgs& r, hipStream_t s) {
 constexpr int kVaD = 128;  // head_dim of the verify-width path
 
 struct QkvEpiArgs {
-  const float* part;  // [kchunks][M][N]
-  const float* ss;    // [kchunks][M]
-  int M, N, K, kchunks;
+  const float* sums;  // [M][N] unscaled projections
+  const float* ss;    // [n_ss][64] per-row sums of squares of the layer input
+  int M, N, K, n_ss;
   float eps;
   float* q_out;  // [M][nq]
   int64_t ldq;
@@ -268,14 +437,12 @@ __global__ __launch_bounds__(256) void k_mm_reduce_qkv(QkvEpiArgs a) {
   const int m = blockIdx.y, t = threadIdx.x, wave = t / kWave;
   const int n = min(blockIdx.x * 256 + t, a.N - 1);
   const bool live = blockIdx.x * 256 + t < a.N;
-  // every load first: the row's chunk sums of squares, this feature's partials,
-  // the position and the cache offset
+  // every load first: the row's sums of squares, this feature's sum, the
+  // position and the cache offset
   float ssum = 0.f;
-  for (int c = 0; c < a.kchunks; ++c) ssum += a.ss[static_cast<int64_t>(c) * a.M + m];
-  const int64_t stride = static_cast<int64_t>(a.M) * a.N;
-  const float* p = a.part + static_cast<int64_t>(m) * a.N + n;
-  float y = 0.f;
-  for (int c = 0; c < a.kchunks; ++c) y += p[c * stride];
+#pragma unroll
+  for (int c = 0; c < 16; ++c) ssum += c < a.n_ss ? a.ss[c * 64 + m] : 0.f;  // n_ss <= 16 (hidden <= 4096)
+  float y = a.sums[static_cast<int64_t>(m) * a.N + n];
   const int offset = *a.offset_dev;
   const int pos = min(max(a.positions ? a.positions[m] : offset + m, 0), a.rope_max - 1);
   y *= 1.f / sqrtf(ssum / static_cast<float>(a.K) + a.eps);
@@ -329,9 +496,6 @@ __global__ __launch_bounds__(256) void k_mm_reduce_qkv(QkvEpiArgs a) {
 // the chunk's transposed V.  The next chunk's K / V and mask bytes load while
 // the current one is consumed.  Partial (m, l, o) per split (m in natural
 // units) go to k_attn_merge.
-typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
-typedef float af32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kVaCH = 64;            // keys per chunk
 constexpr int kVaLdK = kVaD + 8;     // row stride (bf16) of the K chunk: B-fragment reads spread over the banks
 constexpr int kVaLdT = kVaCH + 8;    // row stride (bf16) of the transposed V chunk
@@ -339,25 +503,6 @@ constexpr int kVaLdP = kVaCH + 4;    // row stride (fp32) of a wave's P tile
 constexpr int kVaGroup = 64;         // query vectors per block
 constexpr int kVaMaxRows = 64;       // rows per launch (mask rows staged per chunk)
 constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
-}
-
-// 8 fp32 -> bf16 hi (round to nearest) and lo (the rounding remainder, rounded):
-// hi + lo equals x to ~2^-17 relative, so bf16 MFMA products keep fp32 accuracy.
-__device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo) {
-  float r[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = x[e] - static_cast<float>(static_cast<__bf16>(x[e]));
-  const uint4 h = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]),
-                             pack2_bf16(x[6], x[7]));
-  const uint4 l = make_uint4(pack2_bf16(r[0], r[1]), pack2_bf16(r[2], r[3]), pack2_bf16(r[4], r[5]),
-                             pack2_bf16(r[6], r[7]));
-  hi = __builtin_bit_cast(abf16x8, h);
-  lo = __builtin_bit_cast(abf16x8, l);
-}
 
 struct VaChunk {
   uint4 k[4], v[4];
@@ -592,9 +737,21 @@ static int launch_verify_attention(const AttnArgs& a, int splits, hipStream_t s)
 }
 
 struct TargetWs {
-  float *qkv, *attn, *h1, *act, *part, *ss, *apart;
+  uint16_t *xa_x, *xa_attn, *xa_h1, *xa_act;
+  float *ss_x, *ss_h1, *qkv, *q, *attn, *h1, *part, *apart;
+  unsigned int* ctr;
   size_t bytes;
 };
+
+struct LayerPlans {
+  GemmPlan qkv, o, gu, down;
+};
+
+static LayerPlans layer_plans(const wc_drafter_dims& d) {
+  const int nq = d.heads * d.head_dim, nqkv = nq + 2 * d.kv_heads * d.head_dim;
+  return {plan_gemm(nqkv, d.hidden, false), plan_gemm(d.hidden, nq, false), plan_gemm(2 * d.inter, d.hidden, true),
+          plan_gemm(d.hidden, d.inter, false)};
+}
 
 static TargetWs target_ws(const wc_drafter_dims& d, int max_rows, void* base) {
   TargetWs w{};
@@ -603,21 +760,34 @@ static TargetWs target_ws(const wc_drafter_dims& d, int max_rows, void* base) {
   auto take = [&](size_t bytes) {
     char* q = p ? p + off : nullptr;
     off = (off + bytes + 255) / 256 * 256;
-    return reinterpret_cast<float*>(q);
+    return q;
   };
   const size_t M = static_cast<size_t>(max_rows);
-  const size_t nqkv = static_cast<size_t>(d.heads + 2 * d.kv_heads) * d.head_dim;
-  const size_t hd = static_cast<size_t>(d.heads) * d.head_dim;
-  const size_t kmax = std::max<size_t>(std::max<size_t>(d.hidden, hd), d.inter);
-  const size_t nmax = std::max<size_t>(std::max<size_t>(nqkv, 2 * static_cast<size_t>(d.inter)), d.hidden);
-  w.qkv = take(4 * M * nqkv);
-  w.attn = take(4 * M * hd);
-  w.h1 = take(4 * M * d.hidden);
-  w.act = take(4 * M * d.inter);
-  w.part = take(4 * (kmax / kMmKC) * M * nmax);
-  w.ss = take(4 * (kmax / kMmKC) * M);
+  const size_t nq = static_cast<size_t>(d.heads) * d.head_dim;
+  const size_t nqkv = nq + 2 * static_cast<size_t>(d.kv_heads) * d.head_dim;
+  const LayerPlans pl = layer_plans(d);
+  // activations in fragment order: K / 32 steps of 8 KB = 256 bytes per k
+  w.xa_x = reinterpret_cast<uint16_t*>(take(256 * static_cast<size_t>(d.hidden)));
+  w.xa_attn = reinterpret_cast<uint16_t*>(take(256 * nq));
+  w.xa_h1 = reinterpret_cast<uint16_t*>(take(256 * static_cast<size_t>(d.hidden)));
+  w.xa_act = reinterpret_cast<uint16_t*>(take(256 * static_cast<size_t>(d.inter)));
+  w.ss_x = reinterpret_cast<float*>(take(4 * 64 * static_cast<size_t>(std::max(d.hidden, 256) / 256)));
+  // o_proj epilogue parts (one per column range) or the fallback attention prep's (one per 256 k)
+  const size_t ss_parts = std::max(static_cast<size_t>(d.hidden / 64), nq / 256);
+  w.ss_h1 = reinterpret_cast<float*>(take(4 * 64 * ss_parts));
+  w.qkv = reinterpret_cast<float*>(take(4 * M * nqkv));
+  w.q = reinterpret_cast<float*>(take(4 * M * nq));
+  w.attn = reinterpret_cast<float*>(take(4 * M * nq));
+  w.h1 = reinterpret_cast<float*>(take(4 * M * d.hidden));
+  size_t part = 0, cols = 0;
+  for (const GemmPlan* g : {&pl.qkv, &pl.o, &pl.gu, &pl.down}) {
+    part = std::max(part, static_cast<size_t>(g->ks) * 64 * g->cols * 64 * g->tw);
+    cols = std::max(cols, static_cast<size_t>(g->cols));
+  }
+  w.part = reinterpret_cast<float*>(take(4 * part));
+  w.ctr = reinterpret_cast<unsigned int*>(take(4 * kSkCtrStride * cols));
   const size_t qv = M * static_cast<size_t>(d.heads / std::max(d.kv_heads, 1));
-  w.apart = take(4 * static_cast<size_t>(d.kv_heads) * kMaxSplits * qv * (d.head_dim + 2));
+  w.apart = reinterpret_cast<float*>(take(4 * static_cast<size_t>(d.kv_heads) * kMaxSplits * qv * (d.head_dim + 2)));
   w.bytes = off;
   return w;
 }
@@ -638,10 +808,12 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   using namespace wc;
   WC_REQUIRE(dims && L && x && k_cache && v_cache && offset_dev && workspace, "wc_target_layer: NULL argument");
   const wc_drafter_dims& d = *dims;
-  WC_REQUIRE(rows >= 1 && rows <= kMmMaxRows, "wc_target_layer: rows must be in 1..%d (got %d)", kMmMaxRows, rows);
+  WC_REQUIRE(rows >= 1 && rows <= 64, "wc_target_layer: rows must be in 1..64 (got %d)", rows);
   WC_REQUIRE(d.heads >= 1 && d.kv_heads >= 1 && d.heads % d.kv_heads == 0, "wc_target_layer: bad head counts");
-  WC_REQUIRE(d.hidden % kMmKC == 0 && (d.heads * d.head_dim) % kMmKC == 0 && d.inter % kMmKC == 0,
-             "wc_target_layer: hidden, heads*head_dim and inter must be multiples of %d", kMmKC);
+  WC_REQUIRE(d.hidden % 256 == 0 && (d.heads * d.head_dim) % 256 == 0 && d.inter % 256 == 0,
+             "wc_target_layer: hidden, heads*head_dim and inter must be multiples of 256");
+  WC_REQUIRE(d.head_dim % 32 == 0, "wc_target_layer: head_dim must be a multiple of 32");
+  WC_REQUIRE(d.hidden <= 4096, "wc_target_layer: hidden_size above 4096 is not supported");
   WC_REQUIRE(kv_dtype == WC_F32 || kv_dtype == WC_BF16, "wc_target_layer: kv_dtype must be WC_F32 or WC_BF16");
   WC_REQUIRE(L->in_norm && L->post_norm && L->q && L->k && L->v && L->o && L->q_norm && L->k_norm && L->gate &&
                  L->up && L->down,
@@ -654,14 +826,18 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   WC_REQUIRE(Hk <= kMaxKvHeads && rep <= kMaxQV, "wc_target_layer: head grouping not supported");
   const int nq = H * D, nk = Hk * D, nqkv = nq + 2 * nk;
   const TargetWs ws = target_ws(d, rows, workspace);
+  const LayerPlans pl = layer_plans(d);
   auto s = reinterpret_cast<hipStream_t>(stream);
   auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+  const bool verify_path = D == kVaD && kv_dtype == WC_BF16;
 
-  // 1. QKV = W . RMS_in(x)
-  MmArgs g{};
-  g.x = x;
-  g.ldx = d.hidden;
-  g.gain = u16(L->in_norm);
+  // 1. the layer input as activations: x * in_norm, row sums of squares
+  if (int rc = launch_xa_prep(x, d.hidden, rows, d.hidden, u16(L->in_norm), ws.xa_x, ws.ss_x, s)) return rc;
+
+  // 2. QKV = W . RMS_in(x): unscaled sums for the verify epilogue, scaled otherwise
+  SkArgs g{};
+  g.xa = ws.xa_x;
+  g.eps = d.eps;
   g.w[0] = u16(L->q);
   g.w[1] = u16(L->k);
   g.w[2] = u16(L->v);
@@ -673,35 +849,31 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.M = rows;
   g.N = nqkv;
   g.K = d.hidden;
-  g.kchunks = d.hidden / kMmKC;
+  g.epi = verify_path ? kSkRaw : kSkStore;
+  if (!verify_path) {
+    g.ss = ws.ss_x;
+    g.n_ss = d.hidden / 256;
+    g.ss_k = d.hidden;
+  }
+  g.out = ws.qkv;
+  g.ldo = nqkv;
   g.part = ws.part;
-  g.ss = ws.ss;
-  MmReduceArgs r{};
-  r.part = ws.part;
-  r.ss = ws.ss;
-  r.M = rows;
-  r.N = nqkv;
-  r.K = d.hidden;
-  r.kchunks = g.kchunks;
-  r.eps = d.eps;
-  r.epi = kMmStore;
-  r.out = ws.qkv;
-  r.ldo = nqkv;
+  g.ctr = ws.ctr;
+  if (int rc = launch_stream(g, pl.qkv, s)) return rc;
+
   const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunkMax - 1) / kAttnChunkMax));
-  // head_dim 128 with a bf16 cache: the QKV epilogue normalises / rotates q and
-  // k and appends K / V, then one MFMA attention launch covers every row
-  const bool verify_path = D == kVaD && kv_dtype == WC_BF16 && rows <= kVaMaxRows;
   if (verify_path) {
-    if (int rc = launch_mm_partial(g, s)) return rc;
+    // head_dim 128 with a bf16 cache: the QKV epilogue normalises / rotates q and
+    // k and appends K / V, then one MFMA attention launch covers every row
     QkvEpiArgs e{};
-    e.part = ws.part;
-    e.ss = ws.ss;
+    e.sums = ws.qkv;
+    e.ss = ws.ss_x;
     e.M = rows;
     e.N = nqkv;
     e.K = d.hidden;
-    e.kchunks = g.kchunks;
+    e.n_ss = d.hidden / 256;
     e.eps = d.eps;
-    e.q_out = ws.qkv;
+    e.q_out = ws.q;
     e.ldq = nq;
     e.nq = nq;
     e.nk = nk;
@@ -719,7 +891,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     hipLaunchKernelGGL(k_mm_reduce_qkv, dim3((nqkv + 255) / 256, rows), dim3(256), 0, s, e);
     WC_LAUNCHED();
     AttnArgs at{};
-    at.qkv = ws.qkv;
+    at.qkv = ws.q;
     at.ld_qkv = nq;
     at.H = H;
     at.Hk = Hk;
@@ -736,79 +908,75 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     at.qv_ld = rows * rep;
     at.out = ws.attn;
     at.ld_out = nq;
+    at.xa_out = ws.xa_attn;
     // about two chunks of keys per split
     const int vsplits = std::max(1, std::min(kMaxSplits, (capacity + 2 * kVaCH - 1) / (2 * kVaCH)));
     if (int rc = launch_verify_attention(at, vsplits, s)) return rc;
-  } else if (int rc = launch_mm(g, r, s)) {
-    return rc;
+  } else {
+    // other head sizes / an fp32 cache: the decode attention over tiles of rows
+    // whose query vectors fit one block (it normalises, rotates and appends on
+    // the fly), then the output as activations
+    const int tile = std::max(1, std::min(kMaxQV / rep, WC_MAX_NODES));
+    for (int t0 = 0; t0 < rows; t0 += tile) {
+      AttnArgs at{};
+      at.qkv = ws.qkv + static_cast<int64_t>(t0) * nqkv;
+      at.ld_qkv = nqkv;
+      at.H = H;
+      at.Hk = Hk;
+      at.rows = std::min(tile, rows - t0);
+      at.q_gain = u16(L->q_norm);
+      at.k_gain = u16(L->k_norm);
+      at.eps = d.eps;
+      at.scale = 1.f / sqrtf(static_cast<float>(D));
+      at.rope_cos = rope_cos;
+      at.rope_sin = rope_sin;
+      at.rope_max = rope_max_pos;
+      at.positions = positions_dev ? positions_dev + t0 : nullptr;
+      at.kc = k_cache;
+      at.vc = v_cache;
+      at.cap = capacity;
+      at.offset_dev = offset_dev;
+      at.offset_add = t0;
+      at.mask = mask_dev ? mask_dev + static_cast<int64_t>(t0) * mask_ld : nullptr;
+      at.mask_ld = mask_ld;
+      at.window = d.window;
+      at.partial = ws.apart;
+      at.qv_ld = std::min(tile, rows) * rep;
+      at.out = ws.attn + static_cast<int64_t>(t0) * nq;
+      at.ld_out = nq;
+      if (int rc = launch_attention(at, D, kv_dtype, splits, s)) return rc;
+    }
+    if (int rc = launch_xa_prep(ws.attn, nq, rows, nq, nullptr, ws.xa_attn, ws.ss_h1, s)) return rc;
   }
 
-  // 2. (other head sizes / fp32 cache) attention with the decode kernel over
-  //    tiles of rows whose query vectors fit one block; it normalises, rotates
-  //    and appends on the fly
-  const int tile = verify_path ? rows : std::max(1, std::min(kMaxQV / rep, WC_MAX_NODES));
-  for (int t0 = 0; t0 < rows && !verify_path; t0 += tile) {
-    AttnArgs at{};
-    at.qkv = ws.qkv + static_cast<int64_t>(t0) * nqkv;
-    at.ld_qkv = nqkv;
-    at.H = H;
-    at.Hk = Hk;
-    at.rows = std::min(tile, rows - t0);
-    at.n_rows_dev = nullptr;
-    at.q_gain = u16(L->q_norm);
-    at.k_gain = u16(L->k_norm);
-    at.eps = d.eps;
-    at.scale = 1.f / sqrtf(static_cast<float>(D));
-    at.rope_cos = rope_cos;
-    at.rope_sin = rope_sin;
-    at.rope_max = rope_max_pos;
-    at.positions = positions_dev ? positions_dev + t0 : nullptr;
-    at.kc = k_cache;
-    at.vc = v_cache;
-    at.cap = capacity;
-    at.offset_dev = offset_dev;
-    at.offset_add = t0;
-    at.mask = mask_dev ? mask_dev + static_cast<int64_t>(t0) * mask_ld : nullptr;
-    at.mask_ld = mask_ld;
-    at.window = d.window;
-    at.partial = ws.apart;
-    at.qv_ld = std::min(tile, rows) * rep;
-    at.out = ws.attn + static_cast<int64_t>(t0) * nq;
-    at.ld_out = nq;
-    if (int rc = launch_attention(at, D, kv_dtype, splits, s)) return rc;
-  }
-
-  // 3. h1 = x + W_o . attn
-  g = MmArgs{};
-  g.x = ws.attn;
-  g.ldx = nq;
+  // 3. h1 = x + W_o . attn; the epilogue also writes h1 * post_norm as activations
+  g = SkArgs{};
+  g.xa = ws.xa_attn;
   g.w[0] = u16(L->o);
   g.seg_start[1] = d.hidden;
   g.n_seg = 1;
   g.M = rows;
   g.N = d.hidden;
   g.K = nq;
-  g.kchunks = nq / kMmKC;
+  g.epi = kSkResidual;
+  g.out = ws.h1;
+  g.ldo = d.hidden;
+  g.res = x;
+  g.ldr = d.hidden;
+  g.xa_next = ws.xa_h1;
+  g.gain_next = u16(L->post_norm);
+  g.ss_next = ws.ss_h1;
   g.part = ws.part;
-  g.ss = ws.ss;
-  r = MmReduceArgs{};
-  r.part = ws.part;
-  r.M = rows;
-  r.N = d.hidden;
-  r.K = nq;
-  r.kchunks = g.kchunks;
-  r.epi = kMmResidual;
-  r.out = ws.h1;
-  r.ldo = d.hidden;
-  r.res = x;
-  r.ldr = d.hidden;
-  if (int rc = launch_mm(g, r, s)) return rc;
+  g.ctr = ws.ctr;
+  if (int rc = launch_stream(g, pl.o, s)) return rc;
 
-  // 4. act = silu(W_gate . RMS_post(h1)) * (W_up . RMS_post(h1))
-  g = MmArgs{};
-  g.x = ws.h1;
-  g.ldx = d.hidden;
-  g.gain = u16(L->post_norm);
+  // 4. act = silu(W_gate . RMS_post(h1)) * (W_up . RMS_post(h1)), as activations only
+  g = SkArgs{};
+  g.xa = ws.xa_h1;
+  g.ss = ws.ss_h1;
+  g.n_ss = pl.o.cols;
+  g.ss_k = d.hidden;
+  g.eps = d.eps;
   g.w[0] = u16(L->gate);
   g.w[1] = u16(L->up);
   g.seg_start[1] = d.inter;
@@ -817,47 +985,29 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.M = rows;
   g.N = 2 * d.inter;
   g.K = d.hidden;
-  g.kchunks = d.hidden / kMmKC;
+  g.epi = kSkSiluPair;
+  g.xa_next = ws.xa_act;
   g.part = ws.part;
-  g.ss = ws.ss;
-  r = MmReduceArgs{};
-  r.part = ws.part;
-  r.ss = ws.ss;
-  r.M = rows;
-  r.N = 2 * d.inter;
-  r.K = d.hidden;
-  r.kchunks = g.kchunks;
-  r.eps = d.eps;
-  r.epi = kMmSiluPair;
-  r.out = ws.act;
-  r.ldo = d.inter;
-  if (int rc = launch_mm(g, r, s)) return rc;
+  g.ctr = ws.ctr;
+  if (int rc = launch_stream(g, pl.gu, s)) return rc;
 
   // 5. x = h1 + W_down . act
-  g = MmArgs{};
-  g.x = ws.act;
-  g.ldx = d.inter;
+  g = SkArgs{};
+  g.xa = ws.xa_act;
   g.w[0] = u16(L->down);
   g.seg_start[1] = d.hidden;
   g.n_seg = 1;
   g.M = rows;
   g.N = d.hidden;
   g.K = d.inter;
-  g.kchunks = d.inter / kMmKC;
+  g.epi = kSkResidual;
+  g.out = x;
+  g.ldo = d.hidden;
+  g.res = ws.h1;
+  g.ldr = d.hidden;
   g.part = ws.part;
-  g.ss = ws.ss;
-  r = MmReduceArgs{};
-  r.part = ws.part;
-  r.M = rows;
-  r.N = d.hidden;
-  r.K = d.inter;
-  r.kchunks = g.kchunks;
-  r.epi = kMmResidual;
-  r.out = x;
-  r.ldo = d.hidden;
-  r.res = ws.h1;
-  r.ldr = d.hidden;
-  return launch_mm(g, r, s);
+  g.ctr = ws.ctr;
+  return launch_stream(g, pl.down, s);
 }
 
 }  // extern "C"

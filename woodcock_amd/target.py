@@ -88,7 +88,7 @@ class TargetLayer:
                                      cfg.intermediate_size, cfg.hidden_size, 3, 1, 1, cfg.rms_norm_eps, 0)
         self.max_rows = max_rows
         n = _lib.lib().wc_target_workspace_bytes(C.byref(self.dims), max_rows)
-        self.ws = torch.empty(n, dtype=torch.uint8, device=self.device)
+        self.ws = torch.zeros(n, dtype=torch.uint8, device=self.device)  # split-K counters start at zero
         self._rope: tuple[torch.Tensor, torch.Tensor] | None = None
 
     def rope(self, positions: int) -> tuple[torch.Tensor, torch.Tensor]:
