@@ -312,6 +312,21 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
                     const uint8_t* mask_dev, int64_t mask_ld, void* k_cache, void* v_cache, int kv_dtype,
                     int capacity, const int32_t* offset_dev, void* workspace, wc_stream_t stream);
 
+/* Embedding rows of the target model for a verify block: out [rows][ld] fp32 =
+ * table [vocab][hidden] bf16 at tokens_dev [rows] (ids clamped into the table).
+ * Replaces Target.embed (python/woodcock/target.py:70-71). */
+int wc_target_embed(const void* table, int vocab, int hidden, const int32_t* tokens_dev, int rows, float* out,
+                    int64_t ld, wc_stream_t stream);
+
+/* Target logits of a verify block: logits_out [rows][ld] fp32 =
+ * RMSNorm(x; final_norm) . head_w^T, head_w [vocab][hidden] bf16 (the tied
+ * embedding for Qwen3), rows <= 64, as a streaming MFMA GEMM with the
+ * activations split into bf16 hi + lo (fp32-level products).  Workspace: the
+ * target-layer workspace for >= rows rows.  Replaces
+ * Target.lm_head(model.norm(h)) (python/woodcock/target.py:73-76,113-114). */
+int wc_target_head(const wc_drafter_dims* dims, const void* head_w, const void* final_norm, const float* x, int rows,
+                   int vocab, float* logits_out, int64_t ld, void* workspace, wc_stream_t stream);
+
 /* wc_draft_head for one pre-norm hidden row: the final RMSNorm is applied on the
  * fly (out = RMSNorm(hidden), drafter.py:190) and, when out_norm is not NULL,
  * written to out_norm at the same row index (*row_dev + row_add, or 0) -- the

@@ -298,7 +298,7 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
   }
 #pragma unroll
   for (int c = 0; c < CQ; ++c) {
-    resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + n0 + c] : 0.f;
+    resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + min(n0 + c, a.N - 1)] : 0.f;
     gnv[c] = (a.xa_next && a.gain_next && (!pair || c < 16)) ? a.gain_next[n0 + min(c, pair ? 15 : CQ - 1)] : 0;
   }
   {
@@ -336,8 +336,14 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
     }
     if (a.out) {
       float* op = a.out + static_cast<int64_t>(m) * a.ldo + n0 + c0;
+      if (pair || n0 + c0 + 8 <= a.N) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) op[e] = z[e];
+        for (int e = 0; e < 8; ++e) op[e] = z[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (n0 + c0 + e < a.N) op[e] = z[e];
+      }
     }
     if (a.xa_next) {
 #pragma unroll
@@ -369,7 +375,7 @@ struct GemmPlan {
 static GemmPlan plan_gemm(int n_rows, int K, bool pair) {
   GemmPlan p{};
   p.tw = (pair || n_rows >= 8192) ? 2 : 1;
-  p.cols = pair ? n_rows / 2 / 64 : n_rows / (64 * p.tw);
+  p.cols = pair ? n_rows / 2 / 64 : (n_rows + 64 * p.tw - 1) / (64 * p.tw);
   const int steps = K / 32;
   p.ks = std::max(1, std::min(std::min(6, steps / 16), (224 + p.cols - 1) / p.cols));
   return p;
@@ -736,6 +742,18 @@ static int launch_verify_attention(const AttnArgs& a, int splits, hipStream_t s)
   return WC_OK;
 }
 
+// ------------------------------------------------------------------ embedding
+// out[m] = table[tokens[m]] (bf16 -> fp32), token ids clamped into the table
+// (python/woodcock/target.py:70-71).
+__global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__ table, int vocab, int hidden,
+                                                    const int32_t* __restrict__ tokens, float* __restrict__ out,
+                                                    int64_t ld) {
+  const int m = blockIdx.x;
+  const int tok = min(max(tokens[m], 0), vocab - 1);
+  const uint16_t* src = table + static_cast<int64_t>(tok) * hidden;
+  for (int k = threadIdx.x; k < hidden; k += 256) out[static_cast<int64_t>(m) * ld + k] = bf16_to_float(src[k]);
+}
+
 struct TargetWs {
   uint16_t *xa_x, *xa_attn, *xa_h1, *xa_act;
   float *ss_x, *ss_h1, *qkv, *q, *attn, *h1, *part, *apart;
@@ -1008,6 +1026,52 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.part = ws.part;
   g.ctr = ws.ctr;
   return launch_stream(g, pl.down, s);
+}
+
+int wc_target_embed(const void* table, int vocab, int hidden, const int32_t* tokens_dev, int rows, float* out,
+                    int64_t ld, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(table && tokens_dev && out, "wc_target_embed: NULL buffer");
+  WC_REQUIRE(rows >= 1 && vocab >= 1 && hidden >= 1 && ld >= hidden, "wc_target_embed: bad sizes");
+  hipLaunchKernelGGL(k_embed_rows, dim3(rows), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(table), vocab, hidden, tokens_dev, out, ld);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_target_head(const wc_drafter_dims* dims, const void* head_w, const void* final_norm, const float* x, int rows,
+                   int vocab, float* logits_out, int64_t ld, void* workspace, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(dims && head_w && final_norm && x && logits_out && workspace, "wc_target_head: NULL argument");
+  const wc_drafter_dims& d = *dims;
+  WC_REQUIRE(rows >= 1 && rows <= 64, "wc_target_head: rows must be in 1..64 (got %d)", rows);
+  WC_REQUIRE(d.hidden % 256 == 0 && d.hidden <= 4096, "wc_target_head: hidden_size must be a multiple of 256, <= 4096");
+  WC_REQUIRE(vocab >= 1 && ld >= vocab, "wc_target_head: logits row stride smaller than the vocabulary");
+  WC_REQUIRE(aligned(head_w, 16) && aligned(x, 16) && aligned(workspace, 16), "wc_target_head: misaligned buffer");
+  const TargetWs ws = target_ws(d, rows, workspace);
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  // final RMSNorm folded in: x * gain as activations, 1/rms scales the logits
+  if (int rc = launch_xa_prep(x, d.hidden, rows, d.hidden, static_cast<const uint16_t*>(final_norm), ws.xa_x,
+                              ws.ss_x, s))
+    return rc;
+  GemmPlan p = plan_gemm(vocab, d.hidden, false);
+  p.ks = 1;  // one column range per block: the vocabulary fills the GPU
+  SkArgs g{};
+  g.xa = ws.xa_x;
+  g.ss = ws.ss_x;
+  g.n_ss = d.hidden / 256;
+  g.ss_k = d.hidden;
+  g.eps = d.eps;
+  g.w[0] = static_cast<const uint16_t*>(head_w);
+  g.seg_start[1] = vocab;
+  g.n_seg = 1;
+  g.M = rows;
+  g.N = vocab;
+  g.K = d.hidden;
+  g.epi = kSkStore;
+  g.out = logits_out;
+  g.ldo = ld;
+  return launch_stream(g, p, s);
 }
 
 }  // extern "C"

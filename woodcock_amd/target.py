@@ -1,10 +1,14 @@
-"""Verify-width target forward, one decoder layer at a time (python/woodcock/target.py).
+"""Verify-width target forward (python/woodcock/target.py).
 
 ``TargetLayer`` holds one Qwen3 decoder layer's device weights (the reference's
 parameter names, python/woodcock/target.py:142-156 / mlx-lm Qwen3) and runs
 ``wc_target_layer`` over a verify block of up to 64 rows: the tree or chain
-block at explicit positions with an explicit mask (target.py:82-116).  The
-embedding, the final norm and the LM head of the target are the caller's.
+block at explicit positions with an explicit mask (target.py:82-116).
+``TargetModel`` is the whole forward of ``Target.__call__`` (target.py:82-116):
+embedding rows, every decoder layer, the feature taps at ``feature_layers``
+(target.py:26-32,108-111) and the tied LM head over the final norm
+(target.py:73-76,113-114) -- all device-side, one workspace and RoPE table
+shared by the layers.
 """
 from __future__ import annotations
 
@@ -47,6 +51,8 @@ class TargetConfig:
     rms_norm_eps: float = 1e-6
     rope_theta: float = 1e6
     num_layers: int = 28
+    vocab_size: int = 151936
+    tie_word_embeddings: bool = True
 
 
 def layer_shapes(cfg: TargetConfig) -> dict[str, tuple[int, ...]]:
@@ -124,3 +130,126 @@ class TargetLayer:
                   _lib.WC_BF16 if cache.keys.dtype == torch.bfloat16 else _lib.WC_F32, cache.capacity,
                   ptr(offset_dev), ptr(self.ws), stream_ptr())
         return x
+
+
+def default_feature_layers(num_layers: int) -> tuple[int, int, int]:
+    """Low / mid / high taps (python/woodcock/target.py:26-32)."""
+    return (2, num_layers // 2, num_layers - 3)
+
+
+def random_target(cfg: TargetConfig, seed: int = 0, device="cuda", std: float = 0.02) -> dict[str, torch.Tensor]:
+    """Random-init weights of the whole target under the reference's names."""
+    out = {}
+    for i in range(cfg.num_layers):
+        for name, t in random_layer(cfg, seed=seed * 1000 + i, device=device, std=std).items():
+            out[f"layers.{i}.{name}"] = t
+    g = torch.Generator(device=device)
+    g.manual_seed(seed + 17)
+    out["embed_tokens.weight"] = (std * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g,
+                                                    device=device)).to(torch.bfloat16)
+    out["norm.weight"] = (1.0 + 0.1 * torch.randn(cfg.hidden_size, generator=g, device=device)).to(torch.bfloat16)
+    if not cfg.tie_word_embeddings:
+        out["lm_head.weight"] = (std * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g,
+                                                   device=device)).to(torch.bfloat16)
+    return out
+
+
+class TargetModel:
+    """The verify forward of the target over a block of up to 64 rows."""
+
+    def __init__(self, cfg: TargetConfig, weights: dict[str, torch.Tensor], device="cuda", max_rows: int = MAX_ROWS,
+                 feature_layers: tuple[int, ...] | None = None):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.feature_layers = tuple(feature_layers or default_feature_layers(cfg.num_layers))
+        shapes = layer_shapes(cfg)
+        self.w: dict[str, torch.Tensor] = {}
+        self.lw = []
+        for i in range(cfg.num_layers):
+            lw = _lib.LayerWeights()
+            for f, name in LAYER_NAMES.items():
+                t = weights[f"layers.{i}.{name}"]
+                if tuple(t.shape) != shapes[name]:
+                    raise ValueError(f"layers.{i}.{name}: shape {tuple(t.shape)}, expected {shapes[name]}")
+                t = t.to(self.device, torch.bfloat16).contiguous()
+                self.w[f"layers.{i}.{name}"] = t
+                setattr(lw, f, ptr(t))
+            self.lw.append(lw)
+        for name, shape in (("embed_tokens.weight", (cfg.vocab_size, cfg.hidden_size)),
+                            ("norm.weight", (cfg.hidden_size,))):
+            t = weights[name]
+            if tuple(t.shape) != shape:
+                raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {shape}")
+            self.w[name] = t.to(self.device, torch.bfloat16).contiguous()
+        head = "embed_tokens.weight" if cfg.tie_word_embeddings else "lm_head.weight"
+        if head not in self.w:
+            self.w[head] = weights[head].to(self.device, torch.bfloat16).contiguous()
+        self.head = self.w[head]
+        self.dims = _lib.DrafterDims(cfg.hidden_size, 1, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+                                     cfg.intermediate_size, cfg.hidden_size, 3, 1, 1, cfg.rms_norm_eps, 0)
+        self.max_rows = max_rows
+        n = _lib.lib().wc_target_workspace_bytes(C.byref(self.dims), max_rows)
+        self.ws = torch.zeros(n, dtype=torch.uint8, device=self.device)  # split-K counters start at zero
+        self._rope: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.x = torch.empty(max_rows, cfg.hidden_size, dtype=torch.float32, device=self.device)
+
+    def make_cache(self, capacity: int, dtype=torch.bfloat16) -> list[KVCache]:
+        return [KVCache(self.cfg.num_kv_heads, self.cfg.head_dim, capacity, dtype, self.device)
+                for _ in range(self.cfg.num_layers)]
+
+    def rope(self, positions: int) -> tuple[torch.Tensor, torch.Tensor]:
+        if self._rope is None or self._rope[0].shape[0] < positions:
+            n = max(positions, 64)
+            half = self.cfg.head_dim // 2
+            cos = np.empty((n, half), np.float32)
+            sin = np.empty_like(cos)
+            _lib.call("wc_rope_table", cos.ctypes.data_as(C.c_void_p), sin.ctypes.data_as(C.c_void_p), n,
+                      self.cfg.head_dim, float(self.cfg.rope_theta))
+            self._rope = (torch.from_numpy(cos).to(self.device), torch.from_numpy(sin).to(self.device))
+        return self._rope
+
+    def __call__(self, tokens: torch.Tensor, cache: list[KVCache], offset_dev: torch.Tensor,
+                 positions: torch.Tensor | None = None, mask: torch.Tensor | None = None,
+                 logits: torch.Tensor | None = None, taps: list[torch.Tensor] | None = None
+                 ) -> tuple[torch.Tensor, list[torch.Tensor]]:
+        """tokens [rows] int32 on the device -> (logits [rows, vocab] fp32, feature taps
+        [rows, hidden] fp32 at feature_layers).  K/V of the block land at cache slots
+        *offset_dev .. + rows of every layer (the caller advances the offsets);
+        enqueue only, no host synchronisation."""
+        cfg = self.cfg
+        rows = tokens.numel()
+        if not 1 <= rows <= self.max_rows:
+            raise ValueError(f"rows must be in 1..{self.max_rows}")
+        if len(cache) != cfg.num_layers:
+            raise ValueError(f"{cfg.num_layers} cache layers needed, got {len(cache)}")
+        cap = cache[0].capacity
+        cos, sin = self.rope(cap + 64)
+        pos = None if positions is None else positions.to(self.device, torch.int32).contiguous()
+        if mask is not None:
+            mask = mask.to(self.device, torch.uint8).contiguous()
+            if mask.shape[0] != rows:
+                raise ValueError("mask must have one row per token")
+        kvdt = _lib.WC_BF16 if cache[0].keys.dtype == torch.bfloat16 else _lib.WC_F32
+        x = self.x[:rows]
+        s = stream_ptr()
+        tok = tokens.to(self.device, torch.int32).contiguous()
+        _lib.call("wc_target_embed", ptr(self.w["embed_tokens.weight"]), cfg.vocab_size, cfg.hidden_size, ptr(tok),
+                  rows, ptr(x), x.stride(0), s)
+        if taps is None:
+            taps = [torch.empty(rows, cfg.hidden_size, dtype=torch.float32, device=self.device)
+                    for _ in self.feature_layers]
+        for i in range(cfg.num_layers):
+            c = cache[i]
+            _lib.call("wc_target_layer", C.byref(self.dims), C.byref(self.lw[i]), ptr(cos), ptr(sin), cos.shape[0],
+                      ptr(x), rows, ptr(pos) if pos is not None else None, ptr(mask) if mask is not None else None,
+                      mask.stride(0) if mask is not None else 0, ptr(c.keys), ptr(c.values), kvdt, c.capacity,
+                      ptr(offset_dev), ptr(self.ws), s)
+            for j, f in enumerate(self.feature_layers):
+                if f == i:
+                    taps[j][:rows].copy_(x)
+        if logits is None:
+            logits = torch.empty(rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
+        _lib.call("wc_target_head", C.byref(self.dims), ptr(self.head), ptr(self.w["norm.weight"]), ptr(x), rows,
+                  cfg.vocab_size, ptr(logits), logits.stride(0), ptr(self.ws), s)
+        return logits, taps
+
