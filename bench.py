@@ -296,10 +296,34 @@ def bench_gpu(args):
             _lib.call("wc_verify_tree_greedy", ptr(tlog), 60, cfg.vocab_size, tlog.stride(0), ptr(ttok), ptr(tpar),
                       ptr(vverd), ptr(rnd.vws), s())
 
+    # the whole verify forward of a 28-layer Qwen3-1.7B target (random weights):
+    # embedding, layers with the feature taps, final norm + tied head; the chain
+    # block (5 rows, causal, context 512) and the 60-node tree block (context 2048)
+    from woodcock_amd.target import TargetModel, random_target
+
+    tm = TargetModel(tcfg, random_target(tcfg, seed=args.seed + 5, device=out1.device), out1.device, max_rows=60)
+    tm_cache = tm.make_cache(2048 + 64)
+    for c in tm_cache:
+        c.keys.normal_()
+        c.values.normal_()
+    tm_tok5 = torch.randint(0, tcfg.vocab_size, (5,), dtype=torch.int32, device=out1.device)
+    tm_tok60 = torch.tensor(tree.tokens, dtype=torch.int32, device=out1.device)
+    tm_off512 = torch.tensor([512], dtype=torch.int32, device=out1.device)
+    tm_logits = torch.empty(60, tcfg.vocab_size, device=out1.device)
+    tm_taps = [torch.empty(60, tcfg.hidden_size, device=out1.device) for _ in tm.feature_layers]
+    tm(tm_tok5, tm_cache, tm_off512, logits=tm_logits[:5], taps=tm_taps)
+
+    def target_chain():
+        tm(tm_tok5, tm_cache, tm_off512, logits=tm_logits[:5], taps=tm_taps)
+
+    def target_tree():
+        tm(tm_tok60, tm_cache, toff, tpos, tmask, logits=tm_logits, taps=tm_taps)
+
     comps = {}
-    reps = {"target_layer": REP // 4}
+    reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1}
     for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
-                     ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies)):
+                     ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies),
+                     ("target_chain", target_chain), ("target_tree", target_tree)):
         fn()
         torch.cuda.synchronize()
         g = capture(fn)
@@ -326,6 +350,8 @@ def bench_gpu(args):
         "stochastic_us": comps["stochastic"],
         "target_layer_us": comps["target_layer"],
         "tree_verify_us": comps["tree_verify"],
+        "target_chain_us": comps["target_chain"],
+        "target_tree_us": comps["target_tree"],
         "head_bytes": head_bytes,
         "step_bytes": step_bytes,
         "compact_bytes_avg": compact_bytes,
@@ -581,6 +607,8 @@ def main():
             "target_layer_us_qwen3_1p7b_m60_ctx2048": round(r["target_layer_us"], 2),
             "target_layer_hbm_frac_m60": round(100_663_296 / (r["target_layer_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "verify_tree_greedy_us_n60": round(r["tree_verify_us"], 2),
+            "target_forward_us_qwen3_1p7b_28l_m5_ctx512": round(r["target_chain_us"], 1),
+            "target_forward_us_qwen3_1p7b_28l_m60_tree_ctx2048": round(r["target_tree_us"], 1),
             "head_gemv_us": round(r["head_us"], 2),
         },
         "roofline": {

@@ -304,13 +304,19 @@ size_t wc_target_workspace_bytes(const wc_drafter_dims* dims, int max_rows);
  * The caller advances the offset after the last layer.  dims supplies hidden,
  * heads, kv_heads, head_dim, inter, eps and window; hidden, heads*head_dim and
  * inter must be multiples of 256; the aux fields of L are ignored.
+ * Layer chaining: with next_norm (bf16 [hidden], the next layer's in_norm or
+ * the final norm) the layer also leaves next_norm * x_out and the partial row
+ * sums of squares of x_out in the workspace, and the next call (or
+ * wc_target_head) given input_prepared = 1 and the same workspace starts from
+ * them instead of preparing x itself.
  * Replaces _block_forward (python/woodcock/target.py:142-156) as called by
  * Target.__call__ with positions and a mask (target.py:82-116), and the layer
  * loop of Qwen3::forward (src/core/qwen3.cpp:86-111). */
 int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, const float* rope_cos,
                     const float* rope_sin, int rope_max_pos, float* x, int rows, const int32_t* positions_dev,
                     const uint8_t* mask_dev, int64_t mask_ld, void* k_cache, void* v_cache, int kv_dtype,
-                    int capacity, const int32_t* offset_dev, void* workspace, wc_stream_t stream);
+                    int capacity, const int32_t* offset_dev, const void* next_norm, int input_prepared,
+                    void* workspace, wc_stream_t stream);
 
 /* Embedding rows of the target model for a verify block: out [rows][ld] fp32 =
  * table [vocab][hidden] bf16 at tokens_dev [rows] (ids clamped into the table).
@@ -322,10 +328,12 @@ int wc_target_embed(const void* table, int vocab, int hidden, const int32_t* tok
  * RMSNorm(x; final_norm) . head_w^T, head_w [vocab][hidden] bf16 (the tied
  * embedding for Qwen3), rows <= 64, as a streaming MFMA GEMM with the
  * activations split into bf16 hi + lo (fp32-level products).  Workspace: the
- * target-layer workspace for >= rows rows.  Replaces
+ * target-layer workspace for >= rows rows; input_prepared = 1 when the last
+ * wc_target_layer call on it had next_norm = final_norm.  Replaces
  * Target.lm_head(model.norm(h)) (python/woodcock/target.py:73-76,113-114). */
 int wc_target_head(const wc_drafter_dims* dims, const void* head_w, const void* final_norm, const float* x, int rows,
-                   int vocab, float* logits_out, int64_t ld, void* workspace, wc_stream_t stream);
+                   int vocab, float* logits_out, int64_t ld, int input_prepared, void* workspace,
+                   wc_stream_t stream);
 
 /* wc_draft_head for one pre-norm hidden row: the final RMSNorm is applied on the
  * fly (out = RMSNorm(hidden), drafter.py:190) and, when out_norm is not NULL,

@@ -109,8 +109,9 @@ _SIGS = {
     "wc_draft_head_norm": ([P, P, P, I64, P, C.c_int, P, I64, P, I64, P, P, P, P, P], C.c_int),
     "wc_target_workspace_bytes": ([P, C.c_int], C.c_size_t),
     "wc_target_embed": ([P, C.c_int, C.c_int, P, C.c_int, P, I64, P], C.c_int),
-    "wc_target_head": ([P, P, P, P, C.c_int, C.c_int, P, I64, P, P], C.c_int),
-    "wc_target_layer": ([P, P, P, P, C.c_int, P, C.c_int, P, P, I64, P, P, C.c_int, C.c_int, P, P, P], C.c_int),
+    "wc_target_head": ([P, P, P, P, C.c_int, C.c_int, P, I64, C.c_int, P, P], C.c_int),
+    "wc_target_layer": ([P, P, P, P, C.c_int, P, C.c_int, P, P, I64, P, P, C.c_int, C.c_int, P, P, C.c_int, P, P],
+                        C.c_int),
 }
 
 _lib = None

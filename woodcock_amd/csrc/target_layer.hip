@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void k_xa_prep(XaPrepArgs a) {
 
 // ------------------------------------------------------------------ streaming skinny GEMM
 
-enum SkEpi { kSkRaw = 0, kSkStore = 1, kSkResidual = 2, kSkSiluPair = 3 };
+enum SkEpi { kSkRaw = 0, kSkStore = 1, kSkResidual = 2, kSkSiluPair = 3, kSkQkvHead = 4 };
 constexpr int kSkMaxSeg = 3;
 constexpr int kSkP = 8;            // k steps of weights / activations in flight
 constexpr int kSkCtrStride = 32;   // one 128-byte line per column-range counter
@@ -126,6 +126,17 @@ struct SkArgs {
   float* ss_next;            // with xa_next: per-row sums of squares of the output, [gridDim.x][64]
   float* part;               // ks > 1: [ks][64][cols] partials
   unsigned int* ctr;         // ks > 1: one counter per column range
+  // kSkQkvHead (column ranges of one 128-wide head): q / k heads get their
+  // RMSNorm (q_gain / k_gain) and rotate-half RoPE at the row's position; q
+  // rows land in out [M][ldo], k / v rows in the cache at slot offset + row
+  int nq, nk;
+  const uint16_t *q_gain, *k_gain;
+  const float *rope_cos, *rope_sin;
+  int rope_max;
+  const int32_t* positions;  // [M] or NULL: offset + row
+  const int32_t* offset_dev;
+  void *kc, *vc;  // [Hk][cap][128]
+  int kv_bf16, cap;
 };
 
 // Block (column range cb, K split kz), 4 waves.  TW = tiles of 16 weight rows
@@ -310,6 +321,70 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
     if (g == 0) s_inv[m] = a.ss ? 1.f / sqrtf(tot / static_cast<float>(a.ss_k) + a.eps) : 1.f;
   }
   __syncthreads();
+  if (a.epi == kSkQkvHead) {
+    // one head per column range: RMS_in scale, then for q / k heads the per-head
+    // RMSNorm (q_norm / k_norm gains) and rotate-half RoPE at the row's position
+    // (src/backends/cpu_ops.cpp:61-77), in the order x1 = x inv g,
+    // lo' = x1 c - x2 s, hi' = x2 c + x1 s.  q lands in out; K and V rows go
+    // straight to the cache at slot offset + row, so the attention that follows
+    // reads every key, old or new, from the cache.
+    const int col0 = cb * FB, d0 = g * CQ;
+    const bool is_q = col0 < a.nq, is_k = !is_q && col0 < a.nq + a.nk;
+    const float inv = s_inv[m];
+    float y[CQ];
+    float hs = 0.f;
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) {
+      y[c] = s_c[m * LDC + d0 + c] * inv;
+      hs = fmaf(y[c], y[c], hs);
+    }
+    hs += __shfl_xor(hs, 1);
+    hs += __shfl_xor(hs, 2);
+    const int offset = *a.offset_dev;
+    if (is_q || is_k) {
+      const float invh = 1.f / sqrtf(hs / static_cast<float>(FB) + a.eps);
+      const uint16_t* gain = is_q ? a.q_gain : a.k_gain;
+#pragma unroll
+      for (int c = 0; c < CQ; ++c) {
+        y[c] = y[c] * invh * bf16_to_float(gain[d0 + c]);
+        s_c[m * LDC + d0 + c] = y[c];
+      }
+    }
+    __syncthreads();
+    if (m >= a.M) return;
+    const int pos = min(max(a.positions ? a.positions[m] : offset + m, 0), a.rope_max - 1);
+    if (is_q || is_k) {
+#pragma unroll
+      for (int c = 0; c < CQ; ++c) {
+        const int dd = d0 + c, pi = dd % (FB / 2);
+        const float xp = s_c[m * LDC + (dd ^ (FB / 2))];
+        const float cs = a.rope_cos[static_cast<int64_t>(pos) * (FB / 2) + pi];
+        const float sn = a.rope_sin[static_cast<int64_t>(pos) * (FB / 2) + pi];
+        y[c] = dd < FB / 2 ? y[c] * cs - xp * sn : y[c] * cs + xp * sn;
+      }
+    }
+    if (is_q) {
+      float* op = a.out + static_cast<int64_t>(m) * a.ldo + col0 + d0;
+#pragma unroll
+      for (int c = 0; c < CQ; ++c) op[c] = y[c];
+      return;
+    }
+    const int slot = offset + m;
+    if (slot < 0 || slot >= a.cap) return;
+    const int head = is_k ? (col0 - a.nq) / FB : (col0 - a.nq - a.nk) / FB;
+    const int64_t at = (static_cast<int64_t>(head) * a.cap + slot) * FB + d0;
+    void* base = is_k ? a.kc : a.vc;
+    if (a.kv_bf16) {
+      uint16_t* dst = static_cast<uint16_t*>(base) + at;
+#pragma unroll
+      for (int c = 0; c < CQ; ++c) dst[c] = float_to_bf16(y[c]);
+    } else {
+      float* dst = static_cast<float*>(base) + at;
+#pragma unroll
+      for (int c = 0; c < CQ; ++c) dst[c] = y[c];
+    }
+    return;
+  }
   if (m >= a.M) return;
   const float inv = s_inv[m];
   // this thread's outputs: 8-wide groups of consecutive output columns
@@ -372,9 +447,9 @@ struct GemmPlan {
 // projections), K split into at most 6 parts so that about 192-256 blocks run
 // with >= 16 k steps each (split-K partials cost 8 ks M bytes per weight row
 // against 2 K bytes of weights).
-static GemmPlan plan_gemm(int n_rows, int K, bool pair) {
+static GemmPlan plan_gemm(int n_rows, int K, bool pair, int tw = 0) {
   GemmPlan p{};
-  p.tw = (pair || n_rows >= 8192) ? 2 : 1;
+  p.tw = tw ? tw : (pair || n_rows >= 8192) ? 2 : 1;
   p.cols = pair ? n_rows / 2 / 64 : (n_rows + 64 * p.tw - 1) / (64 * p.tw);
   const int steps = K / 32;
   p.ks = std::max(1, std::min(std::min(6, steps / 16), (224 + p.cols - 1) / p.cols));
@@ -410,85 +485,7 @@ static int launch_xa_prep(const float* x, int64_t ldx, int M, int K, const uint1
   return WC_OK;
 }
 
-// ------------------------------------------------------------------ QKV epilogue
-// The QKV projection's epilogue, for head_dim 128: per (row, 256 output
-// features = two heads) it applies RMS_in to the projection sums, then for q and k
-// heads the per-head RMSNorm (q_norm / k_norm gains) and rotate-half RoPE at
-// the row's position (src/backends/cpu_ops.cpp:61-77), in the order
-// x1 = x inv g, lo' = x1 c - x2 s, hi' = x2 c + x1 s.  q lands in q_out; the
-// block's K and V rows go straight to the cache at slot offset + row, so the
-// attention that follows reads every key, old or new, from the cache.
 constexpr int kVaD = 128;  // head_dim of the verify-width path
-
-struct QkvEpiArgs {
-  const float* sums;  // [M][N] unscaled projections
-  const float* ss;    // [n_ss][64] per-row sums of squares of the layer input
-  int M, N, K, n_ss;
-  float eps;
-  float* q_out;  // [M][nq]
-  int64_t ldq;
-  int nq, nk;
-  const uint16_t *q_gain, *k_gain;
-  const float *rope_cos, *rope_sin;
-  int rope_max;
-  const int32_t* positions;  // [M] or NULL: offset + row
-  const int32_t* offset_dev;
-  void *kc, *vc;  // [Hk][cap][128]
-  int kv_bf16, cap;
-};
-
-__global__ __launch_bounds__(256) void k_mm_reduce_qkv(QkvEpiArgs a) {
-  __shared__ float s_red[256 / kWave];
-  __shared__ float s_x[256];
-  const int m = blockIdx.y, t = threadIdx.x, wave = t / kWave;
-  const int n = min(blockIdx.x * 256 + t, a.N - 1);
-  const bool live = blockIdx.x * 256 + t < a.N;
-  // every load first: the row's sums of squares, this feature's sum, the
-  // position and the cache offset
-  float ssum = 0.f;
-#pragma unroll
-  for (int c = 0; c < 16; ++c) ssum += c < a.n_ss ? a.ss[c * 64 + m] : 0.f;  // n_ss <= 16 (hidden <= 4096)
-  float y = a.sums[static_cast<int64_t>(m) * a.N + n];
-  const int offset = *a.offset_dev;
-  const int pos = min(max(a.positions ? a.positions[m] : offset + m, 0), a.rope_max - 1);
-  y *= 1.f / sqrtf(ssum / static_cast<float>(a.K) + a.eps);
-
-  const int d = n % kVaD;
-  const bool is_q = n < a.nq, is_k = !is_q && n < a.nq + a.nk;  // uniform per head (128 threads)
-  float x = y;
-  {
-    // per-head RMSNorm: a head is two waves
-    float hs = wave_sum_dpp(y * y);
-    if (t % kWave == 0) s_red[wave] = hs;
-    lds_barrier();
-    hs = s_red[wave & ~1] + s_red[wave | 1];
-    const float inv = 1.f / sqrtf(hs / static_cast<float>(kVaD) + a.eps);
-    const float g = bf16_to_float(is_q ? a.q_gain[d] : a.k_gain[min(d, kVaD - 1)]);
-    x = y * inv * g;
-    s_x[t] = x;
-    lds_barrier();
-    const float xp = s_x[t ^ (kVaD / 2)];  // the rotate-half partner, same head
-    const int pi = d % (kVaD / 2);
-    const float c = a.rope_cos[static_cast<int64_t>(pos) * (kVaD / 2) + pi];
-    const float s = a.rope_sin[static_cast<int64_t>(pos) * (kVaD / 2) + pi];
-    if (is_q || is_k) x = d < kVaD / 2 ? x * c - xp * s : x * c + xp * s;
-  }
-  if (!live) return;
-  if (is_q) {
-    a.q_out[static_cast<int64_t>(m) * a.ldq + n] = x;
-    return;
-  }
-  const int slot = offset + m;
-  if (slot < 0 || slot >= a.cap) return;
-  const int j = is_k ? n - a.nq : n - a.nq - a.nk;
-  const int64_t at = (static_cast<int64_t>(j / kVaD) * a.cap + slot) * kVaD + d;
-  void* base = is_k ? a.kc : a.vc;
-  const float v = is_k ? x : y;
-  if (a.kv_bf16)
-    static_cast<uint16_t*>(base)[at] = float_to_bf16(v);
-  else
-    static_cast<float*>(base)[at] = v;
-}
 
 // ------------------------------------------------------------------ verify attention
 // Split-KV GQA attention for a verify block (head_dim 128, bf16 cache) whose q
@@ -767,7 +764,7 @@ struct LayerPlans {
 
 static LayerPlans layer_plans(const wc_drafter_dims& d) {
   const int nq = d.heads * d.head_dim, nqkv = nq + 2 * d.kv_heads * d.head_dim;
-  return {plan_gemm(nqkv, d.hidden, false), plan_gemm(d.hidden, nq, false), plan_gemm(2 * d.inter, d.hidden, true),
+  return {plan_gemm(nqkv, d.hidden, false, 2), plan_gemm(d.hidden, nq, false), plan_gemm(2 * d.inter, d.hidden, true),
           plan_gemm(d.hidden, d.inter, false)};
 }
 
@@ -789,7 +786,8 @@ static TargetWs target_ws(const wc_drafter_dims& d, int max_rows, void* base) {
   w.xa_attn = reinterpret_cast<uint16_t*>(take(256 * nq));
   w.xa_h1 = reinterpret_cast<uint16_t*>(take(256 * static_cast<size_t>(d.hidden)));
   w.xa_act = reinterpret_cast<uint16_t*>(take(256 * static_cast<size_t>(d.inter)));
-  w.ss_x = reinterpret_cast<float*>(take(4 * 64 * static_cast<size_t>(std::max(d.hidden, 256) / 256)));
+  // parts of the layer input's row sums of squares: the prep's (one per 256 k) or a down epilogue's (one per 64 columns)
+  w.ss_x = reinterpret_cast<float*>(take(4 * 64 * static_cast<size_t>(std::max(d.hidden / 64, 4))));
   // o_proj epilogue parts (one per column range) or the fallback attention prep's (one per 256 k)
   const size_t ss_parts = std::max(static_cast<size_t>(d.hidden / 64), nq / 256);
   w.ss_h1 = reinterpret_cast<float*>(take(4 * 64 * ss_parts));
@@ -822,7 +820,8 @@ size_t wc_target_workspace_bytes(const wc_drafter_dims* dims, int max_rows) {
 int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, const float* rope_cos,
                     const float* rope_sin, int rope_max_pos, float* x, int rows, const int32_t* positions_dev,
                     const uint8_t* mask_dev, int64_t mask_ld, void* k_cache, void* v_cache, int kv_dtype,
-                    int capacity, const int32_t* offset_dev, void* workspace, wc_stream_t stream) {
+                    int capacity, const int32_t* offset_dev, const void* next_norm, int input_prepared,
+                    void* workspace, wc_stream_t stream) {
   using namespace wc;
   WC_REQUIRE(dims && L && x && k_cache && v_cache && offset_dev && workspace, "wc_target_layer: NULL argument");
   const wc_drafter_dims& d = *dims;
@@ -849,8 +848,11 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
   const bool verify_path = D == kVaD && kv_dtype == WC_BF16;
 
-  // 1. the layer input as activations: x * in_norm, row sums of squares
-  if (int rc = launch_xa_prep(x, d.hidden, rows, d.hidden, u16(L->in_norm), ws.xa_x, ws.ss_x, s)) return rc;
+  // 1. the layer input as activations: x * in_norm, row sums of squares (or
+  //    already there: the previous layer's down epilogue wrote them)
+  if (!input_prepared)
+    if (int rc = launch_xa_prep(x, d.hidden, rows, d.hidden, u16(L->in_norm), ws.xa_x, ws.ss_x, s)) return rc;
+  const int n_ss_x = input_prepared ? pl.down.cols : d.hidden / 256;
 
   // 2. QKV = W . RMS_in(x): unscaled sums for the verify epilogue, scaled otherwise
   SkArgs g{};
@@ -867,47 +869,36 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.M = rows;
   g.N = nqkv;
   g.K = d.hidden;
-  g.epi = verify_path ? kSkRaw : kSkStore;
-  if (!verify_path) {
-    g.ss = ws.ss_x;
-    g.n_ss = d.hidden / 256;
-    g.ss_k = d.hidden;
-  }
-  g.out = ws.qkv;
-  g.ldo = nqkv;
+  g.epi = verify_path ? kSkQkvHead : kSkStore;
+  g.ss = ws.ss_x;
+  g.n_ss = n_ss_x;
+  g.ss_k = d.hidden;
+  g.out = verify_path ? ws.q : ws.qkv;
+  g.ldo = verify_path ? nq : nqkv;
   g.part = ws.part;
   g.ctr = ws.ctr;
+  if (verify_path) {
+    // head_dim 128 with a bf16 cache: the QKV epilogue normalises / rotates q
+    // and k and appends K / V, so the attention reads every key from the cache
+    g.nq = nq;
+    g.nk = nk;
+    g.q_gain = u16(L->q_norm);
+    g.k_gain = u16(L->k_norm);
+    g.rope_cos = rope_cos;
+    g.rope_sin = rope_sin;
+    g.rope_max = rope_max_pos;
+    g.positions = positions_dev;
+    g.offset_dev = offset_dev;
+    g.kc = k_cache;
+    g.vc = v_cache;
+    g.kv_bf16 = 1;
+    g.cap = capacity;
+  }
   if (int rc = launch_stream(g, pl.qkv, s)) return rc;
 
   const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunkMax - 1) / kAttnChunkMax));
   if (verify_path) {
-    // head_dim 128 with a bf16 cache: the QKV epilogue normalises / rotates q and
-    // k and appends K / V, then one MFMA attention launch covers every row
-    QkvEpiArgs e{};
-    e.sums = ws.qkv;
-    e.ss = ws.ss_x;
-    e.M = rows;
-    e.N = nqkv;
-    e.K = d.hidden;
-    e.n_ss = d.hidden / 256;
-    e.eps = d.eps;
-    e.q_out = ws.q;
-    e.ldq = nq;
-    e.nq = nq;
-    e.nk = nk;
-    e.q_gain = u16(L->q_norm);
-    e.k_gain = u16(L->k_norm);
-    e.rope_cos = rope_cos;
-    e.rope_sin = rope_sin;
-    e.rope_max = rope_max_pos;
-    e.positions = positions_dev;
-    e.offset_dev = offset_dev;
-    e.kc = k_cache;
-    e.vc = v_cache;
-    e.kv_bf16 = 1;
-    e.cap = capacity;
-    hipLaunchKernelGGL(k_mm_reduce_qkv, dim3((nqkv + 255) / 256, rows), dim3(256), 0, s, e);
-    WC_LAUNCHED();
+    // one MFMA attention launch covers every row
     AttnArgs at{};
     at.qkv = ws.q;
     at.ld_qkv = nq;
@@ -1023,6 +1014,11 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.ldo = d.hidden;
   g.res = ws.h1;
   g.ldr = d.hidden;
+  if (next_norm) {  // the next layer's (or the final) norm: its activations written here
+    g.xa_next = ws.xa_x;
+    g.gain_next = u16(next_norm);
+    g.ss_next = ws.ss_x;
+  }
   g.part = ws.part;
   g.ctr = ws.ctr;
   return launch_stream(g, pl.down, s);
@@ -1040,7 +1036,8 @@ int wc_target_embed(const void* table, int vocab, int hidden, const int32_t* tok
 }
 
 int wc_target_head(const wc_drafter_dims* dims, const void* head_w, const void* final_norm, const float* x, int rows,
-                   int vocab, float* logits_out, int64_t ld, void* workspace, wc_stream_t stream) {
+                   int vocab, float* logits_out, int64_t ld, int input_prepared, void* workspace,
+                   wc_stream_t stream) {
   using namespace wc;
   WC_REQUIRE(dims && head_w && final_norm && x && logits_out && workspace, "wc_target_head: NULL argument");
   const wc_drafter_dims& d = *dims;
@@ -1050,16 +1047,18 @@ int wc_target_head(const wc_drafter_dims* dims, const void* head_w, const void* 
   WC_REQUIRE(aligned(head_w, 16) && aligned(x, 16) && aligned(workspace, 16), "wc_target_head: misaligned buffer");
   const TargetWs ws = target_ws(d, rows, workspace);
   auto s = reinterpret_cast<hipStream_t>(stream);
-  // final RMSNorm folded in: x * gain as activations, 1/rms scales the logits
-  if (int rc = launch_xa_prep(x, d.hidden, rows, d.hidden, static_cast<const uint16_t*>(final_norm), ws.xa_x,
-                              ws.ss_x, s))
-    return rc;
+  // final RMSNorm folded in: x * gain as activations (or already there: the last
+  // layer's down epilogue wrote them), 1/rms scales the logits
+  if (!input_prepared)
+    if (int rc = launch_xa_prep(x, d.hidden, rows, d.hidden, static_cast<const uint16_t*>(final_norm), ws.xa_x,
+                                ws.ss_x, s))
+      return rc;
   GemmPlan p = plan_gemm(vocab, d.hidden, false);
   p.ks = 1;  // one column range per block: the vocabulary fills the GPU
   SkArgs g{};
   g.xa = ws.xa_x;
   g.ss = ws.ss_x;
-  g.n_ss = d.hidden / 256;
+  g.n_ss = input_prepared ? layer_plans(d).down.cols : d.hidden / 256;
   g.ss_k = d.hidden;
   g.eps = d.eps;
   g.w[0] = static_cast<const uint16_t*>(head_w);

@@ -128,7 +128,7 @@ class TargetLayer:
                   rows, ptr(pos) if pos is not None else None, ptr(mask) if mask is not None else None,
                   mask.stride(0) if mask is not None else 0, ptr(cache.keys), ptr(cache.values),
                   _lib.WC_BF16 if cache.keys.dtype == torch.bfloat16 else _lib.WC_F32, cache.capacity,
-                  ptr(offset_dev), ptr(self.ws), stream_ptr())
+                  ptr(offset_dev), None, 0, ptr(self.ws), stream_ptr())
         return x
 
 
@@ -238,18 +238,22 @@ class TargetModel:
         if taps is None:
             taps = [torch.empty(rows, cfg.hidden_size, dtype=torch.float32, device=self.device)
                     for _ in self.feature_layers]
+        final_norm = self.w["norm.weight"]
         for i in range(cfg.num_layers):
             c = cache[i]
+            # each layer leaves the next one's (or the head's) normed activations
+            # in the workspace: one prep launch per forward instead of per layer
+            nxt = self.w[f"layers.{i + 1}.input_layernorm.weight"] if i + 1 < cfg.num_layers else final_norm
             _lib.call("wc_target_layer", C.byref(self.dims), C.byref(self.lw[i]), ptr(cos), ptr(sin), cos.shape[0],
                       ptr(x), rows, ptr(pos) if pos is not None else None, ptr(mask) if mask is not None else None,
                       mask.stride(0) if mask is not None else 0, ptr(c.keys), ptr(c.values), kvdt, c.capacity,
-                      ptr(offset_dev), ptr(self.ws), s)
+                      ptr(offset_dev), ptr(nxt), int(i > 0), ptr(self.ws), s)
             for j, f in enumerate(self.feature_layers):
                 if f == i:
                     taps[j][:rows].copy_(x)
         if logits is None:
             logits = torch.empty(rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
-        _lib.call("wc_target_head", C.byref(self.dims), ptr(self.head), ptr(self.w["norm.weight"]), ptr(x), rows,
-                  cfg.vocab_size, ptr(logits), logits.stride(0), ptr(self.ws), s)
+        _lib.call("wc_target_head", C.byref(self.dims), ptr(self.head), ptr(final_norm), ptr(x), rows,
+                  cfg.vocab_size, ptr(logits), logits.stride(0), 1, ptr(self.ws), s)
         return logits, taps
 
