@@ -53,6 +53,7 @@ struct AttnArgs {
   float* out;  // [rows][H*D]
   uint16_t* xa_out;  // optional: the output also as fragment-major bf16 hi / lo (see xa_index), or NULL
   int64_t ld_out;
+  unsigned int* ctr;  // [Hk][kCounterStride] zeroed split counters, or NULL (decode kernel: merge launch)
 };
 
 template <typename KT>
@@ -497,10 +498,311 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) 
   }
 }
 
+// ------------------------------------------------------------------ decode-width attention
+
+// Sum over groups of LK adjacent lanes (8, 16 or 32); every lane of a group
+// receives its group's sum.
+template <int LK>
+__device__ __forceinline__ float group_sum(float v) {
+  v += dpp_move<0xB1>(v);  // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);  // quad_perm [2,3,0,1]
+  if constexpr (LK == 8) {
+    v += dpp_move<0x141>(v);  // row_half_mirror: the other quad of the 8
+  } else {
+    v += dpp_move<0x124>(v);  // row_ror:4
+    v += dpp_move<0x128>(v);  // row_ror:8
+    if constexpr (LK == 32) v += __shfl_xor(v, 16);
+  }
+  return v;
+}
+
+// Few query vectors (rows x GQA group <= QVM), causal / sliding-window
+// visibility, no explicit mask.  One block per (split, kv head); the split's
+// keys go through in chunks of 32: the K and V rows of a chunk are loaded
+// straight into registers (LK lanes per row, 16 bytes per lane, the next chunk
+// requested as soon as the current one is consumed), scores are group sums of
+// the lanes' partial dot products, V goes to LDS once for the
+// probability-weighted sums.  q vectors and appended rows are normalised and
+// rotated by the block while its first chunk is in flight.  With `ctr` (and
+// QVM <= 4) the last split to finish for a kv head merges all splits of that
+// head (device-coherent hand-over of the partials), so no merge launch
+// follows; otherwise the partials go to k_attn_merge.
+template <int D, typename KT, int QVM>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
+  constexpr int VE = 16 / static_cast<int>(sizeof(KT));  // cache elements per 16-byte load
+  constexpr int LK = D / VE;                             // lanes per key row
+  constexpr int KPB = kAttnThreads / LK;                 // key rows per block-wide load
+  constexpr int CHK = 32;
+  constexpr int NL = CHK / KPB;  // loads per thread and tensor per chunk
+  constexpr int OPT = QVM * D / kAttnThreads > 0 ? QVM * D / kAttnThreads : 1;  // outputs per thread
+  constexpr int VSTEP = kAttnThreads / D;                                         // v stride of a thread's outputs
+  static_assert(LK == 8 || LK == 16 || LK == 32, "8, 16 or 32 lanes per key row");
+  static_assert(NL >= 1 && NL * KPB == CHK, "whole key rows per chunk");
+  static_assert(QVM * D >= kAttnThreads && D <= kAttnThreads, "at least one output per thread");
+  __shared__ __attribute__((aligned(16))) float qs[QVM][D];
+  __shared__ __attribute__((aligned(16))) float nks[QVM][D];  // appended rows of this block (cache-rounded)
+  __shared__ __attribute__((aligned(16))) float nvs[QVM][D];
+  __shared__ __attribute__((aligned(16))) float vls[CHK][D];
+  __shared__ float s_p[QVM][CHK];
+  __shared__ float s_m[QVM], s_l[QVM], s_alpha[QVM];
+  constexpr bool kFuse = QVM <= 4;  // the merge's operands fit the registers
+  __shared__ float s_w[kFuse ? QVM : 1][kMaxSplits];
+  __shared__ float s_den[QVM];
+  __shared__ bool s_last;
+
+  const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int rep = a.H / a.Hk;
+  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
+  const int offset = *a.offset_dev + a.offset_add;
+  const int T = min(offset + nr, a.cap);
+  const int QV = nr * rep;
+  KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
+  KT* vc = static_cast<KT*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
+  const int per = (T + S - 1) / S;
+  const int kb = min(T, split * per), ke = min(T, kb + per);
+  const int kr = t / LK, e0 = (t % LK) * VE;  // key row within a load, first element
+
+  // 1. the first chunk in flight, then q vectors and appended rows
+  uint4 kreg[NL], vreg[NL];
+  const int64_t last_row = static_cast<int64_t>(a.cap) - 1;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t r = min(static_cast<int64_t>(kb + i * KPB + kr), last_row);
+    kreg[i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
+    vreg[i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
+  }
+  auto row_pos = [&](int l) {
+    const int pos = a.positions ? a.positions[l] : offset + l;
+    return min(max(pos, 0), a.rope_max - 1);
+  };
+  for (int v = wave; v < QV; v += kAttnThreads / kWave) {
+    HeadVec<D> r;
+    const int l = v / rep, h = kh * rep + v % rep;
+    head_vec_load<D>(a.qkv + l * a.ld_qkv + h * D, a.q_gain, r);
+    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
+    head_vec_norm_rope<D>(r, a.eps);
+#pragma unroll
+    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+      const int p = lane + e * kWave;
+      if (p < D / 2) {
+        qs[v][p] = r.lo[e];
+        qs[v][p + D / 2] = r.hi[e];
+      }
+    }
+  }
+  for (int l = kAttnThreads / kWave - 1 - wave; l < nr; l += kAttnThreads / kWave) {
+    const int tt = offset + l;
+    if (tt < kb || tt >= ke) continue;
+    HeadVec<D> r;
+    head_vec_load<D>(a.qkv + l * a.ld_qkv + (a.H + kh) * D, a.k_gain, r);
+    head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), r);
+    const float* vsrc = a.qkv + l * a.ld_qkv + (a.H + a.Hk + kh) * D;
+    head_vec_norm_rope<D>(r, a.eps);
+#pragma unroll
+    for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+      const int p = lane + e * kWave;
+      if (p < D / 2) {
+        nks[l][p] = kv_store<KT>(kc, static_cast<int64_t>(tt) * D + p, r.lo[e]);
+        nks[l][p + D / 2] = kv_store<KT>(kc, static_cast<int64_t>(tt) * D + p + D / 2, r.hi[e]);
+      }
+    }
+    for (int i = lane; i < D; i += kWave) nvs[l][i] = kv_store<KT>(vc, static_cast<int64_t>(tt) * D + i, vsrc[i]);
+  }
+  if (t < QVM) {
+    s_m[t] = -INFINITY;
+    s_l[t] = 0.f;
+  }
+  __syncthreads();
+
+  float o[OPT];
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) o[k] = 0.f;
+  const int od = t % D, ov0 = t / D;  // outputs (ov0 + VSTEP k, od)
+
+  for (int c0 = kb; c0 < ke; c0 += CHK) {
+    const int n = min(CHK, ke - c0);
+    // 2. scores of the chunk (group sums), V rows -> LDS as fp32
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int j = i * KPB + kr, tt = c0 + j;
+      float kf[VE], vf[VE];
+      if (tt >= offset) {
+        const int l = min(tt - offset, QVM - 1);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+          kf[e] = nks[l][e0 + e];
+          vf[e] = nvs[l][e0 + e];
+        }
+      } else {
+        unpack16<KT>(kreg[i], kf);
+        unpack16<KT>(vreg[i], vf);
+      }
+#pragma unroll
+      for (int e = 0; e < VE; e += 4)
+        *reinterpret_cast<float4*>(&vls[j][e0 + e]) = make_float4(vf[e], vf[e + 1], vf[e + 2], vf[e + 3]);
+#pragma unroll
+      for (int v = 0; v < QVM; ++v) {
+        if (v >= QV) break;
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < VE; e += 4) {
+          const float4 q = *reinterpret_cast<const float4*>(&qs[v][e0 + e]);
+          d = fmaf(kf[e], q.x, d);
+          d = fmaf(kf[e + 1], q.y, d);
+          d = fmaf(kf[e + 2], q.z, d);
+          d = fmaf(kf[e + 3], q.w, d);
+        }
+        d = group_sum<LK>(d);
+        const int l = v / rep;
+        const bool vis = j < n && tt <= offset + l && (a.window <= 0 || tt > offset + l - a.window);
+        if (t % LK == 0) s_p[v][j] = vis ? a.scale * d : -INFINITY;
+      }
+    }
+    if (c0 + CHK < ke) {  // next chunk in flight during the softmax and the weighted sums
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        const int64_t r = min(static_cast<int64_t>(c0 + CHK + i * KPB + kr), last_row);
+        kreg[i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
+        vreg[i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
+      }
+    }
+    lds_barrier();
+    // 3. online softmax: 16 lanes per query vector, keys g and g + 16
+    if (t < QVM * 16) {
+      const int v = t / 16, g = t % 16;
+      const bool live = v < QV;
+      const float s0 = live && g < n ? s_p[v][g] : -INFINITY;
+      const float s1 = live && g + 16 < n ? s_p[v][g + 16] : -INFINITY;
+      const float mx = row16_max(fmaxf(s0, s1));
+      const float m_old = s_m[v];
+      const float m_new = fmaxf(m_old, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : (m_old == -INFINITY ? 0.f : expf(m_old - m_new));
+      const float p0 = s0 == -INFINITY ? 0.f : expf(s0 - m_new);
+      const float p1 = s1 == -INFINITY ? 0.f : expf(s1 - m_new);
+      const float ls = row16_sum(p0 + p1);
+      s_p[v][g] = p0;
+      s_p[v][g + 16] = p1;
+      if (g == 0) {
+        s_m[v] = m_new;
+        s_l[v] = s_l[v] * alpha + ls;
+        s_alpha[v] = alpha;
+      }
+    }
+    lds_barrier();
+    // 4. probability-weighted V rows
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int v = ov0 + VSTEP * k;
+      if (v >= QV) break;
+      float acc0 = o[k] * s_alpha[v], acc1 = 0.f;
+      int j = 0;
+      for (; j + 1 < n; j += 2) {
+        acc0 = fmaf(s_p[v][j], vls[j][od], acc0);
+        acc1 = fmaf(s_p[v][j + 1], vls[j + 1][od], acc1);
+      }
+      if (j < n) acc0 = fmaf(s_p[v][j], vls[j][od], acc0);
+      o[k] = acc0 + acc1;
+    }
+    if (c0 + CHK < ke) lds_barrier();  // vls / s_p are rewritten by the next chunk
+  }
+
+  // 5. this split's (m, l, o); an empty range leaves m = -inf, l = 0, o = 0
+  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * a.qv_ld * (D + 2);
+  const bool fused = kFuse && a.ctr != nullptr;
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    const int v = ov0 + VSTEP * k;
+    if (v >= QV) break;
+    float* pv = part + v * (D + 2);
+    if (fused) {
+      publish_f32(pv + 2 + od, o[k]);
+      if (od == 0) {
+        publish_f32(pv, s_m[v]);
+        publish_f32(pv + 1, s_l[v]);
+      }
+    } else {
+      pv[2 + od] = o[k];
+      if (od == 0) {
+        pv[0] = s_m[v];
+        pv[1] = s_l[v];
+      }
+    }
+  }
+  if constexpr (kFuse) {
+  if (!fused) return;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    unsigned int* ctr = a.ctr + kh * kCounterStride;
+    const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      static_cast<unsigned int>(S - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // 6. last split of this kv head: merge every split's (m, l, o)
+  const float* base = a.partial + static_cast<int64_t>(kh) * S * a.qv_ld * (D + 2);
+  const int64_t sstride = static_cast<int64_t>(a.qv_ld) * (D + 2);
+  float ov[OPT][kMaxSplits];
+#pragma unroll
+  for (int k = 0; k < OPT; ++k)
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+      ov[k][sp] = (sp < S && ov0 + VSTEP * k < QV) ? fetch_f32(base + sp * sstride + (ov0 + VSTEP * k) * (D + 2) + 2 + od)
+                                                   : 0.f;
+  if (wave < QV && wave < QVM) {  // wave v: lane = split, weights exp(m_s - M) / den
+    const float ms = lane < S ? fetch_f32(base + lane * sstride + wave * (D + 2)) : -INFINITY;
+    const float ls = lane < S ? fetch_f32(base + lane * sstride + wave * (D + 2) + 1) : 0.f;
+    const float M = wave_max(ms);
+    const float wgt = ms == -INFINITY ? 0.f : expf(ms - M);
+    const float den = wave_sum(ls * wgt);
+    if (lane < kMaxSplits) s_w[wave][lane] = lane < S ? wgt : 0.f;
+    if (lane == 0) s_den[wave] = den;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    const int v = ov0 + VSTEP * k;
+    if (v >= QV) break;
+    float num = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp) num = fmaf(s_w[v][sp], ov[k][sp], num);
+    const float y = num / s_den[v];
+    const int l = v / rep, h = kh * rep + v % rep;
+    a.out[l * a.ld_out + h * D + od] = y;
+    if (a.xa_out) {
+      const __bf16 hi = static_cast<__bf16>(y);
+      a.xa_out[xa_index(l, h * D + od, 0)] = __builtin_bit_cast(uint16_t, hi);
+      a.xa_out[xa_index(l, h * D + od, 1)] =
+          __builtin_bit_cast(uint16_t, static_cast<__bf16>(y - static_cast<float>(hi)));
+    }
+  }
+  }  // kFuse
+}
+
 template <int D, typename KT>
 static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream) {
   constexpr int CH = attn_chunk<D>();
   const size_t qvb = static_cast<size_t>(a.rows) * (a.H / a.Hk);
+  if constexpr (D == 64 || D == 128) {
+    if (!a.mask && qvb <= 16) {  // decode width: chunked registers, merge fused for <= 4 query vectors
+      if (qvb <= 4) {
+        hipLaunchKernelGGL((k_attn_decode<D, KT, 4>), dim3(splits, a.Hk), dim3(kAttnThreads), 0, stream, a);
+      } else {
+        hipLaunchKernelGGL((k_attn_decode<D, KT, 16>), dim3(splits, a.Hk), dim3(kAttnThreads), 0, stream, a);
+      }
+      WC_LAUNCHED();
+      if (qvb <= 4 && a.ctr) return WC_OK;
+      hipLaunchKernelGGL((k_attn_merge<D>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, stream,
+                         a, splits);
+      WC_LAUNCHED();
+      return WC_OK;
+    }
+  }
   const size_t lds = sizeof(float) * (qvb * D + 2 * CH * D + qvb * CH + 2 * static_cast<size_t>(a.rows) * D);
   static size_t attr_bytes = 64 * 1024;  // default dynamic-LDS limit
   if (lds > attr_bytes) {

@@ -24,6 +24,7 @@ namespace wc {
 struct DrafterWs {
   unsigned int* head_ctr;  // tree counters (kTreeCounterBytes each)
   unsigned int* fin_ctr;
+  unsigned int* attn_ctr;  // per kv head: splits done (decode attention's fused merge)
   unsigned long long* slots;
   float* qkv;
   float* attn;
@@ -48,6 +49,7 @@ static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
   const size_t nqkv = static_cast<size_t>(d.heads + 2 * d.kv_heads) * d.head_dim;
   w.head_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
   w.fin_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
+  w.attn_ctr = reinterpret_cast<unsigned int*>(take(4 * kCounterStride * static_cast<size_t>(kMaxKvHeads)));
   w.slots = reinterpret_cast<unsigned long long*>(take(8 * R * kSlots * kSlotStride));
   w.qkv = reinterpret_cast<float*>(take(4 * R * nqkv));
   w.attn = reinterpret_cast<float*>(take(4 * R * d.heads * d.head_dim));
@@ -542,6 +544,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       at.window = d.window;
       at.partial = ws.partial;
       at.qv_ld = kMaxQV;
+      at.ctr = ws.attn_ctr;
       at.out = ws.attn;
       at.ld_out = H * D;
       if (int rc = launch_attention(at, D, kv_dtype, splits, s)) return rc;
