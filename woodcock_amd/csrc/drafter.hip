@@ -75,8 +75,18 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
   if constexpr (R * (PAIR ? 2 : 1) * NIN * S > kGemv1Budget) {
     return false;
   } else {
+    int gb = 0;
+    for (int i = 0; i < a.n_in; ++i)
+      if (a.in[i].gain) gb |= 1 << i;
     const dim3 grid((a.N + kGemvWaves * R - 1) / (kGemvWaves * R)), block(kGemvThreads);
-    hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, S, XB>), grid, block, 0, s, a);
+    constexpr int kAll = (1 << NIN) - 1;
+    if (gb == kAll) {
+      hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, S, XB, kAll>), grid, block, 0, s, a);
+    } else if constexpr (NIN == 1) {
+      hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, S, XB, 0>), grid, block, 0, s, a);  // no gain
+    } else {
+      return false;  // mixed gains on several segments: the general kernel
+    }
     return true;
   }
 }

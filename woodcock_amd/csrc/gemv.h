@@ -113,6 +113,19 @@ __device__ __forceinline__ float dot8(const uint4 w, const float4 a, const float
   return s;
 }
 
+// acc + w . (a, b) as one running fma chain
+__device__ __forceinline__ float dot8_acc(const uint4 w, const float4 a, const float4 b, float s) {
+  s = fmaf(bf16_lo(w.x), a.x, s);
+  s = fmaf(bf16_hi(w.x), a.y, s);
+  s = fmaf(bf16_lo(w.y), a.z, s);
+  s = fmaf(bf16_hi(w.y), a.w, s);
+  s = fmaf(bf16_lo(w.z), b.x, s);
+  s = fmaf(bf16_hi(w.z), b.y, s);
+  s = fmaf(bf16_lo(w.w), b.z, s);
+  s = fmaf(bf16_hi(w.w), b.w, s);
+  return s;
+}
+
 __device__ __forceinline__ float load_in(const InSeg& s, int64_t row, int k) {
   const int64_t i = row * s.ld + k;
   return s.dtype == WC_BF16 ? bf16_to_float(static_cast<const uint16_t*>(s.x)[i]) : static_cast<const float*>(s.x)[i];
@@ -281,11 +294,17 @@ __device__ __forceinline__ void argmax_epilogue(const GemvArgs& a, int m, unsign
 // ------------------------------------------------------------------ M = 1
 
 // Fast path for one input row when every segment's K is a multiple of 512.
-// Load order is x slices, then gains, then weights, so the norm (which needs
-// only the L2-resident x) waits for nothing the weight stream is carrying, and
-// the dot products retire the weight loads in the order they were issued.
-// XB: bit s set = input segment s is bf16.  S: max 512-wide steps per segment.
-template <int R, bool PAIR, int NIN, int S, int XB>
+// With norm gains (GB != 0): load order is x slices, then gains, then
+// weights, so the norm (which needs only the L2-resident x) waits for nothing
+// the weight stream is carrying, and the dot products retire the weight loads
+// in the order they were issued; the norm scale is applied after the dot
+// product (sum W (x g) * inv).  Without gains (GB == 0: o_proj, down): the
+// weights are requested first, then the x slices are loaded and consumed step
+// by step, so nothing but the weights stays live across the steps, which
+// keeps the register count (and the number of waves streaming per SIMD) high.
+// XB: bit s set = input segment s is bf16; GB: bit s set = segment s has a
+// norm gain (RMSNorm applied).  S: max 512-wide steps per segment.
+template <int R, bool PAIR, int NIN, int S, int XB, int GB>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
   constexpr int P = PAIR ? 2 : 1;
   __shared__ float s_red[kGemvWaves];
@@ -296,120 +315,238 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
   const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
   const int rrow = res_row(a, 0);
 
-  // Every load below is unconditional (addresses clamped into the operands), so
-  // the compiler issues them back to back with no branch or merge between them;
-  // out-of-range steps are zeroed in the x slices, and out-of-range rows are
-  // never stored.
-  // 1. x slices, kept raw until the weights are in flight
-  uint4 xq[NIN][S][2];
-  int steps[NIN];
-#pragma unroll
-  for (int s = 0; s < NIN; ++s) {
-    const InSeg& seg = a.in[s];
-    steps[s] = seg.K / (kWave * 8);
-    const int64_t row = m > 0 ? in_row(seg, 0) : 0;
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      const int k = min(u, steps[s] - 1) * kWave * 8 + lane * 8;
-      if (XB & (1 << s)) {
-        xq[s][u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + row * seg.ld + k);
-      } else {
-        const float* xp = static_cast<const float*>(seg.x) + row * seg.ld + k;
-        xq[s][u][0] = *reinterpret_cast<const uint4*>(xp);
-        xq[s][u][1] = *reinterpret_cast<const uint4*>(xp + 4);
-      }
-    }
-  }
-  // 2. gains (a segment without one reads its weight row 0 and ignores it)
-  uint4 gr[NIN][S];
-#pragma unroll
-  for (int s = 0; s < NIN; ++s) {
-    const uint16_t* gp = a.in[s].gain ? a.in[s].gain : a.w[0][s];
-#pragma unroll
-    for (int u = 0; u < S; ++u)
-      gr[s][u] = *reinterpret_cast<const uint4*>(gp + min(u, steps[s] - 1) * kWave * 8 + lane * 8);
-  }
-  // 3. weights of this wave's rows
-  uint4 w[NIN][R][P][S];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int n = min(row0 + r, a.N - 1);
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-#pragma unroll
-      for (int s = 0; s < NIN; ++s) {
-        const uint16_t* wr = row_ptr<PAIR>(a, n, p, s) + lane * 8;
-#pragma unroll
-        for (int u = 0; u < S; ++u)
-          w[s][r][p][u] = *reinterpret_cast<const uint4*>(wr + min(u, steps[s] - 1) * kWave * 8);
-      }
-    }
-  }
-  float resv[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) resv[r] = res_at(a, rrow, min(row0 + r, a.N - 1));
-  // 4. per-segment 1/rms and x * gain (waits only for x and gain)
-  float4 xr[NIN][S][2];
-  float inv[NIN];
-#pragma unroll
-  for (int s = 0; s < NIN; ++s) {
-    const bool gain = a.in[s].gain != nullptr;
-    float ss = 0.f;
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      float4 x0, x1;
-      if (XB & (1 << s)) {
-        const uint4 h = xq[s][u][0];
-        x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
-        x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
-      } else {
-        x0 = make_float4(__uint_as_float(xq[s][u][0].x), __uint_as_float(xq[s][u][0].y),
-                         __uint_as_float(xq[s][u][0].z), __uint_as_float(xq[s][u][0].w));
-        x1 = make_float4(__uint_as_float(xq[s][u][1].x), __uint_as_float(xq[s][u][1].y),
-                         __uint_as_float(xq[s][u][1].z), __uint_as_float(xq[s][u][1].w));
-      }
-      if (u >= steps[s]) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
-      ss = fmaf(x0.x, x0.x, ss); ss = fmaf(x0.y, x0.y, ss); ss = fmaf(x0.z, x0.z, ss); ss = fmaf(x0.w, x0.w, ss);
-      ss = fmaf(x1.x, x1.x, ss); ss = fmaf(x1.y, x1.y, ss); ss = fmaf(x1.z, x1.z, ss); ss = fmaf(x1.w, x1.w, ss);
-      if (gain) {
-        const uint4 g = gr[s][u];
-        x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
-        x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
-      }
-      xr[s][u][0] = x0;
-      xr[s][u][1] = x1;
-    }
-    inv[s] = gain ? 1.f / sqrtf(wave_sum_dpp(ss) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
-  }
-  if (a.xn_out && blockIdx.x == 0 && wave == 0 && m > 0) {
-    float* xo = a.xn_out + static_cast<int64_t>(in_row(a.in[0], 0)) * a.ld_xn + lane * 8;
-#pragma unroll
-    for (int u = 0; u < S; ++u) {
-      if (u >= steps[0]) continue;
-      const float4 x0 = xr[0][u][0], x1 = xr[0][u][1];
-      *reinterpret_cast<float4*>(xo + u * kWave * 8) =
-          make_float4(x0.x * inv[0], x0.y * inv[0], x0.z * inv[0], x0.w * inv[0]);
-      *reinterpret_cast<float4*>(xo + u * kWave * 8 + 4) =
-          make_float4(x1.x * inv[0], x1.y * inv[0], x1.z * inv[0], x1.w * inv[0]);
-    }
-  }
-  // 5. dot products in weight-issue order
   float acc[R][P];
+  float resv[R];
+  if constexpr (GB != 0) {
+    // Every load below is unconditional (addresses clamped into the operands), so
+    // the compiler issues them back to back with no branch or merge between them;
+    // out-of-range steps are zeroed in the x slices, and out-of-range rows are
+    // never stored.
+    // 1. x slices, kept raw until the weights are in flight
+    uint4 xq[NIN][S][2];
+    int steps[NIN];
 #pragma unroll
-  for (int r = 0; r < R; ++r)
+    for (int s = 0; s < NIN; ++s) {
+      const InSeg& seg = a.in[s];
+      steps[s] = seg.K / (kWave * 8);
+      const int64_t row = m > 0 ? in_row(seg, 0) : 0;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      float t = 0.f;
-#pragma unroll
-      for (int s = 0; s < NIN; ++s) {
-        float part = 0.f;
-#pragma unroll
-        for (int u = 0; u < S; ++u) part += dot8(w[s][r][p][u], xr[s][u][0], xr[s][u][1]);
-        t = fmaf(part, inv[s], t);
+      for (int u = 0; u < S; ++u) {
+        const int k = min(u, steps[s] - 1) * kWave * 8 + lane * 8;
+        if (XB & (1 << s)) {
+          xq[s][u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + row * seg.ld + k);
+        } else {
+          const float* xp = static_cast<const float*>(seg.x) + row * seg.ld + k;
+          xq[s][u][0] = *reinterpret_cast<const uint4*>(xp);
+          xq[s][u][1] = *reinterpret_cast<const uint4*>(xp + 4);
+        }
       }
-      acc[r][p] = wave_sum_dpp(t);
     }
+    // 2. gains
+    uint4 gr[NIN][S];
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      if (!((GB >> s) & 1)) continue;
+      const uint16_t* gp = a.in[s].gain;
+#pragma unroll
+      for (int u = 0; u < S; ++u)
+        gr[s][u] = *reinterpret_cast<const uint4*>(gp + min(u, steps[s] - 1) * kWave * 8 + lane * 8);
+    }
+    // 3. weights of this wave's rows
+    uint4 w[NIN][R][P][S];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = min(row0 + r, a.N - 1);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+#pragma unroll
+        for (int s = 0; s < NIN; ++s) {
+          const uint16_t* wr = row_ptr<PAIR>(a, n, p, s) + lane * 8;
+#pragma unroll
+          for (int u = 0; u < S; ++u)
+            w[s][r][p][u] = *reinterpret_cast<const uint4*>(wr + min(u, steps[s] - 1) * kWave * 8);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) resv[r] = res_at(a, rrow, min(row0 + r, a.N - 1));
+    // 4. per-segment 1/rms and x * gain (waits only for x and gain)
+    float4 xr[NIN][S][2];
+    float inv[NIN];
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      const bool gain = (GB >> s) & 1;
+      float ss = 0.f;
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        float4 x0, x1;
+        if (XB & (1 << s)) {
+          const uint4 h = xq[s][u][0];
+          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
+        } else {
+          x0 = make_float4(__uint_as_float(xq[s][u][0].x), __uint_as_float(xq[s][u][0].y),
+                           __uint_as_float(xq[s][u][0].z), __uint_as_float(xq[s][u][0].w));
+          x1 = make_float4(__uint_as_float(xq[s][u][1].x), __uint_as_float(xq[s][u][1].y),
+                           __uint_as_float(xq[s][u][1].z), __uint_as_float(xq[s][u][1].w));
+        }
+        if (u >= steps[s]) x0 = x1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        ss = fmaf(x0.x, x0.x, ss); ss = fmaf(x0.y, x0.y, ss); ss = fmaf(x0.z, x0.z, ss); ss = fmaf(x0.w, x0.w, ss);
+        ss = fmaf(x1.x, x1.x, ss); ss = fmaf(x1.y, x1.y, ss); ss = fmaf(x1.z, x1.z, ss); ss = fmaf(x1.w, x1.w, ss);
+        if (gain) {
+          const uint4 g = gr[s][u];
+          x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
+          x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
+        }
+        xr[s][u][0] = x0;
+        xr[s][u][1] = x1;
+      }
+      inv[s] = gain ? 1.f / sqrtf(wave_sum_dpp(ss) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+    }
+    if (a.xn_out && blockIdx.x == 0 && wave == 0 && m > 0) {
+      float* xo = a.xn_out + static_cast<int64_t>(in_row(a.in[0], 0)) * a.ld_xn + lane * 8;
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        if (u >= steps[0]) continue;
+        const float4 x0 = xr[0][u][0], x1 = xr[0][u][1];
+        *reinterpret_cast<float4*>(xo + u * kWave * 8) =
+            make_float4(x0.x * inv[0], x0.y * inv[0], x0.z * inv[0], x0.w * inv[0]);
+        *reinterpret_cast<float4*>(xo + u * kWave * 8 + 4) =
+            make_float4(x1.x * inv[0], x1.y * inv[0], x1.z * inv[0], x1.w * inv[0]);
+      }
+    }
+    // 5. dot products in weight-issue order
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float t = 0.f;
+#pragma unroll
+        for (int s = 0; s < NIN; ++s) {
+          float part = 0.f;
+#pragma unroll
+          for (int u = 0; u < S; ++u) part += dot8(w[s][r][p][u], xr[s][u][0], xr[s][u][1]);
+          t = fmaf(part, inv[s], t);
+        }
+        acc[r][p] = wave_sum_dpp(t);
+      }
 
+  } else {
+    // Every load below is unconditional (addresses clamped into the operands), so
+    // the compiler issues them with no branch or merge between them; out-of-range
+    // steps are zeroed in the x slices, and out-of-range rows are never stored.
+    int steps[NIN];
+    int64_t xrow[NIN];
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      steps[s] = a.in[s].K / (kWave * 8);
+      xrow[s] = m > 0 ? in_row(a.in[s], 0) : 0;
+    }
+    // 1. weights of this wave's rows
+    uint4 w[NIN][R][P][S];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int n = min(row0 + r, a.N - 1);
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+#pragma unroll
+        for (int s = 0; s < NIN; ++s) {
+          const uint16_t* wr = row_ptr<PAIR>(a, n, p, s) + lane * 8;
+#pragma unroll
+          for (int u = 0; u < S; ++u)
+            w[s][r][p][u] = *reinterpret_cast<const uint4*>(wr + min(u, steps[s] - 1) * kWave * 8);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) resv[r] = res_at(a, rrow, min(row0 + r, a.N - 1));
+
+    // 2. per step: x slice and gains -> sum of squares, x * gain -> dot products
+    float part[NIN][R][P], ssq[NIN];
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      const InSeg& seg = a.in[s];
+      const bool gain = (GB >> s) & 1;
+      float ss = 0.f;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int p = 0; p < P; ++p) part[s][r][p] = 0.f;
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        const int k = min(u, steps[s] - 1) * kWave * 8 + lane * 8;
+        float4 x0, x1;
+        if (XB & (1 << s)) {
+          const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + xrow[s] * seg.ld + k);
+          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
+        } else {
+          const float* xp = static_cast<const float*>(seg.x) + xrow[s] * seg.ld + k;
+          x0 = *reinterpret_cast<const float4*>(xp);
+          x1 = *reinterpret_cast<const float4*>(xp + 4);
+        }
+        const bool live = u < steps[s];  // selects, not a branch: the loads stay schedulable
+        x0 = make_float4(live ? x0.x : 0.f, live ? x0.y : 0.f, live ? x0.z : 0.f, live ? x0.w : 0.f);
+        x1 = make_float4(live ? x1.x : 0.f, live ? x1.y : 0.f, live ? x1.z : 0.f, live ? x1.w : 0.f);
+        ss = fmaf(x0.x, x0.x, ss); ss = fmaf(x0.y, x0.y, ss); ss = fmaf(x0.z, x0.z, ss); ss = fmaf(x0.w, x0.w, ss);
+        ss = fmaf(x1.x, x1.x, ss); ss = fmaf(x1.y, x1.y, ss); ss = fmaf(x1.z, x1.z, ss); ss = fmaf(x1.w, x1.w, ss);
+        if (gain) {
+          const uint4 g = *reinterpret_cast<const uint4*>(seg.gain + k);
+          x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
+          x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int p = 0; p < P; ++p) part[s][r][p] = dot8_acc(w[s][r][p][u], x0, x1, part[s][r][p]);
+      }
+      ssq[s] = ss;
+    }
+    // 3. per-segment 1/rms, then the row sums
+    float inv[NIN];
+#pragma unroll
+    for (int s = 0; s < NIN; ++s)
+      inv[s] = ((GB >> s) & 1) ? 1.f / sqrtf(wave_sum_dpp(ssq[s]) / static_cast<float>(a.in[s].K) + a.eps) : 1.f;
+    if (a.xn_out && blockIdx.x == 0 && wave == 0 && m > 0) {
+      // the normalised input row (segment 0) for the caller: x * gain * inv
+      const InSeg& seg = a.in[0];
+      float* xo = a.xn_out + static_cast<int64_t>(xrow[0]) * a.ld_xn + lane * 8;
+#pragma unroll
+      for (int u = 0; u < S; ++u) {
+        if (u >= steps[0]) continue;
+        const int k = u * kWave * 8 + lane * 8;
+        float4 x0, x1;
+        if (XB & 1) {
+          const uint4 h = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + xrow[0] * seg.ld + k);
+          x0 = make_float4(bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y));
+          x1 = make_float4(bf16_lo(h.z), bf16_hi(h.z), bf16_lo(h.w), bf16_hi(h.w));
+        } else {
+          const float* xp = static_cast<const float*>(seg.x) + xrow[0] * seg.ld + k;
+          x0 = *reinterpret_cast<const float4*>(xp);
+          x1 = *reinterpret_cast<const float4*>(xp + 4);
+        }
+        if (GB & 1) {
+          const uint4 g = *reinterpret_cast<const uint4*>(seg.gain + k);
+          x0 = make_float4(x0.x * bf16_lo(g.x), x0.y * bf16_hi(g.x), x0.z * bf16_lo(g.y), x0.w * bf16_hi(g.y));
+          x1 = make_float4(x1.x * bf16_lo(g.z), x1.y * bf16_hi(g.z), x1.z * bf16_lo(g.w), x1.w * bf16_hi(g.w));
+        }
+        *reinterpret_cast<float4*>(xo + u * kWave * 8) =
+            make_float4(x0.x * inv[0], x0.y * inv[0], x0.z * inv[0], x0.w * inv[0]);
+        *reinterpret_cast<float4*>(xo + u * kWave * 8 + 4) =
+            make_float4(x1.x * inv[0], x1.y * inv[0], x1.z * inv[0], x1.w * inv[0]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float t = 0.f;
+#pragma unroll
+        for (int s = 0; s < NIN; ++s) t = fmaf(part[s][r][p], inv[s], t);
+        acc[r][p] = wave_sum_dpp(t);
+      }
+
+  }
   // 6. epilogues
   if (a.epi != kEpiArgmax) {
     if (lane == 0) {
