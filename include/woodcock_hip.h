@@ -177,6 +177,51 @@ int wc_sample_without_replacement(const float* q, int rows, int head_rows, int64
                                   const int32_t* k_dev, int k_max, const wc_uniforms* rng, int64_t uniform_base,
                                   int32_t* tokens_out, int32_t* counts_out, wc_stream_t stream);
 
+/* ------------------------------------------------------------------ greedy tree drafting
+ * The drafting loop of SpeculativeDecoder._draft with a StaticPolicy in greedy
+ * mode (python/woodcock/spec.py:216-303; policies.py:49-75) without a host
+ * round trip per level: a node table (token, parent, depth, phat in fp64,
+ * cache slot, feedback row) lives in a caller-owned device state of
+ * wc_tree_draft_state_bytes() bytes (at most 512 nodes, width <= 8).  The
+ * caller runs, per level, the draft head (logits) and wc_probs_from_logits at
+ * T = 1 over the frontier rows, wc_tree_draft_expand, and unless it is the last
+ * level wc_tree_draft_frontier plus wc_drafter_forward with the inputs it
+ * wrote; node ids and level ranges follow from the static shape (root 0, then
+ * rows * width children per level). */
+size_t wc_tree_draft_state_bytes(void);
+
+/* Node 0 = the root token (*root_token_dev); the frontier is the root. */
+int wc_tree_draft_begin(void* state, const int32_t* root_token_dev, wc_stream_t stream);
+
+/* Children of the current frontier: for frontier row r (rows of it) the width
+ * entries of q [rows][ld_q] with the largest probability (descending; the lower
+ * head row first on a tie -- the reference's mx.argpartition leaves this order
+ * open) become nodes node_base + r * width + j with token d2t_dev[row] (NULL =
+ * identity), parent the frontier node and phat = phat(parent) * q in fp64
+ * (spec.py:226-237). */
+int wc_tree_draft_expand(void* state, const float* q, int rows, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
+                         int width, int node_base, wc_stream_t stream);
+
+/* Next frontier: the min(width, level size) nodes of [level_begin, level_end)
+ * with the largest phat, earlier nodes first on a tie (Policy.select_frontier,
+ * policies.py:52-53), in that order.  Writes the drafter forward's inputs for
+ * frontier row r: tokens_out, feat_rows_out (feedback row of the node's parent;
+ * the root's is row 0), positions_out = *offset_dev - 1 + depth, and mask_out
+ * [rows][mask_ld] over cache slots: the prefix [lo, *offset_dev) with lo from
+ * the sliding window (0 = none), the cache slots of the node's ancestors below
+ * the root and its own slot *offset_dev + tree_cache + r (spec.py:281-294).
+ * The node's feedback row becomes store_base + r. */
+int wc_tree_draft_frontier(void* state, int level_begin, int level_end, int width, const int32_t* offset_dev,
+                           int tree_cache, int window, int store_base, int32_t* tokens_out, int32_t* feat_rows_out,
+                           int32_t* positions_out, uint8_t* mask_out, int64_t mask_ld, wc_stream_t stream);
+
+/* The verified tree (StaticPolicy.select_verify + _to_tree, policies.py:66-75;
+ * spec.py:297-303): all n_nodes nodes when n_nodes - 1 <= budget, else the root
+ * plus the budget nodes ranked first by (-phat, depth, id), in node order, with
+ * parents remapped (-1 for the root).  *count_out receives the node count. */
+int wc_tree_draft_select(const void* state, int n_nodes, int budget, int32_t* tokens_out, int32_t* parents_out,
+                         int32_t* depth_out, int32_t* count_out, wc_stream_t stream);
+
 /* ------------------------------------------------------------------ KV compaction */
 
 /* In-place gather of the accepted entries of the last verify block, in every
@@ -259,7 +304,7 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
  * *offset_dev + offset_add: every layer (dual-stream layer 0, GQA attention
  * with q/k RMSNorm and rotate-half RoPE, SwiGLU MLP), then the final RMSNorm.
  *   tokens_dev [rows]; feat [rows][feat_ld] fp32 (feat_row_dev optionally
- *   gathers one feature row: row *feat_row_dev + feat_row_add);
+ *   gathers the feature rows: row r is feat_row_dev[r] + feat_row_add);
  *   k_cache/v_cache: num_layers device pointers [kv_heads][capacity][head_dim]
  *   of kv_dtype; positions_dev [rows] (NULL = offset + r); mask_dev
  *   [rows][mask_ld] uint8 over cache slots (NULL = causal, sliding window

@@ -1,0 +1,117 @@
+"""Greedy tree drafting on the device (woodcock_amd.tree_draft.TreeDrafter:
+python/woodcock/spec.py:216-303 with a StaticPolicy) against the oracle
+restatement (oracle/tree_draft.py) on identical weights, cache and root:
+identical verified trees (tokens, parents, depths, node count), the drafter
+cache offset untouched, and the tree entries written to the drafter cache
+within the fp32 tolerance.  Shapes: a small drafter with an fp32 and a bf16
+cache, and the Qwen3-1.7B drafter with the config-5 tree (depth 6, width 4,
+60 verified rows)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import core
+from oracle import tree_draft as otd
+
+pytestmark = pytest.mark.gpu
+
+
+def _small_cfg():
+    from woodcock_amd.config import DrafterConfig
+
+    return DrafterConfig(hidden_size=256, num_layers=1, num_heads=4, num_kv_heads=2, head_dim=64,
+                         intermediate_size=512, vocab_size=4096, target_hidden_size=192, rope_theta=1e6)
+
+
+def _setup(cuda, cfg, head_rows, ctx, cap, kv_dtype, seed):
+    from woodcock_amd.drafter import Drafter
+    from woodcock_amd.synthetic import draft_vocab, random_drafter, to_bits
+
+    ids = draft_vocab(cfg.vocab_size, head_rows, seed=seed)
+    w = random_drafter(cfg, seed=seed, device=cuda, head_rows=head_rows)
+    d = Drafter(cfg, dict(w), cuda, kv_dtype)
+    d._vocab_ids = torch.from_numpy(ids).to(cuda)
+    d._build_structs(d._rope[0].shape[0])
+    cache = d.make_cache(cap)
+    od = core.Drafter(cfg.as_dict(), {k: to_bits(v) for k, v in w.items()})
+    od.d2t = ids
+    oc = od.make_cache(cap, kv_bf16=kv_dtype == torch.bfloat16)
+    g = torch.Generator(device=cuda).manual_seed(seed)
+    c = cache[0]
+    c.keys[0, :, :ctx] = torch.randn(c.keys[0, :, :ctx].shape, generator=g, device=cuda).to(kv_dtype)
+    c.values[0, :, :ctx] = torch.randn(c.values[0, :, :ctx].shape, generator=g, device=cuda).to(kv_dtype)
+    if kv_dtype == torch.bfloat16:
+        oc.k[0][:] = to_bits(c.keys[0])
+        oc.v[0][:] = to_bits(c.values[0])
+    else:
+        oc.k[0][:] = c.keys[0].cpu().numpy()
+        oc.v[0][:] = c.values[0].cpu().numpy()
+    oc.offset = ctx
+    root_out = torch.randn(cfg.hidden_size, generator=g, device=cuda)
+    return d, cache, od, oc, root_out
+
+
+def _run(cuda, cfg, head_rows, ctx, cap, kv_dtype, depth, width, budget, seed, tol):
+    from woodcock_amd.tree_draft import TreeDrafter
+
+    d, cache, od, oc, root_out = _setup(cuda, cfg, head_rows, ctx, cap, kv_dtype, seed)
+    root_tok = 11
+    tdr = TreeDrafter(d, cache, depth, width, budget)
+    off = torch.tensor([ctx], dtype=torch.int32, device=cuda)
+    tree = tdr.draft(torch.tensor([root_tok], dtype=torch.int32, device=cuda), root_out, root_out, off)
+    torch.cuda.synchronize()
+    want, _, nodes = otd.draft_tree_greedy(od, oc, root_tok, root_out.cpu().numpy(), root_out.cpu().numpy(),
+                                           depth, width, budget)
+    n = int(tree.count.item())
+    assert n == len(want)
+    assert tree.tokens[:n].tolist() == want.tokens
+    assert tree.parents[:n].tolist() == want.parents
+    assert tree.depth[:n].tolist() == want.depth
+    assert int(off.item()) == ctx and oc.offset == ctx
+    # tree entries in the drafter cache: (depth - 1) * width forwarded rows after the context
+    t = (depth - 1) * width
+    k_gpu = cache[0].keys[0, :, ctx:ctx + t].float().cpu().numpy()
+    k_ref = oc.keys_f32(0)[:, ctx:ctx + t]
+    assert np.abs(k_gpu - k_ref).max() / np.abs(k_ref).max() <= tol
+    return tdr, tree
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_small_tree_matches_oracle(cuda, kv_dtype):
+    _run(cuda, _small_cfg(), 1024, 40, 256, kv_dtype, depth=4, width=3, budget=10, seed=2, tol=1e-5 if
+         kv_dtype == torch.float32 else 1e-2)
+
+
+def test_every_node_kept_when_within_budget(cuda):
+    tdr, tree = _run(cuda, _small_cfg(), 1024, 24, 128, torch.float32, depth=3, width=2, budget=64, seed=4, tol=1e-5)
+    assert int(tree.count.item()) == tdr.n_nodes == 1 + 2 + 2 * 4
+
+
+def test_width_one_is_a_chain(cuda):
+    _, tree = _run(cuda, _small_cfg(), 1024, 30, 128, torch.float32, depth=4, width=1, budget=4, seed=6, tol=1e-5)
+    assert tree.parents[:5].tolist() == [-1, 0, 1, 2, 3]
+
+
+def test_qwen3_1p7b_config5_tree(cuda):
+    from woodcock_amd.config import qwen3_1p7b_drafter
+
+    _run(cuda, qwen3_1p7b_drafter(), 16384, 512, 1024, torch.bfloat16, depth=6, width=4, budget=59, seed=8,
+         tol=1e-2)
+
+
+def test_enqueue_never_synchronises(cuda):
+    from woodcock_amd.tree_draft import TreeDrafter
+
+    d, cache, _, _, root_out = _setup(cuda, _small_cfg(), 1024, 20, 128, torch.float32, 9)
+    tdr = TreeDrafter(d, cache, 3, 3, 8)
+    tok = torch.tensor([3], dtype=torch.int32, device=cuda)
+    off = torch.tensor([20], dtype=torch.int32, device=cuda)
+    tdr.draft(tok, root_out, root_out, off)  # warm-up
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        tdr.draft(tok, root_out, root_out, off)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    assert int(tdr.tree.count.item()) == 9

@@ -439,7 +439,6 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
              "wc_drafter_forward: feature row stride must be >= hidden_size and a multiple of 4");
   WC_REQUIRE(al16(feat) && al16(hidden_out) && (out_out == nullptr || al16(out_out)),
              "wc_drafter_forward: buffers must be 16-byte aligned");
-  WC_REQUIRE(feat_row_dev == nullptr || rows == 1, "wc_drafter_forward: a gathered feature row needs rows == 1");
   WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
              "wc_drafter_forward: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
   WC_REQUIRE(mask_dev == nullptr || mask_ld >= rows, "wc_drafter_forward: mask row stride too small");
@@ -483,7 +482,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       if (li == 0) {
         xin.x = feat + (feat_row_dev ? 0 : t0 * feat_ld);
         xin.ld = feat_ld;
-        xin.row_idx = feat_row_dev;
+        xin.row_idx = feat_row_dev ? feat_row_dev + t0 : nullptr;
         xin.row_add = feat_row_dev ? feat_row_add : 0;
       } else {
         xin.x = hidden_out + t0 * d.hidden;

@@ -10,6 +10,25 @@
 // nonzero entry in vocabulary order, key log q(x) - log(-log u), the k largest
 // keys in descending order.  Rows consume the stream one after another (the
 // reference draws every frontier node from one generator, spec.py:238-249).
+//
+// Greedy tree drafting on the device (python/woodcock/spec.py:216-303 with
+// StaticPolicy, python/woodcock/policies.py:49-75): a node table in a
+// caller-owned state buffer, filled level by level without a host round trip.
+//   wc_tree_draft_begin     node 0 = the root token;
+//   wc_tree_draft_expand    the `width` most probable head rows of each
+//                           frontier row's draft distribution become children
+//                           (token = d2t[row], phat = phat(parent) * q), in
+//                           descending q order, the lower head row first on a tie;
+//   wc_tree_draft_frontier  the `width` level nodes of largest phat (ties: the
+//                           earlier node) become the next frontier, with the
+//                           drafter inputs of that forward: tokens, the rows of
+//                           their parents' feedback, positions base - 1 + depth
+//                           and the attention mask (the prefix within the
+//                           window, the cache slots of the ancestors below the
+//                           root, the node's own slot);
+//   wc_tree_draft_select    the verified tree: every node, or the root plus the
+//                           `budget` nodes of largest phat (ties: shallower,
+//                           then earlier) in node order, parents remapped.
 #include "wc_common.h"
 
 namespace wc {
@@ -43,6 +62,184 @@ __global__ __launch_bounds__(kMaskThreads) void k_tree_mask(const int32_t* __res
   const int cols = prefix + n;
   for (int c = blockIdx.x * kMaskThreads + threadIdx.x; c < cols; c += gridDim.x * kMaskThreads)
     row[c] = c < prefix ? 1 : static_cast<uint8_t>((anc >> (c - prefix)) & 1ull);
+}
+
+// ------------------------------------------------------------------ greedy tree drafting
+
+constexpr int kTdMaxNodes = 512;
+constexpr int kTdMaxWidth = 8;
+constexpr int kTdThreads = 256;
+
+struct TreeDraftState {
+  double phat[kTdMaxNodes];
+  int32_t token[kTdMaxNodes], parent[kTdMaxNodes], depth[kTdMaxNodes];
+  int32_t slot[kTdMaxNodes];   // drafter cache slot once forwarded
+  int32_t store[kTdMaxNodes];  // row of the node's out / feedback once forwarded (the root: 0)
+  int32_t front[kTdMaxWidth];  // node ids of the current frontier, in frontier-row order
+};
+
+__global__ void k_td_begin(TreeDraftState* st, const int32_t* __restrict__ root_token) {
+  if (threadIdx.x == 0) {
+    st->token[0] = *root_token;
+    st->parent[0] = -1;
+    st->depth[0] = 0;
+    st->phat[0] = 1.0;
+    st->slot[0] = -1;
+    st->store[0] = 0;
+    st->front[0] = 0;
+  }
+}
+
+// Largest key over the block (every thread receives it).
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* red) {
+  v = wave_max_u64(v);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  unsigned long long b = 0;
+#pragma unroll
+  for (int w = 0; w < kTdThreads / kWave; ++w) b = red[w] > b ? red[w] : b;
+  return b;
+}
+
+// Block r: the `width` largest (q, lowest row first) entries of q row r.  Each
+// thread keeps a sorted top-width list of its stride of the row; `width`
+// block-wide maxima then pop the winners in order.
+__global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, const float* __restrict__ q,
+                                                          int head_rows, int64_t ld_q,
+                                                          const int32_t* __restrict__ d2t, int width,
+                                                          int node_base) {
+  __shared__ unsigned long long red[kTdThreads / kWave];
+  const int r = blockIdx.x, t = threadIdx.x;
+  const float* qr = q + static_cast<int64_t>(r) * ld_q;
+  unsigned long long top[kTdMaxWidth];
+#pragma unroll
+  for (int j = 0; j < kTdMaxWidth; ++j) top[j] = 0;
+  for (int i = t; i < head_rows; i += kTdThreads) {
+    unsigned long long k = argmax_key(qr[i], i);
+#pragma unroll
+    for (int j = 0; j < kTdMaxWidth; ++j) {
+      const bool take = j < width && k > top[j];
+      const unsigned long long o = top[j];
+      top[j] = take ? k : o;
+      k = take ? o : k;
+    }
+  }
+  const int v = st->front[r];
+  for (int j = 0; j < width; ++j) {
+    const unsigned long long best = block_max_u64(top[0], red);
+    if (best != 0 && top[0] == best) {  // keys are unique (the row is in the key): one owner pops
+#pragma unroll
+      for (int i = 0; i + 1 < kTdMaxWidth; ++i) top[i] = top[i + 1];
+      top[kTdMaxWidth - 1] = 0;
+    }
+    if (t == 0) {
+      const int row = argmax_key_index(best);
+      const int c = node_base + r * width + j;
+      st->token[c] = d2t ? d2t[row] : row;
+      st->parent[c] = v;
+      st->depth[c] = st->depth[v] + 1;
+      st->phat[c] = st->phat[v] * static_cast<double>(qr[row]);
+      st->slot[c] = -1;
+      st->store[c] = -1;
+    }
+  }
+}
+
+// One block: next frontier among the level's nodes [lb, le) and the inputs of
+// its drafter forward.
+__global__ __launch_bounds__(kTdThreads) void k_td_frontier(TreeDraftState* st, int lb, int le, int width,
+                                                            const int32_t* __restrict__ offset_dev, int tree_cache,
+                                                            int window, int store_base, int32_t* __restrict__ tokens,
+                                                            int32_t* __restrict__ feat_rows,
+                                                            int32_t* __restrict__ positions,
+                                                            uint8_t* __restrict__ mask, int64_t mask_ld) {
+  __shared__ int s_front[kTdMaxWidth];
+  __shared__ int s_anc[kTdMaxWidth][kTdMaxNodes / kTdMaxWidth];
+  __shared__ int s_nanc[kTdMaxWidth];
+  const int t = threadIdx.x;
+  const int n = le - lb, m = min(width, n);
+  for (int i = t; i < n; i += kTdThreads) {
+    const int v = lb + i;
+    const double ph = st->phat[v];
+    int rank = 0;
+    for (int u = lb; u < le; ++u) {
+      const double pu = st->phat[u];
+      rank += (pu > ph || (pu == ph && u < v)) ? 1 : 0;
+    }
+    if (rank < m) s_front[rank] = v;
+  }
+  __syncthreads();
+  const int base = *offset_dev;
+  if (t < m) {
+    const int v = s_front[t];
+    st->front[t] = v;
+    tokens[t] = st->token[v];
+    feat_rows[t] = st->store[st->parent[v]];
+    positions[t] = base - 1 + st->depth[v];
+    st->slot[v] = base + tree_cache + t;
+    st->store[v] = store_base + t;
+    // cache slots of the ancestors below the root
+    int na = 0;
+    for (int u = st->parent[v]; u > 0 && na < kTdMaxNodes / kTdMaxWidth; u = st->parent[u]) s_anc[t][na++] = st->slot[u];
+    s_nanc[t] = na;
+  }
+  __syncthreads();
+  for (int r = 0; r < m; ++r) {
+    const int v = s_front[r];
+    const int pos = base - 1 + st->depth[v];
+    const int lo = window > 0 ? max(0, pos - window + 1) : 0;
+    const int self = base + tree_cache + r, na = s_nanc[r];
+    uint8_t* row = mask + static_cast<int64_t>(r) * mask_ld;
+    for (int64_t c = t; c < mask_ld; c += kTdThreads) {
+      bool on = (c >= lo && c < base) || c == self;
+      for (int k = 0; k < na; ++k) on = on || c == s_anc[r][k];
+      row[c] = on ? 1 : 0;
+    }
+  }
+}
+
+// One block: the verified subset in node order with parents remapped.
+__global__ __launch_bounds__(kTdThreads) void k_td_select(const TreeDraftState* st, int n_nodes, int budget,
+                                                          int32_t* __restrict__ tokens, int32_t* __restrict__ parents,
+                                                          int32_t* __restrict__ depth, int32_t* __restrict__ count) {
+  __shared__ int s_pos[kTdMaxNodes];
+  const int t = threadIdx.x;
+  const bool all = n_nodes - 1 <= budget;
+  for (int v = t; v < n_nodes; v += kTdThreads) {
+    bool keep = v == 0 || all;
+    if (!keep) {
+      const double ph = st->phat[v];
+      const int dv = st->depth[v];
+      int rank = 0;
+      for (int u = 1; u < n_nodes; ++u) {
+        const double pu = st->phat[u];
+        const int du = st->depth[u];
+        rank += (pu > ph || (pu == ph && (du < dv || (du == dv && u < v)))) ? 1 : 0;
+      }
+      keep = rank < budget;
+    }
+    s_pos[v] = keep ? 1 : 0;
+  }
+  __syncthreads();
+  if (t == 0) {  // exclusive scan; -1 marks a dropped node
+    int k = 0;
+    for (int v = 0; v < n_nodes; ++v) {
+      const int kept = s_pos[v];
+      s_pos[v] = kept ? k : -1;
+      k += kept;
+    }
+    *count = k;
+  }
+  __syncthreads();
+  for (int v = t; v < n_nodes; v += kTdThreads) {
+    const int i = s_pos[v];
+    if (i < 0) continue;
+    const int p = st->parent[v];
+    tokens[i] = st->token[v];
+    depth[i] = st->depth[v];
+    parents[i] = p < 0 ? -1 : s_pos[p];
+  }
 }
 
 // ------------------------------------------------------------------ Gumbel-top-k
@@ -200,6 +397,63 @@ int wc_sample_without_replacement(const float* q, int rows, int head_rows, int64
   hipLaunchKernelGGL(k_gumbel_topk, dim3(1), dim3(kGkThreads), 0, reinterpret_cast<hipStream_t>(stream), q, rows,
                      head_rows, ld_q, d2t_dev, k_dev, k_max, static_cast<unsigned long long>(rng->seed),
                      rng->round_dev, rng->purpose, static_cast<long long>(uniform_base), tokens_out, counts_out);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+size_t wc_tree_draft_state_bytes(void) { return sizeof(wc::TreeDraftState); }
+
+int wc_tree_draft_begin(void* state, const int32_t* root_token_dev, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && root_token_dev, "wc_tree_draft_begin: NULL buffer");
+  hipLaunchKernelGGL(k_td_begin, dim3(1), dim3(kWave), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<TreeDraftState*>(state), root_token_dev);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_tree_draft_expand(void* state, const float* q, int rows, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
+                         int width, int node_base, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && q, "wc_tree_draft_expand: NULL buffer");
+  WC_REQUIRE(width >= 1 && width <= kTdMaxWidth, "wc_tree_draft_expand: width must be in 1..%d", kTdMaxWidth);
+  WC_REQUIRE(rows >= 1 && rows <= kTdMaxWidth, "wc_tree_draft_expand: rows must be in 1..%d", kTdMaxWidth);
+  WC_REQUIRE(head_rows >= width && ld_q >= head_rows, "wc_tree_draft_expand: need head_rows >= width, ld_q >= head_rows");
+  WC_REQUIRE(node_base >= 1 && node_base + rows * width <= kTdMaxNodes,
+             "wc_tree_draft_expand: nodes %d..%d outside the table of %d", node_base, node_base + rows * width,
+             kTdMaxNodes);
+  hipLaunchKernelGGL(k_td_expand, dim3(rows), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<TreeDraftState*>(state), q, head_rows, ld_q, d2t_dev, width, node_base);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_tree_draft_frontier(void* state, int level_begin, int level_end, int width, const int32_t* offset_dev,
+                           int tree_cache, int window, int store_base, int32_t* tokens_out, int32_t* feat_rows_out,
+                           int32_t* positions_out, uint8_t* mask_out, int64_t mask_ld, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && offset_dev && tokens_out && feat_rows_out && positions_out && mask_out,
+             "wc_tree_draft_frontier: NULL buffer");
+  WC_REQUIRE(width >= 1 && width <= kTdMaxWidth, "wc_tree_draft_frontier: width must be in 1..%d", kTdMaxWidth);
+  WC_REQUIRE(level_begin >= 1 && level_end > level_begin && level_end <= kTdMaxNodes,
+             "wc_tree_draft_frontier: bad level range %d..%d", level_begin, level_end);
+  WC_REQUIRE(tree_cache >= 0 && store_base >= 1 && mask_ld >= 1, "wc_tree_draft_frontier: bad offsets");
+  hipLaunchKernelGGL(k_td_frontier, dim3(1), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<TreeDraftState*>(state), level_begin, level_end, width, offset_dev, tree_cache,
+                     window, store_base, tokens_out, feat_rows_out, positions_out, mask_out, mask_ld);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_tree_draft_select(const void* state, int n_nodes, int budget, int32_t* tokens_out, int32_t* parents_out,
+                         int32_t* depth_out, int32_t* count_out, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && tokens_out && parents_out && depth_out && count_out, "wc_tree_draft_select: NULL buffer");
+  WC_REQUIRE(n_nodes >= 1 && n_nodes <= kTdMaxNodes, "wc_tree_draft_select: n_nodes must be in 1..%d", kTdMaxNodes);
+  WC_REQUIRE(budget >= 0, "wc_tree_draft_select: negative budget");
+  hipLaunchKernelGGL(k_td_select, dim3(1), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const TreeDraftState*>(state), n_nodes, budget, tokens_out, parents_out, depth_out,
+                     count_out);
   WC_LAUNCHED();
   return WC_OK;
 }

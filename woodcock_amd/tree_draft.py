@@ -1,0 +1,134 @@
+"""Greedy tree drafting on the device: the level loop of SpeculativeDecoder._draft
+with a StaticPolicy (python/woodcock/spec.py:216-303; python/woodcock/policies.py:49-75)
+without a host round trip per level.
+
+Per level the frontier's drafter outputs go through the draft head (logits over
+the head rows), the T = 1 softmax (spec.py:120-121), ``wc_tree_draft_expand``
+(top-``width`` children per frontier row, phat products) and, unless the level
+is the last, ``wc_tree_draft_frontier`` (top-``width`` nodes by phat become the
+next frontier; it writes their tokens, parent-feedback rows, positions and
+attention mask) and one drafter forward over the frontier rows, appended to
+the drafter cache at offset + tree entries so far.  The cache offset itself
+never moves: the reference rolls it back to the round's base after drafting
+(spec.py:295-296).  ``wc_tree_draft_select`` then writes the verified tree.
+
+Every launch is stream-ordered and nothing is read back: ``draft`` returns
+device tensors (tokens, parents, depth, count).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .drafter import Drafter
+from .runtime import device_of, ptr, stream_ptr, workspace
+
+
+@dataclass
+class DeviceTree:
+    tokens: torch.Tensor   # [max_nodes] int32, the first `count` valid
+    parents: torch.Tensor  # [max_nodes] int32 (-1 for the root)
+    depth: torch.Tensor    # [max_nodes] int32
+    count: torch.Tensor    # [1] int32
+
+
+class TreeDrafter:
+    """Static greedy tree shape: ``max_depth`` levels, ``width`` children per
+    frontier node and ``width`` frontier nodes per level, ``budget`` verified
+    nodes besides the root (StaticPolicy(depth, width, budget))."""
+
+    def __init__(self, drafter: Drafter, cache, max_depth: int, width: int, budget: int | None = None):
+        if width < 1 or width > 8:
+            raise ValueError("width must be in 1..8")
+        if max_depth < 1:
+            raise ValueError("max_depth must be positive")
+        self.d = drafter
+        self.cache = cache
+        self.max_depth, self.width = max_depth, width
+        self.budget = budget if budget is not None else (max_depth if width == 1 else 4 * max_depth)
+        dev = drafter.device
+        self.device = dev
+        # static shape: level 1 has `width` nodes, every later level width * width
+        self.levels = []  # (node_base, rows) of each level's expansion
+        n, rows = 1, 1
+        for _ in range(max_depth):
+            self.levels.append((n, rows))
+            n += rows * width
+            rows = min(width, rows * width)
+        self.n_nodes = n
+        if self.n_nodes > 512:
+            raise ValueError(f"tree of {self.n_nodes} nodes exceeds the 512-node table")
+        hid = drafter.cfg.hidden_size
+        self.n_store = 1 + (max_depth - 1) * width  # root + every forwarded frontier row
+        self.store_hid = torch.zeros(self.n_store, hid, dtype=torch.float32, device=dev)
+        self.store_out = torch.zeros(self.n_store, hid, dtype=torch.float32, device=dev)
+        head_rows = drafter._head.shape[0]
+        self.logits = torch.empty(width, head_rows, dtype=torch.float32, device=dev)
+        self.q = torch.empty_like(self.logits)
+        self.tok_rows = torch.empty(width, dtype=torch.int32, device=dev)
+        self.tokens = torch.empty(width, dtype=torch.int32, device=dev)
+        self.feat_rows = torch.empty(width, dtype=torch.int32, device=dev)
+        self.positions = torch.empty(width, dtype=torch.int32, device=dev)
+        cap = cache[0].capacity
+        self.mask = torch.zeros(width, cap, dtype=torch.uint8, device=dev)
+        self.state = torch.zeros(int(_lib.lib().wc_tree_draft_state_bytes()), dtype=torch.uint8, device=dev)
+        self.tree = DeviceTree(torch.zeros(self.n_nodes, dtype=torch.int32, device=dev),
+                               torch.zeros(self.n_nodes, dtype=torch.int32, device=dev),
+                               torch.zeros(self.n_nodes, dtype=torch.int32, device=dev),
+                               torch.zeros(1, dtype=torch.int32, device=dev))
+
+    def draft(self, root_token: torch.Tensor, root_out: torch.Tensor, root_fb: torch.Tensor,
+              offset_dev: torch.Tensor) -> DeviceTree:
+        """root_token [1] int32 (device), root_out / root_fb [hidden] fp32 rows, the
+        drafter's context length n = *offset_dev.  Enqueue only.  With post_norm
+        the feedback of a node is its `out` (drafter.py:193-194), so root_fb is
+        read only when post_norm is off."""
+        device_of(root_out)
+        d, w = self.d, self.width
+        cfg = d.cfg
+        hidden = cfg.hidden_size
+        s = stream_ptr()
+        # store row 0: the root; row 1 + (level - 1) * width + r: frontier row r of a level
+        self.store_out[0].copy_(root_out.reshape(hidden))
+        self.store_hid[0].copy_(root_fb.reshape(hidden))
+        fb_store = self.store_out if cfg.post_norm else self.store_hid
+        _lib.call("wc_tree_draft_begin", ptr(self.state), ptr(root_token), s)
+        cache = self.cache
+        cap = cache[0].capacity
+        kp = (C.c_void_p * len(cache))(*[c.keys.data_ptr() for c in cache])
+        vp = (C.c_void_p * len(cache))(*[c.values.data_ptr() for c in cache])
+        kvdt = _lib.WC_BF16 if cache[0].keys.dtype == torch.bfloat16 else _lib.WC_F32
+        head_rows = self.logits.shape[1]
+        tree_cache = 0
+        store_row = 0  # first store row of the current frontier
+        for depth, (node_base, rows) in enumerate(self.levels, start=1):
+            # (a) children of every frontier node: head logits, q = softmax(z), top-width
+            _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]), hidden,
+                      None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None, None,
+                      ptr(d.ws), s)
+            _lib.call("wc_probs_from_logits", ptr(self.logits), rows, head_rows, self.logits.stride(0), 1.0,
+                      ptr(self.q), self.q.stride(0), ptr(workspace(d.device)), s)
+            _lib.call("wc_tree_draft_expand", ptr(self.state), ptr(self.q), rows, head_rows, self.q.stride(0),
+                      ptr(d._vocab_ids), w, node_base, s)
+            if depth == self.max_depth:
+                break
+            # (b) the most probable nodes of this level become the frontier and are forwarded
+            lb, le = node_base, node_base + rows * w
+            m = min(w, le - lb)
+            store_base = 1 + (depth - 1) * w
+            _lib.call("wc_tree_draft_frontier", ptr(self.state), lb, le, w, ptr(offset_dev), tree_cache,
+                      int(cfg.window or 0), store_base, ptr(self.tokens), ptr(self.feat_rows), ptr(self.positions),
+                      ptr(self.mask), self.mask.stride(0), s)
+            _lib.call("wc_drafter_forward", C.byref(d.dims), C.byref(d.wstruct), ptr(self.tokens), ptr(fb_store),
+                      fb_store.stride(0), ptr(self.feat_rows), 0, m, None, kp, vp, kvdt, cap, ptr(offset_dev),
+                      tree_cache, ptr(self.positions), ptr(self.mask), self.mask.stride(0),
+                      ptr(self.store_hid[store_base]), ptr(self.store_out[store_base]), None, ptr(d.ws), s)
+            tree_cache += m
+            store_row = store_base
+        t = self.tree
+        _lib.call("wc_tree_draft_select", ptr(self.state), self.n_nodes, self.budget, ptr(t.tokens), ptr(t.parents),
+                  ptr(t.depth), ptr(t.count), s)
+        return t
