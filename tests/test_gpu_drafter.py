@@ -318,3 +318,26 @@ def test_head_dim_sweep_multi_row_forward(cuda, head_dim, heads, kv_heads):
         assert _rel(out.cpu().numpy(), oout) <= 1e-5, L
         n = oc.offset
         assert _rel(cache[0].keys[0, :, :n].cpu().numpy(), oc.keys_f32(0)[:, :n]) <= 1e-5, L
+
+
+def test_saved_drafter_reloads_and_computes_identically(cuda, tmp_path):
+    """Drafter.save -> Drafter.load (config.json, model.safetensors, woodcock.json;
+    python/woodcock/export.py:55-63 self-check): identical forward and head."""
+    from woodcock_amd.config import DrafterConfig
+    from woodcock_amd.drafter import Drafter
+
+    cfg = DrafterConfig(hidden_size=256, num_layers=1, num_heads=4, num_kv_heads=2, head_dim=64,
+                        intermediate_size=512, vocab_size=2048, target_hidden_size=192)
+    d = Drafter.from_synthetic(cfg, seed=3, device=cuda, kv_dtype=torch.float32)
+    d.save(tmp_path)
+    e = Drafter.load(tmp_path, device=cuda, kv_dtype=torch.float32)
+    g = torch.Generator(device=cuda).manual_seed(1)
+    feat = torch.randn(3, cfg.hidden_size, generator=g, device=cuda)
+    toks = torch.tensor([5, 77, 1000], dtype=torch.int32, device=cuda)
+    outs = []
+    for m in (d, e):
+        cache = m.make_cache(16)
+        hid, out = m(toks, feat, cache)
+        outs.append((hid, out, m.draft(out)))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[0][2], outs[1][2])

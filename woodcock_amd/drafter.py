@@ -11,7 +11,6 @@ ABI on the current stream; nothing falls back to the CPU.
 from __future__ import annotations
 
 import ctypes as C
-from pathlib import Path
 
 import numpy as np
 import torch
@@ -122,14 +121,13 @@ class Drafter:
         return cls(cfg, random_drafter(cfg, seed=seed, device=device, head_rows=head_rows), device, kv_dtype)
 
     @classmethod
-    def load(cls, path, device="cuda", kv_dtype=torch.bfloat16) -> "Drafter":
-        """A drafter directory in the reference format: config.json + model.safetensors
-        (python/woodcock/drafter.py:310-330)."""
-        from safetensors.torch import load_file
+    def load(cls, path, device="cuda", kv_dtype=torch.bfloat16, verify_sha: bool = True) -> "Drafter":
+        """A local drafter directory in the reference format: config.json +
+        model.safetensors, checked against woodcock.json when present
+        (python/woodcock/drafter.py:321-330; python/woodcock/export.py:1-64)."""
+        from .weights import read_drafter_dir
 
-        path = Path(path)
-        cfg = DrafterConfig.load(path / "config.json")
-        weights = load_file(str(path / "model.safetensors"), device="cpu")
+        cfg, weights, _ = read_drafter_dir(path, verify_sha)
         return cls(cfg, weights, device, kv_dtype)
 
     # ------------------------------------------------------------------ caches
@@ -279,13 +277,10 @@ class Drafter:
         self._vocab_ids = ids_t.to(self.device, torch.int32)
         self._build_structs(self._rope[0].shape[0])
 
-    def save(self, path) -> None:
+    def save(self, path, target_name: str | None = None) -> None:
+        """config.json + model.safetensors + woodcock.json (drafter.py:310-319; export.py:27-53)."""
         if self._vocab_ids is not None:
             raise ValueError("a drafter with a restricted vocabulary cannot be saved")
-        from safetensors.torch import save_file
+        from .weights import write_drafter_dir
 
-        path = Path(path)
-        path.mkdir(parents=True, exist_ok=True)
-        self.cfg.save(path / "config.json")
-        save_file({k: v.cpu() for k, v in self.w.items()}, str(path / "model.safetensors"),
-                  metadata={"format": "woodcock-drafter-v1"})
+        write_drafter_dir(path, self.cfg, self.w, target_name)
