@@ -319,11 +319,24 @@ def bench_gpu(args):
     def target_tree():
         tm(tm_tok60, tm_cache, toff, tpos, tmask, logits=tm_logits, taps=tm_taps)
 
+    # greedy tree drafting on the device at the config-5 shape: depth 6, width 4,
+    # 59 verified nodes + root, drafter context 512 (six head + softmax + expand
+    # levels, five frontier forwards of 4 rows, the verify-set selection)
+    from woodcock_amd.tree_draft import TreeDrafter
+
+    tdr = TreeDrafter(d, rnd.cache, 6, 4, 59)
+    td_tok = torch.tensor([7], dtype=torch.int32, device=out1.device)
+    td_off = torch.tensor([BASE_CTX], dtype=torch.int32, device=out1.device)
+    td_root = torch.randn(cfg.hidden_size, device=out1.device)
+
+    def tree_drafts():
+        tdr.draft(td_tok, td_root, td_root, td_off)
+
     comps = {}
-    reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1}
+    reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1, "tree_draft": 1}
     for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
                      ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies),
-                     ("target_chain", target_chain), ("target_tree", target_tree)):
+                     ("target_chain", target_chain), ("target_tree", target_tree), ("tree_draft", tree_drafts)):
         fn()
         torch.cuda.synchronize()
         g = capture(fn)
@@ -352,6 +365,7 @@ def bench_gpu(args):
         "tree_verify_us": comps["tree_verify"],
         "target_chain_us": comps["target_chain"],
         "target_tree_us": comps["target_tree"],
+        "tree_draft_us": comps["tree_draft"],
         "head_bytes": head_bytes,
         "step_bytes": step_bytes,
         "compact_bytes_avg": compact_bytes,
@@ -371,7 +385,7 @@ def bench_gpu(args):
 # each scaled by what the same counter reads for a plain copy kernel of known
 # size run in the same process.  `bench.py --pmc-summary FETCH_DIR WRITE_DIR`
 # turns the two counter CSVs into the committed summary that later runs read.
-HEAD_KERNEL = "k_gemv1<4, false, 1, 4, 0>"
+HEAD_KERNEL = "k_gemv1<4, false, 1, 4, 0, 1>"
 PROBE_HEADS = 16
 PROBE_COPIES = 4
 PROBE_COPY_FLOATS = 64 << 20  # 256 MiB read + 256 MiB written per copy
@@ -609,6 +623,7 @@ def main():
             "verify_tree_greedy_us_n60": round(r["tree_verify_us"], 2),
             "target_forward_us_qwen3_1p7b_28l_m5_ctx512": round(r["target_chain_us"], 1),
             "target_forward_us_qwen3_1p7b_28l_m60_tree_ctx2048": round(r["target_tree_us"], 1),
+            "tree_draft_us_qwen3_1p7b_depth6_width4_n60": round(r["tree_draft_us"], 1),
             "head_gemv_us": round(r["head_us"], 2),
         },
         "roofline": {

@@ -103,8 +103,10 @@ __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v
 }
 
 // Block r: the `width` largest (q, lowest row first) entries of q row r.  Each
-// thread keeps a sorted top-width list of its stride of the row; `width`
-// block-wide maxima then pop the winners in order.
+// thread keeps a sorted top-width list of its share of the row, read as
+// 16-byte vectors kTdVec at a time (all loads of a pass issued before the
+// first insert); `width` block-wide maxima then pop the winners in order.
+constexpr int kTdVec = 8;
 __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, const float* __restrict__ q,
                                                           int head_rows, int64_t ld_q,
                                                           const int32_t* __restrict__ d2t, int width,
@@ -115,8 +117,8 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
   unsigned long long top[kTdMaxWidth];
 #pragma unroll
   for (int j = 0; j < kTdMaxWidth; ++j) top[j] = 0;
-  for (int i = t; i < head_rows; i += kTdThreads) {
-    unsigned long long k = argmax_key(qr[i], i);
+  auto insert = [&](float v, int i) {
+    unsigned long long k = argmax_key(v, i);
 #pragma unroll
     for (int j = 0; j < kTdMaxWidth; ++j) {
       const bool take = j < width && k > top[j];
@@ -124,7 +126,27 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
       top[j] = take ? k : o;
       k = take ? o : k;
     }
+  };
+  // 16-byte vectors where the row is 16-byte aligned, the tail (and unaligned rows) element-wise
+  const bool al = (reinterpret_cast<uintptr_t>(qr) & 15) == 0;
+  const int n4 = al ? head_rows / 4 : 0;
+  const float4* q4 = reinterpret_cast<const float4*>(qr);
+  for (int b = 0; b < n4; b += kTdThreads * kTdVec) {
+    float4 v[kTdVec];
+#pragma unroll
+    for (int u = 0; u < kTdVec; ++u) v[u] = q4[min(b + u * kTdThreads + t, n4 - 1)];
+#pragma unroll
+    for (int u = 0; u < kTdVec; ++u) {
+      const int i4 = b + u * kTdThreads + t;
+      if (i4 < n4) {
+        insert(v[u].x, 4 * i4);
+        insert(v[u].y, 4 * i4 + 1);
+        insert(v[u].z, 4 * i4 + 2);
+        insert(v[u].w, 4 * i4 + 3);
+      }
+    }
   }
+  for (int i = 4 * n4 + t; i < head_rows; i += kTdThreads) insert(qr[i], i);
   const int v = st->front[r];
   for (int j = 0; j < width; ++j) {
     const unsigned long long best = block_max_u64(top[0], red);
@@ -157,17 +179,19 @@ __global__ __launch_bounds__(kTdThreads) void k_td_frontier(TreeDraftState* st, 
   __shared__ int s_front[kTdMaxWidth];
   __shared__ int s_anc[kTdMaxWidth][kTdMaxNodes / kTdMaxWidth];
   __shared__ int s_nanc[kTdMaxWidth];
+  __shared__ double s_ph[kTdMaxNodes];
   const int t = threadIdx.x;
   const int n = le - lb, m = min(width, n);
+  for (int i = t; i < n; i += kTdThreads) s_ph[i] = st->phat[lb + i];
+  __syncthreads();
   for (int i = t; i < n; i += kTdThreads) {
-    const int v = lb + i;
-    const double ph = st->phat[v];
+    const double ph = s_ph[i];
     int rank = 0;
-    for (int u = lb; u < le; ++u) {
-      const double pu = st->phat[u];
-      rank += (pu > ph || (pu == ph && u < v)) ? 1 : 0;
+    for (int u = 0; u < n; ++u) {
+      const double pu = s_ph[u];
+      rank += (pu > ph || (pu == ph && u < i)) ? 1 : 0;
     }
-    if (rank < m) s_front[rank] = v;
+    if (rank < m) s_front[rank] = lb + i;
   }
   __syncthreads();
   const int base = *offset_dev;
@@ -204,17 +228,24 @@ __global__ __launch_bounds__(kTdThreads) void k_td_select(const TreeDraftState* 
                                                           int32_t* __restrict__ tokens, int32_t* __restrict__ parents,
                                                           int32_t* __restrict__ depth, int32_t* __restrict__ count) {
   __shared__ int s_pos[kTdMaxNodes];
+  __shared__ double s_ph[kTdMaxNodes];
+  __shared__ int s_dep[kTdMaxNodes];
   const int t = threadIdx.x;
   const bool all = n_nodes - 1 <= budget;
   for (int v = t; v < n_nodes; v += kTdThreads) {
+    s_ph[v] = st->phat[v];
+    s_dep[v] = st->depth[v];
+  }
+  __syncthreads();
+  for (int v = t; v < n_nodes; v += kTdThreads) {
     bool keep = v == 0 || all;
     if (!keep) {
-      const double ph = st->phat[v];
-      const int dv = st->depth[v];
+      const double ph = s_ph[v];
+      const int dv = s_dep[v];
       int rank = 0;
       for (int u = 1; u < n_nodes; ++u) {
-        const double pu = st->phat[u];
-        const int du = st->depth[u];
+        const double pu = s_ph[u];
+        const int du = s_dep[u];
         rank += (pu > ph || (pu == ph && (du < dv || (du == dv && u < v)))) ? 1 : 0;
       }
       keep = rank < budget;
