@@ -15,6 +15,7 @@
 // read from device memory.
 #include "attention.h"
 #include "gemv.h"
+#include "gemvf.h"
 
 namespace wc {
 
@@ -154,6 +155,35 @@ static bool launch_gemvx_r(const GemvArgs& a, int steps, hipStream_t s) {
   return launch_gemvx_m<1, PAIR, NIN, XB, MM>(a, steps, s);
 }
 
+// Few-row MFMA GEMV: 16 (TW = 1) or 32 (TW = 2, and the gate / up pair) rows
+// per block, every K a multiple of 32, no last-block norm / normalised-input
+// epilogues (those are the one-row kernel's; a bare offset advance is done).
+template <bool PAIR, int NIN, int XB>
+static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
+  if (a.M < 2 || a.M > kMaxM || a.fin_gain || a.xn_out) return false;
+  int gb = 0;
+  for (int i = 0; i < a.n_in; ++i) {
+    if (a.in[i].K % 32 != 0) return false;
+    if (a.in[i].gain) gb |= 1 << i;
+  }
+  constexpr int kAll = (1 << NIN) - 1;
+  const bool wide = PAIR || a.N >= 8192;
+  const int rb = PAIR ? 16 : wide ? 32 : 16;
+  const dim3 grid((a.N + rb - 1) / rb);
+#define WC_GF(TW, GBV)                                                                                 \
+  hipLaunchKernelGGL((k_gemvf<TW, TW == 1 ? 8 : 4, TW == 1 ? 6 : 4, PAIR, NIN, XB, GBV>), grid,           \
+                     dim3((TW == 1 ? 8 : 4) * kWave), 0, s, a)
+  if (gb == kAll) {
+    if (wide) WC_GF(2, kAll); else if constexpr (!PAIR) WC_GF(1, kAll);
+  } else if constexpr (NIN == 1) {
+    if (wide) WC_GF(2, 0); else if constexpr (!PAIR) WC_GF(1, 0);
+  } else {
+    return false;
+  }
+#undef WC_GF
+  return true;
+}
+
 template <bool PAIR, int NIN, int XB>
 static bool launch_gemvx(const GemvArgs& a, int steps, hipStream_t s) {
   if (a.M <= 2) return launch_gemvx_r<PAIR, NIN, XB, 2>(a, steps, s);
@@ -198,7 +228,19 @@ static int launch_gemv(const GemvArgs& a, int /*R hint*/, hipStream_t s) {
   const int steps = max_k / 512;
   const bool pair = a.epi == kEpiSiluPair;
   bool done = false;
-  if (a.M > 1 && k512) {
+  if (a.M > 1) {
+    if (pair && a.n_in == 1 && xb == 0)
+      done = launch_gemvf<true, 1, 0>(a, s);
+    else if (!pair && a.n_in == 1 && xb == 0)
+      done = launch_gemvf<false, 1, 0>(a, s);
+    else if (!pair && a.n_in == 2 && xb == 2)
+      done = launch_gemvf<false, 2, 2>(a, s);
+    else if (!pair && a.n_in == 3 && xb == 0)
+      done = launch_gemvf<false, 3, 0>(a, s);
+    else if (!pair && a.n_in == 3 && xb == 7)
+      done = launch_gemvf<false, 3, 7>(a, s);
+  }
+  if (!done && a.M > 1 && k512) {
     if (pair && a.n_in == 1 && xb == 0)
       done = launch_gemvx<true, 1, 0>(a, steps, s);
     else if (!pair && a.n_in == 1 && xb == 0)

@@ -274,7 +274,7 @@ __device__ __forceinline__ void argmax_epilogue(const GemvArgs& a, int m, unsign
   // lanes of the row's slots (kSlots == 32 lanes, half a wave)
   static_assert(kSlots == 32, "one half-wave per row");
   const int j = threadIdx.x % kSlots;
-  for (int mi = threadIdx.x / kSlots; mi < m; mi += kGemvThreads / kSlots) {
+  for (int mi = threadIdx.x / kSlots; mi < m; mi += static_cast<int>(blockDim.x) / kSlots) {
     unsigned long long* sl = &a.slots[(mi * kSlots + j) * kSlotStride];
     unsigned long long best = atomic_load_u64(sl);
     atomic_store_u64(sl, 0ull);
