@@ -229,8 +229,8 @@ def bench_gpu(args):
             _lib.call("wc_kv_compact", kp_, vp_, len(tc), 8, tc[0].capacity, 256, ptr(karr[i, 1:2]),
                       ptr(karr[i, 2:8]), ptr(karr[i, 0:1]), 6, ptr(koff[i:i + 1]), None, s())
 
-    # stochastic accept/reject at k=5 -- target softmax [6,151936], draft softmax
-    # [5,16384] and the rule over device probabilities
+    # stochastic accept/reject at k=5 -- target logits [6,151936] straight into the
+    # rule; the draft softmax [5,16384] timed on its own
     from woodcock_amd.synthetic import draw_rows, stochastic_workload
 
     s_lg, s_dl, s_d2t = stochastic_workload(5, cfg.vocab_size, 16384, seed=args.seed + 5)
@@ -249,14 +249,19 @@ def bench_gpu(args):
     s_verd = torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, device=out1.device)
     sws = ptr(rnd.vws)
 
-    def stochastic():
+    def draft_probs():
+        # the draft distribution q, formed at draft time in a sampling round
         for _ in range(REP):
-            _lib.call("wc_probs_from_logits", ptr(s_tl), 6, s_tl.shape[1], s_tl.stride(0), 1.0, ptr(s_p),
-                      s_p.stride(0), sws, s())
             _lib.call("wc_probs_from_logits", ptr(s_dlg), 5, s_dlg.shape[1], s_dlg.stride(0), 1.0, ptr(s_q),
                       s_q.stride(0), sws, s())
-            _lib.call("wc_verify_chain_stochastic", ptr(s_p), 6, s_p.shape[1], s_p.stride(0), ptr(s_q), 16384,
-                      s_q.stride(0), ptr(s_d2), ptr(s_dr), None, C.byref(s_u), ptr(s_verd), sws, s())
+
+    def stochastic():
+        # the verify step from the target logits: p = softmax(logits / T), accept
+        # tests, residual draw (two launches, p never written)
+        for _ in range(REP):
+            _lib.call("wc_verify_chain_stochastic_logits", ptr(s_tl), 6, s_tl.shape[1], s_tl.stride(0), 1.0,
+                      ptr(s_q), 16384, s_q.stride(0), ptr(s_d2), ptr(s_dr), None, C.byref(s_u), ptr(s_verd), sws,
+                      s())
 
     # one Qwen3-1.7B target layer over a 60-node draft tree (depth <= 6) at context
     # 2048 with the tree mask, then the greedy tree verify over [60, 151936] logits
@@ -335,7 +340,7 @@ def bench_gpu(args):
     comps = {}
     reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1, "tree_draft": 1}
     for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
-                     ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies),
+                     ("draft_probs", draft_probs), ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies),
                      ("target_chain", target_chain), ("target_tree", target_tree), ("tree_draft", tree_drafts)):
         fn()
         torch.cuda.synchronize()
@@ -361,6 +366,7 @@ def bench_gpu(args):
         "verify_accept_us": comps["verify"],
         "kv_compact_us": comps["compact"],
         "stochastic_us": comps["stochastic"],
+        "draft_probs_us": comps["draft_probs"],
         "target_layer_us": comps["target_layer"],
         "tree_verify_us": comps["tree_verify"],
         "target_chain_us": comps["target_chain"],
@@ -618,6 +624,7 @@ def main():
             "verify_accept_us_k5": round(r["verify_accept_us"], 2),
             "kv_compact_us_28l_ctx2048_window6": round(r["kv_compact_us"], 2),
             "verify_stochastic_us_k5_vocab151936": round(r["stochastic_us"], 2),
+            "draft_probs_us_k5_head16384": round(r["draft_probs_us"], 2),
             "target_layer_us_qwen3_1p7b_m60_ctx2048": round(r["target_layer_us"], 2),
             "target_layer_hbm_frac_m60": round(100_663_296 / (r["target_layer_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "verify_tree_greedy_us_n60": round(r["tree_verify_us"], 2),

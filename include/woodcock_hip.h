@@ -132,6 +132,22 @@ int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p
                                const int32_t* draft_rows_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
                                void* workspace, wc_stream_t stream);
 
+/* wc_probs_from_logits at temperature T followed by wc_verify_chain_stochastic,
+ * with p never written: logits [rows][ld] are the target logits at
+ * [x_n, d_1..d_K]; p_i = softmax(logits_i / max(T, 1e-6)) is formed in place
+ * with the same arithmetic (so the decisions and draws equal the two-call
+ * path's bit for bit).  Two launches: per (vocabulary chunk, row) softmax
+ * partials plus the draft rows' masses, whose last block merges them, runs the
+ * accept tests and picks the row to draw from; then the draw over that row.
+ * Replaces the verify step of the engine's stochastic chain path
+ * (python/woodcock/spec.py:316-324: probs_from_logits + verify_tree_stochastic
+ * at width 1). */
+int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, int64_t ld, float temperature,
+                                      const float* q, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
+                                      const int32_t* draft_tokens_dev, const int32_t* draft_rows_dev,
+                                      const wc_uniforms* rng, wc_verdict* verdict_dev, void* workspace,
+                                      wc_stream_t stream);
+
 /* Stochastic tree verification, fp64 decisions: N = rows flattened nodes (node 0
  * the root, parents[0] = -1, 0 <= parents[i] < i, children in ascending node
  * order = draw order), p [N][ld_p] the target probabilities at every node,

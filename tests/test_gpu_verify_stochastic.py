@@ -212,3 +212,58 @@ def test_invalid_inputs_raise(cuda):
         verify_chain_stochastic(p, q, [5, 100], PhiloxStream(seed=1), d2t=ok_d2t)
     with pytest.raises(ValueError):
         verify_chain_stochastic(p, q, [5], PhiloxStream(seed=1), d2t=ok_d2t)
+
+
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_logits_path_equals_two_call_path(workload, temperature):
+    """wc_verify_chain_stochastic_logits (p formed in place from the logits)
+    returns the verdict of wc_probs_from_logits + wc_verify_chain_stochastic,
+    every field, over rounds with rejections at every depth and drafts outside
+    the draft vocabulary."""
+    from woodcock_amd.sampling import verify_chain_stochastic_logits_dev
+
+    lg, dl, d2t, tl, dlg, d2, _, q = workload
+    dev = tl.device
+    p = probs_from_logits(tl, temperature)
+    rng = np.random.default_rng(17)
+    rows = draw_rows(q.cpu().numpy(), 120, rng)
+    drafts = d2t[rows]
+    outside = np.setdiff1d(np.arange(V), d2t)
+    drafts[::13, 2] = outside[rng.integers(0, len(outside), size=len(drafts[::13]))]
+    dd = torch.from_numpy(drafts).to(dev)
+    drows = torch.from_numpy(rows.astype(np.int32)).to(dev)
+    rounds = torch.arange(len(drafts), dtype=torch.int32, device=dev)
+    v2 = torch.zeros(len(drafts), _lib.VERDICT_INTS, dtype=torch.int32, device=dev)
+    v1 = torch.zeros_like(v2)
+    for r in range(len(drafts)):
+        u = _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0)
+        verify_chain_stochastic_dev(p, q, dd[r], u, d2, verdict=v2[r])
+        verify_chain_stochastic_logits_dev(tl, temperature, q, dd[r], u, d2, verdict=v1[r])
+        # with the drafts' head rows given (draft time knows them)
+        if r % 3 == 0:
+            v3 = torch.zeros_like(v1[r])
+            verify_chain_stochastic_logits_dev(tl, temperature, q, dd[r], u, d2, draft_rows=drows[r], verdict=v3)
+            assert torch.equal(v3, v1[r]), r
+    assert torch.equal(v1, v2)
+    assert len(set(v1[:, _lib.V_N_ACCEPTED].tolist())) >= 3
+
+
+def test_logits_path_no_drafts_and_identity_vocab(cuda):
+    """K = 0 draws from softmax(logits_0); without d2t the head rows are the
+    first ids of the vocabulary."""
+    from woodcock_amd.sampling import verify_chain_stochastic_logits_dev
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+    lg = torch.randn(4, 9000, generator=g, device=dev) * 3
+    q = probs_from_logits(torch.randn(3, 5000, generator=g, device=dev), 1.0)
+    rounds = torch.arange(40, dtype=torch.int32, device=dev)
+    for r in range(40):
+        u = _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0)
+        d = torch.randint(0, 5000, (3,), generator=g, device=dev, dtype=torch.int32)
+        a = verify_chain_stochastic_dev(probs_from_logits(lg, 1.0), q, d, u)
+        b = verify_chain_stochastic_logits_dev(lg, 1.0, q, d, u)
+        assert torch.equal(a, b), r
+        a0 = verify_chain_stochastic_dev(probs_from_logits(lg[:1], 1.0), None, d[:0], u)
+        b0 = verify_chain_stochastic_logits_dev(lg[:1], 1.0, None, d[:0], u)
+        assert torch.equal(a0, b0), r

@@ -103,6 +103,8 @@ _SIGS = {
     "wc_draft_head": ([P, P, P, I64, P, C.c_int, C.c_int, P, I64, P, P, P, P, P], C.c_int),
     "wc_probs_from_logits": ([P, C.c_int, C.c_int, I64, C.c_float, P, I64, P, P], C.c_int),
     "wc_verify_chain_stochastic": ([P, C.c_int, C.c_int, I64, P, C.c_int, I64, P, P, P, P, P, P, P], C.c_int),
+    "wc_verify_chain_stochastic_logits": ([P, C.c_int, C.c_int, I64, C.c_float, P, C.c_int, I64, P, P, P, P, P, P,
+                                           P], C.c_int),
     "wc_verify_tree_stochastic": ([P, C.c_int, C.c_int, I64, P, C.c_int, I64, P, P, P, P, P, P, P], C.c_int),
     "wc_tree_mask": ([P, C.c_int, C.c_int, P, I64, P], C.c_int),
     "wc_sample_without_replacement": ([P, C.c_int, C.c_int, I64, P, P, C.c_int, P, I64, P, P, P], C.c_int),

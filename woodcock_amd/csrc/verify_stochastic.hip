@@ -43,8 +43,18 @@ struct StochArgs {
   int purpose;
   double* row_data;    // [WC_MAX_NODES][4]: Q, p(x), q_raw(x), flags
   double* chunk_data;  // [kMaxVocabChunks][2]: residual mass, target mass
+  int32_t* chunk_rows; // [kMaxVocabChunks + 1]: first head row of each vocabulary chunk
   unsigned int* counter;
   wc_verdict* verdict;
+  // from logits (wc_verify_chain_stochastic_logits): p = softmax(logits / T) computed in place
+  const float* logits;
+  int64_t ld_l;
+  float temperature;
+  float* part;          // [rows][kMaxVocabChunks][2] softmax partials (max, sum)
+  int32_t* dec;         // n, residual, n_uniforms
+  float* dec_ms;        // the chosen row's softmax max and sum
+  unsigned int* bad_flag;  // invalid d2t / drafts seen by the statistics launch (reset by its last block)
+  unsigned int* stats_counter;
 };
 
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
@@ -56,6 +66,58 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
   double t = 0.0;
   for (int w = 0; w < kStThreads / kWave; ++w) t += red[w];
   return t;
+}
+
+// Block sums of two doubles at once (one pair of barriers); s_w holds 2 per wave.
+__device__ __forceinline__ void block_sum2_f64(double& x, double& y, double* s_w) {
+  x = wave_sum(x);
+  y = wave_sum(y);
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane == 0) {
+    s_w[2 * wave] = x;
+    s_w[2 * wave + 1] = y;
+  }
+  __syncthreads();
+  double tx = 0.0, ty = 0.0;
+  for (int w = 0; w < kStThreads / kWave; ++w) {
+    tx += s_w[2 * w];
+    ty += s_w[2 * w + 1];
+  }
+  x = tx;
+  y = ty;
+}
+
+// Exclusive prefix sum over the lanes of one wave (lane order).
+__device__ __forceinline__ double block_wave_excl_scan(double v) {
+  const int lane = threadIdx.x % kWave;
+  double x = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  const double ex = __shfl_up(x, 1);
+  return lane == 0 ? 0.0 : ex;
+}
+
+// before + the exclusive prefix sum of one value per thread, in thread order:
+// a wave-level scan by lane shifts, then the totals of the lower waves.
+__device__ __forceinline__ double block_excl_scan(double v, double before, double* s_w) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  double x = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const double y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  const double ex = __shfl_up(x, 1);
+  __syncthreads();
+  if (lane == kWave - 1) s_w[wave] = x;
+  __syncthreads();
+  double base = before;
+  for (int w = 0; w < wave; ++w) base += s_w[w];
+  return lane == 0 ? base : base + ex;
 }
 
 // first index r in [0, n) with d2t[r] >= x (d2t ascending)
@@ -70,6 +132,84 @@ __device__ __forceinline__ int lower_bound_i32(const int32_t* d2t, int n, int x)
 
 // ------------------------------------------------------------------ per-row prologue
 
+// chunk_rows[c] = the first head row whose id is in vocabulary chunk c or later
+// (d2t ascending; an invalid d2t yields some table within [0, head_rows], and
+// is reported separately).  Head row r writes the entries of the chunks that
+// start after row r - 1's chunk, up to and including its own.
+__device__ __forceinline__ void chunk_table(const StochArgs& a, int rb, int re) {
+  const int nch = (a.vocab + kVocabChunk - 1) / kVocabChunk;
+  int32_t* __restrict__ tab = a.chunk_rows;
+  if (!a.d2t) {
+    if (rb == 0)
+      for (int c = threadIdx.x; c <= nch; c += kStThreads) tab[c] = min(c * kVocabChunk, a.head_rows);
+    return;
+  }
+  // batches of 8 rows per thread: every id of a batch is loaded before the
+  // first table store, so the loads of a batch are in flight together
+  const int32_t* __restrict__ d2t = a.d2t;
+  constexpr int kB = 8;
+  for (int r0 = rb + threadIdx.x; r0 < re; r0 += kStThreads * kB) {
+    int cur[kB], prv[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int r = min(r0 + u * kStThreads, a.head_rows - 1);
+      cur[u] = d2t[r];
+      prv[u] = d2t[max(r - 1, 0)];
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int r = r0 + u * kStThreads;
+      if (r >= re) continue;
+      const int ci = min(max(cur[u], 0) / kVocabChunk, nch);
+      const int prev = r == 0 ? -1 : min(max(prv[u], 0) / kVocabChunk, nch);
+      for (int c = prev + 1; c <= ci; ++c) tab[c] = r;
+      if (r == a.head_rows - 1)
+        for (int c = ci + 1; c <= nch; ++c) tab[c] = a.head_rows;
+    }
+  }
+}
+
+// 1 when this thread's share of d2t rows [rb, re) is not ascending or leaves
+// the vocabulary (branch-free, in batches of 8 rows whose loads are in flight
+// together).
+__device__ __forceinline__ int d2t_bad(const StochArgs& a, int rb, int re) {
+  const int32_t* __restrict__ d2t = a.d2t;
+  constexpr int kB = 8;
+  int bad = 0;
+  for (int j0 = rb + threadIdx.x; j0 < re; j0 += kStThreads * kB) {
+    int t[kB], nx[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int j = min(j0 + u * kStThreads, a.head_rows - 1);
+      t[u] = d2t[j];
+      nx[u] = d2t[min(j + 1, a.head_rows - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const int j = j0 + u * kStThreads;
+      const bool b = t[u] < 0 || t[u] >= a.vocab || (j + 1 < a.head_rows && nx[u] <= t[u]);
+      bad |= (j < re && b) ? 1 : 0;
+    }
+  }
+  return bad;
+}
+
+// Q_i = sum of draft row i over the head rows in fp64: thread t adds rows
+// t, t + 256, ... in order, 16 loads in flight per batch; then the block sum.
+__device__ __forceinline__ double draft_mass(const float* qr, int head_rows, double* red) {
+  constexpr int kB = 16;
+  double s = 0.0;
+  for (int b0 = threadIdx.x; b0 < head_rows; b0 += kStThreads * kB) {
+    float v[kB];
+#pragma unroll
+    for (int u = 0; u < kB; ++u) v[u] = qr[min(b0 + u * kStThreads, head_rows - 1)];
+#pragma unroll
+    for (int u = 0; u < kB; ++u)
+      if (b0 + u * kStThreads < head_rows) s += static_cast<double>(v[u]);
+  }
+  return block_sum_f64(s, red);
+}
+
 // Block i < K: draft mass Q_i = sum_r q_i[r] (fp64), the head row of d_i, and
 // p_i(d_i), q_i[row].  Block K validates d2t (ascending, within the vocabulary)
 // and the drafted tokens.
@@ -81,24 +221,17 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_rows(StochArgs a) {
   __syncthreads();
   if (i == K) {
     int bad = 0;
-    if (a.d2t) {
-      for (int r = threadIdx.x; r < a.head_rows; r += kStThreads) {
-        const int t = a.d2t[r];
-        if (t < 0 || t >= a.vocab || (r + 1 < a.head_rows && a.d2t[r + 1] <= t)) bad = 1;
-      }
-    }
+    if (a.d2t) bad = d2t_bad(a, 0, a.head_rows);
     for (int k = threadIdx.x; k < K; k += kStThreads)
       if (a.drafts[k] < 0 || a.drafts[k] >= a.vocab) bad = 1;
     if (bad) s_bad = 1;
+    chunk_table(a, 0, a.head_rows);
     __syncthreads();
     if (threadIdx.x == 0) a.row_data[4 * WC_MAX_NODES - 1] = s_bad ? 1.0 : 0.0;  // flags slot of the last row
     return;
   }
   const float* qr = a.q + static_cast<int64_t>(i) * a.ld_q;
-  double s = 0.0;
-#pragma unroll 8
-  for (int r = threadIdx.x; r < a.head_rows; r += kStThreads) s += static_cast<double>(qr[r]);
-  s = block_sum_f64(s, red);
+  const double s = draft_mass(qr, a.head_rows, red);
   if (threadIdx.x == 0) {
     const int x = min(max(a.drafts[i], 0), a.vocab - 1);
     int row = -1;
@@ -126,18 +259,18 @@ struct Decision {
   int n_uniforms; // consumed by the accept tests
 };
 
-// Sequential accept tests (sampling.py:74-80 / 163-170 at width 1); plain loads
-// of the prologue's results (a previous launch).
-__device__ __forceinline__ Decision decide(const StochArgs& a, unsigned long long round) {
-  const int K = a.rows - 1;
+// Sequential accept tests (sampling.py:74-80 / 163-170 at width 1) over the
+// per-row data rd [K][4] (Q, p(x), q_raw(x)).
+__device__ __forceinline__ Decision decide_rows(const double* row_data, int K, unsigned long long seed,
+                                                unsigned long long round, int purpose) {
   Decision d{K, 0, 0};
   for (int i = 0; i < K; ++i) {
-    const double* rd = a.row_data + 4 * i;
+    const double* rd = row_data + 4 * i;
     const double Q = rd[0];
     const double qx = Q > 0.0 ? rd[2] / Q : 0.0;
     bool accept = false;
     if (qx > 0.0) {
-      const double u = philox_uniform(a.seed, round, a.purpose, static_cast<unsigned long long>(d.n_uniforms++));
+      const double u = philox_uniform(seed, round, purpose, static_cast<unsigned long long>(d.n_uniforms++));
       accept = u < fmin(1.0, rd[1] / qx);
     }
     if (!accept) {
@@ -149,56 +282,88 @@ __device__ __forceinline__ Decision decide(const StochArgs& a, unsigned long lon
   return d;
 }
 
+// The same over the prologue's results (plain loads: a previous launch).
+__device__ __forceinline__ Decision decide(const StochArgs& a, unsigned long long round) {
+  return decide_rows(a.row_data, a.rows - 1, a.seed, round, a.purpose);
+}
+
+// Raw inputs of chunk c of row n, thread t's 16 consecutive entries: the
+// materialised probabilities, or (FL) the logits; issued before anything that
+// waits, the softmax (FL) is applied in chunk_values.
+template <bool FL>
+__device__ __forceinline__ void chunk_raw(const StochArgs& a, int n, int c, float (&raw)[kPerThread]) {
+  const int x0 = c * kVocabChunk + threadIdx.x * kPerThread;
+  const float* src = FL ? a.logits + static_cast<int64_t>(n) * a.ld_l : a.p + static_cast<int64_t>(n) * a.ld_p;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) raw[e] = src[min(x0 + e, a.vocab - 1)];
+}
+
 // Values of chunk c of the row to draw from: residual max(p - q, 0) and p, fp64.
-// q is scattered into LDS from the head rows whose ids fall in the chunk.
-__device__ __forceinline__ void chunk_values(const StochArgs& a, const Decision& d, int c, double* qchunk,
-                                             double (&rv)[kPerThread], double (&pv)[kPerThread]) {
+// raw from chunk_raw; q is scattered into LDS from the head rows [r0, r1) whose
+// ids fall in the chunk (the chunk table), divided by the draft mass Q.  With FL
+// p = exp(logit / T - M) / S exactly as wc_probs_from_logits writes it.
+template <bool FL>
+__device__ __forceinline__ void chunk_values(const StochArgs& a, const Decision& d, int c, float M, float S,
+                                             double Q, int r0, int r1, const float (&raw)[kPerThread],
+                                             double* qchunk, double (&rv)[kPerThread], double (&pv)[kPerThread]) {
+  // LDS-only barriers: the raw loads stay in flight while q is scattered
   const int x0 = c * kVocabChunk;
-  const float* pr = a.p + static_cast<int64_t>(d.n) * a.ld_p;
   for (int j = threadIdx.x; j < kVocabChunk; j += kStThreads) qchunk[j] = 0.0;
-  __syncthreads();
+  lds_barrier();
   if (d.residual) {
-    const double Q = a.row_data[4 * d.n];
     const float* qr = a.q + static_cast<int64_t>(d.n) * a.ld_q;
-    if (a.d2t) {
-      const int r0 = lower_bound_i32(a.d2t, a.head_rows, x0);
-      const int r1 = lower_bound_i32(a.d2t, a.head_rows, x0 + kVocabChunk);
-      for (int r = r0 + threadIdx.x; r < r1; r += kStThreads) qchunk[a.d2t[r] - x0] = static_cast<double>(qr[r]) / Q;
-    } else {
-      for (int j = threadIdx.x; j < kVocabChunk && x0 + j < a.head_rows; j += kStThreads)
-        qchunk[j] = static_cast<double>(qr[x0 + j]) / Q;
+    r0 = min(max(r0, 0), a.head_rows);
+    r1 = min(max(r1, r0), a.head_rows);
+    for (int r = r0 + threadIdx.x; r < r1; r += kStThreads) {
+      const int j = (a.d2t ? a.d2t[r] : r) - x0;
+      if (j >= 0 && j < kVocabChunk) qchunk[j] = static_cast<double>(qr[r]) / Q;
     }
   }
-  __syncthreads();
-  // thread t owns the 16 consecutive entries t*16 .. t*16+15 of the chunk
+  lds_barrier();
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int j = threadIdx.x * kPerThread + e, x = x0 + j;
-    const double pd = x < a.vocab ? static_cast<double>(pr[x]) : 0.0;
+    const float pf = FL ? expf(raw[e] / a.temperature - M) / S : raw[e];
+    const double pd = x < a.vocab ? static_cast<double>(pf) : 0.0;
     pv[e] = pd;
     rv[e] = fmax(pd - qchunk[j], 0.0);
   }
 }
 
+// FL: the decision and the chosen row's softmax (max, sum) come from the
+// statistics launch of wc_verify_chain_stochastic_logits.
+template <bool FL>
 __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
   __shared__ double red[kStThreads / kWave];
   __shared__ double qchunk[kVocabChunk];
   __shared__ double s_tsum[kStThreads];
   __shared__ int s_chunk, s_idx;
+  __shared__ int s_tab[kMaxVocabChunks + 1];
   const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
-  const Decision d = decide(a, round);
+  Decision d;
+  float M = 0.f, S = 1.f;
+  if constexpr (FL) {
+    d = Decision{a.dec[0], a.dec[1], a.dec[2]};
+    M = a.dec_ms[0];
+    S = a.dec_ms[1];
+  } else {
+    d = decide(a, round);
+  }
   const int c = blockIdx.x, nchunks = gridDim.x;
 
+  float raw[kPerThread];
+  chunk_raw<FL>(a, d.n, c, raw);
+  const int r0 = a.chunk_rows[c], r1 = a.chunk_rows[c + 1];
+  const double Q = a.row_data[4 * d.n];
   double rv[kPerThread], pv[kPerThread];
-  chunk_values(a, d, c, qchunk, rv, pv);
+  chunk_values<FL>(a, d, c, M, S, Q, r0, r1, raw, qchunk, rv, pv);
   double sr = 0.0, sp = 0.0;
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     sr += rv[e];
     sp += pv[e];
   }
-  sr = block_sum_f64(sr, red);
-  sp = block_sum_f64(sp, red);
+  block_sum2_f64(sr, sp, s_tsum);
   if (threadIdx.x == 0) {
     unsigned long long* cd = reinterpret_cast<unsigned long long*>(a.chunk_data + 2 * c);
     atomic_store_u64(cd, static_cast<unsigned long long>(__double_as_longlong(sr)));
@@ -206,8 +371,11 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
   }
   if (!last_block_done(a.counter, nchunks, c)) return;
 
-  // ---- last block: totals, the chunk holding the draw, then the entry
+  // ---- last block: totals, the chunk holding the draw, then the entry.  The
+  // chunk table and the drafts are loaded with the chunk masses.
   const bool bad = a.row_data[4 * WC_MAX_NODES - 1] != 0.0;
+  for (int k = threadIdx.x; k <= nchunks; k += kStThreads) s_tab[k] = a.chunk_rows[k];
+  const int dtok = threadIdx.x < d.n ? a.drafts[threadIdx.x] : 0;
   double cr[2], cp[2];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -216,8 +384,8 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
     cr[h] = k < nchunks ? __longlong_as_double(static_cast<long long>(atomic_load_u64(cd))) : 0.0;
     cp[h] = k < nchunks ? __longlong_as_double(static_cast<long long>(atomic_load_u64(cd + 1))) : 0.0;
   }
-  const double tot_r = block_sum_f64(cr[0] + cr[1], red);
-  const double tot_p = block_sum_f64(cp[0] + cp[1], red);
+  double tot_r = cr[0] + cr[1], tot_p = cp[0] + cp[1];
+  block_sum2_f64(tot_r, tot_p, s_tsum);
   const bool use_r = d.residual && tot_r > 1e-12;  // sampling.py:184: residual mass <= 1e-12 -> p
   const double total = use_r ? tot_r : tot_p;
   const double u = philox_uniform(a.seed, round, a.purpose, static_cast<unsigned long long>(d.n_uniforms));
@@ -230,7 +398,22 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
     if (k < nchunks) qchunk[k] = use_r ? cr[h] : cp[h];
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (nchunks <= kWave) {
+    // wave 0, lane k = chunk k: exclusive running sums by lane shifts, the
+    // first chunk whose inclusive sum exceeds the target by a ballot
+    if (threadIdx.x < kWave) {
+      const int k = threadIdx.x;
+      const double v = k < nchunks ? qchunk[k] : 0.0;
+      const double ex = block_wave_excl_scan(v);
+      const unsigned long long hit = __ballot(k < nchunks && ex + v > target);
+      const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : nchunks - 1;
+      if (k == cs) {
+        s_chunk = cs;
+        red[0] = hit ? ex : ex + v;  // mass before the chunk (all of it when no chunk is hit, as the walk leaves it)
+      }
+      if (k == 0) s_idx = kVocabChunk;
+    }
+  } else if (threadIdx.x == 0) {
     double run = 0.0;
     int cs = nchunks - 1;
     for (int k = 0; k < nchunks; ++k) {
@@ -249,22 +432,12 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
   const int cs = s_chunk;
   const double before = red[0];
   __syncthreads();
-  chunk_values(a, d, cs, qchunk, rv, pv);
+  chunk_raw<FL>(a, d.n, cs, raw);
+  chunk_values<FL>(a, d, cs, M, S, Q, s_tab[cs], s_tab[cs + 1], raw, qchunk, rv, pv);
   double tsum = 0.0;
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) tsum += use_r ? rv[e] : pv[e];
-  s_tsum[threadIdx.x] = tsum;
-  __syncthreads();
-  if (threadIdx.x == 0) {  // exclusive running sums of the 256 thread ranges, in order
-    double run = before;
-    for (int t = 0; t < kStThreads; ++t) {
-      const double v = s_tsum[t];
-      s_tsum[t] = run;
-      run += v;
-    }
-  }
-  __syncthreads();
-  double run = s_tsum[threadIdx.x];
+  double run = block_excl_scan(tsum, before, s_tsum);  // running sum before this thread's 16 entries
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     run += use_r ? rv[e] : pv[e];
@@ -277,10 +450,6 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
   if (threadIdx.x == 0) {
     const int x = min(cs * kVocabChunk + s_idx, a.vocab - 1);  // searchsorted clamp (sampling.py:193)
     wc_verdict* v = a.verdict;
-    for (int k = 0; k < d.n; ++k) {
-      v->tokens[k] = a.drafts[k];
-      v->keep[k] = k;
-    }
     v->tokens[d.n] = x;
     v->keep[d.n] = d.n;
     v->n_accepted = d.n;
@@ -288,6 +457,170 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_sample(StochArgs a) {
     v->n_keep = d.n + 1;
     v->n_uniforms = d.n_uniforms + 1;
     v->status = bad ? WC_E_INVALID : 0;
+  }
+  if (threadIdx.x < d.n) {
+    a.verdict->tokens[threadIdx.x] = dtok;
+    a.verdict->keep[threadIdx.x] = threadIdx.x;
+  }
+}
+
+// ------------------------------------------------------------------ from logits
+
+// Statistics launch of wc_verify_chain_stochastic_logits, grid (chunks, rows + 1):
+//   row r < rows, chunk c: the chunk's (max, sum of exp) of logits / T, the
+//     arithmetic of the softmax's first launch, handed over device-coherently;
+//   row `rows`, block i < K: draft mass Q_i, q_i at the draft's head row and
+//     p's logit at the draft (k_stoch_rows' work); block K: d2t / draft
+//     validation and the chunk -> head-row table.
+// The last block merges each row's partials as the softmax's second launch
+// does, forms p_i(d_i), runs the accept tests and leaves the decision and the
+// chosen row's (max, sum) for the sampling launch.
+__global__ __launch_bounds__(kStThreads) void k_stoch_stats(StochArgs a) {
+  __shared__ float s_m[kStThreads / kWave], s_s[kStThreads / kWave];
+  __shared__ double red[kStThreads / kWave];
+  __shared__ float s_M[WC_MAX_NODES], s_S[WC_MAX_NODES];
+  __shared__ double s_rd[4 * WC_MAX_NODES];
+  __shared__ int s_bad;
+  const int c = blockIdx.x, r = blockIdx.y, K = a.rows - 1, nch = gridDim.x;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  if (threadIdx.x == 0) s_bad = 0;
+  __syncthreads();
+  if (r < a.rows) {
+    const int x0 = c * kVocabChunk;
+    const float* lr = a.logits + static_cast<int64_t>(r) * a.ld_l;
+    float v[kPerThread];
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      const int x = x0 + e * kStThreads + threadIdx.x;
+      v[e] = x < a.vocab ? lr[min(x, a.vocab - 1)] / a.temperature : -INFINITY;
+      m = fmaxf(m, v[e]);
+    }
+    m = wave_max(m);
+    if (lane == 0) s_m[wave] = m;
+    __syncthreads();
+    float M = s_m[0];
+    for (int w = 1; w < kStThreads / kWave; ++w) M = fmaxf(M, s_m[w]);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) sum += v[e] == -INFINITY ? 0.f : expf(v[e] - M);
+    sum = wave_sum(sum);
+    if (lane == 0) s_s[wave] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float t = 0.f;
+      for (int w = 0; w < kStThreads / kWave; ++w) t += s_s[w];
+      float* pp = a.part + (static_cast<int64_t>(r) * kMaxVocabChunks + c) * 2;
+      publish_f32(pp, M);
+      publish_f32(pp + 1, t);
+    }
+  } else if (c < K) {
+    const float* qr = a.q + static_cast<int64_t>(c) * a.ld_q;
+    const double sq = draft_mass(qr, a.head_rows, red);
+    if (threadIdx.x == 0) {
+      const int x = min(max(a.drafts[c], 0), a.vocab - 1);
+      int row = -1;
+      if (a.draft_rows) {
+        row = a.draft_rows[c];
+        if (row < 0 || row >= a.head_rows || (a.d2t ? a.d2t[row] : row) != x) row = -1;
+      } else if (a.d2t) {
+        const int rr = lower_bound_i32(a.d2t, a.head_rows, x);
+        row = (rr < a.head_rows && a.d2t[rr] == x) ? rr : -1;
+      } else {
+        row = x < a.head_rows ? x : -1;
+      }
+      unsigned long long* rd = reinterpret_cast<unsigned long long*>(a.row_data + 4 * c);
+      atomic_store_u64(rd, static_cast<unsigned long long>(__double_as_longlong(sq)));
+      atomic_store_u64(rd + 2, static_cast<unsigned long long>(
+                                   __double_as_longlong(row >= 0 ? static_cast<double>(qr[row]) : 0.0)));
+    }
+  } else {
+    // blocks K .. gridDim.x - 1 of the extra row: a slice of the head rows each
+    // for the d2t check and the chunk table; the first also checks the drafts
+    const int ns = nch - K, b = c - K;
+    const int rb = static_cast<int>(static_cast<int64_t>(a.head_rows) * b / ns);
+    const int re = static_cast<int>(static_cast<int64_t>(a.head_rows) * (b + 1) / ns);
+    int bad = 0;
+    if (a.d2t) bad = d2t_bad(a, rb, re);
+    if (b == 0)
+      for (int k = threadIdx.x; k < K; k += kStThreads)
+        if (a.drafts[k] < 0 || a.drafts[k] >= a.vocab) bad = 1;
+    if (bad) s_bad = 1;
+    chunk_table(a, rb, re);
+    __syncthreads();
+    if (threadIdx.x == 0 && s_bad) atomicOr(a.bad_flag, 1u);
+  }
+  if (!last_block_done(a.stats_counter, nch * (a.rows + 1), linear_block())) return;
+
+  // ---- last block.  Every load first: the round, the logits at the drafts,
+  // the draft rows' data, then each row's partials (a wave per row, two rows
+  // per wave in flight, up to kMaxVocabChunks / 64 chunks per lane); the
+  // merges then run as the softmax's second launch runs them (same order).
+  constexpr int kCpl = kMaxVocabChunks / kWave;
+  constexpr int kNw = kStThreads / kWave;
+  const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
+  float lgx = 0.f;
+  if (threadIdx.x < K) {
+    const int x = min(max(a.drafts[threadIdx.x], 0), a.vocab - 1);
+    lgx = a.logits[static_cast<int64_t>(threadIdx.x) * a.ld_l + x];
+  }
+  double rdv = 0.0;
+  if (threadIdx.x < 4 * K)
+    rdv = __longlong_as_double(static_cast<long long>(
+        atomic_load_u64(reinterpret_cast<const unsigned long long*>(a.row_data + threadIdx.x))));
+  for (int i0 = wave; i0 < a.rows; i0 += 2 * kNw) {
+    float mc[2][kCpl], sc[2][kCpl];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float* pp = a.part + static_cast<int64_t>(min(i0 + h * kNw, a.rows - 1)) * kMaxVocabChunks * 2;
+#pragma unroll
+      for (int u = 0; u < kCpl; ++u) {
+        const int cc = min(lane + u * kWave, nch - 1);
+        mc[h][u] = fetch_f32(pp + 2 * cc);
+        sc[h][u] = fetch_f32(pp + 2 * cc + 1);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = i0 + h * kNw;
+      if (i >= a.rows) continue;
+      float m = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kCpl; ++u)
+        if (lane + u * kWave < nch) m = fmaxf(m, mc[h][u]);
+      m = wave_max(m);
+      float sum = 0.f;
+#pragma unroll
+      for (int u = 0; u < kCpl; ++u)
+        if (lane + u * kWave < nch) sum += mc[h][u] == -INFINITY ? 0.f : sc[h][u] * expf(mc[h][u] - m);
+      sum = wave_sum(sum);
+      if (lane == 0) {
+        s_M[i] = m;
+        s_S[i] = sum;
+      }
+    }
+  }
+  if (threadIdx.x < 4 * K) s_rd[threadIdx.x] = rdv;
+  if (threadIdx.x == 0) {  // the flags slot the sampling launch reads; the flag starts at zero for the next call
+    const unsigned int bad = __hip_atomic_exchange(a.bad_flag, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    a.row_data[4 * WC_MAX_NODES - 1] = bad ? 1.0 : 0.0;
+  }
+  __syncthreads();
+  if (threadIdx.x < K) {  // p_i(d_i) as the written probabilities would hold it
+    const int i = threadIdx.x;
+    const float pf = expf(lgx / a.temperature - s_M[i]) / s_S[i];
+    s_rd[4 * i + 1] = static_cast<double>(pf);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const Decision d = decide_rows(s_rd, K, a.seed, round, a.purpose);
+    a.dec[0] = d.n;
+    a.dec[1] = d.residual;
+    a.dec[2] = d.n_uniforms;
+    a.dec_ms[0] = s_M[d.n];
+    a.dec_ms[1] = s_S[d.n];
+    // the sampling launch reads Q_n and the flags with plain loads
+    a.row_data[4 * d.n] = s_rd[4 * d.n];
   }
 }
 
@@ -594,18 +927,7 @@ __global__ __launch_bounds__(kStThreads) void k_tree_sample(TreeArgs a) {
   double tsum = 0.0;
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) tsum += val[e];
-  s_tsum[t] = tsum;
-  __syncthreads();
-  if (t == 0) {
-    double run = before;
-    for (int k = 0; k < kStThreads; ++k) {
-      const double w = s_tsum[k];
-      s_tsum[k] = run;
-      run += w;
-    }
-  }
-  __syncthreads();
-  double run = s_tsum[t];
+  double run = block_excl_scan(tsum, before, s_tsum);
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     run += val[e];
@@ -776,12 +1098,70 @@ int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p
   a.purpose = rng->purpose;
   a.row_data = reinterpret_cast<double*>(static_cast<char*>(workspace) + kStochRowOff);
   a.chunk_data = reinterpret_cast<double*>(static_cast<char*>(workspace) + kStochChunkOff);
+  a.chunk_rows = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + kChunkRowsOff);
   a.counter = verify_counter(workspace, kCtrStochastic);
   a.verdict = verdict_dev;
   auto s = reinterpret_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(k_stoch_rows, dim3(rows), dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
-  hipLaunchKernelGGL(k_stoch_sample, dim3((vocab + kVocabChunk - 1) / kVocabChunk), dim3(kStThreads), 0, s, a);
+  hipLaunchKernelGGL((k_stoch_sample<false>), dim3((vocab + kVocabChunk - 1) / kVocabChunk), dim3(kStThreads), 0, s,
+                     a);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, int64_t ld, float temperature,
+                                      const float* q, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
+                                      const int32_t* draft_tokens_dev, const int32_t* draft_rows_dev,
+                                      const wc_uniforms* rng, wc_verdict* verdict_dev, void* workspace,
+                                      wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(logits && verdict_dev && rng && rng->round_dev, "wc_verify_chain_stochastic_logits: NULL buffer");
+  WC_REQUIRE(workspace && aligned(workspace, 16),
+             "wc_verify_chain_stochastic_logits: workspace is NULL or misaligned");
+  WC_REQUIRE(rows >= 1 && rows <= WC_MAX_NODES, "wc_verify_chain_stochastic_logits: rows must be in 1..%d (got %d)",
+             WC_MAX_NODES, rows);
+  WC_REQUIRE(vocab >= 1 && vocab <= kVocabChunk * kMaxVocabChunks,
+             "wc_verify_chain_stochastic_logits: vocab %d out of range", vocab);
+  WC_REQUIRE(ld >= vocab, "wc_verify_chain_stochastic_logits: logits row stride smaller than vocab");
+  WC_REQUIRE(rows == 1 || (q && draft_tokens_dev),
+             "wc_verify_chain_stochastic_logits: draft probabilities or tokens NULL");
+  WC_REQUIRE(rows == 1 || (head_rows >= 1 && ld_q >= head_rows),
+             "wc_verify_chain_stochastic_logits: bad draft distribution width / stride");
+  WC_REQUIRE(d2t_dev != nullptr || head_rows <= vocab,
+             "wc_verify_chain_stochastic_logits: without d2t the draft distribution must not exceed the vocabulary");
+  StochArgs a{};
+  a.rows = rows;
+  a.vocab = vocab;
+  a.q = q;
+  a.head_rows = head_rows;
+  a.ld_q = ld_q;
+  a.d2t = d2t_dev;
+  a.drafts = draft_tokens_dev;
+  a.draft_rows = draft_rows_dev;
+  a.seed = rng->seed;
+  a.round_dev = rng->round_dev;
+  a.purpose = rng->purpose;
+  char* ws = static_cast<char*>(workspace);
+  a.row_data = reinterpret_cast<double*>(ws + kStochRowOff);
+  a.chunk_data = reinterpret_cast<double*>(ws + kStochChunkOff);
+  a.chunk_rows = reinterpret_cast<int32_t*>(ws + kChunkRowsOff);
+  a.counter = verify_counter(workspace, kCtrStochastic);
+  a.stats_counter = verify_counter(workspace, kCtrStochStats);
+  a.verdict = verdict_dev;
+  a.logits = logits;
+  a.ld_l = ld;
+  a.temperature = temperature > 1e-6f ? temperature : 1e-6f;  // max(T, 1e-6), sampling.py:40
+  a.part = reinterpret_cast<float*>(ws + kProbsOff);
+  a.dec = reinterpret_cast<int32_t*>(ws + kStochDecOff);
+  a.dec_ms = reinterpret_cast<float*>(ws + kStochDecOff + 16);
+  a.bad_flag = reinterpret_cast<unsigned int*>(ws + kStochDecOff + 32);
+  const int nch = (vocab + kVocabChunk - 1) / kVocabChunk;
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  // the extra row needs K draft-mass blocks plus at least one check block
+  hipLaunchKernelGGL(k_stoch_stats, dim3(std::max(nch, rows), rows + 1), dim3(kStThreads), 0, s, a);
+  WC_LAUNCHED();
+  hipLaunchKernelGGL((k_stoch_sample<true>), dim3(nch), dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
   return WC_OK;
 }

@@ -46,7 +46,7 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 constexpr size_t kSlotBytes = 8 * WC_MAX_NODES;
 constexpr size_t kCounterOff = kSlotBytes;
 constexpr int kNumCounters = 4;
-enum Counter { kCtrArgmax = 0, kCtrStochastic = 1, kCtrTree = 2 };
+enum Counter { kCtrArgmax = 0, kCtrStochastic = 1, kCtrTree = 2, kCtrStochStats = 3 };
 
 // ------------------------------------------------------------------ device helpers
 
@@ -234,7 +234,14 @@ constexpr size_t kProbsOff = kStochChunkOff + kStochChunkBytes;
 constexpr size_t kProbsBytes = 4 * 2 * static_cast<size_t>(WC_MAX_NODES) * kMaxVocabChunks;
 constexpr size_t kTreeStateOff = kProbsOff + kProbsBytes;  // stochastic tree walk state
 constexpr size_t kTreeStateBytes = 4096;
-constexpr size_t kVerifyWorkspace = kTreeStateOff + kTreeStateBytes;
+// head row where each vocabulary chunk's ids start (d2t ascending), then the
+// stochastic chain's decision (n, residual, uniforms) and the chosen row's
+// softmax (max, sum) for the sampling launch
+constexpr size_t kChunkRowsOff = kTreeStateOff + kTreeStateBytes;
+constexpr size_t kChunkRowsBytes = 4 * (kMaxVocabChunks + 4);
+constexpr size_t kStochDecOff = kChunkRowsOff + kChunkRowsBytes;
+constexpr size_t kStochDecBytes = 64;
+constexpr size_t kVerifyWorkspace = kStochDecOff + kStochDecBytes;
 inline unsigned int* verify_counter(void* ws, int which) {
   return reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + kCounterOff + which * kTreeCounterBytes);
 }

@@ -218,6 +218,35 @@ def verify_chain_stochastic_dev(p: torch.Tensor, q: torch.Tensor, draft_tokens: 
     return verdict
 
 
+def verify_chain_stochastic_logits_dev(logits: torch.Tensor, temperature: float, q: torch.Tensor,
+                                       draft_tokens: torch.Tensor, rng: _lib.Uniforms,
+                                       d2t: torch.Tensor | None = None, draft_rows: torch.Tensor | None = None,
+                                       verdict: torch.Tensor | None = None) -> torch.Tensor:
+    """The stochastic chain rule straight from the target logits (K+1, V):
+    p = softmax(logits / T) is formed inside the two launches and never written
+    (spec.py:316-324); otherwise as verify_chain_stochastic_dev."""
+    lg = _logits_2d(logits)
+    rows, vocab = lg.shape
+    K = rows - 1
+    if draft_tokens.numel() != K:
+        raise ValueError(f"{rows} logit rows need {K} draft tokens, got {draft_tokens.numel()}")
+    if K > 0:
+        q2 = _logits_2d(q)
+        if q2.shape[0] < K:
+            raise ValueError(f"q has {q2.shape[0]} rows, {K} needed")
+        head_rows, ldq, qp = q2.shape[1], q2.stride(0), ptr(q2)
+    else:
+        head_rows, ldq, qp = 1, 1, None
+    if d2t is not None and d2t.numel() != head_rows:
+        raise ValueError(f"d2t has {d2t.numel()} entries for {head_rows} draft rows")
+    verdict = new_verdict(lg.device) if verdict is None else verdict
+    _lib.call("wc_verify_chain_stochastic_logits", ptr(lg), rows, vocab, lg.stride(0), float(temperature), qp,
+              head_rows, ldq, ptr(d2t) if d2t is not None else None, ptr(draft_tokens) if K > 0 else None,
+              ptr(draft_rows) if draft_rows is not None else None, C.byref(rng), ptr(verdict),
+              ptr(workspace(lg.device)), stream_ptr())
+    return verdict
+
+
 def verify_chain_stochastic(p: torch.Tensor, q: torch.Tensor, draft_tokens, rng: PhiloxStream,
                             d2t: torch.Tensor | None = None) -> tuple[int, int]:
     """p (K+1, V) target probabilities, q (K, H) draft probabilities the tokens were
