@@ -214,7 +214,7 @@ def test_invalid_inputs_raise(cuda):
         verify_chain_stochastic(p, q, [5], PhiloxStream(seed=1), d2t=ok_d2t)
 
 
-@pytest.mark.parametrize("temperature", [1.0, 0.7])
+@pytest.mark.parametrize("temperature", [1.0, 0.7, 0.5])
 def test_logits_path_equals_two_call_path(workload, temperature):
     """wc_verify_chain_stochastic_logits (p formed in place from the logits)
     returns the verdict of wc_probs_from_logits + wc_verify_chain_stochastic,
@@ -245,7 +245,8 @@ def test_logits_path_equals_two_call_path(workload, temperature):
             verify_chain_stochastic_logits_dev(tl, temperature, q, dd[r], u, d2, draft_rows=drows[r], verdict=v3)
             assert torch.equal(v3, v1[r]), r
     assert torch.equal(v1, v2)
-    assert len(set(v1[:, _lib.V_N_ACCEPTED].tolist())) >= 3
+    # T = 0.5 sharpens p away from q (drawn at T = 1): rejections come early
+    assert len(set(v1[:, _lib.V_N_ACCEPTED].tolist())) >= (2 if temperature < 0.6 else 3)
 
 
 def test_logits_path_no_drafts_and_identity_vocab(cuda):
@@ -267,3 +268,47 @@ def test_logits_path_no_drafts_and_identity_vocab(cuda):
         a0 = verify_chain_stochastic_dev(probs_from_logits(lg[:1], 1.0), None, d[:0], u)
         b0 = verify_chain_stochastic_logits_dev(lg[:1], 1.0, None, d[:0], u)
         assert torch.equal(a0, b0), r
+
+
+def test_logits_path_long_chain_and_invalid_inputs(cuda):
+    """K = 9 (beyond the rows a one-launch call holds: the two-launch path)
+    equals the two-call path; an invalid d2t or draft sets status WC_E_INVALID
+    for that call only, on both paths."""
+    from woodcock_amd.sampling import verify_chain_stochastic_logits_dev
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(11)
+    Vs, Hs = 20000, 3000
+    d2t = torch.sort(torch.randperm(Vs, generator=g, device=dev)[:Hs])[0].to(torch.int32)
+    rounds = torch.arange(30, dtype=torch.int32, device=dev)
+    for k in (4, 9):
+        lg = torch.randn(k + 1, Vs, generator=g, device=dev) * 2
+        q = probs_from_logits(torch.randn(k, Hs, generator=g, device=dev), 1.0)
+        p = probs_from_logits(lg, 0.8)
+        seen = set()
+        for r in range(30):
+            u = _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0)
+            rows = torch.randint(0, Hs, (k,), generator=g, device=dev)
+            d = d2t[rows].contiguous()
+            if r % 4 == 0:  # shared drafts: the first accepted more often
+                d = d2t[torch.argmax(q, dim=1)].to(torch.int32).contiguous()
+            a = verify_chain_stochastic_dev(p, q, d, u, d2t)
+            b = verify_chain_stochastic_logits_dev(lg, 0.8, q, d, u, d2t)
+            assert torch.equal(a, b), (k, r)
+            assert int(b[_lib.V_STATUS]) == 0
+            seen.add(int(b[_lib.V_N_ACCEPTED]))
+        assert len(seen) >= 2, k
+        u = _lib.Uniforms(SEED, ptr(rounds[:1]), 0)
+        bad_d2t = d2t.clone()
+        bad_d2t[7] = bad_d2t[6]
+        d = d2t[:k].contiguous()
+        v = verify_chain_stochastic_logits_dev(lg, 0.8, q, d, u, bad_d2t)
+        assert int(v[_lib.V_STATUS]) == _lib.WC_E_INVALID, k
+        v = verify_chain_stochastic_logits_dev(lg, 0.8, q, d, u, d2t)
+        assert int(v[_lib.V_STATUS]) == 0, k
+        d_out = d.clone()
+        d_out[k - 1] = Vs
+        v = verify_chain_stochastic_logits_dev(lg, 0.8, q, d_out, u, d2t)
+        assert int(v[_lib.V_STATUS]) == _lib.WC_E_INVALID, k
+        v = verify_chain_stochastic_logits_dev(lg, 0.8, q, d, u, d2t)
+        assert int(v[_lib.V_STATUS]) == 0, k

@@ -21,12 +21,20 @@
 // the draft mass and the values at the drafted token; then a grid over the
 // vocabulary in which every block repeats the (tiny) accept scan, sums its
 // chunk of the chosen row, and the last block locates the draw.
+#include <atomic>
+#include <cmath>
+
 #include "wc_common.h"
 
 namespace wc {
 
 constexpr int kStThreads = 256;
 constexpr int kPerThread = kVocabChunk / kStThreads;  // 16 entries of a chunk per thread
+
+// LDS slot of chunk entry j in the fp64 chunk buffers: entry e of thread t's
+// 16 (j = 16 t + e) sits at e * 256 + t, so a wave's reads of one e hit
+// consecutive slots instead of one bank every 128 bytes
+__device__ __forceinline__ int qslot(int j) { return (j % kPerThread) * kStThreads + j / kPerThread; }
 
 struct StochArgs {
   const float* p;  // [rows][ld_p] target probabilities
@@ -50,6 +58,7 @@ struct StochArgs {
   const float* logits;
   int64_t ld_l;
   float temperature;
+  float inv_t;          // 1 / T when T is a power of two, else 0
   float* part;          // [rows][kMaxVocabChunks][2] softmax partials (max, sum)
   int32_t* dec;         // n, residual, n_uniforms
   float* dec_ms;        // the chosen row's softmax max and sum
@@ -57,8 +66,10 @@ struct StochArgs {
   unsigned int* stats_counter;
 };
 
+// Block-wide fp64 sum over kStThreads threads (DPP wave sums, then the wave
+// totals in order); red holds one slot per wave.
 __device__ __forceinline__ double block_sum_f64(double v, double* red) {
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   __syncthreads();
   if (lane == 0) red[wave] = v;
@@ -70,8 +81,8 @@ __device__ __forceinline__ double block_sum_f64(double v, double* red) {
 
 // Block sums of two doubles at once (one pair of barriers); s_w holds 2 per wave.
 __device__ __forceinline__ void block_sum2_f64(double& x, double& y, double* s_w) {
-  x = wave_sum(x);
-  y = wave_sum(y);
+  x = wave_sum_dpp(x);
+  y = wave_sum_dpp(y);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   __syncthreads();
   if (lane == 0) {
@@ -88,30 +99,18 @@ __device__ __forceinline__ void block_sum2_f64(double& x, double& y, double* s_w
   y = ty;
 }
 
-// Exclusive prefix sum over the lanes of one wave (lane order).
+// Exclusive prefix sum over the lanes of one wave (lane order); the whole wave
+// must be active.
 __device__ __forceinline__ double block_wave_excl_scan(double v) {
-  const int lane = threadIdx.x % kWave;
-  double x = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  const double ex = __shfl_up(x, 1);
-  return lane == 0 ? 0.0 : ex;
+  return wave_excl_from_incl(wave_incl_scan_dpp(v));
 }
 
 // before + the exclusive prefix sum of one value per thread, in thread order:
-// a wave-level scan by lane shifts, then the totals of the lower waves.
+// a wave-level scan, then the totals of the lower waves.
 __device__ __forceinline__ double block_excl_scan(double v, double before, double* s_w) {
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  double x = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const double y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  const double ex = __shfl_up(x, 1);
+  const double x = wave_incl_scan_dpp(v);
+  const double ex = wave_excl_from_incl(x);
   __syncthreads();
   if (lane == kWave - 1) s_w[wave] = x;
   __syncthreads();
@@ -195,9 +194,9 @@ __device__ __forceinline__ int d2t_bad(const StochArgs& a, int rb, int re) {
 }
 
 // Q_i = sum of draft row i over the head rows in fp64: thread t adds rows
-// t, t + 256, ... in order, 16 loads in flight per batch; then the block sum.
+// t, t + 256, ... in order, kB loads in flight per batch; then the block sum.
+template <int kB = 16>
 __device__ __forceinline__ double draft_mass(const float* qr, int head_rows, double* red) {
-  constexpr int kB = 16;
   double s = 0.0;
   for (int b0 = threadIdx.x; b0 < head_rows; b0 += kStThreads * kB) {
     float v[kB];
@@ -316,7 +315,7 @@ __device__ __forceinline__ void chunk_values(const StochArgs& a, const Decision&
     r1 = min(max(r1, r0), a.head_rows);
     for (int r = r0 + threadIdx.x; r < r1; r += kStThreads) {
       const int j = (a.d2t ? a.d2t[r] : r) - x0;
-      if (j >= 0 && j < kVocabChunk) qchunk[j] = static_cast<double>(qr[r]) / Q;
+      if (j >= 0 && j < kVocabChunk) qchunk[qslot(j)] = static_cast<double>(qr[r]) / Q;
     }
   }
   lds_barrier();
@@ -326,7 +325,7 @@ __device__ __forceinline__ void chunk_values(const StochArgs& a, const Decision&
     const float pf = FL ? expf(raw[e] / a.temperature - M) / S : raw[e];
     const double pd = x < a.vocab ? static_cast<double>(pf) : 0.0;
     pv[e] = pd;
-    rv[e] = fmax(pd - qchunk[j], 0.0);
+    rv[e] = fmax(pd - qchunk[e * kStThreads + threadIdx.x], 0.0);
   }
 }
 
@@ -491,12 +490,16 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_stats(StochArgs a) {
     float v[kPerThread];
     float m = -INFINITY;
 #pragma unroll
+    for (int e = 0; e < kPerThread; ++e) v[e] = lr[min(x0 + e * kStThreads + static_cast<int>(threadIdx.x), a.vocab - 1)];
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) pin(v[e]);  // every load in flight at once
+#pragma unroll
     for (int e = 0; e < kPerThread; ++e) {
       const int x = x0 + e * kStThreads + threadIdx.x;
-      v[e] = x < a.vocab ? lr[min(x, a.vocab - 1)] / a.temperature : -INFINITY;
+      v[e] = x < a.vocab ? v[e] / a.temperature : -INFINITY;
       m = fmaxf(m, v[e]);
     }
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     if (lane == 0) s_m[wave] = m;
     __syncthreads();
     float M = s_m[0];
@@ -504,7 +507,7 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_stats(StochArgs a) {
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < kPerThread; ++e) sum += v[e] == -INFINITY ? 0.f : expf(v[e] - M);
-    sum = wave_sum(sum);
+    sum = wave_sum_dpp(sum);
     if (lane == 0) s_s[wave] = sum;
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -588,12 +591,12 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_stats(StochArgs a) {
 #pragma unroll
       for (int u = 0; u < kCpl; ++u)
         if (lane + u * kWave < nch) m = fmaxf(m, mc[h][u]);
-      m = wave_max(m);
+      m = wave_max_dpp(m);
       float sum = 0.f;
 #pragma unroll
       for (int u = 0; u < kCpl; ++u)
         if (lane + u * kWave < nch) sum += mc[h][u] == -INFINITY ? 0.f : sc[h][u] * expf(mc[h][u] - m);
-      sum = wave_sum(sum);
+      sum = wave_sum_dpp(sum);
       if (lane == 0) {
         s_M[i] = m;
         s_S[i] = sum;
@@ -622,6 +625,552 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_stats(StochArgs a) {
     // the sampling launch reads Q_n and the flags with plain loads
     a.row_data[4 * d.n] = s_rd[4 * d.n];
   }
+}
+
+// ------------------------------------------------------------------ one launch
+
+// wc_verify_chain_stochastic_logits in one launch, when rows <= kFusedRows and
+// the chunk blocks (the only ones that wait) fit on the GPU at once (checked on
+// the host):
+//   statistics blocks (row r, chunk c), rows x nch: the chunk's (max, sum of
+//     exp) of logits / T, k_stoch_stats' arithmetic;
+//   chunk blocks (chunk c, rows [3 g, 3 g + 3)), ceil(rows / 3) per chunk:
+//     this chunk of the block's rows held in registers, a window of head rows
+//     holding those whose ids fall in the chunk (one step of a search of the
+//     ascending d2t) and, when the window has at most kQPre rows, their ids
+//     and the block's draft rows' probabilities staged in LDS;
+//   draft-mass blocks i < K: Q_i and q_i at the draft's head row;
+//   check blocks: a slice of d2t each (ascending, within the vocabulary), the
+//     first also the drafts and the round's uniforms 0..K.
+// Hand-over by mailboxes: every result is one 64-bit word, stored once per call
+// with an agent-scope atomic store as the bitwise complement of its value, and
+// a word reads 0 until it is written.  A chunk block polls (agent-scope atomic
+// loads) every word it needs until none is 0 -- the poll's loads are the data
+// loads, and no read-modify-write or flag is involved; no acquire / release
+// fence at agent scope either, which would write back or invalidate the whole
+// L2.  Once every statistics, mass and check word is in, each chunk block
+// merges the partials of every row, forms p_i(d_i) and takes the accept tests
+// itself -- the same arithmetic on the same data, so the same decision in every
+// block; the block of each chunk that holds the chosen row then sums the
+// residual / target mass of its chunk into its mailbox, the others end.  Once every chunk's masses are in, each chunk block
+// locates the chunk of the draw; that chunk's block finds the entry in the
+// values it holds, writes the verdict, clears the other mailbox set for the
+// next call and advances the call counter.  Calls alternate between the two
+// sets by the parity of the counter, so a set is always cleared by the call
+// before the one that uses it (a zero-initialised workspace starts both
+// clear).  Every probability, sum and scan is formed as the two-launch path
+// (k_stoch_stats + k_stoch_sample<true>) forms it.
+struct MailSet {
+  // kMailRep copies of every word, each written by the producer; a polling
+  // block reads copy (block % kMailRep), which spreads the polls of one word
+  // over several lines
+  unsigned long long part[kMailRep][kMailRows][kMailChunks];  // row r, chunk c: sum bits << 32 | max bits
+  unsigned long long csum[kMailRep][kMailChunks][2];          // chunk c: residual mass, target mass (fp64)
+  // [0, 2K): Q_i, q_i at the draft (fp64); [2K, 3K + 1): uniforms 0..K;
+  // [3K + 1, 3K + 1 + checks): 1 + (a check block found an invalid input)
+  unsigned long long other[kMailRep][kMailOther];
+};
+static_assert(sizeof(MailSet) == 8 * kMailSetWords, "mailbox layout");
+static_assert(kGridBarOff % 8 == 0, "mailbox alignment");
+constexpr unsigned int kSpinLimit = 1u << 22;  // polls before a call gives up (WC_E_HIP in the verdict)
+
+// every copy of a word: w points at copy 0, copies lie `stride` words apart
+__device__ __forceinline__ void mail_put(unsigned long long* w, size_t stride, unsigned long long v) {
+#pragma unroll
+  for (int r = 0; r < kMailRep; ++r) atomic_store_u64(w + r * stride, ~v);
+}
+__device__ __forceinline__ void mail_put_f64(unsigned long long* w, size_t stride, double v) {
+  mail_put(w, stride, static_cast<unsigned long long>(__double_as_longlong(v)));
+}
+constexpr size_t kPartRep = kMailRows * kMailChunks, kCsumRep = 2 * kMailChunks, kOtherRep = kMailOther;
+__device__ __forceinline__ double mail_f64(unsigned long long raw) {
+  return __longlong_as_double(static_cast<long long>(~raw));
+}
+
+constexpr int kFusedRows = kMailRows;           // K + 1 rows whose chunk each chunk block holds
+constexpr int kFusedCpl = kMailChunks / kWave;  // chunks per lane in the merge: nch <= 256
+constexpr int kQPre = 1024;    // head rows of a chunk staged in LDS before the decision
+constexpr int kGroupRows = 3;  // rows of a chunk one chunk block holds: ceil(rows / 3) blocks per chunk
+
+// One step of a block-wide search for the first index r in [lo, hi] with
+// d2t[r] >= x (d2t ascending).  Width <= 256: thread t probes lo + t; else the
+// probes sit `step` apart and the bracket shrinks to step - 1.  Any d2t leaves
+// lo <= hi within the starting range, and the width shrinks every step.
+struct Probe {
+  int lo, hi, step, pos, val;
+};
+__device__ __forceinline__ void probe_issue(const int32_t* d2t, Probe& p) {
+  const int w = p.hi - p.lo;
+  p.step = w <= kStThreads ? 1 : (w + kStThreads - 1) / kStThreads;
+  p.pos = p.lo + (static_cast<int>(threadIdx.x) + 1) * p.step - 1;
+  p.val = w > 0 ? d2t[min(p.pos, p.hi - 1)] : 0;
+}
+__device__ __forceinline__ void probe_apply(Probe& p, int x, int* s_cnt) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const bool less = p.pos < p.hi && p.val < x;
+  const unsigned long long m = __ballot(less);
+  if (lane == 0) s_cnt[wave] = __popcll(m);
+  lds_barrier();
+  int cnt = 0;
+#pragma unroll
+  for (int w = 0; w < kStThreads / kWave; ++w) cnt += s_cnt[w];
+  const int lo = p.lo + cnt * p.step;
+  p.hi = min(p.hi, p.lo + (cnt + 1) * p.step - 1);
+  p.lo = lo;
+}
+
+// logit / T; with P2 (T a power of two) as logit * (1 / T), the same float:
+// both round the same exact quotient once (__fmul_rn: never contracted into a
+// following add, as the quotient is not)
+template <bool P2>
+__device__ __forceinline__ float lscale(const StochArgs& a, float x) {
+  return P2 ? __fmul_rn(x, a.inv_t) : x / a.temperature;
+}
+
+template <bool P2>
+__global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch, int nchecks, int vec,
+                                                           MailSet* sets, unsigned int* calls) {
+  constexpr int kNw = kStThreads / kWave;
+  __shared__ float s_m[kNw], s_s[kNw];
+  __shared__ float s_M[kFusedRows], s_S[kFusedRows], s_lgx[kFusedRows];
+  __shared__ double s_rd[4 * kFusedRows];  // per draft row: Q, -, q_raw(x), uniform i
+  __shared__ double qchunk[kVocabChunk];
+  __shared__ double s_tsum[kStThreads];
+  __shared__ float s_q[kGroupRows][kQPre];
+  __shared__ short s_j[kQPre];
+  __shared__ int s_cnt[1][2][kNw];
+  __shared__ int s_bad, s_chunk, s_idx;
+  __shared__ double s_before;
+  const int b = blockIdx.x, K = a.rows - 1, rows = a.rows;
+  const int nstat = rows * nch, ngroups = (rows + kGroupRows - 1) / kGroupRows, nchunkb = ngroups * nch;
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  // the call counter moves only at the end of the call (after every block has read it)
+  const unsigned int call = __hip_atomic_load(calls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  MailSet* mb = sets + (call & 1u);
+  const int rep = blockIdx.x % kMailRep;  // the mailbox copy this block polls
+
+  if (b < nstat) {
+    // ---- statistics block (row r, chunk c)
+    const int r = b / nch, c = b % nch, x0 = c * kVocabChunk;
+    const float* lr = a.logits + static_cast<int64_t>(r) * a.ld_l;
+    float v[kPerThread];
+    float m = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) v[e] = lr[min(x0 + e * kStThreads + static_cast<int>(threadIdx.x), a.vocab - 1)];
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) pin(v[e]);  // every load in flight at once
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      const int x = x0 + e * kStThreads + threadIdx.x;
+      v[e] = x < a.vocab ? lscale<P2>(a, v[e]) : -INFINITY;
+      m = fmaxf(m, v[e]);
+    }
+    m = wave_max_dpp(m);
+    if (lane == 0) s_m[wave] = m;
+    __syncthreads();
+    float M = s_m[0];
+    for (int w = 1; w < kNw; ++w) M = fmaxf(M, s_m[w]);
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) sum += v[e] == -INFINITY ? 0.f : expf(v[e] - M);
+    sum = wave_sum_dpp(sum);
+    if (lane == 0) s_s[wave] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {  // (max, sum) as one word
+      float t = 0.f;
+      for (int w = 0; w < kNw; ++w) t += s_s[w];
+      mail_put(&mb->part[0][r][c], kPartRep,
+               static_cast<unsigned long long>(__float_as_uint(M)) |
+                   (static_cast<unsigned long long>(__float_as_uint(t)) << 32));
+    }
+    return;
+  }
+  if (b >= nstat + nchunkb) {
+    const int e = b - nstat - nchunkb;
+    if (e < K) {  // ---- draft mass Q_i; uniform i (and uniform K in the last, on another wave)
+      const double sq = draft_mass<64>(a.q + static_cast<int64_t>(e) * a.ld_q, a.head_rows, s_tsum);
+      const int u = threadIdx.x == 0 ? e : (threadIdx.x == kWave && e == K - 1 ? K : -1);
+      if (u >= 0) {
+        const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
+        mail_put_f64(&mb->other[0][2 * K + u], kOtherRep, philox_uniform(a.seed, round, a.purpose, u));
+      }
+      if (threadIdx.x == 0) mail_put_f64(&mb->other[0][2 * e], kOtherRep, sq);
+      return;
+    }
+    // ---- check block bs of ns (ns >= K): a slice of d2t checked; q_bs at
+    // draft bs's head row (bs < K); the drafts checked (bs == 0); a slice of
+    // the other mailbox set cleared for the next call.  Loads first, then the
+    // waits.
+    const int ns = nchecks, bs = e - K;
+    {
+      unsigned long long* nxt = reinterpret_cast<unsigned long long*>(sets + ((call + 1u) & 1u));
+      const int w0 = static_cast<int>(kMailSetWords * bs / ns), w1 = static_cast<int>(kMailSetWords * (bs + 1) / ns);
+      for (int k = w0 + threadIdx.x; k < w1; k += kStThreads) atomic_store_u64(nxt + k, 0ull);
+    }
+    const bool lookup = bs < K;
+    const int x = lookup ? min(max(a.drafts[bs], 0), a.vocab - 1) : 0;
+    int row = lookup && a.draft_rows ? a.draft_rows[bs] : -1;
+    if (threadIdx.x == 0) s_bad = 0;
+    lds_barrier();
+    const int rb = static_cast<int>(static_cast<int64_t>(a.head_rows) * bs / ns);
+    const int re = static_cast<int>(static_cast<int64_t>(a.head_rows) * (bs + 1) / ns);
+    int bad = a.d2t ? d2t_bad(a, rb, re) : 0;
+    if (bs == 0)
+      for (int k = threadIdx.x; k < K; k += kStThreads)
+        if (a.drafts[k] < 0 || a.drafts[k] >= a.vocab) bad = 1;
+    if (lookup) {  // the id at the candidate row and q there load together
+      const float* qr = a.q + static_cast<int64_t>(bs) * a.ld_q;
+      float qx = 0.f;
+      if (a.draft_rows) {  // the given row, if it holds the draft
+        const bool in = row >= 0 && row < a.head_rows;
+        const int rc = in ? row : 0;
+        const int id = a.d2t ? a.d2t[rc] : rc;
+        qx = qr[rc];
+        row = in && id == x ? row : -1;
+      } else if (a.d2t) {  // block-wide search of the ascending d2t
+        Probe p{0, a.head_rows, 1, 0, 0};
+        for (int it = 0;; ++it) {
+          probe_issue(a.d2t, p);
+          probe_apply(p, x, s_cnt[0][it & 1]);
+          if (p.lo == p.hi) break;
+        }
+        const int rc = min(p.lo, a.head_rows - 1);
+        const int id = a.d2t[rc];
+        qx = qr[rc];
+        row = p.lo < a.head_rows && id == x ? p.lo : -1;
+      } else {
+        row = x < a.head_rows ? x : -1;
+        qx = qr[max(row, 0)];
+      }
+      if (threadIdx.x == 0) mail_put_f64(&mb->other[0][2 * bs + 1], kOtherRep, row >= 0 ? static_cast<double>(qx) : 0.0);
+    }
+    if (K == 0 && bs == 0 && threadIdx.x == 0) {  // no draft-mass block: the one uniform here
+      const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
+      mail_put_f64(&mb->other[0][0], kOtherRep, philox_uniform(a.seed, round, a.purpose, 0));
+    }
+    if (bad) s_bad = 1;
+    __syncthreads();
+    if (threadIdx.x == 0) mail_put(&mb->other[0][3 * K + 1 + bs], kOtherRep, ~(1ull + static_cast<unsigned long long>(s_bad)));
+    return;
+  }
+
+  // ---- chunk block (chunk c, rows [rlo, rhi)), ceil(rows / 3) blocks per
+  // chunk so that no block loads more than three rows.  One step of the d2t
+  // search brackets the head rows whose ids fall in the chunk: the window
+  // [w0, w1) holds them (ids outside the chunk are dropped by their offset);
+  // then the window's ids and the block's draft rows' q, the logits at the
+  // drafts and this chunk of the block's rows, all in flight together.
+  const int cb = b - nstat, c = cb % nch, rlo = (cb / nch) * kGroupRows, rhi = min(rlo + kGroupRows, rows);
+  const int x0 = c * kVocabChunk;
+  const bool search = K > 0 && a.d2t != nullptr;
+  Probe pr[2] = {{0, a.head_rows, 1, 0, 0}, {0, a.head_rows, 1, 0, 0}};
+  if (search) {
+    probe_issue(a.d2t, pr[0]);
+    probe_issue(a.d2t, pr[1]);
+  }
+  const int dtok = threadIdx.x < K ? a.drafts[threadIdx.x] : 0;
+  for (int j = threadIdx.x; j < kVocabChunk; j += kStThreads) qchunk[j] = 0.0;
+  int w0 = min(x0, a.head_rows), w1 = min(x0 + kVocabChunk, a.head_rows);
+  if (search) {
+    probe_apply(pr[0], x0, s_cnt[0][0]);
+    probe_apply(pr[1], x0 + kVocabChunk, s_cnt[0][1]);
+    w0 = pr[0].lo;           // the chunk's first head row is in [lo, hi] of the first search
+    w1 = max(pr[1].hi, w0);  // its end in [lo, hi] of the second
+  }
+  const int nr = w1 - w0;
+  const bool pre = rlo < K && nr <= kQPre;  // the block holds a draft row
+  constexpr int kU = kQPre / kStThreads;
+  int jv[kU];
+  float qv[kU][kGroupRows];
+  if (pre) {  // loads at clamped addresses
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int r = min(w0 + static_cast<int>(threadIdx.x) + u * kStThreads, a.head_rows - 1);
+      jv[u] = a.d2t ? a.d2t[r] : r;
+#pragma unroll
+      for (int i = 0; i < kGroupRows; ++i)
+        if (rlo + i < K) qv[u][i] = a.q[static_cast<int64_t>(rlo + i) * a.ld_q + r];
+    }
+  }
+  float lgx = 0.f;
+  if (threadIdx.x < K) lgx = a.logits[static_cast<int64_t>(threadIdx.x) * a.ld_l + min(max(dtok, 0), a.vocab - 1)];
+  // thread t: entries x0 + 16 t .. x0 + 16 t + 15 of each held row (chunk_raw's layout)
+  const int xt = x0 + threadIdx.x * kPerThread;
+  const bool v4 = vec && xt + kPerThread <= a.vocab;
+  float v[kGroupRows][kPerThread];
+#pragma unroll
+  for (int i = 0; i < kGroupRows; ++i) {
+    if (rlo + i < rhi) {
+      const float* lr = a.logits + static_cast<int64_t>(rlo + i) * a.ld_l;
+      if (v4) {
+#pragma unroll
+        for (int e4 = 0; e4 < kPerThread / 4; ++e4) {
+          const float4 f = reinterpret_cast<const float4*>(lr + xt)[e4];
+          v[i][4 * e4] = f.x;
+          v[i][4 * e4 + 1] = f.y;
+          v[i][4 * e4 + 2] = f.z;
+          v[i][4 * e4 + 3] = f.w;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < kPerThread; ++e) v[i][e] = lr[min(xt + e, a.vocab - 1)];
+      }
+    }
+  }
+  if (pre) {  // ids as chunk offsets (-1 outside the window or the chunk) and q into LDS
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      float jf = __int_as_float(jv[u]);
+      pin(jf);
+      jv[u] = __float_as_int(jf);
+#pragma unroll
+      for (int i = 0; i < kGroupRows; ++i)
+        if (rlo + i < K) pin(qv[u][i]);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int k = threadIdx.x + u * kStThreads, j = jv[u] - x0;
+      s_j[k] = static_cast<short>(k < nr && j >= 0 && j < kVocabChunk ? j : -1);
+#pragma unroll
+      for (int i = 0; i < kGroupRows; ++i)
+        if (rlo + i < K) s_q[i][k] = qv[u][i];
+    }
+  }
+  if (threadIdx.x < K) s_lgx[threadIdx.x] = lgx;
+  // ---- wait for every statistics, mass and check word: wave w merges rows w
+  // and w + 4, lane l their chunks l, l + 64, ...; thread t < n_other one
+  // draft-row / uniform / check word
+  const int n_other = 3 * K + 1 + nchecks;
+  unsigned long long pw[2][kFusedCpl], ow = 0;
+  for (unsigned int it = 0;; ++it) {
+    // every word loaded (clamped) before any is tested: one round trip per poll
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int u = 0; u < kFusedCpl; ++u)
+        pw[h][u] = atomic_load_u64(&mb->part[rep][min(wave + h * kNw, rows - 1)][min(lane + u * kWave, nch - 1)]);
+    ow = atomic_load_u64(&mb->other[rep][min(static_cast<int>(threadIdx.x), n_other - 1)]);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int u = 0; u < kFusedCpl; ++u) pin(pw[h][u]);
+    pin(ow);
+    int ok = 1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int u = 0; u < kFusedCpl; ++u)
+        if (wave + h * kNw < rows && lane + u * kWave < nch && pw[h][u] == 0ull) ok = 0;
+    if (threadIdx.x < n_other && ow == 0ull) ok = 0;
+    if (__syncthreads_and(ok)) break;
+    if (it == kSpinLimit) {
+      if (threadIdx.x == 0) a.verdict->status = WC_E_HIP;
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  // the rows' softmax (max, sum), merged as k_stoch_stats merges them
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int i = wave + h * kNw;
+    if (i >= rows) continue;
+    float mc[kFusedCpl], sc[kFusedCpl];
+#pragma unroll
+    for (int u = 0; u < kFusedCpl; ++u) {
+      const unsigned long long w = ~pw[h][u];
+      mc[u] = __uint_as_float(static_cast<unsigned int>(w));
+      sc[u] = __uint_as_float(static_cast<unsigned int>(w >> 32));
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kFusedCpl; ++u)
+      if (lane + u * kWave < nch) m = fmaxf(m, mc[u]);
+    m = wave_max_dpp(m);
+    float sum = 0.f;
+#pragma unroll
+    for (int u = 0; u < kFusedCpl; ++u)
+      if (lane + u * kWave < nch) sum += mc[u] == -INFINITY ? 0.f : sc[u] * expf(mc[u] - m);
+    sum = wave_sum_dpp(sum);
+    if (lane == 0) {
+      s_M[i] = m;
+      s_S[i] = sum;
+    }
+  }
+  // s_rd[4 i] = Q_i, s_rd[4 i + 2] = q_i at the draft, s_rd[4 u + 3] = uniform u
+  const int t = threadIdx.x;
+  if (t < 2 * K) s_rd[4 * (t / 2) + 2 * (t % 2)] = mail_f64(ow);
+  else if (t < 3 * K + 1) s_rd[4 * (t - 2 * K) + 3] = mail_f64(ow);
+  const bool bad = __syncthreads_or(t >= 3 * K + 1 && t < n_other && ow == 2ull) != 0;
+  // The accept tests of decide_rows, every wave at once: lane i < K tests draft
+  // i with the uniform it would consume in order (one per earlier draft whose
+  // q(x) > 0); the first rejection ends the walk.
+  Decision d{K, 0, 0};
+  {
+    double qx = 0.0;
+    bool acc = false;
+    if (lane < K) {
+      const double Q = s_rd[4 * lane];
+      qx = Q > 0.0 ? s_rd[4 * lane + 2] / Q : 0.0;
+    }
+    const unsigned long long hm = __ballot(lane < K && qx > 0.0);
+    if (lane < K && qx > 0.0) {
+      const int ui = __popcll(hm & ((1ull << lane) - 1ull));
+      const float pf = expf(lscale<P2>(a, s_lgx[lane]) - s_M[lane]) / s_S[lane];
+      acc = s_rd[4 * ui + 3] < fmin(1.0, static_cast<double>(pf) / qx);
+    }
+    const unsigned long long rej = __ballot(lane < K && !acc);
+    if (rej) {
+      d.n = __ffsll(static_cast<long long>(rej)) - 1;
+      d.residual = 1;
+      d.n_uniforms = __popcll(hm & ((1ull << d.n) - 1ull)) + static_cast<int>((hm >> d.n) & 1ull);
+    } else {
+      d.n_uniforms = __popcll(hm);
+    }
+  }
+  if (d.n < rlo || d.n >= rhi) return;  // another block of this chunk holds row n
+  const float M = s_M[d.n], S = s_S[d.n];
+  const double Q = s_rd[4 * d.n];
+  float raw[kPerThread];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) raw[e] = v[0][e];
+#pragma unroll
+  for (int i = 1; i < kGroupRows; ++i)
+    if (rlo + i == d.n)
+#pragma unroll
+      for (int e = 0; e < kPerThread; ++e) raw[e] = v[i][e];
+  // q_n / Q_n scattered over the chunk (chunk_values' arithmetic)
+  if (d.residual) {
+    if (pre) {
+      const float* sq = s_q[d.n - rlo];
+      for (int k = threadIdx.x; k < nr; k += kStThreads) {
+        const int j = s_j[k];
+        if (j >= 0) qchunk[qslot(j)] = static_cast<double>(sq[k]) / Q;
+      }
+    } else {
+      const float* qr = a.q + static_cast<int64_t>(d.n) * a.ld_q;
+      for (int r = w0 + threadIdx.x; r < w1; r += kStThreads) {
+        const int j = (a.d2t ? a.d2t[r] : r) - x0;
+        if (j >= 0 && j < kVocabChunk) qchunk[qslot(j)] = static_cast<double>(qr[r]) / Q;
+      }
+    }
+  }
+  lds_barrier();
+  double rv[kPerThread], pv[kPerThread];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    const int j = threadIdx.x * kPerThread + e, x = x0 + j;
+    const float pf = expf(lscale<P2>(a, raw[e]) - M) / S;
+    const double pd = x < a.vocab ? static_cast<double>(pf) : 0.0;
+    pv[e] = pd;
+    rv[e] = fmax(pd - qchunk[e * kStThreads + threadIdx.x], 0.0);
+  }
+  {
+    double sr = 0.0, sp = 0.0;
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) {
+      sr += rv[e];
+      sp += pv[e];
+    }
+    block_sum2_f64(sr, sp, s_tsum);
+    if (threadIdx.x == 0) {
+      mail_put_f64(&mb->csum[0][c][0], kCsumRep, sr);
+      mail_put_f64(&mb->csum[0][c][1], kCsumRep, sp);
+    }
+  }
+
+  // ---- every chunk's masses (thread k: chunk k), the totals and the chunk of
+  // the draw (k_stoch_sample's arithmetic); the block holding that chunk finishes
+  double cr[2] = {0.0, 0.0}, cp[2] = {0.0, 0.0};
+  for (unsigned int it = 0;; ++it) {
+    const int k = min(static_cast<int>(threadIdx.x), nch - 1);
+    unsigned long long wr = atomic_load_u64(&mb->csum[rep][k][0]);
+    unsigned long long wp = atomic_load_u64(&mb->csum[rep][k][1]);
+    pin(wr);
+    pin(wp);
+    const int ok = threadIdx.x >= nch || (wr != 0ull && wp != 0ull) ? 1 : 0;
+    if (threadIdx.x < nch) {
+      cr[0] = mail_f64(wr);
+      cp[0] = mail_f64(wp);
+    }
+    if (__syncthreads_and(ok)) break;
+    if (it == kSpinLimit) {
+      if (threadIdx.x == 0) a.verdict->status = WC_E_HIP;
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  double tot_r = cr[0] + cr[1], tot_p = cp[0] + cp[1];
+  block_sum2_f64(tot_r, tot_p, s_tsum);
+  const bool use_r = d.residual && tot_r > 1e-12;  // sampling.py:184: residual mass <= 1e-12 -> p
+  const double total = use_r ? tot_r : tot_p;
+  const double target = s_rd[4 * d.n_uniforms + 3] * total;
+  if (nch <= kWave) {
+    if (threadIdx.x < kWave) {
+      const int k = threadIdx.x;
+      const double vk = k < nch ? (use_r ? cr[0] : cp[0]) : 0.0;
+      const double ex = block_wave_excl_scan(vk);
+      const unsigned long long hit = __ballot(k < nch && ex + vk > target);
+      const int cs = hit ? __ffsll(static_cast<long long>(hit)) - 1 : nch - 1;
+      if (k == cs) {
+        s_chunk = cs;
+        s_before = hit ? ex : ex + vk;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int k = threadIdx.x + h * kStThreads;
+      if (k < nch) qchunk[k] = use_r ? cr[h] : cp[h];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double run = 0.0;
+      int cs = nch - 1;
+      for (int k = 0; k < nch; ++k) {
+        const double vk = qchunk[k];
+        if (run + vk > target) {
+          cs = k;
+          break;
+        }
+        run += vk;
+      }
+      s_chunk = cs;
+      s_before = run;
+    }
+  }
+  if (threadIdx.x == 0) s_idx = kVocabChunk;
+  __syncthreads();
+  if (s_chunk != c) return;
+  double tsum = 0.0;
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) tsum += use_r ? rv[e] : pv[e];
+  double run = block_excl_scan(tsum, s_before, s_tsum);
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) {
+    run += use_r ? rv[e] : pv[e];
+    if (run > target) {
+      atomicMin(&s_idx, static_cast<int>(threadIdx.x) * kPerThread + e);
+      break;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int x = min(c * kVocabChunk + s_idx, a.vocab - 1);  // searchsorted clamp (sampling.py:193)
+    wc_verdict* vd = a.verdict;
+    vd->tokens[d.n] = x;
+    vd->keep[d.n] = d.n;
+    vd->n_accepted = d.n;
+    vd->next = x;
+    vd->n_keep = d.n + 1;
+    vd->n_uniforms = d.n_uniforms + 1;
+    vd->status = bad ? WC_E_INVALID : 0;
+  }
+  if (threadIdx.x < d.n) {
+    a.verdict->tokens[threadIdx.x] = dtok;
+    a.verdict->keep[threadIdx.x] = threadIdx.x;
+  }
+  // every block of this call has read the counter (its words are in): it moves
+  if (threadIdx.x == 0) atomic_store_u32(calls, call + 1u);
 }
 
 // ------------------------------------------------------------------ stochastic tree
@@ -867,11 +1416,16 @@ __global__ __launch_bounds__(kStThreads) void k_tree_sample(TreeArgs a) {
       }
     }
     __syncthreads();
+    float pxf[kPerThread];  // every load in flight before the first use
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) pxf[e] = pr[min(x0 + t * kPerThread + e, a.vocab - 1)];
+#pragma unroll
+    for (int e = 0; e < kPerThread; ++e) pin(pxf[e]);
 #pragma unroll
     for (int e = 0; e < kPerThread; ++e) {
       const int k = t * kPerThread + e, x = x0 + k;
       double qo;
-      val[e] = x < a.vocab ? tree_chain(static_cast<double>(pr[x]), qchunk[k], x, j, s_x, s_mode, s_div, s_s, qo)
+      val[e] = x < a.vocab ? tree_chain(static_cast<double>(pxf[e]), qchunk[k], x, j, s_x, s_mode, s_div, s_s, qo)
                            : 0.0;
     }
   };
@@ -977,12 +1531,16 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_part(ProbsArgs a) {
   float v[kPerThread];
   float m = -INFINITY;
 #pragma unroll
+  for (int e = 0; e < kPerThread; ++e) v[e] = lr[min(x0 + e * kStThreads + static_cast<int>(threadIdx.x), a.n - 1)];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) pin(v[e]);  // every load in flight at once
+#pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int x = x0 + e * kStThreads + threadIdx.x;
-    v[e] = x < a.n ? scaled(a, lr[min(x, a.n - 1)]) : -INFINITY;
+    v[e] = x < a.n ? scaled(a, v[e]) : -INFINITY;
     m = fmaxf(m, v[e]);
   }
-  m = wave_max(m);
+  m = wave_max_dpp(m);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
@@ -991,7 +1549,7 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_part(ProbsArgs a) {
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) s += v[e] == -INFINITY ? 0.f : expf(v[e] - M);
-  s = wave_sum(s);
+  s = wave_sum_dpp(s);
   if (lane == 0) s_s[wave] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -1011,13 +1569,13 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_write(ProbsArgs a) {
   if (threadIdx.x < kWave) {
     float m = -INFINITY;
     for (int c = threadIdx.x; c < nch; c += kWave) m = fmaxf(m, pp[2 * c]);
-    m = wave_max(m);
+    m = wave_max_dpp(m);
     float s = 0.f;
     for (int c = threadIdx.x; c < nch; c += kWave) {
       const float mc = pp[2 * c];
       s += mc == -INFINITY ? 0.f : pp[2 * c + 1] * expf(mc - m);
     }
-    s = wave_sum(s);
+    s = wave_sum_dpp(s);
     if (threadIdx.x == 0) {
       s_M = m;
       s_S = s;
@@ -1027,11 +1585,37 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_write(ProbsArgs a) {
   const float M = s_M, S = s_S;
   const float* lr = a.logits + static_cast<int64_t>(r) * a.ld;
   float* orow = a.out + static_cast<int64_t>(r) * a.ld_out;
+  float raw[kPerThread];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) raw[e] = lr[min(x0 + e * kStThreads + static_cast<int>(threadIdx.x), a.n - 1)];
+#pragma unroll
+  for (int e = 0; e < kPerThread; ++e) pin(raw[e]);
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int x = x0 + e * kStThreads + threadIdx.x;
-    if (x < a.n) orow[x] = expf(scaled(a, lr[x]) - M) / S;
+    if (x < a.n) orow[x] = expf(scaled(a, raw[e]) - M) / S;
   }
+}
+
+// Blocks of k_stoch_fused the current device holds at once (occupancy per CU
+// times the CUs), queried once per device.
+static int fused_capacity(int* hold) {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  WC_HIP(hipGetDevice(&dev));
+  int n = dev >= 0 && dev < 64 ? cache[dev].load(std::memory_order_relaxed) : 0;
+  if (n == 0) {
+    int cus = 0, per_cu = 0;
+    if (device_cus(&cus) != WC_OK) return WC_E_HIP;
+    int per_cu2 = 0;
+    WC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_stoch_fused<false>, kStThreads, 0));
+    WC_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu2, k_stoch_fused<true>, kStThreads, 0));
+    per_cu = std::min(per_cu, per_cu2);
+    n = cus * per_cu;
+    if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  }
+  *hold = n;
+  return WC_OK;
 }
 
 }  // namespace wc
@@ -1158,7 +1742,30 @@ int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, 
   a.bad_flag = reinterpret_cast<unsigned int*>(ws + kStochDecOff + 32);
   const int nch = (vocab + kVocabChunk - 1) / kVocabChunk;
   auto s = reinterpret_cast<hipStream_t>(stream);
-  // the extra row needs K draft-mass blocks plus at least one check block
+  // check blocks: a d2t slice each, and one per draft for its head-row lookup
+  const int ncheck = std::max(rows - 1, d2t_dev ? std::min(32, std::max(1, (head_rows + 1023) / 1024)) : 1);
+  const int groups = (rows + kGroupRows - 1) / kGroupRows;
+  const int grid = rows * nch + groups * nch + (rows - 1) + ncheck;
+  int hold = 0;
+  if (fused_capacity(&hold) != WC_OK) return WC_E_HIP;
+  // only the chunk blocks wait for other blocks: they must fit at once; the
+  // other blocks never wait, so they run whenever a slot frees
+  if (rows <= kFusedRows && nch <= kMailChunks && groups * nch < hold) {
+    MailSet* sets = reinterpret_cast<MailSet*>(ws + kGridBarOff);
+    unsigned int* calls = reinterpret_cast<unsigned int*>(ws + kGridBarOff + 2 * sizeof(MailSet));
+    const int vec = aligned(logits, 16) && ld % 4 == 0;
+    int e2 = 0;
+    const bool p2 = std::frexp(a.temperature, &e2) == 0.5f;  // T = 2^(e2 - 1)
+    if (p2) {
+      a.inv_t = std::ldexp(1.0f, 1 - e2);
+      hipLaunchKernelGGL(k_stoch_fused<true>, dim3(grid), dim3(kStThreads), 0, s, a, nch, ncheck, vec, sets, calls);
+    } else {
+      hipLaunchKernelGGL(k_stoch_fused<false>, dim3(grid), dim3(kStThreads), 0, s, a, nch, ncheck, vec, sets, calls);
+    }
+    WC_LAUNCHED();
+    return WC_OK;
+  }
+  // two launches; the extra row needs K draft-mass blocks plus at least one check block
   hipLaunchKernelGGL(k_stoch_stats, dim3(std::max(nch, rows), rows + 1), dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
   hipLaunchKernelGGL((k_stoch_sample<true>), dim3(nch), dim3(kStThreads), 0, s, a);

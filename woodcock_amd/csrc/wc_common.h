@@ -17,6 +17,8 @@ namespace wc {
 
 int set_error(int status, const char* fmt, ...);
 const char* last_error();
+// compute units of the current device (queried once per device)
+int device_cus(int* cus);
 
 #define WC_REQUIRE(cond, ...)                                  \
   do {                                                         \
@@ -82,6 +84,66 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Wave-wide max (exact in any order) with DPP moves; lanes outside a
+// broadcast's rows keep their own value.  Every lane of the wave must be active.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move_keep(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_move<0xB1>(v));
+  v = fmaxf(v, dpp_move<0x4E>(v));
+  v = fmaxf(v, dpp_move<0x124>(v));
+  v = fmaxf(v, dpp_move<0x128>(v));
+  v = fmaxf(v, dpp_move_keep<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_move_keep<0x143, 0xC>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// fp64 lane moves: the two halves moved alike.  BC: lanes whose source lies
+// outside the row (or wave) receive 0.
+template <int CTRL, int ROW_MASK = 0xf, bool BC = false>
+__device__ __forceinline__ double dpp_move_f64(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(b), CTRL, ROW_MASK, 0xf, BC);
+  const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(b >> 32), CTRL, ROW_MASK, 0xf, BC);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane(static_cast<int>(b), lane);
+  const int hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane);
+  return __longlong_as_double((static_cast<long long>(hi) << 32) | static_cast<unsigned int>(lo));
+}
+// fp64 wave sum, the association of wave_sum_dpp; same value on every lane.
+// Every lane of the wave must be active.
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+  v += dpp_move_f64<0xB1>(v);
+  v += dpp_move_f64<0x4E>(v);
+  v += dpp_move_f64<0x124>(v);
+  v += dpp_move_f64<0x128>(v);
+  v += dpp_move_f64<0x142, 0xA>(v);
+  v += dpp_move_f64<0x143, 0xC>(v);
+  return readlane_f64(v, 63);
+}
+// Inclusive prefix sum over the lanes in lane order: Hillis-Steele steps of 1,
+// 2, 4, 8 lanes within each 16-lane row, then the row totals carried by the
+// lane-15 and lane-31 broadcasts.  Every lane of the wave must be active.
+__device__ __forceinline__ double wave_incl_scan_dpp(double x) {
+  x += dpp_move_f64<0x111, 0xf, true>(x);  // row_shr:1
+  x += dpp_move_f64<0x112, 0xf, true>(x);  // row_shr:2
+  x += dpp_move_f64<0x114, 0xf, true>(x);  // row_shr:4
+  x += dpp_move_f64<0x118, 0xf, true>(x);  // row_shr:8
+  x += dpp_move_f64<0x142, 0xA>(x);        // row_bcast:15 into rows 1 and 3
+  x += dpp_move_f64<0x143, 0xC>(x);        // row_bcast:31 into rows 2 and 3
+  return x;
+}
+// the inclusive scan moved up one lane (lane 0: 0)
+__device__ __forceinline__ double wave_excl_from_incl(double incl) {
+  return dpp_move_f64<0x138, 0xf, true>(incl);  // wave_shr:1
+}
+
 // Reductions over the 16 lanes of a DPP row (lanes 16r .. 16r + 15); every
 // lane of the row receives the result.
 __device__ __forceinline__ float row16_max(float v) {
@@ -98,6 +160,11 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp_move<0x128>(v);
   return v;
 }
+
+// Ties a loaded value to this point: its load cannot be sunk into a later
+// conditional block, where it would wait on its own, one load after another.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(unsigned long long& v) { asm volatile("" : "+v"(v)); }
 
 // Workgroup barrier that orders LDS only: global loads in flight stay in flight
 // (the plain __syncthreads() fence would wait for every outstanding load).
@@ -241,7 +308,13 @@ constexpr size_t kChunkRowsOff = kTreeStateOff + kTreeStateBytes;
 constexpr size_t kChunkRowsBytes = 4 * (kMaxVocabChunks + 4);
 constexpr size_t kStochDecOff = kChunkRowsOff + kChunkRowsBytes;
 constexpr size_t kStochDecBytes = 64;
-constexpr size_t kVerifyWorkspace = kStochDecOff + kStochDecBytes;
+// the one-launch stochastic chain's two mailbox sets (one per call parity) and
+// its call counter
+constexpr int kMailRows = 8, kMailChunks = 256, kMailOther = 64, kMailRep = 4;
+constexpr size_t kMailSetWords = kMailRep * (kMailRows * kMailChunks + 2 * kMailChunks + kMailOther);
+constexpr size_t kGridBarOff = kStochDecOff + kStochDecBytes;
+constexpr size_t kGridBarBytes = 2 * 8 * kMailSetWords + 128;
+constexpr size_t kVerifyWorkspace = kGridBarOff + kGridBarBytes;
 inline unsigned int* verify_counter(void* ws, int which) {
   return reinterpret_cast<unsigned int*>(static_cast<char*>(ws) + kCounterOff + which * kTreeCounterBytes);
 }

@@ -1,4 +1,6 @@
 // wc_lib.hip -- library-level entry points: version, errors, workspace.
+#include <atomic>
+
 #include "wc_common.h"
 
 namespace wc {
@@ -16,6 +18,19 @@ int set_error(int status, const char* fmt, ...) {
 }
 
 const char* last_error() { return g_error.c_str(); }
+
+int device_cus(int* cus) {
+  static std::atomic<int> cache[64];  // 0 = not yet queried
+  int dev = 0;
+  WC_HIP(hipGetDevice(&dev));
+  int n = dev >= 0 && dev < 64 ? cache[dev].load(std::memory_order_relaxed) : 0;
+  if (n == 0) {
+    WC_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+    if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  }
+  *cus = n;
+  return WC_OK;
+}
 
 // zero-fill with plain vector stores (graph-safe replacement for hipMemsetAsync)
 __global__ void k_fill_zero(uint4* __restrict__ p, size_t n16, unsigned char* __restrict__ tail, size_t ntail) {
