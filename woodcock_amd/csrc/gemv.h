@@ -210,10 +210,16 @@ __device__ __forceinline__ void fin_epilogue(const GemvArgs& a, int m, float* s_
       float ss = 0.f;
       float v[kPer];
       const bool small = a.N <= kPer * kGemvThreads;
+      uint32_t gw[kPer];
       if (small) {
-        // all loads issued back to back from clamped addresses, masked after
+        // all loads issued back to back from clamped addresses (the gains with
+        // them, pinned so that none waits inside the store branch), masked after
 #pragma unroll
         for (int j = 0; j < kPer; ++j) v[j] = fetch_f32(yr + min(static_cast<int>(threadIdx.x) + j * kGemvThreads, a.N - 1));
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) gw[j] = a.fin_gain[min(static_cast<int>(threadIdx.x) + j * kGemvThreads, a.N - 1)];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) pin(gw[j]);
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
           if (static_cast<int>(threadIdx.x) + j * kGemvThreads >= a.N) v[j] = 0.f;
@@ -235,7 +241,7 @@ __device__ __forceinline__ void fin_epilogue(const GemvArgs& a, int m, float* s_
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
           const int k = threadIdx.x + j * kGemvThreads;
-          if (k < a.N) a.fin_out[mi * a.ld_fin + k] = v[j] * inv * bf16_to_float(a.fin_gain[k]);
+          if (k < a.N) a.fin_out[mi * a.ld_fin + k] = v[j] * inv * bf16_to_float(static_cast<uint16_t>(gw[j]));
         }
       } else {
         for (int k = threadIdx.x; k < a.N; k += kGemvThreads)

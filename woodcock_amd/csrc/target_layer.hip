@@ -308,9 +308,19 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
     ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + m] : 0.f;
   }
 #pragma unroll
-  for (int c = 0; c < CQ; ++c) {
+  for (int c = 0; c < CQ; ++c)
     resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + min(n0 + c, a.N - 1)] : 0.f;
-    gnv[c] = (a.xa_next && a.gain_next && (!pair || c < 16)) ? a.gain_next[n0 + min(c, pair ? 15 : CQ - 1)] : 0;
+  if (a.xa_next && a.gain_next) {  // every gain load issued before the first is used
+    uint32_t gw[CQ];
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) gw[c] = a.gain_next[n0 + min(c, pair ? 15 : CQ - 1)];
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) pin(gw[c]);
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) gnv[c] = (!pair || c < 16) ? static_cast<uint16_t>(gw[c]) : 0;
+  } else {
+#pragma unroll
+    for (int c = 0; c < CQ; ++c) gnv[c] = 0;
   }
   {
     float tot = 0.f;

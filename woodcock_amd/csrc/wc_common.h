@@ -165,6 +165,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 // conditional block, where it would wait on its own, one load after another.
 __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(unsigned long long& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
 
 // Workgroup barrier that orders LDS only: global loads in flight stay in flight
 // (the plain __syncthreads() fence would wait for every outstanding load).
