@@ -136,10 +136,12 @@ int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p
  * with p never written: logits [rows][ld] are the target logits at
  * [x_n, d_1..d_K]; p_i = softmax(logits_i / max(T, 1e-6)) is formed in place
  * with the same arithmetic (so the decisions and draws equal the two-call
- * path's bit for bit).  Two launches: per (vocabulary chunk, row) softmax
- * partials plus the draft rows' masses, whose last block merges them, runs the
- * accept tests and picks the row to draw from; then the draw over that row.
- * Replaces the verify step of the engine's stochastic chain path
+ * path's bit for bit).  rows <= 8 (and chunk blocks that fit on the GPU at
+ * once): one launch whose blocks hand results over through mailboxes in the
+ * workspace -- a call that gave up waiting (after ~4 s) leaves status
+ * WC_E_HIP and the workspace must be initialised again; longer chains: two
+ * launches (softmax partials, draft masses and the accept tests; then the
+ * draw).  Replaces the verify step of the engine's stochastic chain path
  * (python/woodcock/spec.py:316-324: probs_from_logits + verify_tree_stochastic
  * at width 1). */
 int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, int64_t ld, float temperature,

@@ -21,6 +21,12 @@
 // the draft mass and the values at the drafted token; then a grid over the
 // vocabulary in which every block repeats the (tiny) accept scan, sums its
 // chunk of the chosen row, and the last block locates the draw.
+//
+// wc_verify_chain_stochastic_logits: the same rule on p = softmax(logits / T)
+// formed in place -- one launch with mailbox hand-over (k_stoch_fused) for
+// K + 1 <= 8 rows, else two launches (k_stoch_stats + k_stoch_sample<true>).
+//
+// wc_verify_tree_stochastic: the recursive rule down a draft tree (below).
 #include <atomic>
 #include <cmath>
 
