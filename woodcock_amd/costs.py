@@ -29,21 +29,25 @@ from . import _lib
 from .runtime import ptr, stream_ptr
 
 
-def _capture(fn):
+def _capture(fn, reps: int = 1):
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        fn()
+        for _ in range(reps):
+            fn()
     torch.cuda.synchronize()
     return g
 
 
-def median_ms(fn, iters: int, warmup: int = 3) -> float:
-    """Median GPU time of one fn() call, from a captured graph of it."""
+def median_ms(fn, iters: int, warmup: int = 3, reps: int = 8) -> float:
+    """Median GPU time of one fn() call: a captured graph of `reps` calls,
+    timed per replay and divided by reps, so the replay's own launch latency
+    is spread over the calls (the reference times each call in a loop of
+    mx.eval's, scripts/time_draft_step.py:39-98)."""
     fn()
     torch.cuda.synchronize()
-    g = _capture(fn)
+    g = _capture(fn, reps)
     for _ in range(warmup):
         g.replay()
     ts = []
@@ -53,7 +57,7 @@ def median_ms(fn, iters: int, warmup: int = 3) -> float:
         g.replay()
         e1.record()
         torch.cuda.synchronize()
-        ts.append(e0.elapsed_time(e1))
+        ts.append(e0.elapsed_time(e1) / reps)
     return float(np.median(ts))
 
 

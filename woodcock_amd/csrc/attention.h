@@ -545,8 +545,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float vls[CHK][D];
   __shared__ float s_p[QVM][CHK];
   __shared__ float s_m[QVM], s_l[QVM], s_alpha[QVM];
-  constexpr bool kFuse = QVM <= 4;  // the merge's operands fit the registers
-  __shared__ float s_w[kFuse ? QVM : 1][kMaxSplits];
+  // the merge's operands fit the registers for <= 4 query vectors (a fused
+  // merge of 8 over half the splits measured slower than split + merge launch)
+  constexpr bool kFuse = QVM <= 4;
+  constexpr int kFS = kMaxSplits;
+  __shared__ float s_w[kFuse ? QVM : 1][kFS];
   __shared__ float s_den[QVM];
   __shared__ bool s_last;
 
@@ -747,21 +750,31 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
   // 6. last split of this kv head: merge every split's (m, l, o)
   const float* base = a.partial + static_cast<int64_t>(kh) * S * a.qv_ld * (D + 2);
   const int64_t sstride = static_cast<int64_t>(a.qv_ld) * (D + 2);
-  float ov[OPT][kMaxSplits];
+  // every partial loaded from clamped addresses before any is used
+  float ov[OPT][kFS];
 #pragma unroll
   for (int k = 0; k < OPT; ++k)
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplits; ++sp)
-      ov[k][sp] = (sp < S && ov0 + VSTEP * k < QV) ? fetch_f32(base + sp * sstride + (ov0 + VSTEP * k) * (D + 2) + 2 + od)
-                                                   : 0.f;
-  if (wave < QV && wave < QVM) {  // wave v: lane = split, weights exp(m_s - M) / den
-    const float ms = lane < S ? fetch_f32(base + lane * sstride + wave * (D + 2)) : -INFINITY;
-    const float ls = lane < S ? fetch_f32(base + lane * sstride + wave * (D + 2) + 1) : 0.f;
-    const float M = wave_max(ms);
-    const float wgt = ms == -INFINITY ? 0.f : expf(ms - M);
-    const float den = wave_sum(ls * wgt);
-    if (lane < kMaxSplits) s_w[wave][lane] = lane < S ? wgt : 0.f;
-    if (lane == 0) s_den[wave] = den;
+    for (int sp = 0; sp < kFS; ++sp)
+      ov[k][sp] = fetch_f32(base + min(sp, S - 1) * sstride + min(ov0 + VSTEP * k, max(QV - 1, 0)) * (D + 2) + 2 + od);
+  constexpr int kNw = kAttnThreads / kWave;
+  float ms[(QVM + kNw - 1) / kNw], ls[(QVM + kNw - 1) / kNw];
+#pragma unroll
+  for (int q = 0; q < (QVM + kNw - 1) / kNw; ++q) {  // wave w: query vectors w, w + 4, ...; lane = split
+    const int v = min(wave + q * kNw, max(QV - 1, 0));
+    ms[q] = fetch_f32(base + min(lane, S - 1) * sstride + v * (D + 2));
+    ls[q] = fetch_f32(base + min(lane, S - 1) * sstride + v * (D + 2) + 1);
+  }
+#pragma unroll
+  for (int q = 0; q < (QVM + kNw - 1) / kNw; ++q) {
+    const int v = wave + q * kNw;
+    if (v >= QV || v >= QVM) continue;  // wave-uniform
+    const float m_s = lane < S ? ms[q] : -INFINITY;
+    const float M = wave_max_dpp(m_s);
+    const float wgt = m_s == -INFINITY ? 0.f : expf(m_s - M);
+    const float den = wave_sum_dpp(lane < S ? ls[q] * wgt : 0.f);
+    if (lane < kFS) s_w[v][lane] = lane < S ? wgt : 0.f;
+    if (lane == 0) s_den[v] = den;
   }
   __syncthreads();
 #pragma unroll
@@ -770,7 +783,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
     if (v >= QV) break;
     float num = 0.f;
 #pragma unroll
-    for (int sp = 0; sp < kMaxSplits; ++sp) num = fmaf(s_w[v][sp], ov[k][sp], num);
+    for (int sp = 0; sp < kFS; ++sp) num = fmaf(s_w[v][sp], sp < S ? ov[k][sp] : 0.f, num);
     const float y = num / s_den[v];
     const int l = v / rep, h = kh * rep + v % rep;
     a.out[l * a.ld_out + h * D + od] = y;

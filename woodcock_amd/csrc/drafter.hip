@@ -170,17 +170,26 @@ static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
   const bool wide = PAIR || a.N >= 8192;
   const int rb = PAIR ? 16 : wide ? 32 : 16;
   const dim3 grid((a.N + rb - 1) / rb);
-#define WC_GF(TW, GBV)                                                                                 \
-  hipLaunchKernelGGL((k_gemvf<TW, TW == 1 ? 8 : 4, TW == 1 ? 6 : 4, PAIR, NIN, XB, GBV>), grid,           \
-                     dim3((TW == 1 ? 8 : 4) * kWave), 0, s, a)
+  // single-tile grids of at most one block per CU split each block's k steps
+  // over 16 waves (4 steps in flight each) instead of 8 (6 in flight)
+  const bool deep = !wide && grid.x <= 256;
+#define WC_GF_L(TW, W, D, GBV) \
+  hipLaunchKernelGGL((k_gemvf<TW, W, D, PAIR, NIN, XB, GBV>), grid, dim3((W) * kWave), 0, s, a)
+#define WC_GF(TW, GBV)                          \
+  do {                                          \
+    if (TW == 2) WC_GF_L(2, 4, 4, GBV);         \
+    else if (deep) WC_GF_L(1, 16, 4, GBV);      \
+    else WC_GF_L(1, 8, 6, GBV);                 \
+  } while (0)
   if (gb == kAll) {
-    if (wide) WC_GF(2, kAll); else if constexpr (!PAIR) WC_GF(1, kAll);
+    if (wide) WC_GF_L(2, 4, 4, kAll); else if constexpr (!PAIR) WC_GF(1, kAll);
   } else if constexpr (NIN == 1) {
-    if (wide) WC_GF(2, 0); else if constexpr (!PAIR) WC_GF(1, 0);
+    if (wide) WC_GF_L(2, 4, 4, 0); else if constexpr (!PAIR) WC_GF(1, 0);
   } else {
     return false;
   }
 #undef WC_GF
+#undef WC_GF_L
   return true;
 }
 
