@@ -200,7 +200,8 @@ int wc_sample_without_replacement(const float* q, int rows, int head_rows, int64
  * mode (python/woodcock/spec.py:216-303; policies.py:49-75) without a host
  * round trip per level: a node table (token, parent, depth, phat in fp64,
  * cache slot, feedback row) lives in a caller-owned device state of
- * wc_tree_draft_state_bytes() bytes (at most 512 nodes, width <= 8).  The
+ * wc_tree_draft_state_bytes() bytes, zero-initialised once (at most 512
+ * nodes, width <= 8; the expansion's counters reset themselves).  The
  * caller runs, per level, the draft head (logits) and wc_probs_from_logits at
  * T = 1 over the frontier rows, wc_tree_draft_expand, and unless it is the last
  * level wc_tree_draft_frontier plus wc_drafter_forward with the inputs it

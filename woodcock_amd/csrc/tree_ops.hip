@@ -70,12 +70,18 @@ constexpr int kTdMaxNodes = 512;
 constexpr int kTdMaxWidth = 8;
 constexpr int kTdThreads = 256;
 
+constexpr int kTdParts = 16;  // blocks per frontier row in the expansion
+
 struct TreeDraftState {
   double phat[kTdMaxNodes];
   int32_t token[kTdMaxNodes], parent[kTdMaxNodes], depth[kTdMaxNodes];
   int32_t slot[kTdMaxNodes];   // drafter cache slot once forwarded
   int32_t store[kTdMaxNodes];  // row of the node's out / feedback once forwarded (the root: 0)
   int32_t front[kTdMaxWidth];  // node ids of the current frontier, in frontier-row order
+  // expansion: each part's top-width keys per frontier row, and a counter per
+  // row (own 128-byte line; reset by the block that completes it)
+  unsigned long long cand[kTdMaxWidth][kTdParts][kTdMaxWidth];
+  unsigned int ctr[kTdMaxWidth][32];
 };
 
 __global__ void k_td_begin(TreeDraftState* st, const int32_t* __restrict__ root_token) {
@@ -112,8 +118,12 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
                                                           const int32_t* __restrict__ d2t, int width,
                                                           int node_base) {
   __shared__ unsigned long long red[kTdThreads / kWave];
-  const int r = blockIdx.x, t = threadIdx.x;
+  __shared__ bool s_last;
+  const int r = blockIdx.x, p = blockIdx.y, P = gridDim.y, t = threadIdx.x;
   const float* qr = q + static_cast<int64_t>(r) * ld_q;
+  // part p: the rows [i0, i1) of the head (a multiple of 4 long, so aligned rows stay aligned)
+  const int span = ((head_rows + P - 1) / P + 3) & ~3;
+  const int i0 = min(p * span, head_rows), i1 = min(i0 + span, head_rows);
   unsigned long long top[kTdMaxWidth];
 #pragma unroll
   for (int j = 0; j < kTdMaxWidth; ++j) top[j] = 0;
@@ -129,16 +139,16 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
   };
   // 16-byte vectors where the row is 16-byte aligned, the tail (and unaligned rows) element-wise
   const bool al = (reinterpret_cast<uintptr_t>(qr) & 15) == 0;
-  const int n4 = al ? head_rows / 4 : 0;
+  const int b4 = i0 / 4, e4 = al ? i1 / 4 : b4;
   const float4* q4 = reinterpret_cast<const float4*>(qr);
-  for (int b = 0; b < n4; b += kTdThreads * kTdVec) {
+  for (int b = b4; b < e4; b += kTdThreads * kTdVec) {
     float4 v[kTdVec];
 #pragma unroll
-    for (int u = 0; u < kTdVec; ++u) v[u] = q4[min(b + u * kTdThreads + t, n4 - 1)];
+    for (int u = 0; u < kTdVec; ++u) v[u] = q4[min(b + u * kTdThreads + t, e4 - 1)];
 #pragma unroll
     for (int u = 0; u < kTdVec; ++u) {
       const int i4 = b + u * kTdThreads + t;
-      if (i4 < n4) {
+      if (i4 < e4) {
         insert(v[u].x, 4 * i4);
         insert(v[u].y, 4 * i4 + 1);
         insert(v[u].z, 4 * i4 + 2);
@@ -146,15 +156,33 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
       }
     }
   }
-  for (int i = 4 * n4 + t; i < head_rows; i += kTdThreads) insert(qr[i], i);
-  const int v = st->front[r];
+  for (int i = 4 * e4 + t; i < i1; i += kTdThreads) insert(qr[i], i);
+  // the part's top keys, largest first (keys are unique: the row is in the key)
   for (int j = 0; j < width; ++j) {
     const unsigned long long best = block_max_u64(top[0], red);
-    if (best != 0 && top[0] == best) {  // keys are unique (the row is in the key): one owner pops
+    if (best != 0 && top[0] == best) {
 #pragma unroll
       for (int i = 0; i + 1 < kTdMaxWidth; ++i) top[i] = top[i + 1];
       top[kTdMaxWidth - 1] = 0;
     }
+    if (t == 0) atomic_store_u64(&st->cand[r][p][j], best);
+  }
+  // the last part of the row to finish merges every part's keys
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const bool last = __hip_atomic_fetch_add(&st->ctr[r][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      static_cast<unsigned int>(P - 1);
+    if (last) __hip_atomic_store(&st->ctr[r][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  unsigned long long k = t < P * width ? atomic_load_u64(&st->cand[r][t / width][t % width]) : 0ull;
+  const int v = st->front[r];
+  for (int j = 0; j < width; ++j) {
+    const unsigned long long best = block_max_u64(k, red);
+    if (best != 0 && k == best) k = 0;
     if (t == 0) {
       const int row = argmax_key_index(best);
       const int c = node_base + r * width + j;
@@ -453,7 +481,9 @@ int wc_tree_draft_expand(void* state, const float* q, int rows, int head_rows, i
   WC_REQUIRE(node_base >= 1 && node_base + rows * width <= kTdMaxNodes,
              "wc_tree_draft_expand: nodes %d..%d outside the table of %d", node_base, node_base + rows * width,
              kTdMaxNodes);
-  hipLaunchKernelGGL(k_td_expand, dim3(rows), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+  // parts of at least 1024 head rows each, at most kTdParts per frontier row
+  const int parts = std::max(1, std::min(kTdParts, head_rows / 1024));
+  hipLaunchKernelGGL(k_td_expand, dim3(rows, parts), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<TreeDraftState*>(state), q, head_rows, ld_q, d2t_dev, width, node_base);
   WC_LAUNCHED();
   return WC_OK;
