@@ -33,6 +33,10 @@ import numpy as np
 
 PEAK_HBM_GBS = 8000.0
 BASE_CTX = 512
+CTX4 = 4096  # drafter context of the Qwen3-4B-shape step
+# algorithmic bytes of that step: head 16384 x 2560, the layer (QKV over the fed
+# feature and the embedding, o, gate / up, down) and the KV at ctx 4096 + 1
+STEP4_BYTES = 83_886_080 + 233_308_160 + 16_781_312
 K = 4
 
 
@@ -337,11 +341,43 @@ def bench_gpu(args):
     def tree_drafts():
         tdr.draft(td_tok, td_root, td_root, td_off)
 
+    # config 4's draft step: Qwen3-4B drafter shape (hidden 2560, 32 / 8 heads,
+    # intermediate 9728, fc 7680 -> 2560), 16k trimmed head, drafter ctx 4096
+    from woodcock_amd.config import QWEN3_EOS, qwen3_4b_drafter
+    from woodcock_amd.drafter import Drafter
+    from woodcock_amd.synthetic import draft_vocab, random_drafter
+
+    cfg4 = qwen3_4b_drafter()
+    d4 = Drafter(cfg4, random_drafter(cfg4, seed=args.seed + 7, device=out1.device), out1.device, torch.bfloat16)
+    d4.restrict_vocab(draft_vocab(cfg4.vocab_size, 16384, seed=args.seed + 7, always=QWEN3_EOS))
+    cache4 = d4.make_cache(CTX4 + 16)
+    g4 = torch.Generator(device=out1.device).manual_seed(args.seed + 8)
+    for c in cache4:
+        c.keys[0, :, :CTX4] = torch.randn(c.keys[0, :, :CTX4].shape, generator=g4, device=out1.device).bfloat16()
+        c.values[0, :, :CTX4] = torch.randn(c.values[0, :, :CTX4].shape, generator=g4, device=out1.device).bfloat16()
+    dims4, W4, ws4 = C.byref(d4.dims), C.byref(d4.wstruct), ptr(d4.ws)
+    hid4 = torch.randn(1, cfg4.hidden_size, generator=g4, device=out1.device)
+    out4 = torch.empty_like(hid4)
+    hid4s = torch.empty_like(hid4)
+    tok4 = torch.zeros(1, dtype=torch.int32, device=out1.device)
+    off4 = torch.tensor([CTX4], dtype=torch.int32, device=out1.device)
+    kp4 = (C.c_void_p * 1)(cache4[0].keys.data_ptr())
+    vp4 = (C.c_void_p * 1)(cache4[0].values.data_ptr())
+
+    def steps_4b():
+        for _ in range(REP):
+            _lib.call("wc_draft_head_norm", dims4, W4, ptr(hid4), cfg4.hidden_size, None, 0, ptr(out4),
+                      cfg4.hidden_size, None, 0, ptr(tok4), None, None, ws4, s())
+            _lib.call("wc_drafter_forward", dims4, W4, ptr(tok4), ptr(out4), cfg4.hidden_size, None, 0, 1, None,
+                      kp4, vp4, _lib.WC_BF16, cache4[0].capacity, ptr(off4), 0, None, None, 0, ptr(hid4s), None,
+                      None, ws4, s())
+
     comps = {}
     reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1, "tree_draft": 1}
     for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
                      ("draft_probs", draft_probs), ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies),
-                     ("target_chain", target_chain), ("target_tree", target_tree), ("tree_draft", tree_drafts)):
+                     ("target_chain", target_chain), ("target_tree", target_tree), ("tree_draft", tree_drafts),
+                     ("draft_step_4b", steps_4b)):
         fn()
         torch.cuda.synchronize()
         g = capture(fn)
@@ -372,6 +408,7 @@ def bench_gpu(args):
         "target_chain_us": comps["target_chain"],
         "target_tree_us": comps["target_tree"],
         "tree_draft_us": comps["tree_draft"],
+        "draft_step_4b_us": comps["draft_step_4b"],
         "head_bytes": head_bytes,
         "step_bytes": step_bytes,
         "compact_bytes_avg": compact_bytes,
@@ -631,6 +668,8 @@ def main():
             "target_forward_us_qwen3_1p7b_28l_m5_ctx512": round(r["target_chain_us"], 1),
             "target_forward_us_qwen3_1p7b_28l_m60_tree_ctx2048": round(r["target_tree_us"], 1),
             "tree_draft_us_qwen3_1p7b_depth6_width4_n60": round(r["tree_draft_us"], 1),
+            "draft_step_us_qwen3_4b_ctx4096": round(r["draft_step_4b_us"], 2),
+            "draft_step_hbm_frac_qwen3_4b": round(STEP4_BYTES / (r["draft_step_4b_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "head_gemv_us": round(r["head_us"], 2),
         },
         "roofline": {

@@ -92,11 +92,16 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
   }
 }
 
+// Step counts: 4 (K 2048), 5 (K 2560), 8, 12 (K 6144) and 20 (K up to 10240,
+// e.g. 9728); a count between two variants runs the larger with its last steps
+// masked, so the Qwen3-1.7B and -4B widths each get an exact variant.
 template <int R, bool PAIR, int NIN, int XB>
 static bool launch_gemv1(const GemvArgs& a, int steps, hipStream_t s) {
   if (steps <= 4) return launch_gemv1_s<R, PAIR, NIN, 4, XB>(a, s);
+  if (steps <= 5) return launch_gemv1_s<R, PAIR, NIN, 5, XB>(a, s);
   if (steps <= 8) return launch_gemv1_s<R, PAIR, NIN, 8, XB>(a, s);
   if (steps <= 12) return launch_gemv1_s<R, PAIR, NIN, 12, XB>(a, s);
+  if (steps <= 20) return launch_gemv1_s<R, PAIR, NIN, 20, XB>(a, s);
   return false;
 }
 
@@ -221,8 +226,9 @@ static int launch_gemvm(GemvArgs a, int max_k, hipStream_t s) {
   return WC_OK;
 }
 
-// Every K a multiple of 512 (up to 6144): one row goes to the register-resident
-// kernel, 2..8 rows to the LDS-staged few-row kernel; anything else to the
+// One row with every K a multiple of 512 (up to 10240) goes to the
+// register-resident kernel; 2..16 rows to the MFMA few-row kernel (K multiple
+// of 32), else 2..8 rows to the LDS-staged few-row kernel; anything else to the
 // chunked LDS kernel.
 static int launch_gemv(const GemvArgs& a, int /*R hint*/, hipStream_t s) {
   if (a.M < 1 || a.M > kMaxM) return set_error(WC_E_INVALID, "gemv: rows %d not in 1..%d", a.M, kMaxM);
