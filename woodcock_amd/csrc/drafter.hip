@@ -13,6 +13,9 @@
 // argmax / Gumbel-max and d2t map (drafter.py:204-215, spec.py:346).
 // Every round-varying integer (offset, row counts, gathered rows, tokens) is
 // read from device memory.
+#include <mutex>
+#include <unordered_map>
+
 #include "attention.h"
 #include "gemv.h"
 #include "gemvf.h"
@@ -160,6 +163,28 @@ static bool launch_gemvx_r(const GemvArgs& a, int steps, hipStream_t s) {
   return launch_gemvx_m<1, PAIR, NIN, XB, MM>(a, steps, s);
 }
 
+// Dynamic LDS of the staged few-row GEMV: a kernel takes `bytes` when its static
+// LDS plus `bytes` fits the CU (its dynamic limit raised once per kernel).
+constexpr size_t kGfStageMax = 136 * 1024;
+static bool gf_stage_ok(const void* kern, size_t bytes) {
+  static std::mutex mu;
+  static std::unordered_map<const void*, size_t> room;  // kernel -> dynamic bytes it may take
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = room.find(kern);
+  if (it == room.end()) {
+    hipFuncAttributes fa{};
+    size_t r = 0;
+    if (hipFuncGetAttributes(&fa, kern) == hipSuccess && fa.sharedSizeBytes + 1024 < kCuLds + 2048) {
+      r = kCuLds + 2048 - 1024 - fa.sharedSizeBytes;
+      if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(r)) != hipSuccess)
+        r = 0;
+    }
+    (void)hipGetLastError();
+    it = room.emplace(kern, r).first;
+  }
+  return bytes <= it->second;
+}
+
 // Few-row MFMA GEMV: 16 (TW = 1) or 32 (TW = 2, and the gate / up pair) rows
 // per block, every K a multiple of 32, no last-block norm / normalised-input
 // epilogues (those are the one-row kernel's; a bare offset advance is done).
@@ -178,8 +203,27 @@ static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
   // single-tile grids of at most one block per CU split each block's k steps
   // over 16 waves (4 steps in flight each) instead of 8 (6 in flight)
   const bool deep = !wide && grid.x <= 256;
-#define WC_GF_L(TW, W, D, GBV) \
-  hipLaunchKernelGGL((k_gemvf<TW, W, D, PAIR, NIN, XB, GBV>), grid, dim3((W) * kWave), 0, s, a)
+  // the input rows staged once per block in LDS (x * gain, fp32) when they fit
+  size_t stage = 0;
+  int units = 0;
+  for (int i = 0; i < a.n_in; ++i) {
+    stage += static_cast<size_t>(a.M) * a.in[i].K * sizeof(float);
+    units += a.M * ((a.in[i].K + kGfUnit - 1) / kGfUnit);
+  }
+  const bool stg = units <= 3 * 16 * 3 && stage <= kGfStageMax;
+  GemvArgs as = a;
+  as.lds_floats = static_cast<int>(stage / sizeof(float));
+  // the dynamic region also holds the waves' partial tiles after the main loop
+#define WC_GF_DYN(TW, W) std::max(stage, static_cast<size_t>(W) * NIN * (TW) * 4 * kWave * sizeof(float))
+#define WC_GF_L(TW, W, D, GBV)                                                                              \
+  do {                                                                                                      \
+    if (stg && gf_stage_ok(reinterpret_cast<const void*>(&k_gemvf<TW, W, D, PAIR, NIN, XB, GBV, true>),       \
+                           WC_GF_DYN(TW, W)))                                                               \
+      hipLaunchKernelGGL((k_gemvf<TW, W, D, PAIR, NIN, XB, GBV, true>), grid, dim3((W) * kWave),              \
+                         WC_GF_DYN(TW, W), s, as);                                                          \
+    else                                                                                                    \
+      hipLaunchKernelGGL((k_gemvf<TW, W, D, PAIR, NIN, XB, GBV>), grid, dim3((W) * kWave), 0, s, a);        \
+  } while (0)
 #define WC_GF(TW, GBV)                          \
   do {                                          \
     if (TW == 2) WC_GF_L(2, 4, 4, GBV);         \
@@ -195,6 +239,7 @@ static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
   }
 #undef WC_GF
 #undef WC_GF_L
+#undef WC_GF_DYN
   return true;
 }
 
