@@ -109,12 +109,14 @@ static bool launch_gemv1(const GemvArgs& a, int steps, hipStream_t s) {
 }
 
 // Largest rows-per-wave that keeps at least 512 blocks and fits the budget;
-// the draft head (argmax epilogue) takes at most two: twice the waves in
-// flight measured faster (16384 x 2048: 14.3 against 15.6 us at four).
+// the draft head (argmax epilogue) takes at most two and the gate/up pair one:
+// more waves in flight measured faster (head 16384 x 2048: 14.3 against 15.6 us
+// at four; the pair: 0.4 us of a 1.7B draft step, 0.9 us of a 4B one).
 template <bool PAIR, int NIN, int XB>
 static bool launch_gemv1_r(const GemvArgs& a, int steps, hipStream_t s) {
-  if (a.N >= 4 * kGemvWaves * 512 && a.epi != kEpiArgmax && launch_gemv1<4, PAIR, NIN, XB>(a, steps, s)) return true;
-  if (a.N >= 2 * kGemvWaves * 512 && launch_gemv1<2, PAIR, NIN, XB>(a, steps, s)) return true;
+  if (a.N >= 4 * kGemvWaves * 512 && a.epi != kEpiArgmax && !PAIR && launch_gemv1<4, PAIR, NIN, XB>(a, steps, s))
+    return true;
+  if (a.N >= 2 * kGemvWaves * 512 && !PAIR && launch_gemv1<2, PAIR, NIN, XB>(a, steps, s)) return true;
   return launch_gemv1<1, PAIR, NIN, XB>(a, steps, s);
 }
 
