@@ -54,7 +54,7 @@ typedef struct wc_verdict {
   int32_t next;        /* target token after the accepted prefix / path */
   int32_t n_keep;      /* n_accepted + 1: verify-block entries the KV compaction keeps */
   int32_t n_uniforms;  /* uniforms consumed (stochastic rules), 0 for greedy */
-  int32_t status;      /* 0, or WC_E_INVALID when the device saw an invalid input */
+  int32_t status;      /* 0; WC_E_INVALID when the device saw an invalid input; WC_E_HIP when a bounded wait gave up */
   int32_t reserved[3];
   int32_t tokens[WC_MAX_NODES + 1]; /* accepted tokens then `next` (n_keep entries) */
   int32_t keep[WC_MAX_NODES + 1];   /* verify-block rows kept: 0 then the accepted nodes */
@@ -139,7 +139,8 @@ int wc_verify_chain_stochastic(const float* p, int rows, int vocab, int64_t ld_p
  * path's bit for bit).  rows <= 8 (and chunk blocks that fit on the GPU at
  * once): one launch whose blocks hand results over through mailboxes in the
  * workspace -- a call that gave up waiting (after ~4 s) leaves status
- * WC_E_HIP and the workspace must be initialised again; longer chains: two
+ * WC_E_HIP and the workspace must be initialised again (wc_workspace_init;
+ * until then every call on it fails fast with WC_E_HIP); longer chains: two
  * launches (softmax partials, draft masses and the accept tests; then the
  * draw).  Replaces the verify step of the engine's stochastic chain path
  * (python/woodcock/spec.py:316-324: probs_from_logits + verify_tree_stochastic
@@ -149,6 +150,15 @@ int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, 
                                       const int32_t* draft_tokens_dev, const int32_t* draft_rows_dev,
                                       const wc_uniforms* rng, wc_verdict* verdict_dev, void* workspace,
                                       wc_stream_t stream);
+
+/* Bounded waits of the one-launch stochastic chain kernel: a waiting block
+ * gives up after `polls` polls (polls < 0 restores the default, ~4 s), leaving
+ * WC_E_HIP in the verdict and a sticky failure flag in the workspace; every
+ * later call on that workspace fails fast with WC_E_HIP until
+ * wc_workspace_init zero-fills it again.  A test hook (process-wide; takes
+ * effect at the next launch) for forcing that path from the host without a
+ * kernel that never ends.  No reference counterpart. */
+int wc_set_spin_limit(int polls);
 
 /* Stochastic tree verification, fp64 decisions: N = rows flattened nodes (node 0
  * the root, parents[0] = -1, 0 <= parents[i] < i, children in ascending node
@@ -313,11 +323,14 @@ size_t wc_drafter_workspace_bytes(const wc_drafter_dims* dims);
 
 /* g[r] = fc(concat_f RMS_f(tap_f[row r])) for r < rows (device count *n_rows_dev
  * when not NULL).  taps: num_features device pointers, [.][tap_ld] of tap_dtype;
- * tap_rows_dev (optional) gathers tap rows (e.g. the accepted path, keep).
+ * tap_rows_dev (optional) gathers tap rows (e.g. the accepted path, keep): row r
+ * reads tap row tap_rows_dev[r], clamped into [0, tap_rows) -- the rows each tap
+ * holds (ignored without tap_rows_dev), so stale entries past the device row
+ * count never read outside the taps.
  * Replaces Drafter.fuse (python/woodcock/drafter.py:149-153; src/core/drafter.cpp:75-89). */
 int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps, int tap_dtype,
-                    int64_t tap_ld, const int32_t* tap_rows_dev, int rows, const int32_t* n_rows_dev, float* g_out,
-                    int64_t g_ld, void* workspace, wc_stream_t stream);
+                    int64_t tap_ld, const int32_t* tap_rows_dev, int tap_rows, int rows, const int32_t* n_rows_dev,
+                    float* g_out, int64_t g_ld, void* workspace, wc_stream_t stream);
 
 /* One drafting forward over `rows` tokens appended at cache offset
  * *offset_dev + offset_add: every layer (dual-stream layer 0, GQA attention
@@ -412,6 +425,64 @@ int wc_draft_head_norm(const wc_drafter_dims* dims, const wc_drafter_weights* w,
                        int64_t hidden_ld, const int32_t* row_dev, int row_add, float* out_norm, int64_t out_ld,
                        float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
                        const wc_gumbel* gumbel, void* workspace, wc_stream_t stream);
+
+/* ------------------------------------------------------------------ backend operations
+ * The reference runtime's backend interface (include/woodcock/ops.h:9-24,
+ * implemented on the CPU by src/backends/cpu_ops.cpp:45-115) on device fp32
+ * buffers, for a backend under the reference's own C++ runtime
+ * (Drafter::forward, src/core/drafter.cpp:106-133; Qwen3::forward,
+ * src/core/qwen3.cpp:86-111).  Same argument meaning and layouts: activations
+ * [rows][cols] row-major, attention K / V as KVCache rows [T][Hk][D].  Weights
+ * are bf16 or fp32 (w_dtype).  The fused entry points above are the hot path;
+ * these are single operations. */
+
+/* y[r] = x[r] * (1 / sqrt(mean(x[r]^2) + eps)) * w for r < rows, row length d,
+ * the mean from an fp64 sum; x and y may alias.  Replaces ops::rmsnorm
+ * (include/woodcock/ops.h:13; src/backends/cpu_ops.cpp:50-59). */
+int wc_rmsnorm(const float* x, float* y, int rows, int d, const void* w, int w_dtype, float eps,
+               wc_stream_t stream);
+
+/* y[L][out] (+)= x[L][in] . W[out][in]^T (accumulate != 0 adds to y).
+ * Replaces ops::linear (include/woodcock/ops.h:11; src/backends/cpu_ops.cpp:45-48). */
+int wc_linear(const float* x, int L, int in, const void* W, int w_dtype, int out, float* y, int accumulate,
+              wc_stream_t stream);
+
+/* Rotate-half RoPE in place on x[L][heads][head_dim] at positions_dev[L]:
+ * inv_i = powf(base, -2i/D) (formed on the host), angle = (float)pos * inv_i.
+ * cos_table / sin_table [max_pos][D/2] (optional, from wc_rope_table) supply
+ * cos / sin for positions below max_pos; otherwise the device computes them.
+ * Replaces ops::rope (include/woodcock/ops.h:15; src/backends/cpu_ops.cpp:61-77). */
+int wc_rope(float* x, int L, int heads, int head_dim, const int32_t* positions_dev, float base,
+            const float* cos_table, const float* sin_table, int max_pos, wc_stream_t stream);
+
+/* gate[i] = silu(gate[i]) * up[i] for i < n.  Replaces ops::silu_mul
+ * (include/woodcock/ops.h:17; src/backends/cpu_ops.cpp:79-84). */
+int wc_silu_mul(float* gate, const float* up, int64_t n, wc_stream_t stream);
+
+/* softmax(scale * q K^T + mask) V: q [L][H][D], K / V [T][Hk][D] (GQA: head h
+ * reads kv head h / (H / Hk)), mask [L][T] uint8 (NULL = all visible),
+ * out [L][H][D], D <= 256.  Replaces ops::attention (include/woodcock/ops.h:19-21;
+ * src/backends/cpu_ops.cpp:98-115). */
+int wc_attention(const float* q, int L, int H, int Hk, int D, const float* K, const float* V, int T,
+                 const uint8_t* mask, float* out, float scale, wc_stream_t stream);
+
+/* In-place softmax of `rows` rows of n: exp(x - max) (0 at -inf), fp64 sum,
+ * multiplied by (float)(1 / sum).  rows = 1 is ops::softmax
+ * (include/woodcock/ops.h:22; src/backends/cpu_ops.cpp:86-96). */
+int wc_softmax(float* x, int rows, int n, wc_stream_t stream);
+
+/* KV rows of L tokens, k / v [L][row] fp32 (row = kv_heads * head_dim), copied
+ * to rows *offset_dev + l of k_cache / v_cache [capacity][row] (rows past the
+ * capacity are dropped); then, when advance_dev is not NULL, *advance_dev =
+ * *offset_dev + L (advance_dev may be offset_dev).  Replaces KVCache::append +
+ * commit (include/woodcock/cache.h:17-19; src/cache/kv_cache.cpp:8-19). */
+int wc_kv_append(float* k_cache, float* v_cache, int capacity, int row, const float* k, const float* v, int L,
+                 const int32_t* offset_dev, int32_t* advance_dev, wc_stream_t stream);
+
+/* *offset_dev = n, stream-ordered (a kernel, graph-safe): the rollback of a
+ * drafting phase.  Replaces KVCache::trim_to (include/woodcock/cache.h:19) and
+ * the cache offset assignment of python/woodcock/spec.py:275-276,351-352. */
+int wc_kv_set_offset(int32_t* offset_dev, int n, wc_stream_t stream);
 
 #ifdef __cplusplus
 }

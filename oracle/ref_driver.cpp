@@ -9,6 +9,7 @@
 // tests can produce golden vectors and cross-check the restatement in
 // oracle/wc_oracle.c.  Exceptions never cross the ABI: every entry point
 // returns 0 on success and -1 on error (message via wcref_last_error).
+#include <array>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -25,9 +26,9 @@ using namespace woodcock;
 
 static thread_local std::string g_err;
 
-#define GUARD(body)                  \
+#define GUARD(...)                   \
   try {                              \
-    body;                            \
+    __VA_ARGS__;                     \
     return 0;                        \
   } catch (const std::exception& e) { \
     g_err = e.what();                \
@@ -108,6 +109,39 @@ int wcref_cache_rows(void* c, int layer, int which, int n, float* dst) {
   })
 }
 
+// ------------------------------------------------------------------ target model (model.h:19-48)
+
+int wcref_qwen3_open(const char* dir, int t0, int t1, int t2, void** out) {
+  GUARD(*out = new Qwen3(dir, std::array<int, 3>{t0, t1, t2}))
+}
+void wcref_qwen3_close(void* m) { delete static_cast<Qwen3*>(m); }
+int wcref_qwen3_cache_new(void* m, void** out) { GUARD(*out = new KVCache(static_cast<Qwen3*>(m)->make_cache())) }
+
+// forward (model.h:36-37): positions [L] and mask [L][cache + L] optional;
+// logits [L][vocab]; taps [3][L][hidden] in the order the forward pushes them
+int wcref_qwen3_forward(void* m, const int* tokens, int L, void* cache, const int* positions, const uint8_t* mask,
+                        float* logits, float* taps) {
+  GUARD({
+    auto* q = static_cast<Qwen3*>(m);
+    auto* kv = static_cast<KVCache*>(cache);
+    std::vector<int> tok(tokens, tokens + L), pos;
+    std::vector<uint8_t> msk;
+    ForwardArgs a;
+    if (positions) {
+      pos.assign(positions, positions + L);
+      a.positions = &pos;
+    }
+    if (mask) {
+      msk.assign(mask, mask + int64_t(L) * (kv->size() + L));
+      a.mask = &msk;
+    }
+    ForwardOut o = q->forward(tok, *kv, a);
+    std::memcpy(logits, o.logits.data(), sizeof(float) * o.logits.size());
+    for (size_t i = 0; i < o.taps.size(); ++i)
+      std::memcpy(taps + i * o.taps[i].size(), o.taps[i].data(), sizeof(float) * o.taps[i].size());
+  })
+}
+
 // ------------------------------------------------------------------ sampling (sampling.h:21-45)
 
 int wcref_argmax(const float* z, int n) { return argmax(z, n); }
@@ -166,6 +200,16 @@ int wcref_rope(float* x, int L, int heads, int D, const int* positions, float ba
   GUARD(ops::rope(x, L, heads, D, positions, base))
 }
 int wcref_softmax(float* x, int n) { GUARD(ops::softmax(x, n)) }
+// linear over an fp32 weight [out][in] held in a Tensor (weights.h:14-24)
+int wcref_linear(const float* x, int L, int in, const float* W, int out, float* y, int accumulate) {
+  GUARD({
+    Tensor t;
+    t.shape = {out, in};
+    t.data.assign(W, W + int64_t(out) * in);
+    ops::linear(x, L, in, t, y, accumulate != 0);
+  })
+}
+int wcref_silu_mul(float* gate, const float* up, int64_t n) { GUARD(ops::silu_mul(gate, up, n)) }
 int wcref_attention(const float* q, int L, int H, int Hk, int D, const float* K, const float* V, int T,
                     const uint8_t* mask, float* out, float scale) {
   GUARD(ops::attention(q, L, H, Hk, D, K, V, T, mask, out, scale))

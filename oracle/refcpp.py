@@ -55,6 +55,12 @@ def lib():
         L.wcref_rope.argtypes = [P, C.c_int, C.c_int, C.c_int, P, C.c_float]
         L.wcref_softmax.argtypes = [P, C.c_int]
         L.wcref_attention.argtypes = [P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, C.c_int, P, P, C.c_float]
+        L.wcref_linear.argtypes = [P, C.c_int, C.c_int, P, C.c_int, P, C.c_int]
+        L.wcref_silu_mul.argtypes = [P, P, C.c_int64]
+        L.wcref_qwen3_open.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+        L.wcref_qwen3_close.argtypes = [P]
+        L.wcref_qwen3_cache_new.argtypes = [P, C.POINTER(C.c_void_p)]
+        L.wcref_qwen3_forward.argtypes = [P, P, C.c_int, P, P, P, P, P]
     return _lib
 
 
@@ -188,6 +194,109 @@ class RefCache:
         out = np.empty((n, self.row), dtype=np.float32)
         _check(lib().wcref_cache_rows(self.h, layer, which, n, _p(out)))
         return out
+
+
+class RefQwen3:
+    """The reference C++ Qwen3 target (include/woodcock/model.h:19-48) over a temp
+    dir holding config.json + model.safetensors under the Hugging Face names
+    (src/core/qwen3.cpp:22-83).  cfg: target.TargetConfig-like; weights: our
+    names (``layers.{i}.*``, ``embed_tokens.weight``, ``norm.weight``) -> bf16 bits."""
+
+    def __init__(self, cfg, weights: dict[str, np.ndarray], taps=(-1, -1, -1)):
+        import torch
+        from safetensors.torch import save_file
+
+        self.cfg = cfg
+        self._tmp = tempfile.TemporaryDirectory()
+        path = Path(self._tmp.name)
+        (path / "config.json").write_text(json.dumps({
+            "hidden_size": cfg.hidden_size, "num_hidden_layers": cfg.num_layers,
+            "num_attention_heads": cfg.num_heads, "num_key_value_heads": cfg.num_kv_heads,
+            "head_dim": cfg.head_dim, "intermediate_size": cfg.intermediate_size, "vocab_size": cfg.vocab_size,
+            "rms_norm_eps": cfg.rms_norm_eps, "rope_theta": cfg.rope_theta,
+            "tie_word_embeddings": cfg.tie_word_embeddings}))
+        tensors = {"model." + k: torch.from_numpy(np.ascontiguousarray(v, dtype=np.uint16).view(np.int16))
+                   .view(torch.bfloat16) for k, v in weights.items()}
+        save_file(tensors, str(path / "model.safetensors"))
+        h = C.c_void_p()
+        _check(lib().wcref_qwen3_open(str(path).encode(), *[int(t) for t in taps], C.byref(h)))
+        self.h = h
+        self.n_taps = 3
+
+    def close(self):
+        if self.h:
+            lib().wcref_qwen3_close(self.h)
+            self.h = None
+        self._tmp.cleanup()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def make_cache(self) -> RefCache:
+        h = C.c_void_p()
+        _check(lib().wcref_qwen3_cache_new(self.h, C.byref(h)))
+        return RefCache(h, self.cfg.num_layers, self.cfg.num_kv_heads * self.cfg.head_dim)
+
+    def forward(self, tokens, cache: RefCache, positions=None, mask=None):
+        """-> (logits [L, vocab], taps [3, L, hidden]); the cache grows by L."""
+        tok = _i32(tokens).reshape(-1)
+        L = tok.size
+        pos = None if positions is None else _i32(positions).reshape(-1)
+        m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+        logits = np.empty((L, self.cfg.vocab_size), np.float32)
+        taps = np.empty((3, L, self.cfg.hidden_size), np.float32)
+        _check(lib().wcref_qwen3_forward(self.h, _p(tok), L, cache.h, _p(pos), _p(m), _p(logits), _p(taps)))
+        return logits, taps
+
+
+def linear(x, W, y=None, accumulate: bool = False) -> np.ndarray:
+    x, W = _f32(x), _f32(W)
+    L = x.size // W.shape[1]
+    y = np.zeros((L, W.shape[0]), np.float32) if y is None else _f32(y).copy()
+    _check(lib().wcref_linear(_p(x), L, W.shape[1], _p(W), W.shape[0], _p(y), int(accumulate)))
+    return y
+
+
+def silu_mul(gate, up) -> np.ndarray:
+    g = _f32(gate).copy()
+    _check(lib().wcref_silu_mul(_p(g), _p(_f32(up)), g.size))
+    return g
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    x = _f32(x)
+    d = x.shape[-1]
+    y = np.empty_like(x)
+    _check(lib().wcref_rmsnorm(_p(x), _p(y), x.size // d, d, _p(_f32(w)), eps))
+    return y
+
+
+def rope(x, positions, base: float) -> np.ndarray:
+    """x [L, heads, D] -> rotated copy."""
+    y = _f32(x).copy()
+    L, heads, D = y.shape
+    _check(lib().wcref_rope(_p(y), L, heads, D, _p(_i32(positions)), base))
+    return y
+
+
+def softmax(x) -> np.ndarray:
+    y = _f32(x).copy()
+    _check(lib().wcref_softmax(_p(y), y.size))
+    return y
+
+
+def attention(q, K, V, mask, scale: float) -> np.ndarray:
+    """q [L, H, D]; K, V [T, Hk, D]; mask [L, T] or None."""
+    q, K, V = _f32(q), _f32(K), _f32(V)
+    L, H, D = q.shape
+    T, Hk, _ = K.shape
+    m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
+    out = np.empty_like(q)
+    _check(lib().wcref_attention(_p(q), L, H, Hk, D, _p(K), _p(V), T, _p(m), _p(out), scale))
+    return out
 
 
 # ------------------------------------------------------------------ sampling / masks

@@ -24,6 +24,8 @@ from woodcock_amd.config import DrafterConfig, tiny_drafter  # noqa: E402
 from woodcock_amd.synthetic import random_drafter, to_bits  # noqa: E402
 
 OUT = Path(__file__).resolve().parent
+sys.path.insert(0, str(OUT))
+import detgen  # noqa: E402
 
 
 def mid_drafter() -> DrafterConfig:
@@ -166,16 +168,73 @@ def verify_case() -> None:
     np.savez_compressed(OUT / "verify.npz", **arrays)
 
 
+def ops_case() -> None:
+    """The backend operations ops::rmsnorm / linear / rope / silu_mul / softmax /
+    attention (include/woodcock/ops.h:9-24; src/backends/cpu_ops.cpp:45-115) on
+    the deterministic inputs of detgen.ops_inputs; the fixture holds the outputs."""
+    x = detgen.ops_inputs()
+    a: dict[str, np.ndarray] = {}
+    for c in range(len(detgen.RMS)):
+        a[f"rms{c}.y"] = refcpp.rmsnorm(x[f"rms{c}.x"], x[f"rms{c}.w"], float(x[f"rms{c}.eps"]))
+    for c in range(len(detgen.LIN)):
+        a[f"lin{c}.y"] = refcpp.linear(x[f"lin{c}.x"], x[f"lin{c}.W"])
+        a[f"lin{c}.y_acc"] = refcpp.linear(x[f"lin{c}.x"], x[f"lin{c}.W"], x[f"lin{c}.y0"], accumulate=True)
+    for c in range(len(detgen.ROPE)):
+        a[f"rope{c}.y"] = refcpp.rope(x[f"rope{c}.x"], x[f"rope{c}.pos"], float(x[f"rope{c}.base"]))
+    a["silu.y"] = refcpp.silu_mul(x["silu.gate"], x["silu.up"])
+    for c in range(len(detgen.SOFTMAX_N)):
+        a[f"sm{c}.y"] = refcpp.softmax(x[f"sm{c}.x"])
+    for c in range(len(detgen.ATT)):
+        a[f"att{c}.out"] = refcpp.attention(x[f"att{c}.q"], x[f"att{c}.K"], x[f"att{c}.V"], x.get(f"att{c}.mask"),
+                                            float(x[f"att{c}.scale"]))
+    np.savez_compressed(OUT / "ops.npz", **a)
+
+
+def qwen3_case() -> None:
+    """Qwen3::forward (src/core/qwen3.cpp:75-114) of the small two-layer target of
+    detgen (hidden 256, 2 x 128 heads, one kv head, SwiGLU 256 -- a shape the
+    GPU verify-width layer also runs): a causal prefill of 9 tokens, then a
+    6-node tree block with explicit positions and the tree mask.  The fixture
+    holds the logits, the feature taps (layers 0, 1, 1) and the KV cache rows."""
+    from woodcock_amd.target import TargetConfig
+
+    cfg = TargetConfig(**detgen.QWEN3)
+    model = refcpp.RefQwen3(cfg, detgen.qwen3_weights(), detgen.QWEN3_TAPS)
+    x = detgen.qwen3_inputs()
+    cache = model.make_cache()
+    a: dict[str, np.ndarray] = {}
+    a["prefill.logits"], a["prefill.taps"] = model.forward(x["prefill.tokens"], cache)
+    mask = refcpp.tree_mask(x["tree.tokens"], x["tree.parents"], x["tree.depth"], 9).astype(np.uint8)
+    a["tree.mask"] = mask
+    a["tree.logits"], a["tree.taps"] = model.forward(x["tree.tokens"], cache, positions=x["tree.positions"],
+                                                     mask=mask)
+    for li in range(cfg.num_layers):
+        a[f"cache.k{li}"] = cache.rows(li, 0)
+        a[f"cache.v{li}"] = cache.rows(li, 1)
+    model.close()
+    np.savez_compressed(OUT / "qwen3_small.npz", **a)
+
+
+CASES = {
+    "drafter": lambda: [drafter_case("tiny", tiny_drafter(), seed=1, ctx=9, tree=True),
+                        drafter_case("tiny_prenorm", tiny_drafter(post_norm=False), seed=2, ctx=7, tree=False),
+                        drafter_case("tiny_window", tiny_drafter(window=5), seed=3, ctx=9, tree=False),
+                        drafter_case("tiny_2layer", tiny_drafter(num_layers=2), seed=4, ctx=6, tree=True),
+                        drafter_case("mid", mid_drafter(), seed=5, ctx=40, tree=True)],
+    "kv": kv_case,
+    "verify": verify_case,
+    "ops": ops_case,
+    "qwen3": qwen3_case,
+}
+
+
 def main():
+    """python tests/golden/make_golden.py [case ...]   (default: every case)"""
     if not refcpp.available():
         sys.exit("oracle/_ref/libwcref.so is missing: run `make -C oracle` where the reference exists")
-    drafter_case("tiny", tiny_drafter(), seed=1, ctx=9, tree=True)
-    drafter_case("tiny_prenorm", tiny_drafter(post_norm=False), seed=2, ctx=7, tree=False)
-    drafter_case("tiny_window", tiny_drafter(window=5), seed=3, ctx=9, tree=False)
-    drafter_case("tiny_2layer", tiny_drafter(num_layers=2), seed=4, ctx=6, tree=True)
-    drafter_case("mid", mid_drafter(), seed=5, ctx=40, tree=True)
-    kv_case()
-    verify_case()
+    names = sys.argv[1:] or list(CASES)
+    for n in names:
+        CASES[n]()
     for f in sorted(OUT.glob("*.npz")):
         print(f.name, f.stat().st_size)
 

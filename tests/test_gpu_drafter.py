@@ -4,6 +4,8 @@ Tolerances (north_star): fp32 activations + fp32 KV within 1e-5 relative of the
 reference's fp32 C++ drafter; bf16 KV within 1e-2 relative.  "Relative" is
 norm-wise: max |got - ref| <= tol * max |ref| per output tensor.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -167,7 +169,7 @@ def test_update_rows_with_device_count(cuda):
         g = torch.full((5, 2048), float("nan"), device=cuda)
         tp = [torch.from_numpy(t).to(cuda) for t in taps]
         arr = (C.c_void_p * 3)(*[t.data_ptr() for t in tp])
-        _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr, _lib.WC_F32, 2048, None, 5,
+        _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr, _lib.WC_F32, 2048, None, 0, 5,
                   ptr(nrow[0:1]), ptr(g), 2048, ptr(d.ws), stream_ptr())
         hid = torch.full((5, 2048), float("nan"), device=cuda)
         out = torch.full_like(hid, float("nan"))
@@ -228,7 +230,7 @@ def test_qwen3_4b_step_and_update_match_oracle(cuda):
     g = torch.empty(5, dm, device=cuda)
     tp = [torch.from_numpy(t).to(cuda) for t in taps]
     arr = (C.c_void_p * 3)(*[t.data_ptr() for t in tp])
-    _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr, _lib.WC_F32, dm, None, 5, ptr(nrow[0:1]),
+    _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr, _lib.WC_F32, dm, None, 0, 5, ptr(nrow[0:1]),
               ptr(g), dm, ptr(d.ws), stream_ptr())
     hid = torch.empty(5, dm, device=cuda)
     kp = (C.c_void_p * 1)(cache[0].keys.data_ptr())
@@ -241,6 +243,47 @@ def test_qwen3_4b_step_and_update_match_oracle(cuda):
     ohid, _ = od.forward(toks, og, oc)
     assert _rel(g.cpu().numpy(), og) <= 1e-5
     assert _rel(hid.cpu().numpy(), ohid) <= tol
+
+
+@pytest.mark.parametrize("tap_dtype", [torch.float32, torch.bfloat16])
+def test_fuse_gathers_kept_tree_rows(cuda, tap_dtype):
+    """Drafter.fuse at the accepted path of a tree (spec.py:327-328): the taps of
+    a 60-row verify block gathered at keep = [0, 3, 17, 41] on the device
+    (wc_drafter_fuse with tap_rows_dev and a device row count), with stale
+    entries past n_keep -- one of them far outside the taps, as an earlier,
+    larger tree could leave -- which must be neither read out of bounds nor
+    written: rows past n_keep stay untouched."""
+    from woodcock_amd import _lib
+    from woodcock_amd.config import qwen3_1p7b_drafter
+    from woodcock_amd.runtime import ptr, stream_ptr
+
+    cfg = qwen3_1p7b_drafter()
+    dm = cfg.hidden_size
+    d, od, _, _, _ = _oracle_step_setup(cfg, 12, cuda, 16, torch.bfloat16)
+    rng = np.random.default_rng(12)
+    tp = [torch.from_numpy(rng.standard_normal((60, dm)).astype(np.float32)).to(cuda).to(tap_dtype)
+          for _ in range(3)]
+    taps = [t.float().cpu().numpy() for t in tp]
+    keep = [0, 3, 17, 41]
+    rows = 7
+    kdev = torch.tensor(keep + [59, 1 << 20, -5], dtype=torch.int32, device=cuda)
+    nk = torch.tensor([len(keep)], dtype=torch.int32, device=cuda)
+    g = torch.full((rows, dm), float("nan"), device=cuda)
+    arr = (C.c_void_p * 3)(*[t.data_ptr() for t in tp])
+    _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr,
+              _lib.WC_F32 if tap_dtype == torch.float32 else _lib.WC_BF16, dm, ptr(kdev), 60, rows, ptr(nk), ptr(g),
+              dm, ptr(d.ws), stream_ptr())
+    og = od.fuse([t[keep] for t in taps])
+    got = g.cpu().numpy()
+    assert _rel(got[:len(keep)], og) <= 1e-5
+    assert np.isnan(got[len(keep):]).all()
+    # the same gather with every row live equals the host-side gather
+    nk.fill_(rows)
+    kdev[len(keep):] = torch.tensor([50, 51, 59], dtype=torch.int32, device=cuda)
+    _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), arr,
+              _lib.WC_F32 if tap_dtype == torch.float32 else _lib.WC_BF16, dm, ptr(kdev), 60, rows, ptr(nk), ptr(g),
+              dm, ptr(d.ws), stream_ptr())
+    assert _rel(g.cpu().numpy(), od.fuse([t[keep + [50, 51, 59]] for t in taps])) <= 1e-5
 
 
 def test_restricted_head_equals_gathered_full_head(cuda):

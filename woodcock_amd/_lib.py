@@ -91,13 +91,14 @@ _SIGS = {
     "wc_last_error": ([], C.c_char_p),
     "wc_workspace_bytes": ([], C.c_size_t),
     "wc_workspace_init": ([P, C.c_size_t, P], C.c_int),
+    "wc_set_spin_limit": ([C.c_int], C.c_int),
     "wc_argmax_rows": ([P, C.c_int, C.c_int, I64, P, P, P], C.c_int),
     "wc_verify_chain_greedy": ([P, C.c_int, C.c_int, I64, P, P, P, P], C.c_int),
     "wc_verify_tree_greedy": ([P, C.c_int, C.c_int, I64, P, P, P, P, P], C.c_int),
     "wc_kv_compact": ([P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, C.c_int, P, P, P], C.c_int),
     "wc_rope_table": ([P, P, C.c_int, C.c_int, C.c_float], C.c_int),
     "wc_drafter_workspace_bytes": ([P], C.c_size_t),
-    "wc_drafter_fuse": ([P, P, P, C.c_int, I64, P, C.c_int, P, P, I64, P, P], C.c_int),
+    "wc_drafter_fuse": ([P, P, P, C.c_int, I64, P, C.c_int, C.c_int, P, P, I64, P, P], C.c_int),
     "wc_drafter_forward": ([P, P, P, P, I64, P, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int, P, C.c_int, P, P, I64,
                             P, P, P, P, P], C.c_int),
     "wc_draft_head": ([P, P, P, I64, P, C.c_int, C.c_int, P, I64, P, P, P, P, P], C.c_int),
@@ -120,6 +121,14 @@ _SIGS = {
     "wc_target_head": ([P, P, P, P, C.c_int, C.c_int, P, I64, C.c_int, P, P], C.c_int),
     "wc_target_layer": ([P, P, P, P, C.c_int, P, C.c_int, P, P, I64, P, P, C.c_int, C.c_int, P, P, C.c_int, P, P],
                         C.c_int),
+    "wc_rmsnorm": ([P, P, C.c_int, C.c_int, P, C.c_int, C.c_float, P], C.c_int),
+    "wc_linear": ([P, C.c_int, C.c_int, P, C.c_int, C.c_int, P, C.c_int, P], C.c_int),
+    "wc_rope": ([P, C.c_int, C.c_int, C.c_int, P, C.c_float, P, P, C.c_int, P], C.c_int),
+    "wc_silu_mul": ([P, P, I64, P], C.c_int),
+    "wc_attention": ([P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, C.c_int, P, P, C.c_float, P], C.c_int),
+    "wc_softmax": ([P, C.c_int, C.c_int, P], C.c_int),
+    "wc_kv_append": ([P, P, C.c_int, C.c_int, P, P, C.c_int, P, P, P], C.c_int),
+    "wc_kv_set_offset": ([P, C.c_int, P], C.c_int),
 }
 
 _lib = None

@@ -487,8 +487,8 @@ size_t wc_drafter_workspace_bytes(const wc_drafter_dims* dims) {
 }
 
 int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps, int tap_dtype,
-                    int64_t tap_ld, const int32_t* tap_rows_dev, int rows, const int32_t* n_rows_dev, float* g_out,
-                    int64_t g_ld, void* workspace, wc_stream_t stream) {
+                    int64_t tap_ld, const int32_t* tap_rows_dev, int tap_rows, int rows, const int32_t* n_rows_dev,
+                    float* g_out, int64_t g_ld, void* workspace, wc_stream_t stream) {
   if (int rc = check_dims(dims)) return rc;
   WC_REQUIRE(w && taps && g_out, "wc_drafter_fuse: NULL argument");
   WC_REQUIRE(w->fc && al16(w->fc), "wc_drafter_fuse: fc weight missing or not 16-byte aligned");
@@ -496,6 +496,8 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
   WC_REQUIRE(tap_ld >= dims->target_hidden && g_ld >= dims->hidden, "wc_drafter_fuse: bad row stride");
   WC_REQUIRE(tap_ld % 8 == 0 && g_ld % 4 == 0, "wc_drafter_fuse: row strides must be multiples of 8 (taps) / 4");
   WC_REQUIRE(rows >= 1, "wc_drafter_fuse: rows must be positive");
+  WC_REQUIRE(tap_rows_dev == nullptr || tap_rows >= 1,
+             "wc_drafter_fuse: gathering tap rows needs the taps' row count (tap_rows >= 1)");
   WC_REQUIRE(n_rows_dev == nullptr || rows <= WC_MAX_STEP_ROWS,
              "wc_drafter_fuse: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
   auto s = reinterpret_cast<hipStream_t>(stream);
@@ -510,6 +512,9 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
       g.in[f].ld = tap_ld;
       g.in[f].dtype = tap_dtype;
       g.in[f].row_idx = tap_rows_dev ? tap_rows_dev + t0 : nullptr;
+      // gathered rows are clamped into the taps: entries past the device row
+      // count may be stale (an earlier round's longer keep list)
+      g.in[f].max_row = tap_rows_dev ? tap_rows : 0;
       g.in[f].gain = u16(w->feature_norm[f]);  // NULL: feature_norm off (drafter.py:151-152)
       g.in[f].K = Dt;
       g.ldw[f] = static_cast<int64_t>(nf) * Dt;

@@ -70,6 +70,7 @@ struct StochArgs {
   float* dec_ms;        // the chosen row's softmax max and sum
   unsigned int* bad_flag;  // invalid d2t / drafts seen by the statistics launch (reset by its last block)
   unsigned int* stats_counter;
+  unsigned int spin_limit;  // polls before a waiting block of the one-launch kernel gives up
 };
 
 // Block-wide fp64 sum over kStThreads threads (DPP wave sums, then the wave
@@ -660,11 +661,21 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_stats(StochArgs a) {
 // block; the block of each chunk that holds the chosen row then sums the
 // residual / target mass of its chunk into its mailbox, the others end.  Once every chunk's masses are in, each chunk block
 // locates the chunk of the draw; that chunk's block finds the entry in the
-// values it holds, writes the verdict, clears the other mailbox set for the
-// next call and advances the call counter.  Calls alternate between the two
-// sets by the parity of the counter, so a set is always cleared by the call
-// before the one that uses it (a zero-initialised workspace starts both
-// clear).  Every probability, sum and scan is formed as the two-launch path
+// values it holds and writes the verdict; the check blocks have cleared the
+// other mailbox set for the next call.  Calls alternate between the two sets by
+// the parity of the call counter, so a set is always cleared by the call before
+// the one that uses it (a zero-initialised workspace starts both clear).  The
+// counter moves only once every block of the call has read it: each chunk block
+// posts an arrival word derived from the value it read, and the finishing block
+// waits for all of them before it advances the counter (the other blocks' words
+// are already in by then), so no block of a call can poll the next call's set,
+// whatever order the blocks are dispatched in.
+// Every wait is bounded (spin_limit polls).  A block that gives up sets the
+// sticky failure flag of the control word and WC_E_HIP in the verdict; every
+// later call then ends at once with WC_E_HIP, without touching the mailboxes,
+// until the host zero-fills the workspace again (wc_workspace_init) -- so words
+// a failed call left behind are never read as another call's.
+// Every probability, sum and scan is formed as the two-launch path
 // (k_stoch_stats + k_stoch_sample<true>) forms it.
 struct MailSet {
   // kMailRep copies of every word, each written by the producer; a polling
@@ -675,10 +686,23 @@ struct MailSet {
   // [0, 2K): Q_i, q_i at the draft (fp64); [2K, 3K + 1): uniforms 0..K;
   // [3K + 1, 3K + 1 + checks): 1 + (a check block found an invalid input)
   unsigned long long other[kMailRep][kMailOther];
+  unsigned long long arrive[kMailArrive];  // chunk block cb: the complement of the call value it read
 };
 static_assert(sizeof(MailSet) == 8 * kMailSetWords, "mailbox layout");
 static_assert(kGridBarOff % 8 == 0, "mailbox alignment");
-constexpr unsigned int kSpinLimit = 1u << 22;  // polls before a call gives up (WC_E_HIP in the verdict)
+constexpr unsigned int kSpinLimit = 1u << 22;  // default polls before a wait gives up (WC_E_HIP in the verdict)
+static std::atomic<unsigned int> g_spin_limit{kSpinLimit};
+
+// A wait that gave up: the sticky failure flag (high half of the control word)
+// and WC_E_HIP in the verdict.  The flag is stored before the status, so a
+// verdict that reads WC_E_HIP always leaves a flagged workspace behind.
+__device__ __forceinline__ void stoch_give_up(const StochArgs& a, unsigned long long* ctl) {
+  if (threadIdx.x == 0) {
+    atomic_store_u32(reinterpret_cast<unsigned int*>(ctl) + 1, 1u);
+    __builtin_amdgcn_s_waitcnt(0);
+    a.verdict->status = WC_E_HIP;
+  }
+}
 
 // every copy of a word: w points at copy 0, copies lie `stride` words apart
 __device__ __forceinline__ void mail_put(unsigned long long* w, size_t stride, unsigned long long v) {
@@ -697,6 +721,7 @@ constexpr int kFusedRows = kMailRows;           // K + 1 rows whose chunk each c
 constexpr int kFusedCpl = kMailChunks / kWave;  // chunks per lane in the merge: nch <= 256
 constexpr int kQPre = 1024;    // head rows of a chunk staged in LDS before the decision
 constexpr int kGroupRows = 3;  // rows of a chunk one chunk block holds: ceil(rows / 3) blocks per chunk
+static_assert(kMailArrive >= (kFusedRows + kGroupRows - 1) / kGroupRows * kMailChunks, "arrival words");
 
 // One step of a block-wide search for the first index r in [lo, hi] with
 // d2t[r] >= x (d2t ascending).  Width <= 256: thread t probes lo + t; else the
@@ -726,8 +751,9 @@ __device__ __forceinline__ void probe_apply(Probe& p, int x, int* s_cnt) {
 }
 
 // logit / T; with P2 (T a power of two) as logit * (1 / T), the same float:
-// both round the same exact quotient once (__fmul_rn: never contracted into a
-// following add, as the quotient is not)
+// both round the same exact quotient once.  The product by a power of two is
+// exact (normal range), so where the compiler contracts it into a following
+// subtraction the fused result equals the two rounded steps.
 template <bool P2>
 __device__ __forceinline__ float lscale(const StochArgs& a, float x) {
   return P2 ? __fmul_rn(x, a.inv_t) : x / a.temperature;
@@ -735,7 +761,7 @@ __device__ __forceinline__ float lscale(const StochArgs& a, float x) {
 
 template <bool P2>
 __global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch, int nchecks, int vec,
-                                                           MailSet* sets, unsigned int* calls) {
+                                                           MailSet* sets, unsigned long long* ctl) {
   constexpr int kNw = kStThreads / kWave;
   __shared__ float s_m[kNw], s_s[kNw];
   __shared__ float s_M[kFusedRows], s_S[kFusedRows], s_lgx[kFusedRows];
@@ -750,8 +776,14 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch
   const int b = blockIdx.x, K = a.rows - 1, rows = a.rows;
   const int nstat = rows * nch, ngroups = (rows + kGroupRows - 1) / kGroupRows, nchunkb = ngroups * nch;
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  // the call counter moves only at the end of the call (after every block has read it)
-  const unsigned int call = __hip_atomic_load(calls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // control word: the call counter (moves only at the end of the call, after
+  // every block has read it) and the sticky failure flag
+  const unsigned long long cw = atomic_load_u64(ctl);
+  const unsigned int call = static_cast<unsigned int>(cw);
+  if (cw >> 32) {  // an earlier call gave up: the mailboxes may hold its words
+    if (b == 0 && threadIdx.x == 0) a.verdict->status = WC_E_HIP;
+    return;
+  }
   MailSet* mb = sets + (call & 1u);
   const int rep = blockIdx.x % kMailRep;  // the mailbox copy this block polls
 
@@ -868,6 +900,9 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch
   // drafts and this chunk of the block's rows, all in flight together.
   const int cb = b - nstat, c = cb % nch, rlo = (cb / nch) * kGroupRows, rhi = min(rlo + kGroupRows, rows);
   const int x0 = c * kVocabChunk;
+  // arrival: its value depends on the counter value read, so it cannot be
+  // posted before that read completed
+  if (threadIdx.x == 0) atomic_store_u64(&mb->arrive[cb], ~static_cast<unsigned long long>(call));
   const bool search = K > 0 && a.d2t != nullptr;
   Probe pr[2] = {{0, a.head_rows, 1, 0, 0}, {0, a.head_rows, 1, 0, 0}};
   if (search) {
@@ -969,8 +1004,8 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch
         if (wave + h * kNw < rows && lane + u * kWave < nch && pw[h][u] == 0ull) ok = 0;
     if (threadIdx.x < n_other && ow == 0ull) ok = 0;
     if (__syncthreads_and(ok)) break;
-    if (it == kSpinLimit) {
-      if (threadIdx.x == 0) a.verdict->status = WC_E_HIP;
+    if (it >= a.spin_limit) {
+      stoch_give_up(a, ctl);
       return;
     }
     __builtin_amdgcn_s_sleep(2);
@@ -1099,8 +1134,8 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch
       cp[0] = mail_f64(wp);
     }
     if (__syncthreads_and(ok)) break;
-    if (it == kSpinLimit) {
-      if (threadIdx.x == 0) a.verdict->status = WC_E_HIP;
+    if (it >= a.spin_limit) {
+      stoch_give_up(a, ctl);
       return;
     }
     __builtin_amdgcn_s_sleep(2);
@@ -1175,8 +1210,20 @@ __global__ __launch_bounds__(kStThreads) void k_stoch_fused(StochArgs a, int nch
     a.verdict->tokens[threadIdx.x] = dtok;
     a.verdict->keep[threadIdx.x] = threadIdx.x;
   }
-  // every block of this call has read the counter (its words are in): it moves
-  if (threadIdx.x == 0) atomic_store_u32(calls, call + 1u);
+  // the counter moves once every block has read it: the statistics, mass and
+  // check blocks' words are in, and every chunk block's arrival
+  for (unsigned int it = 0;; ++it) {
+    int ok = 1;
+    for (int k = threadIdx.x; k < nchunkb; k += kStThreads)
+      if (atomic_load_u64(&mb->arrive[k]) == 0ull) ok = 0;
+    if (__syncthreads_and(ok)) break;
+    if (it >= a.spin_limit) {
+      stoch_give_up(a, ctl);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (threadIdx.x == 0) atomic_store_u32(reinterpret_cast<unsigned int*>(ctl), call + 1u);
 }
 
 // ------------------------------------------------------------------ stochastic tree
@@ -1758,15 +1805,16 @@ int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, 
   // other blocks never wait, so they run whenever a slot frees
   if (rows <= kFusedRows && nch <= kMailChunks && groups * nch < hold) {
     MailSet* sets = reinterpret_cast<MailSet*>(ws + kGridBarOff);
-    unsigned int* calls = reinterpret_cast<unsigned int*>(ws + kGridBarOff + 2 * sizeof(MailSet));
+    auto* ctl = reinterpret_cast<unsigned long long*>(ws + kGridBarOff + 2 * sizeof(MailSet));
+    a.spin_limit = g_spin_limit.load(std::memory_order_relaxed);
     const int vec = aligned(logits, 16) && ld % 4 == 0;
     int e2 = 0;
     const bool p2 = std::frexp(a.temperature, &e2) == 0.5f;  // T = 2^(e2 - 1)
     if (p2) {
       a.inv_t = std::ldexp(1.0f, 1 - e2);
-      hipLaunchKernelGGL(k_stoch_fused<true>, dim3(grid), dim3(kStThreads), 0, s, a, nch, ncheck, vec, sets, calls);
+      hipLaunchKernelGGL(k_stoch_fused<true>, dim3(grid), dim3(kStThreads), 0, s, a, nch, ncheck, vec, sets, ctl);
     } else {
-      hipLaunchKernelGGL(k_stoch_fused<false>, dim3(grid), dim3(kStThreads), 0, s, a, nch, ncheck, vec, sets, calls);
+      hipLaunchKernelGGL(k_stoch_fused<false>, dim3(grid), dim3(kStThreads), 0, s, a, nch, ncheck, vec, sets, ctl);
     }
     WC_LAUNCHED();
     return WC_OK;
@@ -1776,6 +1824,11 @@ int wc_verify_chain_stochastic_logits(const float* logits, int rows, int vocab, 
   WC_LAUNCHED();
   hipLaunchKernelGGL((k_stoch_sample<true>), dim3(nch), dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_set_spin_limit(int polls) {
+  wc::g_spin_limit.store(polls < 0 ? wc::kSpinLimit : static_cast<unsigned int>(polls), std::memory_order_relaxed);
   return WC_OK;
 }
 

@@ -309,10 +309,12 @@ constexpr size_t kChunkRowsOff = kTreeStateOff + kTreeStateBytes;
 constexpr size_t kChunkRowsBytes = 4 * (kMaxVocabChunks + 4);
 constexpr size_t kStochDecOff = kChunkRowsOff + kChunkRowsBytes;
 constexpr size_t kStochDecBytes = 64;
-// the one-launch stochastic chain's two mailbox sets (one per call parity) and
-// its call counter
+// the one-launch stochastic chain's two mailbox sets (one per call parity), then
+// its control word (call counter | sticky failure flag << 32); each set ends with
+// one arrival word per chunk block (at most 3 row groups per chunk)
 constexpr int kMailRows = 8, kMailChunks = 256, kMailOther = 64, kMailRep = 4;
-constexpr size_t kMailSetWords = kMailRep * (kMailRows * kMailChunks + 2 * kMailChunks + kMailOther);
+constexpr int kMailArrive = 3 * kMailChunks;
+constexpr size_t kMailSetWords = kMailRep * (kMailRows * kMailChunks + 2 * kMailChunks + kMailOther) + kMailArrive;
 constexpr size_t kGridBarOff = kStochDecOff + kStochDecBytes;
 constexpr size_t kGridBarBytes = 2 * 8 * kMailSetWords + 128;
 constexpr size_t kVerifyWorkspace = kGridBarOff + kGridBarBytes;

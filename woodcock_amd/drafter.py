@@ -156,7 +156,7 @@ class Drafter:
         g = torch.empty(L, self.cfg.hidden_size, dtype=torch.float32, device=self.device)
         taps = (C.c_void_p * len(rows))(*[r.data_ptr() for r in rows])
         _lib.call("wc_drafter_fuse", C.byref(self.dims), C.byref(self.wstruct), taps,
-                  _BF16 if dt == torch.bfloat16 else _F32, rows[0].stride(0), None, L, None, ptr(g),
+                  _BF16 if dt == torch.bfloat16 else _F32, rows[0].stride(0), None, 0, L, None, ptr(g),
                   g.stride(0), ptr(self.ws), stream_ptr())
         return g
 

@@ -51,11 +51,40 @@ def new_verdict(device) -> torch.Tensor:
     return torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, device=device)
 
 
-def read_verdict(v: torch.Tensor) -> _lib.Verdict:
+def reset_workspace(ws: torch.Tensor, stream: torch.cuda.Stream | None = None) -> None:
+    """Zero-fill a verify workspace again (after a call reported WC_E_HIP: a
+    bounded wait of the one-launch stochastic kernel gave up and left the
+    workspace flagged; every later call on it fails fast until this runs)."""
+    _lib.call("wc_workspace_init", ptr(ws), ws.numel(), stream_ptr(stream))
+
+
+def reset_workspaces(device: torch.device | None = None) -> None:
+    """reset_workspace for every cached (device, stream) workspace of `device` (None = all)."""
+    idx = None if device is None else (device.index if device.index is not None else torch.cuda.current_device())
+    for (d, s), ws in _workspaces.items():
+        if idx is None or d == idx:
+            _lib.call("wc_workspace_init", ptr(ws), ws.numel(), C.c_void_p(s) if s else None)
+
+
+def check_verdict(out: _lib.Verdict, ws: torch.Tensor | None = None) -> _lib.Verdict:
+    """Status of a verdict read back to the host: WC_E_INVALID -> ValueError (the
+    device saw an invalid input); WC_E_HIP -> the workspace (`ws`, else every
+    cached one) is zero-filled again and RuntimeError is raised."""
+    if out.status == _lib.WC_E_HIP:
+        if ws is None:
+            reset_workspaces()
+        else:
+            reset_workspace(ws)
+        raise _lib.WoodcockHipError("a bounded device-side wait gave up (WC_E_HIP); the verify workspace was "
+                                    "re-initialised and this verification has no result")
+    if out.status != 0:
+        raise ValueError(f"device-side verification rejected its inputs (status {out.status})")
+    return out
+
+
+def read_verdict(v: torch.Tensor, ws: torch.Tensor | None = None) -> _lib.Verdict:
     """The round's host synchronisation: one D2H copy of the verdict."""
     host = v.to("cpu")
     out = _lib.Verdict()
     C.memmove(C.addressof(out), host.numpy().ctypes.data, _lib.VERDICT_BYTES)
-    if out.status != 0:
-        raise ValueError(f"device-side verification rejected its inputs (status {out.status})")
-    return out
+    return check_verdict(out, ws)

@@ -1,20 +1,35 @@
-"""The fused greedy chain round with ONE host synchronisation
-(python/woodcock/spec.py:331-374, _fused_chain_round + _update).
+"""Speculative-decoding rounds with ONE host synchronisation each
+(python/woodcock/spec.py:104-374).
 
-Everything between two host reads stays on the device:
+``ChainRound`` holds the device side of a round and enqueues its launches:
 
     head(RMSNorm(root)) -> d_1                          (final norm + draft head + argmax + d2t)
     for k in 1..K-1: drafter layer(d_k, fb) -> head(RMSNorm(h)) -> d_{k+1}
-    target logits at [x_n, d_1..d_K]                    (supplied by the target; out of scope here)
+    target logits at [x_n, d_1..d_K]                    (the target's verify forward)
     fused target argmax + greedy accept -> verdict      (a, accepted tokens + next, keep)
-    compact the target KV with keep (identity for a chain: offset only)
     update: fuse(taps[keep]) and one drafter pass over the a+1 accepted tokens,
             which appends them to the drafter cache and yields the next root
     copy the verdict to pinned host memory              <- the round's single sync
 
+A chain keeps the verify block's prefix, so the target's KV needs no move: its
+committed length is the device count n that the update advances
+(python/woodcock/target.py:170, compact_cache with keep == range(n)).  A tree
+round (``enqueue_tree_*``) keeps ``[0] + path``: the target KV is gathered along
+the accepted branch (wc_kv_compact) and the taps at the same rows feed the
+update (spec.py:325-328).
+
 Round-varying integers -- the committed count n (drafter base == target
-start), the accepted count, the gathered rows -- are read from device memory,
-so the same kernel sequence (or one captured HIP graph) serves every round.
+start), the accepted count, the kept rows, x_n -- are read from device memory,
+so the same kernel sequence (or one captured HIP graph per chain length)
+serves every round.
+
+``SpeculativeDecoder`` is the round loop of SpeculativeDecoder.generate
+(spec.py:151-212): before each round the policy plans the draft shape
+(``CostAwareChain`` re-chooses the chain length every round), after it the
+policy observes the outcome; greedy chains run the fused single-sync round
+(spec.py:331-364), trees the drafting / verify / compact / update sequence of
+spec.py:187-201 -- also with one host synchronisation, since tree drafting and
+the tree verification stay on the device.
 
 State invariants follow python/woodcock/spec.py:1-15: before a round the
 drafter cache holds real entries 0..n-1 and the root is the drafter's hidden
@@ -25,47 +40,61 @@ pass of the round runs a norm of its own on the critical path.
 from __future__ import annotations
 
 import ctypes as C
-from dataclasses import dataclass
+import time
+from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import _lib
 from .cache import KVCache, compact_cache_dev
 from .drafter import Drafter
-from .runtime import new_verdict, ptr, read_verdict, stream_ptr
+from .policies import Plan, Policy
+from .runtime import check_verdict, new_verdict, ptr, read_verdict, stream_ptr
 
 # state vector slots (device int32)
-S_N, S_ROUND, S_TARGET_OFFSET = 0, 1, 2
+S_N, S_ROUND = 0, 1
 
 
 @dataclass
 class RoundResult:
     n_accepted: int
     tokens: list[int]  # accepted drafts + the target's next token
+    k: int = 0         # drafts verified this round (chain length, or tree nodes besides the root)
+    depth: int = 0     # chain length, or the tree's depth
 
 
 class ChainRound:
-    """Device state and buffers of a greedy chain of length K (<= 15).
+    """Device state and buffers of greedy rounds with chains of up to ``k``
+    drafts (<= 15) and kept blocks of up to ``max_keep`` rows (>= k + 1; a tree
+    round keeps its depth + 1 rows at most).
 
-    target: object with ``logits`` [K+1, V] fp32 and ``taps`` (num_features
-    tensors [K+1, target_hidden]) device tensors at [x_n, d_1..d_K] -- the
-    verify-width target forward, which this module does not implement."""
+    The chain methods take the round's chain length (default ``k``): every
+    buffer is sized for the longest, so rounds of different lengths share the
+    drafter cache, the verdict and the device state."""
 
-    def __init__(self, drafter: Drafter, k: int, capacity: int, target_cache: list[KVCache] | None = None):
+    def __init__(self, drafter: Drafter, k: int, capacity: int, target_cache: list[KVCache] | None = None,
+                 max_keep: int | None = None):
         if not 1 <= k <= _lib.WC_MAX_STEP_ROWS - 1:
             raise ValueError(f"chain length must be in 1..{_lib.WC_MAX_STEP_ROWS - 1}")
+        max_keep = max(k + 1, max_keep or 0)
+        if max_keep > _lib.WC_MAX_STEP_ROWS:
+            raise ValueError(f"at most {_lib.WC_MAX_STEP_ROWS} kept rows per round")
         self.d = drafter
         self.K = k
+        self.max_keep = max_keep
         dev = drafter.device
         dm = drafter.cfg.hidden_size
         self.cache = drafter.make_cache(capacity)
         self.target_cache = target_cache
         self.state = torch.zeros(8, dtype=torch.int32, device=dev)
         self.verdict = new_verdict(dev)
-        self.drafts = torch.zeros(k, dtype=torch.int32, device=dev)
+        # the verify block's tokens [x_n, d_1..d_K]; the drafts are written in place
+        self.seq = torch.zeros(k + 1, dtype=torch.int32, device=dev)
+        self.drafts = self.seq[1:]
         self.step_hid = torch.zeros(max(k - 1, 1), dm, dtype=torch.float32, device=dev)
         self.step_out = torch.zeros_like(self.step_hid)
-        self.upd_hid = torch.zeros(k + 1, dm, dtype=torch.float32, device=dev)
+        self.upd_hid = torch.zeros(max_keep, dm, dtype=torch.float32, device=dev)
         self.upd_out = torch.zeros_like(self.upd_hid)
         self.g = torch.zeros_like(self.upd_hid)
         self.host_verdict = torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, pin_memory=True)
@@ -79,26 +108,43 @@ class ChainRound:
 
     # ------------------------------------------------------------------ state
 
-    def set_root(self, n: int, root_hidden: torch.Tensor) -> None:
-        """Start state: n committed entries in the drafter cache and the root --
-        the drafter's pre-norm hidden state of entry n-1 (its output, the final
-        RMSNorm of it, is formed by the first head launch of the round)."""
+    def set_root(self, n: int, root_hidden: torch.Tensor, x_n: int = 0) -> None:
+        """Start state: n committed entries in the drafter cache, x_n the newest
+        committed token (not yet in either cache) and the root -- the drafter's
+        pre-norm hidden state of entry n-1 (its output, the final RMSNorm of it,
+        is formed by the first head launch of the round)."""
         self.upd_hid[0].copy_(root_hidden.reshape(-1))
         self.verdict.zero_()
         self.verdict[_lib.V_N_KEEP] = 1
+        self.verdict[_lib.V_NEXT] = int(x_n)
+        self.verdict[_lib.V_TOKENS] = int(x_n)
         self.state.zero_()
         self.state[S_N] = n
-        self.state[S_TARGET_OFFSET] = n
         for c in self.cache:
             c.offset = n
 
     def _fb_rows(self, hid: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
         return out if self.d.cfg.post_norm else hid
 
-    # ------------------------------------------------------------------ enqueue
+    def n_dev(self) -> torch.Tensor:
+        """The committed count n on the device: the drafter's base and the target's offset."""
+        return self.state[S_N:S_N + 1]
 
-    def enqueue_draft(self) -> None:
-        """K head launches and K-1 drafter layers from the root; drafts -> self.drafts."""
+    def x_n_dev(self) -> torch.Tensor:
+        """x_n on the device: the last round's next token."""
+        return self.verdict[_lib.V_NEXT:_lib.V_NEXT + 1]
+
+    def _k(self, k: int | None) -> int:
+        k = self.K if k is None else int(k)
+        if not 1 <= k <= self.K:
+            raise ValueError(f"chain length {k} outside 1..{self.K}")
+        return k
+
+    # ------------------------------------------------------------------ chain rounds
+
+    def enqueue_draft(self, k: int | None = None) -> None:
+        """k head launches and k-1 drafter layers from the root; drafts -> self.drafts[:k]."""
+        k = self._k(k)
         d = self.d
         dims, W, ws, s = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws), stream_ptr()
         n_keep = ptr(self.verdict[_lib.V_N_KEEP:_lib.V_N_KEEP + 1])
@@ -109,56 +155,93 @@ class ChainRound:
         _lib.call("wc_draft_head_norm", dims, W, ptr(self.upd_hid), dm, n_keep, -1, ptr(self.upd_out), dm, None, 0,
                   ptr(self.drafts[0:1]), None, None, ws, s)
         root_fb = self._fb_rows(self.upd_hid, self.upd_out)
-        for k in range(1, self.K):
-            if k == 1:
+        for i in range(1, k):
+            if i == 1:
                 feat, frow, fadd = root_fb, n_keep, -1
             else:
-                feat, frow, fadd = self._fb_rows(self.step_hid, self.step_out)[k - 2:k - 1], None, 0
-            # the chain appends at n + k - 1 (contiguous positions, causal, python/woodcock/spec.py:349);
+                feat, frow, fadd = self._fb_rows(self.step_hid, self.step_out)[i - 2:i - 1], None, 0
+            # the chain appends at n + i - 1 (contiguous positions, causal, python/woodcock/spec.py:349);
             # the layer's final RMSNorm is left to the next head (out_out = NULL)
-            _lib.call("wc_drafter_forward", dims, W, ptr(self.drafts[k - 1:k]), ptr(feat), dm, frow, fadd, 1, None,
-                      self._kp, self._vp, self._kvdt, cap, ptr(self.state[S_N:S_N + 1]), k - 1, None, None, 0,
-                      ptr(self.step_hid[k - 1:k]), None, None, ws, s)
-            _lib.call("wc_draft_head_norm", dims, W, ptr(self.step_hid[k - 1:k]), dm, None, 0,
-                      ptr(self.step_out[k - 1:k]), dm, None, 0, ptr(self.drafts[k:k + 1]), None, None, ws, s)
-        # the speculative entries n..n+K-2 are simply overwritten later: the
+            _lib.call("wc_drafter_forward", dims, W, ptr(self.drafts[i - 1:i]), ptr(feat), dm, frow, fadd, 1, None,
+                      self._kp, self._vp, self._kvdt, cap, ptr(self.n_dev()), i - 1, None, None, 0,
+                      ptr(self.step_hid[i - 1:i]), None, None, ws, s)
+            _lib.call("wc_draft_head_norm", dims, W, ptr(self.step_hid[i - 1:i]), dm, None, 0,
+                      ptr(self.step_out[i - 1:i]), dm, None, 0, ptr(self.drafts[i:i + 1]), None, None, ws, s)
+        # the speculative entries n..n+k-2 are simply overwritten later: the
         # drafter's committed count n is never advanced by the chain (spec.py:351-352)
 
+    def enqueue_seq(self) -> None:
+        """x_n (the last verdict's next token) into the verify block's first slot."""
+        self.seq[0:1].copy_(self.x_n_dev())
+
     def enqueue_verify(self, target_logits: torch.Tensor) -> None:
-        """Fused target argmax + greedy acceptance (spec.py:355-361) -> verdict."""
-        _lib.call("wc_verify_chain_greedy", ptr(target_logits), target_logits.shape[0], target_logits.shape[1],
+        """Fused target argmax + greedy acceptance (spec.py:355-361) -> verdict;
+        the chain length is the logits' row count - 1."""
+        rows = target_logits.shape[0]
+        self._k(rows - 1)
+        _lib.call("wc_verify_chain_greedy", ptr(target_logits), rows, target_logits.shape[1],
                   target_logits.stride(0), ptr(self.drafts), ptr(self.verdict), ptr(self.vws), stream_ptr())
 
-    def enqueue_commit(self, taps: list[torch.Tensor]) -> None:
-        """Compaction of the target KV (spec.py:362) and the drafter update over
-        the a+1 accepted tokens (spec.py:363-374), all keyed off the verdict."""
+    def _enqueue_update(self, taps: list[torch.Tensor], rows: int) -> None:
+        """fuse(taps at keep) + one drafter pass over the n_keep accepted tokens
+        (spec.py:366-374), appended at n; n advances by n_keep (device)."""
         d = self.d
         V = _lib
         keep = self.verdict[V.V_KEEP:V.V_KEEP + V.WC_MAX_NODES + 1]
         n_keep = self.verdict[V.V_N_KEEP:V.V_N_KEEP + 1]
-        if self.target_cache is not None:
-            compact_cache_dev(self.target_cache, self.state[S_N:S_N + 1], keep, n_keep, self.K + 1,
-                              self.state[S_TARGET_OFFSET:S_TARGET_OFFSET + 1], self.verdict[V.V_STATUS:V.V_STATUS + 1])
         dims, W, ws, s = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws), stream_ptr()
         dm = d.cfg.hidden_size
         tp = (C.c_void_p * len(taps))(*[t.data_ptr() for t in taps])
         tdt = V.WC_BF16 if taps[0].dtype == torch.bfloat16 else V.WC_F32
-        V.call("wc_drafter_fuse", dims, W, tp, tdt, taps[0].stride(0), ptr(keep), self.K + 1, ptr(n_keep), ptr(self.g),
-               dm, ws, s)
+        V.call("wc_drafter_fuse", dims, W, tp, tdt, taps[0].stride(0), ptr(keep), taps[0].shape[0], rows,
+               ptr(n_keep), ptr(self.g), dm, ws, s)
         # appends the accepted entries at n and advances n in place (last kernel of the pass)
-        V.call("wc_drafter_forward", dims, W, ptr(self.verdict[V.V_TOKENS:V.V_TOKENS + self.K + 1]), ptr(self.g), dm,
-               None, 0, self.K + 1, ptr(n_keep), self._kp, self._vp, self._kvdt, self.cache[0].capacity,
-               ptr(self.state[S_N:S_N + 1]), 0, None, None, 0, ptr(self.upd_hid), None,
-               ptr(self.state[S_N:S_N + 1]), ws, s)
+        V.call("wc_drafter_forward", dims, W, ptr(self.verdict[V.V_TOKENS:V.V_TOKENS + rows]), ptr(self.g), dm,
+               None, 0, rows, ptr(n_keep), self._kp, self._vp, self._kvdt, self.cache[0].capacity,
+               ptr(self.n_dev()), 0, None, None, 0, ptr(self.upd_hid), None, ptr(self.n_dev()), ws, s)
+
+    def enqueue_commit(self, taps: list[torch.Tensor], k: int | None = None) -> None:
+        """The chain's commit: the drafter update over the a+1 accepted tokens
+        (spec.py:362-374), keyed off the verdict.  The target KV keeps the
+        verify block's prefix in place, so nothing moves (target.py:170)."""
+        self._enqueue_update(taps, self._k(k) + 1)
 
     def enqueue_readback(self) -> None:
         self.host_verdict.copy_(self.verdict, non_blocking=True)
 
-    def enqueue_round(self, target) -> None:
-        self.enqueue_draft()
-        self.enqueue_verify(target.logits)
-        self.enqueue_commit(target.taps)
+    def enqueue_round(self, target, k: int | None = None) -> None:
+        """A chain round against a target exposing device ``logits`` / ``taps``
+        at [x_n, d_1..d_K] (a synthetic stand-in whose rows are already in place)."""
+        k = self._k(k)
+        self.enqueue_draft(k)
+        self.enqueue_verify(target.logits[:k + 1])
+        self.enqueue_commit([t[:k + 1] for t in target.taps], k)
         self.enqueue_readback()
+
+    # ------------------------------------------------------------------ tree rounds
+
+    def enqueue_tree_verify(self, logits: torch.Tensor, tokens: torch.Tensor, parents: torch.Tensor) -> None:
+        """Target argmax + greedy tree walk (sampling.py:131-140; spec.py:318-319) -> verdict."""
+        rows = logits.shape[0]
+        _lib.call("wc_verify_tree_greedy", ptr(logits), rows, logits.shape[1], logits.stride(0), ptr(tokens),
+                  ptr(parents), ptr(self.verdict), ptr(self.vws), stream_ptr())
+
+    def enqueue_tree_commit(self, taps: list[torch.Tensor], rows: int, max_depth: int) -> None:
+        """Compaction of the target KV along the accepted branch, keep = [0] + path
+        (spec.py:325-326; target.py:159-175), then the update from the taps at
+        the kept rows (spec.py:327-328,366-374).  rows: the verify block's rows;
+        max_depth: the tree's depth (n_keep <= max_depth + 1)."""
+        V = _lib
+        if max_depth + 1 > self.max_keep:
+            raise ValueError(f"a tree of depth {max_depth} keeps up to {max_depth + 1} rows; "
+                             f"this round state holds {self.max_keep}")
+        if self.target_cache is not None:
+            keep = self.verdict[V.V_KEEP:V.V_KEEP + V.WC_MAX_NODES + 1]
+            n_keep = self.verdict[V.V_N_KEEP:V.V_N_KEEP + 1]
+            # start = n, read before the update advances it; the update writes the new n
+            compact_cache_dev(self.target_cache, self.n_dev(), keep, n_keep, rows, None,
+                              self.verdict[V.V_STATUS:V.V_STATUS + 1])
+        self._enqueue_update(taps, max_depth + 1)
 
     # ------------------------------------------------------------------ host side
 
@@ -166,22 +249,256 @@ class ChainRound:
         """The round's single host synchronisation: wait for the verdict copy."""
         torch.cuda.current_stream().synchronize()
         self.syncs += 1
-        v = _lib.Verdict.from_buffer_copy(self.host_verdict.numpy().tobytes())
-        if v.status != 0:
-            raise ValueError(f"device-side verification rejected its inputs (status {v.status})")
+        v = check_verdict(_lib.Verdict.from_buffer_copy(self.host_verdict.numpy().tobytes()), self.vws)
         a = int(v.n_accepted)
         for c in self.cache:
             c.offset += a + 1
+        if self.target_cache is not None:
+            for c in self.target_cache:
+                c.offset = self.cache[0].offset
         return RoundResult(a, [int(t) for t in v.tokens[: a + 1]])
 
-    def run(self, target) -> RoundResult:
-        self.enqueue_round(target)
+    def run(self, target, k: int | None = None) -> RoundResult:
+        self.enqueue_round(target, k)
         return self.finish()
 
     def committed(self) -> int:
         """Device committed count (reads device memory: a sync, for tests only)."""
         return int(self.state[S_N].item())
 
+    def last_keep(self) -> list[int]:
+        """The kept rows of the last round (its host verdict copy)."""
+        v = _lib.Verdict.from_buffer_copy(self.host_verdict.numpy().tobytes())
+        return [int(x) for x in v.keep[: v.n_keep]]
+
 
 def verdict_of(t: torch.Tensor):
     return read_verdict(t)
+
+
+# ---------------------------------------------------------------------- targets
+
+class TargetRunner:
+    """The verify forward of a ``target.TargetModel`` over its own KV cache, as
+    the decoder calls it: tokens [rows] (device) at cache offset *offset_dev,
+    optional positions and mask -> (logits [rows, V] fp32, taps [rows, hidden]
+    fp32).  Output buffers are allocated once (graph capture reuses them)."""
+
+    def __init__(self, model, cache: list[KVCache]):
+        self.model = model
+        self.cache = cache
+        self.vocab_size = model.cfg.vocab_size
+        rows = model.max_rows
+        dev = model.device
+        self.logits = torch.empty(rows, model.cfg.vocab_size, dtype=torch.float32, device=dev)
+        self.taps = [torch.empty(rows, model.cfg.hidden_size, dtype=torch.float32, device=dev)
+                     for _ in model.feature_layers]
+
+    def prepare(self, rows: int) -> None:
+        pass
+
+    def verify_forward(self, tokens: torch.Tensor, rows: int, offset_dev: torch.Tensor,
+                       positions: torch.Tensor | None = None, mask: torch.Tensor | None = None):
+        logits, taps = self.model(tokens[:rows], self.cache, offset_dev, positions, mask, logits=self.logits[:rows],
+                                  taps=self.taps)
+        return logits, [t[:rows] for t in taps]
+
+
+# ---------------------------------------------------------------------- decoder
+
+@dataclass
+class GenStats:
+    """Per-generation counters (python/woodcock/spec.py:39-89)."""
+
+    prompt_tokens: int = 0
+    new_tokens: int = 0
+    rounds: int = 0
+    accepted: list[int] = field(default_factory=list)  # draft tokens accepted per round
+    drafted: list[int] = field(default_factory=list)   # draft tokens verified per round
+    depths: list[int] = field(default_factory=list)
+    t_total: float = 0.0
+    fused: bool = True  # every round has one host synchronisation
+
+    @property
+    def mean_accepted(self) -> float:
+        return float(np.mean(self.accepted)) if self.accepted else 0.0
+
+    @property
+    def tokens_per_round(self) -> float:
+        return self.mean_accepted + 1.0
+
+    @property
+    def acceptance_rate(self) -> float:
+        d = sum(self.drafted)
+        return sum(self.accepted) / d if d else 0.0
+
+    def as_dict(self) -> dict:
+        return {"prompt_tokens": self.prompt_tokens, "new_tokens": self.new_tokens, "rounds": self.rounds,
+                "mean_accepted": self.mean_accepted, "tokens_per_round": self.tokens_per_round,
+                "acceptance_rate": self.acceptance_rate,
+                "mean_verified": float(np.mean(self.drafted)) if self.drafted else 0.0,
+                "mean_depth": float(np.mean(self.depths)) if self.depths else 0.0, "t_total": self.t_total,
+                "fused": self.fused}
+
+
+class SpeculativeDecoder:
+    """Greedy speculative decoding: one drafter cache, one target, one policy.
+
+    target: ``verify_forward(tokens, rows, offset_dev, positions, mask) ->
+    (logits, taps)`` enqueued without a host synchronisation (``TargetRunner``
+    over a TargetModel, or a synthetic stand-in), ``prepare(rows)`` called
+    before each round is enqueued or replayed, and ``cache`` (the target KV
+    list to compact after tree rounds, or None).
+
+    Chain rounds can be captured as one HIP graph per chain length
+    (``use_graphs``): the policy's choice selects the graph to replay.  Tree
+    rounds are enqueued eagerly (their mask prefix is the host-known n)."""
+
+    def __init__(self, drafter: Drafter, target, policy: Policy, capacity: int = 4096, k_max: int = 8,
+                 max_tree_depth: int = 0, use_graphs: bool = False):
+        self.d = drafter
+        self.t = target
+        self.policy = policy
+        self.rnd = ChainRound(drafter, k_max, capacity, getattr(target, "cache", None),
+                              max_keep=max_tree_depth + 1)
+        self.k_max = k_max
+        self.use_graphs = use_graphs
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._trees: dict[tuple[int, int, int], object] = {}
+        self._tree_mask = None
+        self.n = 0
+        self.x_n = 0
+
+    # ------------------------------------------------------------------ state
+
+    def start(self, n: int, x_n: int, root_hidden: torch.Tensor) -> None:
+        """State after prefill (spec.py:129-141): n committed tokens before x_n in
+        both caches, x_n the newest token, root_hidden the drafter's pre-norm
+        hidden state of entry n-1 (the cache entries 0..n-1 are the caller's)."""
+        self.rnd.set_root(n, root_hidden, x_n)
+        if self.rnd.target_cache is not None:
+            for c in self.rnd.target_cache:
+                c.offset = n
+        self.n, self.x_n = n, int(x_n)
+        self.policy.reset()
+
+    # ------------------------------------------------------------------ chain rounds
+
+    def _enqueue_chain(self, k: int) -> None:
+        r = self.rnd
+        r.enqueue_seq()
+        r.enqueue_draft(k)
+        logits, taps = self.t.verify_forward(r.seq, k + 1, r.n_dev())
+        r.enqueue_verify(logits)
+        r.enqueue_commit(taps, k)
+        r.enqueue_readback()
+
+    def chain_round(self, k: int) -> RoundResult:
+        """The fused greedy chain round of length k (spec.py:331-364)."""
+        self.t.prepare(k + 1)
+        g = self._graphs.get(k)
+        if g is not None:
+            g.replay()
+        else:
+            self._enqueue_chain(k)
+        res = self.rnd.finish()
+        if self.use_graphs and g is None:
+            # captured after a first eager round of this length (kernel attributes,
+            # workspaces and allocator pools are in place by then)
+            self._graphs[k] = self._capture(k)
+        res.k = res.depth = k
+        return res
+
+    def _capture(self, k: int) -> torch.cuda.CUDAGraph:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):  # records without executing: the state does not move
+            self._enqueue_chain(k)
+        torch.cuda.current_stream().wait_stream(s)
+        return g
+
+    # ------------------------------------------------------------------ tree rounds
+
+    def tree_drafter(self, plan: Plan):
+        from .tree_draft import TreeDrafter
+
+        key = (plan.max_depth, plan.width, plan.budget)
+        tdr = self._trees.get(key)
+        if tdr is None:
+            tdr = self._trees[key] = TreeDrafter(self.d, self.rnd.cache, plan.max_depth, plan.width, plan.budget)
+        return tdr
+
+    def enqueue_tree_draft(self, plan: Plan):
+        """Greedy tree drafting from the root (spec.py:216-303) -> (device tree, rows)."""
+        r = self.rnd
+        tdr = self.tree_drafter(plan)
+        idx = (r.verdict[_lib.V_N_KEEP:_lib.V_N_KEEP + 1] - 1).long()
+        root_hid = r.upd_hid.index_select(0, idx)
+        tree = tdr.draft(r.x_n_dev(), None, None, r.n_dev(), root_hidden=root_hid)
+        return tree, min(tdr.n_nodes, tdr.budget + 1)
+
+    def enqueue_tree_target(self, tree, rows: int):
+        """The verify forward over the tree block: positions n + depth and the
+        tree attention mask over the cache slots (spec.py:313-317)."""
+        r = self.rnd
+        width = self.n + rows
+        if r.target_cache is not None:
+            width = max(width, r.target_cache[0].capacity)
+        if self._tree_mask is None or self._tree_mask.shape[1] < width:
+            self._tree_mask = torch.zeros(_lib.WC_MAX_NODES, width, dtype=torch.uint8, device=self.d.device)
+        mask = self._tree_mask[:rows]
+        _lib.call("wc_tree_mask", ptr(tree.parents), rows, self.n, ptr(mask), mask.stride(0), stream_ptr())
+        positions = tree.depth[:rows] + r.n_dev()
+        return self.t.verify_forward(tree.tokens, rows, r.n_dev(), positions, mask)
+
+    def tree_round(self, plan: Plan) -> RoundResult:
+        """Greedy tree round (spec.py:187-201) with one host synchronisation."""
+        r = self.rnd
+        tree, rows = self.enqueue_tree_draft(plan)
+        self.t.prepare(rows)
+        logits, taps = self.enqueue_tree_target(tree, rows)
+        r.enqueue_tree_verify(logits, tree.tokens[:rows], tree.parents[:rows])
+        r.enqueue_tree_commit(taps, rows, plan.max_depth)
+        r.enqueue_readback()
+        res = r.finish()
+        res.k, res.depth = rows - 1, plan.max_depth
+        return res
+
+    # ------------------------------------------------------------------ loop
+
+    def round(self) -> RoundResult:
+        """One round as the policy plans it (spec.py:169-201)."""
+        plan = self.policy.plan(context_len=self.n, stochastic=False)
+        t0 = time.perf_counter()
+        if plan.width == 1:
+            if not 1 <= plan.max_depth <= self.k_max:
+                raise ValueError(f"planned chain of {plan.max_depth} outside 1..{self.k_max}")
+            res = self.chain_round(plan.max_depth)
+        else:
+            res = self.tree_round(plan)
+        self.policy.observe(res.n_accepted, res.k, res.depth, 0.0, time.perf_counter() - t0)
+        self.n += len(res.tokens)
+        self.x_n = res.tokens[-1]
+        return res
+
+    def generate(self, max_new_tokens: int, eos=()) -> tuple[list[int], GenStats]:
+        """Rounds from the started state until max_new_tokens (x_n counted) or an
+        EOS token (spec.py:151-212, after the prefill)."""
+        st = GenStats(prompt_tokens=self.n)
+        eos = set(eos)
+        out = [self.x_n]
+        t0 = time.perf_counter()
+        while len(out) < max_new_tokens and out[-1] not in eos:
+            res = self.round()
+            st.rounds += 1
+            st.accepted.append(res.n_accepted)
+            st.drafted.append(res.k)
+            st.depths.append(res.depth)
+            for tok in res.tokens:
+                out.append(tok)
+                if tok in eos or len(out) >= max_new_tokens:
+                    break
+        st.t_total = time.perf_counter() - t0
+        st.new_tokens = len(out)
+        return out, st

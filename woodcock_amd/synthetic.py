@@ -82,39 +82,76 @@ def draft_vocab(vocab: int, k: int, seed: int = 0, always=()) -> np.ndarray:
 
 
 class SyntheticTarget:
-    """Stand-in for the verify-width target forward (out of scope here): fixed
-    target logits [K+1, V] fp32 ~ N(0, scale^2) and feature taps [K+1, Dt].
+    """Stand-in for the verify-width target forward: fixed target logits
+    [K+1, V] fp32 ~ N(0, scale^2) and feature taps [K+1, Dt].
 
     ``plant(drafts_dev, n_agree)`` makes rows i < n_agree take the drafted token
     d_{i+1} as their argmax and keeps row n_agree away from d_{n_agree+1}, so a
     greedy verify accepts exactly n_agree drafts.  It runs as device ops on
     device-resident drafts (capturable in a graph) and restores the previous
-    round's plant first."""
+    round's plant first; n_agree is a host int or a device int32 [1].
+
+    As a decoder's target (``verify_forward``), the agreement of each round is
+    drawn on the host before the round (``prepare``): with ``agree_p`` set,
+    every draft position agrees independently with probability agree_p
+    (seeded), so the round accepts the drafts before the first disagreeing one;
+    the count goes to the device, where the plant reads it."""
 
     BIG, BLOCK = 1.0e4, -1.0e4
 
     def __init__(self, k: int, vocab: int, target_hidden: int, num_features: int = 3, device="cuda", seed: int = 0,
-                 scale: float = 3.0, tap_dtype=torch.bfloat16):
+                 scale: float = 3.0, tap_dtype=torch.bfloat16, agree_p: float | None = None):
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         self.logits = scale * torch.randn(k + 1, vocab, generator=g, device=device, dtype=torch.float32)
         self.taps = [torch.randn(k + 1, target_hidden, generator=g, device=device, dtype=torch.float32).to(tap_dtype)
                      for _ in range(num_features)]
         self.k = k
+        self.vocab_size = vocab
+        self.cache = None
         dev = self.logits.device
         self._rows = torch.arange(k, device=dev)
         self._prev_idx = torch.zeros(k, dtype=torch.long, device=dev)
         self._prev_val = self.logits[self._rows, self._prev_idx].clone()
         self._big = torch.full((k,), self.BIG, device=dev)
         self._block = torch.full((k,), self.BLOCK, device=dev)
+        self.agree_p = agree_p
+        self._rng = np.random.default_rng(seed + 0x5eed)
+        self.n_agree_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+        self._n_agree_host = torch.zeros(1, dtype=torch.int32, pin_memory=dev.type == "cuda")
+        self.agreements: list[int] = []
 
-    def plant(self, drafts_dev: torch.Tensor, n_agree: int) -> None:
+    def plant(self, drafts_dev: torch.Tensor, n_agree) -> None:
         rows = self._rows
         self.logits.index_put_((rows, self._prev_idx), self._prev_val)  # undo the previous plant
         self._prev_idx.copy_(drafts_dev[: self.k].long())
         self._prev_val.copy_(self.logits[rows, self._prev_idx])
         vals = torch.where(rows < n_agree, self._big, torch.where(rows == n_agree, self._block, self._prev_val))
         self.logits.index_put_((rows, self._prev_idx), vals)
+
+    def set_agreement(self, n: int) -> None:
+        """The next plant's agreeing row count (enqueued host -> device copy)."""
+        self._n_agree_host[0] = int(n)
+        self.n_agree_dev.copy_(self._n_agree_host, non_blocking=True)
+
+    def prepare(self, rows: int) -> None:
+        """Draw this round's agreement (chain of rows - 1 drafts), when agree_p is set."""
+        if self.agree_p is None:
+            return
+        k = rows - 1
+        hits = self._rng.random(k) < self.agree_p
+        n = int(np.argmin(hits)) if not hits.all() else k
+        self.agreements.append(n)
+        self.set_agreement(n)
+
+    def verify_forward(self, tokens: torch.Tensor, rows: int, offset_dev: torch.Tensor,
+                       positions: torch.Tensor | None = None, mask: torch.Tensor | None = None):
+        """Logits / taps of the verify block [x_n, d_1..d_K] (tokens [>= k + 1],
+        device): the drafts planted with the device agreement count."""
+        if rows > self.k + 1:
+            raise ValueError(f"synthetic target holds {self.k + 1} rows, {rows} requested")
+        self.plant(tokens[1:self.k + 1], self.n_agree_dev)
+        return self.logits[:rows], [t[:rows] for t in self.taps]
 
 
 def stochastic_workload(k: int, vocab: int, head_rows: int, seed: int = 0, zipf_s: float = 1.1,

@@ -80,20 +80,27 @@ class TreeDrafter:
                                torch.zeros(self.n_nodes, dtype=torch.int32, device=dev),
                                torch.zeros(1, dtype=torch.int32, device=dev))
 
-    def draft(self, root_token: torch.Tensor, root_out: torch.Tensor, root_fb: torch.Tensor,
-              offset_dev: torch.Tensor) -> DeviceTree:
+    def draft(self, root_token: torch.Tensor, root_out: torch.Tensor | None, root_fb: torch.Tensor | None,
+              offset_dev: torch.Tensor, root_hidden: torch.Tensor | None = None) -> DeviceTree:
         """root_token [1] int32 (device), root_out / root_fb [hidden] fp32 rows, the
         drafter's context length n = *offset_dev.  Enqueue only.  With post_norm
         the feedback of a node is its `out` (drafter.py:193-194), so root_fb is
-        read only when post_norm is off."""
-        device_of(root_out)
+        read only when post_norm is off.  Alternatively root_hidden, the root's
+        pre-norm hidden row: the first level's head then applies the final
+        RMSNorm itself (out = RMSNorm(hidden), drafter.py:190) and root_out /
+        root_fb are not used."""
         d, w = self.d, self.width
         cfg = d.cfg
         hidden = cfg.hidden_size
         s = stream_ptr()
         # store row 0: the root; row 1 + (level - 1) * width + r: frontier row r of a level
-        self.store_out[0].copy_(root_out.reshape(hidden))
-        self.store_hid[0].copy_(root_fb.reshape(hidden))
+        if root_hidden is not None:
+            device_of(root_hidden)
+            self.store_hid[0].copy_(root_hidden.reshape(hidden))
+        else:
+            device_of(root_out)
+            self.store_out[0].copy_(root_out.reshape(hidden))
+            self.store_hid[0].copy_(root_fb.reshape(hidden))
         fb_store = self.store_out if cfg.post_norm else self.store_hid
         _lib.call("wc_tree_draft_begin", ptr(self.state), ptr(root_token), s)
         cache = self.cache
@@ -106,9 +113,14 @@ class TreeDrafter:
         store_row = 0  # first store row of the current frontier
         for depth, (node_base, rows) in enumerate(self.levels, start=1):
             # (a) children of every frontier node: head logits, q = softmax(z), top-width
-            _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]), hidden,
-                      None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None, None,
-                      ptr(d.ws), s)
+            if depth == 1 and root_hidden is not None:  # final norm of the root, its `out` -> store row 0
+                _lib.call("wc_draft_head_norm", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_hid), hidden,
+                          None, 0, ptr(self.store_out), hidden, ptr(self.logits), self.logits.stride(0),
+                          ptr(self.tok_rows), None, None, ptr(d.ws), s)
+            else:
+                _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]),
+                          hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None,
+                          None, ptr(d.ws), s)
             _lib.call("wc_probs_from_logits", ptr(self.logits), rows, head_rows, self.logits.stride(0), 1.0,
                       ptr(self.q), self.q.stride(0), ptr(workspace(d.device)), s)
             _lib.call("wc_tree_draft_expand", ptr(self.state), ptr(self.q), rows, head_rows, self.q.stride(0),
