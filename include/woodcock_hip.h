@@ -83,6 +83,18 @@ int wc_argmax_rows(const float* logits, int rows, int vocab, int64_t ld, int32_t
 int wc_verify_chain_greedy(const float* logits, int rows, int vocab, int64_t ld, const int32_t* draft_tokens_dev,
                            wc_verdict* verdict_dev, void* workspace, wc_stream_t stream);
 
+/* wc_verify_chain_greedy without a caller workspace and without any allocation:
+ * its scratch (argmax slots for up to WC_MAX_NODES rows and the kernel's
+ * counters, 8,832 bytes) is a static device array of the library, one per GPU,
+ * kept until the process ends; each call clears it with a kernel first.
+ * rows > WC_MAX_NODES is rejected (WC_E_INVALID).  Every call on one GPU
+ * shares that GPU's array, so calls that overlap on one GPU (two streams at
+ * once) race; calls ordered on one stream are safe.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int wc_verify_chain_greedy_static(const float* logits, int rows, int vocab, int64_t ld,
+                                  const int32_t* draft_tokens_dev, wc_verdict* verdict_dev, wc_stream_t stream);
+
 /* Greedy tree verification fused with the target argmax: N = rows flattened
  * nodes, node 0 the root; tree_tokens_dev/tree_parents_dev [N] (parents[0] = -1,
  * children in ascending node order = draw order).  Writes the accepted path,

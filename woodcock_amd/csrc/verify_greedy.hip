@@ -7,6 +7,8 @@
 // atomicMax per row; the last block to finish runs the acceptance scan with
 // wave-wide ballots and writes a wc_verdict, then clears the slots and its
 // counter so the kernel can be replayed (graph-safe, no memset).
+#include <mutex>
+
 #include "wc_common.h"
 
 namespace wc {
@@ -162,9 +164,59 @@ static int launch_argmax_verify(const float* logits, int rows, int vocab, int64_
   return WC_OK;
 }
 
+// ------------------------------------------------------------------ scratch without allocation
+// wc_verify_chain_greedy_static keeps its scratch -- the argmax slots of up to
+// WC_MAX_NODES rows, then the argmax counter tree, laid out as in a verify
+// workspace -- in this file-scope device array: one copy per GPU, alive until
+// the process ends.  Host code never passes the array's name to a kernel (in
+// host code it is only a stand-in for the symbol); it passes the device
+// address hipGetSymbolAddress returns, queried once per device with that
+// device current.
+constexpr size_t kStaticScratchBytes = kCounterOff + (kCtrArgmax + 1) * kTreeCounterBytes;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices];
+
+static int static_scratch(void** out) {
+  int dev = 0;
+  WC_HIP(hipGetDevice(&dev));
+  WC_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "static scratch: device %d beyond the %d supported", dev,
+             kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(WC_E_HIP, "static scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return WC_OK;
+}
+
 }  // namespace wc
 
 extern "C" {
+
+int wc_verify_chain_greedy_static(const float* logits, int rows, int vocab, int64_t ld,
+                                  const int32_t* draft_tokens_dev, wc_verdict* verdict_dev, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(verdict_dev != nullptr, "wc_verify_chain_greedy_static: verdict is NULL");
+  WC_REQUIRE(rows == 1 || draft_tokens_dev != nullptr, "wc_verify_chain_greedy_static: draft tokens are NULL");
+  WC_REQUIRE(rows >= 1 && rows <= WC_MAX_NODES,
+             "wc_verify_chain_greedy_static: %d rows exceed the %d rows its static scratch holds", rows,
+             WC_MAX_NODES);
+  void* ws = nullptr;
+  if (int rc = static_scratch(&ws)) return rc;
+  // slots and counters start at zero: cleared by a kernel (no memset node, so
+  // a captured call stays valid), whatever an earlier call left
+  if (int rc = wc_workspace_init(ws, kStaticScratchBytes, stream)) return rc;
+  return launch_argmax_verify(logits, rows, vocab, ld, kModeChain, draft_tokens_dev, nullptr, nullptr, nullptr,
+                              verdict_dev, ws, reinterpret_cast<hipStream_t>(stream));
+}
 
 int wc_argmax_rows(const float* logits, int rows, int vocab, int64_t ld, int32_t* out_dev, void* workspace,
                    wc_stream_t stream) {
