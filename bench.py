@@ -40,6 +40,14 @@ STEP4_BYTES = 83_886_080 + 233_308_160 + 16_781_312
 K = 4
 
 
+_T0 = time.perf_counter()
+
+
+def log(msg: str) -> None:
+    """Progress on stderr (the JSON line stays the only stdout output)."""
+    print(f"[bench {time.perf_counter() - _T0:6.1f}s] {msg}", file=sys.stderr, flush=True)
+
+
 def _sleep_gate():
     import torch
 
@@ -142,6 +150,7 @@ def bench_gpu(args):
         g_commit.replay()
         return rnd.finish()
 
+    log("workload built; warm-up rounds")
     for _ in range(args.warmup):
         one_round()
     # host-observed latency: launch of the round to the verdict on the host (single sync)
@@ -176,6 +185,34 @@ def bench_gpu(args):
         plants.append(1e3 * e[1].elapsed_time(e[2]))
     t_timed = time.perf_counter() - t_begin
     assert set(accepted) == {2}, f"accepted lengths {set(accepted)}"
+    log(f"{args.steps} timed rounds: median {np.median(rounds_gpu):.1f} us")
+    if args.round_only:
+        return {"round_gpu_us": float(np.median(rounds_gpu)), "timed_seconds": t_timed}
+
+    # cold start: before each round 1 GiB is read, which evicts the drafter's
+    # weights from the 256 MB Infinity Cache as the target forward between
+    # rounds does in the product (a read leaves clean lines behind: no
+    # write-back competes with the round); the read is outside the timed region
+    flush = torch.zeros(1 << 28, dtype=torch.float32, device=rnd.cache[0].keys.device)
+
+    def evict():
+        flush.sum()
+
+    cold = []
+    for _ in range(max(10, args.steps // 10)):
+        g_rewind.replay()
+        evict()
+        _sleep_gate()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        e[0].record()
+        g_draft.replay()
+        e[1].record()
+        g_plant.replay()
+        e[2].record()
+        g_commit.replay()
+        e[3].record()
+        rnd.finish()
+        cold.append(1e3 * (e[0].elapsed_time(e[1]) + e[2].elapsed_time(e[3])))
 
     # ---- components, each a graph of REP launches
     REP = 32
@@ -372,6 +409,7 @@ def bench_gpu(args):
                       kp4, vp4, _lib.WC_BF16, cache4[0].capacity, ptr(off4), 0, None, None, 0, ptr(hid4s), None,
                       None, ws4, s())
 
+    log("cold rounds done; component graphs")
     comps = {}
     reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1, "tree_draft": 1}
     for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
@@ -385,6 +423,24 @@ def bench_gpu(args):
         comps[name] = float(np.median(t)) / reps.get(name, REP)
     rewind()
     torch.cuda.synchronize()
+    cold_head = []
+    for _ in range(20):
+        evict()
+        _sleep_gate()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        _lib.call("wc_draft_head_norm", dims, W, ptr(hid1), dm, None, 0, ptr(out1), dm, None, 0, ptr(tok), None,
+                  None, ws, s())
+        e1.record()
+        torch.cuda.synchronize()
+        cold_head.append(1e3 * e0.elapsed_time(e1))
+    del flush
+    torch.cuda.empty_cache()
+    log("components done; config-4 round loop")
+    c4 = bench_config4(args, d4)
+    log(f"config-4: mean K {c4['mean_k']:.2f}, {c4['round_us']:.1f} us per round; config-5 tree rounds")
+    c5 = bench_tree_round(args, d, tm, tcfg)
+    log(f"config-5 tree round {c5['round_us']:.1f} us")
 
     head_bytes = 16384 * cfg.hidden_size * 2
     layer_bytes = 2 * (cfg.num_heads + 2 * cfg.num_kv_heads) * cfg.head_dim * dm * 2 + \
@@ -409,6 +465,10 @@ def bench_gpu(args):
         "target_tree_us": comps["target_tree"],
         "tree_draft_us": comps["tree_draft"],
         "draft_step_4b_us": comps["draft_step_4b"],
+        "round_gpu_us_cold": float(np.median(cold)),
+        "head_us_cold": float(np.median(cold_head)),
+        "config4": c4,
+        "config5": c5,
         "head_bytes": head_bytes,
         "step_bytes": step_bytes,
         "compact_bytes_avg": compact_bytes,
@@ -420,6 +480,103 @@ def bench_gpu(args):
         "rnd": rnd,
         "target": target,
     }
+
+
+def bench_config4(args, d4):
+    """Auto chain length at the Qwen3-4B drafter shape (drafter context 4096):
+    the round loop (SpeculativeDecoder) with CostAwareChain, whose costs are
+    measured here -- head and draft step of this drafter, the verify forward
+    of a random-init Qwen3-4B-shape target (36 layers) over 1..9 rows -- and
+    a synthetic target whose draft positions agree with probability 0.68.
+    GPU µs per round exclude the synthetic stand-in (planting the agreement)."""
+    import torch
+
+    from woodcock_amd.costs import time_drafter, time_verify
+    from woodcock_amd.policies import CostAwareChain
+    from woodcock_amd.spec import SpeculativeDecoder
+    from woodcock_amd.synthetic import SyntheticTarget
+    from woodcock_amd.target import TargetConfig, TargetModel, random_target
+
+    dev = d4.device
+    t_d = time_drafter(d4, CTX4, iters=20)
+    tcfg4 = TargetConfig(hidden_size=2560, num_heads=32, num_kv_heads=8, head_dim=128, intermediate_size=9728,
+                         num_layers=36)
+    tm4 = TargetModel(tcfg4, random_target(tcfg4, seed=args.seed + 11, device=dev), dev, max_rows=16)
+    verify = time_verify(tm4, CTX4, 9, iters=5)
+    del tm4
+    torch.cuda.empty_cache()
+    policy = CostAwareChain(t_d["step_ms"], t_d["head_ms"], verify)
+    syn = SyntheticTarget(8, d4.cfg.vocab_size, d4.cfg.target_hidden_size, device=dev, seed=args.seed + 12,
+                          agree_p=0.68)
+    warm, rounds = 24, max(40, args.steps // 2)
+    dec = SpeculativeDecoder(d4, syn, policy, capacity=CTX4 + 16 + 9 * (warm + rounds), k_max=8, use_graphs=True,
+                             timing=True)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 13)
+    for c in dec.rnd.cache:
+        c.keys[0, :, :CTX4] = torch.randn(c.keys[0, :, :CTX4].shape, generator=g, device=dev).bfloat16()
+        c.values[0, :, :CTX4] = torch.randn(c.values[0, :, :CTX4].shape, generator=g, device=dev).bfloat16()
+    dec.start(CTX4, 151643, torch.randn(1, d4.cfg.hidden_size, generator=g, device=dev))
+    for _ in range(warm):  # every length seen here is captured after its first eager round
+        dec.round()
+    us, ks, acc, full = [], [], [], []
+    for _ in range(rounds):
+        _sleep_gate()
+        res = dec.round()
+        t = dec.last_times
+        us.append(t["round_us"])
+        ks.append(res.k)
+        acc.append(res.n_accepted)
+        full.append(t["round_us"] + 1e3 * verify[res.k + 1])
+    return {"round_us": float(np.mean(us)), "round_us_median": float(np.median(us)), "mean_k": float(np.mean(ks)),
+            "k_hist": {int(k): int(n) for k, n in zip(*np.unique(ks, return_counts=True))},
+            "mean_accepted": float(np.mean(acc)), "rounds": rounds,
+            "head_ms": t_d["head_ms"], "step_ms": t_d["step_ms"],
+            "verify_ms_qwen3_4b_36l": {int(n): round(v, 4) for n, v in verify.items()},
+            "round_us_incl_target_forward": float(np.mean(full)),
+            "tokens_per_s_incl_target_forward": float((np.mean(acc) + 1) / (np.mean(full) * 1e-6))}
+
+
+def bench_tree_round(args, d, tm, tcfg):
+    """The config-5 tree round through the round loop: greedy tree drafting
+    (depth 6, width 4, 60 verified rows) at drafter context 2048, the 28-layer
+    Qwen3-1.7B target forward over the tree block (tree mask, context 2048),
+    the tree walk, the target KV compaction along the accepted branch and the
+    drafter update; one host sync.  Per-phase GPU µs from events."""
+    import torch
+
+    from woodcock_amd.policies import StaticPolicy
+    from woodcock_amd.spec import SpeculativeDecoder, TargetRunner
+
+    dev = d.device
+    ctx, rounds = 2048, 12
+    cap = ctx + 64 + 8 * (rounds + 3)
+    tcache = tm.make_cache(cap)
+    for c in tcache:
+        c.keys.normal_()
+        c.values.normal_()
+    dec = SpeculativeDecoder(d, TargetRunner(tm, tcache), StaticPolicy(6, 4, 59), capacity=cap, k_max=4,
+                             max_tree_depth=6, timing=True)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 21)
+    for c in dec.rnd.cache:
+        c.keys[0, :, :ctx] = torch.randn(c.keys[0, :, :ctx].shape, generator=g, device=dev).bfloat16()
+        c.values[0, :, :ctx] = torch.randn(c.values[0, :, :ctx].shape, generator=g, device=dev).bfloat16()
+    dec.start(ctx, 151643, torch.randn(1, d.cfg.hidden_size, generator=g, device=dev))
+    for _ in range(3):
+        dec.round()
+    ph = {"draft_us": [], "target_us": [], "verify_commit_us": []}
+    for _ in range(rounds):
+        if hasattr(torch.cuda, "_sleep"):
+            torch.cuda._sleep(4_000_000)  # the host enqueues the whole round before the GPU reaches it
+        dec.round()
+        for k in ph:
+            ph[k].append(dec.last_times[k])
+    out = {k: float(np.median(v)) for k, v in ph.items()}
+    out["round_us"] = out["draft_us"] + out["target_us"] + out["verify_commit_us"]
+    out["round_us_excl_target_forward"] = out["draft_us"] + out["verify_commit_us"]
+    out["rounds"] = rounds
+    del tcache, dec
+    torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------- HBM traffic
@@ -461,6 +618,157 @@ def pmc_probe(seed=0):
     torch.cuda.synchronize()
     print(f"pmc probe: {PROBE_HEADS} head launches, {PROBE_COPIES} copies of {4 * PROBE_COPY_FLOATS} bytes",
           flush=True)
+
+
+# Counter probe over the round's kernels: phases separated by a one-element
+# torch.abs marker -- heads, draft-step layers (M = 1), update passes (fuse +
+# layer at 5 rows, 3 live), verify-width target layers (M = 60, tree mask) --
+# then the calibration copies.  Per launch of each phase the same kernels run
+# in the same order, so dispatch j of a repeat is one kernel (the table below
+# names it and gives its algorithmic bytes).
+PROBE_REPS = 8
+_D, _HKV, _F, _HD = 2048, 8, 6144, 2048  # Qwen3-1.7B drafter: hidden, kv heads, intermediate, q width
+PHASES = {
+    "head": [("head GEMV + argmax 16384 x 2048", 16384 * _D * 2)],
+    "draft layer (M = 1, ctx 512)": [
+        ("QKV, two streams, 4096 x (2048 + 2048)", 2 * (_HD + 2 * _HKV * 128) * _D * 2),
+        ("decode attention, 513 keys", 2 * 513 * _HKV * 128 * 2),
+        ("o_proj + residual 2048 x 2048", _D * _HD * 2),
+        ("gate / up + SiLU 2 x 6144 x 2048", 2 * _F * _D * 2),
+        ("down + residual 2048 x 6144", _D * _F * 2)],
+    "update pass (5 rows, 3 live)": [
+        ("fuse 2048 x 6144", _D * 3 * _D * 2),
+        ("QKV, two streams", 2 * (_HD + 2 * _HKV * 128) * _D * 2),
+        ("attention, 3 rows", 2 * 515 * _HKV * 128 * 2),
+        ("attention merge", 0),
+        ("o_proj", _D * _HD * 2),
+        ("gate / up", 2 * _F * _D * 2),
+        ("down", _D * _F * 2)],
+    "target layer (M = 60, ctx 2048, tree mask)": [
+        ("input -> fragment-order bf16 hi / lo", 60 * _D * 4 + 60 * _D * 4),
+        ("QKV 4096 x 2048 (+ q/k norm, RoPE, K/V append)", (_HD + 2 * _HKV * 128) * _D * 2),
+        ("tree attention, 2048 + 60 keys", 2 * 2108 * _HKV * 128 * 2),
+        ("attention merge", 0),
+        ("o_proj 2048 x 2048", _D * _HD * 2),
+        ("gate / up 2 x 6144 x 2048", 2 * _F * _D * 2),
+        ("down 2048 x 6144", _D * _F * 2)],
+}
+
+
+def pmc_probe2(seed=0):
+    """The launches of the counter passes over the round's kernels (see PHASES)."""
+    import ctypes as C
+
+    import torch
+
+    from woodcock_amd import _lib
+    from woodcock_amd.cache import KVCache
+    from woodcock_amd.runtime import ptr, stream_ptr
+    from woodcock_amd.sampling import DraftTree, tree_attention_mask
+    from woodcock_amd.target import TargetConfig, TargetLayer, random_layer
+
+    cfg, d, ids, rnd, target, init_state, root = build_workload(seed)
+    dev = rnd.cache[0].keys.device
+    dims, W, ws = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws)
+    dm = cfg.hidden_size
+    mark = torch.zeros(1, device=dev)
+    tcfg = TargetConfig()
+    trng = np.random.default_rng(seed + 9)
+    parents, depth = [-1], [0]
+    while len(parents) < 60:
+        p_ = int(trng.integers(0, len(parents)))
+        if depth[p_] < 6:
+            parents.append(p_)
+            depth.append(depth[p_] + 1)
+    tree = DraftTree([int(t) for t in trng.integers(0, cfg.vocab_size, 60)], parents, depth)
+    tl = TargetLayer(tcfg, random_layer(tcfg, seed=seed, device=dev), dev, max_rows=60)
+    tcache = KVCache(tcfg.num_kv_heads, tcfg.head_dim, 2048 + 64, torch.bfloat16, dev)
+    tx = torch.randn(60, tcfg.hidden_size, device=dev)
+    toff = torch.tensor([2048], dtype=torch.int32, device=dev)
+    tpos = torch.tensor([2048 + dd for dd in depth], dtype=torch.int32, device=dev)
+    tmask = torch.from_numpy(tree_attention_mask(tree, 2048).astype(np.uint8)).to(dev)
+    off = init_state[0:1]
+    hid_s = torch.empty(1, dm, device=dev)
+    x = torch.randn(PROBE_COPY_FLOATS, device=dev)
+    y = torch.empty_like(x)
+    rows = torch.tensor([3], dtype=torch.int32, device=dev)
+    keep = torch.arange(8, dtype=torch.int32, device=dev)
+    tp = (C.c_void_p * 3)(*[t.data_ptr() for t in target.taps])
+    g = torch.empty(5, dm, device=dev)
+    hid5 = torch.empty(5, dm, device=dev)
+    tl(tx, tcache, toff, tpos, tmask)
+    torch.cuda.synchronize()
+    s = stream_ptr()
+    torch.abs(mark, out=mark)
+    for _ in range(PROBE_REPS):
+        _lib.call("wc_draft_head_norm", dims, W, ptr(rnd.upd_hid[0:1]), dm, None, 0, ptr(rnd.upd_out[0:1]), dm,
+                  None, 0, ptr(rnd.drafts[0:1]), None, None, ws, s)
+    torch.abs(mark, out=mark)
+    for _ in range(PROBE_REPS):
+        _lib.call("wc_drafter_forward", dims, W, ptr(rnd.drafts[0:1]), ptr(rnd.upd_out[0:1]), dm, None, 0, 1, None,
+                  rnd._kp, rnd._vp, rnd._kvdt, rnd.cache[0].capacity, ptr(off), 0, None, None, 0, ptr(hid_s), None,
+                  None, ws, s)
+    torch.abs(mark, out=mark)
+    for _ in range(PROBE_REPS):
+        _lib.call("wc_drafter_fuse", dims, W, tp, _lib.WC_BF16, target.taps[0].stride(0), ptr(keep), 5, 5, ptr(rows),
+                  ptr(g), dm, ws, s)
+        _lib.call("wc_drafter_forward", dims, W, ptr(rnd.seq), ptr(g), dm, None, 0, 5, ptr(rows), rnd._kp, rnd._vp,
+                  rnd._kvdt, rnd.cache[0].capacity, ptr(off), 0, None, None, 0, ptr(hid5), None, None, ws, s)
+    torch.abs(mark, out=mark)
+    for _ in range(PROBE_REPS // 2):
+        tl(tx, tcache, toff, tpos, tmask)
+    torch.abs(mark, out=mark)
+    torch.cuda.synchronize()
+    for _ in range(PROBE_COPIES):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    print(f"pmc probe over the round kernels: {PROBE_REPS} repeats per phase, {PROBE_COPIES} copies", flush=True)
+
+
+def pmc_summary2(fetch_dir, write_dir, mfma_dir):
+    """Per-kernel HBM bytes (FETCH_SIZE + WRITE_SIZE, copy-calibrated) and MFMA
+    busy (SQ_VALU_MFMA_BUSY_CYCLES over 1024 SIMDs / (GRBM_GUI_ACTIVE per XCD),
+    the MfmaUtil metric) of the pmc_probe2 phases, as a markdown table."""
+    copy_bytes = 4 * PROBE_COPY_FLOATS
+
+    def phases(d, counter):
+        disp = _per_dispatch(_counter_rows(d), counter)
+        order = sorted(disp)
+        names = [disp[i][0] for i in order]
+        vals = [disp[i][1] for i in order]
+        marks = [i for i, n in enumerate(names) if "abs" in n.lower() and "kernel" in n.lower()]
+        if len(marks) != 5:
+            raise SystemExit(f"{counter}: expected 5 phase markers, found {len(marks)}")
+        copies = [v for n, v in zip(names[marks[-1] + 1:], vals[marks[-1] + 1:]) if "neg" in n.lower()]
+        out = []
+        for a, b in zip(marks, marks[1:]):
+            out.append(list(zip(names[a + 1:b], vals[a + 1:b])))
+        return out, (float(np.mean(copies)) if copies else None)
+
+    fetch, fcopy = phases(fetch_dir, "FETCH_SIZE")
+    write, wcopy = phases(write_dir, "WRITE_SIZE")
+    busy, _ = phases(mfma_dir, "SQ_VALU_MFMA_BUSY_CYCLES")
+    gui, _ = phases(mfma_dir, "GRBM_GUI_ACTIVE")
+    ff, wf = copy_bytes / (fcopy * 1024.0), copy_bytes / (wcopy * 1024.0)
+    lines = [f"Calibration: a {copy_bytes >> 20} MiB copy reads {fcopy:.0f} KiB by FETCH_SIZE (scale {ff:.4f}) and "
+             f"writes {wcopy:.0f} KiB by WRITE_SIZE (scale {wf:.4f}).", "",
+             "| Phase | Kernel | Work | Algorithmic bytes | HBM bytes (fetch + write) | ratio | MFMA busy % |",
+             "|---|---|---|---:|---:|---:|---:|"]
+    for (title, table), F, Wr, B, G in zip(PHASES.items(), fetch, write, busy, gui):
+        per = len(table)
+        reps = len(F) // per
+        for j in range(per):
+            idx = [j + r * per for r in range(reps) if j + r * per < len(F)]
+            name = F[idx[0]][0]
+            short = name if len(name) < 60 else name[:57] + "..."
+            fb = np.mean([F[i][1] for i in idx]) * 1024.0 * ff
+            wb = np.mean([Wr[i][1] for i in idx]) * 1024.0 * wf
+            # the CSV's GRBM_GUI_ACTIVE is summed over the 8 XCDs; MFMA busy cycles over the 1024 SIMDs
+            util = 100.0 * np.mean([B[i][1] for i in idx]) / max(np.mean([G[i][1] for i in idx]) / 8.0 * 1024.0, 1.0)
+            work, algo = table[j]
+            ratio = f"{(fb + wb) / algo:.3f}" if algo else ""
+            lines.append(f"| {title} | `{short}` | {work} | {algo or ''} | {fb + wb:.0f} | {ratio} | {util:.1f} |")
+    print("\n".join(lines))
 
 
 def _counter_rows(d):
@@ -539,6 +847,46 @@ def pmc_summary(fetch_dir, write_dir):
     print("\n".join(lines))
 
 
+def trace_summary(trace_dir: str, steps: int) -> None:
+    """Markdown table of the event-timed rounds of `bench.py --round-only` from a
+    rocprofv3 kernel trace: every dispatch after the first spin kernel (the timed
+    loop gates each round behind one), our kernels (wc::) per round and the rest
+    (torch: the rewind of the state, the synthetic target's plant, the spin)."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {trace_dir}")
+    with open(files[0], newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Dispatch_Id"]))
+    first = next(i for i, r in enumerate(rows) if "spin_kernel" in r["Kernel_Name"])
+    rows = rows[first:]
+    agg: dict[str, list[float]] = {}
+    for r in rows:
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        agg.setdefault(r["Kernel_Name"], []).append(us)
+
+    def short(n: str) -> str:
+        return n if len(n) <= 90 else n[:87] + "..."
+
+    ours = {k: v for k, v in agg.items() if "wc::" in k}
+    rest = {k: v for k, v in agg.items() if "wc::" not in k}
+    tot = sum(sum(v) for v in ours.values())
+    lines = ["| Kernel | Calls / round | Avg µs | Min | Max | µs / round | % of round kernels |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for k, v in sorted(ours.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{short(k)}` | {len(v) / steps:.2f} | {np.mean(v):.2f} | {min(v):.2f} | {max(v):.2f} "
+                     f"| {sum(v) / steps:.2f} | {100 * sum(v) / tot:.1f} |")
+    lines.append(f"| **all round kernels** | {sum(len(v) for v in ours.values()) / steps:.2f} | | | | "
+                 f"**{tot / steps:.2f}** | 100 |")
+    lines += ["", "Outside the measured round (rewind of the device state, the synthetic target's plant, the "
+              "spin gate):", "", "| Kernel | Calls / round | Avg µs |", "|---|---:|---:|"]
+    for k, v in sorted(rest.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{short(k)}` | {len(v) / steps:.2f} | {np.mean(v):.2f} |")
+    print("\n".join(lines))
+
+
 def head_traffic():
     """HBM bytes per head launch from the committed counter summary, or None."""
     try:
@@ -551,17 +899,15 @@ def head_traffic():
     return None
 
 
-def cpu_baseline(gpu, seconds: float):
-    """The oracle (C restatement, OpenMP over output rows) running the same round
-    on the host's cores: K heads, K-1 layers, verify, update (fuse + M=3 layer).
-    Bounded sample of whole rounds."""
-    import torch
-
+def _oracle_rounds(gpu, seconds: float, threads: int):
+    """Whole config-1 rounds on the oracle (C restatement of the reference's
+    arithmetic, OpenMP over output rows): K heads, K-1 layers, the greedy
+    verify, the update (fuse + a 3-row layer pass).  Median µs over a bounded
+    sample, and the sample size."""
     from oracle import core
     from oracle import sampling as osamp
     from woodcock_amd.synthetic import to_bits
 
-    threads = core.default_threads()
     core.set_threads(threads)
     d = gpu["weights"]
     w = {k: to_bits(v) for k, v in d.w.items()}
@@ -577,7 +923,7 @@ def cpu_baseline(gpu, seconds: float):
     root = gpu["root"].cpu().numpy()
     times = []
     t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 2:
+    while (time.perf_counter() < t_end or len(times) < 2) and len(times) < 200:
         oc.offset = BASE_CTX
         t0 = time.perf_counter()
         out = core.rmsnorm(root, od.w["norm.weight"], d.cfg.rms_norm_eps)
@@ -595,12 +941,73 @@ def cpu_baseline(gpu, seconds: float):
         g = od.fuse([t[: a + 1] for t in taps])
         od.forward(acc, g, oc)
         times.append(1e6 * (time.perf_counter() - t0))
-        if len(times) >= 200:
-            break
-    del torch
-    return {"value": float(np.median(times)), "unit": "µs", "cores": threads, "kind": "port",
-            "sample": f"{len(times)} whole rounds of the same workload (oracle drafter in C + numpy verify), "
-                      f"median, {threads} OpenMP threads"}
+    return float(np.median(times)), len(times)
+
+
+def _reference_cpp_step(gpu, seconds: float):
+    """The reference's own C++ runtime (oracle/_ref/libwcref.so, compiled from its
+    sources: Drafter::forward + Drafter::logits + argmax, src/core/drafter.cpp,
+    single-threaded, fp32, no BLAS) on the draft-step unit of
+    scripts/time_draft_step.py: one token at drafter context 512, the full
+    151,936-row head (its C++ drafter has no restricted head).  The head rows
+    are the embedding table's values (timing does not depend on them)."""
+    import tempfile
+
+    from oracle import refcpp
+    from woodcock_amd.synthetic import to_bits
+
+    if not refcpp.available():
+        return None
+    d = gpu["weights"]
+    w = {k: to_bits(v) for k, v in d.w.items()}
+    w["lm_head.weight"] = w["embed_tokens.weight"].copy()
+    cfg = d.cfg.as_dict()
+    rd = refcpp.RefDrafter(cfg, w)
+    cache = rd.make_cache()
+    row = cfg["num_kv_heads"] * cfg["head_dim"]
+    rng = np.random.default_rng(0)
+    kv = rng.standard_normal((BASE_CTX, row)).astype(np.float32)
+    cache.append(0, kv, kv, BASE_CTX)
+    cache.commit(BASE_CTX)
+    feat = rng.standard_normal((1, cfg["hidden_size"])).astype(np.float32)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while (time.perf_counter() < t_end or len(times) < 3) and len(times) < 200:
+        t0 = time.perf_counter()
+        _, out = rd.forward([17], feat, cache)
+        z = rd.logits(out)
+        refcpp.argmax(z[0])
+        times.append(1e3 * (time.perf_counter() - t0))
+        cache.trim_to(BASE_CTX)
+    rd.close()
+    del tempfile
+    return {"value": float(np.median(times)), "unit": "ms", "cores": 1, "kind": "reference",
+            "sample": f"{len(times)} draft steps (one token at drafter context {BASE_CTX}, full 151936-row head, "
+                      "argmax), median; the reference's C++ runtime compiled from its sources"}
+
+
+def cpu_baseline(gpu, seconds: float):
+    """CPU restatement of the reference's semantics (the oracle port) on the same
+    config-1 rounds, at all of the host's cores and at one thread, plus the
+    reference's own compiled C++ draft step when its library is present."""
+    from oracle import core
+
+    threads = core.default_threads()
+    log(f"CPU baseline: oracle rounds at {threads} threads")
+    v_all, n_all = _oracle_rounds(gpu, 0.5 * seconds, threads)
+    log("CPU baseline: oracle rounds at 1 thread")
+    v_one, n_one = _oracle_rounds(gpu, 0.25 * seconds, 1)
+    core.set_threads(threads)
+    log("CPU baseline: the reference's C++ draft step (loading its weights)")
+    ref = _reference_cpp_step(gpu, 0.25 * seconds)
+    out = {"value": v_all, "unit": "µs", "cores": threads, "kind": "port",
+           "sample": f"{n_all} whole config-1 rounds (CPU restatement of reference semantics: drafter in C, numpy "
+                     f"verify), median, {threads} OpenMP threads",
+           "single_thread": {"value": v_one, "unit": "µs", "cores": 1,
+                             "sample": f"{n_one} whole rounds, median, 1 thread"}}
+    if ref is not None:
+        out["reference_cpp_draft_step_full_head"] = ref
+    return out
 
 
 def main():
@@ -609,14 +1016,27 @@ def main():
     ap.add_argument("--steps", type=int, default=200, help="timed rounds")
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=24.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launches the counter passes read")
+    ap.add_argument("--pmc-probe2", action="store_true", help="the launches of the round-kernel counter passes")
+    ap.add_argument("--pmc-summary2", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "MFMA_DIR"),
+                    help="summarise the three counter passes over --pmc-probe2 (no GPU needed)")
+    ap.add_argument("--round-only", action="store_true",
+                    help="only the timed config-1 rounds (for a kernel trace of the round alone)")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="summarise a rocprofv3 kernel trace of --round-only (no GPU needed); --steps as in that run")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 counter passes over --pmc-probe (no GPU needed)")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.pmc_summary2:
+        pmc_summary2(*args.pmc_summary2)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary, args.steps)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the round is a batch-1, single-device path "
@@ -630,7 +1050,13 @@ def main():
     if args.pmc_probe:
         pmc_probe(args.seed)
         return
+    if args.pmc_probe2:
+        pmc_probe2(args.seed)
+        return
     r = bench_gpu(args)
+    if args.round_only:
+        print(json.dumps({"round_gpu_us": round(r["round_gpu_us"], 2), "steps": args.steps}), flush=True)
+        return
     head_gbs = r["head_bytes"] / (r["head_us"] * 1e-6) / 1e9
     step_gbs = r["step_bytes"] / (r["draft_step_us"] * 1e-6) / 1e9
     cpu = None if args.no_cpu_baseline else cpu_baseline(r, args.cpu_seconds)
@@ -671,6 +1097,12 @@ def main():
             "draft_step_us_qwen3_4b_ctx4096": round(r["draft_step_4b_us"], 2),
             "draft_step_hbm_frac_qwen3_4b": round(STEP4_BYTES / (r["draft_step_4b_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "head_gemv_us": round(r["head_us"], 2),
+            "round_gpu_us_cold": round(r["round_gpu_us_cold"], 2),
+            "head_gemv_us_cold": round(r["head_us_cold"], 2),
+            "head_gemv_hbm_frac_cold": round(r["head_bytes"] / (r["head_us_cold"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "config4_auto_k_qwen3_4b": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r["config4"].items()},
+            "config5_tree_round_qwen3_1p7b": {k: (round(v, 2) if isinstance(v, float) else v)
+                                              for k, v in r["config5"].items()},
         },
         "roofline": {
             "kernel": "draft head GEMV + argmax (16384 x 2048 bf16)",

@@ -355,7 +355,7 @@ class SpeculativeDecoder:
     rounds are enqueued eagerly (their mask prefix is the host-known n)."""
 
     def __init__(self, drafter: Drafter, target, policy: Policy, capacity: int = 4096, k_max: int = 8,
-                 max_tree_depth: int = 0, use_graphs: bool = False):
+                 max_tree_depth: int = 0, use_graphs: bool = False, timing: bool = False):
         self.d = drafter
         self.t = target
         self.policy = policy
@@ -363,11 +363,16 @@ class SpeculativeDecoder:
                               max_keep=max_tree_depth + 1)
         self.k_max = k_max
         self.use_graphs = use_graphs
-        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, ...]] = {}
         self._trees: dict[tuple[int, int, int], object] = {}
         self._tree_mask = None
         self.n = 0
         self.x_n = 0
+        # timing: GPU events around the round's three phases -- drafting, the
+        # target's verify forward, verification + commit -- read at the sync
+        self.timing = timing
+        self.last_times: dict[str, float] = {}
+        self._ev: list = []
 
     # ------------------------------------------------------------------ state
 
@@ -384,39 +389,74 @@ class SpeculativeDecoder:
 
     # ------------------------------------------------------------------ chain rounds
 
-    def _enqueue_chain(self, k: int) -> None:
+    def _mark(self) -> None:
+        if self.timing:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            self._ev.append(e)
+
+    def _read_times(self) -> None:
+        """After the round's sync: GPU µs of each phase between the marks."""
+        if self.timing and len(self._ev) == 4:
+            d, t, c = (1e3 * a.elapsed_time(b) for a, b in zip(self._ev, self._ev[1:]))
+            self.last_times = {"draft_us": d, "target_us": t, "verify_commit_us": c, "round_us": d + c}
+        self._ev = []
+
+    def _chain_phases(self, k: int):
         r = self.rnd
-        r.enqueue_seq()
-        r.enqueue_draft(k)
-        logits, taps = self.t.verify_forward(r.seq, k + 1, r.n_dev())
-        r.enqueue_verify(logits)
-        r.enqueue_commit(taps, k)
-        r.enqueue_readback()
+        io = {}
+
+        def draft():
+            r.enqueue_seq()
+            r.enqueue_draft(k)
+
+        def target():
+            io["out"] = self.t.verify_forward(r.seq, k + 1, r.n_dev())
+
+        def commit():
+            logits, taps = io["out"]
+            r.enqueue_verify(logits)
+            r.enqueue_commit(taps, k)
+            r.enqueue_readback()
+
+        return draft, target, commit
 
     def chain_round(self, k: int) -> RoundResult:
         """The fused greedy chain round of length k (spec.py:331-364)."""
         self.t.prepare(k + 1)
-        g = self._graphs.get(k)
-        if g is not None:
-            g.replay()
+        graphs = self._graphs.get(k)
+        self._ev = []
+        self._mark()
+        if graphs is not None:
+            for g in graphs:
+                g.replay()
+                self._mark()
         else:
-            self._enqueue_chain(k)
+            for phase in self._chain_phases(k):
+                phase()
+                self._mark()
         res = self.rnd.finish()
-        if self.use_graphs and g is None:
+        self._read_times()
+        if self.use_graphs and graphs is None:
             # captured after a first eager round of this length (kernel attributes,
             # workspaces and allocator pools are in place by then)
             self._graphs[k] = self._capture(k)
         res.k = res.depth = k
         return res
 
-    def _capture(self, k: int) -> torch.cuda.CUDAGraph:
+    def _capture(self, k: int) -> tuple[torch.cuda.CUDAGraph, ...]:
+        """One graph per phase (drafting, target forward, verify + commit), so a
+        timed replay can tell the target's share apart."""
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):  # records without executing: the state does not move
-            self._enqueue_chain(k)
+        out = []
+        for phase in self._chain_phases(k):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):  # records without executing: the state does not move
+                phase()
+            out.append(g)
         torch.cuda.current_stream().wait_stream(s)
-        return g
+        return tuple(out)
 
     # ------------------------------------------------------------------ tree rounds
 
@@ -455,13 +495,19 @@ class SpeculativeDecoder:
     def tree_round(self, plan: Plan) -> RoundResult:
         """Greedy tree round (spec.py:187-201) with one host synchronisation."""
         r = self.rnd
+        self._ev = []
+        self._mark()
         tree, rows = self.enqueue_tree_draft(plan)
+        self._mark()
         self.t.prepare(rows)
         logits, taps = self.enqueue_tree_target(tree, rows)
+        self._mark()
         r.enqueue_tree_verify(logits, tree.tokens[:rows], tree.parents[:rows])
         r.enqueue_tree_commit(taps, rows, plan.max_depth)
         r.enqueue_readback()
+        self._mark()
         res = r.finish()
+        self._read_times()
         res.k, res.depth = rows - 1, plan.max_depth
         return res
 
