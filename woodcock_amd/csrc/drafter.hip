@@ -35,6 +35,8 @@ struct DrafterWs {
   float* h1;
   float* act;
   float* partial;
+  float* gs_part;        // k-split few-row GEMV: partial tiles per (tile, piece)
+  unsigned int* gs_ctr;  // and one counter line per tile
   size_t bytes;
 };
 
@@ -61,6 +63,8 @@ static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
   w.act = reinterpret_cast<float*>(take(4 * R * d.inter));
   w.partial = reinterpret_cast<float*>(take(4 * static_cast<size_t>(d.kv_heads) * kMaxSplits * kMaxQV *
                                             (d.head_dim + 2)));
+  w.gs_part = reinterpret_cast<float*>(take(4 * static_cast<size_t>(kGsMaxPieces) * kGsPieceFloats));
+  w.gs_ctr = reinterpret_cast<unsigned int*>(take(4 * kCounterStride * static_cast<size_t>(kGsMaxPieces)));
   w.bytes = off;
   return w;
 }
@@ -189,6 +193,96 @@ static bool gf_stage_ok(const void* kern, size_t bytes) {
   return bytes <= it->second;
 }
 
+// Staged few-row MFMA GEMV (k_gemvs): 8-wave blocks, one input segment each
+// (several segments need the split workspace).  The weights stream at what one
+// CU sustains (a 2048 x 6144 GEMV: 7.0 us on 128 blocks, 4.5 us on 256), so the
+// time goes with the blocks the busiest CU runs: each segment's k steps are
+// split into the part count P (1..8) that minimises ceil(blocks / 256) / blocks
+// (ties: fewer parts), unless the launch reduces an argmax.  D = the smallest
+// depth holding a wave's share of its part (chunks of the largest otherwise:
+// 12 steps for one tile, 8 for two, beyond which the weights no longer fit
+// the registers).
+// Two-segment launches (the dual-stream QKV) on k_gemvs with eight waves per
+// segment measured slower than k_gemvf (33.5 MB at M = 5: 17.1 against 14.2
+// us), so they stay there.
+constexpr bool kGsPairedQkv = false;
+
+template <int TW, bool PAIR, int NIN, int XB, int GB>
+static bool launch_gemvs(const GemvArgs& a, hipStream_t s) {
+  constexpr int W = 8;
+  constexpr int WG = 16;  // two-segment blocks: eight waves per segment
+  constexpr int RB = PAIR ? 16 : 16 * TW;
+  const bool split_ok = a.gs_part && a.gs_ctr && a.epi != kEpiArgmax;
+  int kmax = 0, ksum = 0;
+  for (int i = 0; i < a.n_in; ++i) {
+    kmax = std::max(kmax, a.in[i].K);
+    ksum += a.in[i].K + 4;
+  }
+  const int tiles = (a.N + RB - 1) / RB;
+  // two segments and a grid that fills the GPU: one block takes both, eight
+  // waves on each, so no piece hand-over is needed; otherwise the few-row
+  // kernel k_gemvf (one launch, measured faster than pieces here)
+  if constexpr (NIN == 2) {
+    const size_t st2 = static_cast<size_t>(a.M) * ksum * sizeof(float);
+    const int per2 = (kmax / 32 + WG / 2 - 1) / (WG / 2);
+    if (kGsPairedQkv && TW == 1 && tiles >= 256 && st2 <= kGfStageMax && a.M * ((kmax + kGsUnit - 1) / kGsUnit) <= kGsMaxUnits / 2 &&
+        a.epi != kEpiArgmax && per2 <= 12) {
+      const size_t lds2 = std::max(st2, static_cast<size_t>(WG) * TW * 4 * kWave * sizeof(float));
+      const dim3 grid2(tiles, 1), block2(WG * kWave);
+#define WC_GS2(DD)                                                                                              \
+  do {                                                                                                          \
+    if (!gf_stage_ok(reinterpret_cast<const void*>(&k_gemvs<TW, WG, DD, PAIR, NIN, XB, GB, true>), lds2)) break; \
+    hipLaunchKernelGGL((k_gemvs<TW, WG, DD, PAIR, NIN, XB, GB, true>), grid2, block2, lds2, s, a);             \
+    return true;                                                                                                \
+  } while (0)
+      if constexpr (TW == 1) {
+        if (per2 <= 4) WC_GS2(4);
+        else if (per2 <= 8) WC_GS2(8);
+        else WC_GS2(12);
+      }
+#undef WC_GS2
+    }
+    return false;
+  }
+  if (NIN > 1 && !split_ok) return false;
+  int parts = 1;
+  // fewer blocks than CUs, or pieces handed over anyway (several segments):
+  // split the k steps for balance; a full one-segment grid stays whole
+  if (split_ok && (tiles * NIN < 256 || NIN > 1)) {
+    double best = 0.0;
+    for (int pc = 1; pc <= 8; ++pc) {
+      const long blocks = static_cast<long>(tiles) * NIN * pc;
+      if (pc > 1 && (blocks > kGsMaxPieces || kmax / 32 / pc < W)) break;
+      const double per_block = static_cast<double>((blocks + 255) / 256) / static_cast<double>(blocks);
+      if (pc == 1 || per_block < best * (1.0 - 1e-9)) {
+        best = per_block;
+        parts = pc;
+      }
+    }
+  }
+  const int pp = (kmax / 32 + parts - 1) / parts;  // steps of the longest part
+  const int per = (pp + W - 1) / W;
+  const size_t stage = static_cast<size_t>(a.M) * (pp * 32 + 4) * sizeof(float);
+  const size_t lds = std::max(stage, static_cast<size_t>(W) * TW * 4 * kWave * sizeof(float));
+  if (stage > kGfStageMax || a.M * ((pp * 32 + kGsUnit - 1) / kGsUnit) > kGsMaxUnits) return false;
+  if (NIN * parts > 1 && tiles * NIN * parts > kGsMaxPieces) return false;  // the split workspace's slots
+  const dim3 grid(tiles, NIN * parts), block(W * kWave);
+#define WC_GS(DD)                                                                                            \
+  do {                                                                                                       \
+    if (!gf_stage_ok(reinterpret_cast<const void*>(&k_gemvs<TW, W, DD, PAIR, NIN, XB, GB>), lds)) return false; \
+    hipLaunchKernelGGL((k_gemvs<TW, W, DD, PAIR, NIN, XB, GB>), grid, block, lds, s, a);                      \
+    return true;                                                                                             \
+  } while (0)
+  if (per <= 4) WC_GS(4);
+  if constexpr (TW > 1) {
+    WC_GS(8);
+  } else {
+    if (per <= 8) WC_GS(8);
+    WC_GS(12);
+  }
+#undef WC_GS
+}
+
 // Few-row MFMA GEMV: 16 (TW = 1) or 32 (TW = 2, and the gate / up pair) rows
 // per block, every K a multiple of 32, no last-block norm / normalised-input
 // epilogues (those are the one-row kernel's; a bare offset advance is done).
@@ -215,6 +309,23 @@ static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
     units += a.M * ((a.in[i].K + kGfUnit - 1) / kGfUnit);
   }
   const bool stg = units <= 3 * 16 * 3 && stage <= kGfStageMax;
+  // staged with every weight step in flight when a block's piece of the rows
+  // fits the CU (inputs [M][piece K + 4] fp32)
+  {
+    bool ok = true;
+    for (int i = 0; i < a.n_in; ++i) ok = ok && a.in[i].K <= 10240;
+    // one-tile projections only: the gate / up pair and two-tile grids
+    // measured faster on k_gemvf (50 MB gate / up at M = 5: 14.2 against 17 us)
+    if (ok && !wide) {
+      if constexpr (!PAIR) {
+        if (gb == kAll) {
+          if (launch_gemvs<1, PAIR, NIN, XB, kAll>(a, s)) return true;
+        } else if constexpr (NIN == 1) {
+          if (launch_gemvs<1, PAIR, NIN, XB, 0>(a, s)) return true;
+        }
+      }
+    }
+  }
   GemvArgs as = a;
   as.lds_floats = static_cast<int>(stage / sizeof(float));
   // the dynamic region also holds the waves' partial tiles after the main loop
@@ -502,9 +613,12 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
              "wc_drafter_fuse: a device row count needs rows <= %d", WC_MAX_STEP_ROWS);
   auto s = reinterpret_cast<hipStream_t>(stream);
   const int nf = dims->num_features, Dt = dims->target_hidden;
+  const DrafterWs ws = drafter_ws(*dims, workspace);  // NULL workspace: no k split
   for (int t0 = 0; t0 < rows; t0 += WC_MAX_STEP_ROWS) {
     const int tr = std::min(WC_MAX_STEP_ROWS, rows - t0);
     GemvArgs g = gemv_defaults();
+    g.gs_part = ws.gs_part;
+    g.gs_ctr = ws.gs_ctr;
     g.n_in = nf;
     for (int f = 0; f < nf; ++f) {
       WC_REQUIRE(taps[f] != nullptr && al16(taps[f]), "wc_drafter_fuse: tap %d is NULL or not 16-byte aligned", f);
@@ -602,6 +716,8 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
 
       // 1. QKV (dual stream on layers with the token embedding)
       GemvArgs q = gemv_defaults();
+      q.gs_part = ws.gs_part;
+      q.gs_ctr = ws.gs_ctr;
       q.in[0] = xin;
       q.in[0].gain = u16(L.in_norm);
       q.ldw[0] = d.hidden;
@@ -671,6 +787,8 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
 
       // 3. o_proj with the residual: h1 = h + W_o . o
       GemvArgs o = gemv_defaults();
+      o.gs_part = ws.gs_part;
+      o.gs_ctr = ws.gs_ctr;
       o.in[0].x = ws.attn;
       o.in[0].ld = H * D;
       o.in[0].dtype = WC_F32;
@@ -694,6 +812,8 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
 
       // 4. gate / up with SiLU(gate) * up
       GemvArgs gu = gemv_defaults();
+      gu.gs_part = ws.gs_part;
+      gu.gs_ctr = ws.gs_ctr;
       gu.in[0].x = ws.h1;
       gu.in[0].ld = d.hidden;
       gu.in[0].dtype = WC_F32;
@@ -714,6 +834,8 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
 
       // 5. down with the residual; the last layer also writes out = RMSNorm(h)
       GemvArgs dn = gemv_defaults();
+      dn.gs_part = ws.gs_part;
+      dn.gs_ctr = ws.gs_ctr;
       dn.in[0].x = ws.act;
       dn.in[0].ld = d.inter;
       dn.in[0].dtype = WC_F32;

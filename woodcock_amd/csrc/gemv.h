@@ -95,6 +95,10 @@ struct GemvArgs {
   const int32_t* adv_src;                  // *adv_dst = *adv_src + adv_add + (m rows) when adv_dst != NULL
   int adv_add;
   int32_t* adv_dst;
+  // staged few-row kernel split over k: per (tile, piece) partials and per-tile
+  // counters (zero on entry and exit); NULL = no split
+  float* gs_part;
+  unsigned int* gs_ctr;
   // one-row kernel: the normalised input segment 0 (x * gain / rms) written to
   // xn_out at the input's row index by block 0 (the drafter output `out`)
   float* xn_out;

@@ -45,6 +45,29 @@ __device__ __forceinline__ void gf_split3(const float* x, gfbf16x8& hi, gfbf16x8
                                                gf_pack2(r2[4], r2[5]), gf_pack2(r2[6], r2[7])));
 }
 
+// K of input segment s (run time) by selects over the arguments' constant
+// offsets: a run-time index into a register array would move the array to
+// scratch memory, where every use waits on a load
+template <int NIN>
+__device__ __forceinline__ int gf_seg_k(const GemvArgs& a, int s) {
+  int k = a.in[0].K;
+  if constexpr (NIN > 1) k = s == 1 ? a.in[1].K : k;
+  if constexpr (NIN > 2) k = s == 2 ? a.in[2].K : k;
+  return k;
+}
+template <int NIN>
+__device__ __forceinline__ int gf_seg_upr(const GemvArgs& a, int s, int unit) {
+  return (gf_seg_k<NIN>(a, s) + unit - 1) / unit;
+}
+// start of segment s in the staged inputs [segment][M][K]
+template <int NIN>
+__device__ __forceinline__ int gf_seg_off(const GemvArgs& a, int s) {
+  int o = 0;
+  if constexpr (NIN > 1) o = s >= 1 ? a.M * a.in[0].K : o;
+  if constexpr (NIN > 2) o = s >= 2 ? a.M * (a.in[0].K + a.in[1].K) : o;
+  return o;
+}
+
 // Registers of one k step in flight: TW weight fragments, the lane's 8 inputs
 // (fp32: two vectors; bf16: the first) and 8 gains.
 template <int TW>
@@ -187,8 +210,9 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
         u -= a.M * upr[s];
         us = s + 1;
       }
-    um = u / upr[us];
-    uk0 = (u % upr[us]) * kGfUnit;
+    const int up = gf_seg_upr<NIN>(a, us, kGfUnit);
+    um = u / up;
+    uk0 = (u % up) * kGfUnit;
   };
   auto stage_issue = [&](int u) {
     int us, um, uk0;
@@ -227,7 +251,7 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
         for (int e = 0; e < 4; ++e) t2 = fmaf(x[e], x[e], t2);
         const float4 v = make_float4(x[0] * bf16_lo(sg[c].x), x[1] * bf16_hi(sg[c].x), x[2] * bf16_lo(sg[c].y),
                                      x[3] * bf16_hi(sg[c].y));
-        *reinterpret_cast<float4*>(g_xs + soff[us] + um * K + k) = v;
+        *reinterpret_cast<float4*>(g_xs + gf_seg_off<NIN>(a, us) + um * K + k) = v;
       }
     }
     t2 = wave_sum_dpp(t2);
@@ -283,10 +307,14 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
     for (int u = 0; u < kGfD; ++u)
       if (i0 + u < i1) {
         GF_SEG(i0 + u, s_, j_);
+        // one load per segment branch: a select between the segments' row
+        // pointers is folded into a runtime index of wrow, which then lives in
+        // scratch memory and every weight load waits on a scratch load
 #pragma unroll
         for (int tt = 0; tt < TW; ++tt) {
-          const uint16_t* wp = s_ == 0 ? wrow[0][tt] : (s_ == 1 ? wrow[NIN > 1 ? 1 : 0][tt] : wrow[NIN > 2 ? 2 : 0][tt]);
-          ring[u].w[tt] = *reinterpret_cast<const uint4*>(wp + j_ * 32);
+          if (s_ == 0) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[0][tt] + j_ * 32);
+          if constexpr (NIN > 1) if (s_ == 1) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[1 < NIN ? 1 : 0][tt] + j_ * 32);
+          if constexpr (NIN > 2) if (s_ == 2) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[2 < NIN ? 2 : 0][tt] + j_ * 32);
         }
       }
     for (int u = u_first; u < units; u += kGfWaves) {
@@ -300,7 +328,8 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
       if (m < a.M) {
         int base = 0;
         for (int s2 = 0; s2 < sgi; ++s2) base += a.M * upr[s2];
-        for (int q = 0; q < upr[sgi]; ++q) tot += s_ssu[base + m * upr[sgi] + q];
+        const int up = gf_seg_upr<NIN>(a, sgi, kGfUnit);
+        for (int q = 0; q < up; ++q) tot += s_ssu[base + m * up + q];
       }
       s_inv[sgi][m] = a.in[sgi].gain ? 1.f / sqrtf(tot / static_cast<float>(a.in[sgi].K) + a.eps) : 1.f;
     }
@@ -334,6 +363,7 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
 
   // partial tiles and sums of squares -> LDS (STG: over the staged x, so every
   // wave's last reads of it come first)
+  mfma_settle();
   if constexpr (STG) __syncthreads();
 #pragma unroll
   for (int s = 0; s < NIN; ++s) {
@@ -384,6 +414,398 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
   // the cache offset advance of the last projection (no block reads it here)
   if (a.adv_dst && blockIdx.x == 0 && t == 0) *a.adv_dst = *a.adv_src + a.adv_add + m_live;
   if (a.epi == kEpiArgmax) argmax_epilogue<kMaxM>(a, m_live, s_key);
+}
+
+// ------------------------------------------------------------------ staged, every step in flight
+//
+// k_gemvs: the staged few-row MFMA GEMV with every weight step of a wave
+// requested at once (D >= the wave's share of the block's k steps; larger
+// shares go in chunks of D).  Block (tile, piece): W waves on one 16-row tile
+// (TW = 1), two tiles or a gate / up tile pair (TW = 2), over one part of one
+// input segment: piece = segment * P + part, P = gridDim.y / NIN parts per
+// segment.  The block stages its part of the M input rows once in dynamic LDS
+// as fp32 x * gain ([m][part K + 4]) with their sums of squares and
+// accumulates one MFMA tile per output tile, so a block never chooses between
+// accumulators at run time (a branch-selected accumulator was shuffled through
+// copies that read MFMA results early: wrong rows 2-3 of the tiles).  With
+// one piece the block applies the RMS scale itself; otherwise every piece
+// publishes its partial tile and sums of squares and the last block of the
+// tile to finish adds them in piece order, applying each segment's scale
+// (deterministic; the counter resets itself).  Nothing waits on a device
+// value (row count, row index) before the weight loads are issued.
+constexpr int kGsUnit = 1024;               // staged elements per (wave, unit): 4 four-element chunks per lane
+constexpr int kGsMaxUnits = 16 * 10;        // rows x units per row (a part of K <= 10240)
+constexpr int kGsPieceFloats = 1024;        // published per (tile, piece): tile(s) [row][m], then sums [m]
+constexpr int kGsMaxPieces = 4096;          // tiles x pieces of one split launch
+
+// Stage unit u (row um, span from ue0) of one segment: BF = bf16 input,
+// GN = normed (gain); every load issued back to back, addresses clamped.
+template <bool BF, bool GN>
+__device__ __forceinline__ void gs_stage_issue(const void* x, int64_t xr, const uint16_t* gain, int ue0, int pk1,
+                                               uint4* sx, uint2* sg) {
+  const int lane = threadIdx.x % kWave;
+  constexpr int kCh = kGsUnit / (4 * kWave);
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int k = min(ue0 + (lane + c * kWave) * 4, pk1 - 4);
+    if constexpr (BF) {
+      const uint2 h = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(x) + xr + k);
+      sx[c] = make_uint4(h.x, h.y, 0u, 0u);
+    } else {
+      sx[c] = *reinterpret_cast<const uint4*>(static_cast<const float*>(x) + xr + k);
+    }
+    if constexpr (GN) sg[c] = *reinterpret_cast<const uint2*>(gain + k);
+  }
+}
+template <bool BF, bool GN>
+__device__ __forceinline__ float gs_stage_store(const uint4* sx, const uint2* sg, float* dst, int ue0, int pk0, int pk1) {
+  const int lane = threadIdx.x % kWave;
+  constexpr int kCh = kGsUnit / (4 * kWave);
+  float t2 = 0.f;
+#pragma unroll
+  for (int c = 0; c < kCh; ++c) {
+    const int k = ue0 + (lane + c * kWave) * 4;
+    float x[4];
+    if constexpr (BF) {
+      x[0] = bf16_lo(sx[c].x); x[1] = bf16_hi(sx[c].x); x[2] = bf16_lo(sx[c].y); x[3] = bf16_hi(sx[c].y);
+    } else {
+      x[0] = __uint_as_float(sx[c].x); x[1] = __uint_as_float(sx[c].y);
+      x[2] = __uint_as_float(sx[c].z); x[3] = __uint_as_float(sx[c].w);
+    }
+    if (k < pk1) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t2 = fmaf(x[e], x[e], t2);
+      float4 v = make_float4(x[0], x[1], x[2], x[3]);
+      if constexpr (GN) {
+        v.x *= bf16_lo(sg[c].x); v.y *= bf16_hi(sg[c].x); v.z *= bf16_lo(sg[c].y); v.w *= bf16_hi(sg[c].y);
+      }
+      *reinterpret_cast<float4*>(dst + (k - pk0)) = v;
+    }
+  }
+  return wave_sum_dpp(t2);
+}
+
+template <int TW, int W, int D, bool PAIR, int NIN, int XB, int GB, bool GRP = false>
+__global__ __launch_bounds__(W * kWave) void k_gemvs(GemvArgs a) {
+  static_assert(!PAIR || TW == 2, "the pair epilogue takes a gate tile and an up tile");
+  static_assert(!GRP || (NIN > 1 && W % NIN == 0), "wave groups: one group of W / NIN waves per segment");
+  static_assert(NIN >= 1 && NIN <= 3, "one to three input segments");
+  static_assert(GB == 0 || GB == (1 << NIN) - 1, "every segment normed or none");
+  constexpr bool kGain = GB != 0;
+  constexpr int kT = W * kWave;
+  constexpr int RB = PAIR ? 16 : 16 * TW;  // logical output rows per block
+  constexpr int kTiles = PAIR ? 2 : 1;     // published tiles per piece (gate, up)
+  static_assert(RB * kMaxM <= kT, "one output per thread");
+  static_assert(kTiles * RB * kMaxM + kMaxM <= kGsPieceFloats, "piece fits its slot");
+  extern __shared__ __attribute__((aligned(16))) float g_x[];  // [M][xs]; after the main loop: partial tiles
+  __shared__ float s_ssu[kGsMaxUnits];
+  __shared__ float s_ss[NIN][16];
+  __shared__ float s_inv[NIN][16];
+  __shared__ unsigned long long s_key[kGemvWaves][kMaxM];
+  __shared__ bool s_last;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int lm = lane % 16, kg = lane / 16;
+  const int row0 = blockIdx.x * RB;
+  const int M = a.M;
+  // GRP: the block takes every segment whole, a group of W / NIN waves each;
+  // else piece blockIdx.y = segment * P + part with all W waves on it
+  constexpr int kWg = GRP ? W / NIN : W;  // waves on one segment
+  const int KS = GRP ? 1 : gridDim.y, piece = GRP ? 0 : blockIdx.y, P = GRP ? 1 : KS / NIN;
+  const int seg = GRP ? wave / kWg : piece / P, part = GRP ? 0 : piece - seg * P;
+  const int wv = GRP ? wave - seg * kWg : wave;  // wave within its segment group
+  constexpr int S1 = NIN > 1 ? 1 : 0, S2 = NIN > 2 ? 2 : 0;
+
+  // this block's segment: every argument read at a constant offset, then
+  // chosen by value (a segment struct picked by reference at run time turns
+  // into chains of dependent argument loads)
+  const void* sgx = a.in[0].x;
+  int64_t sgld = a.in[0].ld;
+  const int32_t* sgidx = a.in[0].row_idx;
+  int sgadd = a.in[0].row_add, sgmax = a.in[0].max_row, K = a.in[0].K;
+  const uint16_t* sgain = a.in[0].gain;
+  int64_t ldw = a.ldw[0];
+  if constexpr (NIN > 1) {
+    const bool c = seg == 1;
+    sgx = c ? a.in[S1].x : sgx;
+    sgld = c ? a.in[S1].ld : sgld;
+    sgidx = c ? a.in[S1].row_idx : sgidx;
+    sgadd = c ? a.in[S1].row_add : sgadd;
+    sgmax = c ? a.in[S1].max_row : sgmax;
+    K = c ? a.in[S1].K : K;
+    sgain = c ? a.in[S1].gain : sgain;
+    ldw = c ? a.ldw[S1] : ldw;
+  }
+  if constexpr (NIN > 2) {
+    const bool c = seg == 2;
+    sgx = c ? a.in[S2].x : sgx;
+    sgld = c ? a.in[S2].ld : sgld;
+    sgidx = c ? a.in[S2].row_idx : sgidx;
+    sgadd = c ? a.in[S2].row_add : sgadd;
+    sgmax = c ? a.in[S2].max_row : sgmax;
+    K = c ? a.in[S2].K : K;
+    sgain = c ? a.in[S2].gain : sgain;
+    ldw = c ? a.ldw[S2] : ldw;
+  }
+  const bool bf = (XB >> seg) & 1;
+  const int ns = K / 32;
+  const int pp = (ns + P - 1) / P;
+  const int j0 = min(ns, part * pp), j1 = min(ns, j0 + pp);
+  const int xs = (j1 - j0) * 32 + 4;
+  const int per = (j1 - j0 + kWg - 1) / kWg;
+  const int i0 = min(j1, j0 + wv * per), i1 = min(j1, i0 + per);
+  // GRP: segment s's rows after segment s - 1's in LDS (equal row strides not assumed)
+  const int K0a = a.in[0].K, K1a = NIN > 1 ? a.in[S1].K : 0;
+  float* const gx_seg = g_x + (GRP ? (seg == 0 ? 0 : (seg == 1 ? M * (K0a + 4) : M * (K0a + 4 + K1a + 4))) : 0);
+  float* const ssu = s_ssu + (GRP ? seg * (kGsMaxUnits / NIN) : 0);
+  const int ilast = max(i1 - 1, 0);
+
+  // per-lane weight rows of the segment (clamped into the matrix): the row
+  // segments' bases of this input segment, then selects per lane (plain
+  // values, no captured locals: a select between locals held in memory turns
+  // into an indexed scratch load)
+  const uint16_t* wr0;
+  const uint16_t* wr1;
+  {
+    const uint16_t* B0 = a.w[0][0];
+    const uint16_t* B1 = a.w[1][0];
+    const uint16_t* B2 = a.w[2][0];
+    if constexpr (NIN > 1) {
+      B0 = seg == 1 ? a.w[0][S1] : B0;
+      B1 = seg == 1 ? a.w[1][S1] : B1;
+      B2 = seg == 1 ? a.w[2][S1] : B2;
+    }
+    if constexpr (NIN > 2) {
+      B0 = seg == 2 ? a.w[0][S2] : B0;
+      B1 = seg == 2 ? a.w[1][S2] : B1;
+      B2 = seg == 2 ? a.w[2][S2] : B2;
+    }
+    const int nseg = a.n_seg, ss1 = a.seg_start[1], ss2 = a.seg_start[2];
+    const int n0 = min(row0 + lm, a.N - 1);
+    if constexpr (PAIR) {
+      wr0 = B0 + static_cast<int64_t>(n0) * ldw + kg * 8;
+      wr1 = B1 + static_cast<int64_t>(n0) * ldw + kg * 8;
+    } else {
+      const bool a1 = nseg > 1 && n0 >= ss1, a2 = nseg > 2 && n0 >= ss2;
+      const uint16_t* ba = a2 ? B2 : (a1 ? B1 : B0);
+      const int sa = a2 ? ss2 : (a1 ? ss1 : 0);
+      wr0 = ba + static_cast<int64_t>(n0 - sa) * ldw + kg * 8;
+      const int n1 = min(row0 + 16 + lm, a.N - 1);
+      const bool b1 = nseg > 1 && n1 >= ss1, b2 = nseg > 2 && n1 >= ss2;
+      const uint16_t* bb = b2 ? B2 : (b1 ? B1 : B0);
+      const int sb = b2 ? ss2 : (b1 ? ss1 : 0);
+      wr1 = TW > 1 ? bb + static_cast<int64_t>(n1 - sb) * ldw + kg * 8 : wr0;
+    }
+  }
+
+  // staging units: (row, 1024-element span) of the part; the segment's wave wv
+  // takes units wv, wv + its group's waves, ...
+  const int pk0 = j0 * 32, pk1 = j1 * 32;
+  const int upr = (pk1 - pk0 + kGsUnit - 1) / kGsUnit;
+  const int units = M * upr;
+  constexpr int kCh = kGsUnit / (4 * kWave);
+  uint4 sx[kCh];
+  uint2 sg[kCh];
+  auto stage_issue = [&](int u) {
+    const int um = u / upr, ue0 = pk0 + (u - um * upr) * kGsUnit;
+    int xrow = (sgidx ? sgidx[um] : um) + sgadd;
+    if (sgmax > 0) xrow = min(max(xrow, 0), sgmax - 1);
+    const int64_t xr = static_cast<int64_t>(xrow) * sgld;
+    if (bf)
+      gs_stage_issue<true, kGain>(sgx, xr, sgain, ue0, pk1, sx, sg);
+    else
+      gs_stage_issue<false, kGain>(sgx, xr, sgain, ue0, pk1, sx, sg);
+  };
+  auto stage_store = [&](int u) {
+    const int um = u / upr, ue0 = pk0 + (u - um * upr) * kGsUnit;
+    const float t2 = bf ? gs_stage_store<true, kGain>(sx, sg, gx_seg + um * xs, ue0, pk0, pk1)
+                        : gs_stage_store<false, kGain>(sx, sg, gx_seg + um * xs, ue0, pk0, pk1);
+    if (lane == 0) ssu[u] = t2;
+  };
+
+  // 1. staging loads of the first unit (no row index: before the weights, so
+  //    the staging waits on nothing the weights carry), every weight step of
+  //    the first chunk, then the staging loads behind a row index
+  const bool has_idx = sgidx != nullptr;
+  const int u_first = wv;
+  if (!has_idx && u_first < units) stage_issue(u_first);
+  uint4 w[D][TW];
+#pragma unroll
+  for (int u = 0; u < D; ++u) {
+    const int j = min(i0 + u, ilast);
+    w[u][0] = *reinterpret_cast<const uint4*>(wr0 + j * 32);
+    if constexpr (TW > 1) w[u][1] = *reinterpret_cast<const uint4*>(wr1 + j * 32);
+  }
+  if (has_idx && u_first < units) stage_issue(u_first);
+  if (t < kGemvWaves * kMaxM) (&s_key[0][0])[t] = 0ull;
+  // the row count and this thread's residual (output t of the block, if any),
+  // requested behind the weights and used only by the epilogue
+  const int m_live = a.m_dev ? min(max(*a.m_dev, 0), M) : M;
+  float resv = 0.f;
+  if (a.epi == kEpiResidual) resv = res_value(a, min(t / RB, M - 1), min(row0 + t % RB, a.N - 1));
+
+  // 2. x * gain -> LDS with the units' sums of squares; this part's sum of
+  //    squares per row in unit order
+  for (int u = u_first; u < units; u += kWg) {
+    if (u != u_first) stage_issue(u);
+    stage_store(u);
+  }
+  lds_barrier();
+  {
+    const int tg = t - (GRP ? seg * kWg * kWave : 0);  // thread within the segment's group
+    if (tg < 16) {
+      float tot = 0.f;
+      if (tg < M)
+        for (int q = 0; q < upr; ++q) tot += ssu[tg * upr + q];
+      s_ss[GRP ? seg : 0][tg] = tot;
+    }
+  }
+
+  // 3. the k steps: x from LDS (three-term bf16 split), 3 x TW MFMAs per step
+  gff32x4 acc[TW];
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt) acc[tt] = gff32x4{0.f, 0.f, 0.f, 0.f};
+  const float* xrow = gx_seg + min(lm, M - 1) * xs + kg * 8 - pk0;
+  for (int c0 = i0; c0 < i1; c0 += D) {
+    if (c0 != i0) {
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
+        const int j = min(c0 + u, ilast);
+        w[u][0] = *reinterpret_cast<const uint4*>(wr0 + j * 32);
+        if constexpr (TW > 1) w[u][1] = *reinterpret_cast<const uint4*>(wr1 + j * 32);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int j = c0 + u;
+      if (j < i1) {
+        const float4 x0 = *reinterpret_cast<const float4*>(xrow + j * 32);
+        const float4 x1 = *reinterpret_cast<const float4*>(xrow + j * 32 + 4);
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        gfbf16x8 hi, mid, lo;
+        gf_split3(x, hi, mid, lo);
+#pragma unroll
+        for (int tt = 0; tt < TW; ++tt) {
+          const gfbf16x8 wv = __builtin_bit_cast(gfbf16x8, w[u][tt]);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, hi, acc[tt], 0, 0, 0);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, mid, acc[tt], 0, 0, 0);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wv, lo, acc[tt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // 4. partial tiles -> LDS over the staged x (every wave's last reads of it first)
+  mfma_settle();
+  __syncthreads();
+  float(*s_c)[TW][4][kWave] = reinterpret_cast<float(*)[TW][4][kWave]>(g_x);
+#pragma unroll
+  for (int tt = 0; tt < TW; ++tt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s_c[wave][tt][e][lane] = acc[tt][e];
+  __syncthreads();
+
+  // 5. this block's output (row r of the block, input row m), one per thread
+  const int r = t % RB, m = t / RB;
+  const int n = row0 + r;
+  const int tile = PAIR ? 0 : r / 16, ri = r % 16;
+  const int cl = (ri / 4) * 16 + min(m, 15), ce = ri % 4;  // C fragment lane / element of (row ri, column m)
+  // per segment (GRP) or the block's one segment: the waves' partial tiles
+  float pgs[GRP ? NIN : 1], pus[GRP ? NIN : 1];
+#pragma unroll
+  for (int sgi = 0; sgi < (GRP ? NIN : 1); ++sgi) {
+    pgs[sgi] = 0.f;
+    pus[sgi] = 0.f;
+#pragma unroll
+    for (int q = 0; q < kWg; ++q) {
+      pgs[sgi] += s_c[sgi * kWg + q][tile][ce][cl];
+      if (PAIR) pus[sgi] += s_c[sgi * kWg + q][TW - 1][ce][cl];
+    }
+  }
+  const float pg = pgs[0], pu = pus[0];
+  const bool mine = t < RB * M;
+  // the cache offset advance of the last projection, by one block before any
+  // block leaves early (none reads the offset here)
+  if (a.adv_dst && blockIdx.x == 0 && piece == 0 && t == 0) *a.adv_dst = *a.adv_src + a.adv_add + m_live;
+  float g = 0.f, u = 0.f;
+  if (KS > 1) {
+    // hand the piece over: gate [row][m] (pair: then up), then the sums [m]
+    float* pub = a.gs_part + (static_cast<int64_t>(blockIdx.x) * KS + piece) * kGsPieceFloats;
+    if (mine) {
+      publish_f32(pub + r * M + m, pg);
+      if (PAIR) publish_f32(pub + (RB + r) * M + m, pu);
+    }
+    if (t < M) publish_f32(pub + kTiles * RB * M + t, s_ss[0][t]);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t == 0) {
+      unsigned int* ctr = a.gs_ctr + blockIdx.x * kCounterStride;
+      const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                        static_cast<unsigned int>(KS - 1);
+      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // last block of the tile: every piece's partials and sums, in piece order
+    const float* base = a.gs_part + static_cast<int64_t>(blockIdx.x) * KS * kGsPieceFloats;
+    if (t < NIN * 16) {
+      const int sgi = t / 16, mm = t % 16;
+      float tot = 0.f;
+      if (mm < M)
+        for (int q = sgi * P; q < (sgi + 1) * P; ++q) tot += fetch_f32(base + q * kGsPieceFloats + kTiles * RB * M + mm);
+      s_ss[sgi][mm] = tot;
+    }
+    float ps[NIN], us[NIN];
+#pragma unroll
+    for (int sgi = 0; sgi < NIN; ++sgi) {
+      ps[sgi] = 0.f;
+      us[sgi] = 0.f;
+      for (int q = sgi * P; q < (sgi + 1) * P; ++q) {
+        const float* pq = base + q * kGsPieceFloats;
+        ps[sgi] += fetch_f32(pq + r * M + min(m, M - 1));
+        if (PAIR) us[sgi] += fetch_f32(pq + (RB + r) * M + min(m, M - 1));
+      }
+    }
+    __syncthreads();
+    if (t < NIN * 16) {
+      const int sgi = t / 16;
+      const int Ks = sgi == 0 ? a.in[0].K : (sgi == 1 ? a.in[1 < NIN ? 1 : 0].K : a.in[2 < NIN ? 2 : 0].K);
+      s_inv[sgi][t % 16] = ((GB >> sgi) & 1) ? 1.f / sqrtf(s_ss[sgi][t % 16] / static_cast<float>(Ks) + a.eps) : 1.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sgi = 0; sgi < NIN; ++sgi) {
+      g = fmaf(ps[sgi], s_inv[sgi][min(m, 15)], g);
+      u = fmaf(us[sgi], s_inv[sgi][min(m, 15)], u);
+    }
+  } else if constexpr (GRP) {
+    if (t < NIN * 16) {
+      const int sgi = t / 16;
+      const int Ks = sgi == 0 ? a.in[0].K : (sgi == 1 ? a.in[S1].K : a.in[S2].K);
+      s_inv[sgi][t % 16] = kGain ? 1.f / sqrtf(s_ss[sgi][t % 16] / static_cast<float>(Ks) + a.eps) : 1.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sgi = 0; sgi < NIN; ++sgi) {
+      g = fmaf(pgs[sgi], s_inv[sgi][min(m, 15)], g);
+      u = fmaf(pus[sgi], s_inv[sgi][min(m, 15)], u);
+    }
+  } else {
+    if (t < 16) s_inv[0][t] = kGain ? 1.f / sqrtf(s_ss[0][t] / static_cast<float>(K) + a.eps) : 1.f;
+    __syncthreads();
+    g = pg * s_inv[0][min(m, 15)];
+    u = pu * s_inv[0][min(m, 15)];
+  }
+  if (mine && m < m_live && n < a.N) {
+    if (a.epi == kEpiArgmax) {
+      const unsigned long long key = head_key(a, m, n, g);
+      atomicMax(&s_key[0][m], key);
+    } else {
+      store_out<PAIR>(a, m, n, g, u, resv);
+    }
+  }
+  if (a.epi == kEpiArgmax) argmax_epilogue<kMaxM>(a, m_live, s_key);  // one piece per tile (host)
 }
 
 }  // namespace wc

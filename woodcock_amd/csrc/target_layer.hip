@@ -235,6 +235,7 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
   }
 
   // the block's tile -> LDS: row i 16 + 4 (lane / 16) + e, column (w TW + j) 16 + lane % 16
+  mfma_settle();
 #pragma unroll
   for (int j = 0; j < TW; ++j)
 #pragma unroll
@@ -659,6 +660,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
         for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[st], b[kt], sacc[kt], 0, 0, 0);
       }
       // lane holds key kt * 16 + lane % 16 of rows 4 (lane / 16) + e
+      mfma_settle();
       float p[4][4], alpha[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -722,6 +724,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   }
 
   // this split's (m, l, o) per query vector; m back to natural units
+  mfma_settle();
   float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * a.qv_ld * (D + 2);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {

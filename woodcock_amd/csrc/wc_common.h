@@ -167,6 +167,18 @@ __device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(unsigned long long& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
 
+// Wait states between the last MFMA of a loop and the first instruction that
+// reads its result registers (LDS / memory stores, VALU): 24, beyond the 19 the
+// longest XDL operation needs.  Issued explicitly after MFMA loops because the
+// compiler's own count has fallen short on gfx950: with ~13 instructions
+// between a v_mfma_f32_16x16x32_bf16 and the ds_write of its result, elements
+// 2-3 of the tile were read stale, differently from run to run.
+__device__ __forceinline__ void mfma_settle() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Workgroup barrier that orders LDS only: global loads in flight stay in flight
 // (the plain __syncthreads() fence would wait for every outstanding load).
 __device__ __forceinline__ void lds_barrier() {
