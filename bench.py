@@ -293,7 +293,7 @@ def bench_gpu(args):
     def draft_probs():
         # the draft distribution q, formed at draft time in a sampling round
         for _ in range(REP):
-            _lib.call("wc_probs_from_logits", ptr(s_dlg), 5, s_dlg.shape[1], s_dlg.stride(0), 1.0, ptr(s_q),
+            _lib.call("wc_probs_from_logits", ptr(s_dlg), 5, s_dlg.shape[1], s_dlg.stride(0), 1.0, 0, 1.0, ptr(s_q),
                       s_q.stride(0), sws, s())
 
     def stochastic():

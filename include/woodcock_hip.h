@@ -116,13 +116,18 @@ typedef struct wc_uniforms {
   int32_t purpose;
 } wc_uniforms;
 
-/* out[r] = softmax(logits[r] / max(T, 1e-6)) in fp32 for r < rows (width n,
- * row strides ld / ld_out floats; rows <= WC_MAX_NODES).  Top-k / top-p are not
- * implemented (no configuration uses them).  Replaces probs_from_logits
+/* The warped sampling distribution, fp32, for r < rows (width n, row strides
+ * ld / ld_out floats; rows <= WC_MAX_NODES): x = logits[r] / max(T, 1e-6); with
+ * 0 < top_k < n every x below the top_k-th largest x drops out (ties with it
+ * stay); out[r] = softmax(x); with top_p < 1 only the entries of the
+ * descending order whose exclusive cumulative mass is below top_p stay (the
+ * first always; among equal values the lower index first), renormalised by
+ * the kept mass in fp64.  top_k = 0 and top_p = 1 switch the warps off;
+ * top_p must lie in (0, 1].  Replaces probs_from_logits
  * (python/woodcock/sampling.py:39-55; src/sampling/sampling.cpp:9-45) and the
  * draft distribution of SpeculativeDecoder._draft_dist (python/woodcock/spec.py:113-125). */
-int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float temperature, float* out,
-                         int64_t ld_out, void* workspace, wc_stream_t stream);
+int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float temperature, int top_k, float top_p,
+                         float* out, int64_t ld_out, void* workspace, wc_stream_t stream);
 
 /* Stochastic chain verification (Leviathan et al. 2023 / Chen et al. 2023) with
  * fp64 decisions: p [rows][ld_p] target probabilities at [x_n, d_1..d_K]

@@ -16,10 +16,17 @@ import numpy as np
 # ------------------------------------------------------------------ distributions
 
 def probs_from_logits(logits, temperature: float, top_k: int = 0, top_p: float = 1.0) -> np.ndarray:
-    """Warped float32 distribution over the last axis (sampling.py:39-55).
+    """Warped float32 distribution over the last axis (sampling.py:39-55;
+    sampling.cpp:9-45).
 
-    The reference evaluates this with MLX fp32 primitives; here the same steps
-    run as numpy fp32 (max-shifted exp, normalised by the row sum)."""
+    x = logits / T in fp32; top-k drops every x below the k-th largest x (ties
+    with it stay, sampling.py:41-43); softmax as numpy fp32 (max-shifted exp,
+    normalised by the row sum).  Top-p follows the reference runtime's
+    arithmetic (sampling.cpp:28-44): in descending order (equal values lower
+    index first) an entry stays while the fp64 mass before it is below top_p,
+    and the kept entries are divided by their fp64 sum.  (An fp32 running sum,
+    as the MLX path forms it, drifts by ~1e-4 over a 10^5-entry row, more than
+    the entries at the boundary.)"""
     x = np.asarray(logits, dtype=np.float32) / np.float32(max(temperature, 1e-6))
     if top_k and top_k < x.shape[-1]:
         kth = np.sort(x, axis=-1)[..., -top_k][..., None]
@@ -28,12 +35,15 @@ def probs_from_logits(logits, temperature: float, top_k: int = 0, top_p: float =
     p = (e / e.sum(axis=-1, keepdims=True)).astype(np.float32)
     if top_p < 1.0:
         order = np.argsort(-p, axis=-1, kind="stable")
-        srt = np.take_along_axis(p, order, axis=-1)
-        keep_sorted = (np.cumsum(srt, axis=-1) - srt) < top_p  # the first entry is always kept
+        srt = np.take_along_axis(p, order, axis=-1).astype(np.float64)
+        before = np.cumsum(srt, axis=-1) - srt
+        before[..., 1:] = np.cumsum(srt, axis=-1)[..., :-1]  # the exclusive sums themselves, not a difference
+        before[..., 0] = 0.0
+        keep_sorted = before < top_p  # the first entry is always kept
         keep = np.zeros_like(p, dtype=bool)
         np.put_along_axis(keep, order, keep_sorted, axis=-1)
-        p = np.where(keep, p, np.float32(0))
-        p = (p / p.sum(axis=-1, keepdims=True)).astype(np.float32)
+        kept = np.where(keep, p, np.float32(0)).astype(np.float64)
+        p = (kept / kept.sum(axis=-1, keepdims=True)).astype(np.float32)
     return p
 
 

@@ -1,7 +1,10 @@
 """Stochastic chain verification and the temperature softmax on the GPU.
 
 - probabilities: GPU softmax(logits / T) against the oracle's fp32 restatement
-  of probs_from_logits (python/woodcock/sampling.py:39-45), rtol 2e-6;
+  of probs_from_logits (python/woodcock/sampling.py:39-45), rtol 2e-6; top-k /
+  top-p warping (sampling.py:41-54, sampling.cpp:9-45): the kept set equal to the
+  oracle's and to the reference runtime's outputs, values within fp32 rounding,
+  ties at both boundaries;
 - decisions: the accept/reject walk, the uniform count and the emitted token
   equal the oracle's engine-level round (verify_tree_stochastic on the chain,
   python/woodcock/spec.py:316-324) fed the same fp32 p and q and the same
@@ -28,6 +31,8 @@ from woodcock_amd.runtime import new_verdict, ptr
 from woodcock_amd.sampling import PhiloxStream, probs_from_logits, verify_chain_stochastic, verify_chain_stochastic_dev
 from woodcock_amd.synthetic import draw_rows, stochastic_workload
 
+from conftest import load_golden
+
 pytestmark = pytest.mark.gpu
 
 K, V, H = 5, 151936, 16384
@@ -53,6 +58,65 @@ def test_probs_match_oracle(workload, temperature):
         want = S.probs_from_logits(host, temperature)
         np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-12)
         np.testing.assert_allclose(got.sum(-1), 1.0, rtol=1e-5)
+
+
+@pytest.mark.parametrize("temperature,top_k,top_p", [(1.0, 40, 1.0), (0.7, 0, 0.9), (1.0, 50, 0.8), (0.5, 2000, 0.95),
+                                                     (1.0, 1, 1.0), (1.0, 0, 1e-3)])
+def test_warped_probs_match_oracle(workload, temperature, top_k, top_p):
+    """Top-k / top-p on the full target rows [6, 151936] and the draft rows
+    [5, 16384]: the kept set equals the oracle's exactly, the values within fp32
+    rounding (fp64 kept mass against numpy's fp32 sum)."""
+    from woodcock_amd.sampling import SamplingParams
+
+    lg, dl, _, tl, dlg, _, _, _ = workload
+    sp = SamplingParams(temperature=temperature, top_k=top_k, top_p=top_p)
+    for host, dev in ((lg, tl), (dl, dlg)):
+        got = probs_from_logits(dev, sp).cpu().numpy()
+        want = S.probs_from_logits(host, temperature, top_k, top_p)
+        np.testing.assert_array_equal(got > 0, want > 0)
+        np.testing.assert_allclose(got, want, rtol=4e-6, atol=1e-12)
+        np.testing.assert_allclose(got.sum(-1), 1.0, rtol=1e-5)
+
+
+def test_warped_probs_match_reference_cpp(cuda):
+    """The reference's own probs_from_logits outputs (sampling.cpp:9-45) for
+    temperature, top-k and top-p cases (tests/golden/verify.npz)."""
+    from woodcock_amd.sampling import SamplingParams
+
+    z = load_golden("verify.npz")
+    for c in range(5):
+        T, k, p = z[f"p{c}.args"].tolist()
+        x = torch.from_numpy(z[f"p{c}.z"][None]).to(cuda)
+        got = probs_from_logits(x, SamplingParams(temperature=T, top_k=int(k), top_p=p)).cpu().numpy()[0]
+        np.testing.assert_array_equal(got > 0, z[f"p{c}.p"] > 0)
+        np.testing.assert_allclose(got, z[f"p{c}.p"], rtol=4e-6, atol=1e-9)
+
+
+def test_warping_ties_and_edges(cuda):
+    """Ties at the top-k boundary all stay (x < the k-th largest drops out); at
+    the top-p boundary equal values stay lowest index first (four-way, ten-way
+    and thousand-way ties); top_p = 0 is rejected."""
+    from woodcock_amd.sampling import SamplingParams
+
+    rows = np.full((4, 3000), -2.0, np.float32)
+    rows[0, [7, 100, 2999, 5]] = 3.0            # four-way tie for the top
+    rows[1, :10] = 0.0                          # ten equal leaders
+    rows[1, 10:] = -30.0
+    rows[2, ::3] = 1.0                          # a thousand equal entries
+    rows[3] = np.linspace(-1, 1, 3000, dtype=np.float32)
+    x = torch.from_numpy(rows).to(cuda)
+    for sp in (SamplingParams(1.0, top_k=2), SamplingParams(1.0, top_k=4), SamplingParams(1.0, top_p=0.35),
+               SamplingParams(0.3, top_k=1000, top_p=0.3005), SamplingParams(1.0, top_p=1.0)):
+        got = probs_from_logits(x, sp).cpu().numpy()
+        want = S.probs_from_logits(rows, sp.temperature, sp.top_k, sp.top_p)
+        np.testing.assert_array_equal(got > 0, want > 0)
+        np.testing.assert_allclose(got, want, rtol=4e-6, atol=1e-12)
+    got = probs_from_logits(x[:1], SamplingParams(1.0, top_k=2)).cpu().numpy()[0]
+    assert sorted(np.flatnonzero(got).tolist()) == [5, 7, 100, 2999]
+    got = probs_from_logits(x[1:2], SamplingParams(1.0, top_p=0.35)).cpu().numpy()[0]
+    assert np.flatnonzero(got).tolist() == [0, 1, 2, 3]  # ceil(0.35 / 0.1) of the ten, lowest index first
+    with pytest.raises(ValueError):
+        probs_from_logits(x, SamplingParams(1.0, top_p=0.0))
 
 
 def test_probs_small_width_and_stride(cuda):

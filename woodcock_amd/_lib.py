@@ -103,7 +103,7 @@ _SIGS = {
     "wc_drafter_forward": ([P, P, P, P, I64, P, C.c_int, C.c_int, P, P, P, C.c_int, C.c_int, P, C.c_int, P, P, I64,
                             P, P, P, P, P], C.c_int),
     "wc_draft_head": ([P, P, P, I64, P, C.c_int, C.c_int, P, I64, P, P, P, P, P], C.c_int),
-    "wc_probs_from_logits": ([P, C.c_int, C.c_int, I64, C.c_float, P, I64, P, P], C.c_int),
+    "wc_probs_from_logits": ([P, C.c_int, C.c_int, I64, C.c_float, C.c_int, C.c_float, P, I64, P, P], C.c_int),
     "wc_verify_chain_stochastic": ([P, C.c_int, C.c_int, I64, P, C.c_int, I64, P, P, P, P, P, P, P], C.c_int),
     "wc_verify_chain_stochastic_logits": ([P, C.c_int, C.c_int, I64, C.c_float, P, C.c_int, I64, P, P, P, P, P, P,
                                            P], C.c_int),

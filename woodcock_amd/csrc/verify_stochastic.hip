@@ -1571,10 +1571,125 @@ struct ProbsArgs {
   float temperature;
   float* out;
   int64_t ld_out;
-  float* part;  // [rows][kMaxVocabChunks][2]
+  float* part;               // [rows][kMaxVocabChunks][2]
+  const uint32_t* kth_key;   // top-k: per row, the order key of the k-th largest scaled logit (NULL: off)
 };
 
 __device__ __forceinline__ float scaled(const ProbsArgs& a, float v) { return v / a.temperature; }
+// scaled logit x of entry i (in range), or -inf when top-k drops it (x below the k-th largest)
+__device__ __forceinline__ float warped(const ProbsArgs& a, int r, float raw) {
+  const float x = scaled(a, raw);
+  return a.kth_key && float_order(x) < a.kth_key[r] ? -INFINITY : x;
+}
+
+// ------------------------------------------------------------------ top-k / top-p warping
+//
+// Radix select over 32-bit order keys in three digit passes (11, 11, 10 bits),
+// one block per row: each pass histograms the digit of the keys that match the
+// digits fixed so far, weighted by 1 (top-k) or by the value (top-p, fp64
+// sums), and fixes the digit of the bin where the weight of all larger keys
+// first reaches the target.  Finds the k-th largest key exactly; for top-p the
+// key t of the entry whose inclusive descending-order mass first reaches top_p,
+// with the mass G above it and the count of entries equal to it.
+constexpr int kRsBins = 2048;
+constexpr int kRsPerThread = kRsBins / kStThreads;  // bins per thread
+
+// One pass: digit of the crossing bin; `need` (weight still to cover) and
+// `above` (weight of larger keys) are updated.  TOPP: key = bits(p), weight p;
+// else key = float_order(logit / T) (the division the softmax kernels use),
+// weight 1.  When fp64 rounding leaves the crossing just past the last
+// nonempty bin (top-p only), that bin is taken: every remaining entry stays.
+// s_w: kStThreads / kWave + 2 doubles.
+template <bool TOPP>
+__device__ uint32_t rs_pass(const float* row, int n, float temp, int shift, int bits, uint32_t prefix,
+                            uint32_t pmask, double& need, double& above, double* s_mass, unsigned* s_cnt,
+                            double* s_w, uint32_t* s_digit) {
+  const int t = threadIdx.x;
+  const uint32_t nb = 1u << bits;
+  for (int b = t; b < kRsBins; b += kStThreads) {
+    s_mass[b] = 0.0;
+    s_cnt[b] = 0u;
+  }
+  __syncthreads();
+  for (int i = t; i < n; i += kStThreads) {
+    const float v = row[i];
+    const uint32_t key = TOPP ? __float_as_uint(v) : float_order(v / temp);
+    if ((key & pmask) == prefix) {
+      const uint32_t d = (key >> shift) & (nb - 1);
+      if (TOPP) atomicAdd(&s_mass[d], static_cast<double>(v));
+      else atomicAdd(&s_cnt[d], 1u);
+    }
+  }
+  __syncthreads();
+  // thread t holds bins nb - 1 - (t * per + j), j = 0 .. per - 1 (largest keys first)
+  const int per = (static_cast<int>(nb) + kStThreads - 1) / kStThreads;
+  double w[kRsPerThread];
+  double own = 0.0;
+#pragma unroll
+  for (int j = 0; j < kRsPerThread; ++j) {
+    const int b = static_cast<int>(nb) - 1 - (t * per + j);
+    w[j] = (j < per && b >= 0) ? (TOPP ? s_mass[b] : static_cast<double>(s_cnt[b])) : 0.0;
+    own += w[j];
+  }
+  constexpr int kSlot = kStThreads / kWave;
+  if (t == 0) s_digit[0] = 0xffffffffu;  // no crossing yet (ordered by the scan's barriers)
+  double c = block_excl_scan(own, 0.0, s_w);  // weight of every bin above this thread's
+#pragma unroll
+  for (int j = 0; j < kRsPerThread; ++j) {
+    const int b = static_cast<int>(nb) - 1 - (t * per + j);
+    if (j < per && b >= 0 && c < need && c + w[j] >= need) {
+      s_digit[0] = static_cast<uint32_t>(b);
+      s_w[kSlot] = c;  // weight above the chosen bin
+    }
+    c += w[j];
+  }
+  if (t == kStThreads - 1) s_w[kSlot + 1] = c;  // total weight of the pass
+  __syncthreads();
+  if (s_digit[0] == 0xffffffffu) {  // need beyond the total: the lowest nonempty bin
+    __syncthreads();
+    if (t == 0) s_digit[1] = 0xffffffffu;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kRsPerThread; ++j) {
+      const int b = static_cast<int>(nb) - 1 - (t * per + j);
+      if (j < per && b >= 0 && w[j] > 0.0) atomicMin(&s_digit[1], static_cast<uint32_t>(b));
+    }
+    __syncthreads();
+    if (t == 0) {
+      const uint32_t lo = s_digit[1] == 0xffffffffu ? 0u : s_digit[1];
+      s_digit[0] = lo;
+      s_w[kSlot] = s_w[kSlot + 1] - (TOPP ? s_mass[lo] : static_cast<double>(s_cnt[lo]));
+    }
+    __syncthreads();
+  }
+  const uint32_t d = s_digit[0];
+  const double c_above = s_w[kSlot];
+  __syncthreads();
+  need -= c_above;
+  above += c_above;
+  return d;
+}
+
+// top-k: the order key of the k-th largest logit / T of row blockIdx.x
+__global__ __launch_bounds__(kStThreads) void k_topk_key(ProbsArgs a, int k, uint32_t* keys) {
+  __shared__ double s_mass[kRsBins];
+  __shared__ unsigned s_cnt[kRsBins];
+  __shared__ double s_w[kStThreads / kWave + 2];
+  __shared__ uint32_t s_digit[2];
+  const int r = blockIdx.x;
+  const float* row = a.logits + static_cast<int64_t>(r) * a.ld;
+  double need = k, above = 0.0;
+  uint32_t prefix = 0, pmask = 0;
+  const int shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const uint32_t d = rs_pass<false>(row, a.n, a.temperature, shifts[q], widths[q], prefix, pmask, need, above,
+                                      s_mass, s_cnt, s_w, s_digit);
+    prefix |= d << shifts[q];
+    pmask |= ((1u << widths[q]) - 1u) << shifts[q];
+  }
+  if (threadIdx.x == 0) keys[r] = prefix;
+}
 
 // (max, sum of exp(x - max)) of chunk blockIdx.x of row blockIdx.y
 __global__ __launch_bounds__(kStThreads) void k_softmax_part(ProbsArgs a) {
@@ -1590,7 +1705,7 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_part(ProbsArgs a) {
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int x = x0 + e * kStThreads + threadIdx.x;
-    v[e] = x < a.n ? scaled(a, v[e]) : -INFINITY;
+    v[e] = x < a.n ? warped(a, r, v[e]) : -INFINITY;
     m = fmaxf(m, v[e]);
   }
   m = wave_max_dpp(m);
@@ -1646,7 +1761,70 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_write(ProbsArgs a) {
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int x = x0 + e * kStThreads + threadIdx.x;
-    if (x < a.n) orow[x] = expf(scaled(a, raw[e]) - M) / S;
+    const float v = warped(a, r, raw[e]);
+    if (x < a.n) orow[x] = v == -INFINITY ? 0.f : expf(v - M) / S;
+  }
+}
+
+// top-p on the written probabilities of row blockIdx.x, in place: keep the
+// entries of the descending order (ties: lower index first) whose exclusive
+// cumulative mass is below top_p -- every entry above the boundary value t, and
+// of the entries equal to t the first ceil((top_p - G) / t) -- then renormalise
+// by the kept mass (fp64).
+__global__ __launch_bounds__(kStThreads) void k_topp(ProbsArgs a, float top_p) {
+  __shared__ double s_mass[kRsBins];
+  __shared__ unsigned s_cnt[kRsBins];
+  __shared__ double s_w[kStThreads / kWave + 2];
+  __shared__ uint32_t s_digit[2];
+  const int r = blockIdx.x, t = threadIdx.x, n = a.n;
+  float* row = a.out + static_cast<int64_t>(r) * a.ld_out;
+  double need = top_p, above = 0.0;
+  uint32_t prefix = 0, pmask = 0;
+  const int shifts[3] = {21, 10, 0}, widths[3] = {11, 11, 10};
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const uint32_t d =
+        rs_pass<true>(row, n, 1.f, shifts[q], widths[q], prefix, pmask, need, above, s_mass, s_cnt, s_w, s_digit);
+    prefix |= d << shifts[q];
+    pmask |= ((1u << widths[q]) - 1u) << shifts[q];
+  }
+  const uint32_t tk = prefix;  // bits of the boundary value
+  const double tv = static_cast<double>(__uint_as_float(tk)), G = above;
+  // entries equal to t, each thread over a contiguous index range (index order)
+  const int span = (n + kStThreads - 1) / kStThreads;
+  const int b0 = min(n, t * span), b1 = min(n, b0 + span);
+  double eq = 0.0;
+  for (int i = b0; i < b1; ++i) eq += __float_as_uint(row[i]) == tk ? 1.0 : 0.0;
+  double rank = block_excl_scan(eq, 0.0, s_w);
+  __syncthreads();
+  const double keep_eq = tv > 0.0 ? fmax(1.0, ceil((static_cast<double>(top_p) - G) / tv)) : 1.0;
+  double kept = 0.0;
+  for (int i = b0; i < b1; ++i) {
+    const uint32_t k = __float_as_uint(row[i]);
+    bool keep = k > tk;
+    if (k == tk) {
+      keep = rank < keep_eq;
+      rank += 1.0;
+    }
+    if (keep) kept += static_cast<double>(row[i]);
+  }
+  // kept mass: per-thread sums in index order, then the threads in order
+  const double before = block_excl_scan(kept, 0.0, s_w);
+  __syncthreads();
+  __shared__ double s_tot;
+  if (t == kStThreads - 1) s_tot = before + kept;
+  __syncthreads();
+  const double tot = s_tot;
+  rank = block_excl_scan(eq, 0.0, s_w);
+  for (int i = b0; i < b1; ++i) {
+    const float v = row[i];
+    const uint32_t k = __float_as_uint(v);
+    bool keep = k > tk;
+    if (k == tk) {
+      keep = rank < keep_eq;
+      rank += 1.0;
+    }
+    row[i] = keep ? static_cast<float>(static_cast<double>(v) / tot) : 0.f;
   }
 }
 
@@ -1675,10 +1853,13 @@ static int fused_capacity(int* hold) {
 
 extern "C" {
 
-int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float temperature, float* out,
-                         int64_t ld_out, void* workspace, wc_stream_t stream) {
+int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float temperature, int top_k, float top_p,
+                         float* out, int64_t ld_out, void* workspace, wc_stream_t stream) {
   using namespace wc;
   WC_REQUIRE(logits && out, "wc_probs_from_logits: NULL buffer");
+  WC_REQUIRE(top_k >= 0, "wc_probs_from_logits: top_k must be >= 0 (0 = off), got %d", top_k);
+  WC_REQUIRE(top_p > 0.f && top_p <= 1.f, "wc_probs_from_logits: top_p must be in (0, 1] (1 = off), got %g",
+             static_cast<double>(top_p));
   WC_REQUIRE(workspace && aligned(workspace, 16), "wc_probs_from_logits: workspace is NULL or misaligned");
   WC_REQUIRE(rows >= 1 && rows <= WC_MAX_NODES, "wc_probs_from_logits: rows must be in 1..%d (got %d)",
              WC_MAX_NODES, rows);
@@ -1693,12 +1874,23 @@ int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float
   a.out = out;
   a.ld_out = ld_out;
   a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kProbsOff);
+  a.kth_key = nullptr;
   const dim3 grid((n + kVocabChunk - 1) / kVocabChunk, rows);
   auto s = reinterpret_cast<hipStream_t>(stream);
+  if (top_k > 0 && top_k < n) {  // sampling.py:41-43: x < the k-th largest x -> -inf
+    uint32_t* keys = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kWarpOff);
+    hipLaunchKernelGGL(k_topk_key, dim3(rows), dim3(kStThreads), 0, s, a, top_k, keys);
+    WC_LAUNCHED();
+    a.kth_key = keys;
+  }
   hipLaunchKernelGGL(k_softmax_part, grid, dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
   hipLaunchKernelGGL(k_softmax_write, grid, dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
+  if (top_p < 1.f) {  // sampling.py:45-54
+    hipLaunchKernelGGL(k_topp, dim3(rows), dim3(kStThreads), 0, s, a, top_p);
+    WC_LAUNCHED();
+  }
   return WC_OK;
 }
 

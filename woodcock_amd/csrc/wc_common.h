@@ -327,7 +327,10 @@ constexpr size_t kStochDecBytes = 64;
 constexpr int kMailRows = 8, kMailChunks = 256, kMailOther = 64, kMailRep = 4;
 constexpr int kMailArrive = 3 * kMailChunks;
 constexpr size_t kMailSetWords = kMailRep * (kMailRows * kMailChunks + 2 * kMailChunks + kMailOther) + kMailArrive;
-constexpr size_t kGridBarOff = kStochDecOff + kStochDecBytes;
+// top-k warping: the k-th largest scaled logit of each row, as its order key
+constexpr size_t kWarpOff = kStochDecOff + kStochDecBytes;
+constexpr size_t kWarpBytes = 4 * WC_MAX_NODES;
+constexpr size_t kGridBarOff = kWarpOff + kWarpBytes;
 constexpr size_t kGridBarBytes = 2 * 8 * kMailSetWords + 128;
 constexpr size_t kVerifyWorkspace = kGridBarOff + kGridBarBytes;
 inline unsigned int* verify_counter(void* ws, int which) {

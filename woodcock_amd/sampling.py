@@ -92,8 +92,9 @@ def _logits_2d(target_logits: torch.Tensor) -> torch.Tensor:
     if target_logits.dim() != 2 or target_logits.dtype != torch.float32:
         raise ValueError("target logits must be a float32 (rows, vocab) tensor")
     device_of(target_logits)
-    if target_logits.stride(1) != 1:
-        target_logits = target_logits.contiguous()
+    if target_logits.stride(1) != 1 or (target_logits.shape[0] == 1 and target_logits.stride(0) < target_logits.shape[1]):
+        # (one row may carry any stride of its size-1 dimension; the kernels read rows at the stride)
+        target_logits = target_logits.clone(memory_format=torch.contiguous_format)
     return target_logits
 
 
@@ -177,15 +178,18 @@ class PhiloxStream:
 def probs_from_logits(logits: torch.Tensor, sp: SamplingParams | float, out: torch.Tensor | None = None
                       ) -> torch.Tensor:
     """Warped float32 distribution over the last axis (python/woodcock/sampling.py:39-55):
-    softmax(logits / max(T, 1e-6)).  Top-k / top-p raise: no configuration uses them."""
-    t = sp if isinstance(sp, (int, float)) else sp.temperature
-    if not isinstance(sp, (int, float)) and (sp.top_k or sp.top_p < 1.0):
-        raise NotImplementedError("top-k / top-p warping is not implemented on the GPU")
+    softmax(logits / max(T, 1e-6)) after top-k (SamplingParams.top_k > 0: logits
+    below the k-th largest drop out), then top-p (top_p < 1: the smallest
+    descending-order prefix whose mass reaches top_p, renormalised)."""
+    if isinstance(sp, (int, float)):
+        t, top_k, top_p = float(sp), 0, 1.0
+    else:
+        t, top_k, top_p = float(sp.temperature), int(sp.top_k or 0), float(sp.top_p)
     lg = _logits_2d(logits)
     out = torch.empty_like(lg) if out is None else out
     if out.shape != lg.shape or out.dtype != torch.float32 or out.stride(1) != 1:
         raise ValueError("out must be a float32 tensor shaped like logits")
-    _lib.call("wc_probs_from_logits", ptr(lg), lg.shape[0], lg.shape[1], lg.stride(0), float(t), ptr(out),
+    _lib.call("wc_probs_from_logits", ptr(lg), lg.shape[0], lg.shape[1], lg.stride(0), t, top_k, top_p, ptr(out),
               out.stride(0), ptr(workspace(lg.device)), stream_ptr())
     return out
 
@@ -223,8 +227,10 @@ def verify_chain_stochastic_logits_dev(logits: torch.Tensor, temperature: float,
                                        d2t: torch.Tensor | None = None, draft_rows: torch.Tensor | None = None,
                                        verdict: torch.Tensor | None = None) -> torch.Tensor:
     """The stochastic chain rule straight from the target logits (K+1, V):
-    p = softmax(logits / T) is formed inside the two launches and never written
-    (spec.py:316-324); otherwise as verify_chain_stochastic_dev."""
+    p = softmax(logits / T) is formed inside the launch and never written
+    (spec.py:316-324); otherwise as verify_chain_stochastic_dev.  Temperature
+    only: a top-k / top-p target distribution is formed by probs_from_logits
+    and verified by verify_chain_stochastic_dev."""
     lg = _logits_2d(logits)
     rows, vocab = lg.shape
     K = rows - 1

@@ -121,7 +121,7 @@ class TreeDrafter:
                 _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]),
                           hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None,
                           None, ptr(d.ws), s)
-            _lib.call("wc_probs_from_logits", ptr(self.logits), rows, head_rows, self.logits.stride(0), 1.0,
+            _lib.call("wc_probs_from_logits", ptr(self.logits), rows, head_rows, self.logits.stride(0), 1.0, 0, 1.0,
                       ptr(self.q), self.q.stride(0), ptr(workspace(d.device)), s)
             _lib.call("wc_tree_draft_expand", ptr(self.state), ptr(self.q), rows, head_rows, self.q.stride(0),
                       ptr(d._vocab_ids), w, node_base, s)
