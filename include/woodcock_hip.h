@@ -197,6 +197,20 @@ int wc_verify_tree_stochastic(const float* p, int rows, int vocab, int64_t ld_p,
                               const int32_t* tree_parents_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
                               void* workspace, wc_stream_t stream);
 
+/* wc_verify_tree_stochastic for a tree drafted on the device, whose size is
+ * known only there: the node count is *count_dev (1 <= count <= rows; rows
+ * bounds p and the tree arrays), and node v's draft distribution is row
+ * q_rows_dev[v] of q [q_count][ld_q] (0 <= q_rows_dev[v] < q_count, else
+ * status WC_E_INVALID).  Otherwise the same rule, uniforms and outputs.  The
+ * engine's verify step after sampled tree drafting (python/woodcock/spec.py:
+ * 321-324, q = kept[v].q). */
+int wc_verify_tree_stochastic_indexed(const float* p, int rows, int vocab, int64_t ld_p, const float* q,
+                                      int q_count, const int32_t* q_rows_dev, int head_rows, int64_t ld_q,
+                                      const int32_t* d2t_dev, const int32_t* tree_tokens_dev,
+                                      const int32_t* tree_parents_dev, const int32_t* count_dev,
+                                      const wc_uniforms* rng, wc_verdict* verdict_dev, void* workspace,
+                                      wc_stream_t stream);
+
 /* ------------------------------------------------------------------ tree helpers */
 
 /* Attention mask of a verify block holding a flattened draft tree: mask_out
@@ -256,7 +270,12 @@ int wc_tree_draft_expand(void* state, const float* q, int rows, int head_rows, i
  * [rows][mask_ld] over cache slots: the prefix [lo, *offset_dev) with lo from
  * the sliding window (0 = none), the cache slots of the node's ancestors below
  * the root and its own slot *offset_dev + tree_cache + r (spec.py:281-294).
- * The node's feedback row becomes store_base + r. */
+ * The node's feedback row becomes store_base + r.  level_begin = 0 takes the
+ * level that the last wc_tree_draft_expand_sample appended (level_end is then
+ * ignored) and fills rows [frontier size, width) of the outputs with padding
+ * (the root token on feedback row 0 at position *offset_dev, seeing the prefix
+ * and its own slot), so a drafter forward over `width` rows stays valid; the
+ * outputs must hold `width` rows. */
 int wc_tree_draft_frontier(void* state, int level_begin, int level_end, int width, const int32_t* offset_dev,
                            int tree_cache, int window, int store_base, int32_t* tokens_out, int32_t* feat_rows_out,
                            int32_t* positions_out, uint8_t* mask_out, int64_t mask_ld, wc_stream_t stream);
@@ -267,6 +286,43 @@ int wc_tree_draft_frontier(void* state, int level_begin, int level_end, int widt
  * parents remapped (-1 for the root).  *count_out receives the node count. */
 int wc_tree_draft_select(const void* state, int n_nodes, int budget, int32_t* tokens_out, int32_t* parents_out,
                          int32_t* depth_out, int32_t* count_out, wc_stream_t stream);
+
+/* ------------------------------------------------------------------ sampled tree drafting
+ * SpeculativeDecoder._draft at T > 0 (python/woodcock/spec.py:238-249 with
+ * Plan.children_for, policies.py:32-36, and StaticPolicy.select_verify keeping
+ * every node, policies.py:67-69) on the same state: per level the draft head
+ * over the frontier rows, q = wc_probs_from_logits at the temperature (spec.py:
+ * 113-125), wc_tree_draft_expand_sample, and unless it is the last level
+ * wc_tree_draft_frontier with level_begin = 0 plus a drafter forward over
+ * `width` rows; then wc_tree_draft_select_all.  Node counts depend on the
+ * draws, so they stay in the state. */
+
+/* Children of the current frontier (the state's frontier rows, at most `rows`):
+ * frontier row r draws m_r = min(width, budget left after the rows before it)
+ * children -- the number is fixed before drawing; `budget` is the round's
+ * draft budget, shared by every level since wc_tree_draft_begin -- without
+ * replacement from q row r (q [rows][ld_q] over the head rows, renormalised in
+ * fp64; d2t_dev maps head rows to tokens, NULL = identity): the m_r largest
+ * keys log q(i) - log(-log u_i) over the nonzero entries, in descending key
+ * order (the lower head row first on a tie), where u_i is value
+ * v * H4 + i of the Philox stream rng (v the frontier node, H4 = head_rows
+ * rounded up to a multiple of 4).  Children get phat = phat(parent) *
+ * q(i) / sum(q) in fp64 and are appended in frontier order.  Replaces the
+ * per-node sample_without_replacement draws of the drafting loop
+ * (python/woodcock/sampling.py:196-203); each entry owns its uniform instead of
+ * one sequential generator, so every row and part draws at once. */
+int wc_tree_draft_expand_sample(void* state, const float* q, int rows, int head_rows, int64_t ld_q,
+                                const int32_t* d2t_dev, int width, int budget, const wc_uniforms* rng,
+                                wc_stream_t stream);
+
+/* Every node of the table in node order (tokens, parents with -1 for the root,
+ * depth), the row of each node's draft distribution in the caller's q store
+ * (its feedback-store row, where the level's q was written; 0 for nodes never
+ * expanded), and *count_out = the node count; rows [count, max_nodes) are
+ * padding (the root token as a child of the root at depth 1) so a verify block
+ * of max_nodes rows is a valid tree. */
+int wc_tree_draft_select_all(const void* state, int max_nodes, int32_t* tokens_out, int32_t* parents_out,
+                             int32_t* depth_out, int32_t* q_rows_out, int32_t* count_out, wc_stream_t stream);
 
 /* ------------------------------------------------------------------ KV compaction */
 

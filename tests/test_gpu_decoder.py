@@ -15,6 +15,14 @@ against oracle loops built from the CPU restatements.
   (planted along a non-contiguous branch), the compacted target KV, and the
   drafter update from the taps at the kept rows, against the oracle's tree
   drafting, target stack, tree walk and compaction on identical inputs.
+* Sampled rounds at T > 0 (spec.py:187-201 with the stochastic branches
+  238-249 and 320-324) at the same shapes: the drawn tree equals the oracle's
+  sampled drafting on the same Philox stream, the target logits and the
+  warped target distribution (temperature, top-k) match the oracle's, the
+  recursive rejection's path, next token and uniform count equal the oracle
+  rule fed the GPU's p and q rows, and the compaction and drafter update follow
+  the accepted branch.  Through the loop, chains (a width-1 tree) and trees
+  advance every count by the accepted path + 1.
 """
 import numpy as np
 import pytest
@@ -299,3 +307,156 @@ def test_tree_round_through_the_loop(cuda):
         assert dec.n == n0 + res.n_accepted + 1 == dec.rnd.committed()
         assert runner.cache[0].offset == dec.n == dec.rnd.cache[0].offset
         assert res.k == 10 and res.depth == 3
+
+
+def test_sampled_rounds_qwen3_1p7b(cuda):
+    from woodcock_amd import _lib
+    from woodcock_amd.config import qwen3_1p7b_drafter
+    from woodcock_amd.policies import StaticPolicy
+    from woodcock_amd.sampling import SamplingParams
+    from woodcock_amd.spec import PURPOSE_DRAFT, PURPOSE_VERIFY, S_ROUND, SpeculativeDecoder, TargetRunner
+    from woodcock_amd.synthetic import to_bits
+    from woodcock_amd.target import TargetConfig, TargetModel, random_target
+
+    dcfg = qwen3_1p7b_drafter()
+    tcfg = TargetConfig(num_layers=2)
+    ctx, depth, width, budget = 2048, 6, 4, 59
+    cap = ctx + 128
+    feats = (0, 1, 1)
+    # top-k: its boundary is exact on logits / T, so the warped rows can be compared with
+    # the oracle's entry for entry (top-p over a near-flat random-init target would put
+    # thousands of fp32-equal values at the boundary; the warping tests pin top-p)
+    sp = SamplingParams(temperature=0.9, top_k=1000, seed=61)
+    d, od = _drafter(cuda, dcfg, 16384, seed=62)
+    tw = random_target(tcfg, seed=63, device=cuda)
+    model = TargetModel(tcfg, tw, cuda, max_rows=64, feature_layers=feats)
+    tcache = model.make_cache(cap)
+    runner = TargetRunner(model, tcache)
+    policy = StaticPolicy(depth, width, budget)
+    dec = SpeculativeDecoder(d, runner, policy, capacity=cap, k_max=4, max_tree_depth=depth, sampling=sp)
+    oc = od.make_cache(cap, kv_bf16=True)
+    _fill_cache(cuda, dec.rnd.cache, oc, ctx, seed=64)
+    ot = TargetStack(tcfg, {k: to_bits(v) for k, v in tw.items()}, feats, cap, kv_bf16=True)
+    g = torch.Generator(device=cuda).manual_seed(65)
+    for c, o in zip(tcache, ot.caches):
+        c.keys[0, :, :ctx] = torch.randn(c.keys[0, :, :ctx].shape, generator=g, device=cuda).bfloat16()
+        c.values[0, :, :ctx] = torch.randn(c.values[0, :, :ctx].shape, generator=g, device=cuda).bfloat16()
+        o.k[0][:] = to_bits(c.keys[0])
+        o.v[0][:] = to_bits(c.values[0])
+        o.offset = ctx
+    root = torch.randn(1, dcfg.hidden_size, generator=torch.Generator(device=cuda).manual_seed(66), device=cuda)
+    dec.start(ctx, 9000, root)
+    V = _lib
+    d2t = d.vocab_ids.cpu().numpy()
+    rng = np.random.default_rng(67)
+    paths = []
+    for r in range(4):
+        n = dec.n
+        plan = policy.plan(context_len=n, stochastic=True)
+        tree, rows, tdr = dec.enqueue_sampled_draft(plan)
+        logits, taps = dec.enqueue_tree_target(tree, rows)
+        torch.cuda.synchronize()
+        rnd = int(dec.rnd.state[S_ROUND].item())
+        cnt = int(tree.count.item())
+        toks = tree.tokens[:rows].tolist()
+        pars = tree.parents[:rows].tolist()
+        deps = tree.depth[:rows].tolist()
+        root_hid = dec.rnd.upd_hid[int(dec.rnd.verdict[V.V_N_KEEP]) - 1].cpu().numpy()[None]
+        root_out = core.rmsnorm(root_hid, od.w["norm.weight"], dcfg.rms_norm_eps)
+        otree, _, oq = otd.draft_tree_sample(od, oc, dec.x_n, root_out, od.feedback(root_hid, root_out), depth, width,
+                                             budget, sp.temperature, sp.seed, rnd, PURPOSE_DRAFT,
+                                             follow=toks[:cnt])
+        assert (otree.tokens, otree.parents, otree.depth) == (toks[:cnt], pars[:cnt], deps[:cnt]), f"round {r}"
+        assert rows == budget + 1 and cnt == rows
+        pos = np.array([n + dd for dd in deps], np.int32)
+        mask = S.tree_attention_mask(S.DraftTree(toks, pars, deps), n).astype(np.uint8)
+        ologits, otaps = ot.forward(toks, positions=pos, mask=mask)
+        assert _rel(logits.cpu().numpy(), ologits) < 1e-3, f"round {r}"
+        for t, o in zip(taps, otaps):
+            assert _rel(t.cpu().numpy(), o) < 1e-3, f"round {r}"
+        if r % 2 == 0:
+            # even rounds: a target that puts all its mass on a deep, non-contiguous
+            # branch, so the walk accepts it (p(x) = 1 >= q(x)) and the compaction gathers
+            leaves = [v for v in range(rows) if deps[v] >= 3]
+            for v in rng.permutation(leaves):
+                path, u = [], int(v)
+                while u > 0:
+                    path.append(u)
+                    u = pars[u]
+                if path[::-1] != list(range(1, len(path) + 1)):
+                    break
+            path = path[::-1]
+            for u, c in zip([0] + path[:-1], path):
+                logits[u, toks[c]] = 1e4
+            logits[path[-1], 123] = 1e4
+        # GPU: warped target distribution, recursive rejection, compaction, update; one sync
+        p = dec.enqueue_sampled_verify(tdr, tree, logits, rows)
+        dec.rnd.enqueue_tree_commit(taps, rows, plan.max_depth)
+        dec.rnd.enqueue_readback()
+        res = dec.rnd.finish()
+        keep = dec.rnd.last_keep()
+        p_np = p.cpu().numpy()
+        wp = S.probs_from_logits(logits.cpu().numpy(), sp.temperature, sp.top_k, sp.top_p)
+        assert ((p_np > 0) == (wp > 0)).all(), f"round {r}: top-k kept sets differ"
+        assert np.abs(p_np - wp).max() <= 1e-5 * wp.max(), f"round {r}"
+        # the oracle rule on the GPU's p and draft rows
+        qs = tdr.q_store.cpu().numpy()
+        qr = tree.q_rows[:cnt].tolist()
+        tr = S.DraftTree(toks, pars, deps)
+        pd = {v: p_np[v].astype(np.float64) for v in range(rows)}
+        qd = {v: S.scatter_draft_dist(qs[qr[v]], d2t, tcfg.vocab_size) for v in range(rows) if tr.children[v]}
+        for v in qd:
+            assert np.abs(qs[qr[v]] - oq[v]).max() < 1e-2 * oq[v].max(), f"round {r} node {v}"
+        ust = core.UniformStream(sp.seed, rnd, PURPOSE_VERIFY)
+        opath, onext = S.verify_tree_stochastic(pd, qd, tr, ust)
+        v = _lib.Verdict.from_buffer_copy(dec.rnd.host_verdict.numpy().tobytes())
+        assert keep == [0] + opath and res.n_accepted == len(opath), f"round {r}"
+        acc = [toks[u] for u in opath] + [onext]
+        assert res.tokens == acc and int(v.n_uniforms) == ust.pos
+        if r % 2 == 0:
+            assert opath == path and onext == 123, f"round {r}"
+        paths.append(opath)
+        ot.compact(n, keep)
+        for i in range(tcfg.num_layers):
+            gk = tcache[i].keys[0, :, n:n + len(keep)].float().cpu().numpy()
+            assert _rel(gk, ot.caches[i].keys_f32(0)[:, n:n + len(keep)]) < 1e-2, f"round {r} layer {i}"
+        ohid, _ = od.forward(acc, od.fuse([o[keep] for o in otaps]), oc)
+        assert _rel(dec.rnd.upd_hid[len(keep) - 1].cpu().numpy(), ohid[-1]) < 1e-2, f"round {r}"
+        dec.n += len(acc)
+        dec.x_n = acc[-1]
+        assert dec.rnd.committed() == dec.n == oc.offset == ot.offset
+        for i, c in enumerate(dec.rnd.cache):
+            oc.k[i][:] = to_bits(c.keys[0])
+            oc.v[i][:] = to_bits(c.values[0])
+        for i, c in enumerate(tcache):
+            ot.caches[i].k[0][:] = to_bits(c.keys[0])
+            ot.caches[i].v[0][:] = to_bits(c.values[0])
+
+
+@pytest.mark.parametrize("shape", [(4, 1, 4), (3, 3, 10)], ids=["chain", "tree"])
+def test_sampled_rounds_through_the_loop(cuda, shape):
+    from woodcock_amd.config import DrafterConfig
+    from woodcock_amd.drafter import Drafter
+    from woodcock_amd.policies import StaticPolicy
+    from woodcock_amd.sampling import SamplingParams
+    from woodcock_amd.spec import SpeculativeDecoder, TargetRunner
+    from woodcock_amd.synthetic import random_drafter
+    from woodcock_amd.target import TargetConfig, TargetModel, random_target
+
+    dcfg = DrafterConfig(hidden_size=512, num_layers=1, num_heads=4, num_kv_heads=2, head_dim=128,
+                         intermediate_size=1024, vocab_size=1000, target_hidden_size=512)
+    tcfg = TargetConfig(hidden_size=512, num_heads=4, num_kv_heads=2, head_dim=128, intermediate_size=1024,
+                        num_layers=3, vocab_size=1000)
+    d = Drafter(dcfg, random_drafter(dcfg, seed=17, device=cuda), cuda, torch.bfloat16)
+    model = TargetModel(tcfg, random_target(tcfg, seed=18, device=cuda), cuda, max_rows=64, feature_layers=(0, 1, 2))
+    runner = TargetRunner(model, model.make_cache(256))
+    depth, width, budget = shape
+    dec = SpeculativeDecoder(d, runner, StaticPolicy(depth, width, budget), capacity=256, k_max=4,
+                             max_tree_depth=depth, sampling=SamplingParams(temperature=1.0, seed=5))
+    dec.start(20, 5, torch.randn(1, 512, device=cuda))
+    out, st = dec.generate(24)
+    assert len(out) == 24 and st.rounds >= 24 // (depth + 1)
+    assert all(0 <= t < 1000 for t in out)
+    assert dec.rnd.committed() == dec.n == runner.cache[0].offset == dec.rnd.cache[0].offset
+    assert dec.n == 20 + sum(a + 1 for a in st.accepted)
+    assert set(st.drafted) == {budget} and max(st.depths) <= depth

@@ -5,7 +5,16 @@ identical verified trees (tokens, parents, depths, node count), the drafter
 cache offset untouched, and the tree entries written to the drafter cache
 within the fp32 tolerance.  Shapes: a small drafter with an fp32 and a bf16
 cache, and the Qwen3-1.7B drafter with the config-5 tree (depth 6, width 4,
-60 verified rows)."""
+60 verified rows).
+
+Sampled drafting at T > 0 (TreeDrafter(stochastic=True); spec.py:238-249)
+against oracle/tree_draft.draft_tree_sample fed the same Philox stream: the
+same drawn tree (a draw may differ only where two Gumbel keys agree within
+rounding of the fp32 / bf16 forward, and then the GPU's is followed), every
+parent's q row within tolerance at the row the tree names, padding rows
+after the live count, and the shapes where the counts are data-dependent --
+budget-limited levels, a temperature so low that each q has one nonzero entry
+(one child per node instead of `width`), and no budget at all."""
 import numpy as np
 import pytest
 import torch
@@ -111,6 +120,112 @@ def test_enqueue_never_synchronises(cuda):
     torch.cuda.set_sync_debug_mode("error")
     try:
         tdr.draft(tok, root_out, root_out, off)
+    finally:
+        torch.cuda.set_sync_debug_mode(0)
+    torch.cuda.synchronize()
+    assert int(tdr.tree.count.item()) == 9
+
+
+# ------------------------------------------------------------------ sampled drafting (T > 0)
+
+SEED, PURPOSE = 77, 1
+
+
+def _run_sampled(cuda, cfg, head_rows, ctx, cap, kv_dtype, depth, width, budget, seed, temperature, tol, rnd=3):
+    from woodcock_amd import _lib
+    from woodcock_amd.tree_draft import TreeDrafter
+
+    d, cache, od, oc, root_out = _setup(cuda, cfg, head_rows, ctx, cap, kv_dtype, seed)
+    root_tok = 11
+    tdr = TreeDrafter(d, cache, depth, width, budget, stochastic=True)
+    off = torch.tensor([ctx], dtype=torch.int32, device=cuda)
+    rd = torch.tensor([rnd], dtype=torch.int32, device=cuda)
+    tree = tdr.draft(torch.tensor([root_tok], dtype=torch.int32, device=cuda), root_out, root_out, off,
+                     temperature=temperature, rng=_lib.Uniforms(SEED, rd.data_ptr(), PURPOSE))
+    torch.cuda.synchronize()
+    n = int(tree.count.item())
+    toks = tree.tokens.tolist()
+    ro = root_out.cpu().numpy()
+    want, phat, qrow = otd.draft_tree_sample(od, oc, root_tok, ro, ro, depth, width, budget, temperature, SEED, rnd,
+                                             PURPOSE, follow=toks[:n])
+    assert n == len(want) <= tdr.max_nodes
+    assert toks[:n] == want.tokens
+    assert tree.parents[:n].tolist() == want.parents
+    assert tree.depth[:n].tolist() == want.depth
+    pad = tdr.max_nodes - n
+    assert toks[n:] == [root_tok] * pad
+    assert tree.parents[n:].tolist() == [0] * pad and tree.depth[n:].tolist() == [1] * pad
+    assert int(off.item()) == ctx and oc.offset == ctx
+    qr = tree.q_rows[:n].tolist()
+    qs = tdr.q_store.cpu().numpy()
+    for v, qv in qrow.items():  # the rows the verification reads: nodes with children
+        if v in want.parents:
+            assert np.abs(qs[qr[v]] - qv).max() <= tol * qv.max(), f"node {v}"
+    return tdr, tree, want
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.float32, torch.bfloat16])
+def test_sampled_small_tree_matches_oracle(cuda, kv_dtype):
+    for rnd in (1, 2):
+        _, _, t = _run_sampled(cuda, _small_cfg(), 1024, 40, 256, kv_dtype, depth=4, width=3, budget=10, seed=2,
+                               temperature=1.0, tol=1e-5 if kv_dtype == torch.float32 else 1e-2, rnd=rnd)
+        assert len(t) == 11  # 3 + (3 + 3 + 1) draws: the budget runs out in level 2
+
+
+def test_sampled_budget_beyond_the_shape(cuda):
+    # width 2, depth 3: 2 + 4 + 4 draws, budget 20 never binds
+    _, tree, t = _run_sampled(cuda, _small_cfg(), 1024, 24, 128, torch.float32, depth=3, width=2, budget=20, seed=4,
+                              temperature=0.8, tol=1e-5)
+    assert len(t) == 11 and int(tree.count.item()) == 11
+
+
+def test_sampled_one_child_per_node_at_low_temperature(cuda):
+    """T = 1e-6: every q is one-hot, so each node draws one child instead of
+    `width` -- the counts differ from the static shape and the tree is the
+    greedy chain."""
+    _, tree, t = _run_sampled(cuda, _small_cfg(), 1024, 30, 128, torch.float32, depth=4, width=3, budget=12, seed=6,
+                              temperature=1e-6, tol=1e-5)
+    assert t.parents == [-1, 0, 1, 2, 3]
+    _, chain = _run(cuda, _small_cfg(), 1024, 30, 128, torch.float32, depth=4, width=1, budget=4, seed=6,
+                    tol=1e-5)
+    assert tree.tokens[:5].tolist() == chain.tokens[:5].tolist()
+
+
+def test_sampled_zero_budget_is_the_root(cuda):
+    _, tree, t = _run_sampled(cuda, _small_cfg(), 1024, 20, 128, torch.float32, depth=3, width=2, budget=0, seed=5,
+                              temperature=1.0, tol=1e-5)
+    assert len(t) == 1 and int(tree.count.item()) == 1
+
+
+def test_sampled_chain_width_one(cuda):
+    _, tree, t = _run_sampled(cuda, _small_cfg(), 1024, 30, 128, torch.float32, depth=5, width=1, budget=5, seed=7,
+                              temperature=0.7, tol=1e-5)
+    assert t.parents == [-1, 0, 1, 2, 3, 4]
+
+
+def test_sampled_qwen3_1p7b_config5_shape(cuda):
+    from woodcock_amd.config import qwen3_1p7b_drafter
+
+    _, tree, t = _run_sampled(cuda, qwen3_1p7b_drafter(), 16384, 512, 1024, torch.bfloat16, depth=6, width=4,
+                              budget=59, seed=8, temperature=1.0, tol=1e-2)
+    assert len(t) == 60
+
+
+def test_sampled_enqueue_never_synchronises(cuda):
+    from woodcock_amd import _lib
+    from woodcock_amd.tree_draft import TreeDrafter
+
+    d, cache, _, _, root_out = _setup(cuda, _small_cfg(), 1024, 20, 128, torch.float32, 9)
+    tdr = TreeDrafter(d, cache, 3, 3, 8, stochastic=True)
+    tok = torch.tensor([3], dtype=torch.int32, device=cuda)
+    off = torch.tensor([20], dtype=torch.int32, device=cuda)
+    rd = torch.tensor([0], dtype=torch.int32, device=cuda)
+    u = _lib.Uniforms(1, rd.data_ptr(), PURPOSE)
+    tdr.draft(tok, root_out, root_out, off, temperature=1.0, rng=u)  # warm-up
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        tdr.draft(tok, root_out, root_out, off, temperature=1.0, rng=u)
     finally:
         torch.cuda.set_sync_debug_mode(0)
     torch.cuda.synchronize()

@@ -13,10 +13,16 @@
   replacement from q, some tokens outside the draft vocabulary), round by round;
   a chain equals wc_verify_chain_stochastic; the first emitted token follows
   p(root) over 2*10^4 freshly drawn trees (chi-square); a one-node tree samples
-  p[0]; invalid trees raise.
+  p[0]; invalid trees raise;
+- wc_verify_tree_stochastic_indexed (the verify after sampled tree drafting):
+  node v's q at row q_rows[v] of a larger store and the node count read from
+  the device, padding rows after it -- the same outcomes as the oracle; a q
+  row outside the store or a count outside 1..rows is reported.
 Decisions are fp64; sums run in a different order than numpy's, so a decision
 could differ only when a uniform falls within rounding of its threshold.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -25,7 +31,7 @@ from scipy.stats import chisquare
 from oracle import core
 from oracle import sampling as S
 from woodcock_amd import _lib
-from woodcock_amd.runtime import ptr
+from woodcock_amd.runtime import new_verdict, ptr, stream_ptr, workspace
 from woodcock_amd.sampling import (DraftTree, PhiloxStream, probs_from_logits, sample_without_replacement_dev,
                                    tree_attention_mask_dev, verify_chain_stochastic, verify_tree_stochastic,
                                    verify_tree_stochastic_dev)
@@ -224,3 +230,52 @@ def test_invalid_tree_is_reported(workload):
         verify_tree_stochastic(p[:3], q[:3], DraftTree([0, 5, 6], [-1, 2, 0], [0, 1, 1]), PhiloxStream(seed=1), d2)
     with pytest.raises(ValueError):
         verify_tree_stochastic(p[:2], q[:2], DraftTree([0, V + 3], [-1, 0], [0, 1]), PhiloxStream(seed=1), d2)
+
+
+def _indexed(p, store, q_rows, toks, pars, count, rnd, d2):
+    dev = p.device
+    i32 = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
+    rd, cnt, verd = i32([rnd]), i32([count]), new_verdict(dev)
+    qr, tt, pp = i32(q_rows), i32(toks), i32(pars)
+    _lib.call("wc_verify_tree_stochastic_indexed", ptr(p), len(toks), p.shape[1], p.stride(0), ptr(store),
+              store.shape[0], ptr(qr), store.shape[1], store.stride(0), ptr(d2), ptr(tt), ptr(pp), ptr(cnt),
+              C.byref(_lib.Uniforms(SEED, ptr(rd), 0)), ptr(verd), ptr(workspace(dev)), stream_ptr())
+    return verd.cpu().numpy()
+
+
+def test_indexed_rows_and_device_count_equal_oracle(workload):
+    p, q, d2, p_np, q_np, d2t = workload
+    dev = p.device
+    rng = np.random.default_rng(23)
+    store = torch.zeros(40, H, dtype=torch.float32, device=dev)
+    depths = set()
+    for r in range(40):
+        tree = build_tree(int(rng.integers(1, 24)), q_np, d2t, rng, outside_every=9 if r % 4 == 1 else 0)
+        N = len(tree)
+        rows = min(24, N + int(rng.integers(0, 6)))
+        slots = rng.permutation(store.shape[0])[:N]
+        store.zero_()
+        store[torch.from_numpy(slots).to(dev)] = q[:N]
+        pad = rows - N
+        v = _indexed(p[:rows], store, slots.tolist() + [0] * pad, tree.tokens + [tree.tokens[0]] * pad,
+                     tree.parents + [0] * pad, N, r, d2)
+        path, nxt, nu = oracle_tree(p_np, q_np, d2t, tree, r)
+        a = int(v[_lib.V_N_ACCEPTED])
+        assert v[_lib.V_STATUS] == 0
+        got = (v[_lib.V_KEEP + 1:_lib.V_KEEP + 1 + a].tolist(), int(v[_lib.V_NEXT]), int(v[_lib.V_N_UNIFORMS]))
+        assert got == (path, nxt, nu), r
+        depths.add(a)
+    assert len(depths) >= 2, depths
+
+
+def test_indexed_invalid_rows_and_counts_are_reported(workload):
+    p, q, d2, *_ = workload
+    store = q[:4].contiguous()
+    toks, pars = [5, 6, 7], [-1, 0, 0]
+    assert _indexed(p[:3], store, [0, 1, 4], toks, pars, 3, 0, d2)[_lib.V_STATUS] == _lib.WC_E_INVALID
+    assert _indexed(p[:3], store, [0, 1, -1], toks, pars, 3, 0, d2)[_lib.V_STATUS] == _lib.WC_E_INVALID
+    assert _indexed(p[:3], store, [0, 1, 2], toks, pars, 4, 0, d2)[_lib.V_STATUS] == _lib.WC_E_INVALID
+    assert _indexed(p[:3], store, [0, 1, 2], toks, pars, 0, 0, d2)[_lib.V_STATUS] == _lib.WC_E_INVALID
+    # the rows past the count are never looked at, however invalid
+    v = _indexed(p[:3], store, [0, 3, 99], toks, [-1, 0, 7], 2, 0, d2)
+    assert v[_lib.V_STATUS] == 0

@@ -108,6 +108,8 @@ _SIGS = {
     "wc_verify_chain_stochastic_logits": ([P, C.c_int, C.c_int, I64, C.c_float, P, C.c_int, I64, P, P, P, P, P, P,
                                            P], C.c_int),
     "wc_verify_tree_stochastic": ([P, C.c_int, C.c_int, I64, P, C.c_int, I64, P, P, P, P, P, P, P], C.c_int),
+    "wc_verify_tree_stochastic_indexed": ([P, C.c_int, C.c_int, I64, P, C.c_int, P, C.c_int, I64, P, P, P, P, P, P,
+                                           P, P], C.c_int),
     "wc_tree_mask": ([P, C.c_int, C.c_int, P, I64, P], C.c_int),
     "wc_sample_without_replacement": ([P, C.c_int, C.c_int, I64, P, P, C.c_int, P, I64, P, P, P], C.c_int),
     "wc_draft_head_norm": ([P, P, P, I64, P, C.c_int, P, I64, P, I64, P, P, P, P, P], C.c_int),
@@ -118,6 +120,8 @@ _SIGS = {
     "wc_tree_draft_frontier": ([P, C.c_int, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P, P, P, I64, P],
                                C.c_int),
     "wc_tree_draft_select": ([P, C.c_int, C.c_int, P, P, P, P, P], C.c_int),
+    "wc_tree_draft_expand_sample": ([P, P, C.c_int, C.c_int, I64, P, C.c_int, C.c_int, P, P], C.c_int),
+    "wc_tree_draft_select_all": ([P, C.c_int, P, P, P, P, P, P], C.c_int),
     "wc_target_embed": ([P, C.c_int, C.c_int, P, C.c_int, P, I64, P], C.c_int),
     "wc_target_head": ([P, P, P, P, C.c_int, C.c_int, P, I64, C.c_int, P, P], C.c_int),
     "wc_target_layer": ([P, P, P, P, C.c_int, P, C.c_int, P, P, I64, P, P, C.c_int, C.c_int, P, P, C.c_int, P, P],

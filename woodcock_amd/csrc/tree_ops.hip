@@ -29,6 +29,14 @@
 //   wc_tree_draft_select    the verified tree: every node, or the root plus the
 //                           `budget` nodes of largest phat (ties: shallower,
 //                           then earlier) in node order, parents remapped.
+// Sampled drafting at T > 0 (spec.py:238-249; policies.py:25-36) shares the
+// table: wc_tree_draft_expand_sample draws each frontier row's children
+// without replacement (their number fixed before drawing, within the budget)
+// and appends them; wc_tree_draft_frontier then takes the level range from the
+// state; wc_tree_draft_select_all returns every node with the row of its draft
+// distribution.  Node counts are data-dependent there (a row with fewer nonzero
+// entries than draws yields fewer children), so they live in the state and the
+// host's launch shapes are upper bounds.
 #include "wc_common.h"
 
 namespace wc {
@@ -82,7 +90,25 @@ struct TreeDraftState {
   // row (own 128-byte line; reset by the block that completes it)
   unsigned long long cand[kTdMaxWidth][kTdParts][kTdMaxWidth];
   unsigned int ctr[kTdMaxWidth][32];
+  // sampled drafting (T > 0): the table's node count, the last expansion's
+  // node range, the current frontier's row count and the draws granted so far
+  // (Plan.children_for)
+  int32_t n_nodes, lvl_begin, lvl_end, n_front, granted, pad_[3];
+  // per frontier row and part: the part's best keys (fp64 bits), their head
+  // rows and the part's q mass; per row: the drawn children (token, phat bits)
+  // and their number; the level's completion counter (own 128-byte line)
+  unsigned long long skey[kTdMaxWidth][kTdParts][kTdMaxWidth];
+  unsigned int srow[kTdMaxWidth][kTdParts][kTdMaxWidth];
+  unsigned long long smass[kTdMaxWidth][kTdParts];
+  unsigned int stok[kTdMaxWidth][kTdMaxWidth];
+  unsigned long long sphat[kTdMaxWidth][kTdMaxWidth];
+  unsigned int scount[kTdMaxWidth];
+  unsigned int lvl_ctr[32];
 };
+
+__device__ __forceinline__ unsigned int atomic_load_u32(const unsigned int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __global__ void k_td_begin(TreeDraftState* st, const int32_t* __restrict__ root_token) {
   if (threadIdx.x == 0) {
@@ -93,6 +119,11 @@ __global__ void k_td_begin(TreeDraftState* st, const int32_t* __restrict__ root_
     st->slot[0] = -1;
     st->store[0] = 0;
     st->front[0] = 0;
+    st->n_nodes = 1;
+    st->lvl_begin = 0;
+    st->lvl_end = 1;
+    st->n_front = 1;
+    st->granted = 0;
   }
 }
 
@@ -206,10 +237,18 @@ __global__ __launch_bounds__(kTdThreads) void k_td_frontier(TreeDraftState* st, 
                                                             uint8_t* __restrict__ mask, int64_t mask_ld) {
   __shared__ int s_front[kTdMaxWidth];
   __shared__ int s_anc[kTdMaxWidth][kTdMaxNodes / kTdMaxWidth];
-  __shared__ int s_nanc[kTdMaxWidth];
+  __shared__ int s_nanc[kTdMaxWidth], s_pos[kTdMaxWidth];
   __shared__ double s_ph[kTdMaxNodes];
   const int t = threadIdx.x;
-  const int n = le - lb, m = min(width, n);
+  // level_begin 0: the level the last sampled expansion appended (its range is
+  // in the state); rows [m, width) then get inputs of a harmless padding row
+  const bool dyn = lb == 0;
+  if (dyn) {
+    lb = st->lvl_begin;
+    le = st->lvl_end;
+  }
+  const int n = min(max(le - lb, 0), kTdMaxNodes), m = min(width, n);
+  const int rows = dyn ? width : m;
   for (int i = t; i < n; i += kTdThreads) s_ph[i] = st->phat[lb + i];
   __syncthreads();
   for (int i = t; i < n; i += kTdThreads) {
@@ -223,23 +262,28 @@ __global__ __launch_bounds__(kTdThreads) void k_td_frontier(TreeDraftState* st, 
   }
   __syncthreads();
   const int base = *offset_dev;
+  if (t == 0) st->n_front = m;
   if (t < m) {
     const int v = s_front[t];
     st->front[t] = v;
     tokens[t] = st->token[v];
     feat_rows[t] = st->store[st->parent[v]];
-    positions[t] = base - 1 + st->depth[v];
+    s_pos[t] = positions[t] = base - 1 + st->depth[v];
     st->slot[v] = base + tree_cache + t;
     st->store[v] = store_base + t;
     // cache slots of the ancestors below the root
     int na = 0;
     for (int u = st->parent[v]; u > 0 && na < kTdMaxNodes / kTdMaxWidth; u = st->parent[u]) s_anc[t][na++] = st->slot[u];
     s_nanc[t] = na;
+  } else if (t < rows) {  // padding: the root token on the root's feedback at depth 1, seeing the prefix and itself
+    tokens[t] = st->token[0];
+    feat_rows[t] = 0;
+    s_pos[t] = positions[t] = base;
+    s_nanc[t] = 0;
   }
   __syncthreads();
-  for (int r = 0; r < m; ++r) {
-    const int v = s_front[r];
-    const int pos = base - 1 + st->depth[v];
+  for (int r = 0; r < rows; ++r) {
+    const int pos = s_pos[r];
     const int lo = window > 0 ? max(0, pos - window + 1) : 0;
     const int self = base + tree_cache + r, na = s_nanc[r];
     uint8_t* row = mask + static_cast<int64_t>(r) * mask_ld;
@@ -299,6 +343,244 @@ __global__ __launch_bounds__(kTdThreads) void k_td_select(const TreeDraftState* 
     depth[i] = st->depth[v];
     parents[i] = p < 0 ? -1 : s_pos[p];
   }
+}
+
+// ------------------------------------------------------------------ sampled tree drafting (T > 0)
+
+// (key, head row) order of the draws: the larger key first, the lower row on a tie.
+__device__ __forceinline__ bool key_before(double ka, int ia, double kb, int ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+// The best (key, row) over the block; every thread receives it.
+__device__ __forceinline__ void block_best_key(double& k, int& i, double* red_k, int* red_i) {
+  for (int s = kWave / 2; s > 0; s >>= 1) {
+    const double ok = __shfl_xor(k, s);
+    const int oi = __shfl_xor(i, s);
+    if (key_before(ok, oi, k, i)) {
+      k = ok;
+      i = oi;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) {
+    red_k[threadIdx.x / kWave] = k;
+    red_i[threadIdx.x / kWave] = i;
+  }
+  __syncthreads();
+  k = red_k[0];
+  i = red_i[0];
+  for (int w = 1; w < kTdThreads / kWave; ++w)
+    if (key_before(red_k[w], red_i[w], k, i)) {
+      k = red_k[w];
+      i = red_i[w];
+    }
+}
+
+constexpr int kNoRow = 0x7fffffff;
+
+// Block (r, p): part p of frontier row r (rows past the state's frontier count
+// return at once).  Row r's draw count m = min(width, budget left after the
+// rows before it) is fixed before drawing (Plan.children_for,
+// policies.py:32-36).  Every nonzero entry i gets the key
+// log q(i) - log(-log u), u = value v * H4 + i of the drafting stream (v the
+// frontier node, H4 = head_rows rounded up to 4), and the m largest keys are the
+// children in descending key order: Gumbel-top-k = m draws without replacement
+// (sampling.py:196-203; spec.py:238-249).  Each entry owns its uniform, so all
+// rows and parts draw at once.  The part's best m keys and its q mass go to
+// the row's last part, which keeps the best m overall with
+// phat = phat(parent) * q(i) / sum(q); the last row to finish appends every
+// row's children to the node table in frontier order.
+__global__ __launch_bounds__(kTdThreads) void k_td_sample(TreeDraftState* st, const float* __restrict__ q,
+                                                          int head_rows, int64_t ld_q,
+                                                          const int32_t* __restrict__ d2t, int width, int budget,
+                                                          unsigned long long seed, const int32_t* __restrict__ round_dev,
+                                                          int purpose) {
+  __shared__ double red_k[kTdThreads / kWave];
+  __shared__ int red_i[kTdThreads / kWave];
+  __shared__ double red_m[kTdThreads / kWave];
+  __shared__ bool s_last;
+  const int r = blockIdx.x, p = blockIdx.y, P = gridDim.y, t = threadIdx.x;
+  const int nf = min(st->n_front, static_cast<int>(gridDim.x));
+  if (nf <= 0) {  // an empty frontier: the level is empty
+    if (r == 0 && p == 0 && t == 0) {
+      st->lvl_begin = st->n_nodes;
+      st->lvl_end = st->n_nodes;
+    }
+    return;
+  }
+  if (r >= nf) return;
+  const int rem = max(0, budget - st->granted);
+  const int m = min(width, max(0, rem - r * width));
+  const int v = st->front[r];
+  const float* qr = q + static_cast<int64_t>(r) * ld_q;
+  const int span = ((head_rows + P - 1) / P + 3) & ~3;
+  const int i0 = min(p * span, head_rows), i1 = min(i0 + span, head_rows);
+  const unsigned long long round = static_cast<unsigned long long>(*round_dev);
+  const unsigned long long ubase =
+      static_cast<unsigned long long>(v) * static_cast<unsigned long long>((head_rows + 3) & ~3);
+  double lk[kTdMaxWidth];
+  int li[kTdMaxWidth];
+#pragma unroll
+  for (int e = 0; e < kTdMaxWidth; ++e) {
+    lk[e] = -INFINITY;
+    li[e] = kNoRow;
+  }
+  double mass = 0.0;
+  if (m > 0) {
+    // four consecutive entries per thread share one Philox block (i0 is a multiple of 4)
+    for (int g = i0 + 4 * t; g < i1; g += 4 * kTdThreads) {
+      unsigned long long c[4] = {(ubase + static_cast<unsigned long long>(g)) >> 2, round,
+                                 static_cast<unsigned long long>(purpose), 0ull};
+      philox4x64(c, seed, 0ull);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = g + e;
+        if (i >= i1) break;
+        const float x = qr[i];
+        mass += static_cast<double>(x);
+        if (!(x > 0.f)) continue;
+        const double u = static_cast<double>(c[e] >> 11) * (1.0 / 9007199254740992.0);
+        double kk = log(static_cast<double>(x)) - log(-log(u));
+        int ki = i;
+#pragma unroll
+        for (int j = 0; j < kTdMaxWidth; ++j) {  // sorted insert into the thread's best list
+          const bool take = j < m && key_before(kk, ki, lk[j], li[j]);
+          const double tk = lk[j];
+          const int ti = li[j];
+          lk[j] = take ? kk : tk;
+          li[j] = take ? ki : ti;
+          kk = take ? tk : kk;
+          ki = take ? ti : ki;
+        }
+      }
+    }
+  }
+  // the part's best m, popped from the list heads in order
+  for (int sel = 0; sel < m; ++sel) {
+    double bk = lk[0];
+    int bi = li[0];
+    block_best_key(bk, bi, red_k, red_i);
+    if (t == 0) {
+      atomic_store_u64(&st->skey[r][p][sel], static_cast<unsigned long long>(__double_as_longlong(bk)));
+      atomic_store_u32(&st->srow[r][p][sel], static_cast<unsigned int>(bi));
+    }
+    if (bi != kNoRow && li[0] == bi) {
+#pragma unroll
+      for (int e = 0; e + 1 < kTdMaxWidth; ++e) {
+        lk[e] = lk[e + 1];
+        li[e] = li[e + 1];
+      }
+      lk[kTdMaxWidth - 1] = -INFINITY;
+      li[kTdMaxWidth - 1] = kNoRow;
+    }
+  }
+  mass = wave_sum(mass);
+  __syncthreads();
+  if (t % kWave == 0) red_m[t / kWave] = mass;
+  __syncthreads();
+  if (t == 0) {
+    double ms = 0.0;
+    for (int w = 0; w < kTdThreads / kWave; ++w) ms += red_m[w];
+    atomic_store_u64(&st->smass[r][p], static_cast<unsigned long long>(__double_as_longlong(ms)));
+  }
+  // the row's last part merges the parts' candidates
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const bool last = __hip_atomic_fetch_add(&st->ctr[r][0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      static_cast<unsigned int>(P - 1);
+    if (last) __hip_atomic_store(&st->ctr[r][0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  double ck = -INFINITY;
+  int ci = kNoRow;
+  if (t < P * m) {
+    ck = __longlong_as_double(static_cast<long long>(atomic_load_u64(&st->skey[r][t / m][t % m])));
+    ci = static_cast<int>(atomic_load_u32(&st->srow[r][t / m][t % m]));
+  }
+  double Q = 0.0;  // the row's q mass, parts summed in order
+  for (int pp = 0; pp < P; ++pp)
+    Q += __longlong_as_double(static_cast<long long>(atomic_load_u64(&st->smass[r][pp])));
+  const double ph = st->phat[v];
+  int cnt = 0;
+  for (int sel = 0; sel < m; ++sel) {
+    double bk = ck;
+    int bi = ci;
+    block_best_key(bk, bi, red_k, red_i);
+    if (bi == kNoRow) break;  // fewer nonzero entries than draws
+    if (t == 0) {
+      atomic_store_u32(&st->stok[r][sel], static_cast<unsigned int>(d2t ? d2t[bi] : bi));
+      const double phc = ph * (static_cast<double>(qr[bi]) / Q);
+      atomic_store_u64(&st->sphat[r][sel], static_cast<unsigned long long>(__double_as_longlong(phc)));
+    }
+    if (ci == bi) {
+      ck = -INFINITY;
+      ci = kNoRow;
+    }
+    ++cnt;
+  }
+  if (t == 0) atomic_store_u32(&st->scount[r], static_cast<unsigned int>(cnt));
+  // the last row appends the level
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    const bool last = __hip_atomic_fetch_add(&st->lvl_ctr[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      static_cast<unsigned int>(nf - 1);
+    if (last) __hip_atomic_store(&st->lvl_ctr[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last || t != 0) return;
+  int c = st->n_nodes;
+  const int begin = c;
+  int granted = 0;
+  for (int rr = 0; rr < nf; ++rr) {
+    const int vv = st->front[rr];
+    granted += min(width, max(0, rem - rr * width));
+    const int cr = static_cast<int>(atomic_load_u32(&st->scount[rr]));
+    for (int j = 0; j < cr && c < kTdMaxNodes; ++j, ++c) {
+      st->token[c] = static_cast<int32_t>(atomic_load_u32(&st->stok[rr][j]));
+      st->parent[c] = vv;
+      st->depth[c] = st->depth[vv] + 1;
+      st->phat[c] = __longlong_as_double(static_cast<long long>(atomic_load_u64(&st->sphat[rr][j])));
+      st->slot[c] = -1;
+      st->store[c] = -1;
+    }
+  }
+  st->lvl_begin = begin;
+  st->lvl_end = c;
+  st->n_nodes = c;
+  st->granted += granted;
+}
+
+// One block: every node of a sampled tree (StaticPolicy.select_verify keeps all
+// of them at T > 0, policies.py:67-69) in node order, with the row of each
+// node's draft distribution (its feedback-store row; 0 for nodes never
+// expanded), padded to max_nodes rows with root-token children of the root.
+__global__ __launch_bounds__(kTdThreads) void k_td_select_all(const TreeDraftState* st, int max_nodes,
+                                                              int32_t* __restrict__ tokens,
+                                                              int32_t* __restrict__ parents,
+                                                              int32_t* __restrict__ depth,
+                                                              int32_t* __restrict__ q_rows,
+                                                              int32_t* __restrict__ count) {
+  const int n = min(st->n_nodes, max_nodes);
+  for (int v = threadIdx.x; v < max_nodes; v += kTdThreads) {
+    if (v < n) {
+      tokens[v] = st->token[v];
+      parents[v] = st->parent[v];
+      depth[v] = st->depth[v];
+      q_rows[v] = max(st->store[v], 0);
+    } else {
+      tokens[v] = st->token[0];
+      parents[v] = 0;
+      depth[v] = 1;
+      q_rows[v] = 0;
+    }
+  }
+  if (threadIdx.x == 0) *count = n;
 }
 
 // ------------------------------------------------------------------ Gumbel-top-k
@@ -496,12 +778,45 @@ int wc_tree_draft_frontier(void* state, int level_begin, int level_end, int widt
   WC_REQUIRE(state && offset_dev && tokens_out && feat_rows_out && positions_out && mask_out,
              "wc_tree_draft_frontier: NULL buffer");
   WC_REQUIRE(width >= 1 && width <= kTdMaxWidth, "wc_tree_draft_frontier: width must be in 1..%d", kTdMaxWidth);
-  WC_REQUIRE(level_begin >= 1 && level_end > level_begin && level_end <= kTdMaxNodes,
+  WC_REQUIRE(level_begin == 0 || (level_begin >= 1 && level_end > level_begin && level_end <= kTdMaxNodes),
              "wc_tree_draft_frontier: bad level range %d..%d", level_begin, level_end);
   WC_REQUIRE(tree_cache >= 0 && store_base >= 1 && mask_ld >= 1, "wc_tree_draft_frontier: bad offsets");
   hipLaunchKernelGGL(k_td_frontier, dim3(1), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
                      static_cast<TreeDraftState*>(state), level_begin, level_end, width, offset_dev, tree_cache,
                      window, store_base, tokens_out, feat_rows_out, positions_out, mask_out, mask_ld);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_tree_draft_expand_sample(void* state, const float* q, int rows, int head_rows, int64_t ld_q,
+                                const int32_t* d2t_dev, int width, int budget, const wc_uniforms* rng,
+                                wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && q && rng && rng->round_dev, "wc_tree_draft_expand_sample: NULL buffer");
+  WC_REQUIRE(width >= 1 && width <= kTdMaxWidth, "wc_tree_draft_expand_sample: width must be in 1..%d",
+             kTdMaxWidth);
+  WC_REQUIRE(rows >= 1 && rows <= kTdMaxWidth, "wc_tree_draft_expand_sample: rows must be in 1..%d", kTdMaxWidth);
+  WC_REQUIRE(head_rows >= 1 && ld_q >= head_rows, "wc_tree_draft_expand_sample: need head_rows >= 1, ld_q >= head_rows");
+  WC_REQUIRE(budget >= 0 && budget < kTdMaxNodes, "wc_tree_draft_expand_sample: budget must be in 0..%d",
+             kTdMaxNodes - 1);
+  const int parts = std::max(1, std::min(kTdParts, head_rows / 1024));
+  hipLaunchKernelGGL(k_td_sample, dim3(rows, parts), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<TreeDraftState*>(state), q, head_rows, ld_q, d2t_dev, width, budget,
+                     static_cast<unsigned long long>(rng->seed), rng->round_dev, rng->purpose);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_tree_draft_select_all(const void* state, int max_nodes, int32_t* tokens_out, int32_t* parents_out,
+                             int32_t* depth_out, int32_t* q_rows_out, int32_t* count_out, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && tokens_out && parents_out && depth_out && q_rows_out && count_out,
+             "wc_tree_draft_select_all: NULL buffer");
+  WC_REQUIRE(max_nodes >= 1 && max_nodes <= kTdMaxNodes, "wc_tree_draft_select_all: max_nodes must be in 1..%d",
+             kTdMaxNodes);
+  hipLaunchKernelGGL(k_td_select_all, dim3(1), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const TreeDraftState*>(state), max_nodes, tokens_out, parents_out, depth_out,
+                     q_rows_out, count_out);
   WC_LAUNCHED();
   return WC_OK;
 }

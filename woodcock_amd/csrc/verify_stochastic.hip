@@ -1265,6 +1265,9 @@ struct TreeArgs {
   const float* q;  // [rows][ld_q] draft probabilities of each node's children, over the head rows
   int head_rows;
   int64_t ld_q;
+  const int32_t* q_rows;    // node v's row of q (NULL: row v), each below q_count
+  int q_count;
+  const int32_t* count;     // node count on the device (NULL: rows), at most rows
   const int32_t* d2t;  // [head_rows] ascending target ids, or NULL = identity
   const int32_t* tokens;
   const int32_t* parents;
@@ -1312,19 +1315,22 @@ __global__ __launch_bounds__(kTwThreads) void k_tree_walk(TreeArgs a) {
   __shared__ double s_div[WC_MAX_NODES], s_s[WC_MAX_NODES];
   __shared__ int s_bad, s_acc, s_nu;
   __shared__ unsigned long long s_kids;
-  const int t = threadIdx.x, N = a.rows;
+  const int t = threadIdx.x;
+  const int N = a.count ? *a.count : a.rows;
+  const bool n_ok = N >= 1 && N <= a.rows;
   const unsigned long long round = static_cast<unsigned long long>(*a.round_dev);
   if (t == 0) {
-    s_bad = 0;
+    s_bad = n_ok ? 0 : 1;
     s_nu = 0;
   }
   __syncthreads();
-  {  // parents[0] = -1, 0 <= parents[i] < i, tokens inside the vocabulary, d2t ascending
+  if (n_ok) {  // parents[0] = -1, 0 <= parents[i] < i, tokens inside the vocabulary, d2t ascending
     int bad = 0;
     for (int i = t; i < N; i += kTwThreads) {
       const int par = a.parents[i], tok = a.tokens[i];
       if (i == 0 ? par != -1 : (par < 0 || par >= i)) bad = 1;
       if (tok < 0 || tok >= a.vocab) bad = 1;
+      if (a.q_rows && (a.q_rows[i] < 0 || a.q_rows[i] >= a.q_count)) bad = 1;
     }
     if (a.d2t)
       for (int r = t; r < a.head_rows; r += kTwThreads) {
@@ -1348,7 +1354,7 @@ __global__ __launch_bounds__(kTwThreads) void k_tree_walk(TreeArgs a) {
     if (kids == 0) break;  // a leaf: the draw is from p[v]
     // node sums: Q, the target mass on the head rows and on the whole vocabulary
     const float* pr = a.p + static_cast<int64_t>(v) * a.ld_p;
-    const float* qr = a.q + static_cast<int64_t>(v) * a.ld_q;
+    const float* qr = a.q + static_cast<int64_t>(a.q_rows ? a.q_rows[v] : v) * a.ld_q;
     double sq = 0.0, sph = 0.0, spa = 0.0;
     for (int r = t; r < a.head_rows; r += kTwThreads) {
       sq += static_cast<double>(qr[r]);
@@ -1451,7 +1457,7 @@ __global__ __launch_bounds__(kStThreads) void k_tree_sample(TreeArgs a) {
     s_s[t] = st->s[t];
   }
   const float* pr = a.p + static_cast<int64_t>(v) * a.ld_p;
-  const float* qr = a.q ? a.q + static_cast<int64_t>(v) * a.ld_q : nullptr;
+  const float* qr = a.q ? a.q + static_cast<int64_t>(a.q_rows ? a.q_rows[v] : v) * a.ld_q : nullptr;
   // values of chunk c of the final distribution: q of the head rows in the chunk
   // scattered into LDS (zero elsewhere), then the j-step map per entry
   auto values = [&](int c, double (&val)[kPerThread]) {
@@ -1851,6 +1857,56 @@ static int fused_capacity(int* hold) {
 
 }  // namespace wc
 
+namespace wc {
+
+// Both tree entry points: q_rows / count NULL read node v's q at row v and
+// take `rows` nodes.
+static int tree_stochastic(const float* p, int rows, int vocab, int64_t ld_p, const float* q, const int32_t* q_rows,
+                           int q_count, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
+                           const int32_t* tree_tokens_dev, const int32_t* tree_parents_dev, const int32_t* count_dev,
+                           const wc_uniforms* rng, wc_verdict* verdict_dev, void* workspace, wc_stream_t stream,
+                           const char* fn) {
+  WC_REQUIRE(p && tree_tokens_dev && tree_parents_dev && verdict_dev && rng && rng->round_dev, "%s: NULL buffer", fn);
+  WC_REQUIRE(workspace && aligned(workspace, 16), "%s: workspace is NULL or misaligned", fn);
+  WC_REQUIRE(rows >= 1 && rows <= WC_MAX_NODES, "%s: rows must be in 1..%d (got %d)", fn, WC_MAX_NODES, rows);
+  WC_REQUIRE(vocab >= 1 && vocab <= kVocabChunk * kMaxVocabChunks, "%s: vocab %d out of range", fn, vocab);
+  WC_REQUIRE(ld_p >= vocab, "%s: p row stride smaller than vocab", fn);
+  const bool any_q = rows > 1 || count_dev != nullptr;
+  WC_REQUIRE(!any_q || (q && head_rows >= 1 && ld_q >= head_rows), "%s: bad draft distribution buffer / width / stride",
+             fn);
+  WC_REQUIRE(d2t_dev != nullptr || head_rows <= vocab,
+             "%s: without d2t the draft distribution must not exceed the vocabulary", fn);
+  TreeArgs a{};
+  a.p = p;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.ld_p = ld_p;
+  a.q = q;
+  a.head_rows = any_q ? head_rows : 0;
+  a.ld_q = ld_q;
+  a.q_rows = q_rows;
+  a.q_count = q_count;
+  a.count = count_dev;
+  a.d2t = d2t_dev;
+  a.tokens = tree_tokens_dev;
+  a.parents = tree_parents_dev;
+  a.seed = rng->seed;
+  a.round_dev = rng->round_dev;
+  a.purpose = rng->purpose;
+  a.st = reinterpret_cast<TreeState*>(static_cast<char*>(workspace) + kTreeStateOff);
+  a.chunk_data = reinterpret_cast<double*>(static_cast<char*>(workspace) + kStochChunkOff);
+  a.counter = verify_counter(workspace, kCtrTree);
+  a.verdict = verdict_dev;
+  auto s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_tree_walk, dim3(1), dim3(kTwThreads), 0, s, a);
+  WC_LAUNCHED();
+  hipLaunchKernelGGL(k_tree_sample, dim3((vocab + kVocabChunk - 1) / kVocabChunk), dim3(kStThreads), 0, s, a);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+}  // namespace wc
+
 extern "C" {
 
 int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float temperature, int top_k, float top_p,
@@ -2028,43 +2084,22 @@ int wc_verify_tree_stochastic(const float* p, int rows, int vocab, int64_t ld_p,
                               int64_t ld_q, const int32_t* d2t_dev, const int32_t* tree_tokens_dev,
                               const int32_t* tree_parents_dev, const wc_uniforms* rng, wc_verdict* verdict_dev,
                               void* workspace, wc_stream_t stream) {
+  return wc::tree_stochastic(p, rows, vocab, ld_p, q, nullptr, 0, head_rows, ld_q, d2t_dev, tree_tokens_dev,
+                             tree_parents_dev, nullptr, rng, verdict_dev, workspace, stream, "wc_verify_tree_stochastic");
+}
+
+int wc_verify_tree_stochastic_indexed(const float* p, int rows, int vocab, int64_t ld_p, const float* q,
+                                      int q_count, const int32_t* q_rows_dev, int head_rows, int64_t ld_q,
+                                      const int32_t* d2t_dev, const int32_t* tree_tokens_dev,
+                                      const int32_t* tree_parents_dev, const int32_t* count_dev,
+                                      const wc_uniforms* rng, wc_verdict* verdict_dev, void* workspace,
+                                      wc_stream_t stream) {
   using namespace wc;
-  WC_REQUIRE(p && tree_tokens_dev && tree_parents_dev && verdict_dev && rng && rng->round_dev,
-             "wc_verify_tree_stochastic: NULL buffer");
-  WC_REQUIRE(workspace && aligned(workspace, 16), "wc_verify_tree_stochastic: workspace is NULL or misaligned");
-  WC_REQUIRE(rows >= 1 && rows <= WC_MAX_NODES, "wc_verify_tree_stochastic: rows must be in 1..%d (got %d)",
-             WC_MAX_NODES, rows);
-  WC_REQUIRE(vocab >= 1 && vocab <= kVocabChunk * kMaxVocabChunks, "wc_verify_tree_stochastic: vocab %d out of range",
-             vocab);
-  WC_REQUIRE(ld_p >= vocab, "wc_verify_tree_stochastic: p row stride smaller than vocab");
-  WC_REQUIRE(rows == 1 || (q && head_rows >= 1 && ld_q >= head_rows),
-             "wc_verify_tree_stochastic: bad draft distribution buffer / width / stride");
-  WC_REQUIRE(d2t_dev != nullptr || head_rows <= vocab,
-             "wc_verify_tree_stochastic: without d2t the draft distribution must not exceed the vocabulary");
-  TreeArgs a{};
-  a.p = p;
-  a.rows = rows;
-  a.vocab = vocab;
-  a.ld_p = ld_p;
-  a.q = q;
-  a.head_rows = rows == 1 ? 0 : head_rows;
-  a.ld_q = ld_q;
-  a.d2t = d2t_dev;
-  a.tokens = tree_tokens_dev;
-  a.parents = tree_parents_dev;
-  a.seed = rng->seed;
-  a.round_dev = rng->round_dev;
-  a.purpose = rng->purpose;
-  a.st = reinterpret_cast<TreeState*>(static_cast<char*>(workspace) + kTreeStateOff);
-  a.chunk_data = reinterpret_cast<double*>(static_cast<char*>(workspace) + kStochChunkOff);
-  a.counter = verify_counter(workspace, kCtrTree);
-  a.verdict = verdict_dev;
-  auto s = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(k_tree_walk, dim3(1), dim3(kTwThreads), 0, s, a);
-  WC_LAUNCHED();
-  hipLaunchKernelGGL(k_tree_sample, dim3((vocab + kVocabChunk - 1) / kVocabChunk), dim3(kStThreads), 0, s, a);
-  WC_LAUNCHED();
-  return WC_OK;
+  WC_REQUIRE(q && q_rows_dev && count_dev, "wc_verify_tree_stochastic_indexed: NULL buffer");
+  WC_REQUIRE(q_count >= 1, "wc_verify_tree_stochastic_indexed: q_count must be positive");
+  return tree_stochastic(p, rows, vocab, ld_p, q, q_rows_dev, q_count, head_rows, ld_q, d2t_dev, tree_tokens_dev,
+                         tree_parents_dev, count_dev, rng, verdict_dev, workspace, stream,
+                         "wc_verify_tree_stochastic_indexed");
 }
 
 }  // extern "C"

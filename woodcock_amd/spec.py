@@ -29,7 +29,10 @@ serves every round.
 policy observes the outcome; greedy chains run the fused single-sync round
 (spec.py:331-364), trees the drafting / verify / compact / update sequence of
 spec.py:187-201 -- also with one host synchronisation, since tree drafting and
-the tree verification stay on the device.
+the tree verification stay on the device.  At T > 0 every round (a chain is a
+width-1 tree) takes that sequence with the stochastic branches: sampled
+drafting (spec.py:238-249), the warped target distribution and recursive
+rejection down the tree (spec.py:320-324).
 
 State invariants follow python/woodcock/spec.py:1-15: before a round the
 drafter cache holds real entries 0..n-1 and the root is the drafter's hidden
@@ -51,9 +54,12 @@ from .cache import KVCache, compact_cache_dev
 from .drafter import Drafter
 from .policies import Plan, Policy
 from .runtime import check_verdict, new_verdict, ptr, read_verdict, stream_ptr
+from .sampling import SamplingParams, probs_from_logits
 
 # state vector slots (device int32)
 S_N, S_ROUND = 0, 1
+# sub-streams of a sampled round's uniforms (Philox under the sampling seed, keyed by the round counter)
+PURPOSE_VERIFY, PURPOSE_DRAFT = 0, 1
 
 
 @dataclass
@@ -342,7 +348,8 @@ class GenStats:
 
 
 class SpeculativeDecoder:
-    """Greedy speculative decoding: one drafter cache, one target, one policy.
+    """Speculative decoding: one drafter cache, one target, one policy, greedy
+    or sampled (``sampling``: SamplingParams with temperature > 0).
 
     target: ``verify_forward(tokens, rows, offset_dev, positions, mask) ->
     (logits, taps)`` enqueued without a host synchronisation (``TargetRunner``
@@ -355,10 +362,14 @@ class SpeculativeDecoder:
     rounds are enqueued eagerly (their mask prefix is the host-known n)."""
 
     def __init__(self, drafter: Drafter, target, policy: Policy, capacity: int = 4096, k_max: int = 8,
-                 max_tree_depth: int = 0, use_graphs: bool = False, timing: bool = False):
+                 max_tree_depth: int = 0, use_graphs: bool = False, timing: bool = False,
+                 sampling: SamplingParams | None = None):
         self.d = drafter
         self.t = target
         self.policy = policy
+        self.sp = sampling if sampling is not None else SamplingParams()
+        self._p = None  # target probabilities of a sampled round's verify block
+        self._host_tree = None
         self.rnd = ChainRound(drafter, k_max, capacity, getattr(target, "cache", None),
                               max_keep=max_tree_depth + 1)
         self.k_max = k_max
@@ -460,13 +471,14 @@ class SpeculativeDecoder:
 
     # ------------------------------------------------------------------ tree rounds
 
-    def tree_drafter(self, plan: Plan):
+    def tree_drafter(self, plan: Plan, stochastic: bool = False):
         from .tree_draft import TreeDrafter
 
-        key = (plan.max_depth, plan.width, plan.budget)
+        key = (plan.max_depth, plan.width, plan.budget, stochastic)
         tdr = self._trees.get(key)
         if tdr is None:
-            tdr = self._trees[key] = TreeDrafter(self.d, self.rnd.cache, plan.max_depth, plan.width, plan.budget)
+            tdr = self._trees[key] = TreeDrafter(self.d, self.rnd.cache, plan.max_depth, plan.width, plan.budget,
+                                                 stochastic=stochastic)
         return tdr
 
     def enqueue_tree_draft(self, plan: Plan):
@@ -511,13 +523,79 @@ class SpeculativeDecoder:
         res.k, res.depth = rows - 1, plan.max_depth
         return res
 
+    # ------------------------------------------------------------------ sampled rounds
+
+    def _uniforms(self, purpose: int) -> _lib.Uniforms:
+        return _lib.Uniforms(int(self.sp.seed), ptr(self.rnd.state[S_ROUND:S_ROUND + 1]), purpose)
+
+    def enqueue_sampled_draft(self, plan: Plan):
+        """Sampled tree drafting from the root (spec.py:216-303, T > 0) under a
+        fresh round counter -> (device tree, verify-block rows, drafter)."""
+        r = self.rnd
+        tdr = self.tree_drafter(plan, stochastic=True)
+        r.state[S_ROUND:S_ROUND + 1].add_(1)
+        idx = (r.verdict[_lib.V_N_KEEP:_lib.V_N_KEEP + 1] - 1).long()
+        root_hid = r.upd_hid.index_select(0, idx)
+        tree = tdr.draft(r.x_n_dev(), None, None, r.n_dev(), root_hidden=root_hid,
+                         temperature=self.sp.temperature, rng=self._uniforms(PURPOSE_DRAFT))
+        return tree, tdr.max_nodes, tdr
+
+    def enqueue_sampled_verify(self, tdr, tree, logits: torch.Tensor, rows: int) -> torch.Tensor:
+        """p = the warped target distribution at every node (spec.py:321), then
+        recursive rejection down the tree with each node's draft distribution
+        (spec.py:322-324) -> verdict.  Returns p."""
+        r = self.rnd
+        V = logits.shape[1]
+        if self._p is None or self._p.shape[1] != V:
+            self._p = torch.empty(_lib.WC_MAX_NODES, V, dtype=torch.float32, device=self.d.device)
+        p = self._p[:rows]
+        probs_from_logits(logits[:rows], self.sp, out=p)
+        qs = tdr.q_store
+        u = self._uniforms(PURPOSE_VERIFY)
+        _lib.call("wc_verify_tree_stochastic_indexed", ptr(p), rows, V, p.stride(0), ptr(qs), qs.shape[0],
+                  ptr(tree.q_rows), qs.shape[1], qs.stride(0), ptr(self.d.vocab_ids), ptr(tree.tokens),
+                  ptr(tree.parents), ptr(tree.count), C.byref(u), ptr(r.verdict), ptr(r.vws), stream_ptr())
+        return p
+
+    def sampled_round(self, plan: Plan) -> RoundResult:
+        """A T > 0 round (spec.py:187-201 with the stochastic branches of _draft
+        and _verify): sampled drafting (a chain when width == 1), the target's
+        verify forward over the tree block, recursive rejection, compaction
+        along the accepted branch and the update -- one host synchronisation."""
+        r = self.rnd
+        self._ev = []
+        self._mark()
+        tree, rows, tdr = self.enqueue_sampled_draft(plan)
+        self._mark()
+        self.t.prepare(rows)
+        logits, taps = self.enqueue_tree_target(tree, rows)
+        self._mark()
+        self.enqueue_sampled_verify(tdr, tree, logits, rows)
+        r.enqueue_tree_commit(taps, rows, plan.max_depth)
+        # the drawn tree's size and depths ride along with the verdict copy
+        if self._host_tree is None:
+            self._host_tree = torch.zeros(_lib.WC_MAX_NODES + 1, dtype=torch.int32, pin_memory=True)
+        self._host_tree[:1].copy_(tree.count, non_blocking=True)
+        self._host_tree[1:rows + 1].copy_(tree.depth[:rows], non_blocking=True)
+        r.enqueue_readback()
+        self._mark()
+        res = r.finish()
+        self._read_times()
+        count = int(self._host_tree[0])
+        res.k = count - 1
+        res.depth = int(self._host_tree[1:count + 1].max())
+        return res
+
     # ------------------------------------------------------------------ loop
 
     def round(self) -> RoundResult:
         """One round as the policy plans it (spec.py:169-201)."""
-        plan = self.policy.plan(context_len=self.n, stochastic=False)
+        stochastic = not self.sp.greedy
+        plan = self.policy.plan(context_len=self.n, stochastic=stochastic)
         t0 = time.perf_counter()
-        if plan.width == 1:
+        if stochastic:
+            res = self.sampled_round(plan)
+        elif plan.width == 1:
             if not 1 <= plan.max_depth <= self.k_max:
                 raise ValueError(f"planned chain of {plan.max_depth} outside 1..{self.k_max}")
             res = self.chain_round(plan.max_depth)
