@@ -443,6 +443,16 @@ int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, cons
 /* Device workspace for wc_target_layer with up to max_rows rows. */
 size_t wc_target_workspace_bytes(const wc_drafter_dims* dims, int max_rows);
 
+/* One-time weight layout for the verify-width GEMMs: w [rows][cols] bf16
+ * row-major (nn.Linear [out][in]) -> out, the same bytes in fragment-major
+ * order: 16-row tile T, 32-column step s, lane l of 64 holds w[16 T + l % 16]
+ * [32 s + 8 (l / 16) .. + 8] at ((T cols / 32 + s) 64 + l) 8.  That is the A
+ * operand of v_mfma_f32_16x16x32_bf16, so every weight load of the GEMM reads
+ * one contiguous kilobyte.  rows a multiple of 16, cols of 32, out not
+ * aliasing w.  No reference counterpart (a storage format: the reference keeps
+ * nn.Linear weights row-major). */
+int wc_weights_frag(const void* w, int rows, int cols, void* out, wc_stream_t stream);
+
 /* One Qwen3 decoder layer over a verify block of `rows` <= 64 tokens, in place
  * on the fp32 residual stream x [rows][hidden]:
  *   h = x + W_o . attn(q_norm(W_q xn), k_norm(W_k xn), W_v xn), xn = RMS_in(x);
@@ -453,7 +463,9 @@ size_t wc_target_workspace_bytes(const wc_drafter_dims* dims, int max_rows);
  * *offset_dev in k_cache / v_cache [kv_heads][capacity][head_dim] of kv_dtype.
  * The caller advances the offset after the last layer.  dims supplies hidden,
  * heads, kv_heads, head_dim, inter, eps and window; hidden, heads*head_dim and
- * inter must be multiples of 256; the aux fields of L are ignored.
+ * inter must be multiples of 256; the aux fields of L are ignored; the
+ * matrices q, k, v, o, gate, up and down are fragment-major (wc_weights_frag),
+ * the norm gains plain.
  * Layer chaining: with next_norm (bf16 [hidden], the next layer's in_norm or
  * the final norm) the layer also leaves next_norm * x_out and the partial row
  * sums of squares of x_out in the workspace, and the next call (or
@@ -475,8 +487,9 @@ int wc_target_embed(const void* table, int vocab, int hidden, const int32_t* tok
                     int64_t ld, wc_stream_t stream);
 
 /* Target logits of a verify block: logits_out [rows][ld] fp32 =
- * RMSNorm(x; final_norm) . head_w^T, head_w [vocab][hidden] bf16 (the tied
- * embedding for Qwen3), rows <= 64, as a streaming MFMA GEMM with the
+ * RMSNorm(x; final_norm) . head_w^T, head_w [vocab][hidden] bf16 in
+ * fragment-major order (wc_weights_frag of the tied embedding for Qwen3, its
+ * rows padded to a multiple of 16), rows <= 64, as a streaming MFMA GEMM with the
  * activations split into bf16 hi + lo (fp32-level products).  Workspace: the
  * target-layer workspace for >= rows rows; input_prepared = 1 when the last
  * wc_target_layer call on it had next_norm = final_norm.  Replaces

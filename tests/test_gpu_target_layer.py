@@ -118,3 +118,17 @@ def test_target_layer_rejects_bad_shapes(cuda):
         layer(torch.zeros(65, SMALL.hidden_size, device=dev), cache, off)
     with pytest.raises(ValueError):
         layer(torch.zeros(4, SMALL.hidden_size + 1, device=dev), cache, off)
+
+
+@pytest.mark.parametrize("rows,cols", [(16, 32), (48, 96), (4096, 2048), (2048, 6144)])
+def test_fragment_major_weight_layout(cuda, rows, cols):
+    """wc_weights_frag: tile T, step s, lane l holds w[16 T + l % 16][32 s + 8 (l / 16) .. + 8]
+    (the A fragment of v_mfma_f32_16x16x32_bf16), the same bytes as the row-major matrix."""
+    from woodcock_amd.target import frag_weights
+
+    g = torch.Generator(device=cuda).manual_seed(rows + cols)
+    w = torch.randn(rows, cols, generator=g, device=cuda).bfloat16()
+    got = frag_weights(w).view(torch.int16).cpu().numpy().reshape(-1)
+    a = w.view(torch.int16).cpu().numpy().reshape(rows // 16, 16, cols // 32, 4, 8)
+    want = a.transpose(0, 2, 3, 1, 4).reshape(-1)  # [T][s][g][i][e]: lane l = 16 g + i
+    np.testing.assert_array_equal(got, want)

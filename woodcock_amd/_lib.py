@@ -122,6 +122,7 @@ _SIGS = {
     "wc_tree_draft_select": ([P, C.c_int, C.c_int, P, P, P, P, P], C.c_int),
     "wc_tree_draft_expand_sample": ([P, P, C.c_int, C.c_int, I64, P, C.c_int, C.c_int, P, P], C.c_int),
     "wc_tree_draft_select_all": ([P, C.c_int, P, P, P, P, P, P], C.c_int),
+    "wc_weights_frag": ([P, C.c_int, C.c_int, P, P], C.c_int),
     "wc_target_embed": ([P, C.c_int, C.c_int, P, C.c_int, P, I64, P], C.c_int),
     "wc_target_head": ([P, P, P, P, C.c_int, C.c_int, P, I64, C.c_int, P, P], C.c_int),
     "wc_target_layer": ([P, P, P, P, C.c_int, P, C.c_int, P, P, I64, P, P, C.c_int, C.c_int, P, P, C.c_int, P, P],

@@ -451,12 +451,12 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
 // addresses that do not depend on the row count; the block then exits if its
 // vector is past the live rows.  Runs after k_attention (stream order), so
 // plain loads see the partials.
-template <int D>
+template <int D, int FS = kMaxSplits>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) {
   constexpr int kPer = (D + kAttnThreads - 1) / kAttnThreads;  // elements per thread (D <= 256: 1)
   static_assert(kPer == 1, "head_dim up to the block size");
-  static_assert(kMaxSplits <= kWave, "one lane per split");
-  __shared__ float s_w[kMaxSplits];
+  static_assert(FS <= kWave, "one lane per split");
+  __shared__ float s_w[FS];
   __shared__ float s_den;
   const int v = blockIdx.x, kh = blockIdx.y;
   const int rep = a.H / a.Hk;
@@ -464,9 +464,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) 
   const float* base = a.partial + static_cast<int64_t>(kh) * S * a.qv_ld * (D + 2) + v * (D + 2);
   const int64_t kSplitStride = static_cast<int64_t>(a.qv_ld) * (D + 2);
   const int i = min(t, D - 1);
-  float o[kMaxSplits];
+  float o[FS];
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp) o[sp] = base[min(sp, S - 1) * kSplitStride + 2 + i];
+  for (int sp = 0; sp < FS; ++sp) o[sp] = base[min(sp, S - 1) * kSplitStride + 2 + i];
   float ms = -INFINITY, ls = 0.f;
   if (t < S) {
     ms = base[t * kSplitStride];
@@ -484,7 +484,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) 
   __syncthreads();
   float num = 0.f;
 #pragma unroll
-  for (int sp = 0; sp < kMaxSplits; ++sp)
+  for (int sp = 0; sp < FS; ++sp)
     if (sp < S) num = fmaf(s_w[sp], o[sp], num);
   if (t < D) {
     const int l = v / rep, h = kh * rep + v % rep;

@@ -18,9 +18,13 @@
 // (the norm's 1/rms scales the products afterwards).  k_mm_stream streams the
 // weights straight into B fragments eight k steps ahead while a three-slot LDS
 // ring hands each k step of activations to the block's four waves; blocks
-// split K when the projection is too narrow to fill the GPU, and the last
-// block of a column range sums the partials in a fixed order and runs the
-// epilogue (store, residual, SiLU(gate) * up, next activations).
+// split K when the projection is too narrow to fill the GPU, each split
+// storing its fp32 tile with plain stores, and k_mm_fix (the next launch, over
+// column ranges x 16-row groups) sums the splits in a fixed order and runs the
+// epilogue (store, residual, SiLU(gate) * up, next activations, or the QKV
+// head epilogue) -- no device-scope hand-over inside the GEMM.
+#include <array>
+
 #include "attention.h"
 
 namespace wc {
@@ -51,9 +55,9 @@ __device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo)
 
 // ------------------------------------------------------------------ activation prep
 // x [M][ldx] fp32 (times gain when given) -> fragment-major hi / lo, plus the
-// rows' sums of squares of x per 256-wide k block: ss [K / 256][64].  Block b
-// covers k [256 b, 256 b + 256) of all 64 rows (rows >= M are zero); thread t
-// row t / 4, k [256 b + 64 (t % 4), + 64).
+// rows' sums of squares of x per 256-wide k block: ss [K / 256][64].  Block
+// (b, r) covers k [256 b, 256 b + 256) of rows 16 r .. 16 r + 15 (rows >= M are
+// zero); thread t row 16 r + t / 16, k [256 b + 16 (t % 16), + 16).
 struct XaPrepArgs {
   const float* x;
   int64_t ldx;
@@ -64,20 +68,20 @@ struct XaPrepArgs {
 };
 
 __global__ __launch_bounds__(256) void k_xa_prep(XaPrepArgs a) {
-  const int t = threadIdx.x, m = t / 4, k0 = blockIdx.x * 256 + (t % 4) * 64;
+  const int t = threadIdx.x, m = blockIdx.y * 16 + t / 16, k0 = blockIdx.x * 256 + (t % 16) * 16;
   const bool live = m < a.M;
   const float* xr = a.x + static_cast<int64_t>(min(m, a.M - 1)) * a.ldx + k0;
-  float4 xv[16];
+  float4 xv[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) xv[i] = *reinterpret_cast<const float4*>(xr + 4 * i);
-  uint4 gv[8];
+  for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const float4*>(xr + 4 * i);
+  uint4 gv[2];
   if (a.gain) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) gv[i] = *reinterpret_cast<const uint4*>(a.gain + k0 + 8 * i);
+    for (int i = 0; i < 2; ++i) gv[i] = *reinterpret_cast<const uint4*>(a.gain + k0 + 8 * i);
   }
   float ss = 0.f;
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
+  for (int g = 0; g < 2; ++g) {
     float v[8] = {xv[2 * g].x, xv[2 * g].y, xv[2 * g].z, xv[2 * g].w,
                   xv[2 * g + 1].x, xv[2 * g + 1].y, xv[2 * g + 1].z, xv[2 * g + 1].w};
 #pragma unroll
@@ -95,9 +99,9 @@ __global__ __launch_bounds__(256) void k_xa_prep(XaPrepArgs a) {
     *reinterpret_cast<uint4*>(a.xa + xa_index(m, k0 + 8 * g, 0)) = hi;
     *reinterpret_cast<uint4*>(a.xa + xa_index(m, k0 + 8 * g, 1)) = lo;
   }
-  ss += __shfl_xor(ss, 1);
-  ss += __shfl_xor(ss, 2);
-  if (t % 4 == 0) a.ss[blockIdx.x * 64 + m] = ss;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+  if (t % 16 == 0) a.ss[blockIdx.x * 64 + m] = ss;
 }
 
 // ------------------------------------------------------------------ streaming skinny GEMM
@@ -105,7 +109,6 @@ __global__ __launch_bounds__(256) void k_xa_prep(XaPrepArgs a) {
 enum SkEpi { kSkRaw = 0, kSkStore = 1, kSkResidual = 2, kSkSiluPair = 3, kSkQkvHead = 4 };
 constexpr int kSkMaxSeg = 3;
 constexpr int kSkP = 8;            // k steps of weights / activations in flight
-constexpr int kSkCtrStride = 32;   // one 128-byte line per column-range counter
 
 struct SkArgs {
   const uint16_t* xa;  // fragment-major activations, K / 32 steps
@@ -124,8 +127,7 @@ struct SkArgs {
   uint16_t* xa_next;         // optional: the output as the next projection's activations
   const uint16_t* gain_next; // its RMSNorm gain (NULL = none)
   float* ss_next;            // with xa_next: per-row sums of squares of the output, [gridDim.x][64]
-  float* part;               // ks > 1: [ks][64][cols] partials
-  unsigned int* ctr;         // ks > 1: one counter per column range
+  float* part;               // ks > 1: [ks][64][cols] partials (summed by k_mm_fix)
   // kSkQkvHead (column ranges of one 128-wide head): q / k heads get their
   // RMSNorm (q_gain / k_gain) and rotate-half RoPE at the row's position; q
   // rows land in out [M][ldo], k / v rows in the cache at slot offset + row
@@ -139,178 +141,33 @@ struct SkArgs {
   int kv_bf16, cap;
 };
 
-// Block (column range cb, K split kz), 4 waves.  TW = tiles of 16 weight rows
-// per wave (block columns FB = 64 TW); wave w owns tiles w TW .. w TW + TW - 1
-// (the SiLU pair: wave w's gate tile and up tile of act features 64 cb + 16 w ..).
-template <int MT, int TW>
-__global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
-  constexpr int FB = 64 * TW;
-  constexpr int AQ = MT * 128;                // uint4 of activations per k step
-  constexpr int AR = (AQ + 255) / 256;        // per thread
-  constexpr int LDC = FB + 4;
-  __shared__ __attribute__((aligned(16))) uint4 s_a[3][AQ];
-  __shared__ float s_c[64 * LDC];
-  __shared__ float s_inv[64];
-  __shared__ bool s_last;
-  const int t = threadIdx.x, lane = t % kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-  const int cb = blockIdx.x, kz = blockIdx.y;
+// Operands of the epilogue that do not depend on the tile: the row scale's
+// partial sums of squares (thread t sums parts t % 4 + 4 q of row t / 4), the
+// residuals and the next gains of the thread's columns.  Loaded on their own so
+// that a caller can issue them before the loads the tile waits on.
+constexpr int kSsMax = 16;  // row-scale parts <= 64
+template <int TW>
+struct EpiOps {
+  float ssv[kSsMax], resv[16 * TW];
+  uint16_t gnv[16 * TW];
+};
+
+template <int TW>
+__device__ __forceinline__ void sk_epi_load(const SkArgs& a, int cb, EpiOps<TW>& o) {
+  constexpr int FB = 64 * TW, CQ = FB / 4;
+  const int t = threadIdx.x;
   const bool pair = a.epi == kSkSiluPair;
-
-  const uint16_t* wp[TW];
-#pragma unroll
-  for (int j = 0; j < TW; ++j) {
-    int row = pair ? (j == 0 ? 0 : a.N / 2) + cb * 64 + wave * 16 + lane % 16
-                   : cb * FB + (wave * TW + j) * 16 + lane % 16;
-    row = min(row, a.N - 1);
-    int seg = 0;
-#pragma unroll
-    for (int q = 1; q < kSkMaxSeg; ++q)
-      if (q < a.n_seg && row >= a.seg_start[q]) seg = q;
-    const uint16_t* base = seg == 0 ? a.w[0] : seg == 1 ? a.w[1] : a.w[2];
-    const int s0r = seg == 0 ? a.seg_start[0] : seg == 1 ? a.seg_start[1] : a.seg_start[2];
-    wp[j] = base + static_cast<int64_t>(row - s0r) * a.K + (lane / 16) * 8;
-  }
-  const int S = a.K / 32, per = (S + a.ks - 1) / a.ks;
-  const int s0 = min(S, kz * per), ns = min(S, s0 + per) - s0;
-
-  af32x4 acc[TW][MT];
-#pragma unroll
-  for (int j = 0; j < TW; ++j)
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[j][i] = af32x4{0.f, 0.f, 0.f, 0.f};
-  // P steps of weights and activations in flight; the activations of step i
-  // are staged in LDS slot i % 3 just before step i's barrier (the barrier of
-  // step i - 1 guarantees every wave is done with the slot, last read by step
-  // i - 3).  Native vectors (not the uint4 struct) keep the buffers in registers.
-  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
-  uint4 wb[kSkP][TW];
-  u32x4v ab[kSkP][AR];
-#pragma unroll
-  for (int u = 0; u < kSkP; ++u) {
-    if (u < ns) {
-#pragma unroll
-      for (int j_ = 0; j_ < TW; ++j_) wb[u][j_] = *reinterpret_cast<const uint4*>(wp[j_] + static_cast<int64_t>(s0 + u) * 32);
-      const uint4* ap_ = reinterpret_cast<const uint4*>(a.xa + static_cast<int64_t>(s0 + u) * kXaStepElems);
-#pragma unroll
-      for (int r_ = 0; r_ < AR; ++r_) ab[u][r_] = reinterpret_cast<const u32x4v*>(ap_)[(t + r_ * 256) % AQ];
-    }
-  }
-  for (int b = 0; b < ns; b += kSkP) {
-#pragma unroll
-    for (int u = 0; u < kSkP; ++u) {
-      const int i = b + u;
-      if (i < ns) {
-        const int slot = i % 3;
-#pragma unroll
-        for (int r_ = 0; r_ < AR; ++r_) reinterpret_cast<u32x4v*>(s_a[slot])[(t + r_ * 256) % AQ] = ab[u][r_];
-        lds_barrier();
-        abf16x8 ah[MT], al[MT];
-#pragma unroll
-        for (int q = 0; q < MT; ++q) {
-          ah[q] = __builtin_bit_cast(abf16x8, s_a[slot][(2 * q) * 64 + lane]);
-          al[q] = __builtin_bit_cast(abf16x8, s_a[slot][(2 * q + 1) * 64 + lane]);
-        }
-#pragma unroll
-        for (int q = 0; q < MT; ++q)
-#pragma unroll
-          for (int j = 0; j < TW; ++j)
-            acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[q], __builtin_bit_cast(abf16x8, wb[u][j]),
-                                                                acc[j][q], 0, 0, 0);
-#pragma unroll
-        for (int q = 0; q < MT; ++q)
-#pragma unroll
-          for (int j = 0; j < TW; ++j)
-            acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[q], __builtin_bit_cast(abf16x8, wb[u][j]),
-                                                                acc[j][q], 0, 0, 0);
-        if (i + kSkP < ns) {
-#pragma unroll
-          for (int j_ = 0; j_ < TW; ++j_) wb[u][j_] = *reinterpret_cast<const uint4*>(wp[j_] + static_cast<int64_t>(s0 + i + kSkP) * 32);
-          const uint4* ap_ = reinterpret_cast<const uint4*>(a.xa + static_cast<int64_t>(s0 + i + kSkP) * kXaStepElems);
-#pragma unroll
-          for (int r_ = 0; r_ < AR; ++r_) ab[u][r_] = reinterpret_cast<const u32x4v*>(ap_)[(t + r_ * 256) % AQ];
-        }
-      }
-    }
-  }
-
-  // the block's tile -> LDS: row i 16 + 4 (lane / 16) + e, column (w TW + j) 16 + lane % 16
-  mfma_settle();
-#pragma unroll
-  for (int j = 0; j < TW; ++j)
-#pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        s_c[(i * 16 + (lane / 16) * 4 + e) * LDC + (wave * TW + j) * 16 + lane % 16] = acc[j][i][e];
-  __syncthreads();
-
-  const int m = t / 4, g = t % 4;  // epilogue: row m, column quarter g
-  constexpr int CQ = FB / 4;
-  const int n0 = pair ? cb * 64 + g * 16 : cb * FB + g * CQ;  // first output column of this thread
-  if (a.ks > 1) {
-    // publish this split's tile (a wave per row, lanes along the columns, so
-    // every store is one contiguous run); the last split of the column range
-    // sums the ks tiles in a fixed order
-    const int cols = gridDim.x * FB;
-    float* base = a.part + static_cast<int64_t>(cb) * FB;
-    for (int r = wave; r < a.M; r += 4)
-#pragma unroll
-      for (int c = lane; c < FB; c += kWave)
-        publish_f32(base + (static_cast<int64_t>(kz) * 64 + r) * cols + c, s_c[r * LDC + c]);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (t == 0) {
-      unsigned int* ctr = a.ctr + cb * kSkCtrStride;
-      const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                        static_cast<unsigned int>(a.ks - 1);
-      if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // element e = t + 256 i of the row-major M x FB tile, 16 elements and two
-    // splits per round
-    constexpr int EPT = 64 * FB / 256, EH = EPT > 16 ? 16 : EPT;
-#pragma unroll
-    for (int i0 = 0; i0 < EPT; i0 += EH) {
-      float v[EH];
-#pragma unroll
-      for (int i = 0; i < EH; ++i) v[i] = 0.f;
-      for (int z = 0; z < a.ks; z += 2) {
-        float u0[EH], u1[EH];
-#pragma unroll
-        for (int i = 0; i < EH; ++i) {
-          const int e = t + 256 * (i0 + i), r = min(e / FB, a.M - 1), c = e % FB;
-          const float* q = base + (static_cast<int64_t>(z) * 64 + r) * cols + c;
-          u0[i] = fetch_f32(q);
-          u1[i] = z + 1 < a.ks ? fetch_f32(q + 64 * static_cast<int64_t>(cols)) : 0.f;
-        }
-#pragma unroll
-        for (int i = 0; i < EH; ++i) v[i] += u0[i] + u1[i];
-      }
-#pragma unroll
-      for (int i = 0; i < EH; ++i) {
-        const int e = t + 256 * (i0 + i);
-        s_c[(e / FB) * LDC + e % FB] = v[i];
-      }
-    }
-    __syncthreads();
-  }
-  // epilogue operands in one batch: the row scale's partial sums of squares
-  // (thread t sums parts t % 4 + 4 q of row t / 4), residuals, next gains
-  constexpr int kSsMax = 16;  // row-scale parts <= 64
+  const int m = t / 4, g = t % 4;
+  const int n0 = pair ? cb * 64 + g * 16 : cb * FB + g * CQ;
   const int mr = min(m, a.M - 1);
-  float ssv[kSsMax], resv[CQ];
-  uint16_t gnv[CQ];
 #pragma unroll
   for (int q = 0; q < kSsMax; ++q) {
     const int pp = g + 4 * q;
-    ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + m] : 0.f;
+    o.ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + m] : 0.f;
   }
 #pragma unroll
   for (int c = 0; c < CQ; ++c)
-    resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + min(n0 + c, a.N - 1)] : 0.f;
+    o.resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + min(n0 + c, a.N - 1)] : 0.f;
   if (a.xa_next && a.gain_next) {  // every gain load issued before the first is used
     uint32_t gw[CQ];
 #pragma unroll
@@ -318,11 +175,31 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
 #pragma unroll
     for (int c = 0; c < CQ; ++c) pin(gw[c]);
 #pragma unroll
-    for (int c = 0; c < CQ; ++c) gnv[c] = (!pair || c < 16) ? static_cast<uint16_t>(gw[c]) : 0;
+    for (int c = 0; c < CQ; ++c) o.gnv[c] = (!pair || c < 16) ? static_cast<uint16_t>(gw[c]) : 0;
   } else {
 #pragma unroll
-    for (int c = 0; c < CQ; ++c) gnv[c] = 0;
+    for (int c = 0; c < CQ; ++c) o.gnv[c] = 0;
   }
+}
+
+// Epilogue of a column range for rows [r0, r1) of the tile in s_c (row r,
+// column c at s_c[r * (FB + 4) + c]): the row scale, then store / residual /
+// SiLU(gate) * up / the next activations, or the QKV head epilogue.  Every
+// thread of the block calls it; rows outside [r0, r1) or >= M write nothing.
+template <int TW>
+__device__ __forceinline__ void sk_epi_run(const SkArgs& a, float* s_c, float* s_inv, int cb, int r0, int r1,
+                                           const EpiOps<TW>& ops) {
+  constexpr int FB = 64 * TW;
+  constexpr int LDC = FB + 4;
+  const int t = threadIdx.x;
+  const bool pair = a.epi == kSkSiluPair;
+  const int m = t / 4, g = t % 4;  // row m, column quarter g
+  const bool live = m < a.M && m >= r0 && m < r1;
+  constexpr int CQ = FB / 4;
+  const int n0 = pair ? cb * 64 + g * 16 : cb * FB + g * CQ;  // first output column of this thread
+  const float* ssv = ops.ssv;
+  const float* resv = ops.resv;
+  const uint16_t* gnv = ops.gnv;
   {
     float tot = 0.f;
 #pragma unroll
@@ -362,7 +239,7 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
       }
     }
     __syncthreads();
-    if (m >= a.M) return;
+    if (!live) return;
     const int pos = min(max(a.positions ? a.positions[m] : offset + m, 0), a.rope_max - 1);
     if (is_q || is_k) {
 #pragma unroll
@@ -396,7 +273,7 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
     }
     return;
   }
-  if (m >= a.M) return;
+  if (!live) return;
   const float inv = s_inv[m];
   // this thread's outputs: 8-wide groups of consecutive output columns
   constexpr int NC = CQ < 16 ? CQ : 16;  // the pair's outputs per thread
@@ -450,20 +327,302 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
   }
 }
 
+template <int TW>
+__device__ __forceinline__ void sk_epilogue(const SkArgs& a, float* s_c, float* s_inv, int cb, int r0, int r1) {
+  EpiOps<TW> ops;
+  sk_epi_load<TW>(a, cb, ops);
+  sk_epi_run<TW>(a, s_c, s_inv, cb, r0, r1, ops);
+}
+
+// Block (column range cb, K split kz), 4 waves.  TW = tiles of 16 weight rows
+// per wave (block columns FB = 64 TW); wave w owns tiles w TW .. w TW + TW - 1
+// (the SiLU pair: wave w's gate tile and up tile of act features 64 cb + 16 w ..).
+template <int MT, int TW>
+__global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
+  constexpr int FB = 64 * TW;
+  constexpr int AQ = MT * 128;                // uint4 of activations per k step
+  constexpr int AR = (AQ + 255) / 256;        // per thread
+  constexpr int LDC = FB + 4;
+  __shared__ __attribute__((aligned(16))) uint4 s_a[3][AQ];
+  __shared__ __attribute__((aligned(16))) float s_c[64 * LDC];
+  __shared__ float s_inv[64];
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int cb = blockIdx.x, kz = blockIdx.y;
+  const bool pair = a.epi == kSkSiluPair;
+
+  // weights are fragment-major (wc_weights_frag): the A fragment of 16-row
+  // tile T at k step s is 64 lanes x 8 bf16 at ((T S + s) 64 + lane) 8, so
+  // every weight load is one contiguous kilobyte
+  const int S = a.K / 32, per = (S + a.ks - 1) / a.ks;
+  const uint16_t* wp[TW];
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    int tb = pair ? (j == 0 ? 0 : a.N / 2) + cb * 64 + wave * 16 : cb * FB + (wave * TW + j) * 16;
+    tb = min(tb, ((a.N + 15) / 16 - 1) * 16);  // a tile past the last one re-reads it (its columns are not stored)
+    int seg = 0;
+#pragma unroll
+    for (int q = 1; q < kSkMaxSeg; ++q)
+      if (q < a.n_seg && tb >= a.seg_start[q]) seg = q;
+    const uint16_t* base = seg == 0 ? a.w[0] : seg == 1 ? a.w[1] : a.w[2];
+    const int s0r = seg == 0 ? a.seg_start[0] : seg == 1 ? a.seg_start[1] : a.seg_start[2];
+    wp[j] = base + (static_cast<int64_t>((tb - s0r) >> 4) * S * 64 + lane) * 8;
+  }
+  const int s0 = min(S, kz * per), ns = min(S, s0 + per) - s0;
+
+  af32x4 acc[TW][MT];
+#pragma unroll
+  for (int j = 0; j < TW; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) acc[j][i] = af32x4{0.f, 0.f, 0.f, 0.f};
+  // P steps of weights and activations in flight; the activations of step i
+  // are staged in LDS slot i % 3 just before step i's barrier (the barrier of
+  // step i - 1 guarantees every wave is done with the slot, last read by step
+  // i - 3).  Native vectors (not the uint4 struct) keep the buffers in registers.
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  uint4 wb[kSkP][TW];
+  u32x4v ab[kSkP][AR];
+#pragma unroll
+  for (int u = 0; u < kSkP; ++u) {
+    if (u < ns) {
+#pragma unroll
+      for (int j_ = 0; j_ < TW; ++j_) wb[u][j_] = *reinterpret_cast<const uint4*>(wp[j_] + static_cast<int64_t>(s0 + u) * 512);
+      const uint4* ap_ = reinterpret_cast<const uint4*>(a.xa + static_cast<int64_t>(s0 + u) * kXaStepElems);
+#pragma unroll
+      for (int r_ = 0; r_ < AR; ++r_) ab[u][r_] = reinterpret_cast<const u32x4v*>(ap_)[(t + r_ * 256) % AQ];
+    }
+  }
+  for (int b = 0; b < ns; b += kSkP) {
+#pragma unroll
+    for (int u = 0; u < kSkP; ++u) {
+      const int i = b + u;
+      if (i < ns) {
+        const int slot = i % 3;
+#pragma unroll
+        for (int r_ = 0; r_ < AR; ++r_) reinterpret_cast<u32x4v*>(s_a[slot])[(t + r_ * 256) % AQ] = ab[u][r_];
+        lds_barrier();
+        abf16x8 ah[MT], al[MT];
+#pragma unroll
+        for (int q = 0; q < MT; ++q) {
+          ah[q] = __builtin_bit_cast(abf16x8, s_a[slot][(2 * q) * 64 + lane]);
+          al[q] = __builtin_bit_cast(abf16x8, s_a[slot][(2 * q + 1) * 64 + lane]);
+        }
+#pragma unroll
+        for (int q = 0; q < MT; ++q)
+#pragma unroll
+          for (int j = 0; j < TW; ++j)
+            acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[q], __builtin_bit_cast(abf16x8, wb[u][j]),
+                                                                acc[j][q], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < MT; ++q)
+#pragma unroll
+          for (int j = 0; j < TW; ++j)
+            acc[j][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[q], __builtin_bit_cast(abf16x8, wb[u][j]),
+                                                                acc[j][q], 0, 0, 0);
+        if (i + kSkP < ns) {
+#pragma unroll
+          for (int j_ = 0; j_ < TW; ++j_) wb[u][j_] = *reinterpret_cast<const uint4*>(wp[j_] + static_cast<int64_t>(s0 + i + kSkP) * 512);
+          const uint4* ap_ = reinterpret_cast<const uint4*>(a.xa + static_cast<int64_t>(s0 + i + kSkP) * kXaStepElems);
+#pragma unroll
+          for (int r_ = 0; r_ < AR; ++r_) ab[u][r_] = reinterpret_cast<const u32x4v*>(ap_)[(t + r_ * 256) % AQ];
+        }
+      }
+    }
+  }
+
+  // the block's tile -> LDS: row i 16 + 4 (lane / 16) + e, column (w TW + j) 16 + lane % 16
+  mfma_settle();
+#pragma unroll
+  for (int j = 0; j < TW; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        s_c[(i * 16 + (lane / 16) * 4 + e) * LDC + (wave * TW + j) * 16 + lane % 16] = acc[j][i][e];
+  __syncthreads();
+
+  if (a.ks > 1) {
+    // this split's tile, rows < M, as plain coalesced stores (a wave per row,
+    // lanes along the columns); k_mm_fix sums the splits after the launch
+    const int cols = gridDim.x * FB;
+    float* base = a.part + static_cast<int64_t>(cb) * FB;
+    for (int r = wave; r < a.M; r += 4)
+#pragma unroll
+      for (int c = lane * 4; c < FB; c += kWave * 4)
+        *reinterpret_cast<float4*>(base + (static_cast<int64_t>(kz) * 64 + r) * cols + c) =
+            *reinterpret_cast<const float4*>(&s_c[r * LDC + c]);
+    return;
+  }
+  sk_epilogue<TW>(a, s_c, s_inv, cb, 0, 64);
+}
+
+// Barrier-free skinny GEMM for the layer's projections.  Block (column group
+// cg, K split kz), 4 waves; the group is G 16-column tiles, tile tau covering
+// output columns 16 tau .. 16 tau + 15 (the SiLU pair interleaves gate and up
+// tiles: tau = 8 cb + 2 w + j is gate (j = 0) or up (j = 1) rows
+// 64 cb + 16 w ..).  Wave w takes the split's k steps w, w + 4, ..., so the
+// four waves read each tile's consecutive fragment-major kilobytes together.
+// Per k step a wave loads its G weight fragments and the 2 MT activation
+// fragments straight into registers (each load one contiguous kilobyte) and
+// runs 2 MT G MFMAs: every activation fragment feeds G tiles, with no LDS and
+// no barrier in the loop.  The four waves' tiles are summed in LDS in wave
+// order and stored as this split's partial (k_mm_fix sums the splits and runs
+// the epilogue).
+constexpr int kMwG = 4;  // column tiles per block
+constexpr int kMwP = 3;  // k steps in flight per wave
+
+template <int MT>
+__global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
+  constexpr int G = kMwG, FB = 16 * G, LDR = FB + 4;
+  typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) float s_red[4][64 * LDR];
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int cg = blockIdx.x, kz = blockIdx.y;
+  const bool pair = a.epi == kSkSiluPair;
+  const int S = a.K / 32, per = (S + a.ks - 1) / a.ks;
+  const int sb = min(S, kz * per), se = min(S, sb + per);
+  const int nw = sb + wave < se ? (se - sb - wave + 3) / 4 : 0;  // this wave's steps
+  const uint16_t* wp[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int tau = cg * G + g;
+    int tb = pair ? ((tau & 1) ? a.N / 2 : 0) + 64 * (tau >> 3) + 16 * ((tau >> 1) & 3) : 16 * tau;
+    tb = min(tb, ((a.N + 15) / 16 - 1) * 16);
+    int seg = 0;
+#pragma unroll
+    for (int q = 1; q < kSkMaxSeg; ++q)
+      if (q < a.n_seg && tb >= a.seg_start[q]) seg = q;
+    const uint16_t* base = seg == 0 ? a.w[0] : seg == 1 ? a.w[1] : a.w[2];
+    const int s0r = seg == 0 ? a.seg_start[0] : seg == 1 ? a.seg_start[1] : a.seg_start[2];
+    wp[g] = base + (static_cast<int64_t>((tb - s0r) >> 4) * S * 64 + lane) * 8;
+  }
+  const u32x4v* xa4 = reinterpret_cast<const u32x4v*>(a.xa);
+  af32x4 acc[G][MT];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int q = 0; q < MT; ++q) acc[g][q] = af32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4v wb[kMwP][G], ab[kMwP][2 * MT];
+  auto issue = [&](int slot, int i) {
+    const int st = min(sb + wave + 4 * i, S - 1);
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      wb[slot][g] = *reinterpret_cast<const u32x4v*>(wp[g] + static_cast<int64_t>(st) * 512);
+#pragma unroll
+    for (int h = 0; h < 2 * MT; ++h)
+      ab[slot][h] = xa4[static_cast<int64_t>(st) * (kXaStepElems / 8) + h * 64 + lane];
+  };
+#pragma unroll
+  for (int u = 0; u < kMwP; ++u)
+    if (u < nw) issue(u, u);
+  for (int b = 0; b < nw; b += kMwP) {
+#pragma unroll
+    for (int u = 0; u < kMwP; ++u) {
+      const int i = b + u;
+      if (i < nw) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int q = 0; q < MT; ++q)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+              acc[g][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, ab[u][2 * q + h]),
+                                                                 __builtin_bit_cast(abf16x8, wb[u][g]), acc[g][q], 0,
+                                                                 0, 0);
+        if (i + kMwP < nw) issue(u, i + kMwP);
+      }
+    }
+  }
+  // the wave's tile -> LDS (row 16 q + 4 (lane / 16) + e, column 16 g + lane % 16)
+  mfma_settle();
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int q = 0; q < MT; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s_red[wave][(q * 16 + (lane / 16) * 4 + e) * LDR + g * 16 + lane % 16] = acc[g][q][e];
+  __syncthreads();
+  // four waves summed in order; rows < M as this split's partial
+  const int cols = gridDim.x * FB;
+  float* base = a.part + static_cast<int64_t>(cg) * FB;
+  for (int e = t * 4; e < a.M * FB; e += 256 * 4) {
+    const int r = e / FB, c = e % FB;
+    float4 v = *reinterpret_cast<const float4*>(&s_red[0][r * LDR + c]);
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      const float4 o = *reinterpret_cast<const float4*>(&s_red[w][r * LDR + c]);
+      v.x += o.x;
+      v.y += o.y;
+      v.z += o.z;
+      v.w += o.w;
+    }
+    *reinterpret_cast<float4*>(base + (static_cast<int64_t>(kz) * 64 + r) * cols + c) = v;
+  }
+}
+
+// The split-K fix-up of a column range and a quarter of the rows: the ks
+// partial tiles summed in split order (deterministic), then the epilogue.
+// Launched after k_mm_stream, so plain loads see every split's stores.
+template <int TW>
+__global__ __launch_bounds__(256) void k_mm_fix(SkArgs a) {
+  constexpr int FB = 64 * TW;
+  constexpr int LDC = FB + 4;
+  constexpr int V4 = 16 * FB / 4 / 256;  // float4 per thread: 16 rows x FB columns
+  __shared__ __attribute__((aligned(16))) float s_c[64 * LDC];
+  __shared__ float s_inv[64];
+  const int t = threadIdx.x, cb = blockIdx.x, r0 = blockIdx.y * 16;
+  const int cols = gridDim.x * FB;
+  const float* base = a.part + static_cast<int64_t>(cb) * FB;
+  EpiOps<TW> ops;  // issued first: one round trip covers them and the partials
+  sk_epi_load<TW>(a, cb, ops);
+  float4 acc[V4];
+#pragma unroll
+  for (int i = 0; i < V4; ++i) acc[i] = float4{0.f, 0.f, 0.f, 0.f};
+  for (int z = 0; z < a.ks; z += 8) {  // up to eight splits' loads in flight per round
+    float4 u[8][V4];
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+#pragma unroll
+      for (int i = 0; i < V4; ++i) {
+        const int e = (t + 256 * i) * 4, r = min(r0 + e / FB, a.M - 1), c = e % FB;
+        const int zz = min(z + h, a.ks - 1);
+        u[h][i] = *reinterpret_cast<const float4*>(base + (static_cast<int64_t>(zz) * 64 + r) * cols + c);
+      }
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+      if (z + h < a.ks)
+#pragma unroll
+        for (int i = 0; i < V4; ++i) {
+          acc[i].x += u[h][i].x;
+          acc[i].y += u[h][i].y;
+          acc[i].z += u[h][i].z;
+          acc[i].w += u[h][i].w;
+        }
+  }
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int e = (t + 256 * i) * 4, r = r0 + e / FB, c = e % FB;
+    *reinterpret_cast<float4*>(&s_c[r * LDC + c]) = acc[i];
+  }
+  __syncthreads();
+  sk_epi_run<TW>(a, s_c, s_inv, cb, r0, r0 + 16, ops);
+}
+
 struct GemmPlan {
   int tw, cols, ks;
 };
 
 // Column ranges of 64 TW weight rows (TW = 2 for the SiLU pair and wide
-// projections), K split into at most 6 parts so that about 192-256 blocks run
-// with >= 16 k steps each (split-K partials cost 8 ks M bytes per weight row
-// against 2 K bytes of weights).
+// projections), K split into at most 8 parts of >= 8 k steps so that about
+// 256 blocks stream at once (each split stores an M x 64 TW fp32 tile that
+// k_mm_fix sums: 8 ks M bytes per weight row against 2 K bytes of weights).
 static GemmPlan plan_gemm(int n_rows, int K, bool pair, int tw = 0) {
   GemmPlan p{};
   p.tw = tw ? tw : (pair || n_rows >= 8192) ? 2 : 1;
   p.cols = pair ? n_rows / 2 / 64 : (n_rows + 64 * p.tw - 1) / (64 * p.tw);
   const int steps = K / 32;
-  p.ks = std::max(1, std::min(std::min(6, steps / 16), (224 + p.cols - 1) / p.cols));
+  p.ks = std::max(1, std::min(std::min(8, steps / 8), (256 + p.cols - 1) / p.cols));
   return p;
 }
 
@@ -477,21 +636,57 @@ static int launch_stream_t(const SkArgs& g, const GemmPlan& p, hipStream_t s) {
     default: hipLaunchKernelGGL((k_mm_stream<4, TW>), grid, dim3(256), 0, s, g); break;
   }
   WC_LAUNCHED();
+  if (p.ks > 1) {
+    hipLaunchKernelGGL((k_mm_fix<TW>), dim3(p.cols, (g.M + 15) / 16), dim3(256), 0, s, g);
+    WC_LAUNCHED();
+  }
   return WC_OK;
 }
 
 static int launch_stream(SkArgs g, const GemmPlan& p, hipStream_t s) {
   WC_REQUIRE(g.M >= 1 && g.M <= 64, "target layer: rows must be in 1..64");
   WC_REQUIRE(g.K % 256 == 0, "target layer: K %d must be a multiple of 256", g.K);
+  WC_REQUIRE(g.N >= 1, "target layer: no weight rows");
   WC_REQUIRE(g.n_ss <= 64, "target layer: at most 64 row-scale parts");
   g.ks = p.ks;
   return p.tw == 2 ? launch_stream_t<2>(g, p, s) : launch_stream_t<1>(g, p, s);
 }
 
+// k_mm_wave over column groups of 64 and K splits (so that about 256 blocks run
+// with >= 4 k steps each), then k_mm_fix with column ranges of 64 fix_tw (the
+// epilogue's own width: one 128-wide head for QKV, 64 act features for the pair).
+static int wave_ks(int N, int K) {
+  const int cg = N / (16 * kMwG), steps = K / 32;
+  return std::max(1, std::min(std::min(8, steps / 4), (256 + cg - 1) / cg));
+}
+
+static int launch_wave(SkArgs g, int fix_tw, hipStream_t s) {
+  WC_REQUIRE(g.M >= 1 && g.M <= 64, "target layer: rows must be in 1..64");
+  WC_REQUIRE(g.K % 256 == 0, "target layer: K %d must be a multiple of 256", g.K);
+  WC_REQUIRE(g.N % (64 * fix_tw) == 0, "target layer: %d weight rows must be a multiple of %d", g.N, 64 * fix_tw);
+  WC_REQUIRE(g.n_ss <= 64, "target layer: at most 64 row-scale parts");
+  g.ks = wave_ks(g.N, g.K);
+  const dim3 grid(g.N / (16 * kMwG), g.ks);
+  switch ((g.M + 15) / 16) {
+    case 1: hipLaunchKernelGGL((k_mm_wave<1>), grid, dim3(256), 0, s, g); break;
+    case 2: hipLaunchKernelGGL((k_mm_wave<2>), grid, dim3(256), 0, s, g); break;
+    case 3: hipLaunchKernelGGL((k_mm_wave<3>), grid, dim3(256), 0, s, g); break;
+    default: hipLaunchKernelGGL((k_mm_wave<4>), grid, dim3(256), 0, s, g); break;
+  }
+  WC_LAUNCHED();
+  const dim3 fgrid(g.N / (64 * fix_tw), (g.M + 15) / 16);
+  if (fix_tw == 2)
+    hipLaunchKernelGGL((k_mm_fix<2>), fgrid, dim3(256), 0, s, g);
+  else
+    hipLaunchKernelGGL((k_mm_fix<1>), fgrid, dim3(256), 0, s, g);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
 static int launch_xa_prep(const float* x, int64_t ldx, int M, int K, const uint16_t* gain, uint16_t* xa, float* ss,
                           hipStream_t s) {
   XaPrepArgs a{x, ldx, M, K, gain, xa, ss};
-  hipLaunchKernelGGL(k_xa_prep, dim3(K / 256), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_xa_prep, dim3(K / 256, 4), dim3(256), 0, s, a);
   WC_LAUNCHED();
   return WC_OK;
 }
@@ -516,6 +711,7 @@ constexpr int kVaLdT = kVaCH + 8;    // row stride (bf16) of the transposed V ch
 constexpr int kVaLdP = kVaCH + 4;    // row stride (fp32) of a wave's P tile
 constexpr int kVaGroup = 64;         // query vectors per block
 constexpr int kVaMaxRows = 64;       // rows per launch (mask rows staged per chunk)
+constexpr int kVaMaxSplits = kMaxSplits;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct VaChunk {
@@ -741,15 +937,35 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 
 static int launch_verify_attention(const AttnArgs& a, int splits, hipStream_t s) {
   WC_REQUIRE(a.rows >= 1 && a.rows <= kVaMaxRows, "verify attention: rows must be in 1..%d", kVaMaxRows);
+  WC_REQUIRE(splits >= 1 && splits <= kVaMaxSplits, "verify attention: 1..%d splits", kVaMaxSplits);
   const int qvb = a.rows * (a.H / a.Hk);
   WC_REQUIRE(a.qv_ld >= qvb, "verify attention: partial stride too small");
   const unsigned groups = static_cast<unsigned>((qvb + kVaGroup - 1) / kVaGroup);
   hipLaunchKernelGGL(k_verify_attention<0>, dim3(splits, a.Hk, groups), dim3(kAttnThreads), 0, s, a);
   WC_LAUNCHED();
-  hipLaunchKernelGGL((k_attn_merge<kVaD>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, s, a,
-                     splits);
+  hipLaunchKernelGGL((k_attn_merge<kVaD, kVaMaxSplits>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads),
+                     0, s, a, splits);
   WC_LAUNCHED();
   return WC_OK;
+}
+
+// ------------------------------------------------------------------ weight layout
+// W [rows][cols] bf16 row-major -> fragment-major: chunk c = (T S + s) 64 + l
+// (S = cols / 32) holds W[16 T + l % 16][32 s + 8 (l / 16) .. + 8], the A
+// fragment lane l of v_mfma_f32_16x16x32_bf16 needs for 16-row tile T at k step s.
+__global__ __launch_bounds__(256) void k_frag_layout(const uint16_t* __restrict__ w, int rows, int cols,
+                                                     uint16_t* __restrict__ out) {
+  const int64_t chunks = static_cast<int64_t>(rows) * cols / 8;
+  const int S = cols / 32;
+  for (int64_t c = blockIdx.x * 256ll + threadIdx.x; c < chunks; c += static_cast<int64_t>(gridDim.x) * 256) {
+    const int l = static_cast<int>(c % 64);
+    const int64_t ts = c / 64;
+    const int s = static_cast<int>(ts % S);
+    const int64_t T = ts / S;
+    const int64_t row = 16 * T + l % 16;
+    const int col = 32 * s + 8 * (l / 16);
+    *reinterpret_cast<uint4*>(out + c * 8) = *reinterpret_cast<const uint4*>(w + row * cols + col);
+  }
 }
 
 // ------------------------------------------------------------------ embedding
@@ -767,7 +983,6 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__
 struct TargetWs {
   uint16_t *xa_x, *xa_attn, *xa_h1, *xa_act;
   float *ss_x, *ss_h1, *qkv, *q, *attn, *h1, *part, *apart;
-  unsigned int* ctr;
   size_t bytes;
 };
 
@@ -808,15 +1023,19 @@ static TargetWs target_ws(const wc_drafter_dims& d, int max_rows, void* base) {
   w.q = reinterpret_cast<float*>(take(4 * M * nq));
   w.attn = reinterpret_cast<float*>(take(4 * M * nq));
   w.h1 = reinterpret_cast<float*>(take(4 * M * d.hidden));
-  size_t part = 0, cols = 0;
+  size_t part = 0;
   for (const GemmPlan* g : {&pl.qkv, &pl.o, &pl.gu, &pl.down}) {
     part = std::max(part, static_cast<size_t>(g->ks) * 64 * g->cols * 64 * g->tw);
-    cols = std::max(cols, static_cast<size_t>(g->cols));
   }
+  for (const int* nk : {std::array<int, 2>{static_cast<int>(nqkv), d.hidden}.data(),
+                        std::array<int, 2>{d.hidden, static_cast<int>(nq)}.data(),
+                        std::array<int, 2>{2 * d.inter, d.hidden}.data(),
+                        std::array<int, 2>{d.hidden, d.inter}.data()})
+    part = std::max(part, static_cast<size_t>(wave_ks(nk[0], nk[1])) * 64 * nk[0]);
   w.part = reinterpret_cast<float*>(take(4 * part));
-  w.ctr = reinterpret_cast<unsigned int*>(take(4 * kSkCtrStride * cols));
   const size_t qv = M * static_cast<size_t>(d.heads / std::max(d.kv_heads, 1));
-  w.apart = reinterpret_cast<float*>(take(4 * static_cast<size_t>(d.kv_heads) * kMaxSplits * qv * (d.head_dim + 2)));
+  w.apart = reinterpret_cast<float*>(
+      take(4 * static_cast<size_t>(d.kv_heads) * std::max(kMaxSplits, kVaMaxSplits) * qv * (d.head_dim + 2)));
   w.bytes = off;
   return w;
 }
@@ -889,7 +1108,6 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.out = verify_path ? ws.q : ws.qkv;
   g.ldo = verify_path ? nq : nqkv;
   g.part = ws.part;
-  g.ctr = ws.ctr;
   if (verify_path) {
     // head_dim 128 with a bf16 cache: the QKV epilogue normalises / rotates q
     // and k and appends K / V, so the attention reads every key from the cache
@@ -907,7 +1125,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     g.kv_bf16 = 1;
     g.cap = capacity;
   }
-  if (int rc = launch_stream(g, pl.qkv, s)) return rc;
+  if (int rc = launch_wave(g, 2, s)) return rc;
 
   const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunkMax - 1) / kAttnChunkMax));
   if (verify_path) {
@@ -931,8 +1149,9 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     at.out = ws.attn;
     at.ld_out = nq;
     at.xa_out = ws.xa_attn;
-    // about two chunks of keys per split
-    const int vsplits = std::max(1, std::min(kMaxSplits, (capacity + 2 * kVaCH - 1) / (2 * kVaCH)));
+    // about two chunks of keys per split (one chunk per split measured no faster:
+    // the split's fixed costs dominate, and the merge then reads twice the partials)
+    const int vsplits = std::max(1, std::min(kVaMaxSplits, (capacity + 2 * kVaCH - 1) / (2 * kVaCH)));
     if (int rc = launch_verify_attention(at, vsplits, s)) return rc;
   } else {
     // other head sizes / an fp32 cache: the decode attention over tiles of rows
@@ -989,8 +1208,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.gain_next = u16(L->post_norm);
   g.ss_next = ws.ss_h1;
   g.part = ws.part;
-  g.ctr = ws.ctr;
-  if (int rc = launch_stream(g, pl.o, s)) return rc;
+  if (int rc = launch_wave(g, 1, s)) return rc;
 
   // 4. act = silu(W_gate . RMS_post(h1)) * (W_up . RMS_post(h1)), as activations only
   g = SkArgs{};
@@ -1010,8 +1228,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.epi = kSkSiluPair;
   g.xa_next = ws.xa_act;
   g.part = ws.part;
-  g.ctr = ws.ctr;
-  if (int rc = launch_stream(g, pl.gu, s)) return rc;
+  if (int rc = launch_wave(g, 2, s)) return rc;
 
   // 5. x = h1 + W_down . act
   g = SkArgs{};
@@ -1033,8 +1250,21 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     g.ss_next = ws.ss_x;
   }
   g.part = ws.part;
-  g.ctr = ws.ctr;
-  return launch_stream(g, pl.down, s);
+  return launch_wave(g, 1, s);
+}
+
+int wc_weights_frag(const void* w, int rows, int cols, void* out, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(w && out && w != out, "wc_weights_frag: NULL or aliased buffer");
+  WC_REQUIRE(rows >= 16 && rows % 16 == 0 && cols >= 32 && cols % 32 == 0,
+             "wc_weights_frag: rows must be a multiple of 16 and cols a multiple of 32 (got %d x %d)", rows, cols);
+  WC_REQUIRE(aligned(w, 16) && aligned(out, 16), "wc_weights_frag: buffers must be 16-byte aligned");
+  const int64_t chunks = static_cast<int64_t>(rows) * cols / 8;
+  const int grid = static_cast<int>(std::min<int64_t>((chunks + 255) / 256, 8192));
+  hipLaunchKernelGGL(k_frag_layout, dim3(grid), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(w), rows, cols, static_cast<uint16_t*>(out));
+  WC_LAUNCHED();
+  return WC_OK;
 }
 
 int wc_target_embed(const void* table, int vocab, int hidden, const int32_t* tokens_dev, int rows, float* out,

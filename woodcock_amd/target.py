@@ -55,6 +55,19 @@ class TargetConfig:
     tie_word_embeddings: bool = True
 
 
+def frag_weights(w: torch.Tensor) -> torch.Tensor:
+    """The fragment-major copy of a bf16 [rows, cols] matrix that the
+    verify-width GEMMs stream (wc_weights_frag), rows padded with zeros to a
+    multiple of 16."""
+    device_of(w)
+    rows = (w.shape[0] + 15) // 16 * 16
+    if rows != w.shape[0]:
+        w = torch.cat([w, w.new_zeros(rows - w.shape[0], w.shape[1])])
+    out = torch.empty_like(w)
+    _lib.call("wc_weights_frag", ptr(w), w.shape[0], w.shape[1], ptr(out), stream_ptr())
+    return out
+
+
 def layer_shapes(cfg: TargetConfig) -> dict[str, tuple[int, ...]]:
     d, H, Hk, D, F = cfg.hidden_size, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.intermediate_size
     return {
@@ -87,9 +100,11 @@ class TargetLayer:
             if tuple(t.shape) != shape:
                 raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {shape}")
             self.w[name] = t.to(self.device, torch.bfloat16).contiguous()
+        # the matrices in the GEMMs' fragment-major order, the gains as they are
+        self.wf = {name: frag_weights(t) if t.dim() == 2 else t for name, t in self.w.items()}
         self.lw = _lib.LayerWeights()
         for f, name in LAYER_NAMES.items():
-            setattr(self.lw, f, ptr(self.w[name]))
+            setattr(self.lw, f, ptr(self.wf[name]))
         self.dims = _lib.DrafterDims(cfg.hidden_size, 1, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
                                      cfg.intermediate_size, cfg.hidden_size, 3, 1, 1, cfg.rms_norm_eps, 0)
         self.max_rows = max_rows
@@ -172,6 +187,8 @@ class TargetModel:
                 if tuple(t.shape) != shapes[name]:
                     raise ValueError(f"layers.{i}.{name}: shape {tuple(t.shape)}, expected {shapes[name]}")
                 t = t.to(self.device, torch.bfloat16).contiguous()
+                if t.dim() == 2:  # the GEMMs stream the fragment-major copy
+                    t = frag_weights(t)
                 self.w[f"layers.{i}.{name}"] = t
                 setattr(lw, f, ptr(t))
             self.lw.append(lw)
@@ -184,7 +201,7 @@ class TargetModel:
         head = "embed_tokens.weight" if cfg.tie_word_embeddings else "lm_head.weight"
         if head not in self.w:
             self.w[head] = weights[head].to(self.device, torch.bfloat16).contiguous()
-        self.head = self.w[head]
+        self.head = frag_weights(self.w[head])  # the embedding gather keeps the row-major table
         self.dims = _lib.DrafterDims(cfg.hidden_size, 1, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
                                      cfg.intermediate_size, cfg.hidden_size, 3, 1, 1, cfg.rms_norm_eps, 0)
         self.max_rows = max_rows
