@@ -737,9 +737,18 @@ __device__ __forceinline__ void va_chunk_load(const uint16_t* kc, const uint16_t
   }
   if (mask) {
     const int r = min(t / 4, max(nr - 1, 0));
-    const uint8_t* mr = mask + static_cast<int64_t>(r) * mask_ld;
+    const uint8_t* mp = mask + static_cast<int64_t>(r) * mask_ld + c0 + (t % 4) * 16;
+    if (c0 + kVaCH <= mask_ld && (reinterpret_cast<uintptr_t>(mp) & 15) == 0) {
+      // one 16-byte load (bytes past ke are masked by the key count later)
+      const uint4 q = *reinterpret_cast<const uint4*>(mp);
+      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int e = 0; e < 16; ++e) ch.mb[e] = mr[min(c0 + (t % 4) * 16 + e, max(ke - 1, 0))];
+      for (int e = 0; e < 16; ++e) ch.mb[e] = static_cast<uint8_t>(qw[e / 4] >> (8 * (e % 4)));
+    } else {
+      const uint8_t* mr = mask + static_cast<int64_t>(r) * mask_ld;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ch.mb[e] = mr[min(c0 + (t % 4) * 16 + e, max(ke - 1, 0))];
+    }
   }
 }
 
