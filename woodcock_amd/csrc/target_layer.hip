@@ -146,29 +146,86 @@ struct SkArgs {
 // residuals and the next gains of the thread's columns.  Loaded on their own so
 // that a caller can issue them before the loads the tile waits on.
 constexpr int kSsMax = 16;  // row-scale parts <= 64
-template <int TW>
+template <int TW, bool QKV = false>
 struct EpiOps {
   float ssv[kSsMax], resv[16 * TW];
   uint16_t gnv[16 * TW];
+  // the QKV head epilogue: the row's cache offset / position, and the cos, sin
+  // and head-norm gains of the thread's columns
+  int offset, pos;
+  float cs[QKV ? 16 * TW : 1], sn[QKV ? 16 * TW : 1];
+  uint16_t hg[QKV ? 16 * TW : 1];
 };
 
-template <int TW>
-__device__ __forceinline__ void sk_epi_load(const SkArgs& a, int cb, EpiOps<TW>& o) {
+template <int TW, bool QKV = false>
+__device__ __forceinline__ void sk_epi_load(const SkArgs& a, int cb, EpiOps<TW, QKV>& o) {
   constexpr int FB = 64 * TW, CQ = FB / 4;
   const int t = threadIdx.x;
   const bool pair = a.epi == kSkSiluPair;
   const int m = t / 4, g = t % 4;
   const int n0 = pair ? cb * 64 + g * 16 : cb * FB + g * CQ;
   const int mr = min(m, a.M - 1);
+  if constexpr (QKV) {  // one 128-wide head per column range: 16-byte loads of the thread's 32 columns
+    static_assert(FB == 128, "one head per column range");
+    const int col0 = cb * FB, d0 = g * CQ;
+    const bool is_q = col0 < a.nq, is_k = !is_q && col0 < a.nq + a.nk;
+    o.offset = *a.offset_dev;
+    o.pos = a.positions ? a.positions[mr] : -1;  // resolved (and the table read) by sk_epi_rope
+    if (is_q || is_k) {
+      const uint4* gp = reinterpret_cast<const uint4*>((is_q ? a.q_gain : a.k_gain) + d0);
+      uint4 gv[CQ / 8];
+#pragma unroll
+      for (int i = 0; i < CQ / 8; ++i) gv[i] = gp[i];
+#pragma unroll
+      for (int i = 0; i < CQ / 8; ++i) {
+        const uint32_t w4[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o.hg[8 * i + e] = static_cast<uint16_t>(w4[e / 2] >> (16 * (e % 2)));
+      }
+    }
+  }
+
 #pragma unroll
   for (int q = 0; q < kSsMax; ++q) {
     const int pp = g + 4 * q;
     o.ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + m] : 0.f;
   }
+  // residuals and gains as 16-byte loads where the thread's columns are whole
+  // and aligned (scalar loads of 16 rows x 4 column runs per instruction cost
+  // as much as the partial sums they wait beside)
+  const bool res = !pair && a.epi == kSkResidual;
+  const float* rp = res ? a.res + static_cast<int64_t>(mr) * a.ldr + n0 : nullptr;
+  if (res && n0 + CQ <= a.N && (reinterpret_cast<uintptr_t>(rp) & 15) == 0) {
+    float4 rv[CQ / 4];
 #pragma unroll
-  for (int c = 0; c < CQ; ++c)
-    o.resv[c] = (!pair && a.epi == kSkResidual) ? a.res[static_cast<int64_t>(mr) * a.ldr + min(n0 + c, a.N - 1)] : 0.f;
-  if (a.xa_next && a.gain_next) {  // every gain load issued before the first is used
+    for (int i = 0; i < CQ / 4; ++i) rv[i] = reinterpret_cast<const float4*>(rp)[i];
+#pragma unroll
+    for (int i = 0; i < CQ / 4; ++i) {
+      o.resv[4 * i] = rv[i].x;
+      o.resv[4 * i + 1] = rv[i].y;
+      o.resv[4 * i + 2] = rv[i].z;
+      o.resv[4 * i + 3] = rv[i].w;
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < CQ; ++c)
+      o.resv[c] = res ? a.res[static_cast<int64_t>(mr) * a.ldr + min(n0 + c, a.N - 1)] : 0.f;
+  }
+  constexpr int NG = 16 * TW;  // gains read: CQ (one per output column), the pair's first 16
+  const int ng = pair ? 16 : CQ;
+  const uint16_t* gp = a.gain_next ? a.gain_next + n0 : nullptr;
+  if (a.xa_next && gp && (reinterpret_cast<uintptr_t>(gp) & 15) == 0 && (pair || n0 + CQ <= a.N)) {
+    uint4 gq[NG / 8];
+#pragma unroll
+    for (int i = 0; i < NG / 8; ++i) gq[i] = reinterpret_cast<const uint4*>(gp)[min(i, ng / 8 - 1)];
+#pragma unroll
+    for (int i = 0; i < NG / 8; ++i) {
+      const uint32_t w4[4] = {gq[i].x, gq[i].y, gq[i].z, gq[i].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o.gnv[8 * i + e] = 8 * i < ng ? static_cast<uint16_t>(w4[e / 2] >> (16 * (e % 2))) : 0;
+    }
+  } else if (a.xa_next && gp) {  // every gain load issued before the first is used
     uint32_t gw[CQ];
 #pragma unroll
     for (int c = 0; c < CQ; ++c) gw[c] = a.gain_next[n0 + min(c, pair ? 15 : CQ - 1)];
@@ -182,13 +239,40 @@ __device__ __forceinline__ void sk_epi_load(const SkArgs& a, int cb, EpiOps<TW>&
   }
 }
 
+// The QKV head epilogue's cos / sin at the row's position: a load that waits
+// for the position, so callers issue it after the loads that do not.
+template <int TW, bool QKV>
+__device__ __forceinline__ void sk_epi_rope(const SkArgs& a, int cb, EpiOps<TW, QKV>& o) {
+  if constexpr (QKV) {
+    constexpr int FB = 64 * TW, CQ = FB / 4;
+    const int t = threadIdx.x, m = t / 4, g = t % 4, d0 = g * CQ, col0 = cb * FB;
+    const bool is_q = col0 < a.nq, is_k = !is_q && col0 < a.nq + a.nk;
+    o.pos = min(max(o.pos >= 0 ? o.pos : o.offset + min(m, a.M - 1), 0), a.rope_max - 1);
+    if (is_q || is_k) {
+      const float4* cp = reinterpret_cast<const float4*>(a.rope_cos + static_cast<int64_t>(o.pos) * (FB / 2) + d0 % (FB / 2));
+      const float4* sp = reinterpret_cast<const float4*>(a.rope_sin + static_cast<int64_t>(o.pos) * (FB / 2) + d0 % (FB / 2));
+      float4 cv[CQ / 4], sv[CQ / 4];
+#pragma unroll
+      for (int i = 0; i < CQ / 4; ++i) {
+        cv[i] = cp[i];
+        sv[i] = sp[i];
+      }
+#pragma unroll
+      for (int i = 0; i < CQ / 4; ++i) {
+        o.cs[4 * i] = cv[i].x; o.cs[4 * i + 1] = cv[i].y; o.cs[4 * i + 2] = cv[i].z; o.cs[4 * i + 3] = cv[i].w;
+        o.sn[4 * i] = sv[i].x; o.sn[4 * i + 1] = sv[i].y; o.sn[4 * i + 2] = sv[i].z; o.sn[4 * i + 3] = sv[i].w;
+      }
+    }
+  }
+}
+
 // Epilogue of a column range for rows [r0, r1) of the tile in s_c (row r,
 // column c at s_c[r * (FB + 4) + c]): the row scale, then store / residual /
 // SiLU(gate) * up / the next activations, or the QKV head epilogue.  Every
 // thread of the block calls it; rows outside [r0, r1) or >= M write nothing.
-template <int TW>
+template <int TW, bool QKV = false>
 __device__ __forceinline__ void sk_epi_run(const SkArgs& a, float* s_c, float* s_inv, int cb, int r0, int r1,
-                                           const EpiOps<TW>& ops) {
+                                           const EpiOps<TW, QKV>& ops) {
   constexpr int FB = 64 * TW;
   constexpr int LDC = FB + 4;
   const int t = threadIdx.x;
@@ -228,33 +312,53 @@ __device__ __forceinline__ void sk_epi_run(const SkArgs& a, float* s_c, float* s
     }
     hs += __shfl_xor(hs, 1);
     hs += __shfl_xor(hs, 2);
-    const int offset = *a.offset_dev;
+    int offset, pos;
+    if constexpr (QKV) {
+      offset = ops.offset;
+      pos = ops.pos;
+    } else {
+      offset = *a.offset_dev;
+      pos = min(max(a.positions ? a.positions[min(m, a.M - 1)] : offset + m, 0), a.rope_max - 1);
+    }
     if (is_q || is_k) {
       const float invh = 1.f / sqrtf(hs / static_cast<float>(FB) + a.eps);
       const uint16_t* gain = is_q ? a.q_gain : a.k_gain;
 #pragma unroll
       for (int c = 0; c < CQ; ++c) {
-        y[c] = y[c] * invh * bf16_to_float(gain[d0 + c]);
+        float gc;
+        if constexpr (QKV) gc = bf16_to_float(ops.hg[c]);
+        else gc = bf16_to_float(gain[d0 + c]);
+        y[c] = y[c] * invh * gc;
         s_c[m * LDC + d0 + c] = y[c];
       }
     }
     __syncthreads();
     if (!live) return;
-    const int pos = min(max(a.positions ? a.positions[m] : offset + m, 0), a.rope_max - 1);
     if (is_q || is_k) {
 #pragma unroll
       for (int c = 0; c < CQ; ++c) {
         const int dd = d0 + c, pi = dd % (FB / 2);
         const float xp = s_c[m * LDC + (dd ^ (FB / 2))];
-        const float cs = a.rope_cos[static_cast<int64_t>(pos) * (FB / 2) + pi];
-        const float sn = a.rope_sin[static_cast<int64_t>(pos) * (FB / 2) + pi];
+        float cs, sn;
+        if constexpr (QKV) {
+          cs = ops.cs[c];
+          sn = ops.sn[c];
+        } else {
+          cs = a.rope_cos[static_cast<int64_t>(pos) * (FB / 2) + pi];
+          sn = a.rope_sin[static_cast<int64_t>(pos) * (FB / 2) + pi];
+        }
         y[c] = dd < FB / 2 ? y[c] * cs - xp * sn : y[c] * cs + xp * sn;
       }
     }
     if (is_q) {
       float* op = a.out + static_cast<int64_t>(m) * a.ldo + col0 + d0;
+      if ((reinterpret_cast<uintptr_t>(op) & 15) == 0) {
 #pragma unroll
-      for (int c = 0; c < CQ; ++c) op[c] = y[c];
+        for (int c = 0; c < CQ; c += 4) *reinterpret_cast<float4*>(op + c) = float4{y[c], y[c + 1], y[c + 2], y[c + 3]};
+      } else {
+#pragma unroll
+        for (int c = 0; c < CQ; ++c) op[c] = y[c];
+      }
       return;
     }
     const int slot = offset + m;
@@ -265,11 +369,16 @@ __device__ __forceinline__ void sk_epi_run(const SkArgs& a, float* s_c, float* s
     if (a.kv_bf16) {
       uint16_t* dst = static_cast<uint16_t*>(base) + at;
 #pragma unroll
-      for (int c = 0; c < CQ; ++c) dst[c] = float_to_bf16(y[c]);
+      for (int c = 0; c < CQ; c += 8)  // d0 is a multiple of 32: 16-byte aligned rows of 128 bf16
+        *reinterpret_cast<uint4*>(dst + c) = make_uint4(
+            static_cast<uint32_t>(float_to_bf16(y[c])) | (static_cast<uint32_t>(float_to_bf16(y[c + 1])) << 16),
+            static_cast<uint32_t>(float_to_bf16(y[c + 2])) | (static_cast<uint32_t>(float_to_bf16(y[c + 3])) << 16),
+            static_cast<uint32_t>(float_to_bf16(y[c + 4])) | (static_cast<uint32_t>(float_to_bf16(y[c + 5])) << 16),
+            static_cast<uint32_t>(float_to_bf16(y[c + 6])) | (static_cast<uint32_t>(float_to_bf16(y[c + 7])) << 16));
     } else {
       float* dst = static_cast<float*>(base) + at;
 #pragma unroll
-      for (int c = 0; c < CQ; ++c) dst[c] = y[c];
+      for (int c = 0; c < CQ; c += 4) *reinterpret_cast<float4*>(dst + c) = float4{y[c], y[c + 1], y[c + 2], y[c + 3]};
     }
     return;
   }
@@ -564,7 +673,7 @@ __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
 // The split-K fix-up of a column range and a quarter of the rows: the ks
 // partial tiles summed in split order (deterministic), then the epilogue.
 // Launched after k_mm_stream, so plain loads see every split's stores.
-template <int TW>
+template <int TW, bool QKV = false>
 __global__ __launch_bounds__(256) void k_mm_fix(SkArgs a) {
   constexpr int FB = 64 * TW;
   constexpr int LDC = FB + 4;
@@ -574,39 +683,39 @@ __global__ __launch_bounds__(256) void k_mm_fix(SkArgs a) {
   const int t = threadIdx.x, cb = blockIdx.x, r0 = blockIdx.y * 16;
   const int cols = gridDim.x * FB;
   const float* base = a.part + static_cast<int64_t>(cb) * FB;
-  EpiOps<TW> ops;  // issued first: one round trip covers them and the partials
-  sk_epi_load<TW>(a, cb, ops);
+  EpiOps<TW, QKV> ops;  // issued first: one round trip covers them and the partials
+  sk_epi_load<TW, QKV>(a, cb, ops);
   float4 acc[V4];
 #pragma unroll
   for (int i = 0; i < V4; ++i) acc[i] = float4{0.f, 0.f, 0.f, 0.f};
-  for (int z = 0; z < a.ks; z += 8) {  // up to eight splits' loads in flight per round
-    float4 u[8][V4];
+  // every split's loads in flight at once (ks <= 8), then the loads that wait on the position
+  float4 u[8][V4];
 #pragma unroll
-    for (int h = 0; h < 8; ++h)
+  for (int h = 0; h < 8; ++h)
+#pragma unroll
+    for (int i = 0; i < V4; ++i) {
+      const int e = (t + 256 * i) * 4, r = min(r0 + e / FB, a.M - 1), c = e % FB;
+      const int zz = min(h, a.ks - 1);
+      u[h][i] = *reinterpret_cast<const float4*>(base + (static_cast<int64_t>(zz) * 64 + r) * cols + c);
+    }
+  sk_epi_rope<TW, QKV>(a, cb, ops);
+#pragma unroll
+  for (int h = 0; h < 8; ++h)
+    if (h < a.ks)
 #pragma unroll
       for (int i = 0; i < V4; ++i) {
-        const int e = (t + 256 * i) * 4, r = min(r0 + e / FB, a.M - 1), c = e % FB;
-        const int zz = min(z + h, a.ks - 1);
-        u[h][i] = *reinterpret_cast<const float4*>(base + (static_cast<int64_t>(zz) * 64 + r) * cols + c);
+        acc[i].x += u[h][i].x;
+        acc[i].y += u[h][i].y;
+        acc[i].z += u[h][i].z;
+        acc[i].w += u[h][i].w;
       }
-#pragma unroll
-    for (int h = 0; h < 8; ++h)
-      if (z + h < a.ks)
-#pragma unroll
-        for (int i = 0; i < V4; ++i) {
-          acc[i].x += u[h][i].x;
-          acc[i].y += u[h][i].y;
-          acc[i].z += u[h][i].z;
-          acc[i].w += u[h][i].w;
-        }
-  }
 #pragma unroll
   for (int i = 0; i < V4; ++i) {
     const int e = (t + 256 * i) * 4, r = r0 + e / FB, c = e % FB;
     *reinterpret_cast<float4*>(&s_c[r * LDC + c]) = acc[i];
   }
   __syncthreads();
-  sk_epi_run<TW>(a, s_c, s_inv, cb, r0, r0 + 16, ops);
+  sk_epi_run<TW, QKV>(a, s_c, s_inv, cb, r0, r0 + 16, ops);
 }
 
 struct GemmPlan {
@@ -665,7 +774,7 @@ static int launch_wave(SkArgs g, int fix_tw, hipStream_t s) {
   WC_REQUIRE(g.K % 256 == 0, "target layer: K %d must be a multiple of 256", g.K);
   WC_REQUIRE(g.N % (64 * fix_tw) == 0, "target layer: %d weight rows must be a multiple of %d", g.N, 64 * fix_tw);
   WC_REQUIRE(g.n_ss <= 64, "target layer: at most 64 row-scale parts");
-  g.ks = wave_ks(g.N, g.K);
+  g.ks = wave_ks(g.N, g.K);  // <= 8: k_mm_fix issues every split's loads at once
   const dim3 grid(g.N / (16 * kMwG), g.ks);
   switch ((g.M + 15) / 16) {
     case 1: hipLaunchKernelGGL((k_mm_wave<1>), grid, dim3(256), 0, s, g); break;
@@ -675,7 +784,10 @@ static int launch_wave(SkArgs g, int fix_tw, hipStream_t s) {
   }
   WC_LAUNCHED();
   const dim3 fgrid(g.N / (64 * fix_tw), (g.M + 15) / 16);
-  if (fix_tw == 2)
+  if (g.epi == kSkQkvHead) {
+    WC_REQUIRE(fix_tw == 2, "target layer: the QKV head epilogue takes 128-column ranges");
+    hipLaunchKernelGGL((k_mm_fix<2, true>), fgrid, dim3(256), 0, s, g);
+  } else if (fix_tw == 2)
     hipLaunchKernelGGL((k_mm_fix<2>), fgrid, dim3(256), 0, s, g);
   else
     hipLaunchKernelGGL((k_mm_fix<1>), fgrid, dim3(256), 0, s, g);
