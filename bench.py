@@ -646,12 +646,16 @@ PHASES = {
         ("down", _D * _F * 2)],
     "target layer (M = 60, ctx 2048, tree mask)": [
         ("input -> fragment-order bf16 hi / lo", 60 * _D * 4 + 60 * _D * 4),
-        ("QKV 4096 x 2048 (+ q/k norm, RoPE, K/V append)", (_HD + 2 * _HKV * 128) * _D * 2),
+        ("QKV 4096 x 2048, K split", (_HD + 2 * _HKV * 128) * _D * 2),
+        ("QKV fix-up (+ q/k norm, RoPE, K/V append)", 0),
         ("tree attention, 2048 + 60 keys", 2 * 2108 * _HKV * 128 * 2),
         ("attention merge", 0),
-        ("o_proj 2048 x 2048", _D * _HD * 2),
-        ("gate / up 2 x 6144 x 2048", 2 * _F * _D * 2),
-        ("down 2048 x 6144", _D * _F * 2)],
+        ("o_proj 2048 x 2048, K split", _D * _HD * 2),
+        ("o_proj fix-up (+ residual, next activations)", 0),
+        ("gate / up 2 x 6144 x 2048, K split", 2 * _F * _D * 2),
+        ("gate / up fix-up (SiLU * up, next activations)", 0),
+        ("down 2048 x 6144, K split", _D * _F * 2),
+        ("down fix-up (+ residual)", 0)],
 }
 
 
@@ -723,6 +727,43 @@ def pmc_probe2(seed=0):
         torch.neg(x, out=y)
     torch.cuda.synchronize()
     print(f"pmc probe over the round kernels: {PROBE_REPS} repeats per phase, {PROBE_COPIES} copies", flush=True)
+
+
+def target_layer_only(seed=0, calls=45):
+    """The config-5 target layer alone (Qwen3-1.7B shape, a 60-node tree of depth
+    <= 6 at context 2048 with its mask, bf16 KV), called `calls` times."""
+    import torch
+
+    from woodcock_amd.cache import KVCache
+    from woodcock_amd.sampling import DraftTree, tree_attention_mask
+    from woodcock_amd.target import TargetConfig, TargetLayer, random_layer
+
+    dev = torch.device("cuda", 0)
+    tcfg = TargetConfig()
+    trng = np.random.default_rng(seed + 9)
+    parents, depth = [-1], [0]
+    while len(parents) < 60:
+        p_ = int(trng.integers(0, len(parents)))
+        if depth[p_] < 6:
+            parents.append(p_)
+            depth.append(depth[p_] + 1)
+    tree = DraftTree([int(t) for t in trng.integers(0, tcfg.vocab_size, 60)], parents, depth)
+    tl = TargetLayer(tcfg, random_layer(tcfg, seed=seed, device=dev), dev, max_rows=60)
+    tcache = KVCache(tcfg.num_kv_heads, tcfg.head_dim, 2048 + 64, torch.bfloat16, dev)
+    tcache.keys.normal_()
+    tcache.values.normal_()
+    tx = torch.randn(60, tcfg.hidden_size, device=dev)
+    toff = torch.tensor([2048], dtype=torch.int32, device=dev)
+    tpos = torch.tensor([2048 + dd for dd in depth], dtype=torch.int32, device=dev)
+    tmask = torch.from_numpy(tree_attention_mask(tree, 2048).astype(np.uint8)).to(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(calls):
+        tl(tx, tcache, toff, tpos, tmask)
+    e1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"target_layer_us": round(1e3 * e0.elapsed_time(e1) / calls, 2), "calls": calls}), flush=True)
 
 
 def pmc_summary2(fetch_dir, write_dir, mfma_dir):
@@ -1022,6 +1063,8 @@ def main():
     ap.add_argument("--pmc-probe2", action="store_true", help="the launches of the round-kernel counter passes")
     ap.add_argument("--pmc-summary2", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "MFMA_DIR"),
                     help="summarise the three counter passes over --pmc-probe2 (no GPU needed)")
+    ap.add_argument("--target-layer-only", action="store_true",
+                    help="only the M = 60 verify-width target layer, 45 calls (for a kernel trace of the layer)")
     ap.add_argument("--round-only", action="store_true",
                     help="only the timed config-1 rounds (for a kernel trace of the round alone)")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
@@ -1039,8 +1082,8 @@ def main():
         trace_summary(args.trace_summary, args.steps)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the round is a batch-1, single-device path "
-              "(see DESIGN.md for how it would shard); run with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: the round is a batch-1, single-device path with no collective; "
+              "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
 
@@ -1052,6 +1095,9 @@ def main():
         return
     if args.pmc_probe2:
         pmc_probe2(args.seed)
+        return
+    if args.target_layer_only:
+        target_layer_only(args.seed)
         return
     r = bench_gpu(args)
     if args.round_only:
