@@ -358,6 +358,9 @@ static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
   return true;
 }
 
+// Few-row VALU GEMV (k_gemvk, csrc/gemvk.hip): false when the launch does not fit it.
+bool launch_gemvk_any(const GemvArgs& a, bool pair, int xb, hipStream_t s);
+
 template <bool PAIR, int NIN, int XB>
 static bool launch_gemvx(const GemvArgs& a, int steps, hipStream_t s) {
   if (a.M <= 2) return launch_gemvx_r<PAIR, NIN, XB, 2>(a, steps, s);
@@ -403,7 +406,8 @@ static int launch_gemv(const GemvArgs& a, int /*R hint*/, hipStream_t s) {
   const int steps = max_k / 512;
   const bool pair = a.epi == kEpiSiluPair;
   bool done = false;
-  if (a.M > 1) {
+  if (a.M > 1 && a.M <= 8) done = launch_gemvk_any(a, pair, xb, s);
+  if (!done && a.M > 1) {
     if (pair && a.n_in == 1 && xb == 0)
       done = launch_gemvf<true, 1, 0>(a, s);
     else if (!pair && a.n_in == 1 && xb == 0)
