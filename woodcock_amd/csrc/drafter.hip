@@ -19,6 +19,7 @@
 #include "attention.h"
 #include "gemv.h"
 #include "gemvf.h"
+#include "gemv1s.h"
 
 namespace wc {
 
@@ -88,6 +89,17 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
       if (a.in[i].gain) gb |= 1 << i;
     const dim3 grid((a.N + kGemvWaves * R - 1) / (kGemvWaves * R)), block(kGemvThreads);
     constexpr int kAll = (1 << NIN) - 1;
+    // a long gain-free input row (the down projection, K >= 6144) is staged
+    // once per block (k_gemv1s): each wave would otherwise read twice its
+    // weight bytes of x from L2 (2048 x 6144: 7.1 -> 6.2 us); for shorter or
+    // normed rows the per-wave loads measured as fast or faster
+    if constexpr (NIN == 1 && !PAIR && S >= 12) {
+      if (gb == 0) {
+        const size_t lds = static_cast<size_t>(a.in[0].K) * sizeof(float);
+        hipLaunchKernelGGL((k_gemv1s<R, PAIR, NIN, S, XB, 0>), grid, block, lds, s, a);
+        return true;
+      }
+    }
     if (gb == kAll) {
       hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, S, XB, kAll>), grid, block, 0, s, a);
     } else if constexpr (NIN == 1) {
