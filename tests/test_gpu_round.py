@@ -22,14 +22,14 @@ def small_cfg():
                          intermediate_size=512, vocab_size=4096, target_hidden_size=192, rope_theta=1e6)
 
 
-def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256):
+def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256, cfg=None, head_rows=1024):
     from woodcock_amd.drafter import Drafter
     from woodcock_amd.spec import ChainRound
     from woodcock_amd.synthetic import SyntheticTarget, draft_vocab, random_drafter, to_bits
 
-    cfg = small_cfg()
-    ids = draft_vocab(cfg.vocab_size, 1024, seed=seed)
-    w = random_drafter(cfg, seed=seed, device=cuda, head_rows=1024)
+    cfg = cfg or small_cfg()
+    ids = draft_vocab(cfg.vocab_size, head_rows, seed=seed)
+    w = random_drafter(cfg, seed=seed, device=cuda, head_rows=head_rows)
     d = Drafter(cfg, dict(w), cuda, kv_dtype)
     d._vocab_ids = torch.from_numpy(ids).to(cuda)
     d._build_structs(d._rope[0].shape[0])
@@ -103,6 +103,34 @@ def test_rounds_match_oracle_round(cuda):
         k_gpu = rnd.cache[0].keys[0, :, :n].float().cpu().numpy()
         assert _rel(k_gpu, oc.keys_f32(0)[:, :n]) <= 1e-5, f"round {r}"
     assert rnd.syncs == len(pattern)
+
+
+def test_config1_rounds_match_oracle_round(cuda):
+    """The benchmarked round at its full shape: Qwen3-1.7B drafter, 16,384-row
+    head, bf16 drafter cache at context 512 (capacity 1024), K = 4, the
+    update pass at 5 host rows (a + 1 live) -- drafts, accepted lengths and
+    tokens equal the oracle round's; root state and appended cache rows within
+    the bf16-cache tolerance."""
+    from woodcock_amd.config import qwen3_1p7b_drafter
+
+    cfg, d, rnd, od, oc, target, root = setup(cuda, 7, ctx=512, kv_dtype=torch.bfloat16, cap=1024,
+                                              cfg=qwen3_1p7b_drafter(), head_rows=16384)
+    root_out = core.rmsnorm(root, od.w["norm.weight"], cfg.rms_norm_eps)
+    root_fb = od.feedback(root, root_out)
+    for r, n_agree in enumerate([2, 4, 0]):
+        res = gpu_round(rnd, target, n_agree)
+        logits = target.logits.cpu().numpy()
+        taps = [t.float().cpu().numpy() for t in target.taps]
+        drafts, a, acc, root_out, root_fb, root_hid = oracle_round(od, oc, root_out, root_fb, logits, taps)
+        assert rnd.drafts.tolist() == drafts, f"round {r}"
+        assert res.n_accepted == a == n_agree, f"round {r}"
+        assert res.tokens == acc, f"round {r}"
+        assert _rel(rnd.upd_hid[a].cpu().numpy(), root_hid[0]) <= 1e-3, f"round {r}"
+        n = oc.offset
+        assert rnd.committed() == n
+        k_gpu = rnd.cache[0].keys[0, :, 512:n].float().cpu().numpy()
+        assert _rel(k_gpu, oc.keys_f32(0)[:, 512:n]) <= 1e-2, f"round {r}"
+    assert rnd.syncs == 3
 
 
 def test_enqueue_never_synchronises(cuda):
