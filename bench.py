@@ -352,6 +352,7 @@ def bench_gpu(args):
     for c in tm_cache:
         c.keys.normal_()
         c.values.normal_()
+        c.offset = 512  # the chain block's context (the tree block passes its own offset and mask)
     tm_tok5 = torch.randint(0, tcfg.vocab_size, (5,), dtype=torch.int32, device=out1.device)
     tm_tok60 = torch.tensor(tree.tokens, dtype=torch.int32, device=out1.device)
     tm_off512 = torch.tensor([512], dtype=torch.int32, device=out1.device)

@@ -98,6 +98,7 @@ def time_verify(tm, ctx: int, max_n: int, iters: int) -> dict[int, float]:
     for c in cache:
         c.keys[0, :, :ctx].normal_()
         c.values[0, :, :ctx].normal_()
+        c.offset = ctx
     off = torch.tensor([ctx], dtype=torch.int32, device=dev)
     logits = torch.empty(max_n, tm.cfg.vocab_size, device=dev)
     taps = [torch.empty(max_n, tm.cfg.hidden_size, device=dev) for _ in tm.feature_layers]

@@ -23,6 +23,8 @@ from .cache import KVCache
 from .runtime import device_of, ptr, stream_ptr
 
 MAX_ROWS = 64
+FEW_ROWS = 8  # chain verify blocks up to this many rows may run on the few-row path
+FEW_ROWS_MAX_KEYS = 1024  # ... with more than 4 query vectors: contexts up to this many keys
 
 LAYER_NAMES = {
     "in_norm": "input_layernorm.weight",
@@ -179,19 +181,24 @@ class TargetModel:
         self.feature_layers = tuple(feature_layers or default_feature_layers(cfg.num_layers))
         shapes = layer_shapes(cfg)
         self.w: dict[str, torch.Tensor] = {}
+        self.wr: dict[str, torch.Tensor] = {}  # row-major matrices: the few-row path
         self.lw = []
+        self.lwr = []
         for i in range(cfg.num_layers):
-            lw = _lib.LayerWeights()
+            lw, lwr = _lib.LayerWeights(), _lib.LayerWeights()
             for f, name in LAYER_NAMES.items():
                 t = weights[f"layers.{i}.{name}"]
                 if tuple(t.shape) != shapes[name]:
                     raise ValueError(f"layers.{i}.{name}: shape {tuple(t.shape)}, expected {shapes[name]}")
                 t = t.to(self.device, torch.bfloat16).contiguous()
-                if t.dim() == 2:  # the GEMMs stream the fragment-major copy
+                setattr(lwr, f, ptr(t))
+                if t.dim() == 2:  # the verify-width GEMMs stream the fragment-major copy
+                    self.wr[f"layers.{i}.{name}"] = t
                     t = frag_weights(t)
                 self.w[f"layers.{i}.{name}"] = t
                 setattr(lw, f, ptr(t))
             self.lw.append(lw)
+            self.lwr.append(lwr)
         for name, shape in (("embed_tokens.weight", (cfg.vocab_size, cfg.hidden_size)),
                             ("norm.weight", (cfg.hidden_size,))):
             t = weights[name]
@@ -209,6 +216,24 @@ class TargetModel:
         self.ws = torch.zeros(n, dtype=torch.uint8, device=self.device)  # split-K counters start at zero
         self._rope: tuple[torch.Tensor, torch.Tensor] | None = None
         self.x = torch.empty(max_rows, cfg.hidden_size, dtype=torch.float32, device=self.device)
+        # few-row path: groups of up to WC_MAX_DRAFTER_LAYERS decoder layers per
+        # wc_drafter_forward call (a drafter layer without the token stream is a
+        # Qwen3 decoder layer), split after every feature layer
+        self.fdims = _lib.DrafterDims(cfg.hidden_size, 1, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+                                      cfg.intermediate_size, cfg.hidden_size, 1, 1, cfg.vocab_size,
+                                      cfg.rms_norm_eps, 0)
+        n = int(_lib.lib().wc_drafter_workspace_bytes(C.byref(self.fdims)))
+        self.fws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device=self.device)
+        _lib.call("wc_workspace_init", ptr(self.fws), self.fws.numel(), stream_ptr())
+        self.x2 = torch.empty_like(self.x)
+        self._groups = []
+        g0 = 0
+        for i in range(cfg.num_layers):
+            if i - g0 + 1 == _lib.WC_MAX_DRAFTER_LAYERS or i in self.feature_layers or i == cfg.num_layers - 1:
+                self._groups.append((g0, i + 1))
+                g0 = i + 1
+        self._fw_key = None
+        self._fw: list[tuple[_lib.DrafterDims, _lib.DrafterWeights]] = []
 
     def make_cache(self, capacity: int, dtype=torch.bfloat16) -> list[KVCache]:
         return [KVCache(self.cfg.num_kv_heads, self.cfg.head_dim, capacity, dtype, self.device)
@@ -256,6 +281,8 @@ class TargetModel:
             taps = [torch.empty(rows, cfg.hidden_size, dtype=torch.float32, device=self.device)
                     for _ in self.feature_layers]
         final_norm = self.w["norm.weight"]
+        if mask is None and self._few_rows_fit(rows, cache[0].offset + rows):
+            return self._few_rows(tok, rows, cache, offset_dev, pos, kvdt, cos, sin, logits, taps)
         for i in range(cfg.num_layers):
             c = cache[i]
             # each layer leaves the next one's (or the head's) normed activations
@@ -272,5 +299,63 @@ class TargetModel:
             logits = torch.empty(rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
         _lib.call("wc_target_head", C.byref(self.dims), ptr(self.head), ptr(final_norm), ptr(x), rows,
                   cfg.vocab_size, ptr(logits), logits.stride(0), 1, ptr(self.ws), s)
+        return logits, taps
+
+    def _few_rows_fit(self, rows: int, keys: int) -> bool:
+        """Whether a mask-less block runs on the few-row path: its query vectors
+        (rows x GQA group) fit one decode-attention block, and either the
+        attention merges its splits in the same launch (<= 4 vectors) or every
+        split holds one 32-key chunk (keys <= 1024; `keys` is the host's view of
+        the cache offset plus the block -- the choice affects speed only).
+        Measured: Qwen3-1.7B at 5 rows, context 512: 28 layers + head 2038 ->
+        1738 us; Qwen3-4B at one row, context 4096: 3.74 -> 2.66 ms; Qwen3-4B at
+        2..8 rows, context 4096 (several chunks per split for 8+ query vectors,
+        or two row tiles that stream the weights twice): slower than the
+        verify-width path."""
+        qv = rows * (self.cfg.num_heads // self.cfg.num_kv_heads)
+        return rows <= FEW_ROWS and qv <= 16 and (qv <= 4 or keys <= FEW_ROWS_MAX_KEYS)
+
+    def _few_weights(self, cos: torch.Tensor, sin: torch.Tensor):
+        """(dims, weights) of each layer group for wc_drafter_forward, rebuilt when
+        the RoPE table moves."""
+        key = (cos.data_ptr(), sin.data_ptr(), cos.shape[0])
+        if key != self._fw_key:
+            self._fw = []
+            for g0, g1 in self._groups:
+                dims = _lib.DrafterDims.from_buffer_copy(self.fdims)
+                dims.num_layers = g1 - g0
+                W = _lib.DrafterWeights()
+                W.embed = ptr(self.w["embed_tokens.weight"])
+                W.final_norm = ptr(self.w["norm.weight"])
+                W.rope_cos, W.rope_sin, W.rope_max_pos = ptr(cos), ptr(sin), cos.shape[0]
+                for j in range(g1 - g0):
+                    W.layers[j] = self.lwr[g0 + j]
+                self._fw.append((dims, W))
+            self._fw_key = key
+        return self._fw
+
+    def _few_rows(self, tok, rows, cache, offset_dev, pos, kvdt, cos, sin, logits, taps):
+        """A chain verify block of <= FEW_ROWS rows without a mask: the decoder
+        layers on the drafter's one-/few-row GEMVs over the row-major weights
+        (K split over the waves of a block, 1 KB weight rows per load) and the
+        decode attention that normalises, rotates and appends on the fly -- six
+        launches per layer against eleven on the verify-width path."""
+        cfg = self.cfg
+        s = stream_ptr()
+        x, xo = self.x[:rows], self.x2[:rows]
+        for (g0, g1), (dims, W) in zip(self._groups, self._few_weights(cos, sin)):
+            kp = (C.c_void_p * (g1 - g0))(*[cache[i].keys.data_ptr() for i in range(g0, g1)])
+            vp = (C.c_void_p * (g1 - g0))(*[cache[i].values.data_ptr() for i in range(g0, g1)])
+            _lib.call("wc_drafter_forward", C.byref(dims), C.byref(W), ptr(tok), ptr(x), x.stride(0), None, 0, rows,
+                      None, kp, vp, kvdt, cache[g0].capacity, ptr(offset_dev), 0,
+                      ptr(pos) if pos is not None else None, None, 0, ptr(xo), None, None, ptr(self.fws), s)
+            x, xo = xo, x
+            for j, f in enumerate(self.feature_layers):
+                if f == g1 - 1:
+                    taps[j][:rows].copy_(x)
+        if logits is None:
+            logits = torch.empty(rows, cfg.vocab_size, dtype=torch.float32, device=self.device)
+        _lib.call("wc_target_head", C.byref(self.dims), ptr(self.head), ptr(self.w["norm.weight"]), ptr(x), rows,
+                  cfg.vocab_size, ptr(logits), logits.stride(0), 0, ptr(self.ws), s)
         return logits, taps
 
