@@ -730,6 +730,31 @@ def pmc_probe2(seed=0):
     print(f"pmc probe over the round kernels: {PROBE_REPS} repeats per phase, {PROBE_COPIES} copies", flush=True)
 
 
+def target_chain_only(seed=0, calls=20):
+    """The 28-layer Qwen3-1.7B target forward over a 5-row chain block at
+    context 512 (the few-row path), called `calls` times (for a kernel trace)."""
+    import torch
+
+    from woodcock_amd.target import TargetConfig, TargetModel, random_target
+
+    dev = torch.device("cuda", 0)
+    tcfg = TargetConfig()
+    tm = TargetModel(tcfg, random_target(tcfg, seed=seed + 5, device=dev), dev, max_rows=8)
+    cache = tm.make_cache(2048 + 64)
+    for c in cache:
+        c.keys.normal_()
+        c.values.normal_()
+        c.offset = 512
+    tok = torch.randint(0, tcfg.vocab_size, (5,), dtype=torch.int32, device=dev)
+    off = torch.tensor([512], dtype=torch.int32, device=dev)
+    logits = torch.empty(5, tcfg.vocab_size, device=dev)
+    taps = [torch.empty(5, tcfg.hidden_size, device=dev) for _ in tm.feature_layers]
+    for _ in range(calls):
+        tm(tok, cache, off, logits=logits, taps=taps)
+    torch.cuda.synchronize()
+    print(json.dumps({"target_chain_calls": calls}), flush=True)
+
+
 def target_layer_only(seed=0, calls=45):
     """The config-5 target layer alone (Qwen3-1.7B shape, a 60-node tree of depth
     <= 6 at context 2048 with its mask, bf16 KV), called `calls` times."""
@@ -1064,6 +1089,8 @@ def main():
     ap.add_argument("--pmc-probe2", action="store_true", help="the launches of the round-kernel counter passes")
     ap.add_argument("--pmc-summary2", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "MFMA_DIR"),
                     help="summarise the three counter passes over --pmc-probe2 (no GPU needed)")
+    ap.add_argument("--target-chain-only", action="store_true",
+                    help="only the 28-layer target forward over a 5-row chain block, 20 calls (for a kernel trace)")
     ap.add_argument("--target-layer-only", action="store_true",
                     help="only the M = 60 verify-width target layer, 45 calls (for a kernel trace of the layer)")
     ap.add_argument("--round-only", action="store_true",
@@ -1096,6 +1123,9 @@ def main():
         return
     if args.pmc_probe2:
         pmc_probe2(args.seed)
+        return
+    if args.target_chain_only:
+        target_chain_only(args.seed)
         return
     if args.target_layer_only:
         target_layer_only(args.seed)
