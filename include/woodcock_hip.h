@@ -34,7 +34,7 @@ extern "C" {
 
 typedef struct ihipStream_t* wc_stream_t; /* == hipStream_t */
 
-#define WC_ABI_VERSION 1
+#define WC_ABI_VERSION 2
 #define WC_MAX_NODES 64   /* verify rows per round: chain k+1 or tree nodes */
 #define WC_MAX_LAYERS 64  /* KV compaction: layers per call */
 
@@ -358,10 +358,13 @@ typedef struct wc_drafter_dims {
 } wc_drafter_dims;
 
 /* One decoder layer's device weights, bf16 row-major [out][in] (nn.Linear layout).
- * aux_norm / aux_q / aux_k / aux_v are NULL for layers without the token stream. */
+ * aux_norm / aux_q / aux_k / aux_v are NULL for layers without the token stream.
+ * gate_frag / up_frag (optional, NULL = none): fragment-major copies of gate / up
+ * (wc_weights_frag); when both are set, passes over several rows stream them. */
 typedef struct wc_layer_weights {
   const void *in_norm, *post_norm, *aux_norm;
   const void *q, *k, *v, *o, *aux_q, *aux_k, *aux_v, *q_norm, *k_norm, *gate, *up, *down;
+  const void *gate_frag, *up_frag;
 } wc_layer_weights;
 
 typedef struct wc_drafter_weights {

@@ -29,6 +29,36 @@ def test_library_exports_every_declared_symbol():
     assert sorted(_lib.exported_symbols()) == declared, "ctypes signatures must cover exactly the header"
 
 
+def test_ctypes_structs_match_the_header(tmp_path):
+    """Sizes and field offsets of the ctypes mirrors equal the C header's (gcc
+    compiles a probe against include/woodcock_hip.h)."""
+    import shutil
+    import subprocess
+
+    from woodcock_amd import _lib
+
+    if not shutil.which("gcc"):
+        pytest.skip("no C compiler")
+    mirrors = {"wc_drafter_dims": _lib.DrafterDims, "wc_layer_weights": _lib.LayerWeights,
+               "wc_drafter_weights": _lib.DrafterWeights, "wc_gumbel": _lib.Gumbel, "wc_uniforms": _lib.Uniforms}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "woodcock_hip.h"', "int main(void) {"]
+    for cname, py in mirrors.items():
+        lines.append(f'  printf("{cname} %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{cname}.{f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "probe.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                          check=True).stdout.splitlines())
+    for cname, py in mirrors.items():
+        assert int(got[cname]) == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert int(got[f"{cname}.{f}"]) == getattr(py, f).offset, f"{cname}.{f}"
+
+
 def test_library_loads_and_reports_abi():
     from woodcock_amd import _lib
 

@@ -17,7 +17,7 @@ WC_OK, WC_E_INVALID, WC_E_HIP, WC_E_UNSUPPORTED = 0, 1, 2, 3
 WC_F32, WC_BF16 = 0, 1
 WC_MAX_NODES = 64
 WC_MAX_LAYERS = 64
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 class Verdict(C.Structure):
@@ -63,7 +63,7 @@ class LayerWeights(C.Structure):
     """Mirror of wc_layer_weights (device pointers)."""
 
     _fields_ = [(n, C.c_void_p) for n in ("in_norm", "post_norm", "aux_norm", "q", "k", "v", "o", "aux_q", "aux_k",
-                                          "aux_v", "q_norm", "k_norm", "gate", "up", "down")]
+                                          "aux_v", "q_norm", "k_norm", "gate", "up", "down", "gate_frag", "up_frag")]
 
 
 class DrafterWeights(C.Structure):

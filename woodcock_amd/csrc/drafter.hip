@@ -357,6 +357,21 @@ static bool launch_gemvf(const GemvArgs& a, hipStream_t s) {
     else if (deep) WC_GF_L(1, 16, 4, GBV);      \
     else WC_GF_L(1, 8, 6, GBV);                 \
   } while (0)
+  if constexpr (PAIR && NIN == 1) {
+    if (a.wfrag) {
+      if (gb != kAll) return false;
+      // four waves of four k steps in flight: 15.1 us for the Qwen3-1.7B pair at
+      // 5 rows (eight waves 14.8, sixteen 18.1; 17.0 on the row-major layout)
+      if (stg && gf_stage_ok(reinterpret_cast<const void*>(&k_gemvf<2, 4, 4, PAIR, NIN, XB, kAll, true, true>),
+                             WC_GF_DYN(2, 4)))
+        hipLaunchKernelGGL((k_gemvf<2, 4, 4, PAIR, NIN, XB, kAll, true, true>), grid, dim3(4 * kWave),
+                           WC_GF_DYN(2, 4), s, as);
+      else
+        hipLaunchKernelGGL((k_gemvf<2, 4, 4, PAIR, NIN, XB, kAll, false, true>), grid, dim3(4 * kWave), 0, s, a);
+      return true;
+    }
+  }
+  if (a.wfrag) return false;
   if (gb == kAll) {
     if (wide) WC_GF_L(2, 4, 4, kAll); else if constexpr (!PAIR) WC_GF(1, kAll);
   } else if constexpr (NIN == 1) {
@@ -418,6 +433,13 @@ static int launch_gemv(const GemvArgs& a, int /*R hint*/, hipStream_t s) {
   const int steps = max_k / 512;
   const bool pair = a.epi == kEpiSiluPair;
   bool done = false;
+  if (a.wfrag) {
+    // fragment-major gate / up pair: the few-row MFMA kernel only
+    if (pair && a.n_in == 1 && xb == 0 && a.M > 1) done = launch_gemvf<true, 1, 0>(a, s);
+    if (!done) return set_error(WC_E_UNSUPPORTED, "gemv: fragment-major weights need the few-row gate / up pair");
+    WC_LAUNCHED();
+    return WC_OK;
+  }
   if (a.M > 1 && a.M <= 8) done = launch_gemvk_any(a, pair, xb, s);
   if (!done && a.M > 1) {
     if (pair && a.n_in == 1 && xb == 0)
@@ -839,6 +861,13 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       gu.ldw[0] = d.hidden;
       gu.w[0][0] = u16(L.gate);
       gu.w[1][0] = u16(L.up);
+      if (L.gate_frag && L.up_frag && tr > 1) {
+        // several rows: the MFMA pair kernel over the fragment-major copies,
+        // one contiguous kilobyte per weight load instruction
+        gu.w[0][0] = u16(L.gate_frag);
+        gu.w[1][0] = u16(L.up_frag);
+        gu.wfrag = 1;
+      }
       gu.N = d.inter;
       gu.M = tr;
       gu.m_dev = n_rows_dev;

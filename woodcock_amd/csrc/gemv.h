@@ -103,6 +103,9 @@ struct GemvArgs {
   // xn_out at the input's row index by block 0 (the drafter output `out`)
   float* xn_out;
   int64_t ld_xn;
+  // w[][] hold fragment-major matrices (wc_weights_frag): only the few-row MFMA
+  // kernel reads that layout
+  int wfrag;
 };
 
 __device__ __forceinline__ float dot8(const uint4 w, const float4 a, const float4 b) {

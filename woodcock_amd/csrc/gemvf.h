@@ -68,6 +68,14 @@ __device__ __forceinline__ int gf_seg_off(const GemvArgs& a, int s) {
   return o;
 }
 
+// Elements between consecutive k steps of a lane's weight stream: 32 along a
+// row-major row, or one 1 KB fragment in the fragment-major layout
+// (wc_weights_frag: chunk (T, s) of 16-row tile T at k step s holds lane l's
+// W[16 T + l % 16][32 s + 8 (l / 16) .. + 8], so every load instruction of a
+// wave is one contiguous kilobyte).
+template <bool FRAG>
+__device__ __forceinline__ constexpr int gf_step() { return FRAG ? 64 * 8 : 32; }
+
 // Registers of one k step in flight: TW weight fragments, the lane's 8 inputs
 // (fp32: two vectors; bf16: the first) and 8 gains.
 template <int TW>
@@ -78,13 +86,13 @@ struct GfStep {
 
 // Issue the loads of step i (segment s, local step j of that segment).  STG:
 // the lane's input row of segment S is staged in LDS as fp32 x * gain (xs).
-template <int S, int TW, bool PAIR, int XB, int GB, bool STG>
+template <int S, int TW, bool PAIR, int XB, int GB, bool STG, bool FRAG = false>
 __device__ __forceinline__ void gf_load(const GemvArgs& a, const uint16_t* (*wrow)[TW], const int64_t* xoff,
                                         const float* const* xs, int j, GfStep<TW>& st) {
   const int kg = (threadIdx.x % kWave) / 16;
   const int k = j * 32 + kg * 8;
 #pragma unroll
-  for (int t = 0; t < TW; ++t) st.w[t] = *reinterpret_cast<const uint4*>(wrow[S][t] + j * 32);
+  for (int t = 0; t < TW; ++t) st.w[t] = *reinterpret_cast<const uint4*>(wrow[S][t] + j * gf_step<FRAG>());
   if constexpr (STG) {
     st.x0 = *reinterpret_cast<const uint4*>(xs[S] + k);
     st.x1 = *reinterpret_cast<const uint4*>(xs[S] + k + 4);
@@ -141,8 +149,9 @@ __device__ __forceinline__ void gf_compute(const GfStep<TW>& st, gff32x4 (*acc)[
 // a.lds_floats), with their sums of squares, so the k steps read x from LDS
 // instead of every lane loading its 32 bytes of x and 16 of gain from memory.
 constexpr int kGfUnit = 2048;  // staged elements per (wave, unit): 8 four-element chunks per lane
-template <int TW, int W, int D, bool PAIR, int NIN, int XB, int GB, bool STG = false>
+template <int TW, int W, int D, bool PAIR, int NIN, int XB, int GB, bool STG = false, bool FRAG = false>
 __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
+  static_assert(!FRAG || NIN == 1, "fragment-major weights: one input segment");
   constexpr int kGfWaves = W, kGfThreads = W * kWave, kGfD = D;
   static_assert(!PAIR || TW == 2, "the pair epilogue takes a gate tile and an up tile");
   constexpr int RB = PAIR ? 16 : 16 * TW;  // logical output rows per block
@@ -174,7 +183,13 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
       const int n = PAIR ? min(row0 + lm, a.N - 1) : min(row0 + tt * 16 + lm, a.N - 1);
-      wrow[s][tt] = row_ptr<PAIR>(a, n, PAIR ? tt : 0, s) + kg * 8;
+      if constexpr (FRAG) {
+        // tile n / 16 of the fragment-major matrix (rows padded to 16), lane l's chunk
+        const uint16_t* base = PAIR ? (tt ? a.w[1][s] : a.w[0][s]) : a.w[0][s];
+        wrow[s][tt] = base + static_cast<int64_t>(n / 16) * (a.in[s].K / 32) * (64 * 8) + lane * 8;
+      } else {
+        wrow[s][tt] = row_ptr<PAIR>(a, n, PAIR ? tt : 0, s) + kg * 8;
+      }
     }
     xoff[s] = static_cast<int64_t>(in_row(a.in[s], min(lm, a.M - 1))) * a.in[s].ld;
     nsteps[s] = a.in[s].K / 32;
@@ -286,7 +301,7 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
 #define GF_LOAD(i, ST)                                                                         \
   do {                                                                                         \
     GF_SEG(i, s_, j_);                                                                         \
-    if (s_ == 0) gf_load<0, TW, PAIR, XB, GB, STG>(a, wrow, xoff, xs, j_, ST);                \
+    if (s_ == 0) gf_load<0, TW, PAIR, XB, GB, STG, FRAG>(a, wrow, xoff, xs, j_, ST);          \
     if constexpr (NIN > 1) if (s_ == 1) gf_load<1 < NIN ? 1 : 0, TW, PAIR, XB, GB, STG>(a, wrow, xoff, xs, j_, ST); \
     if constexpr (NIN > 2) if (s_ == 2) gf_load<2 < NIN ? 2 : 0, TW, PAIR, XB, GB, STG>(a, wrow, xoff, xs, j_, ST); \
   } while (0)
@@ -312,7 +327,7 @@ __global__ __launch_bounds__(W * kWave) void k_gemvf(GemvArgs a) {
         // scratch memory and every weight load waits on a scratch load
 #pragma unroll
         for (int tt = 0; tt < TW; ++tt) {
-          if (s_ == 0) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[0][tt] + j_ * 32);
+          if (s_ == 0) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[0][tt] + j_ * gf_step<FRAG>());
           if constexpr (NIN > 1) if (s_ == 1) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[1 < NIN ? 1 : 0][tt] + j_ * 32);
           if constexpr (NIN > 2) if (s_ == 2) ring[u].w[tt] = *reinterpret_cast<const uint4*>(wrow[2 < NIN ? 2 : 0][tt] + j_ * 32);
         }

@@ -197,6 +197,9 @@ class TargetModel:
                     t = frag_weights(t)
                 self.w[f"layers.{i}.{name}"] = t
                 setattr(lw, f, ptr(t))
+            # the few-row path's gate / up pair streams the fragment-major copies
+            lwr.gate_frag = ptr(self.w[f"layers.{i}.mlp.gate_proj.weight"])
+            lwr.up_frag = ptr(self.w[f"layers.{i}.mlp.up_proj.weight"])
             self.lw.append(lw)
             self.lwr.append(lwr)
         for name, shape in (("embed_tokens.weight", (cfg.vocab_size, cfg.hidden_size)),
