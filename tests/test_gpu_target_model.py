@@ -137,3 +137,37 @@ def test_target_forward_rejects_bad_shapes(cuda):
         model(torch.zeros(9, dtype=torch.int32, device=dev), cache, off)
     with pytest.raises(ValueError):
         model(torch.zeros(4, dtype=torch.int32, device=dev), cache[:3], off)
+
+
+@pytest.mark.parametrize("cfg,rows,prefix", [(SMALL, 5, 40), (TargetConfig(num_layers=2), 5, 512),
+                                             (TargetConfig(num_layers=2), 2, 300)])
+def test_few_row_path_equals_verify_width_path(cuda, cfg, rows, prefix):
+    """A chain block that takes the few-row path (no mask, few query vectors)
+    gives the logits, taps and appended K/V of the same block forced onto the
+    verify-width path by an explicit causal mask, to the fp32 tolerance."""
+    dev = torch.device("cuda", 0)
+    w = random_target(cfg, seed=rows + prefix + 1, device=dev)
+    model = TargetModel(cfg, w, dev, max_rows=64, feature_layers=(0, cfg.num_layers - 1))
+    assert model._few_rows_fit(rows, prefix + rows)
+    cap = prefix + rows + 8
+    g = torch.Generator(device=dev).manual_seed(prefix)
+    caches = [model.make_cache(cap), model.make_cache(cap)]
+    for ca, cb in zip(*caches):
+        ca.keys[0, :, :prefix] = torch.randn(ca.keys[0, :, :prefix].shape, generator=g, device=dev).bfloat16()
+        ca.values[0, :, :prefix] = torch.randn(ca.values[0, :, :prefix].shape, generator=g, device=dev).bfloat16()
+        cb.keys.copy_(ca.keys)
+        cb.values.copy_(ca.values)
+        ca.offset = cb.offset = prefix
+    tokens = torch.from_numpy(np.random.default_rng(prefix).integers(0, cfg.vocab_size, rows).astype(np.int32))
+    off = torch.tensor([prefix], dtype=torch.int32, device=dev)
+    causal = np.tril(np.ones((rows, prefix + rows), np.uint8), k=prefix)
+    za, ta = model(tokens.to(dev), caches[0], off)
+    za, ta = za.clone(), [t.clone() for t in ta]
+    zb, tb = model(tokens.to(dev), caches[1], off, mask=torch.from_numpy(causal))
+    assert rel(za.cpu().numpy(), zb.cpu().numpy()) < 1e-4
+    for x, y in zip(ta, tb):
+        assert rel(x.cpu().numpy(), y.cpu().numpy()) < 1e-4
+    for ca, cb in zip(*caches):
+        kx = ca.keys[0, :, prefix:prefix + rows].float().cpu().numpy()
+        ky = cb.keys[0, :, prefix:prefix + rows].float().cpu().numpy()
+        assert rel(kx, ky) < 1e-2
