@@ -30,6 +30,8 @@
 
 namespace wc {
 
+constexpr int kGkWavesMax = 16;  // waves of a block, at most
+
 // sum over each 16-lane row by DPP moves; every lane of a row holds its row's total
 __device__ __forceinline__ float row16_total(float v) {
   v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
@@ -37,6 +39,76 @@ __device__ __forceinline__ float row16_total(float v) {
   v += dpp_move<0x124>(v);  // row_ror:4
   v += dpp_move<0x128>(v);  // row_ror:8
   return v;
+}
+
+// Last block of the launch (device counter, reset by the finisher): the final
+// RMSNorm of the m produced rows, read back coherently (they were published),
+// into fin_out, and the offset advance.  Every row's values and the gains are
+// requested at once (one round trip for all rows, from clamped addresses) when
+// a row is at most kFinPer values per thread; sums in wave order.
+constexpr int kFinPer = 8;
+template <int MM>
+__device__ __forceinline__ void gk_fin_epilogue(const GemvArgs& a, int m, float (*s_red)[kGkWavesMax]) {
+  if (!last_block_done(a.fin_counter, gridDim.x)) return;
+  const int nt = blockDim.x, nw = nt / kWave, lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int t = threadIdx.x;
+  const int adv = (t == 0 && a.adv_dst) ? *a.adv_src : 0;
+  if (a.N <= kFinPer * nt) {
+    float v[MM][kFinPer];
+    uint32_t gw[kFinPer];
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi)
+#pragma unroll
+      for (int j = 0; j < kFinPer; ++j)
+        v[mi][j] = fetch_f32(a.y + min(mi, max(m - 1, 0)) * a.ldy + min(t + j * nt, a.N - 1));
+#pragma unroll
+    for (int j = 0; j < kFinPer; ++j) gw[j] = a.fin_gain[min(t + j * nt, a.N - 1)];
+#pragma unroll
+    for (int j = 0; j < kFinPer; ++j) pin(gw[j]);
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kFinPer; ++j) {
+        const float x = t + j * nt < a.N ? v[mi][j] : 0.f;
+        ss = fmaf(x, x, ss);
+      }
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) s_red[mi][wave] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mi = 0; mi < MM; ++mi) {
+      if (mi >= m) continue;
+      float tot = 0.f;
+      for (int w = 0; w < nw; ++w) tot += s_red[mi][w];
+      const float inv = 1.f / sqrtf(tot / static_cast<float>(a.N) + a.eps);
+#pragma unroll
+      for (int j = 0; j < kFinPer; ++j) {
+        const int k = t + j * nt;
+        if (k < a.N) a.fin_out[mi * a.ld_fin + k] = v[mi][j] * inv * bf16_to_float(static_cast<uint16_t>(gw[j]));
+      }
+    }
+  } else {
+    for (int mi = 0; mi < m; ++mi) {
+      const float* yr = a.y + mi * a.ldy;
+      float ss = 0.f;
+      for (int k = t; k < a.N; k += nt) {
+        const float x = fetch_f32(yr + k);
+        ss = fmaf(x, x, ss);
+      }
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) s_red[0][wave] = ss;
+      __syncthreads();
+      float tot = 0.f;
+      for (int w = 0; w < nw; ++w) tot += s_red[0][w];
+      const float inv = 1.f / sqrtf(tot / static_cast<float>(a.N) + a.eps);
+      for (int k = t; k < a.N; k += nt)
+        a.fin_out[mi * a.ld_fin + k] = fetch_f32(yr + k) * inv * bf16_to_float(a.fin_gain[k]);
+      __syncthreads();
+    }
+  }
+  if (t == 0 && a.adv_dst) *a.adv_dst = adv + a.adv_add + m;
 }
 
 // R: logical output rows per block (gate rows for PAIR); S: 512-wide k steps
@@ -54,6 +126,7 @@ __global__ __launch_bounds__(WB * kWave) void k_gemvk(GemvArgs a) {
   __shared__ float s_ss[WB][MM][4];
   __shared__ float s_dot[WB][R * P][MM][4];
   __shared__ float s_inv[NIN][MM];
+  __shared__ float s_fin[MM][kGkWavesMax];
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int nw = blockDim.x / kWave;
@@ -269,7 +342,13 @@ __global__ __launch_bounds__(WB * kWave) void k_gemvk(GemvArgs a) {
     }
     store_out<PAIR>(a, m, n, g, u, res_value(a, m, n));
   }
-  // the cache offset advance of the last projection (no block reads it here)
+  // the final RMSNorm of the produced rows (the drafter's `out`) by the last
+  // block, which then also advances the offset
+  if (a.fin_gain) {
+    gk_fin_epilogue<MM>(a, m_live, s_fin);
+    return;
+  }
+  // otherwise the cache offset advance of the last projection (no block reads it here)
   if (a.adv_dst && blockIdx.x == 0 && t == 0) *a.adv_dst = *a.adv_src + a.adv_add + m_live;
 }
 

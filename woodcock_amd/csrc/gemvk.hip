@@ -47,7 +47,8 @@ static bool launch_gemvk_g(const GemvArgs& a, int S, int waves, bool wide, hipSt
 // rows (fuse, down: fewer blocks for the same bytes in flight).
 template <int NIN, int XB>
 static bool launch_gemvk(const GemvArgs& a, hipStream_t s) {
-  if (a.M < 2 || a.M > 8 || a.fin_gain || a.xn_out || a.epi == kEpiArgmax || a.n_in != NIN) return false;
+  if (a.M < 2 || a.M > 8 || a.xn_out || a.epi == kEpiArgmax || a.n_in != NIN) return false;
+  if (a.fin_gain && (!a.fin_counter || !a.fin_out)) return false;
   int gb = 0, st[kMaxIn] = {0, 0, 0};
   for (int i = 0; i < NIN; ++i) {
     if (a.in[i].K % 512 != 0 || a.in[i].K == 0) return false;
