@@ -14,11 +14,14 @@
 // (row, input row) product with fp32 FMAs.  A wave's x slices are its own (the
 // waves of a block tile K), so nothing is staged in LDS and x is read once per
 // block (the x rows are L2-resident after the first blocks), against once per
-// block for all of K in an LDS-staged design.  The vector ALU work is what
-// limits this kernel at a few hundred blocks per CU-wave of M = 3..8 rows:
-// the weights are widened once (not once per input row), input rows past the
-// device row count are skipped by wave-uniform branches, and the lanes are
-// reduced within 16-lane rows only (four DPP steps per value).
+// block for all of K in an LDS-staged design.  Each wave's vector-ALU work
+// between its loads' arrival and its partial sums (M fused multiply-adds per
+// weight element, the lane reductions) sits on the block's critical path, so
+// it is kept short: the weights are widened once (not once per input row),
+// input rows past the device row count are skipped by wave-uniform branches,
+// and the lanes are reduced within 16-lane rows only (four DPP steps per
+// value).  (Counters show 8-26% VALU busy over the launch: the limit is the
+// latency of each block's load -> compute -> reduce chain, not ALU throughput.)
 // Per (output row, input row) each 16-lane row of the wave is summed with DPP
 // moves and leaves its total of the partial product and of the partial sum of
 // squares in LDS;
