@@ -27,6 +27,7 @@ static bool launch_gemvk_w(const GemvArgs& a, int waves, hipStream_t s) {
 template <int R, bool PAIR, int NIN, int S, int XB, int GB>
 static bool launch_gemvk_m(const GemvArgs& a, int waves, hipStream_t s) {
   if (a.M <= 4) return launch_gemvk_w<R, PAIR, NIN, S, 4, XB, GB>(a, waves, s);
+  if (a.M <= 6) return launch_gemvk_w<R, PAIR, NIN, S, 6, XB, GB>(a, waves, s);
   return launch_gemvk_w<R, PAIR, NIN, S, 8, XB, GB>(a, waves, s);
 }
 // R: output rows per block, the wide choice (twice the rows) on one step per wave only
