@@ -131,8 +131,7 @@ def bench_gpu(args):
         target.plant(rnd.drafts, 2)
 
     def commit():
-        rnd.enqueue_verify(target.logits)
-        rnd.enqueue_commit(target.taps)
+        rnd.enqueue_verify_commit(target.logits, target.taps)
         rnd.enqueue_readback()
 
     # eager warm-up round (kernel attributes, allocator), then capture

@@ -408,6 +408,23 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
                     int64_t tap_ld, const int32_t* tap_rows_dev, int tap_rows, int rows, const int32_t* n_rows_dev,
                     float* g_out, int64_t g_ld, void* workspace, wc_stream_t stream);
 
+/* A chain round's verify and fuse in one launch: wc_verify_chain_greedy over
+ * logits [rows][vocab] and the drafts, and wc_drafter_fuse of tap rows
+ * 0..rows-1 into g_out (every row, no gather).  A chain keeps the prefix
+ * [0..a] of its verify block (python/woodcock/spec.py:362-366) and the fuse is
+ * row-wise (python/woodcock/drafter.py:149-153), so the fused rows 0..a are
+ * the ones the update pass needs whatever a turns out to be.  Equal to the two
+ * calls in sequence, which it makes when the shapes do not fit one launch
+ * (one launch: 2..8 rows, three taps of 2048, every tap normed or none,
+ * 16-byte logits rows, enough CUs beside the fuse's blocks for the verify's
+ * chunks).  No counterpart call in the reference: its round runs the two
+ * steps one after the other (python/woodcock/spec.py:356-372). */
+int wc_verify_chain_greedy_fuse(const float* logits, int rows, int vocab, int64_t ld,
+                                const int32_t* draft_tokens_dev, wc_verdict* verdict_dev, void* verify_workspace,
+                                const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps,
+                                int tap_dtype, int64_t tap_ld, float* g_out, int64_t g_ld, void* drafter_workspace,
+                                wc_stream_t stream);
+
 /* One drafting forward over `rows` tokens appended at cache offset
  * *offset_dev + offset_add: every layer (dual-stream layer 0, GQA attention
  * with q/k RMSNorm and rotate-half RoPE, SwiGLU MLP), then the final RMSNorm.

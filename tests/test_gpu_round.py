@@ -22,7 +22,7 @@ def small_cfg():
                          intermediate_size=512, vocab_size=4096, target_hidden_size=192, rope_theta=1e6)
 
 
-def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256, cfg=None, head_rows=1024):
+def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256, cfg=None, head_rows=1024, k=K):
     from woodcock_amd.drafter import Drafter
     from woodcock_amd.spec import ChainRound
     from woodcock_amd.synthetic import SyntheticTarget, draft_vocab, random_drafter, to_bits
@@ -33,7 +33,7 @@ def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256, cfg=None, head_ro
     d = Drafter(cfg, dict(w), cuda, kv_dtype)
     d._vocab_ids = torch.from_numpy(ids).to(cuda)
     d._build_structs(d._rope[0].shape[0])
-    rnd = ChainRound(d, K, cap)
+    rnd = ChainRound(d, k, cap)
     od = core.Drafter(cfg.as_dict(), {k: to_bits(v) for k, v in w.items()})
     od.d2t = ids
     oc = od.make_cache(cap, kv_bf16=kv_dtype == torch.bfloat16)
@@ -50,7 +50,7 @@ def setup(cuda, seed, ctx=40, kv_dtype=torch.float32, cap=256, cfg=None, head_ro
     oc.offset = ctx
     root = torch.randn(1, cfg.hidden_size, generator=g, device=cuda)  # the root's pre-norm hidden state
     rnd.set_root(ctx, root)
-    target = SyntheticTarget(K, cfg.vocab_size, cfg.target_hidden_size, device=cuda, seed=seed + 1)
+    target = SyntheticTarget(k, cfg.vocab_size, cfg.target_hidden_size, device=cuda, seed=seed + 1)
     return cfg, d, rnd, od, oc, target, root.cpu().numpy()
 
 
@@ -71,11 +71,14 @@ def oracle_round(od, oc, root_out, root_fb, logits, taps):
     return drafts, a, acc, out[-1:], od.feedback(hid[-1:], out[-1:]), hid[-1:]
 
 
-def gpu_round(rnd, target, n_agree):
+def gpu_round(rnd, target, n_agree, fused=False):
     rnd.enqueue_draft()
     target.plant(rnd.drafts, n_agree)
-    rnd.enqueue_verify(target.logits)
-    rnd.enqueue_commit(target.taps)
+    if fused:  # the verify and the fuse of every tap row in one launch
+        rnd.enqueue_verify_commit(target.logits, target.taps)
+    else:
+        rnd.enqueue_verify(target.logits)
+        rnd.enqueue_commit(target.taps)
     rnd.enqueue_readback()
     return rnd.finish()
 
@@ -118,7 +121,7 @@ def test_config1_rounds_match_oracle_round(cuda):
     root_out = core.rmsnorm(root, od.w["norm.weight"], cfg.rms_norm_eps)
     root_fb = od.feedback(root, root_out)
     for r, n_agree in enumerate([2, 4, 0]):
-        res = gpu_round(rnd, target, n_agree)
+        res = gpu_round(rnd, target, n_agree, fused=True)
         logits = target.logits.cpu().numpy()
         taps = [t.float().cpu().numpy() for t in target.taps]
         drafts, a, acc, root_out, root_fb, root_hid = oracle_round(od, oc, root_out, root_fb, logits, taps)
@@ -131,6 +134,57 @@ def test_config1_rounds_match_oracle_round(cuda):
         k_gpu = rnd.cache[0].keys[0, :, 512:n].float().cpu().numpy()
         assert _rel(k_gpu, oc.keys_f32(0)[:, 512:n]) <= 1e-2, f"round {r}"
     assert rnd.syncs == 3
+
+
+@pytest.mark.parametrize("kv,shape,k", [("f32", "small", 4), ("bf16", "small", 4), ("bf16", "qwen3_1p7b", 4),
+                                        ("f32", "qwen3_1p7b", 7), ("bf16", "qwen3_1p7b", 8)])
+def test_fused_verify_commit_equals_sequential(cuda, kv, shape, k):
+    """enqueue_verify_commit (the greedy verify and the fuse of all k + 1 tap
+    rows in one launch) leaves the verdict, root rows, drafter cache and device
+    state of enqueue_verify + enqueue_commit (the fuse of the kept rows after
+    the verdict) bit for bit, eagerly and replayed from captured graphs between
+    eager rounds; at the small shape the taps' width takes the two-launch
+    fallback, at the Qwen3-1.7B shape the one-launch kernel (k = 4: 250 verify
+    units of 3,072 logits over 256 blocks, one each; k = 7: 400, two in some)
+    up to its bound of eight rows (k = 8 falls back)."""
+    from woodcock_amd.config import qwen3_1p7b_drafter
+
+    kv_dtype = torch.float32 if kv == "f32" else torch.bfloat16
+    kw = dict(cfg=qwen3_1p7b_drafter(), head_rows=16384, ctx=512, cap=1024) if shape != "small" else {}
+    kw["k"] = k
+    pattern = [3, 0, 4, 1, 2] if k == 4 else [k, 0, 5, k - 1, 2]
+    _, _, seq, _, _, ts, _ = setup(cuda, 11, kv_dtype=kv_dtype, **kw)
+    _, _, fus, _, _, tf, _ = setup(cuda, 11, kv_dtype=kv_dtype, **kw)
+    for r, n in enumerate(pattern):
+        a = gpu_round(seq, ts, n)
+        b = gpu_round(fus, tf, n, fused=True)
+        assert (a.n_accepted, a.tokens) == (b.n_accepted, b.tokens) and a.n_accepted == n, f"round {r}"
+        assert torch.equal(seq.verdict, fus.verdict), f"round {r}"
+        assert torch.equal(seq.state, fus.state), f"round {r}"
+        assert torch.equal(seq.upd_hid[: n + 1], fus.upd_hid[: n + 1]), f"round {r}"
+        assert torch.equal(seq.cache[0].keys, fus.cache[0].keys), f"round {r}"
+        assert torch.equal(seq.cache[0].values, fus.cache[0].values), f"round {r}"
+    s = torch.cuda.Stream()
+    graphs = {}
+    for r, n in enumerate(pattern):
+        a = gpu_round(seq, ts, n)
+        if n not in graphs:
+            s.wait_stream(torch.cuda.current_stream())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                fus.enqueue_draft()
+                tf.plant(fus.drafts, n)
+                fus.enqueue_verify_commit(tf.logits, tf.taps)
+                fus.enqueue_readback()
+            torch.cuda.synchronize()
+            graphs[n] = g
+        graphs[n].replay()
+        b = fus.finish()
+        _ = torch.ones(3, device=cuda).sum().item()  # eager work between replays
+        assert (a.n_accepted, a.tokens) == (b.n_accepted, b.tokens), f"replay {r}"
+        assert torch.equal(seq.verdict, fus.verdict), f"replay {r}"
+        assert torch.equal(seq.upd_hid[: n + 1], fus.upd_hid[: n + 1]), f"replay {r}"
+        assert torch.equal(seq.cache[0].keys, fus.cache[0].keys), f"replay {r}"
 
 
 def test_enqueue_never_synchronises(cuda):

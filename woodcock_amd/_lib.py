@@ -94,6 +94,8 @@ _SIGS = {
     "wc_set_spin_limit": ([C.c_int], C.c_int),
     "wc_argmax_rows": ([P, C.c_int, C.c_int, I64, P, P, P], C.c_int),
     "wc_verify_chain_greedy": ([P, C.c_int, C.c_int, I64, P, P, P, P], C.c_int),
+    "wc_verify_chain_greedy_fuse": ([P, C.c_int, C.c_int, I64, P, P, P, P, P, P, C.c_int, I64, P, I64, P, P],
+                                    C.c_int),
     "wc_verify_chain_greedy_static": ([P, C.c_int, C.c_int, I64, P, P, P], C.c_int),
     "wc_verify_tree_greedy": ([P, C.c_int, C.c_int, I64, P, P, P, P, P], C.c_int),
     "wc_kv_compact": ([P, P, C.c_int, C.c_int, C.c_int, C.c_int, P, P, P, C.c_int, P, P, P], C.c_int),

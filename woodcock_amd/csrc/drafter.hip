@@ -635,6 +635,48 @@ size_t wc_drafter_workspace_bytes(const wc_drafter_dims* dims) {
   return drafter_ws(*dims, nullptr).bytes;
 }
 
+}  // extern "C"
+
+namespace wc {
+// The fuse's GEMV arguments for rows 0..rows-1 of the taps (no gather, every
+// row live, rows <= WC_MAX_STEP_ROWS): the launch that runs the greedy verify
+// beside the fuse builds its GEMV part from these.
+int fuse_gemv_args(const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps, int tap_dtype,
+                   int64_t tap_ld, int rows, float* g_out, int64_t g_ld, GemvArgs* out) {
+  if (int rc = check_dims(dims)) return rc;
+  WC_REQUIRE(w && taps && g_out && out, "fuse: NULL argument");
+  WC_REQUIRE(w->fc && al16(w->fc), "fuse: fc weight missing or not 16-byte aligned");
+  WC_REQUIRE(tap_dtype == WC_F32 || tap_dtype == WC_BF16, "fuse: tap dtype must be f32 or bf16");
+  WC_REQUIRE(tap_ld >= dims->target_hidden && g_ld >= dims->hidden && tap_ld % 8 == 0 && g_ld % 4 == 0,
+             "fuse: bad row stride");
+  WC_REQUIRE(rows >= 1 && rows <= WC_MAX_STEP_ROWS, "fuse: rows must be in 1..%d", WC_MAX_STEP_ROWS);
+  const int nf = dims->num_features, Dt = dims->target_hidden;
+  GemvArgs g = gemv_defaults();
+  g.n_in = nf;
+  for (int f = 0; f < nf; ++f) {
+    WC_REQUIRE(taps[f] != nullptr && al16(taps[f]), "fuse: tap %d is NULL or not 16-byte aligned", f);
+    g.in[f].x = taps[f];
+    g.in[f].ld = tap_ld;
+    g.in[f].dtype = tap_dtype;
+    g.in[f].gain = u16(w->feature_norm[f]);
+    g.in[f].K = Dt;
+    g.ldw[f] = static_cast<int64_t>(nf) * Dt;
+    g.w[0][f] = u16(w->fc) + static_cast<int64_t>(f) * Dt;
+  }
+  g.N = dims->hidden;
+  g.seg_start[1] = g.N;
+  g.M = rows;
+  g.eps = dims->eps;
+  g.epi = kEpiStore;
+  g.y = g_out;
+  g.ldy = g_ld;
+  *out = g;
+  return WC_OK;
+}
+}  // namespace wc
+
+extern "C" {
+
 int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, const void* const* taps, int tap_dtype,
                     int64_t tap_ld, const int32_t* tap_rows_dev, int tap_rows, int rows, const int32_t* n_rows_dev,
                     float* g_out, int64_t g_ld, void* workspace, wc_stream_t stream) {

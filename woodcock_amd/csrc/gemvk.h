@@ -51,8 +51,9 @@ __device__ __forceinline__ float row16_total(float v) {
 // a row is at most kFinPer values per thread; sums in wave order.
 constexpr int kFinPer = 8;
 template <int MM>
-__device__ __forceinline__ void gk_fin_epilogue(const GemvArgs& a, int m, float (*s_red)[kGkWavesMax]) {
-  if (!last_block_done(a.fin_counter, gridDim.x)) return;
+__device__ __forceinline__ void gk_fin_epilogue(const GemvArgs& a, int m, float (*s_red)[kGkWavesMax], int blk,
+                                                int nblk) {
+  if (!last_block_done(a.fin_counter, nblk, blk)) return;
   const int nt = blockDim.x, nw = nt / kWave, lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int t = threadIdx.x;
   const int adv = (t == 0 && a.adv_dst) ? *a.adv_src : 0;
@@ -120,8 +121,10 @@ __device__ __forceinline__ void gk_fin_epilogue(const GemvArgs& a, int m, float 
 // launch uses blockDim.x / 64 waves).  Waves are segment-aligned: the host
 // checks that every segment's step count is a multiple of S, except with one
 // segment, where the last wave's steps past the end are zeroed.
+// One block of the GEMV: block blk of nblk (a kernel of its own, or the GEMV
+// part of a launch that runs other work in its other blocks).
 template <int R, bool PAIR, int NIN, int S, int MM, int XB, int GB, int WB>
-__global__ __launch_bounds__(WB * kWave) void k_gemvk(GemvArgs a) {
+__device__ __forceinline__ void gemvk_block(const GemvArgs& a, const int blk, const int nblk) {
   static_assert(NIN >= 1 && NIN <= 3, "one to three input segments");
   static_assert(GB == 0 || GB == (1 << NIN) - 1, "every segment normed or none");
   constexpr int P = PAIR ? 2 : 1;
@@ -133,7 +136,7 @@ __global__ __launch_bounds__(WB * kWave) void k_gemvk(GemvArgs a) {
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int nw = blockDim.x / kWave;
-  const int row0 = blockIdx.x * R;
+  const int row0 = blk * R;
   constexpr int S1 = NIN > 1 ? 1 : 0, S2 = NIN > 2 ? 2 : 0;
 
   // this wave's segment and first local step (scalar selects over arguments
@@ -348,11 +351,16 @@ __global__ __launch_bounds__(WB * kWave) void k_gemvk(GemvArgs a) {
   // the final RMSNorm of the produced rows (the drafter's `out`) by the last
   // block, which then also advances the offset
   if (a.fin_gain) {
-    gk_fin_epilogue<MM>(a, m_live, s_fin);
+    gk_fin_epilogue<MM>(a, m_live, s_fin, blk, nblk);
     return;
   }
   // otherwise the cache offset advance of the last projection (no block reads it here)
-  if (a.adv_dst && blockIdx.x == 0 && t == 0) *a.adv_dst = *a.adv_src + a.adv_add + m_live;
+  if (a.adv_dst && blk == 0 && t == 0) *a.adv_dst = *a.adv_src + a.adv_add + m_live;
+}
+
+template <int R, bool PAIR, int NIN, int S, int MM, int XB, int GB, int WB>
+__global__ __launch_bounds__(WB * kWave) void k_gemvk(GemvArgs a) {
+  gemvk_block<R, PAIR, NIN, S, MM, XB, GB, WB>(a, blockIdx.x, gridDim.x);
 }
 
 }  // namespace wc

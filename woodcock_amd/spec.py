@@ -201,16 +201,45 @@ class ChainRound:
         tdt = V.WC_BF16 if taps[0].dtype == torch.bfloat16 else V.WC_F32
         V.call("wc_drafter_fuse", dims, W, tp, tdt, taps[0].stride(0), ptr(keep), taps[0].shape[0], rows,
                ptr(n_keep), ptr(self.g), dm, ws, s)
-        # appends the accepted entries at n and advances n in place (last kernel of the pass)
-        V.call("wc_drafter_forward", dims, W, ptr(self.verdict[V.V_TOKENS:V.V_TOKENS + rows]), ptr(self.g), dm,
-               None, 0, rows, ptr(n_keep), self._kp, self._vp, self._kvdt, self.cache[0].capacity,
-               ptr(self.n_dev()), 0, None, None, 0, ptr(self.upd_hid), None, ptr(self.n_dev()), ws, s)
+        self._enqueue_pass(rows)
+
+    def _enqueue_pass(self, rows: int) -> None:
+        """The drafter pass of the update over the n_keep accepted tokens and the
+        fused rows in self.g; appends at n and advances n in place (its last kernel)."""
+        d = self.d
+        V = _lib
+        n_keep = self.verdict[V.V_N_KEEP:V.V_N_KEEP + 1]
+        V.call("wc_drafter_forward", C.byref(d.dims), C.byref(d.wstruct),
+               ptr(self.verdict[V.V_TOKENS:V.V_TOKENS + rows]), ptr(self.g), d.cfg.hidden_size, None, 0, rows,
+               ptr(n_keep), self._kp, self._vp, self._kvdt, self.cache[0].capacity, ptr(self.n_dev()), 0, None, None,
+               0, ptr(self.upd_hid), None, ptr(self.n_dev()), ptr(d.ws), stream_ptr())
 
     def enqueue_commit(self, taps: list[torch.Tensor], k: int | None = None) -> None:
         """The chain's commit: the drafter update over the a+1 accepted tokens
         (spec.py:362-374), keyed off the verdict.  The target KV keeps the
         verify block's prefix in place, so nothing moves (target.py:170)."""
         self._enqueue_update(taps, self._k(k) + 1)
+
+    def enqueue_verify_commit(self, target_logits: torch.Tensor, taps: list[torch.Tensor],
+                              k: int | None = None) -> None:
+        """enqueue_verify + enqueue_commit of a chain round with the verify and
+        the fuse in one launch (wc_verify_chain_greedy_fuse): a chain keeps the
+        prefix [0..a] of its verify block (spec.py:362-366) and the fuse is
+        row-wise, so the fuse of all k + 1 tap rows need not wait for the
+        verdict; the drafter pass then reads rows 0..a.  Verdict, drafter cache
+        and state equal those of the two calls in sequence."""
+        k = self._k(k)
+        rows = k + 1
+        if target_logits.shape[0] != rows or any(t.shape[0] < rows for t in taps):
+            raise ValueError(f"a chain of {k} drafts verifies {rows} rows")
+        d = self.d
+        tp = (C.c_void_p * len(taps))(*[t.data_ptr() for t in taps])
+        tdt = _lib.WC_BF16 if taps[0].dtype == torch.bfloat16 else _lib.WC_F32
+        _lib.call("wc_verify_chain_greedy_fuse", ptr(target_logits), rows, target_logits.shape[1],
+                  target_logits.stride(0), ptr(self.drafts), ptr(self.verdict), ptr(self.vws), C.byref(d.dims),
+                  C.byref(d.wstruct), tp, tdt, taps[0].stride(0), ptr(self.g), d.cfg.hidden_size, ptr(d.ws),
+                  stream_ptr())
+        self._enqueue_pass(rows)
 
     def enqueue_readback(self) -> None:
         self.host_verdict.copy_(self.verdict, non_blocking=True)
@@ -220,8 +249,7 @@ class ChainRound:
         at [x_n, d_1..d_K] (a synthetic stand-in whose rows are already in place)."""
         k = self._k(k)
         self.enqueue_draft(k)
-        self.enqueue_verify(target.logits[:k + 1])
-        self.enqueue_commit([t[:k + 1] for t in target.taps], k)
+        self.enqueue_verify_commit(target.logits[:k + 1], [t[:k + 1] for t in target.taps], k)
         self.enqueue_readback()
 
     # ------------------------------------------------------------------ tree rounds
@@ -426,8 +454,7 @@ class SpeculativeDecoder:
 
         def commit():
             logits, taps = io["out"]
-            r.enqueue_verify(logits)
-            r.enqueue_commit(taps, k)
+            r.enqueue_verify_commit(logits, taps, k)
             r.enqueue_readback()
 
         return draft, target, commit
