@@ -3,6 +3,8 @@ oracle round built from the CPU drafter restatement, round after round:
 identical drafted tokens, accepted lengths and accepted tokens; root outputs
 and drafter caches within the fp32 tolerance; exactly one host sync per
 round; a captured HIP graph replays to the same results as eager rounds."""
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -185,6 +187,68 @@ def test_fused_verify_commit_equals_sequential(cuda, kv, shape, k):
         assert torch.equal(seq.verdict, fus.verdict), f"replay {r}"
         assert torch.equal(seq.upd_hid[: n + 1], fus.upd_hid[: n + 1]), f"replay {r}"
         assert torch.equal(seq.cache[0].keys, fus.cache[0].keys), f"replay {r}"
+
+
+@pytest.mark.parametrize("tap_dtype", ["bf16", "f32"])
+def test_verify_fuse_entry_edges(cuda, tap_dtype):
+    """wc_verify_chain_greedy_fuse against wc_verify_chain_greedy followed by
+    wc_drafter_fuse over the same rows, through the C-ABI, at the Qwen3-1.7B
+    fuse shape: rows 1..8 (1 takes the two-call path, 2..8 the one launch), a
+    ragged vocab (151,933 logits in rows of 151,936: the last float4 of a row
+    is partial), the argmax planted in the last chunk, at index 0 and as ties
+    (lowest index wins), and drafts that agree for a chosen prefix.  The
+    verdict and the fused rows must be bit-identical."""
+    from woodcock_amd import _lib
+    from woodcock_amd.config import qwen3_1p7b_drafter
+    from woodcock_amd.runtime import new_verdict, ptr, stream_ptr
+
+    _, d, rnd, _, _, _, _ = setup(cuda, 5, cfg=qwen3_1p7b_drafter(), head_rows=16384, ctx=64, cap=128, k=7)
+    V, LD, Dt = 151933, 151936, d.cfg.target_hidden_size
+    g = torch.Generator(device=cuda).manual_seed(3)
+    dt = torch.bfloat16 if tap_dtype == "bf16" else torch.float32
+    tdt = _lib.WC_BF16 if tap_dtype == "bf16" else _lib.WC_F32
+    ws = [torch.empty_like(rnd.vws) for _ in range(2)]
+    for w in ws:
+        _lib.call("wc_workspace_init", ptr(w), w.numel(), stream_ptr())
+    for rows in range(1, 9):
+        for case in range(3):
+            buf = torch.randn(rows, LD, generator=g, device=cuda)
+            logits = buf[:, :V]
+            if case == 0:
+                logits[0, V - 1] = 50.0  # the ragged end of row 0
+                if rows > 1:
+                    logits[1, 0] = 50.0
+            elif case == 1:  # ties: the lowest index wins
+                logits[:, 1000] = 40.0
+                logits[:, 99000] = 40.0
+            am = logits.argmax(dim=1).to(torch.int32)
+            n_agree = (rows - 1) // 2 if case != 2 else rows - 1
+            drafts = am[: rows - 1].clone()  # draft c is checked against row c's argmax
+            if n_agree < rows - 1:
+                drafts[n_agree] = (drafts[n_agree] + 1) % V
+            drafts = drafts if rows > 1 else torch.zeros(1, dtype=torch.int32, device=cuda)
+            taps = [torch.randn(rows, Dt, generator=g, device=cuda).to(dt) for _ in range(3)]
+            tp = (C.c_void_p * 3)(*[x.data_ptr() for x in taps])
+            outs = []
+            for which in range(2):
+                verdict = new_verdict(cuda)
+                gout = torch.full((rows, d.cfg.hidden_size), float("nan"), device=cuda)
+                if which == 0:
+                    _lib.call("wc_verify_chain_greedy_fuse", ptr(logits), rows, V, LD, ptr(drafts), ptr(verdict),
+                              ptr(ws[0]), C.byref(d.dims), C.byref(d.wstruct), tp, tdt, Dt, ptr(gout),
+                              d.cfg.hidden_size, ptr(d.ws), stream_ptr())
+                else:
+                    _lib.call("wc_verify_chain_greedy", ptr(logits), rows, V, LD, ptr(drafts), ptr(verdict),
+                              ptr(ws[1]), stream_ptr())
+                    _lib.call("wc_drafter_fuse", C.byref(d.dims), C.byref(d.wstruct), tp, tdt, Dt, None, 0, rows,
+                              None, ptr(gout), d.cfg.hidden_size, ptr(d.ws), stream_ptr())
+                outs.append((verdict, gout))
+            torch.cuda.synchronize()
+            (v0, g0), (v1, g1) = outs
+            assert torch.equal(v0, v1), (rows, case)
+            assert int(v0[_lib.V_N_ACCEPTED]) == n_agree, (rows, case)
+            assert int(v0[_lib.V_TOKENS + n_agree]) == int(am[n_agree]), (rows, case)
+            assert torch.equal(g0, g1), (rows, case)
 
 
 def test_enqueue_never_synchronises(cuda):
