@@ -423,9 +423,13 @@ def bench_gpu(args):
         comps[name] = float(np.median(t)) / reps.get(name, REP)
     rewind()
     torch.cuda.synchronize()
-    cold_head = []
-    for _ in range(20):
-        evict()
+    # one head launch between two events behind the spin gate, after the 1 GiB
+    # read (cold) or straight after the previous launch (warm, the same timing
+    # method: event overhead included in both)
+    cold_head, warm_head = [], []
+    for i in range(40):
+        if i % 2 == 0:
+            evict()
         _sleep_gate()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
@@ -433,7 +437,7 @@ def bench_gpu(args):
                   None, ws, s())
         e1.record()
         torch.cuda.synchronize()
-        cold_head.append(1e3 * e0.elapsed_time(e1))
+        (cold_head if i % 2 == 0 else warm_head).append(1e3 * e0.elapsed_time(e1))
     del flush
     torch.cuda.empty_cache()
     log("components done; config-4 round loop")
@@ -467,6 +471,7 @@ def bench_gpu(args):
         "draft_step_4b_us": comps["draft_step_4b"],
         "round_gpu_us_cold": float(np.median(cold)),
         "head_us_cold": float(np.median(cold_head)),
+        "head_us_warm_single": float(np.median(warm_head)),
         "config4": c4,
         "config5": c5,
         "head_bytes": head_bytes,
@@ -1175,6 +1180,7 @@ def main():
             "head_gemv_us": round(r["head_us"], 2),
             "round_gpu_us_cold": round(r["round_gpu_us_cold"], 2),
             "head_gemv_us_cold": round(r["head_us_cold"], 2),
+            "head_gemv_us_warm_same_method": round(r["head_us_warm_single"], 2),
             "head_gemv_hbm_frac_cold": round(r["head_bytes"] / (r["head_us_cold"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
             "config4_auto_k_qwen3_4b": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r["config4"].items()},
             "config5_tree_round_qwen3_1p7b": {k: (round(v, 2) if isinstance(v, float) else v)
