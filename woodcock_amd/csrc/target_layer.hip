@@ -580,7 +580,11 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
 constexpr int kMwG = 4;  // column tiles per block
 constexpr int kMwP = 3;  // k steps in flight per wave
 
-template <int MT>
+// PE: the SiLU pair with K unsplit (ks = 1): the block owns its 32 act
+// features outright, so instead of a partial it runs the pair's epilogue
+// itself (row scale from the ss parts, SiLU(gate) * up, the next projection's
+// activations), and no fix-up launch follows.
+template <int MT, bool PE = false>
 __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
   constexpr int G = kMwG, FB = 16 * G, LDR = FB + 4;
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
@@ -643,6 +647,16 @@ __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
       }
     }
   }
+  // the pair's row-scale parts (thread t: row t / 4, parts t % 4 + 4 q), in
+  // flight during the LDS reduction
+  float ssv[PE ? kSsMax : 1];
+  if constexpr (PE) {
+#pragma unroll
+    for (int q = 0; q < kSsMax; ++q) {
+      const int pp = t % 4 + 4 * q;
+      ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + t / 4] : 0.f;
+    }
+  }
   // the wave's tile -> LDS (row 16 q + 4 (lane / 16) + e, column 16 g + lane % 16)
   mfma_settle();
 #pragma unroll
@@ -652,6 +666,48 @@ __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) s_red[wave][(q * 16 + (lane / 16) * 4 + e) * LDR + g * 16 + lane % 16] = acc[g][q][e];
   __syncthreads();
+  if constexpr (PE) {
+    // four waves summed in order into wave 0's tile, then the pair epilogue
+    // of thread (row m, 8 act features from g * 8): gate at column
+    // 32 (f / 16) + f % 16 of the tile, up 16 columns further
+    for (int e = t * 4; e < a.M * FB; e += 256 * 4) {
+      const int r = e / FB, c = e % FB;
+      float4 v = *reinterpret_cast<const float4*>(&s_red[0][r * LDR + c]);
+#pragma unroll
+      for (int w = 1; w < 4; ++w) {
+        const float4 o = *reinterpret_cast<const float4*>(&s_red[w][r * LDR + c]);
+        v.x += o.x;
+        v.y += o.y;
+        v.z += o.z;
+        v.w += o.w;
+      }
+      *reinterpret_cast<float4*>(&s_red[0][r * LDR + c]) = v;
+    }
+    __shared__ float s_inv[64];
+    const int m = t / 4, g = t % 4;
+    float tot = 0.f;
+#pragma unroll
+    for (int q = 0; q < kSsMax; ++q) tot += ssv[q];
+    tot += __shfl_xor(tot, 1);
+    tot += __shfl_xor(tot, 2);
+    if (g == 0) s_inv[m] = a.ss ? 1.f / sqrtf(tot / static_cast<float>(a.ss_k) + a.eps) : 1.f;
+    __syncthreads();
+    if (m >= a.M) return;
+    const float inv = s_inv[m];
+    float z[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int f = g * 8 + e, gc = (f / 16) * 32 + f % 16;
+      const float gv = s_red[0][m * LDR + gc] * inv, uv = s_red[0][m * LDR + gc + 16] * inv;
+      z[e] = gv / (1.f + expf(-gv)) * uv;
+    }
+    const int n0 = (cg >> 1) * 64 + (cg & 1) * 32 + g * 8;
+    uint4 hi, lo;
+    split8(z, hi, lo);
+    *reinterpret_cast<uint4*>(a.xa_next + xa_index(m, n0, 0)) = hi;
+    *reinterpret_cast<uint4*>(a.xa_next + xa_index(m, n0, 1)) = lo;
+    return;
+  }
   // four waves summed in order; rows < M as this split's partial
   const int cols = gridDim.x * FB;
   float* base = a.part + static_cast<int64_t>(cg) * FB;
@@ -775,6 +831,20 @@ static int launch_wave(SkArgs g, int fix_tw, hipStream_t s) {
   WC_REQUIRE(g.N % (64 * fix_tw) == 0, "target layer: %d weight rows must be a multiple of %d", g.N, 64 * fix_tw);
   WC_REQUIRE(g.n_ss <= 64, "target layer: at most 64 row-scale parts");
   g.ks = wave_ks(g.N, g.K);  // <= 8: k_mm_fix issues every split's loads at once
+  // the SiLU pair over >= 128 column groups: K unsplit, the epilogue in the GEMM
+  if (g.epi == kSkSiluPair && fix_tw == 2 && g.xa_next && !g.out && g.N / (16 * kMwG) >= 128 &&
+      g.n_ss <= 4 * kSsMax) {
+    g.ks = 1;
+    const dim3 grid1(g.N / (16 * kMwG), 1);
+    switch ((g.M + 15) / 16) {
+      case 1: hipLaunchKernelGGL((k_mm_wave<1, true>), grid1, dim3(256), 0, s, g); break;
+      case 2: hipLaunchKernelGGL((k_mm_wave<2, true>), grid1, dim3(256), 0, s, g); break;
+      case 3: hipLaunchKernelGGL((k_mm_wave<3, true>), grid1, dim3(256), 0, s, g); break;
+      default: hipLaunchKernelGGL((k_mm_wave<4, true>), grid1, dim3(256), 0, s, g); break;
+    }
+    WC_LAUNCHED();
+    return WC_OK;
+  }
   const dim3 grid(g.N / (16 * kMwG), g.ks);
   switch ((g.M + 15) / 16) {
     case 1: hipLaunchKernelGGL((k_mm_wave<1>), grid, dim3(256), 0, s, g); break;
