@@ -626,8 +626,9 @@ def pmc_probe(seed=0):
 
 
 # Counter probe over the round's kernels: phases separated by a one-element
-# torch.abs marker -- heads, draft-step layers (M = 1), update passes (fuse +
-# layer at 5 rows, 3 live), verify-width target layers (M = 60, tree mask) --
+# torch.abs marker -- heads, draft-step layers (M = 1), update passes (verify +
+# fuse, then the layer at 5 rows, 3 live), verify-width target layers (M = 60,
+# tree mask) --
 # then the calibration copies.  Per launch of each phase the same kernels run
 # in the same order, so dispatch j of a repeat is one kernel (the table below
 # names it and gives its algorithmic bytes).
@@ -642,7 +643,7 @@ PHASES = {
         ("gate / up + SiLU 2 x 6144 x 2048", 2 * _F * _D * 2),
         ("down + residual 2048 x 6144", _D * _F * 2)],
     "update pass (5 rows, 3 live)": [
-        ("fuse 2048 x 6144", _D * 3 * _D * 2),
+        ("greedy verify of [5, 151936] fp32 logits + fuse 2048 x 6144, one launch", 5 * 151936 * 4 + _D * 3 * _D * 2),
         ("QKV, two streams", 2 * (_HD + 2 * _HKV * 128) * _D * 2),
         ("attention, 3 rows", 2 * 515 * _HKV * 128 * 2),
         ("attention merge", 0),
@@ -657,8 +658,7 @@ PHASES = {
         ("attention merge", 0),
         ("o_proj 2048 x 2048, K split", _D * _HD * 2),
         ("o_proj fix-up (+ residual, next activations)", 0),
-        ("gate / up 2 x 6144 x 2048, K split", 2 * _F * _D * 2),
-        ("gate / up fix-up (SiLU * up, next activations)", 0),
+        ("gate / up 2 x 6144 x 2048, K unsplit, SiLU * up and next activations in the block", 2 * _F * _D * 2),
         ("down 2048 x 6144, K split", _D * _F * 2),
         ("down fix-up (+ residual)", 0)],
 }
@@ -701,7 +701,6 @@ def pmc_probe2(seed=0):
     x = torch.randn(PROBE_COPY_FLOATS, device=dev)
     y = torch.empty_like(x)
     rows = torch.tensor([3], dtype=torch.int32, device=dev)
-    keep = torch.arange(8, dtype=torch.int32, device=dev)
     tp = (C.c_void_p * 3)(*[t.data_ptr() for t in target.taps])
     g = torch.empty(5, dm, device=dev)
     hid5 = torch.empty(5, dm, device=dev)
@@ -719,8 +718,9 @@ def pmc_probe2(seed=0):
                   None, ws, s)
     torch.abs(mark, out=mark)
     for _ in range(PROBE_REPS):
-        _lib.call("wc_drafter_fuse", dims, W, tp, _lib.WC_BF16, target.taps[0].stride(0), ptr(keep), 5, 5, ptr(rows),
-                  ptr(g), dm, ws, s)
+        _lib.call("wc_verify_chain_greedy_fuse", ptr(target.logits), 5, target.logits.shape[1],
+                  target.logits.stride(0), ptr(rnd.drafts), ptr(rnd.verdict), ptr(rnd.vws), dims, W, tp, _lib.WC_BF16,
+                  target.taps[0].stride(0), ptr(g), dm, ws, s)
         _lib.call("wc_drafter_forward", dims, W, ptr(rnd.seq), ptr(g), dm, None, 0, 5, ptr(rows), rnd._kp, rnd._vp,
                   rnd._kvdt, rnd.cache[0].capacity, ptr(off), 0, None, None, 0, ptr(hid5), None, None, ws, s)
     torch.abs(mark, out=mark)
