@@ -578,9 +578,11 @@ int wc_attention(const float* q, int L, int H, int Hk, int D, const float* K, co
 int wc_softmax(float* x, int rows, int n, wc_stream_t stream);
 
 /* KV rows of L tokens, k / v [L][row] fp32 (row = kv_heads * head_dim), copied
- * to rows *offset_dev + l of k_cache / v_cache [capacity][row] (rows past the
- * capacity are dropped); then, when advance_dev is not NULL, *advance_dev =
- * *offset_dev + L (advance_dev may be offset_dev).  Replaces KVCache::append +
+ * to rows *offset_dev + l of k_cache / v_cache [capacity][row] (rows outside
+ * [0, capacity) are dropped: the caches are allocated up front and never
+ * grow); then, when advance_dev is not NULL, *advance_dev = *offset_dev + L
+ * clamped into [0, capacity] (advance_dev may be offset_dev), so an offset
+ * never counts rows the append dropped.  Replaces KVCache::append +
  * commit (include/woodcock/cache.h:17-19; src/cache/kv_cache.cpp:8-19). */
 int wc_kv_append(float* k_cache, float* v_cache, int capacity, int row, const float* k, const float* v, int L,
                  const int32_t* offset_dev, int32_t* advance_dev, wc_stream_t stream);

@@ -131,6 +131,20 @@ def test_kv_append_and_trim(cuda):
     assert torch.equal(kc[3:5], k1[:2]) and torch.equal(kc[5:7], k2) and torch.equal(kc[7:8], k1[4:5])
     with pytest.raises(ValueError):
         _lib.call("wc_kv_set_offset", ptr(off), -1, stream_ptr())
+    # overflow: rows at or past the capacity are dropped and the offset stops
+    # at the capacity, so a later read of `offset` rows stays inside the cache
+    _lib.call("wc_kv_set_offset", ptr(off), cap - 2, stream_ptr())
+    k3, v3 = torch.randn(5, row, device=cuda), torch.randn(5, row, device=cuda)
+    before = kc.clone()
+    _lib.call("wc_kv_append", ptr(kc), ptr(vc), cap, row, ptr(k3), ptr(v3), 5, ptr(off), ptr(off), stream_ptr())
+    assert int(off.item()) == cap
+    assert torch.equal(kc[cap - 2:], k3[:2]) and torch.equal(vc[cap - 2:], v3[:2])
+    assert torch.equal(kc[:cap - 2], before[:cap - 2])
+    # a negative offset writes nothing before the cache and advances from 0
+    off.fill_(-3)
+    before = kc.clone()
+    _lib.call("wc_kv_append", ptr(kc), ptr(vc), cap, row, ptr(k3), ptr(v3), 2, ptr(off), ptr(off), stream_ptr())
+    assert torch.equal(kc, before) and int(off.item()) == 0
 
 
 def test_target_forward_matches_reference_qwen3(cuda):

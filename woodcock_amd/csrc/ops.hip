@@ -217,7 +217,7 @@ __global__ __launch_bounds__(kOpThreads) void k_op_linear(const float* x, int L,
 // ------------------------------------------------------------------ KV cache rows
 
 // rows [L][row] of K and V into the caches at rows *offset_dev + l, [cap][row]
-// (rows past the capacity are dropped; the host checks what it can)
+// (rows outside [0, cap) are dropped; the host checks what it can)
 __global__ void k_op_kv_append(float* kc, float* vc, int row, int cap, const float* k, const float* v, int L,
                                const int32_t* offset_dev) {
   const int off = *offset_dev;
@@ -225,15 +225,18 @@ __global__ void k_op_kv_append(float* kc, float* vc, int row, int cap, const flo
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t l = i / row;
-    if (off + l < cap) {
+    if (off + l >= 0 && off + l < cap) {
       kc[(off + l) * row + i % row] = k[i];
       vc[(off + l) * row + i % row] = v[i];
     }
   }
 }
 
-// *dst = *src + add (one thread; src may be dst)
-__global__ void k_op_add_i32(int32_t* dst, const int32_t* src, int add) { *dst = *src + add; }
+// *dst = *src + add clamped into [0, cap] (one thread; src may be dst): an
+// offset never points past the rows an append could write
+__global__ void k_op_advance_i32(int32_t* dst, const int32_t* src, int add, int cap) {
+  *dst = min(max(*src + add, 0), cap);
+}
 
 __global__ void k_op_set_i32(int32_t* p, int v) { *p = v; }
 
@@ -329,7 +332,7 @@ int wc_kv_append(float* k_cache, float* v_cache, int capacity, int row, const fl
     WC_LAUNCHED();
   }
   if (advance_dev != nullptr) {  // after every block has read the offset (stream order): commit(L)
-    hipLaunchKernelGGL(k_op_add_i32, dim3(1), dim3(1), 0, s, advance_dev, offset_dev, L);
+    hipLaunchKernelGGL(k_op_advance_i32, dim3(1), dim3(1), 0, s, advance_dev, offset_dev, L, capacity);
     WC_LAUNCHED();
   }
   return WC_OK;

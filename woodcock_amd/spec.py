@@ -653,3 +653,70 @@ class SpeculativeDecoder:
         st.t_total = time.perf_counter() - t0
         st.new_tokens = len(out)
         return out, st
+
+
+# ---------------------------------------------------------------------- baseline
+
+def target_prefill(model, cache: list, prompt, offset_dev: torch.Tensor | None = None) -> tuple[int, torch.Tensor]:
+    """The prompt through ``model`` (a ``target.TargetModel``) into ``cache``, in
+    causal blocks of up to ``model.max_rows`` rows (Target.__call__ over the
+    prompt, python/woodcock/spec.py:386).  Returns (n, logits of the last prompt
+    row [vocab] fp32 on the device); the cache offsets (host and device) end at n."""
+    dev = model.device
+    toks = torch.as_tensor(list(prompt), dtype=torch.int32, device=dev)
+    if toks.numel() < 1:
+        raise ValueError("empty prompt")
+    if offset_dev is None:
+        offset_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+    n0 = int(cache[0].offset)
+    last = None
+    for b0 in range(0, toks.numel(), model.max_rows):
+        blk = toks[b0:b0 + model.max_rows]
+        logits, _ = model(blk, cache, offset_dev)
+        offset_dev.add_(blk.numel())
+        for c in cache:
+            c.offset += blk.numel()
+        last = logits[-1]
+    return n0 + toks.numel(), last
+
+
+def generate_autoregressive(model, cache: list, prompt, max_new_tokens: int, eos=(), on_logits=None
+                            ) -> tuple[list[int], GenStats]:
+    """Baseline A of python/woodcock/spec.py:377-397 (greedy): plain target
+    decoding through the same target forward -- the prompt, then one row per
+    token.  The argmax of each row is the library's (wc_verify_chain_greedy
+    over one row: the verdict's `next`).  ``on_logits(step, logits_row)`` sees
+    every row's logits before its argmax is read (step 0: the prompt's last)."""
+    st = GenStats(prompt_tokens=len(prompt), fused=False)
+    eos = set(eos)
+    dev = model.device
+    t0 = time.perf_counter()
+    off = torch.full((1,), int(cache[0].offset), dtype=torch.int32, device=dev)
+    _, logits = target_prefill(model, cache, prompt, off)
+    verdict = new_verdict(dev)
+    n = int(_lib.lib().wc_workspace_bytes())
+    ws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device=dev)
+    _lib.call("wc_workspace_init", ptr(ws), ws.numel(), stream_ptr())
+    tok_dev = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def argmax(row: torch.Tensor, step: int) -> int:
+        if on_logits is not None:
+            on_logits(step, row)
+        _lib.call("wc_verify_chain_greedy", ptr(row), 1, row.shape[-1], row.shape[-1], None, ptr(verdict), ptr(ws),
+                  stream_ptr())
+        return int(read_verdict(verdict, ws).next)
+
+    tok = argmax(logits, 0)
+    out = [tok]
+    while len(out) < max_new_tokens and tok not in eos:
+        tok_dev.fill_(tok)
+        logits, _ = model(tok_dev, cache, off)
+        off.add_(1)
+        for c in cache:
+            c.offset += 1
+        tok = argmax(logits[0], len(out))
+        out.append(tok)
+    st.t_total = time.perf_counter() - t0
+    st.new_tokens = len(out)
+    st.rounds = len(out) - 1
+    return out, st
