@@ -1,6 +1,7 @@
 """Build libwoodcock_hip.so for gfx950 with hipcc (in-tree, no JIT cache).
 
-    python -m woodcock_amd.build        # compiles every csrc/*.hip, links the .so
+    python -m woodcock_amd.build                 # compiles every csrc/*.hip, links the .so
+    python -m woodcock_amd.build --incremental   # only sources older than their object
 
 Objects go to woodcock_amd/_build/ (git-ignored); the shared library lands next
 to this file so it travels with the source tree.
@@ -18,6 +19,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libwoodcock_hip.so"
+ROOT_HEADER = PKG.parent / "include" / "woodcock_hip.h"
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -43,8 +45,12 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path, incremental: bool = False) -> Path:
     obj = BUILD / (src.stem + ".o")
+    if incremental and obj.exists():
+        newest = max(p.stat().st_mtime for p in [src, *CSRC.glob("*.h"), ROOT_HEADER])
+        if obj.stat().st_mtime > newest:
+            return obj
     cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -52,13 +58,14 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(jobs: int | None = None) -> Path:
-    """Compile every kernel source and link the shared library; returns its path."""
+def build(jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compile every kernel source and link the shared library; returns its path.
+    incremental: keep objects newer than their source and every header."""
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), int(os.environ.get("MAX_JOBS", "8")))
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda p: _compile(p, incremental), srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -69,5 +76,5 @@ def build(jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    path = build()
+    path = build(incremental="--incremental" in sys.argv[1:])
     print(path, file=sys.stderr)
