@@ -89,11 +89,10 @@ def capture(fn):
 def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=None):
     """The reference's draft-step unit (scripts/time_draft_step.py:51-56: the
     final norm, head + argmax, one drafter layer; KV rolled back) on drafter d
-    at cache offset ctx, as one launch (wc_draft_step) and as the per-op
-    launches (wc_set_one_launch_step(0)).  Warm: a graph of `reps` steps
-    replayed back to back (median over `samples` replays, per step).  Cold:
-    one step between two events after `evict()` streamed 1 GiB (median over
-    `cold_samples`), so the drafter's weights come from HBM."""
+    at cache offset ctx.  Warm: a graph of `reps` steps replayed back to back
+    (median over `samples` replays, per step).  Cold: one step between two
+    events after `evict()` streamed 1 GiB (median over `cold_samples`), so the
+    drafter's weights come from HBM."""
     import ctypes as C
 
     import torch
@@ -113,118 +112,41 @@ def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=N
     nxt = torch.empty_like(hid)
     tok = torch.zeros(1, dtype=torch.int32, device=dev)
     off = torch.tensor([ctx], dtype=torch.int32, device=dev)
-    fb = int(bool(d.cfg.post_norm))
+    fb = out if d.cfg.post_norm else hid
 
     def one():
-        _lib.call("wc_draft_step", dims, W, ptr(hid), dm, None, 0, ptr(out), dm, ptr(tok), None, kp, vp, kvdt,
-                  cache[0].capacity, ptr(off), 0, fb, ptr(nxt), ws, stream_ptr())
+        # the layer leaves its final norm to the next head, as in the chain
+        _lib.call("wc_draft_head_norm", dims, W, ptr(hid), dm, None, 0, ptr(out), dm, None, 0, ptr(tok), None, None,
+                  ws, stream_ptr())
+        _lib.call("wc_drafter_forward", dims, W, ptr(tok), ptr(fb), dm, None, 0, 1, None, kp, vp, kvdt,
+                  cache[0].capacity, ptr(off), 0, None, None, 0, ptr(nxt), None, None, ws, stream_ptr())
 
     def many():
         for _ in range(reps):
             one()
 
-    res = {}
-    for name, flag in (("one_launch", 1), ("per_op", 0)):
-        _lib.call("wc_set_one_launch_step", flag)
-        try:
-            many()
-            torch.cuda.synchronize()
-            gr = capture(many)
-            res[name + "_us"] = float(np.median(gpu_time_graphs([gr], samples))) / reps
-            if evict is not None:
-                t = []
-                for _ in range(cold_samples):
-                    evict()
-                    _sleep_gate()
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    one()
-                    e1.record()
-                    torch.cuda.synchronize()
-                    t.append(1e3 * e0.elapsed_time(e1))
-                res[name + "_us_cold"] = float(np.median(t))
-            del gr
-        finally:
-            _lib.call("wc_set_one_launch_step", 1)
+    many()
     torch.cuda.synchronize()
-    status = int(d.step_status().item())
-    if status:
-        raise RuntimeError("a bounded wait of the one-launch draft step gave up during timing")
+    gr = capture(many)
+    res = {"warm_us": float(np.median(gpu_time_graphs([gr], samples))) / reps}
+    if evict is not None:
+        t = []
+        for _ in range(cold_samples):
+            evict()
+            _sleep_gate()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            one()
+            e1.record()
+            torch.cuda.synchronize()
+            t.append(1e3 * e0.elapsed_time(e1))
+        res["cold_us"] = float(np.median(t))
     return res
 
 
-def step_trace(args):
-    """Per-block timestamps of one config-1 one-launch draft step (warm, then
-    cold): for each point the spread over blocks (min, median, max) in µs from
-    the first block's entry.  Diagnostics, one JSON line."""
-    import ctypes as C
-
-    import torch
-
-    from woodcock_amd import _lib
-    from woodcock_amd.runtime import ptr, stream_ptr
-
-    if args.step_tuning:
-        st, sl = (int(v) for v in args.step_tuning.split(","))
-        _lib.call("wc_set_step_tuning", st, sl)
-    cfg, d, ids, rnd, target, init_state, root = build_workload(args.seed)
-    dev = d.device
-    dm = cfg.hidden_size
-    cap = rnd.cache[0].capacity
-    nb = int(_lib.lib().wc_draft_step_grid(C.byref(d.dims), rnd._kvdt))
-    names = {0: "wait_head", 1: "got_head", 2: "wait_qkv", 3: "got_qkv", 4: "wait_attn", 5: "got_attn",
-             6: "wait_o", 7: "got_o", 8: "wait_gate_up", 9: "got_gate_up", 12: "entry", 13: "exit"}
-    buf = torch.zeros(nb * 16, dtype=torch.int64, device=dev)
-    flush = torch.zeros(1 << 28, dtype=torch.float32, device=dev)
-    hid = torch.randn(1, dm, device=dev)
-    out = torch.empty_like(hid)
-    nxt = torch.empty_like(hid)
-    tok = torch.zeros(1, dtype=torch.int32, device=dev)
-    off = torch.tensor([BASE_CTX], dtype=torch.int32, device=dev)
-
-    def one():
-        _lib.call("wc_draft_step", C.byref(d.dims), C.byref(d.wstruct), ptr(hid), dm, None, 0, ptr(out), dm,
-                  ptr(tok), None, rnd._kp, rnd._vp, rnd._kvdt, cap, ptr(off), 0, 1, ptr(nxt), ptr(d.ws), stream_ptr())
-
-    res = {"grid_blocks": nb}
-    for mode in ("warm", "cold"):
-        for _ in range(10):
-            one()
-        torch.cuda.synchronize()
-        if mode == "cold":
-            flush.sum()
-        _sleep_gate()
-        buf.zero_()
-        _lib.call("wc_set_step_trace", ptr(buf))
-        try:
-            one()
-        finally:
-            _lib.call("wc_set_step_trace", None)
-        torch.cuda.synchronize()
-        t = buf.view(-1, 16).cpu().numpy().astype(np.float64)
-        t0 = t[:, 12][t[:, 12] > 0].min()
-        st = {}
-        for k, lab in names.items():
-            v = t[:, k]
-            v = v[v > 0]
-            if v.size:
-                v = (v - t0) / 100.0  # 100 MHz ticks -> µs
-                st[lab] = [round(float(v.min()), 2), round(float(np.median(v)), 2), round(float(v.max()), 2)]
-        res[mode] = st
-    print(json.dumps(res), flush=True)
-
-
 def step_only(args):
-    """Only the draft steps of configs 1 and 4 (warm and cold, one launch and
-    per-op); one JSON line.  --step-tuning S,P sets the one-launch step's leaf
-    stride and poll pause first (wc_set_step_tuning)."""
+    """Only the draft steps of configs 1 and 4, warm and cold; one JSON line."""
     import torch
-
-    if args.step_tuning:
-        from woodcock_amd import _lib
-
-        st, sl = (int(v) for v in args.step_tuning.split(","))
-        _lib.call("wc_set_step_tuning", st, sl)
 
     from woodcock_amd.config import QWEN3_EOS, qwen3_4b_drafter
     from woodcock_amd.drafter import Drafter
@@ -1255,11 +1177,8 @@ def main():
                     help="only the 28-layer target forward over a 5-row chain block, 20 calls (for a kernel trace)")
     ap.add_argument("--target-layer-only", action="store_true",
                     help="only the M = 60 verify-width target layer, 45 calls (for a kernel trace of the layer)")
-    ap.add_argument("--step-trace", action="store_true",
-                    help="per-phase block timestamps of one config-1 one-launch draft step (diagnostics)")
-    ap.add_argument("--step-tuning", default="", help="LEAF_STRIDE,POLL_SLEEP for --step-only / --step-trace")
     ap.add_argument("--step-only", action="store_true",
-                    help="only the draft steps of configs 1 and 4, one launch and per-op, warm and cold")
+                    help="only the draft steps of configs 1 and 4, warm and cold")
     ap.add_argument("--round-only", action="store_true",
                     help="only the timed config-1 rounds (for a kernel trace of the round alone)")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
@@ -1299,9 +1218,6 @@ def main():
         return
     if args.step_only:
         step_only(args)
-        return
-    if args.step_trace:
-        step_trace(args)
         return
     r = bench_gpu(args)
     if args.round_only:

@@ -532,65 +532,6 @@ int wc_draft_head_norm(const wc_drafter_dims* dims, const wc_drafter_weights* w,
                        float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
                        const wc_gumbel* gumbel, void* workspace, wc_stream_t stream);
 
-/* One draft step in one launch: the head over RMSNorm(hidden_rows[row]) with
- * its argmax and d2t map (as wc_draft_head_norm: out_norm receives out at the
- * same row, token_out[0] / row_out[0] the drafted token and head row), then
- * the drafter layer on that token (as wc_drafter_forward with rows = 1, no
- * mask, no explicit positions, no final norm, no offset advance) with the
- * feature row `out` (feedback_out = 1, post_norm) or hidden_rows[row]
- * (feedback_out = 0); its K / V land at cache slot *offset_dev + offset_add and
- * hidden_out[0..hidden) receives the layer's pre-norm output.  Equal to those
- * two calls in sequence: the token, `out` and the QKV rows bit for bit, the
- * layer's output within fp32 rounding.  The phases (head, QKV, attention,
- * o_proj, gate / up, down) run in one grid of as many blocks as the device
- * holds at once, each wave owning a fixed share of every phase and requesting
- * its next weights before it waits; the phases hand over through monotone
- * counters in the drafter workspace.  Every wait is bounded
- * (wc_set_spin_limit) and a wait that gives up leaves a nonzero int32 at byte
- * wc_draft_step_status_offset(dims) of the workspace (sticky, the results of
- * that call invalid; clear it with a zero store).  Covered shapes: hidden and
- * q width 2048, head_dim 128, intermediate size up to 6144, GQA groups of at
- * most four heads, one decoder layer with the token stream; other drafters
- * (and devices whose resident grid cannot hold the work) run the two calls.
- * Replaces Drafter.norm + Drafter.logits +
- * mx.argmax + token_ids + Drafter.__call__ of one chain step
- * (python/woodcock/spec.py:346-350; drafter.py:164-215;
- * src/core/drafter.cpp:91-136). */
-int wc_draft_step(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* hidden_rows,
-                  int64_t hidden_ld, const int32_t* row_dev, int row_add, float* out_norm, int64_t out_ld,
-                  int32_t* token_out, int32_t* row_out, void* const* k_cache, void* const* v_cache, int kv_dtype,
-                  int capacity, const int32_t* offset_dev, int offset_add, int feedback_out, float* hidden_out,
-                  void* workspace, wc_stream_t stream);
-
-/* Byte offset of the one-launch step's status word in the drafter workspace
- * (0 = every wait of every call so far completed).  No reference counterpart. */
-size_t wc_draft_step_status_offset(const wc_drafter_dims* dims);
-
-/* Process-wide switch (default 1): 0 makes wc_draft_step run its two calls and
- * wc_drafter_forward its per-op launches for one row, for comparisons of the
- * two paths.  Returns WC_OK.  No reference counterpart. */
-int wc_set_one_launch_step(int enable);
-
-/* Diagnostics: when buffer is not NULL, every later one-launch step writes, per
- * block b, sixteen uint64 stamps of the GPU's 100 MHz real-time counter at
- * buffer[16 b .. 16 b + 15]: for the phase waited on, p = 0 (head) .. 4 (gate /
- * up), 2 p = starts waiting and 2 p + 1 = resumes; 12 = entry, 13 = exit (zero
- * where a block has no such point).  The buffer must hold 16 stamps per block
- * of the grid (wc_draft_step_grid).  NULL turns it off.  Returns WC_OK.  No
- * reference counterpart. */
-int wc_set_step_trace(void* buffer);
-
-/* Hand-over tuning of the one-launch step, process-wide, for every later
- * launch: leaf_stride (1..16) uint64s between the leaves of a phase counter,
- * poll_sleep (0, 1, 4, 16, 64) the s_sleep argument between two polls.  Every
- * launch on one workspace must use the same leaf stride: change it only with
- * a freshly zero-filled workspace.  No reference counterpart. */
-int wc_set_step_tuning(int leaf_stride, int poll_sleep);
-
-/* Blocks of the one-launch step's grid on the current device (the blocks it
- * holds at once), 0 where it does not run.  No reference counterpart. */
-int wc_draft_step_grid(const wc_drafter_dims* dims, int kv_dtype);
-
 /* ------------------------------------------------------------------ backend operations
  * The reference runtime's backend interface (include/woodcock/ops.h:9-24,
  * implemented on the CPU by src/backends/cpu_ops.cpp:45-115) on device fp32

@@ -16,10 +16,59 @@
 #include <mutex>
 #include <unordered_map>
 
-#include "drafter_ws.h"
+#include "attention.h"
+#include "gemv.h"
+#include "gemvf.h"
 #include "gemv1s.h"
 
 namespace wc {
+
+// ------------------------------------------------------------------ workspace
+
+
+struct DrafterWs {
+  unsigned int* head_ctr;  // tree counters (kTreeCounterBytes each)
+  unsigned int* fin_ctr;
+  unsigned int* attn_ctr;  // per kv head: splits done (decode attention's fused merge)
+  unsigned long long* slots;
+  float* qkv;
+  float* attn;
+  float* h1;
+  float* act;
+  float* partial;
+  float* gs_part;        // k-split few-row GEMV: partial tiles per (tile, piece)
+  unsigned int* gs_ctr;  // and one counter line per tile
+  size_t bytes;
+};
+
+static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+static DrafterWs drafter_ws(const wc_drafter_dims& d, void* base) {
+  DrafterWs w{};
+  char* p = static_cast<char*>(base);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* q = p ? p + off : nullptr;
+    off = align256(off + bytes);
+    return q;
+  };
+  const size_t R = WC_MAX_STEP_ROWS;
+  const size_t nqkv = static_cast<size_t>(d.heads + 2 * d.kv_heads) * d.head_dim;
+  w.head_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
+  w.fin_ctr = reinterpret_cast<unsigned int*>(take(kTreeCounterBytes));
+  w.attn_ctr = reinterpret_cast<unsigned int*>(take(4 * kCounterStride * static_cast<size_t>(kMaxKvHeads)));
+  w.slots = reinterpret_cast<unsigned long long*>(take(8 * R * kSlots * kSlotStride));
+  w.qkv = reinterpret_cast<float*>(take(4 * R * nqkv));
+  w.attn = reinterpret_cast<float*>(take(4 * R * d.heads * d.head_dim));
+  w.h1 = reinterpret_cast<float*>(take(4 * R * d.hidden));
+  w.act = reinterpret_cast<float*>(take(4 * R * d.inter));
+  w.partial = reinterpret_cast<float*>(take(4 * static_cast<size_t>(d.kv_heads) * kMaxSplits * kMaxQV *
+                                            (d.head_dim + 2)));
+  w.gs_part = reinterpret_cast<float*>(take(4 * static_cast<size_t>(kGsMaxPieces) * kGsPieceFloats));
+  w.gs_ctr = reinterpret_cast<unsigned int*>(take(4 * kCounterStride * static_cast<size_t>(kGsMaxPieces)));
+  w.bytes = off;
+  return w;
+}
 
 // ------------------------------------------------------------------ GEMV launch
 
@@ -722,20 +771,6 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
   }
   const DrafterWs ws = drafter_ws(d, workspace);
   auto s = reinterpret_cast<hipStream_t>(stream);
-  if (step_layer_fits(d, *w, rows, n_rows_dev, mask_dev, kv_dtype, out_out, advance_dev) &&
-      step_layer_grid_ok(d, *w, kv_dtype, capacity)) {
-    // one row: each layer is one launch (step.hip), the same values as the
-    // per-op launches below
-    for (int li = 0; li < d.num_layers; ++li) {
-      const bool first = li == 0;
-      if (int rc = step_layer_launch(d, *w, li, tokens_dev, first ? feat : hidden_out, first ? feat_ld : d.hidden,
-                                     first ? feat_row_dev : nullptr, first ? feat_row_add : 0, k_cache[li],
-                                     v_cache[li], kv_dtype, capacity, offset_dev, offset_add, positions_dev,
-                                     hidden_out, workspace, s))
-        return rc;
-    }
-    return WC_OK;
-  }
   const int nqkv = (H + 2 * Hk) * D;
   const int splits = std::max(1, std::min(kMaxSplits, (capacity + kAttnChunkMax - 1) / kAttnChunkMax));
 

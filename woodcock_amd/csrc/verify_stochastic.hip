@@ -692,7 +692,6 @@ static_assert(sizeof(MailSet) == 8 * kMailSetWords, "mailbox layout");
 static_assert(kGridBarOff % 8 == 0, "mailbox alignment");
 constexpr unsigned int kSpinLimit = 1u << 22;  // default polls before a wait gives up (WC_E_HIP in the verdict)
 static std::atomic<unsigned int> g_spin_limit{kSpinLimit};
-unsigned int current_spin_limit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 // A wait that gave up: the sticky failure flag (high half of the control word)
 // and WC_E_HIP in the verdict.  The flag is stored before the status, so a

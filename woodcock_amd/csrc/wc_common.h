@@ -19,8 +19,6 @@ int set_error(int status, const char* fmt, ...);
 const char* last_error();
 // compute units of the current device (queried once per device)
 int device_cus(int* cus);
-// polls before a bounded device-side wait gives up (wc_set_spin_limit)
-unsigned int current_spin_limit();
 
 #define WC_REQUIRE(cond, ...)                                  \
   do {                                                         \

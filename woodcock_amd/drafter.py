@@ -130,12 +130,6 @@ class Drafter:
         cfg, weights, _ = read_drafter_dir(path, verify_sha)
         return cls(cfg, weights, device, kv_dtype)
 
-    def step_status(self) -> torch.Tensor:
-        """The one-launch draft step's status word in the workspace (an int32
-        device view: nonzero once a bounded wait of wc_draft_step gave up)."""
-        off = int(_lib.lib().wc_draft_step_status_offset(C.byref(self.dims)))
-        return self.ws[off:off + 4].view(torch.int32)
-
     # ------------------------------------------------------------------ caches
 
     def make_cache(self, capacity: int = 4096, dtype=None) -> list[KVCache]:

@@ -104,10 +104,6 @@ class ChainRound:
         self.upd_out = torch.zeros_like(self.upd_hid)
         self.g = torch.zeros_like(self.upd_hid)
         self.host_verdict = torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, pin_memory=True)
-        # status words of the one-launch draft step (the drafter's, and any the
-        # target's forward adds): copied with the verdict, checked at the sync
-        self._status = [drafter.step_status()]
-        self.host_step_status = torch.zeros(1, dtype=torch.int32, pin_memory=True)
         n = int(_lib.lib().wc_workspace_bytes())
         self.vws = torch.empty((n + 255) // 256 * 256, dtype=torch.uint8, device=dev)
         _lib.call("wc_workspace_init", ptr(self.vws), self.vws.numel(), stream_ptr())
@@ -153,29 +149,30 @@ class ChainRound:
     # ------------------------------------------------------------------ chain rounds
 
     def enqueue_draft(self, k: int | None = None) -> None:
-        """k heads and k-1 drafter layers from the root; drafts -> self.drafts[:k].
-        Step i < k is one launch (wc_draft_step): the head over RMSNorm(h_{i-1})
-        -> d_i, then the layer on d_i with the feedback row -> h_i; the last
-        head runs alone."""
+        """k head launches and k-1 drafter layers from the root; drafts -> self.drafts[:k]."""
         k = self._k(k)
         d = self.d
         dims, W, ws, s = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws), stream_ptr()
         n_keep = ptr(self.verdict[_lib.V_N_KEEP:_lib.V_N_KEEP + 1])
         dm = d.cfg.hidden_size
         cap = self.cache[0].capacity
-        fb_out = int(bool(d.cfg.post_norm))
-        # h_0 is the root = update row n_keep - 1; its output (the final RMSNorm)
-        # lands in upd_out at the same row
-        hid, row, add, out = self.upd_hid, n_keep, -1, self.upd_out
+        # d_1 from the root = update row n_keep - 1; the head applies the final
+        # RMSNorm and leaves the root's output in upd_out (same row)
+        _lib.call("wc_draft_head_norm", dims, W, ptr(self.upd_hid), dm, n_keep, -1, ptr(self.upd_out), dm, None, 0,
+                  ptr(self.drafts[0:1]), None, None, ws, s)
+        root_fb = self._fb_rows(self.upd_hid, self.upd_out)
         for i in range(1, k):
+            if i == 1:
+                feat, frow, fadd = root_fb, n_keep, -1
+            else:
+                feat, frow, fadd = self._fb_rows(self.step_hid, self.step_out)[i - 2:i - 1], None, 0
             # the chain appends at n + i - 1 (contiguous positions, causal, python/woodcock/spec.py:349);
-            # the layer's final RMSNorm is left to the next head
-            _lib.call("wc_draft_step", dims, W, ptr(hid), dm, row, add, ptr(out), dm, ptr(self.drafts[i - 1:i]), None,
-                      self._kp, self._vp, self._kvdt, cap, ptr(self.n_dev()), i - 1, fb_out,
-                      ptr(self.step_hid[i - 1:i]), ws, s)
-            hid, row, add, out = self.step_hid[i - 1:i], None, 0, self.step_out[i - 1:i]
-        _lib.call("wc_draft_head_norm", dims, W, ptr(hid), dm, row, add, ptr(out), dm, None, 0,
-                  ptr(self.drafts[k - 1:k]), None, None, ws, s)
+            # the layer's final RMSNorm is left to the next head (out_out = NULL)
+            _lib.call("wc_drafter_forward", dims, W, ptr(self.drafts[i - 1:i]), ptr(feat), dm, frow, fadd, 1, None,
+                      self._kp, self._vp, self._kvdt, cap, ptr(self.n_dev()), i - 1, None, None, 0,
+                      ptr(self.step_hid[i - 1:i]), None, None, ws, s)
+            _lib.call("wc_draft_head_norm", dims, W, ptr(self.step_hid[i - 1:i]), dm, None, 0,
+                      ptr(self.step_out[i - 1:i]), dm, None, 0, ptr(self.drafts[i:i + 1]), None, None, ws, s)
         # the speculative entries n..n+k-2 are simply overwritten later: the
         # drafter's committed count n is never advanced by the chain (spec.py:351-352)
 
@@ -244,15 +241,8 @@ class ChainRound:
                   stream_ptr())
         self._enqueue_pass(rows)
 
-    def watch_status(self, words: list[torch.Tensor]) -> None:
-        """More one-launch step status words (int32 device views) to check at each sync."""
-        self._status += [w for w in words if all(w.data_ptr() != o.data_ptr() for o in self._status)]
-        self.host_step_status = torch.zeros(len(self._status), dtype=torch.int32, pin_memory=True)
-
     def enqueue_readback(self) -> None:
         self.host_verdict.copy_(self.verdict, non_blocking=True)
-        for i, w in enumerate(self._status):
-            self.host_step_status[i:i + 1].copy_(w, non_blocking=True)
 
     def enqueue_round(self, target, k: int | None = None) -> None:
         """A chain round against a target exposing device ``logits`` / ``taps``
@@ -293,14 +283,6 @@ class ChainRound:
         """The round's single host synchronisation: wait for the verdict copy."""
         torch.cuda.current_stream().synchronize()
         self.syncs += 1
-        if bool(self.host_step_status.any()):
-            # a bounded wait of a one-launch step gave up: this round's results
-            # are invalid (the counters stay consistent for the next call)
-            for w in self._status:
-                w.zero_()
-            self.host_step_status.zero_()
-            raise _lib.WoodcockHipError("a bounded device-side wait of the draft step gave up (WC_E_HIP); "
-                                        "this round has no result")
         v = check_verdict(_lib.Verdict.from_buffer_copy(self.host_verdict.numpy().tobytes()), self.vws)
         a = int(v.n_accepted)
         for c in self.cache:
@@ -348,10 +330,6 @@ class TargetRunner:
 
     def prepare(self, rows: int) -> None:
         pass
-
-    def status_words(self) -> list[torch.Tensor]:
-        """The target forward's one-launch step status word (checked at each round's sync)."""
-        return [self.model.step_status()]
 
     def verify_forward(self, tokens: torch.Tensor, rows: int, offset_dev: torch.Tensor,
                        positions: torch.Tensor | None = None, mask: torch.Tensor | None = None):
@@ -422,8 +400,6 @@ class SpeculativeDecoder:
         self._host_tree = None
         self.rnd = ChainRound(drafter, k_max, capacity, getattr(target, "cache", None),
                               max_keep=max_tree_depth + 1)
-        if hasattr(target, "status_words"):
-            self.rnd.watch_status(target.status_words())
         self.k_max = k_max
         self.use_graphs = use_graphs
         self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, ...]] = {}

@@ -242,12 +242,6 @@ class TargetModel:
         return [KVCache(self.cfg.num_kv_heads, self.cfg.head_dim, capacity, dtype, self.device)
                 for _ in range(self.cfg.num_layers)]
 
-    def step_status(self) -> torch.Tensor:
-        """Status word of the one-launch layers that one-row blocks run (an int32
-        device view in the few-row workspace: nonzero once a bounded wait gave up)."""
-        off = int(_lib.lib().wc_draft_step_status_offset(C.byref(self.fdims)))
-        return self.fws[off:off + 4].view(torch.int32)
-
     def rope(self, positions: int) -> tuple[torch.Tensor, torch.Tensor]:
         if self._rope is None or self._rope[0].shape[0] < positions:
             n = max(positions, 64)
