@@ -154,7 +154,12 @@ def step_only(args):
 
     cfg, d, ids, rnd, target, init_state, root = build_workload(args.seed)
     flush = torch.zeros(1 << 28, dtype=torch.float32, device=d.device)
-    out = {"config1": time_draft_step(d, rnd.cache, BASE_CTX, evict=flush.sum)}
+    out = {}
+    if args.step_config in ("1", "both"):
+        out["config1"] = time_draft_step(d, rnd.cache, BASE_CTX, evict=flush.sum)
+    if args.step_config == "1":
+        print(json.dumps({k: {n: round(v, 2) for n, v in t.items()} for k, t in out.items()}), flush=True)
+        return
     cfg4 = qwen3_4b_drafter()
     d4 = Drafter(cfg4, random_drafter(cfg4, seed=args.seed + 7, device=d.device), d.device, torch.bfloat16)
     d4.restrict_vocab(draft_vocab(cfg4.vocab_size, 16384, seed=args.seed + 7, always=QWEN3_EOS))
@@ -1179,6 +1184,8 @@ def main():
                     help="only the M = 60 verify-width target layer, 45 calls (for a kernel trace of the layer)")
     ap.add_argument("--step-only", action="store_true",
                     help="only the draft steps of configs 1 and 4, warm and cold")
+    ap.add_argument("--step-config", choices=("1", "4", "both"), default="both",
+                    help="with --step-only: the drafter shapes to time")
     ap.add_argument("--round-only", action="store_true",
                     help="only the timed config-1 rounds (for a kernel trace of the round alone)")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",

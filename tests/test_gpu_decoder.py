@@ -172,7 +172,12 @@ def test_generate_stops_at_eos_and_max_tokens(cuda):
     assert st2.rounds <= st.rounds
 
 
-def test_tree_rounds_qwen3_1p7b(cuda):
+@pytest.mark.parametrize("layers,ctx,rounds", [(2, 2048, 3), (28, 256, 2)], ids=["2l-ctx2048", "28l-ctx256"])
+def test_tree_rounds_qwen3_1p7b(cuda, layers, ctx, rounds):
+    """Config-5 tree rounds (depth 6, top-4, 60 nodes) against the oracle: the
+    drafted tree, the target's tree-masked logits and taps (2 layers at ctx 2048,
+    and the full 28-layer depth at ctx 256), the accepted branch, the target
+    and drafter KV compacted along it, and the update pass's last hidden row."""
     from woodcock_amd import _lib
     from woodcock_amd.config import qwen3_1p7b_drafter
     from woodcock_amd.policies import StaticPolicy
@@ -181,10 +186,10 @@ def test_tree_rounds_qwen3_1p7b(cuda):
     from woodcock_amd.target import TargetConfig, TargetModel, random_target
 
     dcfg = qwen3_1p7b_drafter()
-    tcfg = TargetConfig(num_layers=2)
-    ctx, depth, width, budget = 2048, 6, 4, 59
+    tcfg = TargetConfig(num_layers=layers)
+    depth, width, budget = 6, 4, 59
     cap = ctx + 128
-    feats = (0, 1, 1)
+    feats = (0, 1, 1) if layers == 2 else (2, 14, 25)
     d, od = _drafter(cuda, dcfg, 16384, seed=51)
     tw = random_target(tcfg, seed=52, device=cuda)
     model = TargetModel(tcfg, tw, cuda, max_rows=64, feature_layers=feats)
@@ -206,7 +211,7 @@ def test_tree_rounds_qwen3_1p7b(cuda):
     dec.start(ctx, 9000, root)
     V = _lib
     rng = np.random.default_rng(56)
-    for r in range(3):
+    for r in range(rounds):
         n = dec.n
         plan = policy.plan(context_len=n, stochastic=False)
         tree, rows = dec.enqueue_tree_draft(plan)

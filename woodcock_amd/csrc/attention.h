@@ -81,6 +81,20 @@ __device__ __forceinline__ float kv_store<uint16_t>(uint16_t* p, int64_t i, floa
   return bf16_to_float(b);
 }
 
+// The value a cache entry takes (bf16 rounding), and the store of such a value.
+template <typename KT>
+__device__ __forceinline__ float kv_round(float v) {
+  if constexpr (sizeof(KT) == 2) return bf16_to_float(float_to_bf16(v));
+  return v;
+}
+template <typename KT>
+__device__ __forceinline__ void kv_put(KT* p, int64_t i, float rounded) {
+  if constexpr (sizeof(KT) == 2)
+    p[i] = float_to_bf16(rounded);
+  else
+    p[i] = rounded;
+}
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
   __syncthreads();
@@ -797,11 +811,433 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
   }  // kFuse
 }
 
+// Decode attention over fixed key ranges, for up to 4 query vectors with the
+// merge fused: split s of kv head kh owns keys [s * per, s * per + per), per =
+// a multiple of 32 chosen from the capacity, so every block requests its first
+// CPS chunks of K and V, its raw q row and appended k / v rows at entry, before
+// the offset (and with it the live length) has been read; later chunks follow
+// in a ring of CPS register slots, each refilled as soon as its chunk is
+// consumed.  Splits whose range starts past the live length skip the work.
+// The appended rows are rounded into LDS at once and stored to the cache after
+// the chunks, so no wait in the chunk loop covers those stores.  The chunk
+// math is latency-bound (a wave or two per SIMD), so blocks of one-chunk
+// splits have 512 threads (two waves per SIMD), others 256, and the math is
+// written as independent chains: the four query vectors' dot products side by side
+// (vectors past the live count are computed and masked), and the weighted V
+// sums over all 32 keys with every LDS read issued first (rows past the chunk
+// end are zero, their probabilities too).  The last split of a kv head to
+// finish merges the live splits in one round of 16-byte coherent loads (wave v
+// takes query vector v; a lane holds 4 dims of every other split).
+constexpr int kFxMaxSplits = 64;
+constexpr int kFxThreads = 512;  // block size of the one-chunk splits
+constexpr int kFxRec = 132;  // floats per (split, vector) record: o[128], m, l, 2 pad (16-byte multiple)
+
+// 16-byte device-coherent load from a buffer resource; reads past num_records
+// return zeros without a memory access.
+__device__ __forceinline__ float4 fetch_f32x4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16 /* sc1 */));
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
+
+typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
+typedef float af32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+}
+
+// 8 fp32 -> bf16 hi (round to nearest) and lo (the rounding remainder, rounded):
+// hi + lo equals x to ~2^-17 relative, so bf16 MFMA products keep fp32 accuracy.
+__device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& lo) {
+  float r[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = x[e] - static_cast<float>(static_cast<__bf16>(x[e]));
+  hi = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
+  lo = make_uint4(pack2_bf16(r[0], r[1]), pack2_bf16(r[2], r[3]), pack2_bf16(r[4], r[5]), pack2_bf16(r[6], r[7]));
+}
+__device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo) {
+  uint4 h, l;
+  split8(x, h, l);
+  hi = __builtin_bit_cast(abf16x8, h);
+  lo = __builtin_bit_cast(abf16x8, l);
+}
+
+// This split's (m, l, o) records of the fixed-range decode kernels, handed
+// over coherently (outputs (ov0 + VSTEP k, od) of thread t, ov0 = t / 128).
+template <int OPT, int VSTEP>
+__device__ __forceinline__ void fx_publish(const AttnArgs& a, const float* o, const float* s_m, const float* s_l,
+                                           int QV) {
+  constexpr int D = 128, QVM = 4;
+  const int t = threadIdx.x, od = t % D, ov0 = t / D;
+  float* part = a.partial + (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * QVM * kFxRec;
+#pragma unroll
+  for (int k = 0; k < OPT; ++k) {
+    const int v = ov0 + VSTEP * k;
+    if (v >= QV) break;
+    float* pv = part + v * kFxRec;
+    publish_f32(pv + od, o[k]);
+    if (od == 0) {
+      publish_f32(pv + D, s_m[v]);
+      publish_f32(pv + D + 1, s_l[v]);
+    }
+  }
+}
+
+// Split counter of this kv head; the last split to arrive merges the SL live
+// splits in one round of coherent 16-byte loads (records of splits >= SL lie
+// past the resource's range and read as zeros): wave v takes query vector v,
+// lane j split j's (m, l), and each lane 4 dims of every other split.
+__device__ __forceinline__ void fx_merge(const AttnArgs& a, float (*s_w)[kFxMaxSplits], bool& s_last, int T, int per,
+                                         int QV, int rep) {
+  constexpr int D = 128, QVM = 4;
+  const int kh = blockIdx.y, S = gridDim.x;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (t == 0) {
+    unsigned int* ctr = a.ctr + kh * kCounterStride;
+    const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      static_cast<unsigned int>(S - 1);
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  const int SL = min(S, (T + per - 1) / per);
+  if (wave >= QV || SL <= 0) return;  // wave-uniform
+  const int rec_bytes = QVM * kFxRec * 4;  // one split's records
+  const __amdgpu_buffer_rsrc_t rs =
+      buffer_rsrc(a.partial + static_cast<int64_t>(kh) * S * QVM * kFxRec, SL * rec_bytes);
+  const int half = lane / 32, d4 = lane % 32;
+  float4 ov[kFxMaxSplits / 2];
+#pragma unroll
+  for (int jj = 0; jj < kFxMaxSplits / 2; ++jj)
+    ov[jj] = fetch_f32x4(rs, (2 * jj + half) * rec_bytes + wave * kFxRec * 4 + 16 * d4);
+  const float4 ml = fetch_f32x4(rs, lane * rec_bytes + wave * kFxRec * 4 + 4 * D);  // (m, l, pad, pad)
+  const float m_s = lane < SL ? ml.x : -INFINITY;
+  const float M = wave_max_dpp(m_s);
+  const float wgt = m_s == -INFINITY ? 0.f : expf(m_s - M);
+  const float den = wave_sum_dpp(lane < SL ? ml.y * wgt : 0.f);
+  s_w[wave][lane] = wgt;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int jj = 0; jj < kFxMaxSplits / 2; ++jj) {
+    const float w = s_w[wave][2 * jj + half];
+    num.x = fmaf(w, ov[jj].x, num.x);
+    num.y = fmaf(w, ov[jj].y, num.y);
+    num.z = fmaf(w, ov[jj].z, num.z);
+    num.w = fmaf(w, ov[jj].w, num.w);
+  }
+  num.x += __shfl_xor(num.x, 32);
+  num.y += __shfl_xor(num.y, 32);
+  num.z += __shfl_xor(num.z, 32);
+  num.w += __shfl_xor(num.w, 32);
+  if (half) return;
+  const int l = wave / rep, h = kh * rep + wave % rep;
+  const float y[4] = {num.x / den, num.y / den, num.z / den, num.w / den};
+  *reinterpret_cast<float4*>(a.out + l * a.ld_out + h * D + 4 * d4) = make_float4(y[0], y[1], y[2], y[3]);
+  if (a.xa_out) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int col = h * D + 4 * d4 + q;
+      const __bf16 hi = static_cast<__bf16>(y[q]);
+      a.xa_out[xa_index(l, col, 0)] = __builtin_bit_cast(uint16_t, hi);
+      a.xa_out[xa_index(l, col, 1)] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y[q] - static_cast<float>(hi)));
+    }
+  }
+}
+
+template <int D, typename KT, int CPS, int NT>
+__global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
+  constexpr int QVM = 4;
+  constexpr int VE = 16 / static_cast<int>(sizeof(KT));
+  constexpr int LK = D / VE;
+  constexpr int KPB = NT / LK;
+  constexpr int CHK = 32;
+  constexpr int NL = CHK / KPB;
+  constexpr int OPT = QVM * D / NT;
+  constexpr int VSTEP = NT / D;
+  static_assert(D == 128 && kFxRec >= D + 2 && kFxRec % 4 == 0, "record layout");
+  static_assert(LK == 16 || LK == 32, "16 or 32 lanes per key row");
+  static_assert(NL >= 1 && NL * KPB == CHK, "whole key rows per chunk");
+  static_assert(NT / kWave >= QVM && OPT >= 1, "a wave per query vector, an output per thread");
+  __shared__ __attribute__((aligned(16))) float qs[QVM][D];
+  __shared__ __attribute__((aligned(16))) float nks[QVM][D];
+  __shared__ __attribute__((aligned(16))) float nvs[QVM][D];
+  __shared__ __attribute__((aligned(16))) float vls[CHK][D];
+  __shared__ __attribute__((aligned(16))) float s_p[QVM][CHK];
+  __shared__ float s_m[QVM], s_l[QVM], s_alpha[QVM];
+  __shared__ float s_w[QVM][kFxMaxSplits];
+  __shared__ bool s_last;
+
+  const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
+  KT* vc = static_cast<KT*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
+  const int kb = split * per;
+  const int kr = t / LK, e0 = (t % LK) * VE;
+  const int64_t last_row = static_cast<int64_t>(a.cap) - 1;
+  const int rep = a.H / a.Hk;
+
+  // 0. the offset and the live row count, requested before anything else
+  const int off_raw = *a.offset_dev;
+  const int nr_raw = *(a.n_rows_dev ? a.n_rows_dev : a.offset_dev);
+
+  // 1. in flight at entry: the split's first CPS chunks, the raw q vector of
+  // this wave (v = wave) and, on wave QVM-1-l, the raw k / v rows of row l
+  uint4 kreg[CPS][NL], vreg[CPS][NL];
+#pragma unroll
+  for (int c = 0; c < CPS; ++c)
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int64_t r = min(static_cast<int64_t>(kb + c * CHK + i * KPB + kr), last_row);
+      kreg[c][i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
+      vreg[c][i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
+    }
+  const int vq = wave, lq = min(vq / rep, a.rows - 1), hq = kh * rep + vq % rep;
+  HeadVec<D> rq;
+  head_vec_load<D>(a.qkv + lq * a.ld_qkv + hq * D, a.q_gain, rq);
+  const int lk = max(0, min(QVM - 1 - wave, a.rows - 1));
+  HeadVec<D> rk;
+  head_vec_load<D>(a.qkv + lk * a.ld_qkv + (a.H + kh) * D, a.k_gain, rk);
+  const float* vsrc = a.qkv + lk * a.ld_qkv + (a.H + a.Hk + kh) * D;
+  float vraw[D / kWave];
+#pragma unroll
+  for (int i = 0; i < D / kWave; ++i) vraw[i] = vsrc[lane + i * kWave];
+
+  const int nr = a.n_rows_dev ? min(max(nr_raw, 0), a.rows) : a.rows;
+  const int offset = off_raw + a.offset_add;
+  const int T = min(offset + nr, a.cap);
+  const int QV = nr * rep;
+  const int ke = min(T, kb + per);
+  const bool live = kb < ke;
+
+  if (live) {
+    auto row_pos = [&](int l) {
+      const int pos = a.positions ? a.positions[l] : offset + l;
+      return min(max(pos, 0), a.rope_max - 1);
+    };
+    if (vq < QV) {
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(lq), rq);
+      head_vec_norm_rope<D>(rq, a.eps);
+#pragma unroll
+      for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+        const int p = lane + e * kWave;
+        if (p < D / 2) {
+          qs[vq][p] = rq.lo[e];
+          qs[vq][p + D / 2] = rq.hi[e];
+        }
+      }
+    }
+    const int tk = offset + (QVM - 1 - wave);
+    const bool owner = wave < QVM && QVM - 1 - wave < nr && tk >= kb && tk < ke;  // wave-uniform: this split holds row l
+    if (owner) {
+      const int l = QVM - 1 - wave;
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), rk);
+      head_vec_norm_rope<D>(rk, a.eps);
+#pragma unroll
+      for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+        const int p = lane + e * kWave;
+        if (p < D / 2) {
+          nks[l][p] = kv_round<KT>(rk.lo[e]);
+          nks[l][p + D / 2] = kv_round<KT>(rk.hi[e]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < D / kWave; ++i)
+        nvs[l][lane + i * kWave] = kv_round<KT>(vraw[i]);
+    }
+    if (t < QVM) {
+      s_m[t] = -INFINITY;
+      s_l[t] = 0.f;
+    }
+    __syncthreads();
+
+    float o[OPT];
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) o[k] = 0.f;
+    const int od = t % D, ov0 = t / D;
+
+    for (int g0 = kb; g0 < ke; g0 += CPS * CHK) {
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) {
+        const int c0 = g0 + c * CHK;
+        if (c0 >= ke) break;  // block-uniform
+        const int n = min(CHK, ke - c0);
+        // 2. scores of the chunk (group sums of the four vectors side by side), V rows -> LDS
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+          const int j = i * KPB + kr, tt = c0 + j;
+          float kf[VE], vf[VE];
+          unpack16<KT>(kreg[c][i], kf);
+          unpack16<KT>(vreg[c][i], vf);
+          if (tt >= offset) {  // appended rows: the values this launch stored
+            const int l = min(tt - offset, QVM - 1);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) {
+              kf[e] = nks[l][e0 + e];
+              vf[e] = nvs[l][e0 + e];
+            }
+          }
+          if (j >= n) {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) vf[e] = 0.f;
+          }
+#pragma unroll
+          for (int e = 0; e < VE; e += 4)
+            *reinterpret_cast<float4*>(&vls[j][e0 + e]) = make_float4(vf[e], vf[e + 1], vf[e + 2], vf[e + 3]);
+          float d0[QVM], d1[QVM];
+#pragma unroll
+          for (int v = 0; v < QVM; ++v) {
+            d0[v] = 0.f;
+            d1[v] = 0.f;
+          }
+#pragma unroll
+          for (int e = 0; e < VE; e += 4) {
+#pragma unroll
+            for (int v = 0; v < QVM; ++v) {
+              const float4 q = *reinterpret_cast<const float4*>(&qs[v][e0 + e]);
+              d0[v] = fmaf(kf[e], q.x, d0[v]);
+              d1[v] = fmaf(kf[e + 1], q.y, d1[v]);
+              d0[v] = fmaf(kf[e + 2], q.z, d0[v]);
+              d1[v] = fmaf(kf[e + 3], q.w, d1[v]);
+            }
+          }
+          float dv[QVM];
+#pragma unroll
+          for (int v = 0; v < QVM; ++v) dv[v] = group_sum<LK>(d0[v] + d1[v]);
+          if (t % LK == 0) {
+#pragma unroll
+            for (int v = 0; v < QVM; ++v) {
+              const int l = v / rep;
+              const bool vis = v < QV && j < n && tt <= offset + l && (a.window <= 0 || tt > offset + l - a.window);
+              s_p[v][j] = vis ? a.scale * dv[v] : -INFINITY;
+            }
+          }
+        }
+        // the slot's next chunk in flight during the softmax and the weighted sums
+        if (c0 + CPS * CHK < ke) {
+#pragma unroll
+          for (int i = 0; i < NL; ++i) {
+            const int64_t r = min(static_cast<int64_t>(c0 + CPS * CHK + i * KPB + kr), last_row);
+            kreg[c][i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
+            vreg[c][i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
+          }
+        }
+        lds_barrier();
+        // 3. online softmax: 16 lanes per query vector, keys g and g + 16
+        if (t < QVM * 16) {
+          const int v = t / 16, g = t % 16;
+          const float s0 = s_p[v][g];
+          const float s1 = s_p[v][g + 16];
+          const float mx = row16_max(fmaxf(s0, s1));
+          const float m_old = s_m[v];
+          const float m_new = fmaxf(m_old, mx);
+          const float alpha = m_new == -INFINITY ? 1.f : (m_old == -INFINITY ? 0.f : expf(m_old - m_new));
+          const float p0 = s0 == -INFINITY ? 0.f : expf(s0 - m_new);
+          const float p1 = s1 == -INFINITY ? 0.f : expf(s1 - m_new);
+          const float ls = row16_sum(p0 + p1);
+          s_p[v][g] = p0;
+          s_p[v][g + 16] = p1;
+          if (g == 0) {
+            s_m[v] = m_new;
+            s_l[v] = s_l[v] * alpha + ls;
+            s_alpha[v] = alpha;
+          }
+        }
+        lds_barrier();
+        // 4. probability-weighted V rows: every read first, four accumulators
+#pragma unroll
+        for (int k = 0; k < OPT; ++k) {
+          const int v = ov0 + VSTEP * k;
+          float vv[CHK];
+#pragma unroll
+          for (int j = 0; j < CHK; ++j) vv[j] = vls[j][od];
+          float4 pp[CHK / 4];
+#pragma unroll
+          for (int j = 0; j < CHK / 4; ++j) pp[j] = *reinterpret_cast<const float4*>(&s_p[v][4 * j]);
+          float acc[4] = {o[k] * s_alpha[v], 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int j = 0; j < CHK / 4; ++j) {
+            acc[0] = fmaf(pp[j].x, vv[4 * j], acc[0]);
+            acc[1] = fmaf(pp[j].y, vv[4 * j + 1], acc[1]);
+            acc[2] = fmaf(pp[j].z, vv[4 * j + 2], acc[2]);
+            acc[3] = fmaf(pp[j].w, vv[4 * j + 3], acc[3]);
+          }
+          o[k] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        }
+        lds_barrier();  // vls / s_p are rewritten by the next chunk
+      }
+    }
+
+    // the appended rows into the cache (after the chunks, so no wait in the
+    // chunk loop covers these stores); the lanes that wrote nks / nvs read them
+    if (owner) {
+      const int l = QVM - 1 - wave;
+#pragma unroll
+      for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+        const int p = lane + e * kWave;
+        if (p < D / 2) {
+          kv_put<KT>(kc, static_cast<int64_t>(tk) * D + p, nks[l][p]);
+          kv_put<KT>(kc, static_cast<int64_t>(tk) * D + p + D / 2, nks[l][p + D / 2]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < D / kWave; ++i)
+        kv_put<KT>(vc, static_cast<int64_t>(tk) * D + lane + i * kWave, nvs[l][lane + i * kWave]);
+    }
+    fx_publish<OPT, VSTEP>(a, o, s_m, s_l, QV);
+  }
+  fx_merge(a, s_w, s_last, T, per, QV, rep);
+}
+
+// Fixed-range decode split plan for a capacity: chunks of 32 keys, at most
+// kFxMaxSplits splits, per = keys per split (whole chunks), cps = chunks per split.
+struct FxPlan {
+  int splits, per, cps;
+};
+inline FxPlan fx_plan(int cap, int chunk) {
+  const int chunks = (cap + chunk - 1) / chunk;
+  const int cps = std::max(1, (chunks + kFxMaxSplits - 1) / kFxMaxSplits);
+  const int splits = std::max(1, (chunks + cps - 1) / cps);
+  return FxPlan{splits, cps * chunk, cps};
+}
+
 template <int D, typename KT>
 static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream) {
   constexpr int CH = attn_chunk<D>();
   const size_t qvb = static_cast<size_t>(a.rows) * (a.H / a.Hk);
   if constexpr (D == 64 || D == 128) {
+    if constexpr (D == 128) {
+    if (!a.mask && qvb <= 4 && a.ctr && a.ld_out % 4 == 0 && aligned(a.out, 16) &&
+        static_cast<size_t>(a.qv_ld) * kMaxSplits * (D + 2) >= static_cast<size_t>(kFxMaxSplits) * 4 * kFxRec) {
+      // fixed key ranges from the capacity, merge fused; the partials as
+      // (split, vector) records of kFxRec floats, 4 vectors per split, in the
+      // same workspace
+      constexpr int NT = kAttnThreads;
+      const FxPlan pl = fx_plan(a.cap, 32);
+      if (pl.cps == 1)  // one chunk per split: two waves per SIMD share its latency-bound math
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 1, kFxThreads>), dim3(pl.splits, a.Hk), dim3(kFxThreads), 0,
+                           stream, a, pl.per);
+      else if (pl.cps == 2)
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 2, NT>), dim3(pl.splits, a.Hk), dim3(NT), 0, stream, a, pl.per);
+      else if (pl.cps == 3)
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 3, NT>), dim3(pl.splits, a.Hk), dim3(NT), 0, stream, a, pl.per);
+      else  // four chunks in flight, the rest through the ring
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 4, NT>), dim3(pl.splits, a.Hk), dim3(NT), 0, stream, a, pl.per);
+      WC_LAUNCHED();
+      return WC_OK;
+    }
+    }
     if (!a.mask && qvb <= 16) {  // decode width: chunked registers, merge fused for <= 4 query vectors
       if (qvb <= 4) {
         hipLaunchKernelGGL((k_attn_decode<D, KT, 4>), dim3(splits, a.Hk), dim3(kAttnThreads), 0, stream, a);

@@ -29,30 +29,6 @@
 
 namespace wc {
 
-typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
-typedef float af32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
-}
-
-// 8 fp32 -> bf16 hi (round to nearest) and lo (the rounding remainder, rounded):
-// hi + lo equals x to ~2^-17 relative, so bf16 MFMA products keep fp32 accuracy.
-__device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& lo) {
-  float r[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = x[e] - static_cast<float>(static_cast<__bf16>(x[e]));
-  hi = make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
-  lo = make_uint4(pack2_bf16(r[0], r[1]), pack2_bf16(r[2], r[3]), pack2_bf16(r[4], r[5]), pack2_bf16(r[6], r[7]));
-}
-__device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo) {
-  uint4 h, l;
-  split8(x, h, l);
-  hi = __builtin_bit_cast(abf16x8, h);
-  lo = __builtin_bit_cast(abf16x8, l);
-}
-
 // ------------------------------------------------------------------ activation prep
 // x [M][ldx] fp32 (times gain when given) -> fragment-major hi / lo, plus the
 // rows' sums of squares of x per 256-wide k block: ss [K / 256][64].  Block
