@@ -86,13 +86,15 @@ def capture(fn):
     return g
 
 
-def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=None):
+def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=None, pending=None):
     """The reference's draft-step unit (scripts/time_draft_step.py:51-56: the
     final norm, head + argmax, one drafter layer; KV rolled back) on drafter d
     at cache offset ctx.  Warm: a graph of `reps` steps replayed back to back
     (median over `samples` replays, per step).  Cold: one step between two
     events after `evict()` streamed 1 GiB (median over `cold_samples`), so the
-    drafter's weights come from HBM."""
+    drafter's weights come from HBM.  pending (default: what the chain uses):
+    the head's argmax is handed to the forward (wc_draft_head_norm_pending /
+    wc_drafter_forward_pending)."""
     import ctypes as C
 
     import torch
@@ -102,6 +104,8 @@ def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=N
 
     dev = d.device
     dm = d.cfg.hidden_size
+    if pending is None:
+        pending = d.pending_ok
     dims, W, ws = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws)
     kp = (C.c_void_p * len(cache))(*[c.keys.data_ptr() for c in cache])
     vp = (C.c_void_p * len(cache))(*[c.values.data_ptr() for c in cache])
@@ -115,7 +119,14 @@ def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=N
     fb = out if d.cfg.post_norm else hid
 
     def one():
-        # the layer leaves its final norm to the next head, as in the chain
+        # the layer leaves its final norm to the next head, as in the chain; with
+        # pending, the head's argmax is resolved by the forward (the chain's path)
+        if pending:
+            _lib.call("wc_draft_head_norm_pending", dims, W, ptr(hid), dm, None, 0, ptr(out), dm, None, 0, None, ws,
+                      stream_ptr())
+            _lib.call("wc_drafter_forward_pending", dims, W, ptr(tok), None, ptr(fb), dm, None, 0, kp, vp, kvdt,
+                      cache[0].capacity, ptr(off), 0, None, ptr(nxt), None, None, ws, stream_ptr())
+            return
         _lib.call("wc_draft_head_norm", dims, W, ptr(hid), dm, None, 0, ptr(out), dm, None, 0, ptr(tok), None, None,
                   ws, stream_ptr())
         _lib.call("wc_drafter_forward", dims, W, ptr(tok), ptr(fb), dm, None, 0, 1, None, kp, vp, kvdt,
@@ -157,6 +168,7 @@ def step_only(args):
     out = {}
     if args.step_config in ("1", "both"):
         out["config1"] = time_draft_step(d, rnd.cache, BASE_CTX, evict=flush.sum)
+        out["config1_plain_head"] = time_draft_step(d, rnd.cache, BASE_CTX, evict=flush.sum, pending=False)
     if args.step_config == "1":
         print(json.dumps({k: {n: round(v, 2) for n, v in t.items()} for k, t in out.items()}), flush=True)
         return
@@ -168,6 +180,7 @@ def step_only(args):
         c.keys.normal_()
         c.values.normal_()
     out["config4"] = time_draft_step(d4, cache4, CTX4, evict=flush.sum)
+    out["config4_plain_head"] = time_draft_step(d4, cache4, CTX4, evict=flush.sum, pending=False)
     print(json.dumps({k: {n: round(v, 2) for n, v in t.items()} for k, t in out.items()}), flush=True)
 
 

@@ -532,6 +532,31 @@ int wc_draft_head_norm(const wc_drafter_dims* dims, const wc_drafter_weights* w,
                        float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
                        const wc_gumbel* gumbel, void* workspace, wc_stream_t stream);
 
+/* The chain step with the head's argmax hand-over moved out of the head launch.
+ * wc_draft_head_norm_pending: wc_draft_head_norm for one row whose argmax is
+ * left pending in the workspace (every block's maximum key, no token written),
+ * so the head launch ends without a last-block reduction.
+ * wc_drafter_forward_pending: wc_drafter_forward for one row whose token is that
+ * pending argmax: its first QKV launch resolves it (the d2t-mapped token of the
+ * largest key) as the token-embedding row, writes the token to token_out[0] and
+ * the head row to row_out[0] (row_out may be NULL), and the attention launch after
+ * it clears the keys for the next head.  The pair must run in this order on one
+ * workspace and stream with nothing else on that workspace between them;
+ * the result equals wc_draft_head_norm followed by wc_drafter_forward on its
+ * token.  Needs hidden_size a multiple of 512 (at most 10240) and a first layer
+ * with the token stream (EAGLE-3).  Same reference interfaces as the two calls
+ * it replaces (drafter.py:190,204-215; spec.py:346-352). */
+int wc_draft_head_norm_pending(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* hidden_rows,
+                               int64_t hidden_ld, const int32_t* row_dev, int row_add, float* out_norm, int64_t out_ld,
+                               float* logits_out, int64_t logits_ld, const wc_gumbel* gumbel, void* workspace,
+                               wc_stream_t stream);
+int wc_drafter_forward_pending(const wc_drafter_dims* dims, const wc_drafter_weights* w, int32_t* token_out,
+                               int32_t* row_out, const float* feat, int64_t feat_ld, const int32_t* feat_row_dev,
+                               int feat_row_add, void* const* k_cache, void* const* v_cache, int kv_dtype,
+                               int capacity, const int32_t* offset_dev, int offset_add, const int32_t* positions_dev,
+                               float* hidden_out, float* out_out, int32_t* advance_dev, void* workspace,
+                               wc_stream_t stream);
+
 /* ------------------------------------------------------------------ backend operations
  * The reference runtime's backend interface (include/woodcock/ops.h:9-24,
  * implemented on the CPU by src/backends/cpu_ops.cpp:45-115) on device fp32

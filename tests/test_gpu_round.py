@@ -307,3 +307,40 @@ def test_graph_replay_equals_eager_rounds(cuda):
         assert (a.n_accepted, a.tokens) == (b.n_accepted, b.tokens), f"replay {r}"
     assert torch.equal(rnd.cache[0].keys, eager_k)
     del n_agree
+
+
+@pytest.mark.parametrize("kv_dtype", [torch.bfloat16, torch.float32])
+def test_pending_chain_equals_plain_chain(cuda, kv_dtype):
+    """The chain with each head's argmax left pending for the next forward
+    (wc_draft_head_norm_pending / wc_drafter_forward_pending) drafts the same
+    tokens, hidden rows and drafter KV entries, bit for bit, as the chain of
+    standalone heads and forwards; the workspace keys are clear afterwards, so a
+    plain head can follow."""
+    from woodcock_amd.config import qwen3_1p7b_drafter
+
+    cfg = qwen3_1p7b_drafter()
+    cfg, d, rnd, od, oc, target, root = setup(cuda, 11, ctx=300, kv_dtype=kv_dtype, cap=512, cfg=cfg,
+                                              head_rows=4096, k=5)
+    assert d.pending_ok
+    c = rnd.cache[0]
+    k0, v0 = c.keys.clone(), c.values.clone()
+
+    def run(pending):
+        c.keys.copy_(k0)
+        c.values.copy_(v0)
+        rnd.drafts.zero_()
+        rnd.step_hid.zero_()
+        rnd.pending = pending
+        rnd.enqueue_draft()
+        torch.cuda.synchronize()
+        return rnd.drafts.clone(), rnd.step_hid.clone(), rnd.step_out.clone(), c.keys.clone(), c.values.clone()
+
+    plain = run(False)
+    pend = run(True)
+    again = run(False)  # a plain chain right after the pending one: no stale keys in the workspace
+    for a, b, name in zip(plain, pend, ("drafts", "step_hid", "step_out", "keys", "values")):
+        assert torch.equal(a, b), name
+    for a, b, name in zip(plain, again, ("drafts", "step_hid", "step_out", "keys", "values")):
+        assert torch.equal(a, b), name
+    assert len(set(plain[0].tolist())) > 1
+    rnd.pending = True

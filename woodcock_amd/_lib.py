@@ -115,6 +115,9 @@ _SIGS = {
     "wc_tree_mask": ([P, C.c_int, C.c_int, P, I64, P], C.c_int),
     "wc_sample_without_replacement": ([P, C.c_int, C.c_int, I64, P, P, C.c_int, P, I64, P, P, P], C.c_int),
     "wc_draft_head_norm": ([P, P, P, I64, P, C.c_int, P, I64, P, I64, P, P, P, P, P], C.c_int),
+    "wc_draft_head_norm_pending": ([P, P, P, I64, P, C.c_int, P, I64, P, I64, P, P, P], C.c_int),
+    "wc_drafter_forward_pending": ([P, P, P, P, P, I64, P, C.c_int, P, P, C.c_int, C.c_int, P, C.c_int, P, P, P, P,
+                                    P, P], C.c_int),
     "wc_target_workspace_bytes": ([P, C.c_int], C.c_size_t),
     "wc_tree_draft_state_bytes": ([], C.c_size_t),
     "wc_tree_draft_begin": ([P, P, P], C.c_int),

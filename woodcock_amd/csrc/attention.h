@@ -54,6 +54,9 @@ struct AttnArgs {
   uint16_t* xa_out;  // optional: the output also as fragment-major bf16 hi / lo (see xa_index), or NULL
   int64_t ld_out;
   unsigned int* ctr;  // [Hk][kCounterStride] zeroed split counters, or NULL (decode kernel: merge launch)
+  // optional: the kSlots keys of a pending draft-head argmax (stride kSlotStride)
+  // that the launch before this one consumed; the first block clears them
+  unsigned long long* clear_slots;
 };
 
 template <typename KT>
@@ -246,6 +249,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];  // 16-byte aligned for b128 accesses
   constexpr int CH = attn_chunk<D>();
   constexpr int ACC = (kMaxQV * D + kAttnThreads - 1) / kAttnThreads;
+  if (a.clear_slots && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < kSlots)
+    a.clear_slots[threadIdx.x * kSlotStride] = 0ull;
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
   const int rep = a.H / a.Hk;
   const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
@@ -567,6 +572,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
   __shared__ float s_den[QVM];
   __shared__ bool s_last;
 
+  if (a.clear_slots && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < kSlots)
+    a.clear_slots[threadIdx.x * kSlotStride] = 0ull;
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
@@ -991,6 +998,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   // 0. the offset and the live row count, requested before anything else
   const int off_raw = *a.offset_dev;
   const int nr_raw = *(a.n_rows_dev ? a.n_rows_dev : a.offset_dev);
+  if (a.clear_slots && blockIdx.x == 0 && blockIdx.y == 0 && t < kSlots) a.clear_slots[t * kSlotStride] = 0ull;
 
   // 1. in flight at entry: the split's first CPS chunks, the raw q vector of
   // this wave (v = wave) and, on wave QVM-1-l, the raw k / v rows of row l

@@ -546,9 +546,11 @@ __global__ __launch_bounds__(256) void k_row_rmsnorm(const float* __restrict__ x
 static int draft_head_impl(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* out_rows,
                            int64_t out_ld, const int32_t* out_row_dev, int out_row_add, int rows, float* xn_out,
                            int64_t ld_xn, float* logits_out, int64_t logits_ld, int32_t* token_out, int32_t* row_out,
-                           const wc_gumbel* gumbel, void* workspace, wc_stream_t stream, bool norm) {
+                           const wc_gumbel* gumbel, void* workspace, wc_stream_t stream, bool norm,
+                           bool pending = false) {
   if (int rc = check_dims(dims)) return rc;
-  WC_REQUIRE(w && w->head && out_rows && token_out && workspace, "wc_draft_head: NULL argument");
+  WC_REQUIRE(w && w->head && out_rows && (token_out || pending) && workspace, "wc_draft_head: NULL argument");
+  WC_REQUIRE(!pending || rows == 1, "wc_draft_head_norm_pending: one row");
   WC_REQUIRE(xn_out == nullptr || (rows == 1 && ld_xn >= dims->hidden && ld_xn % 4 == 0 && al16(xn_out)),
              "wc_draft_head_norm: the normalised row needs rows == 1 and a 16-byte aligned output, stride >= hidden");
   WC_REQUIRE(al16(w->head) && al16(workspace), "wc_draft_head: head weight / workspace must be 16-byte aligned");
@@ -569,7 +571,7 @@ static int draft_head_impl(const wc_drafter_dims* dims, const wc_drafter_weights
                                     dims->eps, xn_out, ld_xn);
     WC_LAUNCHED();
     return draft_head_impl(dims, w, xn_out, ld_xn, out_row_dev, out_row_add, 1, nullptr, 0, logits_out, logits_ld,
-                           token_out, row_out, gumbel, workspace, stream, false);
+                           token_out, row_out, gumbel, workspace, stream, false, pending);
   }
   for (int t0 = 0; t0 < rows; t0 += WC_MAX_STEP_ROWS) {
     const int tr = std::min(WC_MAX_STEP_ROWS, rows - t0);
@@ -594,10 +596,10 @@ static int draft_head_impl(const wc_drafter_dims* dims, const wc_drafter_weights
     h.y = logits_out ? logits_out + t0 * logits_ld : nullptr;
     h.ldy = logits_ld;
     h.slots = ws.slots;
-    h.counter = ws.head_ctr;
+    h.counter = pending ? nullptr : ws.head_ctr;  // pending: only the block maxima, resolved by the next forward
     h.d2t = w->d2t;
-    h.tok_out = token_out + t0;
-    h.row_out = row_out ? row_out + t0 : nullptr;
+    h.tok_out = pending ? nullptr : token_out + t0;
+    h.row_out = row_out && !pending ? row_out + t0 : nullptr;
     if (gumbel) {
       h.use_gumbel = 1;
       h.gumbel.seed = gumbel->seed;
@@ -727,16 +729,33 @@ int wc_drafter_fuse(const wc_drafter_dims* dims, const wc_drafter_weights* w, co
   return WC_OK;
 }
 
-int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w, const int32_t* tokens_dev,
-                       const float* feat, int64_t feat_ld, const int32_t* feat_row_dev, int feat_row_add, int rows,
-                       const int32_t* n_rows_dev, void* const* k_cache, void* const* v_cache, int kv_dtype,
-                       int capacity, const int32_t* offset_dev, int offset_add, const int32_t* positions_dev,
-                       const uint8_t* mask_dev, int64_t mask_ld, float* hidden_out, float* out_out,
-                       int32_t* advance_dev, void* workspace, wc_stream_t stream) {
+}  // extern "C"
+
+namespace wc {
+// The token of the pending draft-head argmax (left in the workspace slots by
+// the head launch before): where the forward writes it and its head row.
+struct PendTok {
+  int32_t* tok;
+  int32_t* row;
+};
+
+static int drafter_forward_impl(const wc_drafter_dims* dims, const wc_drafter_weights* w, const int32_t* tokens_dev,
+                                const float* feat, int64_t feat_ld, const int32_t* feat_row_dev, int feat_row_add,
+                                int rows, const int32_t* n_rows_dev, void* const* k_cache, void* const* v_cache,
+                                int kv_dtype, int capacity, const int32_t* offset_dev, int offset_add,
+                                const int32_t* positions_dev, const uint8_t* mask_dev, int64_t mask_ld,
+                                float* hidden_out, float* out_out, int32_t* advance_dev, void* workspace,
+                                wc_stream_t stream, const PendTok* pend) {
   if (int rc = check_dims(dims)) return rc;
   const wc_drafter_dims& d = *dims;
-  WC_REQUIRE(w && tokens_dev && feat && hidden_out && workspace && offset_dev && k_cache && v_cache,
+  WC_REQUIRE(w && (tokens_dev || pend) && feat && hidden_out && workspace && offset_dev && k_cache && v_cache,
              "wc_drafter_forward: NULL argument");
+  WC_REQUIRE(pend == nullptr || (rows == 1 && n_rows_dev == nullptr && mask_dev == nullptr && pend->tok &&
+                                 w->layers[0].aux_norm),
+             "wc_drafter_forward_pending: one row, no device row count or mask, a token output and a first layer "
+             "with the token stream");
+  WC_REQUIRE(pend == nullptr || (d.hidden % 512 == 0 && d.hidden <= 10240 && w->layers[0].in_norm),
+             "wc_drafter_forward_pending: hidden_size must be a multiple of 512 (at most 10240)");
   WC_REQUIRE(al16(workspace), "wc_drafter_forward: workspace must be 16-byte aligned");
   WC_REQUIRE(rows >= 1, "wc_drafter_forward: rows must be positive");
   WC_REQUIRE(kv_dtype == WC_F32 || kv_dtype == WC_BF16, "wc_drafter_forward: kv dtype must be f32 or bf16");
@@ -810,7 +829,14 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
         e.x = w->embed;
         e.ld = d.hidden;
         e.dtype = WC_BF16;
-        e.row_idx = tokens_dev + t0;
+        if (pend && li == 0) {  // the token of the pending head argmax, published by block 0
+          e.pend_slots = ws.slots;
+          e.pend_d2t = w->d2t;
+          q.pend_tok_out = pend->tok;
+          q.pend_row_out = pend->row;
+        } else {
+          e.row_idx = pend ? pend->tok : tokens_dev + t0;  // later layers: the token layer 0 published
+        }
         e.max_row = d.vocab;
         e.gain = u16(L.aux_norm);
         e.K = d.hidden;
@@ -863,6 +889,7 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
       at.ctr = ws.attn_ctr;
       at.out = ws.attn;
       at.ld_out = H * D;
+      at.clear_slots = pend && li == 0 ? ws.slots : nullptr;  // the QKV launch above consumed them
       if (int rc = launch_attention(at, D, kv_dtype, splits, s)) return rc;
 
       // 3. o_proj with the residual: h1 = h + W_o . o
@@ -962,6 +989,32 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
   }
   return WC_OK;
 }
+}  // namespace wc
+
+extern "C" {
+
+int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w, const int32_t* tokens_dev,
+                       const float* feat, int64_t feat_ld, const int32_t* feat_row_dev, int feat_row_add, int rows,
+                       const int32_t* n_rows_dev, void* const* k_cache, void* const* v_cache, int kv_dtype,
+                       int capacity, const int32_t* offset_dev, int offset_add, const int32_t* positions_dev,
+                       const uint8_t* mask_dev, int64_t mask_ld, float* hidden_out, float* out_out,
+                       int32_t* advance_dev, void* workspace, wc_stream_t stream) {
+  return wc::drafter_forward_impl(dims, w, tokens_dev, feat, feat_ld, feat_row_dev, feat_row_add, rows, n_rows_dev,
+                                  k_cache, v_cache, kv_dtype, capacity, offset_dev, offset_add, positions_dev,
+                                  mask_dev, mask_ld, hidden_out, out_out, advance_dev, workspace, stream, nullptr);
+}
+
+int wc_drafter_forward_pending(const wc_drafter_dims* dims, const wc_drafter_weights* w, int32_t* token_out,
+                               int32_t* row_out, const float* feat, int64_t feat_ld, const int32_t* feat_row_dev,
+                               int feat_row_add, void* const* k_cache, void* const* v_cache, int kv_dtype,
+                               int capacity, const int32_t* offset_dev, int offset_add, const int32_t* positions_dev,
+                               float* hidden_out, float* out_out, int32_t* advance_dev, void* workspace,
+                               wc_stream_t stream) {
+  const wc::PendTok pend{token_out, row_out};
+  return wc::drafter_forward_impl(dims, w, nullptr, feat, feat_ld, feat_row_dev, feat_row_add, 1, nullptr, k_cache,
+                                  v_cache, kv_dtype, capacity, offset_dev, offset_add, positions_dev, nullptr, 0,
+                                  hidden_out, out_out, advance_dev, workspace, stream, &pend);
+}
 
 int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* out_rows, int64_t out_ld,
                   const int32_t* out_row_dev, int out_row_add, int rows, float* logits_out, int64_t logits_ld,
@@ -980,6 +1033,17 @@ int wc_draft_head_norm(const wc_drafter_dims* dims, const wc_drafter_weights* w,
              "wc_draft_head_norm: out rows must be 16-byte aligned with a stride >= hidden_size, multiple of 4");
   return wc::draft_head_impl(dims, w, hidden_rows, hidden_ld, row_dev, row_add, 1, out_norm, out_ld, logits_out,
                              logits_ld, token_out, row_out, gumbel, workspace, stream, true);
+}
+
+int wc_draft_head_norm_pending(const wc_drafter_dims* dims, const wc_drafter_weights* w, const float* hidden_rows,
+                               int64_t hidden_ld, const int32_t* row_dev, int row_add, float* out_norm, int64_t out_ld,
+                               float* logits_out, int64_t logits_ld, const wc_gumbel* gumbel, void* workspace,
+                               wc_stream_t stream) {
+  WC_REQUIRE(dims && w && w->final_norm, "wc_draft_head_norm_pending: final norm missing");
+  WC_REQUIRE(out_norm == nullptr || (out_ld >= dims->hidden && out_ld % 4 == 0 && wc::aligned(out_norm, 16)),
+             "wc_draft_head_norm_pending: out rows must be 16-byte aligned with a stride >= hidden_size, multiple of 4");
+  return wc::draft_head_impl(dims, w, hidden_rows, hidden_ld, row_dev, row_add, 1, out_norm, out_ld, logits_out,
+                             logits_ld, nullptr, nullptr, gumbel, workspace, stream, true, true);
 }
 
 }  // extern "C"

@@ -36,8 +36,6 @@ constexpr int kMaxM = 16;
 constexpr int kMaxIn = 3;
 constexpr int kMaxSeg = 3;
 constexpr int kGemvLdsBytes = 48 * 1024;
-constexpr int kSlots = 32;       // argmax atomics are spread over kSlots addresses per row
-constexpr int kSlotStride = 16;  // uint64s between slots: one 128-byte line each
 constexpr int kMaxSteps1 = 24;   // M=1 kernel: up to 24 x 512 = 12288 inputs per segment
 
 struct InSeg {
@@ -49,6 +47,11 @@ struct InSeg {
   const uint16_t* gain;    // RMSNorm gain [K] (bf16) or NULL: no norm
   int K;                   // multiple of 8
   int max_row;             // > 0: gathered rows are clamped to [0, max_row)
+  // optional (one input row): the row is the token of a pending draft-head
+  // argmax -- the largest of the kSlots keys at pend_slots (stride
+  // kSlotStride), its head row mapped through pend_d2t (NULL = identity)
+  const unsigned long long* pend_slots;
+  const int32_t* pend_d2t;
 };
 
 enum Epi { kEpiStore = 0, kEpiResidual = 1, kEpiSiluPair = 2, kEpiArgmax = 3 };
@@ -106,6 +109,10 @@ struct GemvArgs {
   // w[][] hold fragment-major matrices (wc_weights_frag): only the few-row MFMA
   // kernel reads that layout
   int wfrag;
+  // a segment with pend_slots: block 0 also writes the resolved token and head
+  // row (one-row kernel only)
+  int32_t* pend_tok_out;
+  int32_t* pend_row_out;
 };
 
 __device__ __forceinline__ float dot8(const uint4 w, const float4 a, const float4 b) {
@@ -138,7 +145,31 @@ __device__ __forceinline__ float load_in(const InSeg& s, int64_t row, int k) {
   return s.dtype == WC_BF16 ? bf16_to_float(static_cast<const uint16_t*>(s.x)[i]) : static_cast<const float*>(s.x)[i];
 }
 
+// Head row of the pending argmax: the largest key over the slots (each a
+// device-scope maximum of block keys written by the head launch before this
+// one), read with one wave-wide load (lane j: slot j) and reduced across the
+// wave.  Every lane of the wave must call it.
+__device__ __forceinline__ unsigned long long pend_key(const unsigned long long* slots) {
+  return slots[min(static_cast<int>(threadIdx.x % kWave), kSlots - 1) * kSlotStride];
+}
+__device__ __forceinline__ int pend_reduce(unsigned long long best) {
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    const unsigned long long v = __shfl_xor(best, o);
+    best = v > best ? v : best;
+  }
+  return __builtin_amdgcn_readfirstlane(argmax_key_index(best));
+}
+__device__ __forceinline__ int pend_head_row(const unsigned long long* slots) { return pend_reduce(pend_key(slots)); }
+__device__ __forceinline__ int pend_token(const InSeg& s, int head_row) {
+  int r = s.pend_d2t ? s.pend_d2t[head_row] : head_row;
+  if (s.max_row > 0) r = min(max(r, 0), s.max_row - 1);
+  return r;
+}
+
+// Input row m of segment s (every lane of the wave calls it).
 __device__ __forceinline__ int in_row(const InSeg& s, int m) {
+  if (s.pend_slots) return pend_token(s, pend_head_row(s.pend_slots));
   int r = (s.row_idx ? s.row_idx[m] : m) + s.row_add;
   if (s.max_row > 0) r = min(max(r, 0), s.max_row - 1);
   return r;
@@ -282,6 +313,7 @@ __device__ __forceinline__ void argmax_epilogue(const GemvArgs& a, int m, unsign
     for (int w = 0; w < kGemvWaves; ++w) best = s_key[w][threadIdx.x] > best ? s_key[w][threadIdx.x] : best;
     if (best) atomic_max_u64(&a.slots[(threadIdx.x * kSlots + blockIdx.x % kSlots) * kSlotStride], best);
   }
+  if (!a.counter) return;  // pending: the next launch resolves the slots
   if (!last_block_done(a.counter, gridDim.x)) return;
   // thread (row, slot): every slot read in parallel, then a max over the 32
   // lanes of the row's slots (kSlots == 32 lanes, half a wave)
@@ -335,24 +367,37 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
     // the compiler issues them back to back with no branch or merge between them;
     // out-of-range steps are zeroed in the x slices, and out-of-range rows are
     // never stored.
-    // 1. x slices, kept raw until the weights are in flight
+    // 1. x slices, kept raw until the weights are in flight; a segment whose row
+    // is a pending head argmax is resolved now and loaded after the weights, so
+    // its chain (keys -> d2t -> row) holds back no weight load
     uint4 xq[NIN][S][2];
     int steps[NIN];
-#pragma unroll
-    for (int s = 0; s < NIN; ++s) {
+    int64_t xrow[NIN];
+    auto load_x = [&](int s) {
       const InSeg& seg = a.in[s];
-      steps[s] = seg.K / (kWave * 8);
-      const int64_t row = m > 0 ? in_row(seg, 0) : 0;
 #pragma unroll
       for (int u = 0; u < S; ++u) {
         const int k = min(u, steps[s] - 1) * kWave * 8 + lane * 8;
         if (XB & (1 << s)) {
-          xq[s][u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + row * seg.ld + k);
+          xq[s][u][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + xrow[s] * seg.ld + k);
         } else {
-          const float* xp = static_cast<const float*>(seg.x) + row * seg.ld + k;
+          const float* xp = static_cast<const float*>(seg.x) + xrow[s] * seg.ld + k;
           xq[s][u][0] = *reinterpret_cast<const uint4*>(xp);
           xq[s][u][1] = *reinterpret_cast<const uint4*>(xp + 4);
         }
+      }
+    };
+    // the pending keys first (one wave-wide load), reduced after the weights are requested
+    unsigned long long pkey = 0;
+#pragma unroll
+    for (int s = 0; s < NIN; ++s)
+      if (a.in[s].pend_slots) pkey = pend_key(a.in[s].pend_slots);
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      steps[s] = a.in[s].K / (kWave * 8);
+      if (!a.in[s].pend_slots) {
+        xrow[s] = m > 0 ? in_row(a.in[s], 0) : 0;
+        load_x(s);
       }
     }
     // 2. gains
@@ -381,8 +426,24 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1(GemvArgs a) {
         }
       }
     }
+    int pend_hr = 0;  // head row of the pending segment
+#pragma unroll
+    for (int s = 0; s < NIN; ++s)
+      if (a.in[s].pend_slots) {
+        pend_hr = pend_reduce(pkey);
+        xrow[s] = m > 0 ? pend_token(a.in[s], pend_hr) : 0;
+        load_x(s);
+      }
 #pragma unroll
     for (int r = 0; r < R; ++r) resv[r] = res_at(a, rrow, min(row0 + r, a.N - 1));
+    if (a.pend_tok_out && blockIdx.x == 0 && threadIdx.x == 0) {
+#pragma unroll
+      for (int s = 0; s < NIN; ++s) {
+        if (!a.in[s].pend_slots) continue;
+        a.pend_tok_out[0] = a.in[s].pend_d2t ? a.in[s].pend_d2t[pend_hr] : pend_hr;
+        if (a.pend_row_out) a.pend_row_out[0] = pend_hr;
+      }
+    }
     // 4. per-segment 1/rms and x * gain (waits only for x and gain)
     float4 xr[NIN][S][2];
     float inv[NIN];

@@ -53,6 +53,8 @@ enum Counter { kCtrArgmax = 0, kCtrStochastic = 1, kCtrTree = 2, kCtrStochStats 
 // ------------------------------------------------------------------ device helpers
 
 constexpr int kWave = 64;
+constexpr int kSlots = 32;       // draft-head argmax atomics are spread over kSlots addresses per row
+constexpr int kSlotStride = 16;  // uint64s between slots: one 128-byte line each
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -98,6 +98,14 @@ class Drafter:
                 setattr(L, field, None if t is None else t.data_ptr())
         self.wstruct = W
 
+    @property
+    def pending_ok(self) -> bool:
+        """The chain may leave each head's argmax pending for the next forward
+        (wc_draft_head_norm_pending / wc_drafter_forward_pending): the first
+        layer takes the token stream and hidden_size is a multiple of 512."""
+        h = self.cfg.hidden_size
+        return "layers.0.aux_norm.weight" in self.w and h % 512 == 0 and h <= 10240
+
     def _ensure_rope(self, positions: int) -> None:
         if self._rope is not None and self._rope[0].shape[0] >= positions:
             return

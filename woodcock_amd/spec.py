@@ -88,6 +88,7 @@ class ChainRound:
             raise ValueError(f"at most {_lib.WC_MAX_STEP_ROWS} kept rows per round")
         self.d = drafter
         self.K = k
+        self.pending = True  # chain heads hand their argmax to the next forward (Drafter.pending_ok)
         self.max_keep = max_keep
         dev = drafter.device
         dm = drafter.cfg.hidden_size
@@ -158,8 +159,13 @@ class ChainRound:
         cap = self.cache[0].capacity
         # d_1 from the root = update row n_keep - 1; the head applies the final
         # RMSNorm and leaves the root's output in upd_out (same row)
-        _lib.call("wc_draft_head_norm", dims, W, ptr(self.upd_hid), dm, n_keep, -1, ptr(self.upd_out), dm, None, 0,
-                  ptr(self.drafts[0:1]), None, None, ws, s)
+        # every head but the last leaves its argmax pending in the workspace: the
+        # next forward resolves it as its token (and writes drafts[i - 1]), so no
+        # head launch ends in a last-block reduction on the critical path
+        pend = self.pending and d.pending_ok
+        head = "wc_draft_head_norm_pending" if pend and k > 1 else "wc_draft_head_norm"
+        tok0 = () if head == "wc_draft_head_norm_pending" else (ptr(self.drafts[0:1]), None)
+        _lib.call(head, dims, W, ptr(self.upd_hid), dm, n_keep, -1, ptr(self.upd_out), dm, None, 0, *tok0, None, ws, s)
         root_fb = self._fb_rows(self.upd_hid, self.upd_out)
         for i in range(1, k):
             if i == 1:
@@ -168,11 +174,20 @@ class ChainRound:
                 feat, frow, fadd = self._fb_rows(self.step_hid, self.step_out)[i - 2:i - 1], None, 0
             # the chain appends at n + i - 1 (contiguous positions, causal, python/woodcock/spec.py:349);
             # the layer's final RMSNorm is left to the next head (out_out = NULL)
-            _lib.call("wc_drafter_forward", dims, W, ptr(self.drafts[i - 1:i]), ptr(feat), dm, frow, fadd, 1, None,
-                      self._kp, self._vp, self._kvdt, cap, ptr(self.n_dev()), i - 1, None, None, 0,
-                      ptr(self.step_hid[i - 1:i]), None, None, ws, s)
-            _lib.call("wc_draft_head_norm", dims, W, ptr(self.step_hid[i - 1:i]), dm, None, 0,
-                      ptr(self.step_out[i - 1:i]), dm, None, 0, ptr(self.drafts[i:i + 1]), None, None, ws, s)
+            if pend:
+                _lib.call("wc_drafter_forward_pending", dims, W, ptr(self.drafts[i - 1:i]), None, ptr(feat), dm, frow,
+                          fadd, self._kp, self._vp, self._kvdt, cap, ptr(self.n_dev()), i - 1, None,
+                          ptr(self.step_hid[i - 1:i]), None, None, ws, s)
+            else:
+                _lib.call("wc_drafter_forward", dims, W, ptr(self.drafts[i - 1:i]), ptr(feat), dm, frow, fadd, 1,
+                          None, self._kp, self._vp, self._kvdt, cap, ptr(self.n_dev()), i - 1, None, None, 0,
+                          ptr(self.step_hid[i - 1:i]), None, None, ws, s)
+            if pend and i < k - 1:
+                _lib.call("wc_draft_head_norm_pending", dims, W, ptr(self.step_hid[i - 1:i]), dm, None, 0,
+                          ptr(self.step_out[i - 1:i]), dm, None, 0, None, ws, s)
+            else:
+                _lib.call("wc_draft_head_norm", dims, W, ptr(self.step_hid[i - 1:i]), dm, None, 0,
+                          ptr(self.step_out[i - 1:i]), dm, None, 0, ptr(self.drafts[i:i + 1]), None, None, ws, s)
         # the speculative entries n..n+k-2 are simply overwritten later: the
         # drafter's committed count n is never advanced by the chain (spec.py:351-352)
 
