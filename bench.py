@@ -155,6 +155,66 @@ def time_draft_step(d, cache, ctx, reps=32, samples=10, cold_samples=20, evict=N
     return res
 
 
+def time_head(d, pending, reps=32, samples=10, cold_samples=20, evict=None):
+    """The chain's draft head on its own (final norm + 16k-row head GEMV with
+    argmax keys; pending: the keys stay in the workspace for the next forward,
+    as in every chain step but the last) at one row.  Warm: a graph of `reps`
+    launches (median over `samples` replays, per launch).  Cold: one launch
+    between two events after `evict()` streamed 1 GiB, behind the spin gate
+    (median over `cold_samples`).  A plain head launch afterwards clears the
+    pending keys."""
+    import ctypes as C
+
+    import torch
+
+    from woodcock_amd import _lib
+    from woodcock_amd.runtime import ptr, stream_ptr
+
+    dev = d.device
+    dm = d.cfg.hidden_size
+    dims, W, ws = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws)
+    g = torch.Generator(device=dev).manual_seed(11)
+    hid = torch.randn(1, dm, generator=g, device=dev)
+    out = torch.empty_like(hid)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def plain():
+        _lib.call("wc_draft_head_norm", dims, W, ptr(hid), dm, None, 0, ptr(out), dm, None, 0, ptr(tok), None, None,
+                  ws, stream_ptr())
+
+    def one():
+        if pending:
+            _lib.call("wc_draft_head_norm_pending", dims, W, ptr(hid), dm, None, 0, ptr(out), dm, None, 0, None, ws,
+                      stream_ptr())
+        else:
+            plain()
+
+    def many():
+        for _ in range(reps):
+            one()
+
+    many()
+    torch.cuda.synchronize()
+    gr = capture(many)
+    res = {"warm_us": float(np.median(gpu_time_graphs([gr], samples))) / reps}
+    if evict is not None:
+        t = []
+        for _ in range(cold_samples):
+            evict()
+            _sleep_gate()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            one()
+            e1.record()
+            torch.cuda.synchronize()
+            t.append(1e3 * e0.elapsed_time(e1))
+        res["cold_us"] = float(np.median(t))
+    if pending:
+        plain()
+        torch.cuda.synchronize()
+    return res
+
+
 def step_only(args):
     """Only the draft steps of configs 1 and 4, warm and cold; one JSON line."""
     import torch
@@ -167,6 +227,7 @@ def step_only(args):
     flush = torch.zeros(1 << 28, dtype=torch.float32, device=d.device)
     out = {}
     if args.step_config in ("1", "both"):
+        out["config1_head"] = time_head(d, pending=d.pending_ok, evict=flush.sum)
         out["config1"] = time_draft_step(d, rnd.cache, BASE_CTX, evict=flush.sum)
         out["config1_plain_head"] = time_draft_step(d, rnd.cache, BASE_CTX, evict=flush.sum, pending=False)
     if args.step_config == "1":
@@ -318,23 +379,6 @@ def bench_gpu(args):
     hid1 = rnd.upd_hid[0:1]
     out1 = rnd.upd_out[0:1]
     tok = rnd.drafts[0:1]
-    hid_s = torch.empty(1, dm, device=out1.device)
-
-    def heads():
-        for _ in range(REP):
-            _lib.call("wc_draft_head_norm", dims, W, ptr(hid1), dm, None, 0, ptr(out1), dm, None, 0, ptr(tok),
-                      None, None, ws, s())
-
-    def steps():
-        # the reference's draft-step unit: (final norm +) head + argmax + one drafter layer, KV rolled back;
-        # the layer leaves its final norm to the next head, as in the chain
-        for _ in range(REP):
-            _lib.call("wc_draft_head_norm", dims, W, ptr(hid1), dm, None, 0, ptr(out1), dm, None, 0, ptr(tok),
-                      None, None, ws, s())
-            _lib.call("wc_drafter_forward", dims, W, ptr(tok), ptr(out1), dm, None, 0, 1, None, rnd._kp, rnd._vp,
-                      rnd._kvdt, rnd.cache[0].capacity, ptr(init_state[0:1]), 0, None, None, 0, ptr(hid_s),
-                      None, None, ws, s())
-
     vlog = torch.randn(6, cfg.vocab_size, device=out1.device) * 3
     vdr = torch.randint(0, cfg.vocab_size, (5,), dtype=torch.int32, device=out1.device)
     vverd = torch.zeros(_lib.VERDICT_INTS, dtype=torch.int32, device=out1.device)
@@ -490,30 +534,12 @@ def bench_gpu(args):
     for c in cache4:
         c.keys[0, :, :CTX4] = torch.randn(c.keys[0, :, :CTX4].shape, generator=g4, device=out1.device).bfloat16()
         c.values[0, :, :CTX4] = torch.randn(c.values[0, :, :CTX4].shape, generator=g4, device=out1.device).bfloat16()
-    dims4, W4, ws4 = C.byref(d4.dims), C.byref(d4.wstruct), ptr(d4.ws)
-    hid4 = torch.randn(1, cfg4.hidden_size, generator=g4, device=out1.device)
-    out4 = torch.empty_like(hid4)
-    hid4s = torch.empty_like(hid4)
-    tok4 = torch.zeros(1, dtype=torch.int32, device=out1.device)
-    off4 = torch.tensor([CTX4], dtype=torch.int32, device=out1.device)
-    kp4 = (C.c_void_p * 1)(cache4[0].keys.data_ptr())
-    vp4 = (C.c_void_p * 1)(cache4[0].values.data_ptr())
-
-    def steps_4b():
-        for _ in range(REP):
-            _lib.call("wc_draft_head_norm", dims4, W4, ptr(hid4), cfg4.hidden_size, None, 0, ptr(out4),
-                      cfg4.hidden_size, None, 0, ptr(tok4), None, None, ws4, s())
-            _lib.call("wc_drafter_forward", dims4, W4, ptr(tok4), ptr(out4), cfg4.hidden_size, None, 0, 1, None,
-                      kp4, vp4, _lib.WC_BF16, cache4[0].capacity, ptr(off4), 0, None, None, 0, ptr(hid4s), None,
-                      None, ws4, s())
-
     log("cold rounds done; component graphs")
     comps = {}
     reps = {"target_layer": REP // 4, "target_chain": 1, "target_tree": 1, "tree_draft": 1}
-    for name, fn in (("head", heads), ("draft_step", steps), ("verify", verifies), ("compact", compacts),
+    for name, fn in (("verify", verifies), ("compact", compacts),
                      ("draft_probs", draft_probs), ("stochastic", stochastic), ("target_layer", target_layers), ("tree_verify", tree_verifies),
-                     ("target_chain", target_chain), ("target_tree", target_tree), ("tree_draft", tree_drafts),
-                     ("draft_step_4b", steps_4b)):
+                     ("target_chain", target_chain), ("target_tree", target_tree), ("tree_draft", tree_drafts)):
         fn()
         torch.cuda.synchronize()
         g = capture(fn)
@@ -521,21 +547,14 @@ def bench_gpu(args):
         comps[name] = float(np.median(t)) / reps.get(name, REP)
     rewind()
     torch.cuda.synchronize()
-    # one head launch between two events behind the spin gate, after the 1 GiB
-    # read (cold) or straight after the previous launch (warm, the same timing
-    # method: event overhead included in both)
-    cold_head, warm_head = [], []
-    for i in range(40):
-        if i % 2 == 0:
-            evict()
-        _sleep_gate()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        _lib.call("wc_draft_head_norm", dims, W, ptr(hid1), dm, None, 0, ptr(out1), dm, None, 0, ptr(tok), None,
-                  None, ws, s())
-        e1.record()
-        torch.cuda.synchronize()
-        (cold_head if i % 2 == 0 else warm_head).append(1e3 * e0.elapsed_time(e1))
+    # the chain's head and draft step (pending argmax hand-over), warm and cold
+    # (each cold sample after the 1 GiB read, one launch or step between events)
+    head = time_head(d, pending=d.pending_ok, evict=evict)
+    head_plain = time_head(d, pending=False, evict=None)
+    step = time_draft_step(d, rnd.cache, BASE_CTX, evict=evict)
+    step4 = time_draft_step(d4, cache4, CTX4, evict=evict)
+    rewind()
+    torch.cuda.synchronize()
     del flush
     torch.cuda.empty_cache()
     log("components done; config-4 round loop")
@@ -555,8 +574,11 @@ def bench_gpu(args):
         "round_gpu_us_mean": float(np.mean(rounds_gpu)),
         "round_wall_us": float(np.median(walls)),
         "target_standin_us": float(np.median(plants)),
-        "draft_step_us": comps["draft_step"],
-        "head_us": comps["head"],
+        "draft_step_us": step["warm_us"],
+        "draft_step_us_cold": step["cold_us"],
+        "head_us": head["warm_us"],
+        "head_us_cold": head["cold_us"],
+        "head_plain_us": head_plain["warm_us"],
         "verify_accept_us": comps["verify"],
         "kv_compact_us": comps["compact"],
         "stochastic_us": comps["stochastic"],
@@ -566,10 +588,9 @@ def bench_gpu(args):
         "target_chain_us": comps["target_chain"],
         "target_tree_us": comps["target_tree"],
         "tree_draft_us": comps["tree_draft"],
-        "draft_step_4b_us": comps["draft_step_4b"],
+        "draft_step_4b_us": step4["warm_us"],
+        "draft_step_4b_us_cold": step4["cold_us"],
         "round_gpu_us_cold": float(np.median(cold)),
-        "head_us_cold": float(np.median(cold_head)),
-        "head_us_warm_single": float(np.median(warm_head)),
         "config4": c4,
         "config5": c5,
         "head_bytes": head_bytes,
@@ -1056,6 +1077,48 @@ def trace_summary(trace_dir: str, steps: int) -> None:
     print("\n".join(lines))
 
 
+def cold_trace_summary(trace_dir: str) -> None:
+    """Markdown table of our kernels (wc::) in a rocprofv3 kernel trace, split
+    into cold launches -- the first launch of a kind after a 1 GiB flush (a
+    torch reduction of >= 50 µs), up to the next flush -- and warm launches
+    (all others, e.g. inside the replayed graphs)."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {trace_dir}")
+    with open(files[0], newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    cold: dict[str, list[float]] = {}
+    warm: dict[str, list[float]] = {}
+    seen = None  # kernel kinds launched since the last flush, or None before the first
+    for r in rows:
+        name, us = r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        if "reduce_kernel" in name and us >= 50.0:
+            seen = set()
+            continue
+        if "wc::" not in name:
+            continue
+        if seen is not None and name not in seen:
+            seen.add(name)
+            cold.setdefault(name, []).append(us)
+        else:
+            warm.setdefault(name, []).append(us)
+
+    def short(n: str) -> str:
+        return n if len(n) <= 90 else n[:87] + "..."
+
+    lines = ["| Kernel | Cold launches | Cold avg µs | Cold min | Warm launches | Warm avg µs | Warm min |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for k in sorted(set(cold) | set(warm), key=lambda k: -np.mean(cold.get(k, warm.get(k)))):
+        c, w = cold.get(k, []), warm.get(k, [])
+        cs = f"{len(c)} | {np.mean(c):.2f} | {min(c):.2f}" if c else "0 | | "
+        ws = f"{len(w)} | {np.mean(w):.2f} | {min(w):.2f}" if w else "0 | | "
+        lines.append(f"| `{short(k)}` | {cs} | {ws} |")
+    print("\n".join(lines))
+
+
 def head_traffic():
     """HBM bytes per head launch from the committed counter summary, or None."""
     try:
@@ -1201,6 +1264,8 @@ def main():
                     help="with --step-only: the drafter shapes to time")
     ap.add_argument("--round-only", action="store_true",
                     help="only the timed config-1 rounds (for a kernel trace of the round alone)")
+    ap.add_argument("--cold-trace-summary", metavar="TRACE_DIR",
+                    help="print the cold / warm split of our kernels in a rocprofv3 kernel trace")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="summarise a rocprofv3 kernel trace of --round-only (no GPU needed); --steps as in that run")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -1214,6 +1279,9 @@ def main():
         return
     if args.trace_summary:
         trace_summary(args.trace_summary, args.steps)
+        return
+    if args.cold_trace_summary:
+        cold_trace_summary(args.cold_trace_summary)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the round is a batch-1, single-device path with no collective; "
@@ -1243,8 +1311,10 @@ def main():
     if args.round_only:
         print(json.dumps({"round_gpu_us": round(r["round_gpu_us"], 2), "steps": args.steps}), flush=True)
         return
-    head_gbs = r["head_bytes"] / (r["head_us"] * 1e-6) / 1e9
-    step_gbs = r["step_bytes"] / (r["draft_step_us"] * 1e-6) / 1e9
+    def frac(nbytes, us):
+        return nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS
+
+    head_gbs = r["head_bytes"] / (r["head_us_cold"] * 1e-6) / 1e9  # cold: the weights come from HBM
     cpu = None if args.no_cpu_baseline else cpu_baseline(r, args.cpu_seconds)
     line = {
         "metric": "µs per spec round (draft step, verify+accept, KV compact) + % HBM roofline",
@@ -1260,8 +1330,11 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded random-init weights and inputs)",
         "config": {
-            "workload": "greedy chain round, Qwen3-1.7B drafter shape, 16k trimmed head, drafter ctx 512, K=4, "
-                        "a=2 accepted; target logits [5,151936] fp32; 28-layer target KV compaction",
+            "workload": "greedy chain round, Qwen3-1.7B drafter shape, 16k trimmed head, drafter ctx 512: K=4 "
+                        "draft steps, greedy verify + accept of the 5-row block against target logits "
+                        "[5,151936] fp32 (a=2 accepted), the drafter update over the accepted rows; a chain "
+                        "commit is contiguous, so the round has no KV compaction (the tree-path compaction "
+                        "of a 28-layer target cache is timed on its own)",
             "k": K, "drafter_ctx": BASE_CTX, "head_rows": 16384, "vocab": 151936, "parallelism": "none (1 GPU)",
         },
         "breakdown": {
@@ -1269,7 +1342,9 @@ def main():
             "round_wall_us_incl_sync": round(r["round_wall_us"], 2),
             "target_standin_us_excluded": round(r["target_standin_us"], 2),
             "draft_step_us": round(r["draft_step_us"], 2),
-            "draft_step_hbm_frac": round(step_gbs / PEAK_HBM_GBS, 4),
+            "draft_step_us_cold": round(r["draft_step_us_cold"], 2),
+            "draft_step_hbm_frac": round(frac(r["step_bytes"], r["draft_step_us_cold"]), 4),
+            "draft_step_hbm_frac_warm": round(frac(r["step_bytes"], r["draft_step_us"]), 4),
             "verify_accept_us_k5": round(r["verify_accept_us"], 2),
             "kv_compact_us_28l_ctx2048_window6": round(r["kv_compact_us"], 2),
             "verify_stochastic_us_k5_vocab151936": round(r["stochastic_us"], 2),
@@ -1281,24 +1356,28 @@ def main():
             "target_forward_us_qwen3_1p7b_28l_m60_tree_ctx2048": round(r["target_tree_us"], 1),
             "tree_draft_us_qwen3_1p7b_depth6_width4_n60": round(r["tree_draft_us"], 1),
             "draft_step_us_qwen3_4b_ctx4096": round(r["draft_step_4b_us"], 2),
-            "draft_step_hbm_frac_qwen3_4b": round(STEP4_BYTES / (r["draft_step_4b_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "draft_step_us_cold_qwen3_4b_ctx4096": round(r["draft_step_4b_us_cold"], 2),
+            "draft_step_hbm_frac_qwen3_4b": round(frac(STEP4_BYTES, r["draft_step_4b_us_cold"]), 4),
+            "draft_step_hbm_frac_warm_qwen3_4b": round(frac(STEP4_BYTES, r["draft_step_4b_us"]), 4),
             "head_gemv_us": round(r["head_us"], 2),
-            "round_gpu_us_cold": round(r["round_gpu_us_cold"], 2),
             "head_gemv_us_cold": round(r["head_us_cold"], 2),
-            "head_gemv_us_warm_same_method": round(r["head_us_warm_single"], 2),
-            "head_gemv_hbm_frac_cold": round(r["head_bytes"] / (r["head_us_cold"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            "head_gemv_us_with_argmax_reduction": round(r["head_plain_us"], 2),
+            "round_gpu_us_cold": round(r["round_gpu_us_cold"], 2),
             "config4_auto_k_qwen3_4b": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in r["config4"].items()},
             "config5_tree_round_qwen3_1p7b": {k: (round(v, 2) if isinstance(v, float) else v)
                                               for k, v in r["config5"].items()},
         },
         "roofline": {
-            "kernel": "draft head GEMV + argmax (16384 x 2048 bf16)",
+            "kernel": "draft head GEMV with argmax keys (16384 x 2048 bf16), cold: after a 1 GiB read that "
+                      "evicts the Infinity Cache; one launch between events",
             "bound": "hbm",
             "achieved": round(head_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(head_gbs / PEAK_HBM_GBS, 4),
             "traffic": head_traffic(),
+            "warm_achieved": round(r["head_bytes"] / (r["head_us"] * 1e-6) / 1e9, 1),
+            "warm_frac": round(frac(r["head_bytes"], r["head_us"]), 4),
         },
         "cpu_baseline": cpu,
     }
