@@ -836,6 +836,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_decode(AttnArgs a) {
 // finish merges the live splits in one round of 16-byte coherent loads (wave v
 // takes query vector v; a lane holds 4 dims of every other split).
 constexpr int kFxMaxSplits = 64;
+constexpr int kFxMaxRows = 8;  // rows of one launch (appended rows held in LDS)
 constexpr int kFxThreads = 512;  // block size of the one-chunk splits
 constexpr int kFxRec = 132;  // floats per (split, vector) record: o[128], m, l, 2 pad (16-byte multiple)
 
@@ -877,10 +878,10 @@ __device__ __forceinline__ void split8(const float* x, abf16x8& hi, abf16x8& lo)
 // over coherently (outputs (ov0 + VSTEP k, od) of thread t, ov0 = t / 128).
 template <int OPT, int VSTEP>
 __device__ __forceinline__ void fx_publish(const AttnArgs& a, const float* o, const float* s_m, const float* s_l,
-                                           int QV) {
+                                           int QV, int64_t rec) {
   constexpr int D = 128, QVM = 4;
   const int t = threadIdx.x, od = t % D, ov0 = t / D;
-  float* part = a.partial + (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) * QVM * kFxRec;
+  float* part = a.partial + rec * QVM * kFxRec;
 #pragma unroll
   for (int k = 0; k < OPT; ++k) {
     const int v = ov0 + VSTEP * k;
@@ -894,20 +895,21 @@ __device__ __forceinline__ void fx_publish(const AttnArgs& a, const float* o, co
   }
 }
 
-// Split counter of this kv head; the last split to arrive merges the SL live
-// splits in one round of coherent 16-byte loads (records of splits >= SL lie
-// past the resource's range and read as zeros): wave v takes query vector v,
-// lane j split j's (m, l), and each lane 4 dims of every other split.
+// Split counter of this (kv head, row group) -- group g = kh * Z + z; the
+// last split to arrive merges the SL live splits in one round of coherent
+// 16-byte loads (records of splits >= SL lie past the resource's range and
+// read as zeros): wave v takes query vector v (row lz0 + v / rep), lane j split
+// j's (m, l), and each lane 4 dims of every other split.
 __device__ __forceinline__ void fx_merge(const AttnArgs& a, float (*s_w)[kFxMaxSplits], bool& s_last, int T, int per,
-                                         int QV, int rep) {
+                                         int QV, int rep, int lz0) {
   constexpr int D = 128, QVM = 4;
-  const int kh = blockIdx.y, S = gridDim.x;
+  const int kh = blockIdx.y, S = gridDim.x, g = blockIdx.y * gridDim.z + blockIdx.z;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (t == 0) {
-    unsigned int* ctr = a.ctr + kh * kCounterStride;
+    unsigned int* ctr = a.ctr + g * kCounterStride;
     const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                       static_cast<unsigned int>(S - 1);
     if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -919,7 +921,7 @@ __device__ __forceinline__ void fx_merge(const AttnArgs& a, float (*s_w)[kFxMaxS
   if (wave >= QV || SL <= 0) return;  // wave-uniform
   const int rec_bytes = QVM * kFxRec * 4;  // one split's records
   const __amdgpu_buffer_rsrc_t rs =
-      buffer_rsrc(a.partial + static_cast<int64_t>(kh) * S * QVM * kFxRec, SL * rec_bytes);
+      buffer_rsrc(a.partial + static_cast<int64_t>(g) * S * QVM * kFxRec, SL * rec_bytes);
   const int half = lane / 32, d4 = lane % 32;
   float4 ov[kFxMaxSplits / 2];
 #pragma unroll
@@ -948,7 +950,7 @@ __device__ __forceinline__ void fx_merge(const AttnArgs& a, float (*s_w)[kFxMaxS
   num.z += __shfl_xor(num.z, 32);
   num.w += __shfl_xor(num.w, 32);
   if (half) return;
-  const int l = wave / rep, h = kh * rep + wave % rep;
+  const int l = lz0 + wave / rep, h = kh * rep + wave % rep;
   const float y[4] = {num.x / den, num.y / den, num.z / den, num.w / den};
   *reinterpret_cast<float4*>(a.out + l * a.ld_out + h * D + 4 * d4) = make_float4(y[0], y[1], y[2], y[3]);
   if (a.xa_out) {
@@ -977,8 +979,8 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   static_assert(NL >= 1 && NL * KPB == CHK, "whole key rows per chunk");
   static_assert(NT / kWave >= QVM && OPT >= 1, "a wave per query vector, an output per thread");
   __shared__ __attribute__((aligned(16))) float qs[QVM][D];
-  __shared__ __attribute__((aligned(16))) float nks[QVM][D];
-  __shared__ __attribute__((aligned(16))) float nvs[QVM][D];
+  __shared__ __attribute__((aligned(16))) float nks[kFxMaxRows][D];  // appended rows (cache-rounded)
+  __shared__ __attribute__((aligned(16))) float nvs[kFxMaxRows][D];
   __shared__ __attribute__((aligned(16))) float vls[CHK][D];
   __shared__ __attribute__((aligned(16))) float s_p[QVM][CHK];
   __shared__ float s_m[QVM], s_l[QVM], s_alpha[QVM];
@@ -994,14 +996,19 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   const int kr = t / LK, e0 = (t % LK) * VE;
   const int64_t last_row = static_cast<int64_t>(a.cap) - 1;
   const int rep = a.H / a.Hk;
+  // row group z of the block: rows lz0 .. lz0 + rpz - 1 (rep query vectors each)
+  const int z = blockIdx.z, rpz = QVM / rep, lz0 = z * rpz;
+  constexpr int NW = NT / kWave;
+  constexpr int RPW = (kFxMaxRows + NW - 1) / NW;  // appended rows per wave (rows w, w + NW, ...)
 
   // 0. the offset and the live row count, requested before anything else
   const int off_raw = *a.offset_dev;
   const int nr_raw = *(a.n_rows_dev ? a.n_rows_dev : a.offset_dev);
-  if (a.clear_slots && blockIdx.x == 0 && blockIdx.y == 0 && t < kSlots) a.clear_slots[t * kSlotStride] = 0ull;
+  if (a.clear_slots && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && t < kSlots)
+    a.clear_slots[t * kSlotStride] = 0ull;
 
   // 1. in flight at entry: the split's first CPS chunks, the raw q vector of
-  // this wave (v = wave) and, on wave QVM-1-l, the raw k / v rows of row l
+  // this wave (v = wave) and the raw k / v rows of rows wave + NW i
   uint4 kreg[CPS][NL], vreg[CPS][NL];
 #pragma unroll
   for (int c = 0; c < CPS; ++c)
@@ -1011,23 +1018,27 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
       kreg[c][i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
       vreg[c][i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
     }
-  const int vq = wave, lq = min(vq / rep, a.rows - 1), hq = kh * rep + vq % rep;
+  const int vq = wave, lq = min(lz0 + vq / rep, a.rows - 1), hq = kh * rep + vq % rep;
   HeadVec<D> rq;
   head_vec_load<D>(a.qkv + lq * a.ld_qkv + hq * D, a.q_gain, rq);
-  const int lk = max(0, min(QVM - 1 - wave, a.rows - 1));
-  HeadVec<D> rk;
-  head_vec_load<D>(a.qkv + lk * a.ld_qkv + (a.H + kh) * D, a.k_gain, rk);
-  const float* vsrc = a.qkv + lk * a.ld_qkv + (a.H + a.Hk + kh) * D;
-  float vraw[D / kWave];
+  HeadVec<D> rk[RPW];
+  float vraw[RPW][D / kWave];
 #pragma unroll
-  for (int i = 0; i < D / kWave; ++i) vraw[i] = vsrc[lane + i * kWave];
+  for (int r = 0; r < RPW; ++r) {
+    const int lk = min(wave + NW * r, a.rows - 1);
+    head_vec_load<D>(a.qkv + lk * a.ld_qkv + (a.H + kh) * D, a.k_gain, rk[r]);
+    const float* vsrc = a.qkv + lk * a.ld_qkv + (a.H + a.Hk + kh) * D;
+#pragma unroll
+    for (int i = 0; i < D / kWave; ++i) vraw[r][i] = vsrc[lane + i * kWave];
+  }
 
   const int nr = a.n_rows_dev ? min(max(nr_raw, 0), a.rows) : a.rows;
   const int offset = off_raw + a.offset_add;
   const int T = min(offset + nr, a.cap);
-  const int QV = nr * rep;
+  const int nlast = min(nr, lz0 + rpz);           // rows 0 .. nlast - 1 are visible to this group
+  const int QV = max(0, nlast - lz0) * rep;       // live query vectors of this group
   const int ke = min(T, kb + per);
-  const bool live = kb < ke;
+  const bool live = kb < ke && QV > 0;
 
   if (live) {
     auto row_pos = [&](int l) {
@@ -1046,23 +1057,23 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
         }
       }
     }
-    const int tk = offset + (QVM - 1 - wave);
-    const bool owner = wave < QVM && QVM - 1 - wave < nr && tk >= kb && tk < ke;  // wave-uniform: this split holds row l
-    if (owner) {
-      const int l = QVM - 1 - wave;
-      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), rk);
-      head_vec_norm_rope<D>(rk, a.eps);
+    // appended rows of this split's key range that the group's rows see
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int l = wave + NW * r, tk = offset + l;
+      if (!(l < nlast && tk >= kb && tk < ke)) continue;  // wave-uniform
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), rk[r]);
+      head_vec_norm_rope<D>(rk[r], a.eps);
 #pragma unroll
       for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
         const int p = lane + e * kWave;
         if (p < D / 2) {
-          nks[l][p] = kv_round<KT>(rk.lo[e]);
-          nks[l][p + D / 2] = kv_round<KT>(rk.hi[e]);
+          nks[l][p] = kv_round<KT>(rk[r].lo[e]);
+          nks[l][p + D / 2] = kv_round<KT>(rk[r].hi[e]);
         }
       }
 #pragma unroll
-      for (int i = 0; i < D / kWave; ++i)
-        nvs[l][lane + i * kWave] = kv_round<KT>(vraw[i]);
+      for (int i = 0; i < D / kWave; ++i) nvs[l][lane + i * kWave] = kv_round<KT>(vraw[r][i]);
     }
     if (t < QVM) {
       s_m[t] = -INFINITY;
@@ -1088,12 +1099,13 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
           float kf[VE], vf[VE];
           unpack16<KT>(kreg[c][i], kf);
           unpack16<KT>(vreg[c][i], vf);
-          if (tt >= offset) {  // appended rows: the values this launch stored
-            const int l = min(tt - offset, QVM - 1);
+          if (tt >= offset) {  // appended rows: this launch's values (zero past the group's last row)
+            const int l = min(tt - offset, kFxMaxRows - 1);
+            const bool mine = tt - offset < nlast;
 #pragma unroll
             for (int e = 0; e < VE; ++e) {
-              kf[e] = nks[l][e0 + e];
-              vf[e] = nvs[l][e0 + e];
+              kf[e] = mine ? nks[l][e0 + e] : 0.f;
+              vf[e] = mine ? nvs[l][e0 + e] : 0.f;
             }
           }
           if (j >= n) {
@@ -1126,7 +1138,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
           if (t % LK == 0) {
 #pragma unroll
             for (int v = 0; v < QVM; ++v) {
-              const int l = v / rep;
+              const int l = lz0 + v / rep;
               const bool vis = v < QV && j < n && tt <= offset + l && (a.window <= 0 || tt > offset + l - a.window);
               s_p[v][j] = vis ? a.scale * dv[v] : -INFINITY;
             }
@@ -1188,9 +1200,12 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
     }
 
     // the appended rows into the cache (after the chunks, so no wait in the
-    // chunk loop covers these stores); the lanes that wrote nks / nvs read them
-    if (owner) {
-      const int l = QVM - 1 - wave;
+    // chunk loop covers these stores), each by the group holding its row; the
+    // lanes that wrote nks / nvs read them
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int l = wave + NW * r, tk = offset + l;
+      if (!(l < nlast && l >= lz0 && tk >= kb && tk < ke)) continue;  // wave-uniform
 #pragma unroll
       for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
         const int p = lane + e * kWave;
@@ -1203,9 +1218,10 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
       for (int i = 0; i < D / kWave; ++i)
         kv_put<KT>(vc, static_cast<int64_t>(tk) * D + lane + i * kWave, nvs[l][lane + i * kWave]);
     }
-    fx_publish<OPT, VSTEP>(a, o, s_m, s_l, QV);
+    fx_publish<OPT, VSTEP>(a, o, s_m, s_l, QV,
+                           (static_cast<int64_t>(kh) * gridDim.z + z) * gridDim.x + split);
   }
-  fx_merge(a, s_w, s_last, T, per, QV, rep);
+  fx_merge(a, s_w, s_last, T, per, QV, rep, lz0);
 }
 
 // Fixed-range decode split plan for a capacity: chunks of 32 keys, at most
@@ -1226,22 +1242,28 @@ static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream)
   const size_t qvb = static_cast<size_t>(a.rows) * (a.H / a.Hk);
   if constexpr (D == 64 || D == 128) {
     if constexpr (D == 128) {
-    if (!a.mask && qvb <= 4 && a.ctr && a.ld_out % 4 == 0 && aligned(a.out, 16) &&
-        static_cast<size_t>(a.qv_ld) * kMaxSplits * (D + 2) >= static_cast<size_t>(kFxMaxSplits) * 4 * kFxRec) {
-      // fixed key ranges from the capacity, merge fused; the partials as
-      // (split, vector) records of kFxRec floats, 4 vectors per split, in the
-      // same workspace
+    const int rep = a.H / std::max(a.Hk, 1);
+    const int groups = rep >= 1 && rep <= 4 ? (a.rows * rep + 3) / 4 : 0;  // row groups of <= 4 query vectors
+    if (!a.mask && a.ctr && groups >= 1 && a.rows <= kFxMaxRows && a.Hk * groups <= kMaxKvHeads &&
+        a.ld_out % 4 == 0 && aligned(a.out, 16) &&
+        static_cast<size_t>(a.qv_ld) * kMaxSplits * (D + 2) >=
+            static_cast<size_t>(groups) * kFxMaxSplits * 4 * kFxRec) {
+      // fixed key ranges from the capacity, merge fused per (kv head, row
+      // group); the partials as (group, split, vector) records of kFxRec
+      // floats, 4 vectors per split, in the same workspace
       constexpr int NT = kAttnThreads;
       const FxPlan pl = fx_plan(a.cap, 32);
-      if (pl.cps == 1)  // one chunk per split: two waves per SIMD share its latency-bound math
-        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 1, kFxThreads>), dim3(pl.splits, a.Hk), dim3(kFxThreads), 0,
-                           stream, a, pl.per);
+      const dim3 grid(pl.splits, a.Hk, groups);
+      if (pl.cps == 1 && groups == 1)  // one chunk per split: two waves per SIMD share its latency-bound math
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 1, kFxThreads>), grid, dim3(kFxThreads), 0, stream, a, pl.per);
+      else if (pl.cps == 1)  // several row groups: 256-thread blocks keep the grid resident at once
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 1, NT>), grid, dim3(NT), 0, stream, a, pl.per);
       else if (pl.cps == 2)
-        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 2, NT>), dim3(pl.splits, a.Hk), dim3(NT), 0, stream, a, pl.per);
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 2, NT>), grid, dim3(NT), 0, stream, a, pl.per);
       else if (pl.cps == 3)
-        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 3, NT>), dim3(pl.splits, a.Hk), dim3(NT), 0, stream, a, pl.per);
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 3, NT>), grid, dim3(NT), 0, stream, a, pl.per);
       else  // four chunks in flight, the rest through the ring
-        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 4, NT>), dim3(pl.splits, a.Hk), dim3(NT), 0, stream, a, pl.per);
+        hipLaunchKernelGGL((k_attn_decode_fx<D, KT, 4, NT>), grid, dim3(NT), 0, stream, a, pl.per);
       WC_LAUNCHED();
       return WC_OK;
     }
