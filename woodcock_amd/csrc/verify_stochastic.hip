@@ -1582,10 +1582,13 @@ struct ProbsArgs {
 };
 
 __device__ __forceinline__ float scaled(const ProbsArgs& a, float v) { return v / a.temperature; }
-// scaled logit x of entry i (in range), or -inf when top-k drops it (x below the k-th largest)
-__device__ __forceinline__ float warped(const ProbsArgs& a, int r, float raw) {
+// The k-th largest scaled logit's order key of row r, read once per block; 0
+// (below every key) when top-k is off.
+__device__ __forceinline__ uint32_t kth_order(const ProbsArgs& a, int r) { return a.kth_key ? a.kth_key[r] : 0u; }
+// scaled logit x of an entry, or -inf when top-k drops it (x below the k-th largest)
+__device__ __forceinline__ float warped(const ProbsArgs& a, uint32_t kth, float raw) {
   const float x = scaled(a, raw);
-  return a.kth_key && float_order(x) < a.kth_key[r] ? -INFINITY : x;
+  return float_order(x) < kth ? -INFINITY : x;
 }
 
 // ------------------------------------------------------------------ top-k / top-p warping
@@ -1704,6 +1707,7 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_part(ProbsArgs a) {
   const float* lr = a.logits + static_cast<int64_t>(r) * a.ld;
   float v[kPerThread];
   float m = -INFINITY;
+  const uint32_t kth = kth_order(a, r);
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) v[e] = lr[min(x0 + e * kStThreads + static_cast<int>(threadIdx.x), a.n - 1)];
 #pragma unroll
@@ -1711,7 +1715,7 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_part(ProbsArgs a) {
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int x = x0 + e * kStThreads + threadIdx.x;
-    v[e] = x < a.n ? warped(a, r, v[e]) : -INFINITY;
+    v[e] = x < a.n ? warped(a, kth, v[e]) : -INFINITY;
     m = fmaxf(m, v[e]);
   }
   m = wave_max_dpp(m);
@@ -1759,6 +1763,7 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_write(ProbsArgs a) {
   const float M = s_M, S = s_S;
   const float* lr = a.logits + static_cast<int64_t>(r) * a.ld;
   float* orow = a.out + static_cast<int64_t>(r) * a.ld_out;
+  const uint32_t kth = kth_order(a, r);
   float raw[kPerThread];
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) raw[e] = lr[min(x0 + e * kStThreads + static_cast<int>(threadIdx.x), a.n - 1)];
@@ -1767,8 +1772,57 @@ __global__ __launch_bounds__(kStThreads) void k_softmax_write(ProbsArgs a) {
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
     const int x = x0 + e * kStThreads + threadIdx.x;
-    const float v = warped(a, r, raw[e]);
+    const float v = warped(a, kth, raw[e]);
     if (x < a.n) orow[x] = v == -INFINITY ? 0.f : expf(v - M) / S;
+  }
+}
+
+// Rows of at most kSrMax entries (the draft head's 16k trimmed vocabulary): one
+// block per row holds the whole row in registers, so the max, the sum of exp
+// and the probabilities come from one launch and one read of the logits.
+constexpr int kSrThreads = 1024;
+constexpr int kSrMax = 16384;
+__global__ __launch_bounds__(kSrThreads) void k_softmax_row(ProbsArgs a) {
+  constexpr int PER = kSrMax / kSrThreads;
+  constexpr int NW = kSrThreads / kWave;
+  __shared__ float s_m[NW], s_s[NW];
+  const int r = blockIdx.x, t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  const float* lr = a.logits + static_cast<int64_t>(r) * a.ld;
+  const uint32_t kth = kth_order(a, r);
+  float v[PER];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) v[e] = lr[min(e * kSrThreads + t, a.n - 1)];
+#pragma unroll
+  for (int e = 0; e < PER; ++e) pin(v[e]);  // every load in flight at once
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    v[e] = e * kSrThreads + t < a.n ? warped(a, kth, v[e]) : -INFINITY;
+    m = fmaxf(m, v[e]);
+  }
+  m = wave_max_dpp(m);
+  if (lane == 0) s_m[wave] = m;
+  __syncthreads();
+  float M = s_m[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w]);
+  float sum = 0.f;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    v[e] = v[e] == -INFINITY ? 0.f : expf(v[e] - M);  // each exp once, kept for the write
+    sum += v[e];
+  }
+  sum = wave_sum_dpp(sum);
+  if (lane == 0) s_s[wave] = sum;
+  __syncthreads();
+  float S = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) S += s_s[w];
+  float* orow = a.out + static_cast<int64_t>(r) * a.ld_out;
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int x = e * kSrThreads + t;
+    if (x < a.n) orow[x] = v[e] / S;
   }
 }
 
@@ -1938,6 +1992,11 @@ int wc_probs_from_logits(const float* logits, int rows, int n, int64_t ld, float
     hipLaunchKernelGGL(k_topk_key, dim3(rows), dim3(kStThreads), 0, s, a, top_k, keys);
     WC_LAUNCHED();
     a.kth_key = keys;
+  }
+  if (n <= kSrMax && top_p >= 1.f) {  // the draft head's width: one launch, a block per row
+    hipLaunchKernelGGL(k_softmax_row, dim3(rows), dim3(kSrThreads), 0, s, a);
+    WC_LAUNCHED();
+    return WC_OK;
   }
   hipLaunchKernelGGL(k_softmax_part, grid, dim3(kStThreads), 0, s, a);
   WC_LAUNCHED();
