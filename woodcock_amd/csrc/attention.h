@@ -985,6 +985,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   __shared__ __attribute__((aligned(16))) float s_p[QVM][CHK];
   __shared__ float s_m[QVM], s_l[QVM], s_alpha[QVM];
   __shared__ float s_w[QVM][kFxMaxSplits];
+  __shared__ uint8_t s_mk[CPS][QVM][CHK];  // explicit mask bytes of the group's rows, chunk by chunk
   __shared__ bool s_last;
 
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
@@ -1018,6 +1019,16 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
       kreg[c][i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
       vreg[c][i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
     }
+  // with an explicit mask (every chunk of the split in flight: no ring), its
+  // bytes for the group's rows: thread t row t / 32, key t % 32 of each chunk
+  uint8_t mb[CPS];
+  if (a.mask) {
+    const int mr = min(lz0 + (t / CHK) % QVM, a.rows - 1);
+#pragma unroll
+    for (int c = 0; c < CPS; ++c)
+      mb[c] = a.mask[static_cast<int64_t>(mr) * a.mask_ld +
+                     min(static_cast<int64_t>(kb + c * CHK + t % CHK), a.mask_ld - 1)];
+  }
   const int vq = wave, lq = min(lz0 + vq / rep, a.rows - 1), hq = kh * rep + vq % rep;
   HeadVec<D> rq;
   head_vec_load<D>(a.qkv + lq * a.ld_qkv + hq * D, a.q_gain, rq);
@@ -1036,6 +1047,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   const int offset = off_raw + a.offset_add;
   const int T = min(offset + nr, a.cap);
   const int nlast = min(nr, lz0 + rpz);           // rows 0 .. nlast - 1 are visible to this group
+  const int nvis = a.mask ? nr : nlast;           // appended rows the group may see (a mask may show any)
   const int QV = max(0, nlast - lz0) * rep;       // live query vectors of this group
   const int ke = min(T, kb + per);
   const bool live = kb < ke && QV > 0;
@@ -1061,7 +1073,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       const int l = wave + NW * r, tk = offset + l;
-      if (!(l < nlast && tk >= kb && tk < ke)) continue;  // wave-uniform
+      if (!(l < nvis && tk >= kb && tk < ke)) continue;  // wave-uniform
       head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), rk[r]);
       head_vec_norm_rope<D>(rk[r], a.eps);
 #pragma unroll
@@ -1078,6 +1090,10 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
     if (t < QVM) {
       s_m[t] = -INFINITY;
       s_l[t] = 0.f;
+    }
+    if (a.mask && t < QVM * CHK) {
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) s_mk[c][t / CHK][t % CHK] = mb[c];
     }
     __syncthreads();
 
@@ -1101,7 +1117,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
           unpack16<KT>(vreg[c][i], vf);
           if (tt >= offset) {  // appended rows: this launch's values (zero past the group's last row)
             const int l = min(tt - offset, kFxMaxRows - 1);
-            const bool mine = tt - offset < nlast;
+            const bool mine = tt - offset < nvis;
 #pragma unroll
             for (int e = 0; e < VE; ++e) {
               kf[e] = mine ? nks[l][e0 + e] : 0.f;
@@ -1139,7 +1155,9 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
 #pragma unroll
             for (int v = 0; v < QVM; ++v) {
               const int l = lz0 + v / rep;
-              const bool vis = v < QV && j < n && tt <= offset + l && (a.window <= 0 || tt > offset + l - a.window);
+              const bool seen = a.mask ? s_mk[c][v / rep][j] != 0
+                                       : tt <= offset + l && (a.window <= 0 || tt > offset + l - a.window);
+              const bool vis = v < QV && j < n && seen;
               s_p[v][j] = vis ? a.scale * dv[v] : -INFINITY;
             }
           }
@@ -1244,7 +1262,9 @@ static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream)
     if constexpr (D == 128) {
     const int rep = a.H / std::max(a.Hk, 1);
     const int groups = rep >= 1 && rep <= 4 ? (a.rows * rep + 3) / 4 : 0;  // row groups of <= 4 query vectors
-    if (!a.mask && a.ctr && groups >= 1 && a.rows <= kFxMaxRows && a.Hk * groups <= kMaxKvHeads &&
+    // an explicit mask needs every chunk of a split in flight at entry (its bytes are fetched then)
+    const int fx_cps = fx_plan(a.cap, 32).cps;
+    if ((!a.mask || fx_cps <= 4) && a.ctr && groups >= 1 && a.rows <= kFxMaxRows && a.Hk * groups <= kMaxKvHeads &&
         a.ld_out % 4 == 0 && aligned(a.out, 16) &&
         static_cast<size_t>(a.qv_ld) * kMaxSplits * (D + 2) >=
             static_cast<size_t>(groups) * kFxMaxSplits * 4 * kFxRec) {
