@@ -1011,20 +1011,19 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   // 1. in flight at entry: the split's first CPS chunks, the raw q vector of
   // this wave (v = wave) and the raw k / v rows of rows wave + NW i
   uint4 kreg[CPS][NL], vreg[CPS][NL];
-  auto load_chunk = [&](int c) {
+#pragma unroll
+  for (int c = 0; c < CPS; ++c)
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
       const int64_t r = min(static_cast<int64_t>(kb + c * CHK + i * KPB + kr), last_row);
       kreg[c][i] = *reinterpret_cast<const uint4*>(kc + r * D + e0);
       vreg[c][i] = *reinterpret_cast<const uint4*>(vc + r * D + e0);
     }
-  };
-  load_chunk(0);  // the split's later chunks follow the RoPE rows (below), so no wait for those covers them
   // with an explicit mask (every chunk of the split in flight: no ring), its
   // bytes for the group's rows: thread t row t / 32, key t % 32 of each chunk;
   // one register per byte (packing them would wait for the loads here), and
-  // loaded without a branch (without a mask from the offset word, unused), so
-  // no path needs a wait before its registers are written
+  // loaded without a branch (without a mask from the offset word, unused): a
+  // conditional load becomes a select whose other arm waits for the chunk loads
   uint32_t mb[CPS];
   {
     const int mr = min(lz0 + (t / CHK) % QVM, a.rows - 1);
@@ -1064,17 +1063,8 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
       const int pos = a.positions ? a.positions[l] : offset + l;
       return min(max(pos, 0), a.rope_max - 1);
     };
-    // the RoPE rows, then the split's other chunks, then the norms: the
-    // wait for the RoPE rows (in-order counter) covers the first chunk only
-    if (vq < QV) head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(lq), rq);
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-      const int l = wave + NW * r, tk = offset + l;
-      if (l < nvis && tk >= kb && tk < ke) head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), rk[r]);
-    }
-#pragma unroll
-    for (int c = 1; c < CPS; ++c) load_chunk(c);
     if (vq < QV) {
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(lq), rq);
       head_vec_norm_rope<D>(rq, a.eps);
 #pragma unroll
       for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
@@ -1090,6 +1080,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
     for (int r = 0; r < RPW; ++r) {
       const int l = wave + NW * r, tk = offset + l;
       if (!(l < nvis && tk >= kb && tk < ke)) continue;  // wave-uniform
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, row_pos(l), rk[r]);
       head_vec_norm_rope<D>(rk[r], a.eps);
 #pragma unroll
       for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
