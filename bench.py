@@ -448,7 +448,7 @@ def bench_gpu(args):
     # one Qwen3-1.7B target layer over a 60-node draft tree (depth <= 6) at context
     # 2048 with the tree mask, then the greedy tree verify over [60, 151936] logits
     from woodcock_amd.cache import KVCache
-    from woodcock_amd.sampling import tree_attention_mask, DraftTree
+    from woodcock_amd.sampling import DraftTree
     from woodcock_amd.target import TargetConfig, TargetLayer, random_layer
 
     tcfg = TargetConfig()
@@ -467,7 +467,7 @@ def bench_gpu(args):
     tx = torch.randn(60, tcfg.hidden_size, device=out1.device)
     toff = torch.tensor([2048], dtype=torch.int32, device=out1.device)
     tpos = torch.tensor([2048 + dd for dd in depth], dtype=torch.int32, device=out1.device)
-    tmask = torch.from_numpy(tree_attention_mask(tree, 2048).astype(np.uint8)).to(out1.device)
+    tmask = tree_mask_rows(tree, 2048, out1.device)
     tl(tx, tcache, toff, tpos, tmask)  # rope table, workspace touched before capture
 
     def target_layers():
@@ -792,7 +792,7 @@ def pmc_probe2(seed=0):
     from woodcock_amd import _lib
     from woodcock_amd.cache import KVCache
     from woodcock_amd.runtime import ptr, stream_ptr
-    from woodcock_amd.sampling import DraftTree, tree_attention_mask
+    from woodcock_amd.sampling import DraftTree
     from woodcock_amd.target import TargetConfig, TargetLayer, random_layer
 
     cfg, d, ids, rnd, target, init_state, root = build_workload(seed)
@@ -814,7 +814,7 @@ def pmc_probe2(seed=0):
     tx = torch.randn(60, tcfg.hidden_size, device=dev)
     toff = torch.tensor([2048], dtype=torch.int32, device=dev)
     tpos = torch.tensor([2048 + dd for dd in depth], dtype=torch.int32, device=dev)
-    tmask = torch.from_numpy(tree_attention_mask(tree, 2048).astype(np.uint8)).to(dev)
+    tmask = tree_mask_rows(tree, 2048, dev)
     off = init_state[0:1]
     hid_s = torch.empty(1, dm, device=dev)
     x = torch.randn(PROBE_COPY_FLOATS, device=dev)
@@ -878,13 +878,26 @@ def target_chain_only(seed=0, calls=20):
     print(json.dumps({"target_chain_calls": calls}), flush=True)
 
 
+def tree_mask_rows(tree, prefix, device):
+    """The tree attention mask [N, prefix + N] as a row view of a buffer whose
+    rows are padded to 16 bytes -- the layout the tree round's mask buffer has."""
+    import torch
+
+    from woodcock_amd.sampling import tree_attention_mask
+
+    m = torch.from_numpy(tree_attention_mask(tree, prefix).astype(np.uint8))
+    buf = torch.zeros(m.shape[0], (m.shape[1] + 15) // 16 * 16, dtype=torch.uint8, device=device)
+    buf[:, : m.shape[1]] = m.to(device)
+    return buf[:, : m.shape[1]]
+
+
 def target_layer_only(seed=0, calls=45):
     """The config-5 target layer alone (Qwen3-1.7B shape, a 60-node tree of depth
     <= 6 at context 2048 with its mask, bf16 KV), called `calls` times."""
     import torch
 
     from woodcock_amd.cache import KVCache
-    from woodcock_amd.sampling import DraftTree, tree_attention_mask
+    from woodcock_amd.sampling import DraftTree
     from woodcock_amd.target import TargetConfig, TargetLayer, random_layer
 
     dev = torch.device("cuda", 0)
@@ -904,7 +917,7 @@ def target_layer_only(seed=0, calls=45):
     tx = torch.randn(60, tcfg.hidden_size, device=dev)
     toff = torch.tensor([2048], dtype=torch.int32, device=dev)
     tpos = torch.tensor([2048 + dd for dd in depth], dtype=torch.int32, device=dev)
-    tmask = torch.from_numpy(tree_attention_mask(tree, 2048).astype(np.uint8)).to(dev)
+    tmask = tree_mask_rows(tree, 2048, dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()

@@ -109,6 +109,48 @@ def test_target_layer_matches_oracle(cuda, cfg, M, prefix, kv_bf16, tree):
     assert torch.equal(cache.keys[0, :, :prefix], before_k)
 
 
+@pytest.mark.parametrize("cfg,M,prefix", [(SMALL, 7, 42), (SMALL, 60, 300), (FULL, 60, 2048)])
+def test_target_layer_mask_row_stride(cuda, cfg, M, prefix):
+    """The verify attention reads a mask whose rows are 16-byte aligned 16 bytes
+    at a time and any other mask byte by byte: a tree mask given as a row view
+    of a 16-byte-padded buffer gives the same bits as the same mask contiguous
+    (row stride prefix + M), both within the bf16 tolerance of the oracle.  The
+    cache slots past the block hold NaN: the last, partial key chunk of a split
+    must not let them into the outputs."""
+    dev = torch.device("cuda", 0)
+    rng = np.random.default_rng(7 * M + prefix)
+    w = random_layer(cfg, seed=M + prefix + 1, device=dev)
+    layer = TargetLayer(cfg, w, dev)
+    cap = prefix + M + 40
+    cache = KVCache(cfg.num_kv_heads, cfg.head_dim, cap, torch.bfloat16, dev)
+    g = torch.Generator(device=dev).manual_seed(int(rng.integers(1 << 30)))
+    cache.keys[0, :, :prefix] = torch.randn(cache.keys[0, :, :prefix].shape, generator=g, device=dev).bfloat16()
+    cache.values[0, :, :prefix] = torch.randn(cache.values[0, :, :prefix].shape, generator=g, device=dev).bfloat16()
+    cache.keys[0, :, prefix + M:] = float("nan")
+    cache.values[0, :, prefix + M:] = float("nan")
+    k_init, v_init = cache.keys.clone(), cache.values.clone()
+    x = torch.randn(M, cfg.hidden_size, generator=g, device=dev)
+    t = random_tree(M, rng)
+    positions = np.array([prefix + dep for dep in t.depth], np.int32)
+    mask = S.tree_attention_mask(t, prefix).astype(np.uint8)
+    assert mask.shape[1] % 16 != 0
+    pad = torch.zeros(M, (mask.shape[1] + 15) // 16 * 16, dtype=torch.uint8, device=dev)
+    pad[:, : mask.shape[1]] = torch.from_numpy(mask).to(dev)
+    off = torch.tensor([prefix], dtype=torch.int32, device=dev)
+    pos = torch.from_numpy(positions)
+    got = {}
+    for name, m in (("contiguous", torch.from_numpy(mask)), ("padded rows", pad[:, : mask.shape[1]])):
+        cache.keys.copy_(k_init)
+        cache.values.copy_(v_init)
+        got[name] = layer(x.clone(), cache, off, positions=pos, mask=m).cpu().numpy()
+        assert np.isfinite(got[name]).all(), name
+    np.testing.assert_array_equal(got["padded rows"], got["contiguous"])
+    k0 = to_bits(k_init[0])
+    v0 = to_bits(v_init[0])
+    want, _ = oracle_layer(cfg, w, x.cpu().numpy(), k0, v0, True, prefix, positions, mask)
+    assert norm_err(got["padded rows"], want) < 1e-2, norm_err(got["padded rows"], want)
+
+
 def test_target_layer_rejects_bad_shapes(cuda):
     dev = torch.device("cuda", 0)
     layer = TargetLayer(SMALL, random_layer(SMALL, device=dev), dev)

@@ -872,45 +872,70 @@ constexpr int kVaMaxRows = 64;       // rows per launch (mask rows staged per ch
 constexpr int kVaMaxSplits = kMaxSplits;
 constexpr float kLog2e = 1.4426950408889634f;
 
+// One chunk of the split in registers: K as [key][d] (thread t: key t / 16 +
+// 16 i, d chunk t % 16: coalesced); V with lanes along keys (lane l: key
+// l % 32 + 32 (i & 1), d chunk l / 32 + 2 w + 8 (i >> 1)) so that the
+// transposed LDS writes of a wave cover two contiguous 64-byte runs; the mask
+// bytes of row t / 4, keys 16 (t % 4) .. + 16.  Buffer loads at scalar chunk
+// offsets: rows past the capacity read as zeros.
 struct VaChunk {
   uint4 k[4], v[4];
-  uint8_t mb[16];  // mask bytes: this thread's row, keys 16 (t % 4) .. + 16 (packed when staged)
+  uint4 mw;  // the 16 mask bytes (one 16-byte load) or their nonzero bits (byte loads)
 };
 
-// K as [key][d] (thread t: key t / 16 + 16 i, d chunk t % 16: coalesced); V
-// with lanes along keys (lane l: key l % 32 + 32 (i & 1), d chunk l / 32 + 2 w
-// + 8 (i >> 1)) so that the transposed LDS writes of a wave cover two
-// contiguous 64-byte runs; mask bytes of row t / 4, keys 16 (t % 4) .. + 16.
-// Rows clamp into [0, last].
-__device__ __forceinline__ void va_chunk_load(const uint16_t* kc, const uint16_t* vc, int c0, int last,
-                                              const uint8_t* mask, int64_t mask_ld, int nr, int ke, VaChunk& ch) {
-  const int t = threadIdx.x, lane = t % kWave, w = t / kWave;
+// bit e: byte e of w nonzero (bytes spread to bits 0 / 8 / 16 / 24, then
+// gathered by one multiply: byte e's bit lands at 21 + e, no two terms collide)
+__device__ __forceinline__ uint32_t va_nz4(uint32_t w) {
+  const uint32_t h = ((((w & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w) & 0x80808080u) >> 7;
+  return (h * 0x00204081u) >> 21 & 0xfu;
+}
+
+struct VaSrc {
+  __amdgpu_buffer_rsrc_t kr, vr, mr;
+  int kvo, vvo;     // per-thread byte offsets of the K / V loads
+  int mo;           // byte offset of the thread's mask bytes at key 0
+  bool mask_vec;    // mask rows 16-byte aligned: one 16-byte load per chunk
+};
+
+// (the chunk offset rides in the vector offset, which the buffer range check covers)
+template <bool MASK>
+__device__ __forceinline__ void va_chunk_load(const VaSrc& src, int c0, VaChunk& ch) {
+  const int ko = src.kvo + c0 * (kVaD * 2), vo = src.vvo + c0 * (kVaD * 2);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int kj = min(c0 + t / 16 + 16 * i, last);
-    ch.k[i] = *reinterpret_cast<const uint4*>(kc + static_cast<int64_t>(kj) * kVaD + (t % 16) * 8);
-    const int vj = min(c0 + lane % 32 + 32 * (i & 1), last);
-    const int dc = lane / 32 + 2 * w + 8 * (i >> 1);
-    ch.v[i] = *reinterpret_cast<const uint4*>(vc + static_cast<int64_t>(vj) * kVaD + dc * 8);
+    ch.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.kr, ko + i * 16 * (kVaD * 2), 0, 0));
+    ch.v[i] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(src.vr, vo + (i & 1) * 32 * (kVaD * 2) + (i >> 1) * 128, 0, 0));
   }
-  if (mask) {
-    const int r = min(t / 4, max(nr - 1, 0));
-    const uint8_t* mp = mask + static_cast<int64_t>(r) * mask_ld + c0 + (t % 4) * 16;
-    if (c0 + kVaCH <= mask_ld && (reinterpret_cast<uintptr_t>(mp) & 15) == 0) {
-      // one 16-byte load (bytes past ke are masked by the key count later)
-      const uint4 q = *reinterpret_cast<const uint4*>(mp);
-      const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ch.mb[e] = static_cast<uint8_t>(qw[e / 4] >> (8 * (e % 4)));
+  if constexpr (MASK) {
+    const int mo = src.mo + c0;
+    if (src.mask_vec) {
+      ch.mw = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.mr, mo, 0, 0));
     } else {
-      const uint8_t* mr = mask + static_cast<int64_t>(r) * mask_ld;
+      uint32_t b = 0;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) ch.mb[e] = mr[min(c0 + (t % 4) * 16 + e, max(ke - 1, 0))];
+      for (int e = 0; e < 16; ++e) b |= (__builtin_amdgcn_raw_buffer_load_b8(src.mr, mo + e, 0, 0) != 0 ? 1u : 0u) << e;
+      ch.mw = make_uint4(b, 0, 0, 0);
     }
   }
 }
 
-template <int UNUSED = 0>
+template <bool MASK>
+__device__ __forceinline__ uint32_t va_mask_bits(const VaSrc& src, const VaChunk& ch) {
+  if (!src.mask_vec) return ch.mw.x;
+  return va_nz4(ch.mw.x) | va_nz4(ch.mw.y) << 4 | va_nz4(ch.mw.z) << 8 | va_nz4(ch.mw.w) << 12;
+}
+
+// keys [0, k) of a 64-key chunk as bits
+__device__ __forceinline__ uint64_t va_low_bits(int k) {
+  return k >= 64 ? ~0ull : k <= 0 ? 0ull : (1ull << k) - 1;
+}
+
+// MASK: visibility from the explicit mask rows; otherwise causal (and the
+// sliding window).  Split ranges are fixed by the capacity (whole chunks), so a
+// block requests its first chunk before the cache offset arrives; splits past
+// the live keys leave m = -inf, l = 0.
+template <bool MASK>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_verify_attention(AttnArgs a) {
   constexpr int D = kVaD, CH = kVaCH;
   constexpr int nw = kAttnThreads / kWave;
@@ -921,20 +946,27 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x, z = blockIdx.z;
   const int rep = a.H / a.Hk;
-  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
-  const int offset = *a.offset_dev + a.offset_add;
-  const int T = min(offset + nr, a.cap);
-  const int QV = nr * rep, QVb = a.rows * rep;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int dg = (lane / 16) * 8;
-  const uint16_t* kc = static_cast<const uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
-  const uint16_t* vc = static_cast<const uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
-  const int per = ((T + S - 1) / S + CH - 1) / CH * CH;  // whole chunks per split
-  const int kb = min(T, split * per), ke = min(T, kb + per);
-  const int last = max(a.cap - 1, 0);
+  const int per = ((a.cap + S - 1) / S + CH - 1) / CH * CH;  // whole chunks per split
+  const int kb = min(a.cap, split * per);
+  const int QVb = a.rows * rep;
 
-  // q tile (this lane: vector vq, dims 32 st + dg .. + 8) and the first chunk
+  VaSrc src;
+  src.kr = buffer_rsrc(static_cast<const uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
+  src.vr = buffer_rsrc(static_cast<const uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
+  src.kvo = (t / 16) * (D * 2) + (t % 16) * 16;
+  src.vvo = (lane % 32) * (D * 2) + (lane / 32 + 2 * wave) * 16;
+  src.mask_vec = false;
+  src.mo = 0;
+  if constexpr (MASK) {
+    src.mr = buffer_rsrc(a.mask, static_cast<int>(a.rows * a.mask_ld));
+    src.mask_vec = (a.mask_ld & 15) == 0 && (reinterpret_cast<uintptr_t>(a.mask) & 15) == 0;
+    src.mo = static_cast<int>(min(t / 4, a.rows - 1) * a.mask_ld) + (t % 4) * 16;
+  }
+
+  // q tile (this lane: vector vq, dims 32 st + dg .. + 8), then the first chunk
   const int vq = z * kVaGroup + wave * 16 + lane % 16;
   const int vqc = min(vq, QVb - 1);
   const float* qsrc = a.qkv + static_cast<int64_t>(vqc / rep) * a.ld_qkv + (kh * rep + vqc % rep) * D + dg;
@@ -945,29 +977,37 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
     qf[2 * st + 1] = *reinterpret_cast<const float4*>(qsrc + st * 32 + 4);
   }
   VaChunk ch;
-  va_chunk_load(kc, vc, kb, last, a.mask, a.mask_ld, nr, ke, ch);
+  va_chunk_load<MASK>(src, kb, ch);
+  const int nr = a.n_rows_dev ? min(max(*a.n_rows_dev, 0), a.rows) : a.rows;
+  const int offset = *a.offset_dev + a.offset_add;
+  const int T = min(offset + nr, a.cap);
+  const int QV = nr * rep;
+  const int ke = min(T, kb + per);
+  // q scaled by scale * log2(e) before the split: the scores come out in base 2
+  const float sc = a.scale * kLog2e;
   abf16x8 qh[4], ql[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-    const bool lv = vq < QV;
+    const float g = vq < QV ? sc : 0.f;
     const float4 u = qf[2 * st], w = qf[2 * st + 1];
-    const float x[8] = {lv ? u.x : 0.f, lv ? u.y : 0.f, lv ? u.z : 0.f, lv ? u.w : 0.f,
-                        lv ? w.x : 0.f, lv ? w.y : 0.f, lv ? w.z : 0.f, lv ? w.w : 0.f};
+    const float x[8] = {u.x * g, u.y * g, u.z * g, u.w * g, w.x * g, w.y * g, w.z * g, w.w * g};
     split8(x, qh[st], ql[st]);
   }
 
-  // the lane's softmax rows 16 w + 4 (lane / 16) + e: visibility limits in
-  // cache slots (causal and window), or the mask row
-  int lim[4], wlo[4], mrow[4];
+  // the lane's softmax rows 16 w + 4 (lane / 16) + e: live or not, their mask
+  // row, or their causal / window limits in cache slots
+  bool rlive[4];
+  int mrow[4], lim[4], wlo[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int v = z * kVaGroup + wave * 16 + (lane / 16) * 4 + e;
     const int l = min(v, QVb - 1) / rep;
+    rlive[e] = v < QV;
     mrow[e] = l;
-    lim[e] = v < QV ? (a.mask ? 0x7fffffff : offset + l) : -1;
-    wlo[e] = (!a.mask && a.window > 0) ? offset + l - a.window : -0x7fffffff;
+    lim[e] = offset + l;
+    wlo[e] = a.window > 0 ? offset + l - a.window : -0x7fffffff;
   }
-  const float sc = a.scale * kLog2e;
+  const int kl = lane % 16;  // the lane's key within each 16-key tile
   float m_r[4], l_r[4];
   af32x4 o[8];
 #pragma unroll
@@ -979,31 +1019,37 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   for (int dt = 0; dt < 8; ++dt) o[dt] = af32x4{0.f, 0.f, 0.f, 0.f};
   const bool tile_live = z * kVaGroup + wave * 16 < QV;
   float* pw = pb + wave * 16 * kVaLdP;
+  uint16_t* kdst = ksb + (t / 16) * kVaLdK + (t % 16) * 8;
+  const int vj0 = lane % 32, vd0 = (lane / 32 + 2 * wave) * 8;
 
   for (int c0 = kb; c0 < ke; c0 += CH) {
     const int n = min(CH, ke - c0);
     lds_barrier();  // the previous chunk is consumed
+    if (n == CH) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(kdst + 16 * i * kVaLdK) = ch.k[i];
+    } else {
+      // the split's last, partial chunk: V rows past the range zeroed (the
+      // cache there may hold anything; P is 0 for them)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        *reinterpret_cast<uint4*>(kdst + 16 * i * kVaLdK) = ch.k[i];
+        if (vj0 + 32 * (i & 1) >= n) ch.v[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int kj = t / 16 + 16 * i;
-      *reinterpret_cast<uint4*>(ksb + kj * kVaLdK + (t % 16) * 8) = kj < n ? ch.k[i] : make_uint4(0, 0, 0, 0);
-      const int vj = lane % 32 + 32 * (i & 1), d0 = (lane / 32 + 2 * wave + 8 * (i >> 1)) * 8;
-      const uint4 vv = vj < n ? ch.v[i] : make_uint4(0, 0, 0, 0);
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+      const int vj = vj0 + 32 * (i & 1), d0 = vd0 + 64 * (i >> 1);
+      const uint32_t vw[4] = {ch.v[i].x, ch.v[i].y, ch.v[i].z, ch.v[i].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vst[(d0 + 2 * e) * kVaLdT + vj] = static_cast<uint16_t>(vw[e] & 0xffffu);
         vst[(d0 + 2 * e + 1) * kVaLdT + vj] = static_cast<uint16_t>(vw[e] >> 16);
       }
     }
-    if (a.mask) {
-      uint32_t mbits = 0;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mbits |= (ch.mb[e] != 0 ? 1u : 0u) << e;
-      s_mb[t] = static_cast<uint16_t>(mbits);
-    }
+    if constexpr (MASK) s_mb[t] = static_cast<uint16_t>(va_mask_bits<MASK>(src, ch));
     lds_barrier();
-    if (c0 + CH < ke) va_chunk_load(kc, vc, c0 + CH, last, a.mask, a.mask_ld, nr, ke, ch);  // next chunk
+    if (c0 + CH < ke) va_chunk_load<MASK>(src, c0 + CH, ch);  // next chunk
 
     if (tile_live) {
       // S = Q K^T, four independent key tiles
@@ -1016,30 +1062,39 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
           b[kt] = __builtin_bit_cast(
-              abf16x8, *reinterpret_cast<const uint4*>(ksb + (kt * 16 + lane % 16) * kVaLdK + st * 32 + dg));
+              abf16x8, *reinterpret_cast<const uint4*>(ksb + (kt * 16 + kl) * kVaLdK + st * 32 + dg));
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[st], b[kt], sacc[kt], 0, 0, 0);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[st], b[kt], sacc[kt], 0, 0, 0);
+      }
+      // visible keys of each row as 64 bits (key j of the chunk = bit j)
+      const uint64_t nb = va_low_bits(n);
+      uint32_t vlo[4], vhi[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint64_t bits;
+        if constexpr (MASK) {
+          const uint2 mw = *reinterpret_cast<const uint2*>(s_mb + mrow[e] * 4);
+          bits = (static_cast<uint64_t>(mw.y) << 32 | mw.x) & nb;
+        } else {
+          bits = va_low_bits(lim[e] - c0 + 1) & ~va_low_bits(wlo[e] - c0 + 1) & nb;
+        }
+        bits = rlive[e] ? bits : 0ull;
+        vlo[e] = static_cast<uint32_t>(bits);
+        vhi[e] = static_cast<uint32_t>(bits >> 32);
       }
       // lane holds key kt * 16 + lane % 16 of rows 4 (lane / 16) + e
       mfma_settle();
       float p[4][4], alpha[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        uint32_t bits = 0xffffffffu, bits2 = 0xffffffffu;
-        if (a.mask) {
-          const uint2 mw = *reinterpret_cast<const uint2*>(s_mb + mrow[e] * 4);
-          bits = mw.x;
-          bits2 = mw.y;
-        }
         float sv[4];
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const int j = kt * 16 + lane % 16, tk = c0 + j;
-          const uint32_t bw = kt < 2 ? bits : bits2;
-          const bool vis = j < n && tk <= lim[e] && tk > wlo[e] && ((bw >> (j & 31)) & 1u);
-          sv[kt] = vis ? sc * sacc[kt][e] : -INFINITY;
+          const uint32_t bw = kt < 2 ? vlo[e] : vhi[e];
+          const bool vis = __builtin_amdgcn_ubfe(bw, (kt & 1) * 16 + kl, 1) != 0;
+          sv[kt] = vis ? sacc[kt][e] : -INFINITY;
         }
         const float mx = row16_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
         const float m_new = fmaxf(m_r[e], mx);
@@ -1062,14 +1117,14 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pw[((lane / 16) * 4 + e) * kVaLdP + kt * 16 + lane % 16] = p[kt][e];
+        for (int e = 0; e < 4; ++e) pw[((lane / 16) * 4 + e) * kVaLdP + kt * 16 + kl] = p[kt][e];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const float4 u = *reinterpret_cast<const float4*>(pw + (lane % 16) * kVaLdP + kk * 32 + dg);
-        const float4 w = *reinterpret_cast<const float4*>(pw + (lane % 16) * kVaLdP + kk * 32 + dg + 4);
+        const float4 u = *reinterpret_cast<const float4*>(pw + kl * kVaLdP + kk * 32 + dg);
+        const float4 w = *reinterpret_cast<const float4*>(pw + kl * kVaLdP + kk * 32 + dg + 4);
         const float px[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
         abf16x8 ph, pl;
         split8(px, ph, pl);
@@ -1077,7 +1132,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt)
           b[dt] = __builtin_bit_cast(
-              abf16x8, *reinterpret_cast<const uint4*>(vst + (dt * 16 + lane % 16) * kVaLdT + kk * 32 + dg));
+              abf16x8, *reinterpret_cast<const uint4*>(vst + (dt * 16 + kl) * kVaLdT + kk * 32 + dg));
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, b[dt], o[dt], 0, 0, 0);
 #pragma unroll
@@ -1094,8 +1149,8 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
     const int v = z * kVaGroup + wave * 16 + (lane / 16) * 4 + e;
     if (v >= QV) continue;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) part[v * (D + 2) + 2 + dt * 16 + lane % 16] = o[dt][e];
-    if (lane % 16 == 0) {
+    for (int dt = 0; dt < 8; ++dt) part[v * (D + 2) + 2 + dt * 16 + kl] = o[dt][e];
+    if (kl == 0) {
       part[v * (D + 2)] = m_r[e] == -INFINITY ? -INFINITY : m_r[e] / kLog2e;
       part[v * (D + 2) + 1] = l_r[e];
     }
@@ -1107,8 +1162,14 @@ static int launch_verify_attention(const AttnArgs& a, int splits, hipStream_t s)
   WC_REQUIRE(splits >= 1 && splits <= kVaMaxSplits, "verify attention: 1..%d splits", kVaMaxSplits);
   const int qvb = a.rows * (a.H / a.Hk);
   WC_REQUIRE(a.qv_ld >= qvb, "verify attention: partial stride too small");
+  WC_REQUIRE(static_cast<int64_t>(a.cap) * kVaD * 2 < (int64_t{1} << 31) &&
+                 (!a.mask || static_cast<int64_t>(a.rows) * a.mask_ld < (int64_t{1} << 31)),
+             "verify attention: cache or mask too large for 32-bit offsets");
   const unsigned groups = static_cast<unsigned>((qvb + kVaGroup - 1) / kVaGroup);
-  hipLaunchKernelGGL(k_verify_attention<0>, dim3(splits, a.Hk, groups), dim3(kAttnThreads), 0, s, a);
+  if (a.mask)
+    hipLaunchKernelGGL(k_verify_attention<true>, dim3(splits, a.Hk, groups), dim3(kAttnThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL(k_verify_attention<false>, dim3(splits, a.Hk, groups), dim3(kAttnThreads), 0, s, a);
   WC_LAUNCHED();
   hipLaunchKernelGGL((k_attn_merge<kVaD, kVaMaxSplits>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads),
                      0, s, a, splits);

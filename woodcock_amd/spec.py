@@ -539,6 +539,7 @@ class SpeculativeDecoder:
         width = self.n + rows
         if r.target_cache is not None:
             width = max(width, r.target_cache[0].capacity)
+        width = (width + 15) // 16 * 16  # 16-byte mask rows: the verify attention reads them 16 bytes at a time
         if self._tree_mask is None or self._tree_mask.shape[1] < width:
             self._tree_mask = torch.zeros(_lib.WC_MAX_NODES, width, dtype=torch.uint8, device=self.d.device)
         mask = self._tree_mask[:rows]

@@ -138,15 +138,26 @@ class TargetLayer:
         cos, sin = self.rope(cache.capacity + 64)
         pos = None if positions is None else positions.to(self.device, torch.int32).contiguous()
         if mask is not None:
-            mask = mask.to(self.device, torch.uint8).contiguous()
-            if mask.shape[0] != rows:
-                raise ValueError("mask must have one row per input row")
+            mask = _mask_rows(mask, self.device, rows)
         _lib.call("wc_target_layer", C.byref(self.dims), C.byref(self.lw), ptr(cos), ptr(sin), cos.shape[0], ptr(x),
                   rows, ptr(pos) if pos is not None else None, ptr(mask) if mask is not None else None,
                   mask.stride(0) if mask is not None else 0, ptr(cache.keys), ptr(cache.values),
                   _lib.WC_BF16 if cache.keys.dtype == torch.bfloat16 else _lib.WC_F32, cache.capacity,
                   ptr(offset_dev), None, 0, ptr(self.ws), stream_ptr())
         return x
+
+
+def _mask_rows(mask: torch.Tensor, device: torch.device, rows: int) -> torch.Tensor:
+    """The [rows, >= offset + rows] uint8 mask as the layer reads it: rows may
+    be strided (a row view of a wider buffer is used in place, and a row stride
+    that is a multiple of 16 bytes lets the attention read 16 mask bytes at a
+    time); anything else is copied."""
+    mask = mask.to(device, torch.uint8)
+    if mask.dim() != 2 or mask.shape[0] != rows:
+        raise ValueError("mask must have one row per input row")
+    if mask.stride(1) != 1 or mask.stride(0) < mask.shape[1]:
+        mask = mask.contiguous()
+    return mask
 
 
 def default_feature_layers(num_layers: int) -> tuple[int, int, int]:
@@ -271,9 +282,7 @@ class TargetModel:
         cos, sin = self.rope(cap + 64)
         pos = None if positions is None else positions.to(self.device, torch.int32).contiguous()
         if mask is not None:
-            mask = mask.to(self.device, torch.uint8).contiguous()
-            if mask.shape[0] != rows:
-                raise ValueError("mask must have one row per token")
+            mask = _mask_rows(mask, self.device, rows)
         kvdt = _lib.WC_BF16 if cache[0].keys.dtype == torch.bfloat16 else _lib.WC_F32
         x = self.x[:rows]
         s = stream_ptr()
