@@ -866,7 +866,6 @@ constexpr int kVaD = 128;  // head_dim of the verify-width path
 constexpr int kVaCH = 64;            // keys per chunk
 constexpr int kVaLdK = kVaD + 8;     // row stride (bf16) of the K chunk: B-fragment reads spread over the banks
 constexpr int kVaLdT = kVaCH + 8;    // row stride (bf16) of the transposed V chunk
-constexpr int kVaLdP = kVaCH + 4;    // row stride (fp32) of a wave's P tile
 constexpr int kVaGroup = 64;         // query vectors per block
 constexpr int kVaMaxRows = 64;       // rows per launch (mask rows staged per chunk)
 constexpr int kVaMaxSplits = kMaxSplits;
@@ -938,8 +937,6 @@ __device__ __forceinline__ uint64_t va_low_bits(int k) {
 template <bool MASK>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_verify_attention(AttnArgs a) {
   constexpr int D = kVaD, CH = kVaCH;
-  constexpr int nw = kAttnThreads / kWave;
-  __shared__ __attribute__((aligned(16))) float pb[nw * 16 * kVaLdP];  // per-wave P tiles
   __shared__ __attribute__((aligned(16))) uint16_t ksb[CH * kVaLdK];   // [key][d]
   __shared__ __attribute__((aligned(16))) uint16_t vst[D * kVaLdT];    // [d][key]
   __shared__ __attribute__((aligned(16))) uint16_t s_mb[kVaMaxRows * 4];  // mask bits [row][key / 16]
@@ -994,31 +991,25 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
     split8(x, qh[st], ql[st]);
   }
 
-  // the lane's softmax rows 16 w + 4 (lane / 16) + e: live or not, their mask
-  // row, or their causal / window limits in cache slots
-  bool rlive[4];
-  int mrow[4], lim[4], wlo[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int v = z * kVaGroup + wave * 16 + (lane / 16) * 4 + e;
-    const int l = min(v, QVb - 1) / rep;
-    rlive[e] = v < QV;
-    mrow[e] = l;
-    lim[e] = offset + l;
-    wlo[e] = a.window > 0 ? offset + l - a.window : -0x7fffffff;
-  }
-  const int kl = lane % 16;  // the lane's key within each 16-key tile
-  float m_r[4], l_r[4];
+  // S^T = K Q^T per 16-key tile: lane l holds query vector q = l % 16 of the
+  // wave's 16 (its softmax row: live or not, mask row, causal / window limits)
+  // and keys 16 kt + 4 g + e of the chunk (g = l / 16); the four lane groups
+  // share a row, so its max and sum are the lane's 16 values then two
+  // cross-group shuffles.  P^T then feeds O^T = V^T P^T straight from the
+  // lane's registers: the MFMA's k slots 8 g .. 8 g + 7 of key block kk take
+  // keys 32 kk + 4 g + {0..3} and 32 kk + 16 + 4 g + {0..3}, and the V^T
+  // fragments are read from the transposed chunk in that same key order.
+  const int kl = lane % 16, gq = lane / 16;
+  const int vrow = z * kVaGroup + wave * 16 + kl;
+  const bool rlive = vrow < QV;
+  const int mrow = min(vrow, QVb - 1) / rep;
+  const int lim = offset + mrow;
+  const int wlo = a.window > 0 ? offset + mrow - a.window : -0x7fffffff;
+  float m_r = -INFINITY, l_r = 0.f;
   af32x4 o[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    m_r[e] = -INFINITY;
-    l_r[e] = 0.f;
-  }
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = af32x4{0.f, 0.f, 0.f, 0.f};
   const bool tile_live = z * kVaGroup + wave * 16 < QV;
-  float* pw = pb + wave * 16 * kVaLdP;
   uint16_t* kdst = ksb + (t / 16) * kVaLdK + (t % 16) * 8;
   const int vj0 = lane % 32, vd0 = (lane / 32 + 2 * wave) * 8;
 
@@ -1052,7 +1043,7 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
     if (c0 + CH < ke) va_chunk_load<MASK>(src, c0 + CH, ch);  // next chunk
 
     if (tile_live) {
-      // S = Q K^T, four independent key tiles
+      // S^T, four independent key tiles (K fragments as A, q as B)
       af32x4 sacc[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) sacc[kt] = af32x4{0.f, 0.f, 0.f, 0.f};
@@ -1064,97 +1055,89 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
           b[kt] = __builtin_bit_cast(
               abf16x8, *reinterpret_cast<const uint4*>(ksb + (kt * 16 + kl) * kVaLdK + st * 32 + dg));
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qh[st], b[kt], sacc[kt], 0, 0, 0);
+        for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[kt], qh[st], sacc[kt], 0, 0, 0);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ql[st], b[kt], sacc[kt], 0, 0, 0);
+        for (int kt = 0; kt < 4; ++kt) sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[kt], ql[st], sacc[kt], 0, 0, 0);
       }
-      // visible keys of each row as 64 bits (key j of the chunk = bit j)
-      const uint64_t nb = va_low_bits(n);
-      uint32_t vlo[4], vhi[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint64_t bits;
-        if constexpr (MASK) {
-          const uint2 mw = *reinterpret_cast<const uint2*>(s_mb + mrow[e] * 4);
-          bits = (static_cast<uint64_t>(mw.y) << 32 | mw.x) & nb;
-        } else {
-          bits = va_low_bits(lim[e] - c0 + 1) & ~va_low_bits(wlo[e] - c0 + 1) & nb;
-        }
-        bits = rlive[e] ? bits : 0ull;
-        vlo[e] = static_cast<uint32_t>(bits);
-        vhi[e] = static_cast<uint32_t>(bits >> 32);
+      // the row's visible keys of this chunk (key j = bit j), then the lane's
+      // four 4-key runs 16 kt + 4 g ..
+      uint64_t bits;
+      if constexpr (MASK) {
+        const uint2 mw = *reinterpret_cast<const uint2*>(s_mb + mrow * 4);
+        bits = static_cast<uint64_t>(mw.y) << 32 | mw.x;
+      } else {
+        bits = va_low_bits(lim - c0 + 1) & ~va_low_bits(wlo - c0 + 1);
       }
-      // lane holds key kt * 16 + lane % 16 of rows 4 (lane / 16) + e
+      bits = rlive ? bits & va_low_bits(n) : 0ull;
+      const uint32_t blo = static_cast<uint32_t>(bits), bhi = static_cast<uint32_t>(bits >> 32);
       mfma_settle();
-      float p[4][4], alpha[4];
+      float sv[4][4];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float sv[4];
+      for (int kt = 0; kt < 4; ++kt) {
+        const uint32_t nib = __builtin_amdgcn_ubfe(kt < 2 ? blo : bhi, (kt & 1) * 16 + 4 * gq, 4);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          const uint32_t bw = kt < 2 ? vlo[e] : vhi[e];
-          const bool vis = __builtin_amdgcn_ubfe(bw, (kt & 1) * 16 + kl, 1) != 0;
-          sv[kt] = vis ? sacc[kt][e] : -INFINITY;
+        for (int e = 0; e < 4; ++e) {
+          sv[kt][e] = (nib >> e) & 1u ? sacc[kt][e] : -INFINITY;
+          mx = fmaxf(mx, sv[kt][e]);
         }
-        const float mx = row16_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
-        const float m_new = fmaxf(m_r[e], mx);
-        const float mb = m_new == -INFINITY ? 0.f : m_new;  // all hidden so far: exp2(-inf) = 0 below
-        alpha[e] = __builtin_amdgcn_exp2f(m_r[e] - mb);
-        float rs = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-          p[kt][e] = __builtin_amdgcn_exp2f(sv[kt] - mb);
-          rs += p[kt][e];
-        }
-        l_r[e] = l_r[e] * alpha[e] + row16_sum(rs);
-        m_r[e] = m_new;
       }
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[dt][e] *= alpha[e];
-      // P through the wave's LDS tile into the A layout (row lane % 16, keys 32 kk + dg ..)
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_r, mx);
+      const float mb = m_new == -INFINITY ? 0.f : m_new;  // all hidden so far: exp2(-inf) = 0 below
+      const float alpha = __builtin_amdgcn_exp2f(m_r - mb);
+      float p[4][4], rs = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pw[((lane / 16) * 4 + e) * kVaLdP + kt * 16 + kl] = p[kt][e];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        for (int e = 0; e < 4; ++e) {
+          p[kt][e] = __builtin_amdgcn_exp2f(sv[kt][e] - mb);
+          rs += p[kt][e];
+        }
+      rs += __shfl_xor(rs, 16);
+      rs += __shfl_xor(rs, 32);
+      l_r = l_r * alpha + rs;
+      m_r = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[dt][e] *= alpha;
+      // O^T += V^T P^T over the two 32-key blocks
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const float4 u = *reinterpret_cast<const float4*>(pw + kl * kVaLdP + kk * 32 + dg);
-        const float4 w = *reinterpret_cast<const float4*>(pw + kl * kVaLdP + kk * 32 + dg + 4);
-        const float px[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+        const float px[8] = {p[2 * kk][0], p[2 * kk][1], p[2 * kk][2], p[2 * kk][3],
+                             p[2 * kk + 1][0], p[2 * kk + 1][1], p[2 * kk + 1][2], p[2 * kk + 1][3]};
         abf16x8 ph, pl;
         split8(px, ph, pl);
-        abf16x8 b[8];
+        abf16x8 va[8];
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt)
-          b[dt] = __builtin_bit_cast(
-              abf16x8, *reinterpret_cast<const uint4*>(vst + (dt * 16 + kl) * kVaLdT + kk * 32 + dg));
+        for (int dt = 0; dt < 8; ++dt) {
+          const uint16_t* vp = vst + (dt * 16 + kl) * kVaLdT + kk * 32 + 4 * gq;
+          const uint2 r0 = *reinterpret_cast<const uint2*>(vp);
+          const uint2 r1 = *reinterpret_cast<const uint2*>(vp + 16);
+          va[dt] = __builtin_bit_cast(abf16x8, make_uint4(r0.x, r0.y, r1.x, r1.y));
+        }
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, b[dt], o[dt], 0, 0, 0);
+        for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], ph, o[dt], 0, 0, 0);
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, b[dt], o[dt], 0, 0, 0);
+        for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pl, o[dt], 0, 0, 0);
       }
     }
   }
 
-  // this split's (m, l, o) per query vector; m back to natural units
+  // this split's (m, l, o) per query vector (lane: dims 16 dt + 4 g .. + 4 of
+  // vector vrow); m back to natural units
   mfma_settle();
-  float* part = a.partial + (static_cast<int64_t>(kh) * S + split) * a.qv_ld * (D + 2);
+  if (!rlive) return;
+  float* part = a.partial + ((static_cast<int64_t>(kh) * S + split) * a.qv_ld + vrow) * (D + 2);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int v = z * kVaGroup + wave * 16 + (lane / 16) * 4 + e;
-    if (v >= QV) continue;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) part[v * (D + 2) + 2 + dt * 16 + kl] = o[dt][e];
-    if (kl == 0) {
-      part[v * (D + 2)] = m_r[e] == -INFINITY ? -INFINITY : m_r[e] / kLog2e;
-      part[v * (D + 2) + 1] = l_r[e];
-    }
+  for (int dt = 0; dt < 8; ++dt) {
+    float2* pp = reinterpret_cast<float2*>(part + 2 + dt * 16 + 4 * gq);
+    pp[0] = make_float2(o[dt][0], o[dt][1]);
+    pp[1] = make_float2(o[dt][2], o[dt][3]);
   }
+  if (gq == 0) *reinterpret_cast<float2*>(part) = make_float2(m_r == -INFINITY ? -INFINITY : m_r / kLog2e, l_r);
 }
 
 static int launch_verify_attention(const AttnArgs& a, int splits, hipStream_t s) {
