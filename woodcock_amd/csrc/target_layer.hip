@@ -1360,9 +1360,17 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     at.out = ws.attn;
     at.ld_out = nq;
     at.xa_out = ws.xa_attn;
-    // about two chunks of keys per split (one chunk per split measured no faster:
-    // the split's fixed costs dominate, and the merge then reads twice the partials)
-    const int vsplits = std::max(1, std::min(kVaMaxSplits, (capacity + 2 * kVaCH - 1) / (2 * kVaCH)));
+    // the fewest chunks per split (at least two) that keep the grid within one
+    // block per CU: one chunk per split measured slower (the split's fixed costs
+    // dominate and the merge reads twice the partials), and CUs given a second
+    // block set the launch's tail
+    int cus = 0;
+    if (int rc = device_cus(&cus)) return rc;
+    const int groups = (rows * rep + kVaGroup - 1) / kVaGroup;
+    const int chunks = (capacity + kVaCH - 1) / kVaCH;
+    const int slots = std::max(1, cus / (Hk * groups));
+    const int cps = std::max(2, (chunks + slots - 1) / slots);
+    const int vsplits = std::max(1, std::min(kVaMaxSplits, (chunks + cps - 1) / cps));
     if (int rc = launch_verify_attention(at, vsplits, s)) return rc;
   } else {
     // other head sizes / an fp32 cache: the decode attention over tiles of rows
