@@ -111,12 +111,12 @@ def test_target_layer_matches_oracle(cuda, cfg, M, prefix, kv_bf16, tree):
 
 @pytest.mark.parametrize("cfg,M,prefix", [(SMALL, 7, 42), (SMALL, 60, 300), (FULL, 60, 2048)])
 def test_target_layer_mask_row_stride(cuda, cfg, M, prefix):
-    """The verify attention reads a mask whose rows are 16-byte aligned 16 bytes
-    at a time and any other mask byte by byte: a tree mask given as a row view
-    of a 16-byte-padded buffer gives the same bits as the same mask contiguous
-    (row stride prefix + M), both within the bf16 tolerance of the oracle.  The
-    cache slots past the block hold NaN: the last, partial key chunk of a split
-    must not let them into the outputs."""
+    """The verify attention reads mask rows that are 16-byte aligned 16 bytes at
+    a time and any other mask byte by byte: the same tree mask contiguous (row
+    stride prefix + M), as a row view of a 16-byte-padded buffer, and as a view
+    one byte into a buffer gives the same bits, within the bf16 tolerance of the
+    oracle.  The cache slots past the block hold NaN: the last, partial key
+    chunk of a split must not let them into the outputs."""
     dev = torch.device("cuda", 0)
     rng = np.random.default_rng(7 * M + prefix)
     w = random_layer(cfg, seed=M + prefix + 1, device=dev)
@@ -136,15 +136,20 @@ def test_target_layer_mask_row_stride(cuda, cfg, M, prefix):
     assert mask.shape[1] % 16 != 0
     pad = torch.zeros(M, (mask.shape[1] + 15) // 16 * 16, dtype=torch.uint8, device=dev)
     pad[:, : mask.shape[1]] = torch.from_numpy(mask).to(dev)
+    odd = torch.zeros(M, mask.shape[1] + 1, dtype=torch.uint8, device=dev)
+    odd[:, 1:] = torch.from_numpy(mask).to(dev)
+    assert odd[:, 1:].data_ptr() % 16 != 0
     off = torch.tensor([prefix], dtype=torch.int32, device=dev)
     pos = torch.from_numpy(positions)
     got = {}
-    for name, m in (("contiguous", torch.from_numpy(mask)), ("padded rows", pad[:, : mask.shape[1]])):
+    for name, m in (("contiguous", torch.from_numpy(mask)), ("padded rows", pad[:, : mask.shape[1]]),
+                    ("unaligned base", odd[:, 1:])):
         cache.keys.copy_(k_init)
         cache.values.copy_(v_init)
         got[name] = layer(x.clone(), cache, off, positions=pos, mask=m).cpu().numpy()
         assert np.isfinite(got[name]).all(), name
     np.testing.assert_array_equal(got["padded rows"], got["contiguous"])
+    np.testing.assert_array_equal(got["unaligned base"], got["contiguous"])
     k0 = to_bits(k_init[0])
     v0 = to_bits(v_init[0])
     want, _ = oracle_layer(cfg, w, x.cpu().numpy(), k0, v0, True, prefix, positions, mask)

@@ -465,8 +465,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attention(AttnArgs a) {
   }
 }
 
-// Merge the splits: one block per (vector, kv head).  Every load -- the
-// splits' (m, l) and this vector's partial outputs -- is issued up front from
+// Merge the splits: one block per (vector, kv head), of kAttnThreads threads
+// or of D >= 64 threads (thread t < D writes dim t).  Every load -- the splits'
+// (m, l) and this vector's partial outputs -- is issued up front from
 // addresses that do not depend on the row count; the block then exits if its
 // vector is past the live rows.  Runs after k_attention (stream order), so
 // plain loads see the partials.
@@ -515,6 +516,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_merge(AttnArgs a, int S) 
       a.xa_out[xa_index(l, h * D + t, 1)] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(y - static_cast<float>(hi)));
     }
   }
+}
+
+// The merge launch: one thread per output dim where D fills whole waves, one
+// load per split slot (16 slots when they cover the splits).
+template <int D>
+static void launch_merge(const AttnArgs& a, int qvb, int splits, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(qvb), a.Hk), block(D >= kWave && D % kWave == 0 ? D : kAttnThreads);
+  if (splits <= 16)
+    hipLaunchKernelGGL((k_attn_merge<D, 16>), grid, block, 0, stream, a, splits);
+  else
+    hipLaunchKernelGGL((k_attn_merge<D>), grid, block, 0, stream, a, splits);
 }
 
 // ------------------------------------------------------------------ decode-width attention
@@ -1302,8 +1314,7 @@ static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream)
       }
       WC_LAUNCHED();
       if (qvb <= 4 && a.ctr) return WC_OK;
-      hipLaunchKernelGGL((k_attn_merge<D>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, stream,
-                         a, splits);
+      launch_merge<D>(a, qvb, splits, stream);
       WC_LAUNCHED();
       return WC_OK;
     }
@@ -1317,8 +1328,7 @@ static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream)
   }
   hipLaunchKernelGGL((k_attention<D, KT>), dim3(splits, a.Hk), dim3(kAttnThreads), lds, stream, a);
   WC_LAUNCHED();
-  hipLaunchKernelGGL((k_attn_merge<D>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads), 0, stream, a,
-                     splits);
+  launch_merge<D>(a, qvb, splits, stream);
   WC_LAUNCHED();
   return WC_OK;
 }

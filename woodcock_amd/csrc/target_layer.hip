@@ -1154,8 +1154,7 @@ static int launch_verify_attention(const AttnArgs& a, int splits, hipStream_t s)
   else
     hipLaunchKernelGGL(k_verify_attention<false>, dim3(splits, a.Hk, groups), dim3(kAttnThreads), 0, s, a);
   WC_LAUNCHED();
-  hipLaunchKernelGGL((k_attn_merge<kVaD, kVaMaxSplits>), dim3(static_cast<unsigned>(qvb), a.Hk), dim3(kAttnThreads),
-                     0, s, a, splits);
+  launch_merge<kVaD>(a, qvb, splits, s);
   WC_LAUNCHED();
   return WC_OK;
 }
