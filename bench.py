@@ -764,8 +764,7 @@ PHASES = {
     "update pass (5 rows, 3 live)": [
         ("greedy verify of [5, 151936] fp32 logits + fuse 2048 x 6144, one launch", 5 * 151936 * 4 + _D * 3 * _D * 2),
         ("QKV, two streams", 2 * (_HD + 2 * _HKV * 128) * _D * 2),
-        ("attention, 3 rows", 2 * 515 * _HKV * 128 * 2),
-        ("attention merge", 0),
+        ("attention, 3 rows (row groups, merged in the launch)", 2 * 515 * _HKV * 128 * 2),
         ("o_proj", _D * _HD * 2),
         ("gate / up", 2 * _F * _D * 2),
         ("down", _D * _F * 2)],
@@ -773,8 +772,8 @@ PHASES = {
         ("input -> fragment-order bf16 hi / lo", 60 * _D * 4 + 60 * _D * 4),
         ("QKV 4096 x 2048, K split", (_HD + 2 * _HKV * 128) * _D * 2),
         ("QKV fix-up (+ q/k norm, RoPE, K/V append)", 0),
-        ("tree attention, 2048 + 60 keys", 2 * 2108 * _HKV * 128 * 2),
-        ("attention merge", 0),
+        ("tree attention, 2048 + 60 keys, 16-byte mask rows", 2 * 2108 * _HKV * 128 * 2),
+        ("attention merge (11 splits)", 0),
         ("o_proj 2048 x 2048, K split", _D * _HD * 2),
         ("o_proj fix-up (+ residual, next activations)", 0),
         ("gate / up 2 x 6144 x 2048, K unsplit, SiLU * up and next activations in the block", 2 * _F * _D * 2),
@@ -971,6 +970,33 @@ def pmc_summary2(fetch_dir, write_dir, mfma_dir):
             work, algo = table[j]
             ratio = f"{(fb + wb) / algo:.3f}" if algo else ""
             lines.append(f"| {title} | `{short}` | {work} | {algo or ''} | {fb + wb:.0f} | {ratio} | {util:.1f} |")
+    print("\n".join(lines))
+
+
+def pmc_valu_summary(valu_dir):
+    """VALU busy per launch of the pmc_probe2 phases: 100 x SQ_ACTIVE_INST_VALU x 4
+    cycles / 1024 SIMDs / (GRBM_GUI_ACTIVE / 8 XCDs), as a markdown table."""
+    def phases(counter):
+        disp = _per_dispatch(_counter_rows(valu_dir), counter)
+        order = sorted(disp)
+        names = [disp[i][0] for i in order]
+        vals = [disp[i][1] for i in order]
+        marks = [i for i, n in enumerate(names) if "abs" in n.lower() and "kernel" in n.lower()]
+        if len(marks) != 5:
+            raise SystemExit(f"{counter}: expected 5 phase markers, found {len(marks)}")
+        return [list(zip(names[a + 1:b], vals[a + 1:b])) for a, b in zip(marks, marks[1:])]
+
+    valu, gui = phases("SQ_ACTIVE_INST_VALU"), phases("GRBM_GUI_ACTIVE")
+    lines = ["| Phase | Kernel | Work | VALU busy % |", "|---|---|---|---:|"]
+    for (title, table), V, G in zip(PHASES.items(), valu, gui):
+        per = len(table)
+        reps = len(V) // per
+        for j in range(per):
+            idx = [j + r * per for r in range(reps) if j + r * per < len(V)]
+            name = V[idx[0]][0]
+            short = name if len(name) < 60 else name[:57] + "..."
+            busy = 100.0 * 4.0 * np.mean([V[i][1] for i in idx]) / 1024.0 / max(np.mean([G[i][1] for i in idx]) / 8.0, 1.0)
+            lines.append(f"| {title} | `{short}` | {table[j][0]} | {busy:.1f} |")
     print("\n".join(lines))
 
 
@@ -1281,11 +1307,16 @@ def main():
                     help="print the cold / warm split of our kernels in a rocprofv3 kernel trace")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="summarise a rocprofv3 kernel trace of --round-only (no GPU needed); --steps as in that run")
+    ap.add_argument("--pmc-valu-summary", metavar="VALU_DIR",
+                    help="summarise the VALU-busy counter pass over --pmc-probe2 (no GPU needed)")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 counter passes over --pmc-probe (no GPU needed)")
     args = ap.parse_args()
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary)
+        return
+    if args.pmc_valu_summary:
+        pmc_valu_summary(args.pmc_valu_summary)
         return
     if args.pmc_summary2:
         pmc_summary2(*args.pmc_summary2)
