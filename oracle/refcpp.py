@@ -17,20 +17,21 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_ref" / "libwcref.so"
+# the same runtime with woodcock_amd/backends/hip_ops.cpp in its backend slot
+HIP_LIB_PATH = HERE / "_ref" / "libwcref_hip.so"
 
-_lib = None
+_libs: dict[str, C.CDLL] = {}
 P = C.c_void_p
 
 
-def available() -> bool:
-    return LIB_PATH.exists()
+def available(path: Path = LIB_PATH) -> bool:
+    return Path(path).exists()
 
 
-def lib():
-    global _lib
-    if _lib is None:
-        _lib = C.CDLL(str(LIB_PATH))
-        L = _lib
+def lib(path: Path | None = None):
+    key = str(LIB_PATH if path is None else path)
+    if key not in _libs:
+        L = C.CDLL(key)
         L.wcref_last_error.restype = C.c_char_p
         L.wcref_drafter_open.argtypes = [C.c_char_p, C.POINTER(C.c_void_p)]
         L.wcref_drafter_close.argtypes = [P]
@@ -61,12 +62,13 @@ def lib():
         L.wcref_qwen3_close.argtypes = [P]
         L.wcref_qwen3_cache_new.argtypes = [P, C.POINTER(C.c_void_p)]
         L.wcref_qwen3_forward.argtypes = [P, P, C.c_int, P, P, P, P, P]
-    return _lib
+        _libs[key] = L
+    return _libs[key]
 
 
-def _check(rc: int) -> None:
+def _check(rc: int, L=None) -> None:
     if rc != 0:
-        raise RuntimeError(lib().wcref_last_error().decode())
+        raise RuntimeError((L or lib()).wcref_last_error().decode())
 
 
 def _p(a):
@@ -99,18 +101,19 @@ def write_drafter_dir(path: Path, cfg: dict, weights: dict[str, np.ndarray]) -> 
 class RefDrafter:
     """The reference C++ Drafter (include/woodcock/drafter.h:48-58) over a temp dir."""
 
-    def __init__(self, cfg: dict, weights: dict[str, np.ndarray]):
+    def __init__(self, cfg: dict, weights: dict[str, np.ndarray], lib_path: Path | None = None):
         self.cfg = cfg
+        self.L = lib(lib_path)
         self._tmp = tempfile.TemporaryDirectory()
         write_drafter_dir(Path(self._tmp.name), cfg, weights)
         h = C.c_void_p()
-        _check(lib().wcref_drafter_open(self._tmp.name.encode(), C.byref(h)))
+        _check(self.L.wcref_drafter_open(self._tmp.name.encode(), C.byref(h)), self.L)
         self.h = h
         self.head_rows = weights["lm_head.weight"].shape[0]
 
     def close(self):
         if self.h:
-            lib().wcref_drafter_close(self.h)
+            self.L.wcref_drafter_close(self.h)
             self.h = None
         self._tmp.cleanup()
 
@@ -122,15 +125,15 @@ class RefDrafter:
 
     def make_cache(self) -> "RefCache":
         h = C.c_void_p()
-        _check(lib().wcref_drafter_cache_new(self.h, C.byref(h)))
-        return RefCache(h, self.cfg["num_layers"], self.cfg["num_kv_heads"] * self.cfg["head_dim"])
+        _check(self.L.wcref_drafter_cache_new(self.h, C.byref(h)), self.L)
+        return RefCache(h, self.cfg["num_layers"], self.cfg["num_kv_heads"] * self.cfg["head_dim"], self.L)
 
     def fuse(self, taps) -> np.ndarray:
         ts = [_f32(t).reshape(-1, self.cfg["target_hidden_size"]) for t in taps]
         L = ts[0].shape[0]
         arr = (C.c_void_p * len(ts))(*[t.ctypes.data for t in ts])
         g = np.empty((L, self.cfg["hidden_size"]), dtype=np.float32)
-        _check(lib().wcref_drafter_fuse(self.h, arr, len(ts), L, _p(g)))
+        _check(self.L.wcref_drafter_fuse(self.h, arr, len(ts), L, _p(g)), self.L)
         return g
 
     def forward(self, tokens, feat, cache: "RefCache", positions=None, mask=None):
@@ -141,7 +144,7 @@ class RefDrafter:
         m = None if mask is None else np.ascontiguousarray(mask, dtype=np.uint8)
         hid = np.empty_like(f)
         out = np.empty_like(f)
-        _check(lib().wcref_drafter_forward(self.h, _p(tok), L, _p(f), cache.h, _p(pos), _p(m), _p(hid), _p(out)))
+        _check(self.L.wcref_drafter_forward(self.h, _p(tok), L, _p(f), cache.h, _p(pos), _p(m), _p(hid), _p(out)), self.L)
         return hid, out
 
     def logits(self, out) -> np.ndarray:
@@ -149,50 +152,60 @@ class RefDrafter:
         z = np.empty((o.shape[0], self.cfg["vocab_size"]), dtype=np.float32)
         for r in range(o.shape[0]):
             row = np.ascontiguousarray(o[r])
-            _check(lib().wcref_drafter_logits(self.h, _p(row), _p(z[r])))
+            _check(self.L.wcref_drafter_logits(self.h, _p(row), _p(z[r])), self.L)
         return z[:, : self.head_rows]
 
 
 class RefCache:
     """The reference KVCache (include/woodcock/cache.h:9-28): [T][kv_heads*head_dim] fp32 per layer."""
 
-    def __init__(self, h, layers: int, row: int):
+    def __init__(self, h, layers: int, row: int, L=None):
         self.h, self.layers, self.row = h, layers, row
+        self.L = L or lib()
 
     @classmethod
-    def new(cls, layers: int, kv_heads: int, head_dim: int) -> "RefCache":
+    def new(cls, layers: int, kv_heads: int, head_dim: int, lib_path: Path | None = None) -> "RefCache":
+        L = lib(lib_path)
         h = C.c_void_p()
-        _check(lib().wcref_cache_new(layers, kv_heads, head_dim, C.byref(h)))
-        return cls(h, layers, kv_heads * head_dim)
+        _check(L.wcref_cache_new(layers, kv_heads, head_dim, C.byref(h)), L)
+        return cls(h, layers, kv_heads * head_dim, L)
 
     def __del__(self):  # pragma: no cover
         try:
             if self.h:
-                lib().wcref_cache_free(self.h)
+                self.L.wcref_cache_free(self.h)
         except Exception:
             pass
 
     @property
     def size(self) -> int:
-        return int(lib().wcref_cache_size(self.h))
+        return int(self.L.wcref_cache_size(self.h))
+
+    @property
+    def offset(self) -> int:
+        return self.size
+
+    @offset.setter
+    def offset(self, n: int) -> None:
+        self.trim_to(n)
 
     def append(self, layer: int, k, v, L: int):
-        _check(lib().wcref_cache_append(self.h, layer, _p(_f32(k)), _p(_f32(v)), L))
+        _check(self.L.wcref_cache_append(self.h, layer, _p(_f32(k)), _p(_f32(v)), L), self.L)
 
     def commit(self, L: int):
-        lib().wcref_cache_commit(self.h, L)
+        self.L.wcref_cache_commit(self.h, L)
 
     def trim_to(self, n: int):
-        lib().wcref_cache_trim_to(self.h, n)
+        self.L.wcref_cache_trim_to(self.h, n)
 
     def compact(self, start: int, keep):
         k = _i32(keep)
-        _check(lib().wcref_cache_compact(self.h, start, _p(k), k.size))
+        _check(self.L.wcref_cache_compact(self.h, start, _p(k), k.size), self.L)
 
     def rows(self, layer: int, which: int, n: int | None = None) -> np.ndarray:
         n = self.size if n is None else n
         out = np.empty((n, self.row), dtype=np.float32)
-        _check(lib().wcref_cache_rows(self.h, layer, which, n, _p(out)))
+        _check(self.L.wcref_cache_rows(self.h, layer, which, n, _p(out)), self.L)
         return out
 
 
