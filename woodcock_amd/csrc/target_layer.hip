@@ -857,26 +857,26 @@ constexpr int kVaD = 128;  // head_dim of the verify-width path
 // the cache.  Block (split, kv head, group): group z covers query vectors
 // 64 z .. 64 z + 63, wave w of them 16 w .. 16 w + 15, loaded straight into
 // MFMA A fragments (fp32 split into bf16 hi + lo).  Per chunk of 64 keys:
-// S = Q K^T by v_mfma_f32_16x16x32_bf16 (four independent key tiles), an
-// online softmax in base 2 in registers (a query row is one 16-lane DPP row),
-// P through the wave's LDS tile into the A layout (hi + lo), O += P V against
-// the chunk's transposed V.  The next chunk's K / V and mask bytes load while
-// the current one is consumed.  Partial (m, l, o) per split (m in natural
-// units) go to k_attn_merge.
+// S^T = K Q^T by v_mfma_f32_16x16x32_bf16 (four independent key tiles), an
+// online softmax in base 2 in registers (one query row per lane), O^T += V^T
+// P^T with P^T straight from the registers and the V^T fragments read from
+// the chunk's V rows by transposing LDS reads.  The next chunk's K / V and
+// mask bytes load while the current one is consumed.  Partial (m, l, o) per
+// split (m in natural units) go to k_attn_merge.
 constexpr int kVaCH = 64;            // keys per chunk
 constexpr int kVaLdK = kVaD + 8;     // row stride (bf16) of the K chunk: B-fragment reads spread over the banks
-constexpr int kVaLdT = kVaCH + 8;    // row stride (bf16) of the transposed V chunk
+constexpr int kVaLdV = kVaD + 16;    // row stride (bf16) of the V chunk: a transposing read's four rows on distinct banks
 constexpr int kVaGroup = 64;         // query vectors per block
 constexpr int kVaMaxRows = 64;       // rows per launch (mask rows staged per chunk)
 constexpr int kVaMaxSplits = kMaxSplits;
 constexpr float kLog2e = 1.4426950408889634f;
+typedef short vs16x4 __attribute__((ext_vector_type(4)));
+typedef short vs16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) vs16x4 lds_vs16x4;
 
-// One chunk of the split in registers: K as [key][d] (thread t: key t / 16 +
-// 16 i, d chunk t % 16: coalesced); V with lanes along keys (lane l: key
-// l % 32 + 32 (i & 1), d chunk l / 32 + 2 w + 8 (i >> 1)) so that the
-// transposed LDS writes of a wave cover two contiguous 64-byte runs; the mask
-// bytes of row t / 4, keys 16 (t % 4) .. + 16.  Buffer loads at scalar chunk
-// offsets: rows past the capacity read as zeros.
+// One chunk of the split in registers: K and V as [key][d] (thread t: key
+// t / 16 + 16 i, d chunk t % 16: coalesced); the mask bytes of row t / 4, keys
+// 16 (t % 4) .. + 16.  Buffer loads: rows past the capacity read as zeros.
 struct VaChunk {
   uint4 k[4], v[4];
   uint4 mw;  // the 16 mask bytes (one 16-byte load) or their nonzero bits (byte loads)
@@ -891,7 +891,7 @@ __device__ __forceinline__ uint32_t va_nz4(uint32_t w) {
 
 struct VaSrc {
   __amdgpu_buffer_rsrc_t kr, vr, mr;
-  int kvo, vvo;     // per-thread byte offsets of the K / V loads
+  int kvo;          // per-thread byte offset of the K / V loads
   int mo;           // byte offset of the thread's mask bytes at key 0
   bool mask_vec;    // mask rows 16-byte aligned: one 16-byte load per chunk
 };
@@ -899,12 +899,11 @@ struct VaSrc {
 // (the chunk offset rides in the vector offset, which the buffer range check covers)
 template <bool MASK>
 __device__ __forceinline__ void va_chunk_load(const VaSrc& src, int c0, VaChunk& ch) {
-  const int ko = src.kvo + c0 * (kVaD * 2), vo = src.vvo + c0 * (kVaD * 2);
+  const int ko = src.kvo + c0 * (kVaD * 2);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     ch.k[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.kr, ko + i * 16 * (kVaD * 2), 0, 0));
-    ch.v[i] = __builtin_bit_cast(
-        uint4, __builtin_amdgcn_raw_buffer_load_b128(src.vr, vo + (i & 1) * 32 * (kVaD * 2) + (i >> 1) * 128, 0, 0));
+    ch.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(src.vr, ko + i * 16 * (kVaD * 2), 0, 0));
   }
   if constexpr (MASK) {
     const int mo = src.mo + c0;
@@ -938,7 +937,7 @@ template <bool MASK>
 __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_verify_attention(AttnArgs a) {
   constexpr int D = kVaD, CH = kVaCH;
   __shared__ __attribute__((aligned(16))) uint16_t ksb[CH * kVaLdK];   // [key][d]
-  __shared__ __attribute__((aligned(16))) uint16_t vst[D * kVaLdT];    // [d][key]
+  __shared__ __attribute__((aligned(16))) uint16_t vsb[CH * kVaLdV];   // [key][d]
   __shared__ __attribute__((aligned(16))) uint16_t s_mb[kVaMaxRows * 4];  // mask bits [row][key / 16]
 
   const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x, z = blockIdx.z;
@@ -954,7 +953,6 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   src.kr = buffer_rsrc(static_cast<const uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
   src.vr = buffer_rsrc(static_cast<const uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
   src.kvo = (t / 16) * (D * 2) + (t % 16) * 16;
-  src.vvo = (lane % 32) * (D * 2) + (lane / 32 + 2 * wave) * 16;
   src.mask_vec = false;
   src.mo = 0;
   if constexpr (MASK) {
@@ -1011,32 +1009,27 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
   for (int dt = 0; dt < 8; ++dt) o[dt] = af32x4{0.f, 0.f, 0.f, 0.f};
   const bool tile_live = z * kVaGroup + wave * 16 < QV;
   uint16_t* kdst = ksb + (t / 16) * kVaLdK + (t % 16) * 8;
-  const int vj0 = lane % 32, vd0 = (lane / 32 + 2 * wave) * 8;
+  uint16_t* vdst = vsb + (t / 16) * kVaLdV + (t % 16) * 8;
+  // the lane's transposing V reads: source lane 4 e + a of its 16-lane group
+  // points at key (kk block) + 4 g + e, dims 16 dt + 4 a .. + 3, so that lane
+  // i of the group receives V[key + e][16 dt + i] for e = 0..3 (the lane holds
+  // M[i / 4 + 4 e][i % 4] of its group's 16 x 4 block of reads)
+  const int vr0 = 4 * (lane / 16) + (lane % 16) / 4, vc0 = 4 * ((lane % 16) % 4);
 
   for (int c0 = kb; c0 < ke; c0 += CH) {
     const int n = min(CH, ke - c0);
     lds_barrier();  // the previous chunk is consumed
-    if (n == CH) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(kdst + 16 * i * kVaLdK) = ch.k[i];
-    } else {
+    if (n < CH) {
       // the split's last, partial chunk: V rows past the range zeroed (the
       // cache there may hold anything; P is 0 for them)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        *reinterpret_cast<uint4*>(kdst + 16 * i * kVaLdK) = ch.k[i];
-        if (vj0 + 32 * (i & 1) >= n) ch.v[i] = make_uint4(0, 0, 0, 0);
-      }
+      for (int i = 0; i < 4; ++i)
+        if (t / 16 + 16 * i >= n) ch.v[i] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int vj = vj0 + 32 * (i & 1), d0 = vd0 + 64 * (i >> 1);
-      const uint32_t vw[4] = {ch.v[i].x, ch.v[i].y, ch.v[i].z, ch.v[i].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vst[(d0 + 2 * e) * kVaLdT + vj] = static_cast<uint16_t>(vw[e] & 0xffffu);
-        vst[(d0 + 2 * e + 1) * kVaLdT + vj] = static_cast<uint16_t>(vw[e] >> 16);
-      }
+      *reinterpret_cast<uint4*>(kdst + 16 * i * kVaLdK) = ch.k[i];
+      *reinterpret_cast<uint4*>(vdst + 16 * i * kVaLdV) = ch.v[i];
     }
     if constexpr (MASK) s_mb[t] = static_cast<uint16_t>(va_mask_bits<MASK>(src, ch));
     lds_barrier();
@@ -1113,10 +1106,10 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
         abf16x8 va[8];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-          const uint16_t* vp = vst + (dt * 16 + kl) * kVaLdT + kk * 32 + 4 * gq;
-          const uint2 r0 = *reinterpret_cast<const uint2*>(vp);
-          const uint2 r1 = *reinterpret_cast<const uint2*>(vp + 16);
-          va[dt] = __builtin_bit_cast(abf16x8, make_uint4(r0.x, r0.y, r1.x, r1.y));
+          uint16_t* vp = vsb + (kk * 32 + vr0) * kVaLdV + dt * 16 + vc0;
+          const vs16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_vs16x4*)(vp));
+          const vs16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_vs16x4*)(vp + 16 * kVaLdV));
+          va[dt] = __builtin_bit_cast(abf16x8, vs16x8{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]});
         }
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], ph, o[dt], 0, 0, 0);
