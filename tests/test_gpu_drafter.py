@@ -114,14 +114,18 @@ def _rel(a, b):
     return float(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)).max() / np.abs(b).max())
 
 
-@pytest.mark.parametrize("kv_dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-4)])
-def test_qwen3_1p7b_draft_step_matches_oracle(cuda, kv_dtype, tol):
-    """Qwen3-1.7B drafter step at full shape: one layer at ctx 512 + the 16k head,
-    GPU vs the oracle over identical bf16 weights and cache contents."""
+@pytest.mark.parametrize("kv_dtype,tol,ctx", [(torch.float32, 1e-5, 512), (torch.bfloat16, 1e-4, 512),
+                                              (torch.bfloat16, 1e-4, 2000)])
+def test_qwen3_1p7b_draft_step_matches_oracle(cuda, kv_dtype, tol, ctx):
+    """Qwen3-1.7B drafter step at full shape: one layer + the 16k head, GPU vs the
+    oracle over identical bf16 weights and cache contents.  At context 2000 with
+    a bf16 cache the attention runs on the matrix cores (one 64-key chunk per
+    wave), and the step's own key lands inside a wave's chunk (key 16 of the
+    chunk at 1984)."""
     from woodcock_amd.config import qwen3_1p7b_drafter
 
     cfg = qwen3_1p7b_drafter()
-    d, od, cache, oc, ids = _oracle_step_setup(cfg, 3, cuda, 512, kv_dtype)
+    d, od, cache, oc, ids = _oracle_step_setup(cfg, 3, cuda, ctx, kv_dtype)
     rng = np.random.default_rng(3)
     for step in range(3):
         tok = int(rng.integers(0, cfg.vocab_size))

@@ -864,6 +864,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 
 typedef __bf16 abf16x8 __attribute__((ext_vector_type(8)));
 typedef float af32x4 __attribute__((ext_vector_type(4)));
+// operands of ds_read_b64_tr_b16: within each 16-lane group, lane i receives
+// element i % 4 of the 8-byte reads of lanes i / 4 + 4 e (e = 0..3)
+typedef short vs16x4 __attribute__((ext_vector_type(4)));
+typedef short vs16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) vs16x4 lds_vs16x4;
+
+// keys [0, k) of a 64-key chunk as bits
+__device__ __forceinline__ uint64_t low_bits64(int k) {
+  return k >= 64 ? ~0ull : k <= 0 ? 0ull : (1ull << k) - 1;
+}
 
 __device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
   return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
@@ -1260,6 +1270,275 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   fx_merge(a, s_w, s_last, T, per, QV, rep, lz0);
 }
 
+// ------------------------------------------------------------------ decode attention on the matrix cores
+// One query row (a draft step) with up to four query vectors per kv head,
+// head_dim 128, bf16 cache, causal with no mask or window -- the long-context
+// case, where the fixed-range kernel above runs several dependent 32-key
+// chunks per split on the vector ALUs.  Block (split, kv head) of four waves;
+// split s owns keys [s per, s per + per) (per = 256, fixed by the capacity), and
+// wave w the 64-key chunk s per + 64 w, all four independent until their
+// (m, l, o) meet in LDS.  A wave's chunk is requested at entry: its K straight
+// into v_mfma_f32_16x16x32_bf16 A fragments (lane l: key 16 kt + l % 16, dims
+// 32 st + 8 (l / 16) .. + 8) and its V rows, which go to the wave's own LDS
+// region as [key][d].  The block normalises and rotates q (the B operand,
+// split into bf16 hi + lo, scaled into base 2) and the appended row, which
+// replaces the cache row in the wave holding it (the cache gets it at the
+// end).  S^T = K Q^T leaves each lane one query vector (l % 16; lanes past the
+// group's vectors see nothing) and keys 16 kt + 4 (l / 16) + e; the softmax
+// runs on those 16 values and two cross-group shuffles, and O^T = V^T P^T
+// takes P^T from the registers with the V^T fragments read by transposing LDS
+// reads in the same key order.  The block's record goes to the last split of
+// the kv head (fx_publish / fx_merge), so no merge launch follows.
+constexpr int kMfCH = 64;             // keys per wave
+constexpr int kMfPer = 4 * kMfCH;     // keys per split
+constexpr int kMfLdV = 128 + 16;      // row stride (bf16) of a wave's V chunk
+constexpr int kMfMinCap = 1024;       // capacities below this keep the fixed-range kernel
+
+__device__ __forceinline__ uint4 mf_pack8(const float* x) {
+  return make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
+  static_assert(D == 128, "head_dim 128: two 64-dim halves per lane pair, 16-dim MFMA tiles");
+  constexpr int QVM = 4, NW = 4, CH = kMfCH;
+  constexpr int OPT = QVM * D / 256, VSTEP = 256 / D;  // the record layout of fx_publish
+  __shared__ __attribute__((aligned(16))) uint16_t vsb[NW][CH * kMfLdV];  // each wave's V rows [key][d]
+  __shared__ __attribute__((aligned(16))) float qs[QVM][D];              // q, normalised, rotated, base-2 scaled
+  __shared__ __attribute__((aligned(16))) float nkv[2][D];               // the appended row's k and v (cache-rounded)
+  __shared__ __attribute__((aligned(16))) float s_wo[NW][QVM][D];        // each wave's o
+  __shared__ float s_wm[NW][QVM], s_wl[NW][QVM];
+  __shared__ float s_m[QVM], s_l[QVM];
+  __shared__ float s_w[QVM][kFxMaxSplits];
+  __shared__ bool s_last;
+
+  const int kh = blockIdx.y, split = blockIdx.x;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int kl = lane % 16, gq = lane / 16;
+  const int rep = a.H / a.Hk;
+  const int kb = split * kMfPer, c0 = kb + CH * wave;
+
+  // 0. the offset, requested before anything else
+  const int off_raw = *a.offset_dev;
+  if (a.clear_slots && blockIdx.x == 0 && blockIdx.y == 0 && t < kSlots) a.clear_slots[t * kSlotStride] = 0ull;
+
+  // 1. in flight at entry: the wave's K fragments and V rows (rows past the
+  // capacity read as zeros), this wave's raw q vector (v = wave) and the raw
+  // k / v of the appended row (every wave loads them: no load behind a branch)
+  const __amdgpu_buffer_rsrc_t kr =
+      buffer_rsrc(static_cast<const uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
+  const __amdgpu_buffer_rsrc_t vr =
+      buffer_rsrc(static_cast<const uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
+  uint4 kf[4][4], vrow[16];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+      kf[kt][st] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ((c0 + 16 * kt + kl) * D + 32 * st + 8 * gq) * 2, 0, 0));
+#pragma unroll
+  for (int i = 0; i < 16; ++i)  // key c0 + l / 16 + 4 i, dims 8 (l % 16) .. + 8
+    vrow[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, ((c0 + gq + 4 * i) * D + 8 * kl) * 2, 0, 0));
+  const int vq = wave, hq = kh * rep + min(vq, rep - 1);
+  HeadVec<D> rq, rk;
+  head_vec_load<D>(a.qkv + hq * D, a.q_gain, rq);
+  head_vec_load<D>(a.qkv + (a.H + kh) * D, a.k_gain, rk);
+  float vraw[D / kWave];
+#pragma unroll
+  for (int i = 0; i < D / kWave; ++i) vraw[i] = a.qkv[(a.H + a.Hk + kh) * D + lane + i * kWave];
+
+  const int offset = off_raw + a.offset_add;
+  const int T = min(offset + 1, a.cap);
+  const int ke = min(T, kb + kMfPer);
+  uint16_t* kc = static_cast<uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
+  uint16_t* vc = static_cast<uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
+  const bool holds = kb <= offset && offset < ke;  // this split holds the appended row
+  if (kb < ke) {
+    const int pos = min(max(a.positions ? a.positions[0] : offset, 0), a.rope_max - 1);
+    if (vq < rep) {
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, pos, rq);
+      head_vec_norm_rope<D>(rq, a.eps);
+      const float sc = a.scale * 1.4426950408889634f;
+#pragma unroll
+      for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+        const int p = lane + e * kWave;
+        if (p < D / 2) {
+          qs[vq][p] = rq.lo[e] * sc;
+          qs[vq][p + D / 2] = rq.hi[e] * sc;
+        }
+      }
+    }
+    if (holds && wave == 0) {
+      head_vec_rope_load<D>(a.rope_cos, a.rope_sin, pos, rk);
+      head_vec_norm_rope<D>(rk, a.eps);
+#pragma unroll
+      for (int e = 0; e < HeadVec<D>::kPPL; ++e) {
+        const int p = lane + e * kWave;
+        if (p < D / 2) {
+          nkv[0][p] = kv_round<uint16_t>(rk.lo[e]);
+          nkv[0][p + D / 2] = kv_round<uint16_t>(rk.hi[e]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < D / kWave; ++i) nkv[1][lane + i * kWave] = kv_round<uint16_t>(vraw[i]);
+    }
+    lds_barrier();  // q and the appended row in LDS; the chunk loads stay in flight
+
+    // q as the B operand: lane (kl, gq) supplies vector kl (zero past the
+    // group's vectors), dims 32 st + 8 gq .. + 8
+    abf16x8 qh[4], ql[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = kl < rep ? qs[min(kl, QVM - 1)][32 * st + 8 * gq + e] : 0.f;
+      split8(x, qh[st], ql[st]);
+    }
+    float m_r = -INFINITY, l_r = 0.f;
+    af32x4 o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = af32x4{0.f, 0.f, 0.f, 0.f};
+    const int n = min(CH, ke - c0);  // the wave's live keys (none when its chunk starts past them)
+    if (n > 0) {
+      const int jr = offset - c0;  // the appended row's key within the chunk
+      if (jr >= 0 && jr < CH) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          if (16 * kt + kl == jr) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) kf[kt][st] = mf_pack8(&nkv[0][32 * st + 8 * gq]);
+          }
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (gq + 4 * i == jr) vrow[i] = mf_pack8(&nkv[1][8 * kl]);
+      }
+      if (n < CH) {  // V rows past the live keys zeroed (the cache there may hold anything; P is 0 for them)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (gq + 4 * i >= n) vrow[i] = make_uint4(0, 0, 0, 0);
+      }
+      uint16_t* vw = vsb[wave];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) *reinterpret_cast<uint4*>(vw + (gq + 4 * i) * kMfLdV + 8 * kl) = vrow[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      // S^T, four independent key tiles
+      af32x4 sacc[4];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) sacc[kt] = af32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, kf[kt][st]), qh[st], sacc[kt], 0, 0, 0);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, kf[kt][st]), ql[st], sacc[kt], 0, 0, 0);
+      }
+      // every key of the chunk is at or before the query's position
+      const uint64_t bits = kl < rep ? low_bits64(n) : 0ull;
+      const uint32_t blo = static_cast<uint32_t>(bits), bhi = static_cast<uint32_t>(bits >> 32);
+      mfma_settle();
+      float sv[4][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const uint32_t nib = __builtin_amdgcn_ubfe(kt < 2 ? blo : bhi, (kt & 1) * 16 + 4 * gq, 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          sv[kt][e] = (nib >> e) & 1u ? sacc[kt][e] : -INFINITY;
+          mx = fmaxf(mx, sv[kt][e]);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      m_r = mx;
+      const float mb = mx == -INFINITY ? 0.f : mx;
+      float p[4][4], rs = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[kt][e] = __builtin_amdgcn_exp2f(sv[kt][e] - mb);
+          rs += p[kt][e];
+        }
+      rs += __shfl_xor(rs, 16);
+      rs += __shfl_xor(rs, 32);
+      l_r = rs;
+      // O^T = V^T P^T over the two 32-key blocks; the lane's transposing reads:
+      // source lane 4 e + a of its group points at key 32 kk + 4 g + e, dims
+      // 16 dt + 4 a .. + 3 (and the same 16 keys further)
+      const int vr0 = 4 * gq + kl / 4, vc0 = 4 * (kl % 4);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const float px[8] = {p[2 * kk][0], p[2 * kk][1], p[2 * kk][2], p[2 * kk][3],
+                             p[2 * kk + 1][0], p[2 * kk + 1][1], p[2 * kk + 1][2], p[2 * kk + 1][3]};
+        abf16x8 ph, pl;
+        split8(px, ph, pl);
+        abf16x8 va[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          uint16_t* vp = vw + (kk * 32 + vr0) * kMfLdV + dt * 16 + vc0;
+          const vs16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_vs16x4*)(vp));
+          const vs16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_vs16x4*)(vp + 16 * kMfLdV));
+          va[dt] = __builtin_bit_cast(abf16x8, vs16x8{r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3]});
+        }
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], ph, o[dt], 0, 0, 0);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt], pl, o[dt], 0, 0, 0);
+      }
+      mfma_settle();
+    }
+    // the wave's (m, l, o): lane (kl, gq) holds O^T[16 dt + 4 gq + e][vector kl]
+    if (kl < QVM) {
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<float4*>(&s_wo[wave][kl][16 * dt + 4 * gq]) = make_float4(o[dt][0], o[dt][1], o[dt][2], o[dt][3]);
+      if (gq == 0) {
+        s_wm[wave][kl] = m_r;
+        s_wl[wave][kl] = l_r;
+      }
+    }
+    __syncthreads();
+    // the block's record (thread: vectors ov0 + VSTEP k, dim od), m in natural units
+    float ob[OPT];
+    const int od = t % D, ov0 = t / D;
+#pragma unroll
+    for (int k = 0; k < OPT; ++k) {
+      const int v = ov0 + VSTEP * k;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_wm[w][v]);
+      float acc = 0.f, ls = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float mw = s_wm[w][v];
+        const float wt = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        acc = fmaf(wt, s_wo[w][v][od], acc);
+        ls = fmaf(wt, s_wl[w][v], ls);
+      }
+      ob[k] = acc;
+      if (od == 0) {
+        s_m[v] = M == -INFINITY ? -INFINITY : M / 1.4426950408889634f;
+        s_l[v] = ls;
+      }
+    }
+    fx_publish<OPT, VSTEP>(a, ob, s_m, s_l, rep, static_cast<int64_t>(kh) * gridDim.x + split);
+    // the appended row into the cache, after the chunk loads
+    if (holds && wave == 0) {
+#pragma unroll
+      for (int i = 0; i < D / kWave; ++i) {
+        kv_put<uint16_t>(kc, static_cast<int64_t>(offset) * D + lane + i * kWave, nkv[0][lane + i * kWave]);
+        kv_put<uint16_t>(vc, static_cast<int64_t>(offset) * D + lane + i * kWave, nkv[1][lane + i * kWave]);
+      }
+    }
+  }
+  fx_merge(a, s_w, s_last, T, kMfPer, rep, rep, 0);
+}
+
 // Fixed-range decode split plan for a capacity: chunks of 32 keys, at most
 // kFxMaxSplits splits, per = keys per split (whole chunks), cps = chunks per split.
 struct FxPlan {
@@ -1280,6 +1559,18 @@ static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream)
     if constexpr (D == 128) {
     const int rep = a.H / std::max(a.Hk, 1);
     const int groups = rep >= 1 && rep <= 4 ? (a.rows * rep + 3) / 4 : 0;  // row groups of <= 4 query vectors
+    // one query row at long contexts: the matrix-core kernel, one 64-key chunk per wave
+    if constexpr (sizeof(KT) == 2) {
+      const int mf_splits = (a.cap + kMfPer - 1) / kMfPer;
+      if (a.rows == 1 && !a.mask && !a.n_rows_dev && a.window <= 0 && a.ctr && rep >= 1 && rep <= 4 &&
+          a.cap >= kMfMinCap && mf_splits <= kFxMaxSplits && a.Hk <= kMaxKvHeads && a.ld_out % 4 == 0 &&
+          aligned(a.out, 16) &&
+          static_cast<size_t>(a.qv_ld) * kMaxSplits * (D + 2) >= static_cast<size_t>(kFxMaxSplits) * 4 * kFxRec) {
+        hipLaunchKernelGGL(k_attn_decode_mf<D>, dim3(mf_splits, a.Hk), dim3(256), 0, stream, a);
+        WC_LAUNCHED();
+        return WC_OK;
+      }
+    }
     // an explicit mask needs every chunk of a split in flight at entry (its bytes are fetched then)
     const int fx_cps = fx_plan(a.cap, 32).cps;
     if ((!a.mask || fx_cps <= 4) && a.ctr && groups >= 1 && a.rows <= kFxMaxRows && a.Hk * groups <= kMaxKvHeads &&

@@ -870,9 +870,6 @@ constexpr int kVaGroup = 64;         // query vectors per block
 constexpr int kVaMaxRows = 64;       // rows per launch (mask rows staged per chunk)
 constexpr int kVaMaxSplits = kMaxSplits;
 constexpr float kLog2e = 1.4426950408889634f;
-typedef short vs16x4 __attribute__((ext_vector_type(4)));
-typedef short vs16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) vs16x4 lds_vs16x4;
 
 // One chunk of the split in registers: K and V as [key][d] (thread t: key
 // t / 16 + 16 i, d chunk t % 16: coalesced); the mask bytes of row t / 4, keys
@@ -924,10 +921,6 @@ __device__ __forceinline__ uint32_t va_mask_bits(const VaSrc& src, const VaChunk
   return va_nz4(ch.mw.x) | va_nz4(ch.mw.y) << 4 | va_nz4(ch.mw.z) << 8 | va_nz4(ch.mw.w) << 12;
 }
 
-// keys [0, k) of a 64-key chunk as bits
-__device__ __forceinline__ uint64_t va_low_bits(int k) {
-  return k >= 64 ? ~0ull : k <= 0 ? 0ull : (1ull << k) - 1;
-}
 
 // MASK: visibility from the explicit mask rows; otherwise causal (and the
 // sliding window).  Split ranges are fixed by the capacity (whole chunks), so a
@@ -1059,9 +1052,9 @@ __global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(2,
         const uint2 mw = *reinterpret_cast<const uint2*>(s_mb + mrow * 4);
         bits = static_cast<uint64_t>(mw.y) << 32 | mw.x;
       } else {
-        bits = va_low_bits(lim - c0 + 1) & ~va_low_bits(wlo - c0 + 1);
+        bits = low_bits64(lim - c0 + 1) & ~low_bits64(wlo - c0 + 1);
       }
-      bits = rlive ? bits & va_low_bits(n) : 0ull;
+      bits = rlive ? bits & low_bits64(n) : 0ull;
       const uint32_t blo = static_cast<uint32_t>(bits), bhi = static_cast<uint32_t>(bits >> 32);
       mfma_settle();
       float sv[4][4];
