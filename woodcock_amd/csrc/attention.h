@@ -1275,9 +1275,13 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
 // head_dim 128, bf16 cache, causal with no mask or window -- the long-context
 // case, where the fixed-range kernel above runs several dependent 32-key
 // chunks per split on the vector ALUs.  Block (split, kv head) of four waves;
-// split s owns keys [s per, s per + per) (per = 256, fixed by the capacity), and
-// wave w the 64-key chunk s per + 64 w, all four independent until their
-// (m, l, o) meet in LDS.  A wave's chunk is requested at entry: its K straight
+// split s owns keys [s per, s per + per) (per = 4 KPW, fixed by the capacity),
+// and wave w the KPW-key chunk s per + KPW w, all four independent until their
+// (m, l, o) meet in LDS.  The launch uses KPW = 64 (32 keys per wave, twice
+// the splits, measured slower: the merge reads twice the records), from a
+// capacity of 1024 (Qwen3-1.7B step: 52.7 against 53.4 us at context 1024 and
+// against 54.1 at 2048; 52.3 against 49.8 at 512, where the fixed-range kernel
+// stays).  A wave's chunk is requested at entry: its K straight
 // into v_mfma_f32_16x16x32_bf16 A fragments (lane l: key 16 kt + l % 16, dims
 // 32 st + 8 (l / 16) .. + 8) and its V rows, which go to the wave's own LDS
 // region as [key][d].  The block normalises and rotates q (the B operand,
@@ -1289,8 +1293,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
 // takes P^T from the registers with the V^T fragments read by transposing LDS
 // reads in the same key order.  The block's record goes to the last split of
 // the kv head (fx_publish / fx_merge), so no merge launch follows.
-constexpr int kMfCH = 64;             // keys per wave
-constexpr int kMfPer = 4 * kMfCH;     // keys per split
+constexpr int kMfNW = 4;              // waves per block
 constexpr int kMfLdV = 128 + 16;      // row stride (bf16) of a wave's V chunk
 constexpr int kMfMinCap = 1024;       // capacities below this keep the fixed-range kernel
 
@@ -1298,10 +1301,11 @@ __device__ __forceinline__ uint4 mf_pack8(const float* x) {
   return make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
 }
 
-template <int D>
+template <int D, int KPW>
 __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
   static_assert(D == 128, "head_dim 128: two 64-dim halves per lane pair, 16-dim MFMA tiles");
-  constexpr int QVM = 4, NW = 4, CH = kMfCH;
+  static_assert(KPW == 32 || KPW == 64, "32 or 64 keys per wave: whole 32-key blocks of the V^T product");
+  constexpr int QVM = 4, NW = kMfNW, CH = KPW, KTL = KPW / 16, NVR = KPW / 4, PER = NW * KPW;
   constexpr int OPT = QVM * D / 256, VSTEP = 256 / D;  // the record layout of fx_publish
   __shared__ __attribute__((aligned(16))) uint16_t vsb[NW][CH * kMfLdV];  // each wave's V rows [key][d]
   __shared__ __attribute__((aligned(16))) float qs[QVM][D];              // q, normalised, rotated, base-2 scaled
@@ -1317,7 +1321,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int kl = lane % 16, gq = lane / 16;
   const int rep = a.H / a.Hk;
-  const int kb = split * kMfPer, c0 = kb + CH * wave;
+  const int kb = split * PER, c0 = kb + CH * wave;
 
   // 0. the offset, requested before anything else
   const int off_raw = *a.offset_dev;
@@ -1330,15 +1334,15 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
       buffer_rsrc(static_cast<const uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
   const __amdgpu_buffer_rsrc_t vr =
       buffer_rsrc(static_cast<const uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D, a.cap * D * 2);
-  uint4 kf[4][4], vrow[16];
+  uint4 kf[KTL][4], vrow[NVR];
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt)
+  for (int kt = 0; kt < KTL; ++kt)
 #pragma unroll
     for (int st = 0; st < 4; ++st)
       kf[kt][st] = __builtin_bit_cast(
           uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ((c0 + 16 * kt + kl) * D + 32 * st + 8 * gq) * 2, 0, 0));
 #pragma unroll
-  for (int i = 0; i < 16; ++i)  // key c0 + l / 16 + 4 i, dims 8 (l % 16) .. + 8
+  for (int i = 0; i < NVR; ++i)  // key c0 + l / 16 + 4 i, dims 8 (l % 16) .. + 8
     vrow[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, ((c0 + gq + 4 * i) * D + 8 * kl) * 2, 0, 0));
   const int vq = wave, hq = kh * rep + min(vq, rep - 1);
   HeadVec<D> rq, rk;
@@ -1350,7 +1354,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
 
   const int offset = off_raw + a.offset_add;
   const int T = min(offset + 1, a.cap);
-  const int ke = min(T, kb + kMfPer);
+  const int ke = min(T, kb + PER);
   uint16_t* kc = static_cast<uint16_t*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;
   uint16_t* vc = static_cast<uint16_t*>(a.vc) + static_cast<int64_t>(kh) * a.cap * D;
   const bool holds = kb <= offset && offset < ke;  // this split holds the appended row
@@ -1404,47 +1408,47 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
       const int jr = offset - c0;  // the appended row's key within the chunk
       if (jr >= 0 && jr < CH) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < KTL; ++kt)
           if (16 * kt + kl == jr) {
 #pragma unroll
             for (int st = 0; st < 4; ++st) kf[kt][st] = mf_pack8(&nkv[0][32 * st + 8 * gq]);
           }
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < NVR; ++i)
           if (gq + 4 * i == jr) vrow[i] = mf_pack8(&nkv[1][8 * kl]);
       }
       if (n < CH) {  // V rows past the live keys zeroed (the cache there may hold anything; P is 0 for them)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
+        for (int i = 0; i < NVR; ++i)
           if (gq + 4 * i >= n) vrow[i] = make_uint4(0, 0, 0, 0);
       }
       uint16_t* vw = vsb[wave];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) *reinterpret_cast<uint4*>(vw + (gq + 4 * i) * kMfLdV + 8 * kl) = vrow[i];
+      for (int i = 0; i < NVR; ++i) *reinterpret_cast<uint4*>(vw + (gq + 4 * i) * kMfLdV + 8 * kl) = vrow[i];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
       // S^T, four independent key tiles
-      af32x4 sacc[4];
+      af32x4 sacc[KTL];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) sacc[kt] = af32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kt = 0; kt < KTL; ++kt) sacc[kt] = af32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < KTL; ++kt)
           sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, kf[kt][st]), qh[st], sacc[kt], 0, 0, 0);
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < KTL; ++kt)
           sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(abf16x8, kf[kt][st]), ql[st], sacc[kt], 0, 0, 0);
       }
       // every key of the chunk is at or before the query's position
       const uint64_t bits = kl < rep ? low_bits64(n) : 0ull;
       const uint32_t blo = static_cast<uint32_t>(bits), bhi = static_cast<uint32_t>(bits >> 32);
       mfma_settle();
-      float sv[4][4];
+      float sv[KTL][4];
       float mx = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < KTL; ++kt) {
         const uint32_t nib = __builtin_amdgcn_ubfe(kt < 2 ? blo : bhi, (kt & 1) * 16 + 4 * gq, 4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1456,9 +1460,9 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       m_r = mx;
       const float mb = mx == -INFINITY ? 0.f : mx;
-      float p[4][4], rs = 0.f;
+      float p[KTL][4], rs = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < KTL; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           p[kt][e] = __builtin_amdgcn_exp2f(sv[kt][e] - mb);
@@ -1472,7 +1476,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
       // 16 dt + 4 a .. + 3 (and the same 16 keys further)
       const int vr0 = 4 * gq + kl / 4, vc0 = 4 * (kl % 4);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+      for (int kk = 0; kk < KTL / 2; ++kk) {
         const float px[8] = {p[2 * kk][0], p[2 * kk][1], p[2 * kk][2], p[2 * kk][3],
                              p[2 * kk + 1][0], p[2 * kk + 1][1], p[2 * kk + 1][2], p[2 * kk + 1][3]};
         abf16x8 ph, pl;
@@ -1536,7 +1540,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_mf(AttnArgs a) {
       }
     }
   }
-  fx_merge(a, s_w, s_last, T, kMfPer, rep, rep, 0);
+  fx_merge(a, s_w, s_last, T, PER, rep, rep, 0);
 }
 
 // Fixed-range decode split plan for a capacity: chunks of 32 keys, at most
@@ -1561,12 +1565,12 @@ static int launch_attention_t(const AttnArgs& a, int splits, hipStream_t stream)
     const int groups = rep >= 1 && rep <= 4 ? (a.rows * rep + 3) / 4 : 0;  // row groups of <= 4 query vectors
     // one query row at long contexts: the matrix-core kernel, one 64-key chunk per wave
     if constexpr (sizeof(KT) == 2) {
-      const int mf_splits = (a.cap + kMfPer - 1) / kMfPer;
+      const int mf_splits = (a.cap + kMfNW * 64 - 1) / (kMfNW * 64);
       if (a.rows == 1 && !a.mask && !a.n_rows_dev && a.window <= 0 && a.ctr && rep >= 1 && rep <= 4 &&
           a.cap >= kMfMinCap && mf_splits <= kFxMaxSplits && a.Hk <= kMaxKvHeads && a.ld_out % 4 == 0 &&
           aligned(a.out, 16) &&
           static_cast<size_t>(a.qv_ld) * kMaxSplits * (D + 2) >= static_cast<size_t>(kFxMaxSplits) * 4 * kFxRec) {
-        hipLaunchKernelGGL(k_attn_decode_mf<D>, dim3(mf_splits, a.Hk), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_attn_decode_mf<D, 64>), dim3(mf_splits, a.Hk), dim3(256), 0, stream, a);
         WC_LAUNCHED();
         return WC_OK;
       }
