@@ -110,6 +110,55 @@ def test_rounds_match_oracle_round(cuda):
     assert rnd.syncs == len(pattern)
 
 
+@pytest.mark.parametrize("hidden", [2560, 3072])
+def test_wide_dual_stream_chain_matches_oracle(cuda, hidden):
+    """Drafters wider than 2048 run the dual-stream QKV (the feature row and the
+    token's embedding row, each RMS-normed) with x * gain staged once per block
+    and the pending head argmax resolved after the weights are requested; 3072
+    is six 512-wide steps on the eight-step kernel with the last two masked.
+    The pending chain equals the plain chain bit for bit, and both equal the
+    oracle's chain from the same root: drafts, and every step's hidden row
+    within the fp32 tolerance."""
+    from woodcock_amd.config import DrafterConfig
+
+    kk = 5
+    cfg = DrafterConfig(hidden_size=hidden, num_layers=1, num_heads=16, num_kv_heads=4, head_dim=128,
+                        intermediate_size=1536, vocab_size=8192, target_hidden_size=512, rope_theta=1e6)
+    cfg, d, rnd, od, oc, target, root = setup(cuda, 13, ctx=200, kv_dtype=torch.float32, cap=512, cfg=cfg,
+                                              head_rows=4096, k=kk)
+    assert d.pending_ok
+    c = rnd.cache[0]
+    k0, v0 = c.keys.clone(), c.values.clone()
+
+    def run(pending):
+        c.keys.copy_(k0)
+        c.values.copy_(v0)
+        rnd.drafts.zero_()
+        rnd.step_hid.zero_()
+        rnd.pending = pending
+        rnd.enqueue_draft()
+        torch.cuda.synchronize()
+        return rnd.drafts.clone(), rnd.step_hid.clone(), c.keys.clone()
+
+    plain = run(False)
+    pend = run(True)
+    for a, b, name in zip(plain, pend, ("drafts", "step_hid", "keys")):
+        assert torch.equal(a, b), name
+    out = core.rmsnorm(root, od.w["norm.weight"], cfg.rms_norm_eps)
+    fb = od.feedback(root, out)
+    drafts, hids = [], []
+    for i in range(kk):
+        z = od.logits(out)
+        drafts.append(int(od.d2t[core.argmax(z[0])]))
+        if i < kk - 1:
+            hid, out = od.forward([drafts[-1]], fb, oc)
+            fb = od.feedback(hid, out)
+            hids.append(hid[0])
+    assert plain[0][:kk].tolist() == drafts
+    assert len(set(drafts)) > 1
+    assert _rel(plain[1][: kk - 1].cpu().numpy(), np.stack(hids)) <= 1e-5
+
+
 def test_config1_rounds_match_oracle_round(cuda):
     """The benchmarked round at its full shape: Qwen3-1.7B drafter, 16,384-row
     head, bf16 drafter cache at context 512 (capacity 1024), K = 4, the

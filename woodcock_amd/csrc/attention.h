@@ -1010,7 +1010,7 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
   __shared__ uint8_t s_mk[CPS][QVM][CHK];  // explicit mask bytes of the group's rows, chunk by chunk
   __shared__ bool s_last;
 
-  const int kh = blockIdx.y, split = blockIdx.x, S = gridDim.x;
+  const int kh = blockIdx.y, split = blockIdx.x;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   KT* kc = static_cast<KT*>(a.kc) + static_cast<int64_t>(kh) * a.cap * D;

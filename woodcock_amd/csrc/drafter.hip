@@ -100,6 +100,20 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
         return true;
       }
     }
+    // two normed input segments wider than 2048 (the dual-stream QKV of a
+    // 2560-wide drafter): the per-wave kernel holds x, gains and weights of both
+    // segments (210 VGPRs, two waves per SIMD, so a 6144-row launch runs in 1.5
+    // rounds of resident waves); staging x * gain per block keeps 146 (three per
+    // SIMD, one round): Qwen3-4B draft step 88.4 -> 86.8 us.  At 2048 the
+    // per-wave kernel's 2048 waves fit one round, and the staged one measured
+    // slower in the greedy round (264.7 against 261.3 us)
+    if constexpr (NIN == 2 && S >= 5) {
+      const size_t lds = static_cast<size_t>(a.in[0].K + a.in[1].K) * sizeof(float);
+      if (gb == kAll && lds <= 64 * 1024) {  // within the default dynamic LDS limit
+        hipLaunchKernelGGL((k_gemv1s<R, PAIR, NIN, S, XB, kAll>), grid, block, lds, s, a);
+        return true;
+      }
+    }
     if (gb == kAll) {
       hipLaunchKernelGGL((k_gemv1<R, PAIR, NIN, S, XB, kAll>), grid, block, 0, s, a);
     } else if constexpr (NIN == 1) {

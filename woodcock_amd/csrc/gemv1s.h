@@ -11,8 +11,13 @@
 // from LDS.  The L2-to-CU traffic per block drops from 4 x (x + gain) to
 // 1 x (x + gain), and the wave keeps no x registers across the weight wait.
 // It pays where x dominates a wave's loads: a gain-free 6144-wide row (the
-// down projection, 24 KB of fp32 x against 12 KB of weights per wave); on
-// 2048-wide rows the per-wave loads of k_gemv1 measured as fast.
+// down projection, 24 KB of fp32 x against 12 KB of weights per wave), and
+// where the per-wave registers cap the resident waves: two normed segments
+// wider than 2048 (the dual-stream QKV at 2560: 146 VGPRs against 210, so a
+// 6144-row launch is resident at once).  With several segments, a segment
+// whose row is a pending head argmax has its keys loaded first and its row
+// staged only after the weights are requested.  On 2048-wide rows the
+// per-wave loads of k_gemv1 measured as fast.
 #pragma once
 #include "gemv.h"
 
@@ -32,30 +37,47 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1s(GemvArgs a) {
   const int row0 = (blockIdx.x * kGemvWaves + wave) * R;
   const int rrow = res_row(a, 0);
 
+  // 0. with several input segments (the dual-stream QKV), the keys of a
+  // pending head argmax (one wave-wide load) first of all: they are reduced
+  // only after the weights are requested, so the chain keys -> d2t -> row holds
+  // back no weight load (one segment: in_row resolves it up front)
+  constexpr bool kPend = NIN > 1;
+  unsigned long long pkey = 0;
+  if constexpr (kPend) {
+#pragma unroll
+    for (int s = 0; s < NIN; ++s)
+      if (a.in[s].pend_slots) pkey = pend_key(a.in[s].pend_slots);
+  }
   int steps[NIN], soff[NIN];
   int64_t xrow[NIN];
 #pragma unroll
   for (int s = 0; s < NIN; ++s) {
     steps[s] = a.in[s].K / (kWave * 8);
     soff[s] = s == 0 ? 0 : soff[s - 1] + a.in[s - 1].K;
-    xrow[s] = m > 0 ? in_row(a.in[s], 0) : 0;
+    xrow[s] = m > 0 && !(kPend && a.in[s].pend_slots) ? in_row(a.in[s], 0) : 0;
   }
 
-  // 1. the block's share of x and the gains (clamped addresses, unconditional)
+  // 1. the block's share of x and the gains (clamped addresses, unconditional);
+  // a pending segment's row after the weights
   uint4 sx[NIN][C][2], sg[NIN][C];
+  auto stage_x = [&](int s, int c, int k) {
+    const InSeg& seg = a.in[s];
+    if ((XB >> s) & 1) {
+      sx[s][c][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + xrow[s] * seg.ld + k);
+    } else {
+      const float* xp = static_cast<const float*>(seg.x) + xrow[s] * seg.ld + k;
+      sx[s][c][0] = *reinterpret_cast<const uint4*>(xp);
+      sx[s][c][1] = *reinterpret_cast<const uint4*>(xp + 4);
+    }
+  };
 #pragma unroll
   for (int s = 0; s < NIN; ++s) {
     const InSeg& seg = a.in[s];
+    const bool defer = kPend && seg.pend_slots;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int k = min(c * kGemvThreads * 8 + t * 8, seg.K - 8);
-      if ((XB >> s) & 1) {
-        sx[s][c][0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(seg.x) + xrow[s] * seg.ld + k);
-      } else {
-        const float* xp = static_cast<const float*>(seg.x) + xrow[s] * seg.ld + k;
-        sx[s][c][0] = *reinterpret_cast<const uint4*>(xp);
-        sx[s][c][1] = *reinterpret_cast<const uint4*>(xp + 4);
-      }
+      if (!defer) stage_x(s, c, k);
       if ((GB >> s) & 1) sg[s][c] = *reinterpret_cast<const uint4*>(seg.gain + k);
     }
   }
@@ -77,6 +99,21 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv1s(GemvArgs a) {
   float resv[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) resv[r] = res_at(a, rrow, min(row0 + r, a.N - 1));
+  // 2b. the pending segment's row: its token from the keys, then the row's share
+  if constexpr (kPend) {
+#pragma unroll
+    for (int s = 0; s < NIN; ++s) {
+      if (!a.in[s].pend_slots) continue;
+      const int hr = pend_reduce(pkey);
+      xrow[s] = m > 0 ? pend_token(a.in[s], hr) : 0;
+#pragma unroll
+      for (int c = 0; c < C; ++c) stage_x(s, c, min(c * kGemvThreads * 8 + t * 8, a.in[s].K - 8));
+      if (a.pend_tok_out && blockIdx.x == 0 && t == 0) {
+        a.pend_tok_out[0] = a.in[s].pend_d2t ? a.in[s].pend_d2t[hr] : hr;
+        if (a.pend_row_out) a.pend_row_out[0] = hr;
+      }
+    }
+  }
 
   // 3. x * gain -> LDS, sums of squares -> LDS (waits only for the staging loads)
 #pragma unroll
