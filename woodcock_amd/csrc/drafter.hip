@@ -100,15 +100,21 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
         return true;
       }
     }
-    // two normed input segments wider than 2048 (the dual-stream QKV of a
-    // 2560-wide drafter): the per-wave kernel holds x, gains and weights of both
-    // segments (210 VGPRs, two waves per SIMD, so a 6144-row launch runs in 1.5
-    // rounds of resident waves); staging x * gain per block keeps 146 (three per
-    // SIMD, one round): Qwen3-4B draft step 88.4 -> 86.8 us.  At 2048 the
-    // per-wave kernel's 2048 waves fit one round, and the staged one measured
-    // slower in the greedy round (264.7 against 261.3 us)
-    if constexpr (NIN == 2 && S >= 5) {
-      const size_t lds = static_cast<size_t>(a.in[0].K + a.in[1].K) * sizeof(float);
+    // normed rows wider than 2048 (the Qwen3-4B shapes: the drafter's head,
+    // dual-stream QKV and gate / up pair, the target's one-row layers and its
+    // logits head): the per-wave kernel holds every segment's x slices, gains
+    // and weights -- 116 VGPRs for one 2560-wide segment (four waves per SIMD;
+    // the head's 8192 waves and the pair's 9728 run in two or more rounds of
+    // resident waves), 210 for the dual-stream QKV (two per SIMD: 1.5 rounds
+    // for its 6144 rows) -- while staging x * gain per block keeps 73-82 and
+    // 146 (six, five and three per SIMD).  4B draft step 88.4 -> 85.4 us warm
+    // (QKV 87.4, then head and pair), the 36-layer 4B target's one-row forward
+    // 2.342 -> 2.285 ms.  At 2048 the per-wave kernel's waves fit (the 1.7B
+    // QKV's 2048) or the staged one measured no faster, and in the greedy
+    // round slower for the QKV (264.7 against 261.3 us)
+    if constexpr (S >= 5 && NIN <= 2) {
+      size_t lds = 0;
+      for (int i = 0; i < NIN; ++i) lds += static_cast<size_t>(a.in[i].K) * sizeof(float);
       if (gb == kAll && lds <= 64 * 1024) {  // within the default dynamic LDS limit
         hipLaunchKernelGGL((k_gemv1s<R, PAIR, NIN, S, XB, kAll>), grid, block, lds, s, a);
         return true;
