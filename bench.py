@@ -709,7 +709,7 @@ def bench_tree_round(args, d, tm, tcfg):
 # each scaled by what the same counter reads for a plain copy kernel of known
 # size run in the same process.  `bench.py --pmc-summary FETCH_DIR WRITE_DIR`
 # turns the two counter CSVs into the committed summary that later runs read.
-HEAD_KERNEL = "k_gemv1<2, false, 1, 4, 0, 1>"
+HEAD_KERNEL = "k_gemv1s<2, false, 1, 4, 0, 1>"
 PROBE_HEADS = 16
 PROBE_COPIES = 4
 PROBE_COPY_FLOATS = 64 << 20  # 256 MiB read + 256 MiB written per copy

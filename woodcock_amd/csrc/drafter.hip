@@ -107,16 +107,25 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
     // the head's 8192 waves and the pair's 9728 run in two or more rounds of
     // resident waves), 210 for the dual-stream QKV (two per SIMD: 1.5 rounds
     // for its 6144 rows) -- while staging x * gain per block keeps 73-82 and
-    // 146 (six, five and three per SIMD).  4B draft step 88.4 -> 85.4 us warm
-    // (QKV 87.4, then head and pair), the 36-layer 4B target's one-row forward
-    // 2.342 -> 2.285 ms.  At 2048 the per-wave kernel's waves fit (the 1.7B
-    // QKV's 2048) or the staged one measured no faster, and in the greedy
-    // round slower for the QKV (264.7 against 261.3 us)
+    // 146 (six, five and three per SIMD).  4B draft step 87.7 -> 84.4 us warm,
+    // the 36-layer 4B target's one-row forward 2.345 -> 2.300 ms
     if constexpr (S >= 5 && NIN <= 2) {
       size_t lds = 0;
       for (int i = 0; i < NIN; ++i) lds += static_cast<size_t>(a.in[i].K) * sizeof(float);
       if (gb == kAll && lds <= 64 * 1024) {  // within the default dynamic LDS limit
         hipLaunchKernelGGL((k_gemv1s<R, PAIR, NIN, S, XB, kAll>), grid, block, lds, s, a);
+        return true;
+      }
+    }
+    // at 2048 only the draft head (argmax epilogue; 8192 waves at five per SIMD
+    // on the per-wave kernel's 94 VGPRs, six per SIMD on the staged one's 73):
+    // 1.7B draft step 53.25 -> 52.7 us warm, 65.9 -> 64.9 us cold, greedy round
+    // 261.55 -> 260.4 us.  Four head rows per wave (4096 waves, all resident),
+    // the staged gate / up pair and the staged dual-stream QKV (whose 2048
+    // waves already fit one round: round 264.7 against 261.3 us) measured slower
+    if constexpr (S == 4 && NIN == 1 && !PAIR) {
+      if (gb == kAll && a.epi == kEpiArgmax) {
+        hipLaunchKernelGGL((k_gemv1s<R, PAIR, NIN, S, XB, kAll>), grid, block, a.in[0].K * sizeof(float), s, a);
         return true;
       }
     }
