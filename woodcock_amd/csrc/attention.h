@@ -1295,7 +1295,13 @@ __global__ __launch_bounds__(NT) void k_attn_decode_fx(AttnArgs a, int per) {
 // the kv head (fx_publish / fx_merge), so no merge launch follows.
 constexpr int kMfNW = 4;              // waves per block
 constexpr int kMfLdV = 128 + 16;      // row stride (bf16) of a wave's V chunk
-constexpr int kMfMinCap = 1024;       // capacities below this keep the fixed-range kernel
+// Capacities below kMfMinCap keep the fixed-range kernel.  Both kernels size
+// their grids from the capacity (the live length is on the device), and this
+// one takes 256 keys per block: at capacity 1024 that is 4 splits per kv head,
+// so a 513-key context runs on 16 blocks of the 32 (10.5 us against 6.7 on
+// the fixed-range kernel's 32-key splits); at 4112 it is 17 splits (4097 keys:
+// 11.7 against 16.5 us)
+constexpr int kMfMinCap = 2048;
 
 __device__ __forceinline__ uint4 mf_pack8(const float* x) {
   return make_uint4(pack2_bf16(x[0], x[1]), pack2_bf16(x[2], x[3]), pack2_bf16(x[4], x[5]), pack2_bf16(x[6], x[7]));
