@@ -27,6 +27,10 @@ pytestmark = pytest.mark.gpu
 
 SMALL = TargetConfig(hidden_size=512, num_heads=4, num_kv_heads=2, head_dim=128, intermediate_size=1024,
                      num_layers=6, vocab_size=1000)
+# Qwen3-4B widths, two layers: one row runs the one-row kernels with x * gain
+# staged per block (QKV, gate / up pair, the 151,936-row logits head)
+QWEN3_4B_2L = TargetConfig(hidden_size=2560, num_heads=32, num_kv_heads=8, head_dim=128, intermediate_size=9728,
+                           num_layers=2)
 
 
 def oracle_target(cfg, w, layers, kv_bf16, cap):
@@ -69,6 +73,7 @@ def random_parents(n, rng):
     (SMALL, 33, 200, True, True),
     (TargetConfig(num_layers=2), 5, 512, True, False),
     (TargetConfig(num_layers=2), 60, 300, True, True),
+    (QWEN3_4B_2L, 1, 300, True, False),
 ])
 def test_target_forward_matches_oracle(cuda, cfg, rows, prefix, kv_bf16, tree):
     dev = torch.device("cuda", 0)
@@ -140,7 +145,7 @@ def test_target_forward_rejects_bad_shapes(cuda):
 
 
 @pytest.mark.parametrize("cfg,rows,prefix", [(SMALL, 5, 40), (TargetConfig(num_layers=2), 5, 512),
-                                             (TargetConfig(num_layers=2), 2, 300)])
+                                             (TargetConfig(num_layers=2), 2, 300), (QWEN3_4B_2L, 1, 300)])
 def test_few_row_path_equals_verify_width_path(cuda, cfg, rows, prefix):
     """A chain block that takes the few-row path (no mask, few query vectors)
     gives the logits, taps and appended K/V of the same block forced onto the
