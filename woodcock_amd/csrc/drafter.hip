@@ -120,9 +120,10 @@ static bool launch_gemv1_s(const GemvArgs& a, hipStream_t s) {
     // at 2048 only the draft head (argmax epilogue; 8192 waves at five per SIMD
     // on the per-wave kernel's 94 VGPRs, six per SIMD on the staged one's 73):
     // 1.7B draft step 53.25 -> 52.7 us warm, 65.9 -> 64.9 us cold, greedy round
-    // 261.55 -> 260.4 us.  Four head rows per wave (4096 waves, all resident),
-    // the staged gate / up pair and the staged dual-stream QKV (whose 2048
-    // waves already fit one round: round 264.7 against 261.3 us) measured slower
+    // 261.55 -> 260.4 us.  Four head rows per wave (4096 waves, all resident)
+    // and the staged gate / up pair measured slower; the staged dual-stream QKV
+    // (whose 2048 waves already fit one round) within noise (round 252.4
+    // against 253.1 us, step 49.5 against 49.4 us)
     if constexpr (S == 4 && NIN == 1 && !PAIR) {
       if (gb == kAll && a.epi == kEpiArgmax) {
         hipLaunchKernelGGL((k_gemv1s<R, PAIR, NIN, S, XB, kAll>), grid, block, a.in[0].K * sizeof(float), s, a);
