@@ -12,12 +12,13 @@
 // 1 x (x + gain), and the wave keeps no x registers across the weight wait.
 // It pays where x dominates a wave's loads: a gain-free 6144-wide row (the
 // down projection, 24 KB of fp32 x against 12 KB of weights per wave), and
-// where the per-wave registers cap the resident waves: two normed segments
-// wider than 2048 (the dual-stream QKV at 2560: 146 VGPRs against 210, so a
-// 6144-row launch is resident at once).  With several segments, a segment
-// whose row is a pending head argmax has its keys loaded first and its row
-// staged only after the weights are requested.  On 2048-wide rows the
-// per-wave loads of k_gemv1 measured as fast.
+// where the per-wave registers cap the resident waves: normed rows wider than
+// 2048 (at 2560 one segment keeps 73-82 VGPRs against 116, the dual-stream
+// QKV 146 against 210, so its 6144-row launch is resident at once) and the
+// 2048-wide draft head (73 against 94, six waves per SIMD instead of five).
+// With several segments, a segment whose row is a pending head argmax has its
+// keys loaded first and its row staged only after the weights are requested.
+// Other 2048-wide rows keep the per-wave loads of k_gemv1 (measured as fast).
 #pragma once
 #include "gemv.h"
 
