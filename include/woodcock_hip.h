@@ -243,8 +243,9 @@ int wc_sample_without_replacement(const float* q, int rows, int head_rows, int64
  * cache slot, feedback row) lives in a caller-owned device state of
  * wc_tree_draft_state_bytes() bytes, zero-initialised once (at most 512
  * nodes, width <= 8; the expansion's counters reset themselves).  The
- * caller runs, per level, the draft head (logits) and wc_probs_from_logits at
- * T = 1 over the frontier rows, wc_tree_draft_expand, and unless it is the last
+ * caller runs, per level, the draft head (logits) and wc_tree_draft_expand_logits
+ * (or wc_probs_from_logits at T = 1 and wc_tree_draft_expand) over the frontier
+ * rows, and unless it is the last
  * level wc_tree_draft_frontier plus wc_drafter_forward with the inputs it
  * wrote; node ids and level ranges follow from the static shape (root 0, then
  * rows * width children per level). */
@@ -261,6 +262,16 @@ int wc_tree_draft_begin(void* state, const int32_t* root_token_dev, wc_stream_t 
  * (spec.py:226-237). */
 int wc_tree_draft_expand(void* state, const float* q, int rows, int head_rows, int64_t ld_q, const int32_t* d2t_dev,
                          int width, int node_base, wc_stream_t stream);
+
+/* The same expansion from the head logits z [rows][ld] at T = 1, with no
+ * probability row written (the greedy branch of spec.py:226-237 on
+ * _draft_dist's q = softmax(z), spec.py:113-121): the children are the width
+ * largest z (softmax is monotone; same order and tie rule) and each child's
+ * q = exp(z - max) / sum exp(z - max) is formed from per-part row statistics.
+ * Equal to wc_probs_from_logits (T = 1) + wc_tree_draft_expand up to the
+ * association of the row sum (a few ulps of q and phat); one launch. */
+int wc_tree_draft_expand_logits(void* state, const float* logits, int rows, int head_rows, int64_t ld,
+                                const int32_t* d2t_dev, int width, int node_base, wc_stream_t stream);
 
 /* Next frontier: the min(width, level size) nodes of [level_begin, level_end)
  * with the largest phat, earlier nodes first on a tie (Policy.select_frontier,

@@ -230,3 +230,65 @@ def test_sampled_enqueue_never_synchronises(cuda):
         torch.cuda.set_sync_debug_mode(0)
     torch.cuda.synchronize()
     assert int(tdr.tree.count.item()) == 9
+
+
+@pytest.mark.parametrize("head_rows", [16384, 3001])
+def test_expand_from_logits_equals_softmax_then_expand(cuda, head_rows):
+    """wc_tree_draft_expand_logits (the children and their q formed from the
+    logits by per-part row statistics) against wc_probs_from_logits at T = 1
+    followed by wc_tree_draft_expand on the same logits, over two levels (the
+    root's children, then a frontier of `width` rows): the same node table
+    (tokens, parents, depths of every node), and phat within 1e-6 relative --
+    only the association of the softmax sum differs.  3001 head rows: two
+    parts, and rows after the first start off the 16-byte vector alignment
+    (read element by element)."""
+    import ctypes as C
+
+    from woodcock_amd import _lib
+    from woodcock_amd.runtime import ptr, stream_ptr, workspace
+
+    width, off = 4, 40
+    rng = np.random.default_rng(head_rows)
+    d2t = torch.from_numpy(np.sort(rng.choice(151936, head_rows, replace=False)).astype(np.int32)).to(cuda)
+    z1 = torch.from_numpy((rng.standard_normal((1, head_rows)) * 3).astype(np.float32)).to(cuda)
+    z2 = torch.from_numpy((rng.standard_normal((width, head_rows)) * 3).astype(np.float32)).to(cuda)
+    nbytes = int(_lib.lib().wc_tree_draft_state_bytes())
+    n = 1 + width + width * width
+
+    def run(fused):
+        st = torch.zeros(nbytes, dtype=torch.uint8, device=cuda)
+        root = torch.tensor([7], dtype=torch.int32, device=cuda)
+        offset = torch.tensor([off], dtype=torch.int32, device=cuda)
+        q = torch.empty(width, head_rows, device=cuda)
+        s = stream_ptr()
+
+        def expand(z, rows, base):
+            if fused:
+                _lib.call("wc_tree_draft_expand_logits", ptr(st), ptr(z), rows, head_rows, z.stride(0), ptr(d2t),
+                          width, base, s)
+            else:
+                _lib.call("wc_probs_from_logits", ptr(z), rows, head_rows, z.stride(0), 1.0, 0, 1.0, ptr(q),
+                          q.stride(0), ptr(workspace(cuda)), s)
+                _lib.call("wc_tree_draft_expand", ptr(st), ptr(q), rows, head_rows, q.stride(0), ptr(d2t), width,
+                          base, s)
+
+        _lib.call("wc_tree_draft_begin", ptr(st), ptr(root), s)
+        expand(z1, 1, 1)
+        tok, feat, pos = (torch.empty(width, dtype=torch.int32, device=cuda) for _ in range(3))
+        mask = torch.empty(width, 64, dtype=torch.uint8, device=cuda)
+        _lib.call("wc_tree_draft_frontier", ptr(st), 1, 1 + width, width, ptr(offset), 0, 0, 1, ptr(tok), ptr(feat),
+                  ptr(pos), ptr(mask), mask.stride(0), s)
+        expand(z2, width, 1 + width)
+        out = [torch.empty(n, dtype=torch.int32, device=cuda) for _ in range(3)]
+        count = torch.empty(1, dtype=torch.int32, device=cuda)
+        _lib.call("wc_tree_draft_select", ptr(st), n, n - 1, *[ptr(o) for o in out], ptr(count), s)
+        torch.cuda.synchronize()
+        phat = st[: 8 * n].view(torch.float64).cpu().numpy()  # the node table's first field
+        return [o.cpu().numpy() for o in out], int(count.item()), phat
+
+    (ta, ca, pa), (tb, cb, pb) = run(False), run(True)
+    assert ca == cb == n
+    for x, y in zip(ta, tb):
+        assert (x == y).all()
+    assert np.abs(pb - pa).max() <= 1e-6 * np.abs(pa).max()
+    assert np.all(pa[1:] > 0) and np.all(pa[1:] < 1)

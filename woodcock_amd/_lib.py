@@ -122,6 +122,7 @@ _SIGS = {
     "wc_tree_draft_state_bytes": ([], C.c_size_t),
     "wc_tree_draft_begin": ([P, P, P], C.c_int),
     "wc_tree_draft_expand": ([P, P, C.c_int, C.c_int, I64, P, C.c_int, C.c_int, P], C.c_int),
+    "wc_tree_draft_expand_logits": ([P, P, C.c_int, C.c_int, I64, P, C.c_int, C.c_int, P], C.c_int),
     "wc_tree_draft_frontier": ([P, C.c_int, C.c_int, C.c_int, P, C.c_int, C.c_int, C.c_int, P, P, P, P, I64, P],
                                C.c_int),
     "wc_tree_draft_select": ([P, C.c_int, C.c_int, P, P, P, P, P], C.c_int),

@@ -104,6 +104,9 @@ struct TreeDraftState {
   unsigned long long sphat[kTdMaxWidth][kTdMaxWidth];
   unsigned int scount[kTdMaxWidth];
   unsigned int lvl_ctr[32];
+  // greedy expansion from the logits: per frontier row and part, the part's
+  // maximum and its sum of exp(z - maximum) (two fp32 bit patterns)
+  unsigned long long zstat[kTdMaxWidth][kTdParts];
 };
 
 __device__ __forceinline__ unsigned int atomic_load_u32(const unsigned int* p) {
@@ -143,12 +146,23 @@ __device__ __forceinline__ unsigned long long block_max_u64(unsigned long long v
 // thread keeps a sorted top-width list of its share of the row, read as
 // 16-byte vectors kTdVec at a time (all loads of a pass issued before the
 // first insert); `width` block-wide maxima then pop the winners in order.
+// LOGITS: the row holds the head logits z and q = softmax(z) (T = 1) is never
+// written: softmax is monotone, so the top-width of q are the top-width of z
+// (same tie rule), and a child's q = exp(z - M) / S comes from the row's
+// maximum M and sum S = sum_p S_p exp(m_p - M), combined in part order by the
+// last part from each part's maximum m_p and sum S_p of exp(z - m_p).  The
+// exponential and the in-part sums follow k_softmax_row (expf; lane sums, the
+// wave sums, then the waves in order): only the association of the row sum
+// differs, a few ulps of q.
 constexpr int kTdVec = 8;
+template <bool LOGITS>
 __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, const float* __restrict__ q,
                                                           int head_rows, int64_t ld_q,
                                                           const int32_t* __restrict__ d2t, int width,
                                                           int node_base) {
   __shared__ unsigned long long red[kTdThreads / kWave];
+  __shared__ float s_f[kTdThreads / kWave];
+  __shared__ float s_row[2];
   __shared__ bool s_last;
   const int r = blockIdx.x, p = blockIdx.y, P = gridDim.y, t = threadIdx.x;
   const float* qr = q + static_cast<int64_t>(r) * ld_q;
@@ -158,7 +172,9 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
   unsigned long long top[kTdMaxWidth];
 #pragma unroll
   for (int j = 0; j < kTdMaxWidth; ++j) top[j] = 0;
+  float mloc = -INFINITY;  // LOGITS: this thread's maximum
   auto insert = [&](float v, int i) {
+    if constexpr (LOGITS) mloc = fmaxf(mloc, v);
     unsigned long long k = argmax_key(v, i);
 #pragma unroll
     for (int j = 0; j < kTdMaxWidth; ++j) {
@@ -188,6 +204,33 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
     }
   }
   for (int i = 4 * e4 + t; i < i1; i += kTdThreads) insert(qr[i], i);
+  if constexpr (LOGITS) {
+    // the part's maximum, then its sum of exp(z - maximum) over a second pass
+    // of the part (L2-resident after the first; a single pass with running
+    // sums rescaled at each new maximum measured slower)
+    const int lane = t % kWave, wave = t / kWave;
+    const float mw = wave_max_dpp(mloc);
+    if (lane == 0) s_f[wave] = mw;
+    __syncthreads();
+    float mp = s_f[0];
+#pragma unroll
+    for (int w = 1; w < kTdThreads / kWave; ++w) mp = fmaxf(mp, s_f[w]);
+    __syncthreads();
+    float sl = 0.f;
+    for (int i = i0 + t; i < i1; i += kTdThreads) {
+      const float v = qr[i];
+      sl += v == -INFINITY ? 0.f : expf(v - mp);
+    }
+    sl = wave_sum_dpp(sl);
+    if (lane == 0) s_f[wave] = sl;
+    __syncthreads();
+    float sp = 0.f;
+#pragma unroll
+    for (int w = 0; w < kTdThreads / kWave; ++w) sp += s_f[w];
+    if (t == 0)
+      atomic_store_u64(&st->zstat[r][p], (static_cast<unsigned long long>(__float_as_uint(mp)) << 32) |
+                                             static_cast<unsigned long long>(__float_as_uint(sp)));
+  }
   // the part's top keys, largest first (keys are unique: the row is in the key)
   for (int j = 0; j < width; ++j) {
     const unsigned long long best = block_max_u64(top[0], red);
@@ -210,6 +253,22 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
   __syncthreads();
   if (!s_last) return;
   unsigned long long k = t < P * width ? atomic_load_u64(&st->cand[r][t / width][t % width]) : 0ull;
+  if constexpr (LOGITS) {
+    if (t == 0) {
+      float mp[kTdParts], sp[kTdParts], M = -INFINITY;
+      for (int j = 0; j < P; ++j) {
+        const unsigned long long w = atomic_load_u64(&st->zstat[r][j]);
+        mp[j] = __uint_as_float(static_cast<uint32_t>(w >> 32));
+        sp[j] = __uint_as_float(static_cast<uint32_t>(w & 0xffffffffu));
+        M = fmaxf(M, mp[j]);
+      }
+      float S = 0.f;
+      for (int j = 0; j < P; ++j) S += sp[j] == 0.f ? 0.f : sp[j] * expf(mp[j] - M);
+      s_row[0] = M;
+      s_row[1] = S;
+    }
+    __syncthreads();
+  }
   const int v = st->front[r];
   for (int j = 0; j < width; ++j) {
     const unsigned long long best = block_max_u64(k, red);
@@ -220,7 +279,8 @@ __global__ __launch_bounds__(kTdThreads) void k_td_expand(TreeDraftState* st, co
       st->token[c] = d2t ? d2t[row] : row;
       st->parent[c] = v;
       st->depth[c] = st->depth[v] + 1;
-      st->phat[c] = st->phat[v] * static_cast<double>(qr[row]);
+      const float qc = LOGITS ? expf(qr[row] - s_row[0]) / s_row[1] : qr[row];
+      st->phat[c] = st->phat[v] * static_cast<double>(qc);
       st->slot[c] = -1;
       st->store[c] = -1;
     }
@@ -765,8 +825,28 @@ int wc_tree_draft_expand(void* state, const float* q, int rows, int head_rows, i
              kTdMaxNodes);
   // parts of at least 1024 head rows each, at most kTdParts per frontier row
   const int parts = std::max(1, std::min(kTdParts, head_rows / 1024));
-  hipLaunchKernelGGL(k_td_expand, dim3(rows, parts), dim3(kTdThreads), 0, reinterpret_cast<hipStream_t>(stream),
-                     static_cast<TreeDraftState*>(state), q, head_rows, ld_q, d2t_dev, width, node_base);
+  hipLaunchKernelGGL(k_td_expand<false>, dim3(rows, parts), dim3(kTdThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<TreeDraftState*>(state), q, head_rows, ld_q,
+                     d2t_dev, width, node_base);
+  WC_LAUNCHED();
+  return WC_OK;
+}
+
+int wc_tree_draft_expand_logits(void* state, const float* logits, int rows, int head_rows, int64_t ld,
+                                const int32_t* d2t_dev, int width, int node_base, wc_stream_t stream) {
+  using namespace wc;
+  WC_REQUIRE(state && logits, "wc_tree_draft_expand_logits: NULL buffer");
+  WC_REQUIRE(width >= 1 && width <= kTdMaxWidth, "wc_tree_draft_expand_logits: width must be in 1..%d", kTdMaxWidth);
+  WC_REQUIRE(rows >= 1 && rows <= kTdMaxWidth, "wc_tree_draft_expand_logits: rows must be in 1..%d", kTdMaxWidth);
+  WC_REQUIRE(head_rows >= width && ld >= head_rows,
+             "wc_tree_draft_expand_logits: need head_rows >= width, ld >= head_rows");
+  WC_REQUIRE(node_base >= 1 && node_base + rows * width <= kTdMaxNodes,
+             "wc_tree_draft_expand_logits: nodes %d..%d outside the table of %d", node_base, node_base + rows * width,
+             kTdMaxNodes);
+  const int parts = std::max(1, std::min(kTdParts, head_rows / 1024));
+  hipLaunchKernelGGL(k_td_expand<true>, dim3(rows, parts), dim3(kTdThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<TreeDraftState*>(state), logits, head_rows, ld,
+                     d2t_dev, width, node_base);
   WC_LAUNCHED();
   return WC_OK;
 }

@@ -3,8 +3,9 @@ with a StaticPolicy (python/woodcock/spec.py:216-303; python/woodcock/policies.p
 without a host round trip per level, greedy or sampled (T > 0).
 
 Per level the frontier's drafter outputs go through the draft head (logits over
-the head rows), the T = 1 softmax (spec.py:120-121), ``wc_tree_draft_expand``
-(top-``width`` children per frontier row, phat products) and, unless the level
+the head rows), ``wc_tree_draft_expand_logits`` (top-``width`` children per
+frontier row under the T = 1 softmax of spec.py:120-121, whose q it forms only
+for those children; phat products) and, unless the level
 is the last, ``wc_tree_draft_frontier`` (top-``width`` nodes by phat become the
 next frontier; it writes their tokens, parent-feedback rows, positions and
 attention mask) and one drafter forward over the frontier rows, appended to
@@ -87,7 +88,6 @@ class TreeDrafter:
         self.store_out = torch.zeros(self.n_store, hid, dtype=torch.float32, device=dev)
         head_rows = drafter._head.shape[0]
         self.logits = torch.empty(width, head_rows, dtype=torch.float32, device=dev)
-        self.q = torch.empty_like(self.logits)
         self.tok_rows = torch.empty(width, dtype=torch.int32, device=dev)
         self.tokens = torch.empty(width, dtype=torch.int32, device=dev)
         self.feat_rows = torch.empty(width, dtype=torch.int32, device=dev)
@@ -152,10 +152,9 @@ class TreeDrafter:
                 _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]),
                           hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None,
                           None, ptr(d.ws), s)
-            _lib.call("wc_probs_from_logits", ptr(self.logits), rows, head_rows, self.logits.stride(0), 1.0, 0, 1.0,
-                      ptr(self.q), self.q.stride(0), ptr(workspace(d.device)), s)
-            _lib.call("wc_tree_draft_expand", ptr(self.state), ptr(self.q), rows, head_rows, self.q.stride(0),
-                      ptr(d._vocab_ids), w, node_base, s)
+            # q = softmax(z) formed only for the chosen children, in the expansion itself
+            _lib.call("wc_tree_draft_expand_logits", ptr(self.state), ptr(self.logits), rows, head_rows,
+                      self.logits.stride(0), ptr(d._vocab_ids), w, node_base, s)
             if depth == self.max_depth:
                 break
             # (b) the most probable nodes of this level become the frontier and are forwarded
