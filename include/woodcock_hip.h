@@ -460,7 +460,9 @@ int wc_drafter_forward(const wc_drafter_dims* dims, const wc_drafter_weights* w,
 /* Draft head + argmax + d2t over `rows` output rows: logits z = out . head^T
  * (written when logits_out is not NULL, [rows][head_rows] fp32), token_out[r] =
  * d2t[argmax_r z] (lowest row wins a tie), row_out[r] = the row.  With gumbel,
- * the argmax is of z/T + Gumbel noise (a draw from softmax(z/T)).
+ * the argmax is of z/T + Gumbel noise (a draw from softmax(z/T)).  With
+ * token_out NULL (and logits_out given, no gumbel) only the logits are written:
+ * no argmax (the tree drafter's levels choose their children from them).
  * out_row_dev optionally selects input row *out_row_dev + out_row_add (rows = 1).
  * Replaces Drafter.logits + mx.argmax + Drafter.token_ids
  * (python/woodcock/drafter.py:204-215; python/woodcock/spec.py:346). */

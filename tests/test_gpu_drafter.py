@@ -388,3 +388,42 @@ def test_saved_drafter_reloads_and_computes_identically(cuda, tmp_path):
         outs.append((hid, out, m.draft(out)))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     assert torch.equal(outs[0][2], outs[1][2])
+
+
+def test_head_logits_only_equals_argmax_head(cuda):
+    """wc_draft_head / wc_draft_head_norm with no token output write the logits
+    alone (the store epilogue; four rows on the few-row MFMA kernel, like the
+    argmax head): the same logits as the argmax head, at one row (with and
+    without the fused final norm) and at four rows, within 1e-6 of their
+    magnitude (the same products in the same order, so equal in practice)."""
+    import ctypes as C
+
+    from woodcock_amd import _lib
+    from woodcock_amd.config import QWEN3_EOS, qwen3_1p7b_drafter
+    from woodcock_amd.drafter import Drafter
+    from woodcock_amd.runtime import ptr, stream_ptr
+    from woodcock_amd.synthetic import draft_vocab, random_drafter
+
+    cfg = qwen3_1p7b_drafter()
+    d = Drafter(cfg, random_drafter(cfg, seed=5, device=cuda), cuda, torch.bfloat16)
+    d.restrict_vocab(draft_vocab(cfg.vocab_size, 16384, seed=5, always=QWEN3_EOS))
+    dm, hr = cfg.hidden_size, 16384
+    g = torch.Generator(device=cuda).manual_seed(5)
+    x = torch.randn(4, dm, generator=g, device=cuda)
+    dims, W, ws, s = C.byref(d.dims), C.byref(d.wstruct), ptr(d.ws), stream_ptr()
+    for rows, norm in ((1, False), (1, True), (4, False)):
+        outs = []
+        for with_tok in (True, False):
+            z = torch.full((rows, hr), float("nan"), device=cuda)
+            tok = torch.empty(rows, dtype=torch.int32, device=cuda) if with_tok else None
+            if norm:
+                xn = torch.empty(1, dm, device=cuda)
+                _lib.call("wc_draft_head_norm", dims, W, ptr(x), dm, None, 0, ptr(xn), dm, ptr(z), z.stride(0),
+                          ptr(tok) if with_tok else None, None, None, ws, s)
+            else:
+                _lib.call("wc_draft_head", dims, W, ptr(x), dm, None, 0, rows, ptr(z), z.stride(0),
+                          ptr(tok) if with_tok else None, None, None, ws, s)
+            torch.cuda.synchronize()
+            outs.append(z.cpu().numpy())
+        assert np.isfinite(outs[1]).all(), (rows, norm)
+        assert np.abs(outs[1] - outs[0]).max() <= 1e-6 * np.abs(outs[0]).max(), (rows, norm)

@@ -470,7 +470,7 @@ static int launch_gemv(const GemvArgs& a, int /*R hint*/, hipStream_t s) {
     WC_LAUNCHED();
     return WC_OK;
   }
-  if (a.M > 1 && a.M <= 8) done = launch_gemvk_any(a, pair, xb, s);
+  if (a.M > 1 && a.M <= 8 && !a.few_mfma) done = launch_gemvk_any(a, pair, xb, s);
   if (!done && a.M > 1) {
     if (pair && a.n_in == 1 && xb == 0)
       done = launch_gemvf<true, 1, 0>(a, s);
@@ -579,7 +579,10 @@ static int draft_head_impl(const wc_drafter_dims* dims, const wc_drafter_weights
                            const wc_gumbel* gumbel, void* workspace, wc_stream_t stream, bool norm,
                            bool pending = false) {
   if (int rc = check_dims(dims)) return rc;
-  WC_REQUIRE(w && w->head && out_rows && (token_out || pending) && workspace, "wc_draft_head: NULL argument");
+  // no token output (and no pending keys): the logits alone, no argmax
+  const bool logits_only = !token_out && !pending;
+  WC_REQUIRE(w && w->head && out_rows && workspace && (!logits_only || (logits_out && !gumbel)),
+             "wc_draft_head: NULL argument (the logits alone need logits_out and no Gumbel noise)");
   WC_REQUIRE(!pending || rows == 1, "wc_draft_head_norm_pending: one row");
   WC_REQUIRE(xn_out == nullptr || (rows == 1 && ld_xn >= dims->hidden && ld_xn % 4 == 0 && al16(xn_out)),
              "wc_draft_head_norm: the normalised row needs rows == 1 and a 16-byte aligned output, stride >= hidden");
@@ -622,14 +625,19 @@ static int draft_head_impl(const wc_drafter_dims* dims, const wc_drafter_weights
     h.seg_start[1] = h.N;
     h.M = tr;
     h.eps = dims->eps;
-    h.epi = kEpiArgmax;
     h.y = logits_out ? logits_out + t0 * logits_ld : nullptr;
     h.ldy = logits_ld;
-    h.slots = ws.slots;
-    h.counter = pending ? nullptr : ws.head_ctr;  // pending: only the block maxima, resolved by the next forward
-    h.d2t = w->d2t;
-    h.tok_out = pending ? nullptr : token_out + t0;
-    h.row_out = row_out && !pending ? row_out + t0 : nullptr;
+    if (logits_only) {
+      h.epi = kEpiStore;
+      h.few_mfma = 1;
+    } else {
+      h.epi = kEpiArgmax;
+      h.slots = ws.slots;
+      h.counter = pending ? nullptr : ws.head_ctr;  // pending: only the block maxima, resolved by the next forward
+      h.d2t = w->d2t;
+      h.tok_out = pending ? nullptr : token_out + t0;
+      h.row_out = row_out && !pending ? row_out + t0 : nullptr;
+    }
     if (gumbel) {
       h.use_gumbel = 1;
       h.gumbel.seed = gumbel->seed;

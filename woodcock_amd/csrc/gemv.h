@@ -113,6 +113,9 @@ struct GemvArgs {
   // row (one-row kernel only)
   int32_t* pend_tok_out;
   int32_t* pend_row_out;
+  // 2..8 input rows on the few-row MFMA kernel rather than the vector-ALU one
+  // (wide matrices: a draft head storing its logits)
+  int few_mfma;
 };
 
 __device__ __forceinline__ float dot8(const uint4 w, const float4 a, const float4 b) {

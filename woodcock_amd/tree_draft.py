@@ -88,7 +88,6 @@ class TreeDrafter:
         self.store_out = torch.zeros(self.n_store, hid, dtype=torch.float32, device=dev)
         head_rows = drafter._head.shape[0]
         self.logits = torch.empty(width, head_rows, dtype=torch.float32, device=dev)
-        self.tok_rows = torch.empty(width, dtype=torch.int32, device=dev)
         self.tokens = torch.empty(width, dtype=torch.int32, device=dev)
         self.feat_rows = torch.empty(width, dtype=torch.int32, device=dev)
         self.positions = torch.empty(width, dtype=torch.int32, device=dev)
@@ -147,10 +146,10 @@ class TreeDrafter:
             if depth == 1 and root_hidden is not None:  # final norm of the root, its `out` -> store row 0
                 _lib.call("wc_draft_head_norm", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_hid), hidden,
                           None, 0, ptr(self.store_out), hidden, ptr(self.logits), self.logits.stride(0),
-                          ptr(self.tok_rows), None, None, ptr(d.ws), s)
+                          None, None, None, ptr(d.ws), s)
             else:
                 _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]),
-                          hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None,
+                          hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), None, None,
                           None, ptr(d.ws), s)
             # q = softmax(z) formed only for the chosen children, in the expansion itself
             _lib.call("wc_tree_draft_expand_logits", ptr(self.state), ptr(self.logits), rows, head_rows,
@@ -204,10 +203,10 @@ class TreeDrafter:
             if depth == 1 and root_hidden is not None:
                 _lib.call("wc_draft_head_norm", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_hid), hidden,
                           None, 0, ptr(self.store_out), hidden, ptr(self.logits), self.logits.stride(0),
-                          ptr(self.tok_rows), None, None, ptr(d.ws), s)
+                          None, None, None, ptr(d.ws), s)
             else:
                 _lib.call("wc_draft_head", C.byref(d.dims), C.byref(d.wstruct), ptr(self.store_out[store_row]),
-                          hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), ptr(self.tok_rows), None,
+                          hidden, None, 0, rows, ptr(self.logits), self.logits.stride(0), None, None,
                           None, ptr(d.ws), s)
             _lib.call("wc_probs_from_logits", ptr(self.logits), rows, head_rows, self.logits.stride(0), temperature,
                       0, 1.0, ptr(qs[store_row]), qs.stride(0), ptr(workspace(d.device)), s)
