@@ -362,7 +362,8 @@ __global__ __launch_bounds__(kTdThreads) void k_td_select(const TreeDraftState* 
   __shared__ int s_pos[kTdMaxNodes];
   __shared__ double s_ph[kTdMaxNodes];
   __shared__ int s_dep[kTdMaxNodes];
-  const int t = threadIdx.x;
+  __shared__ int s_grp[kTdMaxNodes / kWave];  // kept nodes per 64-node group
+  const int t = threadIdx.x, lane = t % kWave;
   const bool all = n_nodes - 1 <= budget;
   for (int v = t; v < n_nodes; v += kTdThreads) {
     s_ph[v] = st->phat[v];
@@ -385,13 +386,28 @@ __global__ __launch_bounds__(kTdThreads) void k_td_select(const TreeDraftState* 
     s_pos[v] = keep ? 1 : 0;
   }
   __syncthreads();
-  if (t == 0) {  // exclusive scan; -1 marks a dropped node
+  // exclusive scan of the keep flags in node order, -1 marking a dropped node:
+  // within each 64-node group from the wave's ballot, then the groups' counts
+  int flag[kTdMaxNodes / kTdThreads], below[kTdMaxNodes / kTdThreads];
+#pragma unroll
+  for (int j = 0; j < kTdMaxNodes / kTdThreads; ++j) {
+    const int v = t + j * kTdThreads;
+    flag[j] = v < n_nodes ? s_pos[v] : 0;
+    const unsigned long long b = __ballot(flag[j] != 0);
+    below[j] = __popcll(b & ((1ull << lane) - 1ull));
+    if (lane == 0) s_grp[v / kWave] = __popcll(b);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kTdMaxNodes / kTdThreads; ++j) {
+    const int v = t + j * kTdThreads;
+    int off = 0;
+    for (int g = 0; g < v / kWave; ++g) off += s_grp[g];
+    if (v < n_nodes) s_pos[v] = flag[j] ? off + below[j] : -1;
+  }
+  if (t == 0) {
     int k = 0;
-    for (int v = 0; v < n_nodes; ++v) {
-      const int kept = s_pos[v];
-      s_pos[v] = kept ? k : -1;
-      k += kept;
-    }
+    for (int g = 0; g < kTdMaxNodes / kWave; ++g) k += s_grp[g];
     *count = k;
   }
   __syncthreads();
