@@ -64,9 +64,11 @@ def norm_err(a, b):
 @pytest.mark.parametrize("cfg,M,prefix,kv_bf16,tree", [
     (SMALL, 1, 40, False, False),
     (SMALL, 5, 64, False, False),
+    (SMALL, 16, 100, False, True),
     (SMALL, 33, 100, False, True),
     (SMALL, 60, 300, False, True),
     (SMALL, 60, 300, True, True),
+    (FULL, 16, 2048, True, True),
     (FULL, 60, 2048, False, True),
     (FULL, 60, 2048, True, True),
 ])

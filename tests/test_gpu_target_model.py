@@ -74,6 +74,7 @@ def random_parents(n, rng):
     (TargetConfig(num_layers=2), 5, 512, True, False),
     (TargetConfig(num_layers=2), 60, 300, True, True),
     (QWEN3_4B_2L, 1, 300, True, False),
+    (QWEN3_4B_2L, 8, 2000, True, True),
 ])
 def test_target_forward_matches_oracle(cuda, cfg, rows, prefix, kv_bf16, tree):
     dev = torch.device("cuda", 0)

@@ -104,6 +104,7 @@ struct SkArgs {
   const uint16_t* gain_next; // its RMSNorm gain (NULL = none)
   float* ss_next;            // with xa_next: per-row sums of squares of the output, [gridDim.x][64]
   float* part;               // ks > 1: [ks][64][cols] partials (summed by k_mm_fix)
+  unsigned int* fix_ctr;     // <= 16 rows: one zeroed counter per column range (the fix-up in the GEMM)
   // kSkQkvHead (column ranges of one 128-wide head): q / k heads get their
   // RMSNorm (q_gain / k_gain) and rotate-half RoPE at the row's position; q
   // rows land in out [M][ldo], k / v rows in the cache at slot offset + row
@@ -166,6 +167,7 @@ __device__ __forceinline__ void sk_epi_load(const SkArgs& a, int cb, EpiOps<TW, 
     const int pp = g + 4 * q;
     o.ssv[q] = (a.ss && pp < a.n_ss) ? a.ss[pp * 64 + m] : 0.f;
   }
+  if constexpr (QKV) return;  // the head epilogue reads no residual and no next gain
   // residuals and gains as 16-byte loads where the thread's columns are whole
   // and aligned (scalar loads of 16 rows x 4 column runs per instruction cost
   // as much as the partial sums they wait beside)
@@ -269,7 +271,7 @@ __device__ __forceinline__ void sk_epi_run(const SkArgs& a, float* s_c, float* s
     if (g == 0) s_inv[m] = a.ss ? 1.f / sqrtf(tot / static_cast<float>(a.ss_k) + a.eps) : 1.f;
   }
   __syncthreads();
-  if (a.epi == kSkQkvHead) {
+  if (QKV || a.epi == kSkQkvHead) {
     // one head per column range: RMS_in scale, then for q / k heads the per-head
     // RMSNorm (q_norm / k_norm gains) and rotate-half RoPE at the row's position
     // (src/backends/cpu_ops.cpp:61-77), in the order x1 = x inv g,
@@ -556,12 +558,88 @@ __global__ __launch_bounds__(256) void k_mm_stream(SkArgs a) {
 constexpr int kMwG = 4;  // column tiles per block
 constexpr int kMwP = 3;  // k steps in flight per wave
 
+// The split-K fix-up inside the GEMM launch, for at most 16 rows: every block
+// publishes its partial tile with device-coherent stores and counts itself on
+// its column range's counter; the last of the range's ks x FTW blocks sums the
+// partials in split order -- the order k_mm_fix uses, so the results are the
+// same bits -- and runs the range's epilogue.  At 16 rows a split's tile is
+// 4 KB, so the coherent hand-over costs less than the fix-up launch (its
+// launch gap and first loads); with 64 rows the tiles are four times larger
+// and the separate launch stays.
+constexpr int kFixRanges = 256;    // column ranges with a counter of their own
+constexpr int kFixFusedRows = 16;  // rows up to which the fix-up runs in the GEMM
+
+// The last of `total` blocks counting on one counter: each thread first waits
+// for its own device-coherent stores, the block barriers, one relaxed
+// device-scope RMW orders the blocks; the last resets the counter.
+__device__ __forceinline__ bool last_of(unsigned int* ctr, unsigned int total) {
+  __shared__ bool s_last;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const bool last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  return s_last;
+}
+
+// k_mm_fix's work for column range cb and rows 0..15, run by the last block of
+// the range: the partials read with device-coherent 16-byte loads (all splits
+// in flight at once), summed in split order into s_c, then the epilogue.
+template <int TW, bool QKV>
+__device__ __forceinline__ void sk_fix_last(const SkArgs& a, int cb, float* s_c) {
+  constexpr int FB = 64 * TW, LDC = FB + 4;
+  constexpr int V4 = 16 * FB / 4 / 256;  // float4 per thread: 16 rows x FB columns
+  __shared__ float s_inv[64];
+  const int t = threadIdx.x, cols = a.N;
+  EpiOps<TW, QKV> ops;
+  sk_epi_load<TW, QKV>(a, cb, ops);
+  const int64_t first = static_cast<int64_t>(cb) * FB;
+  const __amdgpu_buffer_rsrc_t rs =
+      buffer_rsrc(a.part + first, static_cast<int>((static_cast<int64_t>(a.ks) * 64 * cols - first) * 4));
+  float4 u[8][V4];
+#pragma unroll
+  for (int h = 0; h < 8; ++h)
+#pragma unroll
+    for (int i = 0; i < V4; ++i) {
+      const int e = (t + 256 * i) * 4, r = min(e / FB, a.M - 1), c = e % FB;
+      const int zz = min(h, a.ks - 1);
+      u[h][i] = fetch_f32x4(rs, ((zz * 64 + r) * cols + c) * 4);
+    }
+  sk_epi_rope<TW, QKV>(a, cb, ops);
+  float4 acc[V4];
+#pragma unroll
+  for (int i = 0; i < V4; ++i) acc[i] = float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 8; ++h)
+    if (h < a.ks)
+#pragma unroll
+      for (int i = 0; i < V4; ++i) {
+        acc[i].x += u[h][i].x;
+        acc[i].y += u[h][i].y;
+        acc[i].z += u[h][i].z;
+        acc[i].w += u[h][i].w;
+      }
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int e = (t + 256 * i) * 4;
+    *reinterpret_cast<float4*>(&s_c[(e / FB) * LDC + e % FB]) = acc[i];
+  }
+  __syncthreads();
+  sk_epi_run<TW, QKV>(a, s_c, s_inv, cb, 0, 16, ops);
+}
+
 // PE: the SiLU pair with K unsplit (ks = 1): the block owns its 32 act
 // features outright, so instead of a partial it runs the pair's epilogue
 // itself (row scale from the ss parts, SiLU(gate) * up, the next projection's
 // activations), and no fix-up launch follows.
-template <int MT, bool PE = false>
+// FTW > 0 (MT = 1): the fix-up of column ranges of 64 FTW runs in this launch
+// (sk_fix_last), with the QKV head epilogue when FQKV.
+template <int MT, bool PE = false, int FTW = 0, bool FQKV = false>
 __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
+  static_assert(FTW == 0 || (MT == 1 && !PE), "the fix-up in the GEMM takes one row tile");
   constexpr int G = kMwG, FB = 16 * G, LDR = FB + 4;
   typedef unsigned int u32x4v __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(16))) float s_red[4][64 * LDR];
@@ -698,7 +776,20 @@ __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
       v.z += o.z;
       v.w += o.w;
     }
-    *reinterpret_cast<float4*>(base + (static_cast<int64_t>(kz) * 64 + r) * cols + c) = v;
+    float* dst = base + (static_cast<int64_t>(kz) * 64 + r) * cols + c;
+    if constexpr (FTW > 0) {
+      publish_f32(dst, v.x);
+      publish_f32(dst + 1, v.y);
+      publish_f32(dst + 2, v.z);
+      publish_f32(dst + 3, v.w);
+    } else {
+      *reinterpret_cast<float4*>(dst) = v;
+    }
+  }
+  if constexpr (FTW > 0) {
+    const int fr = cg / FTW;
+    if (last_of(a.fix_ctr + static_cast<int64_t>(fr) * kCounterStride, a.ks * FTW))
+      sk_fix_last<FTW, FQKV>(a, fr, &s_red[0][0]);
   }
 }
 
@@ -822,6 +913,17 @@ static int launch_wave(SkArgs g, int fix_tw, hipStream_t s) {
     return WC_OK;
   }
   const dim3 grid(g.N / (16 * kMwG), g.ks);
+  if (g.M <= kFixFusedRows && g.fix_ctr && g.N / (64 * fix_tw) <= kFixRanges) {
+    if (g.epi == kSkQkvHead) {
+      WC_REQUIRE(fix_tw == 2, "target layer: the QKV head epilogue takes 128-column ranges");
+      hipLaunchKernelGGL((k_mm_wave<1, false, 2, true>), grid, dim3(256), 0, s, g);
+    } else if (fix_tw == 2)
+      hipLaunchKernelGGL((k_mm_wave<1, false, 2>), grid, dim3(256), 0, s, g);
+    else
+      hipLaunchKernelGGL((k_mm_wave<1, false, 1>), grid, dim3(256), 0, s, g);
+    WC_LAUNCHED();
+    return WC_OK;
+  }
   switch ((g.M + 15) / 16) {
     case 1: hipLaunchKernelGGL((k_mm_wave<1>), grid, dim3(256), 0, s, g); break;
     case 2: hipLaunchKernelGGL((k_mm_wave<2>), grid, dim3(256), 0, s, g); break;
@@ -1179,6 +1281,7 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__
 struct TargetWs {
   uint16_t *xa_x, *xa_attn, *xa_h1, *xa_act;
   float *ss_x, *ss_h1, *qkv, *q, *attn, *h1, *part, *apart;
+  unsigned int* fix_ctr;
   size_t bytes;
 };
 
@@ -1232,6 +1335,7 @@ static TargetWs target_ws(const wc_drafter_dims& d, int max_rows, void* base) {
   const size_t qv = M * static_cast<size_t>(d.heads / std::max(d.kv_heads, 1));
   w.apart = reinterpret_cast<float*>(
       take(4 * static_cast<size_t>(d.kv_heads) * std::max(kMaxSplits, kVaMaxSplits) * qv * (d.head_dim + 2)));
+  w.fix_ctr = reinterpret_cast<unsigned int*>(take(4 * static_cast<size_t>(kCounterStride) * kFixRanges));
   w.bytes = off;
   return w;
 }
@@ -1304,6 +1408,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.out = verify_path ? ws.q : ws.qkv;
   g.ldo = verify_path ? nq : nqkv;
   g.part = ws.part;
+  g.fix_ctr = ws.fix_ctr;
   if (verify_path) {
     // head_dim 128 with a bf16 cache: the QKV epilogue normalises / rotates q
     // and k and appends K / V, so the attention reads every key from the cache
@@ -1412,6 +1517,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.gain_next = u16(L->post_norm);
   g.ss_next = ws.ss_h1;
   g.part = ws.part;
+  g.fix_ctr = ws.fix_ctr;
   if (int rc = launch_wave(g, 1, s)) return rc;
 
   // 4. act = silu(W_gate . RMS_post(h1)) * (W_up . RMS_post(h1)), as activations only
@@ -1432,6 +1538,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
   g.epi = kSkSiluPair;
   g.xa_next = ws.xa_act;
   g.part = ws.part;
+  g.fix_ctr = ws.fix_ctr;
   if (int rc = launch_wave(g, 2, s)) return rc;
 
   // 5. x = h1 + W_down . act
@@ -1454,6 +1561,7 @@ int wc_target_layer(const wc_drafter_dims* dims, const wc_layer_weights* L, cons
     g.ss_next = ws.ss_x;
   }
   g.part = ws.part;
+  g.fix_ctr = ws.fix_ctr;
   return launch_wave(g, 1, s);
 }
 
