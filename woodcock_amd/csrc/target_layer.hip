@@ -22,7 +22,9 @@
 // storing its fp32 tile with plain stores, and k_mm_fix (the next launch, over
 // column ranges x 16-row groups) sums the splits in a fixed order and runs the
 // epilogue (store, residual, SiLU(gate) * up, next activations, or the QKV
-// head epilogue) -- no device-scope hand-over inside the GEMM.
+// head epilogue) -- no device-scope hand-over inside the GEMM, except for
+// blocks of at most 16 rows, whose small tiles the last split of each column
+// range sums in the same order inside the GEMM launch (k_mm_wave's FTW).
 #include <array>
 
 #include "attention.h"
