@@ -473,7 +473,9 @@ int wc_draft_head(const wc_drafter_dims* dims, const wc_drafter_weights* w, cons
 
 /* ------------------------------------------------------------------ verify-width target layer */
 
-/* Device workspace for wc_target_layer with up to max_rows rows. */
+/* Device workspace for wc_target_layer with up to max_rows rows.  Zero-filled
+ * once before its first use (wc_workspace_init): blocks of up to 16 rows count
+ * their K splits on counters in it, which every call leaves at zero. */
 size_t wc_target_workspace_bytes(const wc_drafter_dims* dims, int max_rows);
 
 /* One-time weight layout for the verify-width GEMMs: w [rows][cols] bf16
