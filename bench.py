@@ -877,6 +877,40 @@ def target_chain_only(seed=0, calls=20):
     print(json.dumps({"target_chain_calls": calls}), flush=True)
 
 
+def target_verify_only(seed=0, calls=10, rows=8):
+    """The 36-layer Qwen3-4B-shape target forward over an 8-row verify block at
+    context 4096 (more query vectors than the few-row path takes, so the
+    verify-width GEMMs and the tree attention run), called `calls` times (for
+    a kernel trace)."""
+    import torch
+
+    from woodcock_amd.target import TargetConfig, TargetModel, random_target
+
+    dev = torch.device("cuda", 0)
+    tcfg = TargetConfig(hidden_size=2560, num_heads=32, num_kv_heads=8, head_dim=128, intermediate_size=9728,
+                        num_layers=36)
+    tm = TargetModel(tcfg, random_target(tcfg, seed=seed + 11, device=dev), dev, max_rows=16)
+    cache = tm.make_cache(CTX4 + 32)
+    for c in cache:
+        c.keys[0, :, :CTX4].normal_()
+        c.values[0, :, :CTX4].normal_()
+        c.offset = CTX4
+    tok = torch.randint(0, tcfg.vocab_size, (rows,), dtype=torch.int32, device=dev)
+    off = torch.tensor([CTX4], dtype=torch.int32, device=dev)
+    logits = torch.empty(rows, tcfg.vocab_size, device=dev)
+    taps = [torch.empty(rows, tcfg.hidden_size, device=dev) for _ in tm.feature_layers]
+    tm(tok, cache, off, logits=logits, taps=taps)  # weight layout and first-call set-up outside the timed calls
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(calls):
+        tm(tok, cache, off, logits=logits, taps=taps)
+    e1.record()
+    torch.cuda.synchronize()
+    print(json.dumps({"target_verify_calls": calls, "rows": rows, "ctx": CTX4,
+                      "ms_per_forward": round(e0.elapsed_time(e1) / calls, 4)}), flush=True)
+
+
 def tree_mask_rows(tree, prefix, device):
     """The tree attention mask [N, prefix + N] as a row view of a buffer whose
     rows are padded to 16 bytes -- the layout the tree round's mask buffer has."""
@@ -1074,6 +1108,44 @@ def pmc_summary(fetch_dir, write_dir):
         "",
     ]
     print("\n".join(lines))
+
+
+def forward_trace_summary(trace_dir: str, calls: int = 10) -> None:
+    """Markdown table of the timed target forwards of `bench.py
+    --target-verify-only` from a rocprofv3 kernel trace: every dispatch from the
+    second embedding launch on (the first forward is the untimed set-up call),
+    per forward."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {trace_dir}")
+    with open(files[0], newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    starts = [i for i, r in enumerate(rows) if "k_embed_rows" in r["Kernel_Name"]]
+    if len(starts) != calls + 1:
+        raise SystemExit(f"expected {calls + 1} forwards, found {len(starts)}")
+    sel = rows[starts[1]:]
+    agg: dict[str, list] = {}
+    for r in sel:
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        a = agg.setdefault(r["Kernel_Name"], [0, 0.0, float("inf"), 0.0])
+        a[0] += 1
+        a[1] += d
+        a[2] = min(a[2], d)
+        a[3] = max(a[3], d)
+    tot = sum(a[1] for a in agg.values()) / calls
+    span = (int(sel[-1]["End_Timestamp"]) - int(sel[0]["Start_Timestamp"])) / 1e3 / calls
+    print("| Kernel | Calls / forward | Avg µs | Min | Max | µs / forward | % of kernels |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for name, a in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        nm = name if len(name) <= 90 else name[:87] + "..."
+        print(f"| `{nm}` | {a[0] / calls:.2f} | {a[1] / a[0]:.2f} | {a[2]:.2f} | {a[3]:.2f} | {a[1] / calls:.1f} "
+              f"| {100 * a[1] / calls / tot:.1f} |")
+    print(f"| **all kernels** | {sum(a[0] for a in agg.values()) / calls:.1f} | | | | **{tot:.1f}** | 100 |")
+    print()
+    print(f"First launch to last end, per forward: {span:.1f} µs.")
 
 
 def trace_summary(trace_dir: str, steps: int) -> None:
@@ -1295,6 +1367,11 @@ def main():
                     help="summarise the three counter passes over --pmc-probe2 (no GPU needed)")
     ap.add_argument("--target-chain-only", action="store_true",
                     help="only the 28-layer target forward over a 5-row chain block, 20 calls (for a kernel trace)")
+    ap.add_argument("--target-verify-only", action="store_true",
+                    help="only the 36-layer Qwen3-4B-shape forward over an 8-row verify block at context 4096, "
+                         "10 calls (for a kernel trace)")
+    ap.add_argument("--forward-trace-summary", metavar="TRACE_DIR",
+                    help="summarise a kernel trace of --target-verify-only (no GPU needed)")
     ap.add_argument("--target-layer-only", action="store_true",
                     help="only the M = 60 verify-width target layer, 45 calls (for a kernel trace of the layer)")
     ap.add_argument("--step-only", action="store_true",
@@ -1327,6 +1404,9 @@ def main():
     if args.cold_trace_summary:
         cold_trace_summary(args.cold_trace_summary)
         return
+    if args.forward_trace_summary:
+        forward_trace_summary(args.forward_trace_summary)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the round is a batch-1, single-device path with no collective; "
               "run with --gpus 1", file=sys.stderr)
@@ -1347,6 +1427,9 @@ def main():
         return
     if args.target_layer_only:
         target_layer_only(args.seed)
+        return
+    if args.target_verify_only:
+        target_verify_only(args.seed)
         return
     if args.step_only:
         step_only(args)
