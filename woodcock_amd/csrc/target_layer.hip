@@ -589,15 +589,22 @@ __device__ __forceinline__ bool last_of(unsigned int* ctr, unsigned int total) {
 
 // k_mm_fix's work for column range cb and rows 0..15, run by the last block of
 // the range: the partials read with device-coherent 16-byte loads (all splits
-// in flight at once), summed in split order into s_c, then the epilogue.
+// in flight at once), summed in split order into s_c, then the epilogue.  For
+// the QKV head epilogue the caller has loaded the cache offset and the row's
+// position already, so the RoPE table loads go out with the others.
 template <int TW, bool QKV>
-__device__ __forceinline__ void sk_fix_last(const SkArgs& a, int cb, float* s_c) {
+__device__ __forceinline__ void sk_fix_last(const SkArgs& a, int cb, float* s_c, int offset, int pos) {
   constexpr int FB = 64 * TW, LDC = FB + 4;
   constexpr int V4 = 16 * FB / 4 / 256;  // float4 per thread: 16 rows x FB columns
   __shared__ float s_inv[64];
   const int t = threadIdx.x, cols = a.N;
   EpiOps<TW, QKV> ops;
   sk_epi_load<TW, QKV>(a, cb, ops);
+  if constexpr (QKV) {
+    ops.offset = offset;
+    ops.pos = pos;
+    sk_epi_rope<TW, QKV>(a, cb, ops);
+  }
   const int64_t first = static_cast<int64_t>(cb) * FB;
   const __amdgpu_buffer_rsrc_t rs =
       buffer_rsrc(a.part + first, static_cast<int>((static_cast<int64_t>(a.ks) * 64 * cols - first) * 4));
@@ -610,7 +617,6 @@ __device__ __forceinline__ void sk_fix_last(const SkArgs& a, int cb, float* s_c)
       const int zz = min(h, a.ks - 1);
       u[h][i] = fetch_f32x4(rs, ((zz * 64 + r) * cols + c) * 4);
     }
-  sk_epi_rope<TW, QKV>(a, cb, ops);
   float4 acc[V4];
 #pragma unroll
   for (int i = 0; i < V4; ++i) acc[i] = float4{0.f, 0.f, 0.f, 0.f};
@@ -703,6 +709,13 @@ __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
       }
     }
   }
+  // the QKV head epilogue's cache offset and row position (thread t: row t / 4),
+  // in flight during the LDS reduction and the hand-over
+  int fx_offset = 0, fx_pos = -1;
+  if constexpr (FQKV) {
+    fx_offset = *a.offset_dev;
+    fx_pos = a.positions ? a.positions[min(t / 4, a.M - 1)] : -1;
+  }
   // the pair's row-scale parts (thread t: row t / 4, parts t % 4 + 4 q), in
   // flight during the LDS reduction
   float ssv[PE ? kSsMax : 1];
@@ -791,7 +804,7 @@ __global__ __launch_bounds__(256) void k_mm_wave(SkArgs a) {
   if constexpr (FTW > 0) {
     const int fr = cg / FTW;
     if (last_of(a.fix_ctr + static_cast<int64_t>(fr) * kCounterStride, a.ks * FTW))
-      sk_fix_last<FTW, FQKV>(a, fr, &s_red[0][0]);
+      sk_fix_last<FTW, FQKV>(a, fr, &s_red[0][0], fx_offset, fx_pos);
   }
 }
 
