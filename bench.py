@@ -1146,6 +1146,24 @@ def forward_trace_summary(trace_dir: str, calls: int = 10) -> None:
     print(f"| **all kernels** | {sum(a[0] for a in agg.values()) / calls:.1f} | | | | **{tot:.1f}** | 100 |")
     print()
     print(f"First launch to last end, per forward: {span:.1f} µs.")
+    # a kernel launched several times per layer (36 layers), by its place in the layer
+    layers = 36
+    per_fwd: dict[str, list[float]] = {}
+    for r in sel:
+        per_fwd.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    for name, ds in per_fwd.items():
+        n = len(ds) // calls
+        if len(ds) % calls or n % layers or n // layers < 2:
+            continue
+        k = n // layers
+        print()
+        print(f"`{name}`, {k} launches per layer, by their order in the layer:")
+        print()
+        print("| Place in the layer | Avg µs | Min | Max |")
+        print("|---:|---:|---:|---:|")
+        for j in range(k):
+            v = [ds[f * n + l * k + j] for f in range(calls) for l in range(layers)]
+            print(f"| {j + 1} | {sum(v) / len(v):.2f} | {min(v):.2f} | {max(v):.2f} |")
 
 
 def trace_summary(trace_dir: str, steps: int) -> None:
