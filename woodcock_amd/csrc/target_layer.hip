@@ -899,12 +899,16 @@ static int launch_stream(SkArgs g, const GemmPlan& p, hipStream_t s) {
   return p.tw == 2 ? launch_stream_t<2>(g, p, s) : launch_stream_t<1>(g, p, s);
 }
 
-// k_mm_wave over column groups of 64 and K splits (so that about 256 blocks run
-// with >= 4 k steps each), then k_mm_fix with column ranges of 64 fix_tw (the
-// epilogue's own width: one 128-wide head for QKV, 64 act features for the pair).
+// k_mm_wave over column groups of 64 and K splits (at most 256 blocks, one per
+// CU, with >= 4 k steps each), then k_mm_fix with column ranges of 64 fix_tw
+// (the epilogue's own width: one 128-wide head for QKV, 64 act features for the
+// pair).  The split count rounds down: rounding up put a second block on some
+// CUs (280 blocks for the Qwen3-4B o / down projections, 288 for its QKV), and
+// those CUs set the launch's end -- the 36-layer 8-row verify forward took
+// 3.45 ms that way against 3.19 ms with 240 and 192 blocks.
 static int wave_ks(int N, int K) {
   const int cg = N / (16 * kMwG), steps = K / 32;
-  return std::max(1, std::min(std::min(8, steps / 4), (256 + cg - 1) / cg));
+  return std::max(1, std::min(std::min(8, steps / 4), 256 / cg));
 }
 
 static int launch_wave(SkArgs g, int fix_tw, hipStream_t s) {
